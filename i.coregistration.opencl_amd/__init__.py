@@ -1,0 +1,292 @@
+# SPDX-License-Identifier: Unlicense
+"""ctypes binding of libicoreg.so, the MI355X (gfx950) matcher tensor path.
+
+The product is the C-ABI library built from ``csrc/`` (``make`` in this
+folder); this module only loads it and exposes its entry points to Python
+(tests, bench, smoke). There is no Python or CPU fallback: if the library
+is missing, or no gfx950 device is present, every call raises.
+
+The directory name is not a valid Python identifier, so load it with
+``importlib`` (see ``load()`` in bench.py / tests/conftest.py).
+"""
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIBPATH = HERE / "libicoreg.so"
+
+ACT_NONE, ACT_GELU, ACT_RELU, ACT_LEAKY, ACT_GELU_TANH = range(5)
+FATAL_EXIT, FATAL_RECORD = 0, 1
+
+
+class IcoregError(RuntimeError):
+    """A fatal error of the library (the reference's G_fatal_error)."""
+
+
+class OclBuf(C.Structure):
+    _fields_ = [("ptr", C.c_void_p), ("bytes", C.c_size_t), ("owned", C.c_int)]
+
+
+Mem = C.POINTER(OclBuf)
+
+
+class OclBackend(C.Structure):
+    _fields_ = [
+        ("device", C.c_int),
+        ("stream", C.c_void_p),
+        ("device_name", C.c_char * 256),
+        ("platform_name", C.c_char * 256),
+        ("max_alloc", C.c_uint64),
+        ("global_mem", C.c_uint64),
+        ("is_gpu", C.c_int),
+        ("profile", C.c_int),
+        ("cu_count", C.c_int),
+        ("arch", C.c_char * 64),
+    ]
+
+
+class Ops(C.Structure):
+    _fields_ = [
+        ("ocl", C.POINTER(OclBackend)),
+        ("scratch", Mem),
+        ("scratch_bytes", C.c_size_t),
+        ("im2col_bytes", C.c_size_t),
+    ]
+
+
+class Opnd(C.Structure):
+    _fields_ = [
+        ("buf", Mem),
+        ("off", C.c_int64),
+        ("ld", C.c_int32),
+        ("s0", C.c_int64),
+        ("s1", C.c_int64),
+    ]
+
+
+class ConvGeom(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("kh", "kw", "sy", "sx", "py", "px", "dy", "dx", "groups")]
+
+
+_I, _L, _F, _P, _S = C.c_int, C.c_long, C.c_float, C.c_void_p, C.c_char_p
+_B = C.POINTER(OclBackend)
+_O = C.POINTER(Ops)
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    # backend (include/hip_backend.h)
+    "ocl_init": (None, [_B, _S, _S]),
+    "ocl_free": (None, [_B]),
+    "ocl_errstr": (_S, [C.c_int32]),
+    "ocl_check": (None, [C.c_int32, _S]),
+    "ocl_alloc": (Mem, [_B, C.c_size_t, _S]),
+    "ocl_upload": (Mem, [_B, _P, C.c_size_t, _S]),
+    "ocl_write": (None, [_B, Mem, C.c_size_t, _P, C.c_size_t]),
+    "ocl_read": (None, [_B, Mem, C.c_size_t, _P, C.c_size_t]),
+    "ocl_release": (None, [C.POINTER(Mem)]),
+    "ocl_copy": (None, [_B, Mem, C.c_size_t, Mem, C.c_size_t, C.c_size_t]),
+    "ocl_copy_rect": (None, [_B, Mem, C.c_size_t, C.c_size_t, Mem, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t]),
+    "ocl_fill": (None, [_B, Mem, C.c_size_t, C.c_size_t, _F]),
+    "ocl_finish": (None, [_B]),
+    "ocl_wrap": (Mem, [_P, C.c_size_t]),
+    "ocl_event_record": (_I, [_B]),
+    "ocl_event_ms": (_F, [_B, _I, _I]),
+    "ocl_event_reset": (None, [_B]),
+    "icoreg_set_fatal_mode": (None, [_I]),
+    "icoreg_last_error": (_S, []),
+    "icoreg_clear_error": (None, []),
+    "icoreg_prof_entry": (_I, [_I, C.POINTER(_S), C.POINTER(C.c_double), C.POINTER(C.c_long)]),
+    "icoreg_prof_reset": (None, []),
+    # generic ops (include/ops.h)
+    "ops_init": (None, [_O, _B]),
+    "ops_free": (None, [_O]),
+    "ops_report": (None, []),
+    "ops_mat": (Opnd, [Mem, _L, _I]),
+    "ops_bmat": (Opnd, [Mem, _L, _I, _L, _L]),
+    "ops_gemm": (None, [_O, _I, _I, _I, Opnd, Opnd, _I, Opnd, _I, _I, Mem, _I, Mem, _L, _F, _I, _F]),
+    "ops_linear": (None, [_O, _I, _I, _I, Mem, _L, Mem, Mem, Mem, _L, _I, _F, _I]),
+    "ops_conv1x1": (None, [_O, Mem, _L, _I, _I, Mem, Mem, _I, Mem, _L, _I, _F]),
+    "ops_geom": (ConvGeom, [_I, _I, _I]),
+    "ops_conv_out": (_I, [_I, _I, _I, _I, _I]),
+    "ops_conv2d": (None, [_O, Mem, _I, _I, _I, Mem, Mem, _I, C.POINTER(ConvGeom), Mem, Mem, Mem, _I, _F, Mem]),
+    "ops_chan_stats": (None, [_O, Mem, _I, _I, _F, Mem, Mem]),
+    "ops_chan_affine": (None, [_O, Mem, Mem, _I, _I, Mem, Mem, Mem, Mem, _I, _F]),
+    "ops_prelu": (None, [_O, Mem, Mem, _I, _I, Mem]),
+    "ops_act": (None, [_O, Mem, Mem, _L, _I, _F]),
+    "ops_layernorm": (None, [_O, _L, _I, Mem, Mem, Mem, Mem, _F, _I, _F]),
+    "ops_softmax_rows": (None, [_O, Mem, _L, _I, _F]),
+    "ops_attention": (None, [_O, Opnd, Opnd, Opnd, Opnd, _I, _I, _I, _I, _F, Mem]),
+    "ops_rope": (None, [_O, Mem, _L, _I, _L, _I, _I, _I, Mem, _I]),
+    "ops_resize": (None, [_O, Mem, _I, _I, _I, Mem, _I, _I, _I, _I, _F]),
+    "ops_grid_sample": (None, [_O, Mem, _I, _I, _I, Mem, _I, _I, Mem]),
+    "ops_unfold": (None, [_O, Mem, _I, _I, _I, C.POINTER(ConvGeom), Mem]),
+    "ops_avgpool2": (None, [_O, Mem, _I, _I, _I, Mem]),
+    "ops_pool2d": (None, [_O, Mem, _I, _I, _I, _I, _I, _I, _I, Mem]),
+    "ops_transpose": (None, [_O, Mem, Mem, _I, _I, _I]),
+    "ops_axpby": (None, [_O, Mem, Mem, _F, Mem, _F, _L, _L]),
+    "ops_fold_bn": (None, [_P, _P, _I, _L, _P, _P, _P, _P, _F]),
+}
+
+# Entry points that never raise through the fatal path (no error check).
+_NO_CHECK = {"icoreg_set_fatal_mode", "icoreg_last_error", "icoreg_clear_error",
+             "ocl_errstr", "ops_mat", "ops_bmat", "ops_geom", "ops_conv_out",
+             "ocl_wrap", "icoreg_prof_entry", "icoreg_prof_reset", "ops_report"}
+
+_lib = None
+
+
+def library_path():
+    return LIBPATH
+
+
+def lib():
+    """The loaded library with argument types set; raises if not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIBPATH.exists():
+        raise IcoregError(f"{LIBPATH} is not built (run make in {HERE}); "
+                          "this path has no fallback")
+    l = C.CDLL(str(LIBPATH))
+    for name, (res, args) in SIGNATURES.items():
+        f = getattr(l, name)
+        f.restype = res
+        f.argtypes = args
+    l.icoreg_set_fatal_mode(FATAL_RECORD)
+    _lib = l
+    return l
+
+
+def exported_symbols():
+    return sorted(SIGNATURES)
+
+
+class _Checked:
+    """Calls into the library; a recorded fatal error becomes IcoregError."""
+
+    def __init__(self, l):
+        self._l = l
+
+    def __getattr__(self, name):
+        f = getattr(self._l, name)
+        if name in _NO_CHECK:
+            return f
+
+        def call(*args):
+            self._l.icoreg_clear_error()
+            r = f(*args)
+            msg = self._l.icoreg_last_error()
+            if msg:
+                raise IcoregError(msg.decode())
+            return r
+        return call
+
+
+def api():
+    return _Checked(lib())
+
+
+class Buffer:
+    """A device buffer of the library (cl_mem), freed with the object."""
+
+    def __init__(self, dev, mem, nbytes):
+        self.dev, self.mem, self.nbytes = dev, mem, nbytes
+
+    def release(self):
+        if self.mem:
+            lib().ocl_release(C.byref(self.mem))
+            self.mem = None
+
+    def __del__(self):
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
+class Device:
+    """One gfx950 device: the backend struct and the ops struct."""
+
+    def __init__(self, device="auto"):
+        self.api = api()
+        self.ocl = OclBackend()
+        self.api.ocl_init(C.byref(self.ocl), device.encode(), None)
+        self.ops = Ops()
+        self.api.ops_init(C.byref(self.ops), C.byref(self.ocl))
+        self.pb = C.byref(self.ocl)
+        self.po = C.byref(self.ops)
+
+    @property
+    def name(self):
+        return self.ocl.device_name.decode()
+
+    @property
+    def arch(self):
+        return self.ocl.arch.decode()
+
+    def alloc(self, nbytes, what="buffer"):
+        m = self.api.ocl_alloc(self.pb, int(nbytes), what.encode())
+        return Buffer(self, m, int(nbytes))
+
+    def zeros(self, n, dtype=np.float32):
+        b = self.alloc(max(int(n), 1) * np.dtype(dtype).itemsize)
+        self.api.ocl_fill(self.pb, b.mem, 0, b.nbytes // 4, 0.0)
+        return b
+
+    def upload(self, a, what="upload"):
+        a = np.ascontiguousarray(a)
+        b = self.alloc(max(a.nbytes, 4), what)
+        if a.nbytes:
+            self.api.ocl_write(self.pb, b.mem, 0, a.ctypes.data, a.nbytes)
+        return b
+
+    def write(self, buf, a, off_bytes=0):
+        a = np.ascontiguousarray(a)
+        self.api.ocl_write(self.pb, buf.mem, off_bytes, a.ctypes.data, a.nbytes)
+
+    def read(self, buf, count=None, dtype=np.float32, off_bytes=0):
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (buf.nbytes - off_bytes) // dtype.itemsize
+        out = np.empty(int(count), dtype)
+        if out.nbytes:
+            self.api.ocl_read(self.pb, buf.mem, off_bytes, out.ctypes.data, out.nbytes)
+        return out
+
+    def finish(self):
+        self.api.ocl_finish(self.pb)
+
+    def event(self):
+        return self.api.ocl_event_record(self.pb)
+
+    def elapsed_ms(self, e0, e1):
+        return self.api.ocl_event_ms(self.pb, e0, e1)
+
+    def reset_events(self):
+        self.api.ocl_event_reset(self.pb)
+
+    def close(self):
+        if self.ocl.stream:
+            self.api.ops_free(self.po)
+            self.api.ocl_free(self.pb)
+
+
+def mat(buf, off, ld):
+    return Opnd(buf.mem if buf is not None else None, off, ld, 0, 0)
+
+
+def bmat(buf, off, ld, s0, s1):
+    return Opnd(buf.mem if buf is not None else None, off, ld, s0, s1)
+
+
+def mem(buf):
+    """cl_mem of a Buffer, or NULL."""
+    return buf.mem if buf is not None else None
+
+
+def geom(kh, kw, sy, sx, py, px, dy, dx, groups):
+    return ConvGeom(kh, kw, sy, sx, py, px, dy, dx, groups)

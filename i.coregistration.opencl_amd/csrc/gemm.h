@@ -1,0 +1,44 @@
+/* SPDX-License-Identifier: Unlicense */
+
+/* The fp32 MFMA GEMM kernel family behind ops_gemm, ops_linear,
+ * ops_conv1x1 and the one-group ops_conv2d (implicit GEMM). */
+
+#ifndef ICOREG_GEMM_H
+#define ICOREG_GEMM_H
+
+#include <hip/hip_runtime.h>
+
+/* Source of the B operand. */
+enum gemm_bmode {
+    GEMM_B_KN = 0,   /* B(k, n) = B[k * ldb + n]. */
+    GEMM_B_NK = 1,   /* B(k, n) = B[n * ldb + k] (transb). */
+    GEMM_B_CONV = 2, /* B(k, n) = im2col of a (C, H, W) input, gathered. */
+};
+
+struct gemm_args {
+    int M, N, K;
+    const float *A;
+    long long lda, sa0, sa1;
+    const float *B;
+    long long ldb, sb0, sb1;
+    float *C;
+    long long ldc, sc0, sc1;
+    const float *R; /* Already offset by roff; C's layout. */
+    int nb1;
+    const float *bias;
+    int biasrow;
+    float alpha;
+    int act;
+    float slope;
+    /* GEMM_B_CONV: input (C, H, W), window, output width; optional
+     * input normalisation and PReLU gate per input channel. */
+    int cc, ch, cw, kh, kw, sy, sx, py, px, dy, dx, wo;
+    const float *mean, *rstd, *gate;
+};
+
+/* Launch on stream s over nb batches. bm/bn: 128 or 64 (tile). va/vb:
+ * 16-byte vector loads allowed for A / B (every row start aligned). */
+void gemm_launch(const gemm_args &g, int bmode, int nb, int bm, int bn,
+                 bool va, bool vb, hipStream_t s);
+
+#endif /* ICOREG_GEMM_H */

@@ -1,0 +1,379 @@
+/* SPDX-License-Identifier: Unlicense */
+
+/* ops_init/free, the GEMM entry points (ops_gemm, ops_linear,
+ * ops_conv1x1), the convolution dispatch (ops_conv2d: implicit-GEMM MFMA
+ * for one group, a direct kernel for grouped convolutions) and the
+ * host-side BatchNorm fold. Host layer of the reference's ops.c:86-336,
+ * 612-626 (i.coregistration.opencl): same arguments and errors, HIP
+ * launches, and every access checked against its buffer before launch. */
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <string.h>
+
+#include "act.h"
+#include "common.h"
+#include "gemm.h"
+#include "ops.h"
+
+using namespace icoreg;
+
+extern "C" void ops_init(struct ops *o, struct ocl_backend *ocl)
+{
+    memset(o, 0, sizeof(*o));
+    o->ocl = ocl;
+    o->im2col_bytes = (size_t)256 << 20;
+}
+
+extern "C" void ops_free(struct ops *o)
+{
+    if (!o->ocl)
+        return;
+    ocl_release(&o->scratch);
+    memset(o, 0, sizeof(*o));
+}
+
+extern "C" struct opnd ops_mat(cl_mem buf, long off, int ld)
+{
+    struct opnd m = {buf, off, ld, 0, 0};
+
+    return m;
+}
+
+extern "C" struct opnd ops_bmat(cl_mem buf, long off, int ld, long s0, long s1)
+{
+    struct opnd m = {buf, off, ld, s0, s1};
+
+    return m;
+}
+
+extern "C" struct conv_geom ops_geom(int k, int s, int p)
+{
+    struct conv_geom g = {k, k, s, s, p, p, 1, 1, 1};
+
+    return g;
+}
+
+extern "C" int ops_conv_out(int n, int k, int s, int p, int d)
+{
+    return (n + 2 * p - d * (k - 1) - 1) / s + 1;
+}
+
+/* Largest b0 * s0 + b1 * s1 over batches b < nb (b0 = b / nb1, b1 =
+ * b % nb1), strides non-negative. */
+static long long max_batch_off(int nb, int nb1, long long s0, long long s1)
+{
+    long long b0max = (nb - 1) / nb1, v;
+
+    v = b0max * s0 + (long long)((nb - 1) % nb1) * s1;
+    if (b0max >= 1) {
+        long long w = (b0max - 1) * s0 + (long long)(nb1 - 1) * s1;
+
+        if (w > v)
+            v = w;
+    }
+    return v;
+}
+
+/* Check a rows x cols operand with leading dimension ld from element
+ * off, over the batches. */
+static void need_matrix(cl_mem b, long long off, long long ld, long long s0,
+                        long long s1, int rows, int cols, int nb, int nb1,
+                        const char *op, const char *operand)
+{
+    long long span;
+
+    if (rows <= 0 || cols <= 0)
+        return;
+    if (ld < 0 || s0 < 0 || s1 < 0 || off < 0)
+        icoreg_fatal("%s: %s has a negative offset, stride or leading "
+                     "dimension",
+                     op, operand);
+    span = (long long)(rows - 1) * ld + cols;
+    need_floats(b, off, max_batch_off(nb, nb1, s0, s1) + span, op, operand);
+}
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+static bool vec_ok(const struct opnd &x)
+{
+    return x.buf && aligned16(x.buf->ptr) && x.ld % 4 == 0 && x.off % 4 == 0 &&
+           x.s0 % 4 == 0 && x.s1 % 4 == 0;
+}
+
+/* Tile choice: the 128 x 128 tile when it still gives every CU a block,
+ * else smaller tiles for more blocks. */
+static void pick_tile(int M, int N, int nb, int cus, int *bm, int *bn)
+{
+    long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * nb;
+    long long t64 = (long long)((M + 63) / 64) * ((N + 127) / 128) * nb;
+
+    if (M > 64 && t128 >= cus) {
+        *bm = 128;
+        *bn = 128;
+    }
+    else if (t64 >= cus || M <= 64) {
+        *bm = 64;
+        *bn = N > 64 ? 128 : 64;
+        if (*bn == 128 && t64 < cus)
+            *bn = 64;
+    }
+    else {
+        *bm = 64;
+        *bn = 64;
+    }
+}
+
+extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
+                         struct opnd B, int transb, struct opnd C, int nb,
+                         int nb1, cl_mem bias, int biasrow, cl_mem R, long roff,
+                         float alpha, int act, float slope)
+{
+    ICOREG_API_BEGIN
+    const char *op = "ops_gemm";
+    gemm_args g;
+    int bm, bn;
+
+    if (M < 0 || N < 0 || K < 0 || nb < 1 || nb1 < 1 || nb > 65535)
+        icoreg_fatal("%s: invalid sizes M=%d N=%d K=%d nb=%d nb1=%d", op, M, N,
+                     K, nb, nb1);
+    if (act < ACT_NONE || act > ACT_GELU_TANH)
+        icoreg_fatal("%s: unknown activation %d", op, act);
+    if (M == 0 || N == 0)
+        return;
+    need_matrix(A.buf, A.off, A.ld, A.s0, A.s1, M, K, nb, nb1, op, "A");
+    if (transb)
+        need_matrix(B.buf, B.off, B.ld, B.s0, B.s1, N, K, nb, nb1, op, "B");
+    else
+        need_matrix(B.buf, B.off, B.ld, B.s0, B.s1, K, N, nb, nb1, op, "B");
+    need_matrix(C.buf, C.off, C.ld, C.s0, C.s1, M, N, nb, nb1, op, "C");
+    if (R)
+        need_matrix(R, roff, C.ld, C.s0, C.s1, M, N, nb, nb1, op, "R");
+    if (bias)
+        need_floats(bias, 0, biasrow ? M : N, op, "bias");
+    count32((long long)M * N, "gemm output");
+
+    memset(&g, 0, sizeof(g));
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.A = cfptr(A.buf) + A.off;
+    g.lda = A.ld;
+    g.sa0 = A.s0;
+    g.sa1 = A.s1;
+    g.B = cfptr(B.buf) + B.off;
+    g.ldb = B.ld;
+    g.sb0 = B.s0;
+    g.sb1 = B.s1;
+    g.C = fptr(C.buf) + C.off;
+    g.ldc = C.ld;
+    g.sc0 = C.s0;
+    g.sc1 = C.s1;
+    g.R = R ? cfptr(R) + roff : nullptr;
+    g.nb1 = nb1;
+    g.bias = cfptr(bias);
+    g.biasrow = biasrow;
+    g.alpha = alpha;
+    g.act = act;
+    g.slope = slope;
+    pick_tile(M, N, nb, o->ocl->cu_count, &bm, &bn);
+    {
+        prof_scope ps(o->ocl, "gemm");
+
+        gemm_launch(g, transb ? GEMM_B_NK : GEMM_B_KN, nb, bm, bn, vec_ok(A),
+                    vec_ok(B), stream_of(o->ocl));
+        launch_check("gemm");
+    }
+    ICOREG_API_END
+}
+
+extern "C" void ops_linear(struct ops *o, int rows, int in, int out, cl_mem X,
+                           long xoff, cl_mem W, cl_mem b, cl_mem Y, long yoff,
+                           int act, float slope, int residual)
+{
+    ICOREG_API_BEGIN
+    ops_gemm(o, rows, out, in, ops_mat(X, xoff, in), ops_mat(W, 0, in), 1,
+             ops_mat(Y, yoff, out), 1, 1, b, 0, residual ? Y : NULL, yoff, 1.0f,
+             act, slope);
+    ICOREG_API_END
+}
+
+extern "C" void ops_conv1x1(struct ops *o, cl_mem X, long xoff, int C, int HW,
+                            cl_mem W, cl_mem b, int K, cl_mem Y, long yoff,
+                            int act, float slope)
+{
+    ICOREG_API_BEGIN
+    ops_gemm(o, K, HW, C, ops_mat(W, 0, C), ops_mat(X, xoff, HW), 0,
+             ops_mat(Y, yoff, HW), 1, 1, b, 1, NULL, 0, 1.0f, act, slope);
+    ICOREG_API_END
+}
+
+/* Grouped (or general) convolution, one thread per output value: the
+ * contract of the reference's conv2d (ops.cl:389-448), used here for
+ * groups > 1 only (ELoFTR's depthwise 4 x 4 / stride 4 aggregation). */
+__global__ void __launch_bounds__(256)
+    conv2d_direct(const float *__restrict__ in, int C, int H, int W,
+                  const float *__restrict__ wt, const float *__restrict__ bias,
+                  int K, int Ho, int Wo, int kh, int kw, int sy, int sx, int py,
+                  int px, int dy, int dx, int groups,
+                  const float *__restrict__ mean, const float *__restrict__ rstd,
+                  const float *__restrict__ alpha, int act, float slope,
+                  float *__restrict__ out)
+{
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long total = (long long)K * Ho * Wo;
+    int x, y, k, cg, kg, c0;
+    const float *w;
+    float acc = 0.0f;
+
+    if (idx >= total)
+        return;
+    x = (int)(idx % Wo);
+    y = (int)((idx / Wo) % Ho);
+    k = (int)(idx / ((long long)Wo * Ho));
+    cg = C / groups;
+    kg = K / groups;
+    c0 = (k / kg) * cg;
+    w = wt + (long long)k * cg * kh * kw;
+    for (int c = 0; c < cg; c++) {
+        const float *src = in + (long long)(c0 + c) * H * W;
+        float m = 0.0f, r = 1.0f, a = 1.0f;
+
+        if (mean) {
+            m = mean[c0 + c];
+            r = rstd[c0 + c];
+            if (alpha)
+                a = alpha[c0 + c];
+        }
+        for (int i = 0; i < kh; i++) {
+            const int iy = y * sy - py + i * dy;
+
+            if (iy < 0 || iy >= H)
+                continue;
+            for (int j = 0; j < kw; j++) {
+                const int ix = x * sx - px + j * dx;
+                float v;
+
+                if (ix < 0 || ix >= W)
+                    continue;
+                v = src[(long long)iy * W + ix];
+                if (mean) {
+                    v = (v - m) * r;
+                    v = v >= 0.0f ? v : a * v;
+                }
+                acc = fmaf(v, w[(c * kh + i) * kw + j], acc);
+            }
+        }
+    }
+    if (bias)
+        acc += bias[k];
+    out[idx] = icoreg_act(acc, act, slope);
+}
+
+extern "C" void ops_conv2d(struct ops *o, cl_mem in, int C, int H, int W,
+                           cl_mem w, cl_mem b, int K,
+                           const struct conv_geom *g, cl_mem mean, cl_mem rstd,
+                           cl_mem alpha, int act, float slope, cl_mem out)
+{
+    ICOREG_API_BEGIN
+    const char *op = "ops_conv2d";
+    int Ho, Wo, cg;
+
+    if (g->groups < 1 || C % g->groups || K % g->groups)
+        icoreg_fatal("HIP: %d -> %d channels in %d groups", C, K, g->groups);
+    if (g->kh < 1 || g->kw < 1 || g->sy < 1 || g->sx < 1 || g->dy < 1 ||
+        g->dx < 1 || g->py < 0 || g->px < 0)
+        icoreg_fatal("%s: invalid window geometry", op);
+    if (act < ACT_NONE || act > ACT_GELU_TANH)
+        icoreg_fatal("%s: unknown activation %d", op, act);
+    if (mean && !rstd)
+        icoreg_fatal("%s: mean given without rstd", op);
+    Ho = ops_conv_out(H, g->kh, g->sy, g->py, g->dy);
+    Wo = ops_conv_out(W, g->kw, g->sx, g->px, g->dx);
+    if (Ho < 1 || Wo < 1 || C < 1 || K < 1)
+        icoreg_fatal("%s: empty convolution (%d x %d output)", op, Ho, Wo);
+    count32((long long)C * H * W, "convolution input");
+    count32((long long)K * Ho * Wo, "convolution output");
+    cg = C / g->groups;
+    need_floats(in, 0, (long long)C * H * W, op, "input");
+    need_floats(w, 0, (long long)K * cg * g->kh * g->kw, op, "weights");
+    need_floats(out, 0, (long long)K * Ho * Wo, op, "output");
+    if (b)
+        need_floats(b, 0, K, op, "bias");
+    if (mean) {
+        need_floats(mean, 0, C, op, "mean");
+        need_floats(rstd, 0, C, op, "rstd");
+        if (alpha)
+            need_floats(alpha, 0, C, op, "alpha");
+    }
+    if (g->groups == 1) {
+        gemm_args a;
+        int bm, bn, kred = C * g->kh * g->kw;
+
+        count32((long long)kred * 128, "convolution reduction");
+        memset(&a, 0, sizeof(a));
+        a.M = K;
+        a.N = Ho * Wo;
+        a.K = kred;
+        a.A = cfptr(w);
+        a.lda = kred;
+        a.B = cfptr(in);
+        a.C = fptr(out);
+        a.ldc = (long long)Ho * Wo;
+        a.nb1 = 1;
+        a.bias = cfptr(b);
+        a.biasrow = 1;
+        a.alpha = 1.0f;
+        a.act = act;
+        a.slope = slope;
+        a.cc = C;
+        a.ch = H;
+        a.cw = W;
+        a.kh = g->kh;
+        a.kw = g->kw;
+        a.sy = g->sy;
+        a.sx = g->sx;
+        a.py = g->py;
+        a.px = g->px;
+        a.dy = g->dy;
+        a.dx = g->dx;
+        a.wo = Wo;
+        a.mean = cfptr(mean);
+        a.rstd = cfptr(rstd);
+        a.gate = mean ? cfptr(alpha) : nullptr;
+        pick_tile(K, Ho * Wo, 1, o->ocl->cu_count, &bm, &bn);
+        prof_scope ps(o->ocl, "conv_igemm");
+        gemm_launch(a, GEMM_B_CONV, 1, bm, bn,
+                    kred % 4 == 0 && aligned16(w->ptr), false,
+                    stream_of(o->ocl));
+        launch_check("conv_igemm");
+        return;
+    }
+    {
+        long long total = (long long)K * Ho * Wo;
+        prof_scope ps(o->ocl, "conv2d_direct");
+
+        hipLaunchKernelGGL(conv2d_direct, dim3((unsigned)((total + 255) / 256)),
+                           dim3(256), 0, stream_of(o->ocl), cfptr(in), C, H, W,
+                           cfptr(w), cfptr(b), K, Ho, Wo, g->kh, g->kw, g->sy,
+                           g->sx, g->py, g->px, g->dy, g->dx, g->groups,
+                           cfptr(mean), cfptr(rstd), cfptr(alpha), act, slope,
+                           fptr(out));
+        launch_check("conv2d_direct");
+    }
+    ICOREG_API_END
+}
+
+extern "C" void ops_fold_bn(float *w, float *b, int K, long per,
+                            const float *gamma, const float *beta,
+                            const float *mean, const float *var, float eps)
+{
+    for (int k = 0; k < K; k++) {
+        const double s = gamma[k] / sqrt((double)var[k] + eps);
+
+        for (long i = 0; i < per; i++)
+            w[(size_t)k * per + i] = (float)(w[(size_t)k * per + i] * s);
+        b[k] = (float)((b[k] - mean[k]) * s + beta[k]);
+    }
+}

@@ -1,0 +1,320 @@
+/* SPDX-License-Identifier: Unlicense */
+
+/* Resampling and pooling: bilinear resize into a channel offset,
+ * grid_sample (bilinear, zero padding), unfold, 2 x 2 average pooling
+ * and k x k max / average pooling. Contracts of the reference's
+ * ops.cl:718-860 with the host checks of ops.c:496-578
+ * (i.coregistration.opencl); one thread per output value, consecutive
+ * threads along the output row so that stores are coalesced. */
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+
+#include "common.h"
+#include "ops.h"
+
+using namespace icoreg;
+
+/* ---- bilinear resize --------------------------------------------------- */
+
+__global__ void __launch_bounds__(256)
+    resize_kernel(const float *__restrict__ in, int h, int w,
+                  float *__restrict__ out, int H, int W, int coff, int align,
+                  float sy, float sx, int C)
+{
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long total = (long long)C * H * W;
+    int x, y, c, x0, y0, x1, y1;
+    float ux, uy, fx, fy;
+    const float *p;
+
+    if (idx >= total)
+        return;
+    x = (int)(idx % W);
+    y = (int)((idx / W) % H);
+    c = (int)(idx / ((long long)W * H));
+    if (align) {
+        ux = W > 1 ? (float)x * (float)(w - 1) / (float)(W - 1) : 0.0f;
+        uy = H > 1 ? (float)y * (float)(h - 1) / (float)(H - 1) : 0.0f;
+    }
+    else {
+        ux = fmaxf(((float)x + 0.5f) * sx - 0.5f, 0.0f);
+        uy = fmaxf(((float)y + 0.5f) * sy - 0.5f, 0.0f);
+    }
+    x0 = min((int)ux, w - 1);
+    y0 = min((int)uy, h - 1);
+    x1 = min(x0 + 1, w - 1);
+    y1 = min(y0 + 1, h - 1);
+    fx = ux - x0;
+    fy = uy - y0;
+    p = in + (long long)c * h * w;
+    out[((long long)(c + coff) * H + y) * W + x] =
+        (1.0f - fy) * ((1.0f - fx) * p[y0 * w + x0] + fx * p[y0 * w + x1]) +
+        fy * ((1.0f - fx) * p[y1 * w + x0] + fx * p[y1 * w + x1]);
+}
+
+extern "C" void ops_resize(struct ops *o, cl_mem in, int C, int h, int w,
+                           cl_mem out, int H, int W, int coff,
+                           int align_corners, float scale)
+{
+    ICOREG_API_BEGIN
+    const char *op = "ops_resize";
+    float sy = scale > 0 ? 1.0f / scale : (float)h / H;
+    float sx = scale > 0 ? 1.0f / scale : (float)w / W;
+    long long total = (long long)C * H * W;
+
+    if (C < 0 || h < 1 || w < 1 || H < 1 || W < 1 || coff < 0)
+        icoreg_fatal("%s: invalid sizes C=%d %dx%d -> %dx%d coff=%d", op, C, h,
+                     w, H, W, coff);
+    if (total == 0)
+        return;
+    count32((long long)(C + coff) * H * W, "resize output");
+    need_floats(in, 0, (long long)C * h * w, op, "in");
+    need_floats(out, (long long)coff * H * W, total, op, "out");
+    prof_scope ps(o->ocl, "resize_bilinear");
+    hipLaunchKernelGGL(resize_kernel, dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), 0, stream_of(o->ocl), cfptr(in), h, w,
+                       fptr(out), H, W, coff, align_corners, sy, sx, C);
+    launch_check("resize_bilinear");
+    ICOREG_API_END
+}
+
+/* ---- grid_sample -------------------------------------------------------- */
+
+/* Bilinear value of plane p (H x W) at pixel coordinates (ix, iy), zero
+ * outside; non-finite coordinates give 0. Coordinates far outside are
+ * clamped first (all four taps stay outside, so the value is still 0),
+ * which keeps the integer conversion defined. */
+__device__ __forceinline__ float bilinear_zero(const float *__restrict__ p,
+                                               int H, int W, float ix,
+                                               float iy)
+{
+    int x0, y0;
+    float fx, fy, v00, v01, v10, v11;
+
+    if (!isfinite(ix) || !isfinite(iy))
+        return 0.0f;
+    ix = fminf(fmaxf(ix, -2.0f), (float)W + 1.0f);
+    iy = fminf(fmaxf(iy, -2.0f), (float)H + 1.0f);
+    x0 = (int)floorf(ix);
+    y0 = (int)floorf(iy);
+    fx = ix - x0;
+    fy = iy - y0;
+#define AT(yy, xx)                                                             \
+    ((xx) >= 0 && (xx) < W && (yy) >= 0 && (yy) < H ? p[(yy) * W + (xx)] : 0.0f)
+    v00 = AT(y0, x0);
+    v01 = AT(y0, x0 + 1);
+    v10 = AT(y0 + 1, x0);
+    v11 = AT(y0 + 1, x0 + 1);
+#undef AT
+    return (1.0f - fy) * ((1.0f - fx) * v00 + fx * v01) +
+           fy * ((1.0f - fx) * v10 + fx * v11);
+}
+
+__global__ void __launch_bounds__(256)
+    grid_sample_kernel(const float *__restrict__ in, int C, int H, int W,
+                       const float2 *__restrict__ grid, int n, int align,
+                       float *__restrict__ out)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    float2 g;
+    float ix, iy;
+
+    if (i >= n)
+        return;
+    g = grid[i];
+    if (align) {
+        ix = (g.x + 1.0f) * 0.5f * (W - 1);
+        iy = (g.y + 1.0f) * 0.5f * (H - 1);
+    }
+    else {
+        ix = ((g.x + 1.0f) * W - 1.0f) * 0.5f;
+        iy = ((g.y + 1.0f) * H - 1.0f) * 0.5f;
+    }
+    /* One point per thread for every channel: the point's weights and
+     * taps are computed once, the channel planes read at the same
+     * offsets. */
+    for (int c = 0; c < C; c++)
+        out[(long long)c * n + i] =
+            bilinear_zero(in + (long long)c * H * W, H, W, ix, iy);
+}
+
+extern "C" void ops_grid_sample(struct ops *o, cl_mem in, int C, int H, int W,
+                                cl_mem grid, int n, int align_corners,
+                                cl_mem out)
+{
+    ICOREG_API_BEGIN
+    const char *op = "ops_grid_sample";
+
+    if (C < 0 || H < 1 || W < 1 || n < 0)
+        icoreg_fatal("%s: invalid sizes C=%d H=%d W=%d n=%d", op, C, H, W, n);
+    if (C == 0 || n == 0)
+        return;
+    count32((long long)C * H * W, "grid_sample input");
+    count32((long long)C * n, "grid_sample output");
+    need_floats(in, 0, (long long)C * H * W, op, "in");
+    need_floats(grid, 0, 2LL * n, op, "grid");
+    need_floats(out, 0, (long long)C * n, op, "out");
+    prof_scope ps(o->ocl, "grid_sample");
+    hipLaunchKernelGGL(grid_sample_kernel, dim3((unsigned)((n + 255) / 256)),
+                       dim3(256), 0, stream_of(o->ocl), cfptr(in), C, H, W,
+                       (const float2 *)cfptr(grid), n, align_corners,
+                       fptr(out));
+    launch_check("grid_sample");
+    ICOREG_API_END
+}
+
+/* ---- unfold ----------------------------------------------------------------- */
+
+__global__ void __launch_bounds__(256)
+    unfold_kernel(const float *__restrict__ in, int C, int H, int W, int kh,
+                  int kw, int sy, int sx, int py, int px, int Ho, int Wo,
+                  float *__restrict__ out)
+{
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long L = (long long)Ho * Wo, total = (long long)C * kh * kw * L;
+    int row, c, i, j, iy, ix;
+    long long t;
+
+    if (idx >= total)
+        return;
+    t = idx % L;
+    row = (int)(idx / L);
+    c = row / (kh * kw);
+    i = (row / kw) % kh;
+    j = row % kw;
+    iy = (int)(t / Wo) * sy - py + i;
+    ix = (int)(t % Wo) * sx - px + j;
+    out[idx] = iy >= 0 && iy < H && ix >= 0 && ix < W
+                   ? in[((long long)c * H + iy) * W + ix]
+                   : 0.0f;
+}
+
+extern "C" void ops_unfold(struct ops *o, cl_mem in, int C, int H, int W,
+                           const struct conv_geom *g, cl_mem out)
+{
+    ICOREG_API_BEGIN
+    const char *op = "ops_unfold";
+    int Ho = ops_conv_out(H, g->kh, g->sy, g->py, 1);
+    int Wo = ops_conv_out(W, g->kw, g->sx, g->px, 1);
+    long long total = (long long)C * g->kh * g->kw * Ho * Wo;
+
+    if (Ho < 1 || Wo < 1 || C < 1)
+        icoreg_fatal("%s: empty output", op);
+    count32(total, "unfold output");
+    need_floats(in, 0, (long long)C * H * W, op, "in");
+    need_floats(out, 0, total, op, "out");
+    prof_scope ps(o->ocl, "unfold");
+    hipLaunchKernelGGL(unfold_kernel, dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), 0, stream_of(o->ocl), cfptr(in), C, H, W,
+                       g->kh, g->kw, g->sy, g->sx, g->py, g->px, Ho, Wo,
+                       fptr(out));
+    launch_check("unfold");
+    ICOREG_API_END
+}
+
+/* ---- pooling ------------------------------------------------------------- */
+
+__global__ void __launch_bounds__(256)
+    avgpool2_kernel(const float *__restrict__ in, int H, int W, int C,
+                    float *__restrict__ out)
+{
+    const int w = W / 2, h = H / 2;
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long total = (long long)C * h * w;
+    int x, y, c;
+    const float *p;
+
+    if (idx >= total)
+        return;
+    x = (int)(idx % w);
+    y = (int)((idx / w) % h);
+    c = (int)(idx / ((long long)w * h));
+    p = in + ((long long)c * H + 2 * y) * W + 2 * x;
+    out[idx] = 0.25f * (p[0] + p[1] + p[W] + p[W + 1]);
+}
+
+extern "C" void ops_avgpool2(struct ops *o, cl_mem in, int C, int H, int W,
+                             cl_mem out)
+{
+    ICOREG_API_BEGIN
+    const char *op = "ops_avgpool2";
+    long long total = (long long)C * (H / 2) * (W / 2);
+
+    if (C < 0 || H < 2 || W < 2)
+        icoreg_fatal("%s: invalid sizes C=%d H=%d W=%d", op, C, H, W);
+    if (total == 0)
+        return;
+    count32((long long)C * H * W, "avgpool2 input");
+    need_floats(in, 0, (long long)C * H * W, op, "in");
+    need_floats(out, 0, total, op, "out");
+    prof_scope ps(o->ocl, "avgpool2");
+    hipLaunchKernelGGL(avgpool2_kernel, dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), 0, stream_of(o->ocl), cfptr(in), H, W, C,
+                       fptr(out));
+    launch_check("avgpool2");
+    ICOREG_API_END
+}
+
+__global__ void __launch_bounds__(256)
+    pool2d_kernel(const float *__restrict__ in, int H, int W, int Ho, int Wo,
+                  int k, int s, int pad, int ismax, int C,
+                  float *__restrict__ out)
+{
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long total = (long long)C * Ho * Wo;
+    int x, y, c;
+    const float *p;
+    float acc;
+
+    if (idx >= total)
+        return;
+    x = (int)(idx % Wo);
+    y = (int)((idx / Wo) % Ho);
+    c = (int)(idx / ((long long)Wo * Ho));
+    p = in + (long long)c * H * W;
+    acc = ismax ? -INFINITY : 0.0f;
+    for (int i = 0; i < k; i++) {
+        const int iy = y * s - pad + i;
+
+        if (iy < 0 || iy >= H)
+            continue;
+        for (int j = 0; j < k; j++) {
+            const int ix = x * s - pad + j;
+
+            if (ix < 0 || ix >= W)
+                continue;
+            acc = ismax ? fmaxf(acc, p[iy * W + ix]) : acc + p[iy * W + ix];
+        }
+    }
+    out[idx] = ismax ? acc : acc / (k * k);
+}
+
+extern "C" void ops_pool2d(struct ops *o, cl_mem in, int C, int H, int W,
+                           int ks, int s, int p, int max, cl_mem out)
+{
+    ICOREG_API_BEGIN
+    const char *op = "ops_pool2d";
+    int Ho, Wo;
+    long long total;
+
+    if (ks < 1 || s < 1 || p < 0 || C < 0)
+        icoreg_fatal("%s: invalid window k=%d s=%d p=%d", op, ks, s, p);
+    Ho = ops_conv_out(H, ks, s, p, 1);
+    Wo = ops_conv_out(W, ks, s, p, 1);
+    if (Ho < 1 || Wo < 1)
+        icoreg_fatal("%s: empty output", op);
+    total = (long long)C * Ho * Wo;
+    if (total == 0)
+        return;
+    count32((long long)C * H * W, "pool2d input");
+    need_floats(in, 0, (long long)C * H * W, op, "in");
+    need_floats(out, 0, total, op, "out");
+    prof_scope ps(o->ocl, max ? "maxpool" : "avgpool");
+    hipLaunchKernelGGL(pool2d_kernel, dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), 0, stream_of(o->ocl), cfptr(in), H, W, Ho, Wo,
+                       ks, s, p, max, C, fptr(out));
+    launch_check("pool2d");
+    ICOREG_API_END
+}

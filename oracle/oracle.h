@@ -1,0 +1,128 @@
+/* SPDX-License-Identifier: Unlicense */
+
+/* ORACLE — test infrastructure only.
+ *
+ * A plain-C CPU restatement of the kernels of i.coregistration.opencl's
+ * matcher tensor path (ops.cl, eloftr_kernels.cl, roma_kernels.cl,
+ * disk_kernels.cl) and of the network schedules that drive them, in
+ * float32 following each kernel's own arithmetic. It is the checker of
+ * the HIP library: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg load it. The product never links or calls it.
+ *
+ * Pinning (how each function is known to be right, not just retyped):
+ *  - generic ops: tests/golden/ holds outputs of torch float64 closed
+ *    forms (F.conv2d, F.layer_norm, F.scaled_dot_product_attention,
+ *    F.grid_sample, F.interpolate, ...) on the exact inputs of the
+ *    reference's tests/ops_check.c (same xorshift64 stream and cases);
+ *  - eloftr coarse / fine: brute-force torch float64 (full score matrix,
+ *    softmax over both axes, first argmax; per-match windows) on small
+ *    seeded inputs;
+ *  - RoMa / DISK kernels: torch closed forms (grid_sample with shifted
+ *    grids, depthwise conv2d, softplus, max_pool neighbourhoods) and
+ *    brute force.
+ * Functions without such a check say "parity unpinned" below.
+ *
+ * Conventions: tensors are contiguous float arrays, offsets in floats,
+ * the same argument meaning as the reference's ops.h. */
+
+#ifndef ICOREG_ORACLE_H
+#define ICOREG_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The xorshift64 stream of tests/ops_check.c:33-42 (seed
+ * 88172645463325252). */
+void orc_rng_seed(uint64_t s);
+uint64_t orc_rng_state(void);
+float orc_urand(float lo, float hi);
+void orc_rand_fill(float *v, long n, float lo, float hi);
+
+/* ops.cl:23-37 */
+float orc_act(float v, int act, float slope);
+
+/* ops.cl:39-138: batched C = act(alpha A op(B) + bias) + R. R at roff of
+ * buffer R with C's layout; R may alias C. */
+void orc_gemm(int M, int N, int K, const float *A, long aoff, int lda,
+              long sa0, long sa1, const float *B, long boff, int ldb,
+              long sb0, long sb1, int transb, float *C, long coff, int ldc,
+              long sc0, long sc1, int nb, int nb1, const float *bias,
+              int biasrow, const float *R, long roff, float alpha, int act,
+              float slope);
+
+/* ops.cl:389-448 (covers conv5x5 :319-387 and im2col + GEMM, which
+ * compute the same sums). */
+void orc_conv2d(const float *in, int C, int H, int W, const float *w,
+                const float *b, int K, int kh, int kw, int sy, int sx, int py,
+                int px, int dy, int dx, int groups, const float *mean,
+                const float *rstd, const float *alpha, int act, float slope,
+                float *out);
+
+void orc_chan_stats(const float *x, int C, int HW, float eps, float *mean,
+                    float *rstd);                              /* :450-492 */
+void orc_chan_affine(const float *X, float *Y, int C, int HW,
+                     const float *mean, const float *rstd, const float *g,
+                     const float *b, int act, float slope);    /* :494-519 */
+void orc_prelu(const float *X, float *Y, int C, int HW,
+               const float *alpha);                            /* :521-532 */
+void orc_act_map(const float *X, float *Y, long n, int act,
+                 float slope);                                 /* :534-542 */
+void orc_layernorm(long rows, int C, const float *X, float *Y, const float *g,
+                   const float *b, float eps, int act, float slope); /* :544 */
+void orc_softmax_rows(float *S, long rows, int L, float scale); /* :580-602 */
+/* ops.cl:604-687; kmask bytes (NULL: none). */
+void orc_attention(const float *Q, long qoff, int ldq, const float *K,
+                   long koff, int ldk, const float *V, long voff, int ldv,
+                   float *O, long ooff, int ldo, int Nq, int Nk, int nh, int d,
+                   float scale, const unsigned char *kmask);
+void orc_rope(float *X, long off, int ld, long rows, int nh, int d, int npos,
+              const float *cs, int interleaved);               /* :689-716 */
+void orc_resize(const float *in, int C, int h, int w, float *out, int H, int W,
+                int coff, int align_corners, float scale);     /* :718-754 */
+void orc_grid_sample(const float *in, int C, int H, int W, const float *grid,
+                     int n, int align_corners, float *out);    /* :756-793 */
+void orc_unfold(const float *in, int C, int H, int W, int kh, int kw, int sy,
+                int sx, int py, int px, float *out);           /* :795-816 */
+void orc_avgpool2(const float *in, int C, int H, int W, float *out);
+void orc_pool2d(const float *in, int C, int H, int W, int k, int s, int p,
+                int max, float *out);                          /* :832-860 */
+void orc_transpose(const float *in, float *out, int B, int R, int C);
+void orc_axpby(float *out, const float *a, float alpha, const float *b,
+               float beta, long n, long bmod);                 /* :882-893 */
+/* ops.c:612-626 */
+void orc_fold_bn(float *w, float *b, int K, long per, const float *gamma,
+                 const float *beta, const float *mean, const float *var,
+                 float eps);
+
+/* ---- ELoFTR (eloftr_kernels.cl, eloftr.c) ------------------------------ */
+
+/* Coarse dual-softmax statistics and argmaxes of the n x n score matrix
+ * S = alpha F0 F1^T (F0, F1 token-major n x D), eloftr_kernels.cl:10-144
+ * as scheduled by eloftr.c:498-548 (row blocks of blk rows): row_max,
+ * row_arg, col_arg (n each). Also returns the row margin (top-1 minus
+ * top-2 confidence) when margin is not NULL. */
+void orc_eloftr_coarse(const float *F0, const float *F1, int n, int D,
+                       float alpha, int blk, float *row_max, int *row_arg,
+                       int *col_arg, float *row_margin, float *col_margin);
+
+/* Host mutual / threshold / border selection, eloftr.c:552-566. Returns
+ * the match count; mi, mj, mconf sized n. */
+int orc_eloftr_select(const float *row_max, const int *row_arg,
+                      const int *col_arg, int h, int w, float thr, int border,
+                      int *mi, int *mj, float *mconf);
+
+/* Two-stage fine matching, eloftr_kernels.cl:146-295: f0, f1 (64, H, W),
+ * cells (x0, y0, x1, y1) per match, out (x0, y0, x1, y1) per match.
+ * margin (NULL or M floats) gets the first-stage top-2 margin. */
+void orc_eloftr_fine(const float *f0, const float *f1, int H, int W,
+                     const int *cells, int M, float T, float *out,
+                     float *margin);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ICOREG_ORACLE_H */

@@ -1,0 +1,76 @@
+# SPDX-License-Identifier: Unlicense
+"""GPU: every generic op of the HIP library on the reference's own 33
+kernel-check cases (tests/ops_check.c:448-487 of i.coregistration.opencl,
+same xorshift64 inputs), against the torch-float64 golden outputs at the
+reference's bar (2e-5 of the largest reference magnitude,
+ops_compare.py:26) and against the oracle."""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import opcases
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "ops_check_golden.npz"
+CASES = opcases.all_cases()
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN)
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c.name for c in CASES])
+def test_op_case(case, dev, ic, orc, golden):
+    print(f"[case] {case.name}", flush=True)
+    got = opcases.hip_run(dev, case, ic)
+    ora = opcases.oracle_run(orc, case)
+    for name, v in got.items():
+        ref = golden[f"{case.name}/{name}"]
+        assert v.size == ref.size, name
+        assert np.isfinite(v).all(), name
+        err = opcases.rel_err(v, ref)
+        assert err <= opcases.TOL, f"{case.name}/{name}: {err:.2e} vs golden"
+        err_o = opcases.rel_err(v, ora[name])
+        assert err_o <= opcases.TOL, f"{case.name}/{name}: {err_o:.2e} vs oracle"
+
+
+ATT_SHAPES = [
+    # (Nq, Nk, nh, d, masked): ELoFTR 400 x 400, 8 x 32; RoMa ViT 16 x 64 and
+    # decoder 8 x 128 (reduced token counts); odd sizes and masks.
+    (400, 400, 8, 32, 0),
+    (97, 161, 4, 64, 0),
+    (64, 100, 2, 128, 0),
+    (64, 100, 2, 128, 1),
+    (50, 77, 3, 40, 1),
+    (33, 65, 1, 96, 0),
+    (40, 45, 2, 17, 1),
+]
+
+
+@pytest.mark.parametrize("shape", ATT_SHAPES, ids=[str(s) for s in ATT_SHAPES])
+def test_attention_shapes(shape, dev, ic, orc):
+    Nq, Nk, nh, d, masked = shape
+    print(f"[attention] {shape}", flush=True)
+    rng = np.random.default_rng(1234 + d)
+    E = nh * d
+    q = rng.uniform(-2, 2, Nq * E).astype(np.float32)
+    k = rng.uniform(-2, 2, Nk * E).astype(np.float32)
+    v = rng.uniform(-2, 2, Nk * E).astype(np.float32)
+    mask = (rng.uniform(0, 1, Nk) > 0.3).astype(np.uint8) if masked else None
+    scale = float(1.0 / np.sqrt(d))
+    ref = np.zeros(Nq * E, np.float32)
+    from oracle_lib import fp
+    orc.orc_attention(fp(q), 0, E, fp(k), 0, E, fp(v), 0, E, fp(ref), 0, E, Nq, Nk,
+                      nh, d, scale, mask.ctypes.data if mask is not None else None)
+    Q, K, V = dev.upload(q), dev.upload(k), dev.upload(v)
+    O = dev.zeros(Nq * E)
+    Mk = dev.upload(mask) if masked else None
+    dev.api.ops_attention(dev.po, ic.mat(Q, 0, E), ic.mat(K, 0, E), ic.mat(V, 0, E),
+                          ic.mat(O, 0, E), Nq, Nk, nh, d, scale, ic.mem(Mk))
+    got = dev.read(O, Nq * E)
+    err = opcases.rel_err(got, ref)
+    assert err <= 1e-5, f"{shape}: {err:.2e}"
