@@ -129,12 +129,47 @@ SIGNATURES = {
     "ops_transpose": (None, [_O, Mem, Mem, _I, _I, _I]),
     "ops_axpby": (None, [_O, Mem, Mem, _F, Mem, _F, _L, _L]),
     "ops_fold_bn": (None, [_P, _P, _I, _L, _P, _P, _P, _P, _F]),
+    "ocl_fill_u32": (None, [_B, Mem, C.c_size_t, C.c_size_t, C.c_uint32]),
+    # checkpoints (include/pth_loader.h)
+    "pth_open": (None, [_P, _S]),
+    "pth_close": (None, [_P]),
+    "pth_find": (_P, [_P, _S]),
+    "pth_require": (_P, [_P, _S, _I, C.POINTER(C.c_long)]),
+    "pth_strip_prefix": (_I, [_P, _S]),
+    "pth_numel": (C.c_long, [_P]),
+    "pth_bytes": (C.c_double, [_P, _S]),
+    "pth_read_f32": (C.POINTER(C.c_float), [_P, _P]),
+    # ELoFTR (include/eloftr.h, include/icoreg_kernels.h)
+    "eloftr_load": (None, [_P, _O, _P]),
+    "eloftr_alloc": (None, [_P, _I, _I]),
+    "eloftr_match": (None, [_P, _P, _P, _S, _I]),
+    "eloftr_match_device": (None, [_P, Mem, Mem]),
+    "eloftr_free": (None, [_P]),
+    "eloftr_row_lse": (None, [_O, Mem, _I, _I, _I, Mem]),
+    "eloftr_col_lse": (None, [_O, Mem, _I, _I, Mem, Mem]),
+    "eloftr_conf_row": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
+    "eloftr_conf_col": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
+    "eloftr_fine": (None, [_O, Mem, Mem, _I, _I, Mem, _I, _F, Mem]),
+    # binding glue (include/icoreg_glue.h)
+    "icoreg_pth_new": (_P, []),
+    "icoreg_eloftr_new": (_P, []),
+    "icoreg_struct_delete": (None, [_P]),
+    "icoreg_eloftr_result": (_I, [_P, C.POINTER(C.POINTER(C.c_int)), C.POINTER(C.POINTER(C.c_int)),
+                                  C.POINTER(C.POINTER(C.c_float)), C.POINTER(C.POINTER(C.c_float))]),
+    "icoreg_eloftr_coarse_stats": (_I, [_P, C.POINTER(C.POINTER(C.c_float)),
+                                        C.POINTER(C.POINTER(C.c_int)), C.POINTER(C.POINTER(C.c_int))]),
+    "icoreg_eloftr_set_pos_scale": (None, [_P, _F]),
+    "icoreg_eloftr_buffer": (Mem, [_P, _S]),
 }
 
 # Entry points that never raise through the fatal path (no error check).
 _NO_CHECK = {"icoreg_set_fatal_mode", "icoreg_last_error", "icoreg_clear_error",
              "ocl_errstr", "ops_mat", "ops_bmat", "ops_geom", "ops_conv_out",
-             "ocl_wrap", "icoreg_prof_entry", "icoreg_prof_reset", "ops_report"}
+             "ocl_wrap", "icoreg_prof_entry", "icoreg_prof_reset", "ops_report",
+             "pth_find", "pth_numel", "pth_bytes", "pth_strip_prefix",
+             "icoreg_pth_new", "icoreg_eloftr_new", "icoreg_struct_delete",
+             "icoreg_eloftr_result", "icoreg_eloftr_coarse_stats",
+             "icoreg_eloftr_set_pos_scale", "icoreg_eloftr_buffer"}
 
 _lib = None
 
@@ -290,3 +325,57 @@ def mem(buf):
 
 def geom(kh, kw, sy, sx, py, px, dy, dx, groups):
     return ConvGeom(kh, kw, sy, sx, py, px, dy, dx, groups)
+
+
+class Eloftr:
+    """Efficient LoFTR on the device: eloftr_load / eloftr_alloc /
+    eloftr_match of the C-ABI, weights from a safetensors file."""
+
+    def __init__(self, dev, weights_path, H, W, pos_scale=1.0):
+        self.dev = dev
+        a = dev.api
+        self.pf = lib().icoreg_pth_new()
+        a.pth_open(self.pf, str(weights_path).encode())
+        self.m = lib().icoreg_eloftr_new()
+        a.eloftr_load(self.m, dev.po, self.pf)
+        lib().icoreg_eloftr_set_pos_scale(self.m, pos_scale)
+        a.eloftr_alloc(self.m, H, W)
+        self.H, self.W = H, W
+        self.h, self.w = H // 8, W // 8
+
+    def match(self, g0, g1, dump=None, tile=1):
+        g0 = np.ascontiguousarray(g0, np.float32)
+        g1 = np.ascontiguousarray(g1, np.float32)
+        self.dev.api.eloftr_match(self.m, g0.ctypes.data, g1.ctypes.data,
+                                  dump.encode() if dump else None, tile)
+        return self.result()
+
+    def match_device(self, b0, b1):
+        self.dev.api.eloftr_match_device(self.m, b0.mem, b1.mem)
+
+    def result(self):
+        mi, mj = C.POINTER(C.c_int)(), C.POINTER(C.c_int)()
+        mc, kp = C.POINTER(C.c_float)(), C.POINTER(C.c_float)()
+        nm = lib().icoreg_eloftr_result(self.m, C.byref(mi), C.byref(mj), C.byref(mc), C.byref(kp))
+        rm, ra, ca = C.POINTER(C.c_float)(), C.POINTER(C.c_int)(), C.POINTER(C.c_int)()
+        n = lib().icoreg_eloftr_coarse_stats(self.m, C.byref(rm), C.byref(ra), C.byref(ca))
+        arr = lambda p, k: np.ctypeslib.as_array(p, (k,)).copy() if k else np.zeros(0)
+        return {"nm": nm, "mi": arr(mi, nm), "mj": arr(mj, nm), "mconf": arr(mc, nm),
+                "kp": arr(kp, 4 * nm).reshape(-1, 4), "row_max": arr(rm, n),
+                "row_arg": arr(ra, n), "col_arg": arr(ca, n)}
+
+    def buffer(self, name, count):
+        mem = lib().icoreg_eloftr_buffer(self.m, name.encode())
+        out = np.empty(count, np.float32)
+        self.dev.api.ocl_read(self.dev.pb, mem, 0, out.ctypes.data, out.nbytes)
+        return out
+
+    def close(self):
+        if self.m:
+            self.dev.api.eloftr_free(self.m)
+            lib().icoreg_struct_delete(self.m)
+            self.m = None
+        if self.pf:
+            self.dev.api.pth_close(self.pf)
+            lib().icoreg_struct_delete(self.pf)
+            self.pf = None

@@ -13,6 +13,7 @@
 #include <string>
 
 #include "hip_backend.h"
+#include "ops.h"
 
 namespace icoreg {
 
@@ -65,6 +66,10 @@ inline hipStream_t stream_of(struct ocl_backend *ocl)
 
 /* Check the launch just queued (launch-configuration errors). */
 void launch_check(const char *what);
+
+/* The ops work buffer (struct ops.scratch), grown to at least bytes.
+ * Growing synchronises the stream first (the old buffer may be in use). */
+cl_mem scratch_get(struct ops *o, size_t bytes);
 
 } // namespace icoreg
 

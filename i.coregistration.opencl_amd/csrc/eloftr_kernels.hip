@@ -1,0 +1,535 @@
+/* SPDX-License-Identifier: Unlicense */
+
+/* ELoFTR's own kernels on gfx950: the coarse dual-softmax statistics and
+ * argmaxes over a block of score rows, and the two-stage fine matching.
+ * Contracts of eloftr_kernels.cl:10-295 (i.coregistration.opencl).
+ *
+ * Row kernels: one wave64 per score row, 16-byte loads, cross-lane
+ * reductions. Column kernels: the reference walks each column over all
+ * rows of the block with one work-item per column (n = 6400 work-items,
+ * a few percent of 256 CUs); here the rows are cut into chunks of 64,
+ * one thread per (column, chunk) with coalesced row reads, and a second
+ * kernel merges the chunk results per column in increasing row order,
+ * so that the running statistics and the first-argmax rule are those of
+ * the sequential scan. Argmax merges break ties to the lowest index.
+ *
+ * Fine matching: one block per match; both feature windows (8 x 8 of
+ * image 0, 10 x 10 of image 1, 64 channels) staged in LDS once, the
+ * 64 x 100 first-stage scores computed on the matrix cores
+ * (v_mfma_f32_32x32x2f32, 8 output tiles over 4 waves), the softmax
+ * statistics, argmax and the 3 x 3 second stage read from LDS. */
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+
+#include "common.h"
+#include "icoreg_kernels.h"
+#include "reduce.h"
+
+using namespace icoreg;
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+#define COL_CHUNK 64
+
+/* ---- rows ----------------------------------------------------------------- */
+
+__global__ void __launch_bounds__(256)
+    row_lse_kernel(const float *__restrict__ S, int rows, int N, int r0,
+                   float *__restrict__ lse)
+{
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const float *s;
+    float m = -INFINITY, sum = 0.0f;
+
+    if (r >= rows)
+        return;
+    s = S + (long long)r * N;
+    for (int j = lane; j < N; j += 64)
+        m = fmaxf(m, s[j]);
+    m = wave_max(m);
+    for (int j = lane; j < N; j += 64)
+        sum += expf(s[j] - m);
+    sum = wave_sum(sum);
+    if (lane == 0)
+        lse[r0 + r] = m + logf(sum);
+}
+
+/* lc[j] = cm[j] + log(cs[j]): the column log-sum-exp, as dual_conf
+ * (eloftr_kernels.cl:69-72) forms it. */
+__global__ void __launch_bounds__(256)
+    col_logz_kernel(const float *__restrict__ cm, const float *__restrict__ cs,
+                    int N, float *__restrict__ lc)
+{
+    const int j = blockIdx.x * 256 + threadIdx.x;
+
+    if (j < N)
+        lc[j] = cm[j] + logf(cs[j]);
+}
+
+__device__ __forceinline__ float dual_conf(float s, float lr, float lc)
+{
+    return expf(s - lr) * expf(s - lc);
+}
+
+__global__ void __launch_bounds__(256)
+    conf_row_kernel(const float *__restrict__ S, int rows, int N, int r0,
+                    const float *__restrict__ lse, const float *__restrict__ lc,
+                    float *__restrict__ rmax, int *__restrict__ rarg)
+{
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const float *s;
+    float best = -1.0f, lr;
+    int bi = 0;
+
+    if (r >= rows)
+        return;
+    s = S + (long long)r * N;
+    lr = lse[r0 + r];
+    for (int j = lane; j < N; j += 64) {
+        const float c = dual_conf(s[j], lr, lc[j]);
+
+        if (c > best) {
+            best = c;
+            bi = j;
+        }
+    }
+    wave_argmax(best, bi);
+    if (lane == 0) {
+        rmax[r0 + r] = best;
+        rarg[r0 + r] = bi;
+    }
+}
+
+/* ---- columns ---------------------------------------------------------------- */
+
+/* Chunk c of the block's rows: column maximum and sum of exp(x - max). */
+__global__ void __launch_bounds__(256)
+    col_lse_part_kernel(const float *__restrict__ S, int R, int N,
+                        float2 *__restrict__ part)
+{
+    const int j = blockIdx.x * 256 + threadIdx.x, c = blockIdx.y;
+    const int ra = c * COL_CHUNK, rb = min(R, ra + COL_CHUNK);
+    float m = -INFINITY, s = 0.0f;
+
+    if (j >= N)
+        return;
+    for (int r = ra; r < rb; r++)
+        m = fmaxf(m, S[(long long)r * N + j]);
+    for (int r = ra; r < rb; r++)
+        s += expf(S[(long long)r * N + j] - m);
+    part[(long long)c * N + j] = make_float2(m, s);
+}
+
+/* Chunks merged in order into the block's (max, sum), then into the
+ * running (cm, cs) as eloftr_col_lse does (eloftr_kernels.cl:62-65). */
+__global__ void __launch_bounds__(256)
+    col_lse_merge_kernel(const float2 *__restrict__ part, int nchunks, int N,
+                         float *__restrict__ cm, float *__restrict__ cs)
+{
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    float m = -INFINITY, s = 0.0f, mo, mn;
+
+    if (j >= N)
+        return;
+    for (int c = 0; c < nchunks; c++) {
+        const float2 p = part[(long long)c * N + j];
+        const float m2 = fmaxf(m, p.x);
+
+        if (m2 == -INFINITY)
+            continue;
+        s = (m == -INFINITY ? 0.0f : s * expf(m - m2)) +
+            (p.x == -INFINITY ? 0.0f : p.y * expf(p.x - m2));
+        m = m2;
+    }
+    mo = cm[j];
+    mn = fmaxf(mo, m);
+    cs[j] = (mo == -INFINITY ? 0.0f : cs[j] * expf(mo - mn)) + s * expf(m - mn);
+    cm[j] = mn;
+}
+
+/* Chunk c: column maximum of the confidence and its first row. */
+__global__ void __launch_bounds__(256)
+    conf_col_part_kernel(const float *__restrict__ S, int R, int N, int r0,
+                         const float *__restrict__ lse,
+                         const float *__restrict__ lc, float *__restrict__ pv,
+                         int *__restrict__ pi)
+{
+    const int j = blockIdx.x * 256 + threadIdx.x, c = blockIdx.y;
+    const int ra = c * COL_CHUNK, rb = min(R, ra + COL_CHUNK);
+    float best = -1.0f, l;
+    int bi = -1;
+
+    if (j >= N)
+        return;
+    l = lc[j];
+    for (int r = ra; r < rb; r++) {
+        const float v = dual_conf(S[(long long)r * N + j], lse[r0 + r], l);
+
+        if (v > best) {
+            best = v;
+            bi = r0 + r;
+        }
+    }
+    pv[(long long)c * N + j] = best;
+    pi[(long long)c * N + j] = bi;
+}
+
+/* Chunks merged in increasing row order with a strict comparison, from
+ * the running state (cmax, carg): the first row reaching the maximum
+ * wins, as in the sequential scan of eloftr_conf_col. */
+__global__ void __launch_bounds__(256)
+    conf_col_merge_kernel(const float *__restrict__ pv,
+                          const int *__restrict__ pi, int nchunks, int N,
+                          float *__restrict__ cmax, int *__restrict__ carg)
+{
+    const int j = blockIdx.x * 256 + threadIdx.x;
+    float best;
+    int bi;
+
+    if (j >= N)
+        return;
+    best = cmax[j];
+    bi = carg[j];
+    for (int c = 0; c < nchunks; c++) {
+        const float v = pv[(long long)c * N + j];
+
+        if (v > best) {
+            best = v;
+            bi = pi[(long long)c * N + j];
+        }
+    }
+    cmax[j] = best;
+    carg[j] = bi;
+}
+
+/* ---- launchers --------------------------------------------------------------- */
+
+static void check_block(cl_mem S, int rows, int N, const char *op)
+{
+    if (rows < 0 || N < 1)
+        icoreg_fatal("%s: invalid sizes rows=%d N=%d", op, rows, N);
+    need_floats(S, 0, (long long)rows * N, op, "S");
+}
+
+extern "C" void eloftr_row_lse(struct ops *o, cl_mem S, int rows, int N,
+                               int r0, cl_mem lse)
+{
+    ICOREG_API_BEGIN
+    const char *op = "eloftr_row_lse";
+
+    check_block(S, rows, N, op);
+    if (rows == 0)
+        return;
+    need_floats(lse, r0, rows, op, "lse");
+    prof_scope ps(o->ocl, op);
+    hipLaunchKernelGGL(row_lse_kernel, dim3((rows + 3) / 4), dim3(256), 0,
+                       stream_of(o->ocl), cfptr(S), rows, N, r0, fptr(lse));
+    launch_check(op);
+    ICOREG_API_END
+}
+
+extern "C" void eloftr_col_lse(struct ops *o, cl_mem S, int R, int N,
+                               cl_mem cm, cl_mem cs)
+{
+    ICOREG_API_BEGIN
+    const char *op = "eloftr_col_lse";
+    int nch = (R + COL_CHUNK - 1) / COL_CHUNK;
+    cl_mem part;
+
+    check_block(S, R, N, op);
+    if (R == 0)
+        return;
+    need_floats(cm, 0, N, op, "cm");
+    need_floats(cs, 0, N, op, "cs");
+    part = scratch_get(o, (size_t)nch * N * sizeof(float2));
+    prof_scope ps(o->ocl, op);
+    hipLaunchKernelGGL(col_lse_part_kernel, dim3((N + 255) / 256, nch),
+                       dim3(256), 0, stream_of(o->ocl), cfptr(S), R, N,
+                       (float2 *)part->ptr);
+    hipLaunchKernelGGL(col_lse_merge_kernel, dim3((N + 255) / 256), dim3(256),
+                       0, stream_of(o->ocl), (const float2 *)part->ptr, nch, N,
+                       fptr(cm), fptr(cs));
+    launch_check(op);
+    ICOREG_API_END
+}
+
+extern "C" void eloftr_conf_row(struct ops *o, cl_mem S, int rows, int N,
+                                int r0, cl_mem lse, cl_mem cm, cl_mem cs,
+                                cl_mem rmax, cl_mem rarg)
+{
+    ICOREG_API_BEGIN
+    const char *op = "eloftr_conf_row";
+    cl_mem lc;
+
+    check_block(S, rows, N, op);
+    if (rows == 0)
+        return;
+    need_floats(lse, r0, rows, op, "lse");
+    need_floats(cm, 0, N, op, "cm");
+    need_floats(cs, 0, N, op, "cs");
+    need_floats(rmax, r0, rows, op, "rmax");
+    need_bytes(rarg, 4LL * r0, 4LL * rows, op, "rarg");
+    lc = scratch_get(o, (size_t)N * sizeof(float));
+    prof_scope ps(o->ocl, op);
+    hipLaunchKernelGGL(col_logz_kernel, dim3((N + 255) / 256), dim3(256), 0,
+                       stream_of(o->ocl), cfptr(cm), cfptr(cs), N, fptr(lc));
+    hipLaunchKernelGGL(conf_row_kernel, dim3((rows + 3) / 4), dim3(256), 0,
+                       stream_of(o->ocl), cfptr(S), rows, N, r0, cfptr(lse),
+                       cfptr(lc), fptr(rmax), (int *)rarg->ptr);
+    launch_check(op);
+    ICOREG_API_END
+}
+
+extern "C" void eloftr_conf_col(struct ops *o, cl_mem S, int R, int N, int r0,
+                                cl_mem lse, cl_mem cm, cl_mem cs, cl_mem cmax,
+                                cl_mem carg)
+{
+    ICOREG_API_BEGIN
+    const char *op = "eloftr_conf_col";
+    int nch = (R + COL_CHUNK - 1) / COL_CHUNK;
+    size_t lc_bytes, pv_bytes;
+    cl_mem sc;
+    char *base;
+
+    check_block(S, R, N, op);
+    if (R == 0)
+        return;
+    need_floats(lse, r0, R, op, "lse");
+    need_floats(cm, 0, N, op, "cm");
+    need_floats(cs, 0, N, op, "cs");
+    need_floats(cmax, 0, N, op, "cmax");
+    need_bytes(carg, 0, 4LL * N, op, "carg");
+    lc_bytes = ((size_t)N * 4 + 255) & ~(size_t)255;
+    pv_bytes = ((size_t)nch * N * 4 + 255) & ~(size_t)255;
+    sc = scratch_get(o, lc_bytes + 2 * pv_bytes);
+    base = (char *)sc->ptr;
+    prof_scope ps(o->ocl, op);
+    hipLaunchKernelGGL(col_logz_kernel, dim3((N + 255) / 256), dim3(256), 0,
+                       stream_of(o->ocl), cfptr(cm), cfptr(cs), N,
+                       (float *)base);
+    hipLaunchKernelGGL(conf_col_part_kernel, dim3((N + 255) / 256, nch),
+                       dim3(256), 0, stream_of(o->ocl), cfptr(S), R, N, r0,
+                       cfptr(lse), (const float *)base,
+                       (float *)(base + lc_bytes),
+                       (int *)(base + lc_bytes + pv_bytes));
+    hipLaunchKernelGGL(conf_col_merge_kernel, dim3((N + 255) / 256), dim3(256),
+                       0, stream_of(o->ocl), (const float *)(base + lc_bytes),
+                       (const int *)(base + lc_bytes + pv_bytes), nch, N,
+                       fptr(cmax), (int *)carg->ptr);
+    launch_check(op);
+    ICOREG_API_END
+}
+
+/* ---- fine matching ------------------------------------------------------------ */
+
+#define FW 8           /* window of image 0 */
+#define FW1 10         /* window of image 1 (one cell of padding) */
+#define FC 64          /* fine channels */
+#define FS 8           /* second-stage channels (the last ones) */
+#define NP (FW * FW)   /* 64 positions in image 0 */
+#define NQ (FW1 * FW1) /* 100 positions in image 1 */
+#define WP (FC + 1)    /* LDS row pitch of the windows */
+#define SP (NQ + 1)    /* LDS row pitch of the scores */
+
+__global__ void __launch_bounds__(256)
+    fine_kernel(const float *__restrict__ f0, const float *__restrict__ f1,
+                int H, int W, const int4 *__restrict__ cells, int M, float T,
+                float4 *__restrict__ out)
+{
+    __shared__ float A[NP * WP];
+    __shared__ float B[NQ * WP];
+    __shared__ float sc[NP * SP];
+    __shared__ float pm[NQ], ps[NQ], qm[NP], qs[NP];
+    __shared__ float rv[4], s2[9];
+    __shared__ int ri[4];
+    const int k = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int wave = tid >> 6, half = lane >> 5, col = lane & 31;
+    const long long plane = (long long)H * W;
+    int4 cl;
+
+    if (k >= M)
+        return;
+    cl = cells[k];
+
+    /* Windows into LDS, [position][channel], zero outside the image. */
+    for (int e = tid; e < FC * NP; e += 256) {
+        const int c = e / NP, p = e % NP;
+        const int x = cl.x * FW + p % FW, y = cl.y * FW + p / FW;
+
+        A[p * WP + c] = (x >= 0 && y >= 0 && x < W && y < H)
+                            ? f0[c * plane + (long long)y * W + x]
+                            : 0.0f;
+    }
+    for (int e = tid; e < FC * NQ; e += 256) {
+        const int c = e / NQ, q = e % NQ;
+        const int x = cl.z * FW - 1 + q % FW1, y = cl.w * FW - 1 + q / FW1;
+
+        B[q * WP + c] = (x >= 0 && y >= 0 && x < W && y < H)
+                            ? f1[c * plane + (long long)y * W + x]
+                            : 0.0f;
+    }
+    __syncthreads();
+
+    /* First-stage scores on the first FC - FS channels / FC: wave w owns
+     * image-0 rows (w / 2) * 32.. and image-1 columns (w % 2) * 64.. as
+     * two 32 x 32 MFMA tiles (columns past NQ are zero). */
+    {
+        const int pt = wave >> 1, qb = (wave & 1) * 64;
+        floatx16 acc[2];
+
+        for (int j = 0; j < 2; j++)
+            for (int r = 0; r < 16; r++)
+                acc[j][r] = 0.0f;
+#pragma unroll 4
+        for (int st = 0; st < (FC - FS) / 2; st++) {
+            const int c = 2 * st + half;
+            const float a = A[(pt * 32 + col) * WP + c];
+
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int q = qb + j * 32 + col;
+                const float b = q < NQ ? B[q * WP + c] : 0.0f;
+
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[j], 0,
+                                                              0, 0);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int q = qb + j * 32 + col;
+
+            if (q >= NQ)
+                continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int p = pt * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+
+                sc[p * SP + q] = acc[j][r] * (1.0f / FC);
+            }
+        }
+    }
+    __syncthreads();
+
+    /* Softmax statistics over image 0's positions (per q) and over image
+     * 1's positions (per p). */
+    if (tid < NQ) {
+        const int q = tid;
+        float m = -INFINITY, s = 0.0f;
+
+        for (int p = 0; p < NP; p++)
+            m = fmaxf(m, sc[p * SP + q]);
+        for (int p = 0; p < NP; p++)
+            s += expf(sc[p * SP + q] - m);
+        pm[q] = m;
+        ps[q] = s;
+    }
+    else if (tid >= 128 && tid < 128 + NP) {
+        const int p = tid - 128;
+        float m = -INFINITY, s = 0.0f;
+
+        for (int q = 0; q < NQ; q++)
+            m = fmaxf(m, sc[p * SP + q]);
+        for (int q = 0; q < NQ; q++)
+            s += expf(sc[p * SP + q] - m);
+        qm[p] = m;
+        qs[p] = s;
+    }
+    __syncthreads();
+
+    /* First argmax over (p, inner 8 x 8 of image 1) in the flattened
+     * order p * 64 + i * 8 + j. */
+    {
+        float best = -1.0f;
+        int bi = 0;
+
+        for (int e = tid; e < NP * FW * FW; e += 256) {
+            const int pp = e / (FW * FW), ii = (e / FW) % FW, jj = e % FW;
+            const int qq = (ii + 1) * FW1 + jj + 1;
+            const float s = sc[pp * SP + qq];
+            const float v =
+                expf(s - pm[qq]) / ps[qq] * (expf(s - qm[pp]) / qs[pp]);
+
+            if (v > best) {
+                best = v;
+                bi = e;
+            }
+        }
+        wave_argmax(best, bi);
+        if (lane == 0) {
+            rv[wave] = best;
+            ri[wave] = bi;
+        }
+    }
+    __syncthreads();
+    {
+        float best = rv[0];
+        int bi = ri[0];
+
+        for (int w = 1; w < 4; w++)
+            argmax_merge(best, bi, rv[w], ri[w]);
+        {
+            const int bp = bi / (FW * FW), bq = bi % (FW * FW);
+            const int qi = bq / FW, qj = bq % FW;
+
+            /* Second stage: 3 x 3 around the 10 x 10 indices (qi, qj),
+             * index -1 wrapping to 9 as the reference. */
+            if (tid < 9) {
+                const int ii = (qi + tid / 3 - 1 + FW1) % FW1;
+                const int jj = (qj + tid % 3 - 1 + FW1) % FW1;
+                const float *a = A + bp * WP, *b = B + (ii * FW1 + jj) * WP;
+                float d = 0.0f;
+
+                for (int c = FC - FS; c < FC; c++)
+                    d = fmaf(a[c], b[c], d);
+                s2[tid] = d * (1.0f / sqrtf((float)FS)) / T;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                float m = -INFINITY, s = 0.0f, ex = 0.0f, ey = 0.0f;
+
+                for (int t = 0; t < 9; t++)
+                    m = fmaxf(m, s2[t]);
+                for (int t = 0; t < 9; t++)
+                    s += expf(s2[t] - m);
+                for (int t = 0; t < 9; t++) {
+                    const float w = expf(s2[t] - m) / s;
+
+                    ex += w * (t % 3 - 1);
+                    ey += w * (t / 3 - 1);
+                }
+                out[k] = make_float4(cl.x * FW + bp % FW - (FW / 2 - 0.5f),
+                                     cl.y * FW + bp / FW - (FW / 2 - 0.5f),
+                                     cl.z * FW + qj - (FW / 2 - 0.5f) + ex,
+                                     cl.w * FW + qi - (FW / 2 - 0.5f) + ey);
+            }
+        }
+    }
+}
+
+extern "C" void eloftr_fine(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
+                            cl_mem cells, int M, float T, cl_mem out)
+{
+    ICOREG_API_BEGIN
+    const char *op = "eloftr_fine";
+
+    if (M < 0 || H < 1 || W < 1)
+        icoreg_fatal("%s: invalid sizes M=%d H=%d W=%d", op, M, H, W);
+    if (M == 0)
+        return;
+    need_floats(f0, 0, (long long)FC * H * W, op, "f0");
+    need_floats(f1, 0, (long long)FC * H * W, op, "f1");
+    need_bytes(cells, 0, 16LL * M, op, "cells");
+    need_floats(out, 0, 4LL * M, op, "out");
+    if (((uintptr_t)cells->ptr & 15) || ((uintptr_t)out->ptr & 15))
+        icoreg_fatal("%s: cells and out must be 16-byte aligned", op);
+    prof_scope ps(o->ocl, op);
+    hipLaunchKernelGGL(fine_kernel, dim3(M), dim3(256), 0, stream_of(o->ocl),
+                       cfptr(f0), cfptr(f1), H, W, (const int4 *)cells->ptr, M,
+                       T, (float4 *)out->ptr);
+    launch_check(op);
+    ICOREG_API_END
+}

@@ -1,0 +1,73 @@
+/* SPDX-License-Identifier: Unlicense */
+
+/* Struct allocation and result access for bindings (icoreg_glue.h). */
+
+#include <stdlib.h>
+#include <string.h>
+
+#include "icoreg_glue.h"
+
+extern "C" struct pth_file *icoreg_pth_new(void)
+{
+    return (struct pth_file *)calloc(1, sizeof(struct pth_file));
+}
+
+extern "C" struct eloftr_model *icoreg_eloftr_new(void)
+{
+    return (struct eloftr_model *)calloc(1, sizeof(struct eloftr_model));
+}
+
+extern "C" void icoreg_struct_delete(void *p) { free(p); }
+
+extern "C" int icoreg_eloftr_result(const struct eloftr_model *m,
+                                    const int **mi, const int **mj,
+                                    const float **mconf, const float **kp)
+{
+    *mi = m->mi;
+    *mj = m->mj;
+    *mconf = m->mconf;
+    *kp = m->kp;
+    return m->nm;
+}
+
+extern "C" int icoreg_eloftr_coarse_stats(const struct eloftr_model *m,
+                                          const float **row_max,
+                                          const int **row_arg,
+                                          const int **col_arg)
+{
+    *row_max = m->h_rmax;
+    *row_arg = m->h_rarg;
+    *col_arg = m->h_carg;
+    return m->h * m->w;
+}
+
+extern "C" void icoreg_eloftr_set_pos_scale(struct eloftr_model *m, float s)
+{
+    m->pos_scale = s;
+}
+
+extern "C" cl_mem icoreg_eloftr_buffer(const struct eloftr_model *m,
+                                       const char *name)
+{
+    static const struct {
+        const char *name;
+        size_t off;
+    } tab[] = {
+        {"x0", offsetof(struct eloftr_model, x[0])},
+        {"x1", offsetof(struct eloftr_model, x[1])},
+        {"fine0", offsetof(struct eloftr_model, fine[0])},
+        {"fine1", offsetof(struct eloftr_model, fine[1])},
+        {"f1_0", offsetof(struct eloftr_model, f1[0])},
+        {"f1_1", offsetof(struct eloftr_model, f1[1])},
+        {"f2_0", offsetof(struct eloftr_model, f2[0])},
+        {"f2_1", offsetof(struct eloftr_model, f2[1])},
+        {"row_lse", offsetof(struct eloftr_model, row_lse)},
+        {"col_m", offsetof(struct eloftr_model, col_m)},
+        {"col_s", offsetof(struct eloftr_model, col_s)},
+    };
+
+    for (size_t i = 0; i < sizeof(tab) / sizeof(tab[0]); i++)
+        if (strcmp(tab[i].name, name) == 0)
+            return *(const cl_mem *)((const char *)m + tab[i].off);
+    return NULL;
+}

@@ -392,7 +392,8 @@ extern "C" void ocl_copy_rect(struct ocl_backend *ocl, cl_mem src, size_t soff,
     ICOREG_API_END
 }
 
-__global__ void __launch_bounds__(256) fill_kernel(float *p, long n, float v)
+__global__ void __launch_bounds__(256)
+    fill_kernel(uint32_t *p, long n, uint32_t v)
 {
     long i = (long)blockIdx.x * 256 + threadIdx.x;
     long stride = (long)gridDim.x * 256;
@@ -401,25 +402,34 @@ __global__ void __launch_bounds__(256) fill_kernel(float *p, long n, float v)
         p[i] = v;
 }
 
-extern "C" void ocl_fill(struct ocl_backend *ocl, cl_mem buf, size_t off,
-                         size_t n, float value)
+extern "C" void ocl_fill_u32(struct ocl_backend *ocl, cl_mem buf, size_t off,
+                             size_t n, uint32_t bits)
 {
     ICOREG_API_BEGIN
     long blocks;
 
     if (n == 0)
         return;
-    icoreg::need_floats(buf, (long long)off, (long long)n, "ocl_fill",
-                        "buffer");
+    icoreg::need_bytes(buf, 4LL * (long long)off, 4LL * (long long)n,
+                       "ocl_fill", "buffer");
     blocks = (long)((n + 255) / 256);
     if (blocks > 8192)
         blocks = 8192;
     icoreg::prof_scope ps(ocl, "fill");
     hipLaunchKernelGGL(fill_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                       icoreg::stream_of(ocl), icoreg::fptr(buf) + off,
-                       (long)n, value);
+                       icoreg::stream_of(ocl), (uint32_t *)buf->ptr + off,
+                       (long)n, bits);
     icoreg::launch_check("fill");
     ICOREG_API_END
+}
+
+extern "C" void ocl_fill(struct ocl_backend *ocl, cl_mem buf, size_t off,
+                         size_t n, float value)
+{
+    uint32_t bits;
+
+    memcpy(&bits, &value, 4);
+    ocl_fill_u32(ocl, buf, off, n, bits);
 }
 
 extern "C" void ocl_finish(struct ocl_backend *ocl)

@@ -26,6 +26,22 @@ extern "C" void ops_init(struct ops *o, struct ocl_backend *ocl)
     o->im2col_bytes = (size_t)256 << 20;
 }
 
+namespace icoreg {
+
+cl_mem scratch_get(struct ops *o, size_t bytes)
+{
+    if (bytes <= o->scratch_bytes && o->scratch)
+        return o->scratch;
+    hip_check(hipStreamSynchronize(stream_of(o->ocl)), "hipStreamSynchronize");
+    ocl_release(&o->scratch);
+    bytes = (bytes + 0xfffff) & ~(size_t)0xfffff;
+    o->scratch = ocl_alloc(o->ocl, bytes, "ops scratch");
+    o->scratch_bytes = bytes;
+    return o->scratch;
+}
+
+} // namespace icoreg
+
 extern "C" void ops_free(struct ops *o)
 {
     if (!o->ocl)

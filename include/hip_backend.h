@@ -109,6 +109,9 @@ void ocl_copy_rect(struct ocl_backend *ocl, cl_mem src, size_t soff,
  * call can sit inside a captured graph). */
 void ocl_fill(struct ocl_backend *ocl, cl_mem buf, size_t off, size_t n,
               float value);
+/* Same for 32-bit words given by their bit pattern (int -1: 0xffffffff). */
+void ocl_fill_u32(struct ocl_backend *ocl, cl_mem buf, size_t off, size_t n,
+                  uint32_t bits);
 /* Wait for everything queued on the stream. */
 void ocl_finish(struct ocl_backend *ocl);
 

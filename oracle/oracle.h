@@ -121,6 +121,31 @@ void orc_eloftr_fine(const float *f0, const float *f1, int H, int W,
                      const int *cells, int M, float T, float *out,
                      float *margin);
 
+/* A named weight array (the safetensors tensors, float32). */
+struct orc_named {
+    const char *name;
+    const float *data;
+    long numel;
+};
+
+/* Outputs of orc_eloftr_forward; NULL pointers are skipped (but row_max,
+ * row_arg, col_arg, mi, mj, mconf and kp are required, n or 4 n long). */
+struct orc_eloftr_out {
+    float *backbone[2], *coarse[2]; /* 256 x n each */
+    float *row_max, *row_margin, *col_margin;
+    int *row_arg, *col_arg;
+    int nm;
+    int *mi, *mj;
+    float *mconf, *kp, *fine_margin;
+    float *fine[2]; /* 64 x H x W each */
+};
+
+/* The whole Efficient LoFTR pass of eloftr.c:654-681 on grey H x W
+ * images; returns the match count. */
+int orc_eloftr_forward(const struct orc_named *weights, int nweights,
+                       const float *grey0, const float *grey1, int H, int W,
+                       float pos_scale, struct orc_eloftr_out *out);
+
 #ifdef __cplusplus
 }
 #endif

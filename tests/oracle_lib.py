@@ -43,7 +43,71 @@ SIGS = {
     "orc_eloftr_fine": (None, [_FP, _FP, _I, _I, _IP, _I, _F, _FP, _FP]),
 }
 
+class Named(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("data", _FP), ("numel", C.c_long)]
+
+
+class EloftrOut(C.Structure):
+    _fields_ = [
+        ("backbone", _FP * 2), ("coarse", _FP * 2),
+        ("row_max", _FP), ("row_margin", _FP), ("col_margin", _FP),
+        ("row_arg", _IP), ("col_arg", _IP),
+        ("nm", C.c_int), ("mi", _IP), ("mj", _IP),
+        ("mconf", _FP), ("kp", _FP), ("fine_margin", _FP),
+        ("fine", _FP * 2),
+    ]
+
+
+SIGS["orc_eloftr_forward"] = (_I, [C.POINTER(Named), _I, _FP, _FP, _I, _I, _F,
+                                   C.POINTER(EloftrOut)])
+
 _lib = None
+
+
+def named_array(weights):
+    """(ctypes array of Named, keep-alive list) for a dict of float32 arrays."""
+    import numpy as np
+    keep = []
+    arr = (Named * len(weights))()
+    for i, (k, v) in enumerate(sorted(weights.items())):
+        a = np.ascontiguousarray(v, dtype=np.float32)
+        kb = k.encode()
+        keep += [a, kb]
+        arr[i] = Named(kb, a.ctypes.data_as(_FP), a.size)
+    return arr, keep
+
+
+def eloftr_forward(weights, g0, g1, pos_scale=1.0, backbone=False, coarse=False,
+                   fine=False):
+    """Run the oracle's Efficient LoFTR on grey images; dict of outputs."""
+    import numpy as np
+    l = oracle()
+    H, W = g0.shape
+    n = (H // 8) * (W // 8)
+    arr, keep = named_array(weights)
+    out = {k: np.zeros(n, np.float32) for k in ("row_max", "row_margin", "col_margin", "mconf")}
+    for k in ("row_arg", "col_arg", "mi", "mj"):
+        out[k] = np.zeros(n, np.int32)
+    out["kp"] = np.zeros(4 * n, np.float32)
+    out["fine_margin"] = np.zeros(n, np.float32)
+    st = EloftrOut()
+    for k in ("row_max", "row_margin", "col_margin", "mconf", "kp", "fine_margin"):
+        setattr(st, k, fp(out[k]))
+    for k in ("row_arg", "col_arg", "mi", "mj"):
+        setattr(st, k, ip(out[k]))
+    for name, flag, size in (("backbone", backbone, 256 * n), ("coarse", coarse, 256 * n),
+                             ("fine", fine, 64 * H * W)):
+        if flag:
+            bufs = [np.zeros(size, np.float32) for _ in range(2)]
+            out[name] = bufs
+            getattr(st, name)[0] = fp(bufs[0])
+            getattr(st, name)[1] = fp(bufs[1])
+    g0 = np.ascontiguousarray(g0, np.float32)
+    g1 = np.ascontiguousarray(g1, np.float32)
+    nm = l.orc_eloftr_forward(arr, len(weights), fp(g0), fp(g1), H, W, pos_scale,
+                              C.byref(st))
+    out["nm"] = nm
+    return out
 
 
 def oracle():

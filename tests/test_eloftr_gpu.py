@@ -1,0 +1,176 @@
+# SPDX-License-Identifier: Unlicense
+"""GPU: ELoFTR kernels and network on the HIP library against the oracle.
+
+Tolerances: contractions and features <= 1e-3 of the
+largest reference magnitude; index outputs (row / column argmax, fine
+window argmax) bit-exact wherever the oracle's relative top-2 margin
+exceeds 1e-3."""
+
+import os
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import elo_ref
+from oracle_lib import eloftr_forward, fp, ip
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT / "i.coregistration.opencl_amd"))
+import synth  # noqa: E402
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "eloftr_golden.npz"
+TOL = 1e-3
+MARGIN = 1e-3
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+    return np.abs(a - b).max() / max(np.abs(b).max(), 1e-30)
+
+
+@pytest.fixture(scope="module")
+def weights_file(tmp_path_factory):
+    p = tmp_path_factory.mktemp("w") / "eloftr_random.safetensors"
+    return synth.eloftr_weights_file(p)
+
+
+@pytest.fixture(scope="module")
+def weights():
+    return synth.eloftr_weights_calibrated()
+
+
+def test_coarse_kernels_two_blocks(dev, ic, orc):
+    """GEMM + row / column LSE + confidence argmaxes over two row blocks
+    (the running column statistics and the first-argmax rule across
+    blocks) against the oracle's blocked schedule."""
+    print("[eloftr] coarse kernels", flush=True)
+    rng = np.random.default_rng(21)
+    n, D, blk = 1000, 64, 384
+    F0, F1 = elo_ref.match_features(rng, n, D)
+    alpha = np.float32(1.0) / np.float32(D * 0.1)
+    o_rmax = np.zeros(n, np.float32)
+    o_rarg, o_carg = np.zeros(n, np.int32), np.zeros(n, np.int32)
+    o_rmar, o_cmar = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    orc.orc_eloftr_coarse(fp(F0), fp(F1), n, D, alpha, blk, fp(o_rmax), ip(o_rarg),
+                          ip(o_carg), fp(o_rmar), fp(o_cmar))
+    a, M = dev.api, ic.mem
+    f0, f1 = dev.upload(F0), dev.upload(F1)
+    S = dev.zeros(blk * n)
+    lse, cm, cs = dev.zeros(n), dev.upload(np.full(n, -np.inf, np.float32)), dev.zeros(n)
+    rmax, rarg = dev.zeros(n), dev.zeros(n, np.int32)
+    cmax = dev.upload(np.full(n, -1.0, np.float32))
+    carg = dev.upload(np.full(n, -1, np.int32))
+    for p in range(2):
+        for r0 in range(0, n, blk):
+            rows = min(blk, n - r0)
+            a.ops_gemm(dev.po, rows, n, D, ic.mat(f0, r0 * D, D), ic.mat(f1, 0, D), 1,
+                       ic.mat(S, 0, n), 1, 1, None, 0, None, 0, float(alpha), 0, 0.0)
+            if p == 0:
+                a.eloftr_row_lse(dev.po, M(S), rows, n, r0, M(lse))
+                a.eloftr_col_lse(dev.po, M(S), rows, n, M(cm), M(cs))
+            else:
+                a.eloftr_conf_row(dev.po, M(S), rows, n, r0, M(lse), M(cm), M(cs), M(rmax), M(rarg))
+                a.eloftr_conf_col(dev.po, M(S), rows, n, r0, M(lse), M(cm), M(cs), M(cmax), M(carg))
+    g_rmax, g_rarg = dev.read(rmax, n), dev.read(rarg, n, np.int32)
+    g_carg = dev.read(carg, n, np.int32)
+    assert rel(g_rmax, o_rmax) <= TOL
+    sure = o_rmar / np.maximum(o_rmax, 1e-30) > MARGIN
+    assert sure.mean() > 0.9
+    assert np.array_equal(g_rarg[sure], o_rarg[sure])
+    cmaxo = dev.read(cmax, n)
+    sure_c = o_cmar / np.maximum(cmaxo, 1e-30) > MARGIN
+    assert sure_c.mean() > 0.9
+    assert np.array_equal(g_carg[sure_c], o_carg[sure_c])
+
+
+def test_fine_kernel(dev, ic, orc):
+    print("[eloftr] fine kernel", flush=True)
+    rng = np.random.default_rng(22)
+    H, W = 48, 64
+    h, w = H // 8, W // 8
+    f0 = rng.standard_normal((64, H, W)).astype(np.float32)
+    f1 = rng.standard_normal((64, H, W)).astype(np.float32)
+    Mn = 500
+    cells = np.stack([rng.integers(0, w, Mn), rng.integers(0, h, Mn),
+                      rng.integers(0, w, Mn), rng.integers(0, h, Mn)], 1).astype(np.int32)
+    cells[:3] = [[0, 0, 0, 0], [w - 1, h - 1, w - 1, h - 1], [0, h - 1, w - 1, 0]]
+    cells = np.ascontiguousarray(cells)
+    ref = np.zeros(4 * Mn, np.float32)
+    mar = np.zeros(Mn, np.float32)
+    orc.orc_eloftr_fine(fp(f0), fp(f1), H, W, ip(cells), Mn, 10.0, fp(ref), fp(mar))
+    b0, b1, bc = dev.upload(f0), dev.upload(f1), dev.upload(cells)
+    out = dev.zeros(4 * Mn)
+    dev.api.eloftr_fine(dev.po, b0.mem, b1.mem, H, W, bc.mem, Mn, 10.0, out.mem)
+    got = dev.read(out, 4 * Mn).reshape(-1, 4)
+    ref = ref.reshape(-1, 4)
+    _, margin = elo_ref.fine_bruteforce(f0, f1, cells)
+    sure = margin > MARGIN
+    assert sure.mean() > 0.9
+    np.testing.assert_array_equal(np.floor(got[sure, :2]), np.floor(ref[sure, :2]))
+    np.testing.assert_allclose(got[sure], ref[sure], atol=1e-3, rtol=0)
+
+
+def test_network_small_vs_oracle_and_transformers(dev, ic, weights, weights_file, tmp_path):
+    print("[eloftr] network 64x96", flush=True)
+    g = np.load(GOLDEN)
+    H, W = int(g["H"]), int(g["W"])
+    g0, g1, _ = synth.eloftr_pair(H, W)
+    o = eloftr_forward(weights, g0, g1, backbone=True, coarse=True, fine=True)
+    net = ic.Eloftr(dev, weights_file, H, W)
+    try:
+        r = net.match(g0, g1, dump=str(tmp_path), tile=3)
+        n = (H // 8) * (W // 8)
+        for k in range(2):
+            bb = np.fromfile(tmp_path / f"tile003_eloftr_backbone_{k}.f32", np.float32)
+            assert rel(bb, o["backbone"][k]) <= TOL
+            assert rel(bb, g["backbone"][k]) <= TOL
+            x = net.buffer(f"x{k}", 256 * n)
+            assert rel(x, o["coarse"][k]) <= TOL
+            assert rel(x, g["coarse"][k]) <= TOL
+            cx = np.fromfile(tmp_path / f"tile003_eloftr_coarse_{k}.f32", np.float32)
+            assert np.array_equal(cx, x)
+            fine = net.buffer(f"fine{k}", 64 * H * W)
+            assert rel(fine, o["fine"][k]) <= TOL
+            assert rel(fine[g["fine_idx"]], g["fine"][k]) <= TOL
+        assert rel(r["row_max"], o["row_max"]) <= TOL
+        sure = o["row_margin"] / np.maximum(o["row_max"], 1e-30) > MARGIN
+        assert np.array_equal(r["row_arg"][sure], o["row_arg"][sure])
+        if r["nm"] == o["nm"] and r["nm"] > 0:
+            assert np.array_equal(r["mi"], o["mi"][:o["nm"]])
+            np.testing.assert_allclose(r["kp"], o["kp"][:4 * o["nm"]].reshape(-1, 4), atol=1e-2)
+    finally:
+        net.close()
+
+
+def test_network_640_properties(dev, ic, weights_file):
+    """The benchmark config (640 x 640 grey pair): every output is finite
+    and in range, and the matches are exactly the mutual / threshold /
+    border selection of the coarse statistics."""
+    print("[eloftr] network 640x640", flush=True)
+    H = W = 640
+    g0, g1, _ = synth.eloftr_pair(H, W)
+    net = ic.Eloftr(dev, weights_file, H, W)
+    try:
+        r = net.match(g0, g1)
+        h, w = H // 8, W // 8
+        n = h * w
+        rm, ra, ca = r["row_max"], r["row_arg"], r["col_arg"]
+        assert np.isfinite(rm).all() and (rm >= 0).all() and (rm <= 1.0 + 1e-6).all()
+        assert ((ra >= 0) & (ra < n)).all() and ((ca >= 0) & (ca < n)).all()
+        inside = lambda k: (2 <= k % w) & (k % w < w - 2) & (2 <= k // w) & (k // w < h - 2)
+        i = np.arange(n)
+        keep = (rm > 0.2) & (ca[ra] == i) & inside(i) & inside(ra)
+        assert r["nm"] == int(keep.sum())
+        assert np.array_equal(r["mi"], i[keep]) and np.array_equal(r["mj"], ra[keep])
+        x = net.buffer("x0", 256 * n)
+        assert np.isfinite(x).all()
+        fine = net.buffer("fine1", 64 * H * W)
+        assert np.isfinite(fine).all()
+        if r["nm"]:
+            assert np.isfinite(r["kp"]).all()
+    finally:
+        net.close()
