@@ -1,0 +1,217 @@
+# SPDX-License-Identifier: Unlicense
+"""Benchmark of the MI355X matcher tensor path (BASELINE.json metric).
+
+One step = one Efficient LoFTR 640 x 640 grey tile pair through the whole
+device stage of the reference's eloftr_match (eloftr.c:654-681):
+backbone x 2, 4 x (self, self, cross, cross) aggregated attention, coarse
+dual-softmax matching with the host mutual selection, FPN fusion x 2 and
+two-stage fine matching; seeded synthetic pair and seeded random-init
+weights (synth.py), both images resident in HBM before timing.
+
+Prints one JSON line (the driver's contract) with the per-kernel roofline
+of the dominant kernel (the implicit-GEMM fp32 MFMA convolution: HIP
+events around each of its launches over the profiled steps) and the CPU
+baseline (the oracle, a C port of the reference kernels, on a bounded
+sample timed on this host).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+"""
+
+import argparse
+import importlib.util
+import json
+import os
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+PKG_DIR = ROOT / "i.coregistration.opencl_amd"
+PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
+PEAK_HBM = 8000.0        # GB/s
+
+
+def load_package():
+    if "icoreg_amd" in sys.modules:
+        return sys.modules["icoreg_amd"]
+    spec = importlib.util.spec_from_file_location(
+        "icoreg_amd", PKG_DIR / "__init__.py", submodule_search_locations=[str(PKG_DIR)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["icoreg_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def eloftr_flops(H, W, nm=0):
+    """Algorithmic FLOPs of one ELoFTR pair by kernel family: 2 M N K per
+    contraction, 2 K Ho Wo C kh kw per convolution, 4 heads Nq Nk d per
+    attention, one score GEMM (the second pass is a recompute)."""
+    h, w = H // 8, W // 8
+    n, na = h * w, (h // 4) * (w // 4)
+    conv = gemm = attn = other = 0.0
+    # Backbone (eloftr.c:367-394), both images.
+    layers = [(1, 64, 2)] + [(64, 64, 1)] * 2 + [(64, 128, 2)] + [(128, 128, 1)] * 3 + \
+             [(128, 256, 2)] + [(256, 256, 1)] * 13
+    Hc, Wc = H, W
+    for ci, co, s in layers:
+        Hc, Wc = Hc // s, Wc // s
+        conv += 2 * 2.0 * co * Hc * Wc * ci * 9
+    # Transformer: 16 aggregated attention blocks (eloftr.c:405-463).
+    D = 256
+    per = (4 * 2.0 * na * D * D            # q, k, v, o projections
+           + 2.0 * n * 512 * 512 + 2.0 * n * 256 * 512)  # fc1, fc2
+    gemm += 16 * per
+    attn += 16 * 4.0 * 8 * na * na * 32
+    other += 16 * 2.0 * D * na * 16         # depthwise 4 x 4 aggregation
+    # Coarse scores (one pass).
+    gemm += 2.0 * n * n * D
+    # Fusion (eloftr.c:573-604), both images.
+    H4, W4, H2, W2 = 2 * h, 2 * w, 4 * h, 4 * w
+    gemm += 2 * (2.0 * 256 * n * 256 + 2.0 * 256 * H4 * W4 * 128 + 2.0 * 128 * H2 * W2 * 64)
+    conv += 2 * (2.0 * 256 * H4 * W4 * 256 * 9 + 2.0 * 128 * H4 * W4 * 256 * 9
+                 + 2.0 * 128 * H2 * W2 * 128 * 9 + 2.0 * 64 * H2 * W2 * 128 * 9)
+    other += nm * (2.0 * 64 * 100 * 56 + 2.0 * 9 * 8)
+    return {"conv": conv, "gemm": gemm, "attention": attn, "other": other,
+            "total": conv + gemm + attn + other}
+
+
+def cpu_baseline(weights, size=256):
+    """The oracle (C port of the reference kernels and schedule, OpenMP)
+    on one size x size pair, scaled to a 640 x 640 pair by algorithmic
+    FLOPs."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    sys.path.insert(0, str(PKG_DIR))
+    import synth
+    from oracle_lib import eloftr_forward
+    g0, g1, _ = synth.eloftr_pair(size, size)
+    t0 = time.perf_counter()
+    eloftr_forward(weights, g0, g1)
+    dt = time.perf_counter() - t0
+    ratio = eloftr_flops(640, 640)["total"] / eloftr_flops(size, size)["total"]
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": 1.0 / (dt * ratio), "unit": "tile-pairs/s", "cores": cores, "kind": "port",
+            "sample": f"oracle/ (C port of the reference kernels + eloftr.c schedule, OpenMP) "
+                      f"full ELoFTR pass on one {size}x{size} pair in {dt:.1f} s, scaled to a "
+                      f"640x640 pair by algorithmic FLOPs (x{ratio:.2f})"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--size", type=int, default=640)
+    ap.add_argument("--profile-steps", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus}: this build runs on one GPU only (tiles are "
+              "independent; the multi-GPU design is in DESIGN.md). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(1)
+
+    ic = load_package()
+    sys.path.insert(0, str(PKG_DIR))
+    import synth
+
+    H = W = args.size
+    dev = ic.Device("auto")
+    print(f"[bench] {dev.name} ({dev.arch}), {dev.ocl.cu_count} CUs", file=sys.stderr, flush=True)
+    wdir = Path(tempfile.gettempdir()) / "icoreg_bench"
+    wfile = synth.eloftr_weights_file(wdir / "eloftr_random_calibrated.safetensors")
+    g0, g1, _ = synth.eloftr_pair(H, W)
+    net = ic.Eloftr(dev, wfile, H, W)
+    b0, b1 = dev.upload(g0), dev.upload(g1)
+
+    for _ in range(args.warmup):
+        net.match_device(b0, b1)
+    dev.finish()
+    dev.reset_events()
+    t0 = time.perf_counter()
+    e0 = dev.event()
+    for _ in range(args.steps):
+        net.match_device(b0, b1)
+    e1 = dev.event()
+    dev.finish()
+    wall = time.perf_counter() - t0
+    gpu_ms = dev.elapsed_ms(e0, e1)
+    ms = max(gpu_ms, wall * 1e3) / args.steps
+    res = net.result()
+    nm = int(res["nm"])
+
+    # Per-kernel times over a few more steps (event pairs, no sync).
+    dev.profile_reset()
+    dev.set_profile(2)
+    for _ in range(args.profile_steps):
+        net.match_device(b0, b1)
+    dev.finish()
+    table = dev.profile_table()
+    dev.set_profile(0)
+    ps = args.profile_steps
+    fl = eloftr_flops(H, W, nm)
+    conv_ms = table.get("conv_igemm", (0.0, 0))[0] / ps
+    conv_calls = table.get("conv_igemm", (0.0, 0))[1] / ps
+    achieved = fl["conv"] / (conv_ms * 1e-3) / 1e12 if conv_ms > 0 else 0.0
+    kernels = {k: {"ms_per_step": round(v[0] / ps, 4), "launches_per_step": v[1] / ps}
+               for k, v in sorted(table.items(), key=lambda kv: -kv[1][0])}
+    print("[bench] per-kernel ms per pair: " + json.dumps(kernels), file=sys.stderr, flush=True)
+
+    # Fine stage at its largest size (every coarse cell matched once), so
+    # that its cost shows whatever the number of coarse matches.
+    h, w = H // 8, W // 8
+    n = h * w
+    cells = np.stack(np.meshgrid(np.arange(w), np.arange(h)), -1).reshape(-1, 2)
+    cells = np.ascontiguousarray(np.concatenate([cells, cells], 1).astype(np.int32))
+    bc, bo = dev.upload(cells), dev.zeros(4 * n)
+    f0m, f1m = ic.lib().icoreg_eloftr_buffer(net.m, b"fine0"), ic.lib().icoreg_eloftr_buffer(net.m, b"fine1")
+    dev.api.eloftr_fine(dev.po, f0m, f1m, H, W, bc.mem, n, 10.0, bo.mem)
+    dev.finish()
+    dev.reset_events()
+    ea = dev.event()
+    for _ in range(5):
+        dev.api.eloftr_fine(dev.po, f0m, f1m, H, W, bc.mem, n, 10.0, bo.mem)
+    eb = dev.event()
+    fine_nmax_ms = dev.elapsed_ms(ea, eb) / 5
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(synth.eloftr_weights_calibrated())
+
+    line = {
+        "metric": "tile-pairs/sec (1 GPU) ELoFTR 640² & RoMa 560², fp32; % MFMA/HBM peak",
+        "value": round(1000.0 / ms, 3),
+        "unit": "tile-pairs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded blurred-noise grey pair, B = random affine of A + noise; "
+                "seeded He-normal weights, data-calibrated BatchNorm statistics)",
+        "config": {"workload": f"ELoFTR {H}x{W} grey pair, full device stage (backbone, "
+                               "transformer, coarse match, fusion, fine match)",
+                   "tile": [H, W], "coarse_matches": nm,
+                   "gflop_per_pair": round(fl["total"] / 1e9, 1)},
+        "roofline": {"kernel": "conv_igemm (implicit-GEMM 3x3 conv, fp32 MFMA)",
+                     "bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "launches_per_step": conv_calls,
+                     "gflop_per_step": round(fl["conv"] / 1e9, 2)},
+        "pipeline_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
+        "fine_ms_at_max_matches": round(fine_nmax_ms, 4),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    net.close()
+    dev.close()
+
+
+if __name__ == "__main__":
+    main()

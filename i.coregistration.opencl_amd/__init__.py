@@ -101,6 +101,7 @@ SIGNATURES = {
     "icoreg_clear_error": (None, []),
     "icoreg_prof_entry": (_I, [_I, C.POINTER(_S), C.POINTER(C.c_double), C.POINTER(C.c_long)]),
     "icoreg_prof_reset": (None, []),
+    "icoreg_prof_flush": (_I, []),
     # generic ops (include/ops.h)
     "ops_init": (None, [_O, _B]),
     "ops_free": (None, [_O]),
@@ -165,7 +166,7 @@ SIGNATURES = {
 # Entry points that never raise through the fatal path (no error check).
 _NO_CHECK = {"icoreg_set_fatal_mode", "icoreg_last_error", "icoreg_clear_error",
              "ocl_errstr", "ops_mat", "ops_bmat", "ops_geom", "ops_conv_out",
-             "ocl_wrap", "icoreg_prof_entry", "icoreg_prof_reset", "ops_report",
+             "ocl_wrap", "icoreg_prof_entry", "icoreg_prof_reset", "icoreg_prof_flush", "ops_report",
              "pth_find", "pth_numel", "pth_bytes", "pth_strip_prefix",
              "icoreg_pth_new", "icoreg_eloftr_new", "icoreg_struct_delete",
              "icoreg_eloftr_result", "icoreg_eloftr_coarse_stats",
@@ -303,6 +304,24 @@ class Device:
 
     def reset_events(self):
         self.api.ocl_event_reset(self.pb)
+
+    def set_profile(self, mode):
+        """0 off, 1 synchronous per launch, 2 asynchronous event pairs."""
+        self.ocl.profile = mode
+
+    def profile_table(self):
+        """{name: (total ms, launches)} of the launch timing table."""
+        l = lib()
+        l.icoreg_prof_flush()
+        out, i = {}, 0
+        what, ms, calls = C.c_char_p(), C.c_double(), C.c_long()
+        while l.icoreg_prof_entry(i, C.byref(what), C.byref(ms), C.byref(calls)):
+            out[what.value.decode()] = (ms.value, calls.value)
+            i += 1
+        return out
+
+    def profile_reset(self):
+        lib().icoreg_prof_reset()
 
     def close(self):
         if self.ocl.stream:

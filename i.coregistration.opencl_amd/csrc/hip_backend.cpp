@@ -111,13 +111,51 @@ static struct {
 static int nprof;
 static std::mutex prof_mu;
 
+/* Asynchronous event pairs (profile mode 2): recorded around each launch
+ * without synchronising, resolved by icoreg_prof_flush. */
+#define NPAIRS 65536
+static struct {
+    hipEvent_t e0, e1;
+    const char *what;
+} pairs[NPAIRS];
+static int npairs;
+
 namespace icoreg {
+
+void prof_add(const char *what, double ms)
+{
+    int i;
+
+    std::lock_guard<std::mutex> lk(prof_mu);
+    for (i = 0; i < nprof && strcmp(prof[i].what, what) != 0; i++)
+        ;
+    if (i == nprof && nprof < 64)
+        prof[nprof++].what = what;
+    if (i < 64) {
+        prof[i].ms += ms;
+        prof[i].calls++;
+    }
+}
 
 prof_scope::prof_scope(struct ocl_backend *o, const char *n)
     : ocl(o), name(n), e0(nullptr), e1(nullptr)
 {
     if (!ocl || !ocl->profile)
         return;
+    if (ocl->profile == 2) {
+        if (npairs >= NPAIRS)
+            return;
+        if (!pairs[npairs].e0) {
+            hip_check(hipEventCreate(&pairs[npairs].e0), "hipEventCreate");
+            hip_check(hipEventCreate(&pairs[npairs].e1), "hipEventCreate");
+        }
+        e0 = pairs[npairs].e0;
+        e1 = pairs[npairs].e1;
+        pairs[npairs].what = n;
+        npairs++;
+        hip_check(hipEventRecord(e0, stream_of(ocl)), "hipEventRecord");
+        return;
+    }
     hip_check(hipEventCreate(&e0), "hipEventCreate");
     hip_check(hipEventCreate(&e1), "hipEventCreate");
     hip_check(hipEventRecord(e0, stream_of(ocl)), "hipEventRecord");
@@ -126,25 +164,20 @@ prof_scope::prof_scope(struct ocl_backend *o, const char *n)
 prof_scope::~prof_scope()
 {
     float ms = 0;
-    int i;
 
     if (!e0)
         return;
+    if (ocl->profile == 2) {
+        (void)hipEventRecord(e1, stream_of(ocl));
+        return;
+    }
     if (hipEventRecord(e1, stream_of(ocl)) != hipSuccess ||
         hipEventSynchronize(e1) != hipSuccess ||
         hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
         ms = 0;
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
-    std::lock_guard<std::mutex> lk(prof_mu);
-    for (i = 0; i < nprof && strcmp(prof[i].what, name) != 0; i++)
-        ;
-    if (i == nprof && nprof < 64)
-        prof[nprof++].what = name;
-    if (i < 64) {
-        prof[i].ms += ms;
-        prof[i].calls++;
-    }
+    prof_add(name, ms);
 }
 
 } // namespace icoreg
@@ -175,7 +208,26 @@ extern "C" void icoreg_prof_reset(void)
 {
     std::lock_guard<std::mutex> lk(prof_mu);
     nprof = 0;
+    npairs = 0;
     memset(prof, 0, sizeof(prof));
+}
+
+/* Resolve the event pairs of profile mode 2 into the table (waits for
+ * the last one); returns the number of launches resolved. */
+extern "C" int icoreg_prof_flush(void)
+{
+    int n = npairs, i;
+
+    for (i = 0; i < n; i++) {
+        float ms = 0;
+
+        if (hipEventSynchronize(pairs[i].e1) != hipSuccess ||
+            hipEventElapsedTime(&ms, pairs[i].e0, pairs[i].e1) != hipSuccess)
+            ms = 0;
+        icoreg::prof_add(pairs[i].what, ms);
+    }
+    npairs = 0;
+    return n;
 }
 
 /* ---- device selection -------------------------------------------------- */

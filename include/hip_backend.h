@@ -146,6 +146,16 @@ int ocl_event_record(struct ocl_backend *ocl);
 float ocl_event_ms(struct ocl_backend *ocl, int ev0, int ev1);
 void ocl_event_reset(struct ocl_backend *ocl);
 
+/* Per-launch timing table (the reference's ops_run profiling, ops.c:
+ * 25-67), filled when ocl->profile is set: 1 synchronises after every
+ * launch (the reference's mode); 2 records event pairs on the stream
+ * without synchronising and resolves them in icoreg_prof_flush, so that
+ * a timed region is not disturbed. Entry i: name, total ms, launches;
+ * icoreg_prof_entry returns 0 past the end. */
+int icoreg_prof_entry(int i, const char **what, double *ms, long *calls);
+int icoreg_prof_flush(void);
+void icoreg_prof_reset(void);
+
 #ifdef __cplusplus
 }
 #endif
