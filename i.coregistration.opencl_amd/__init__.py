@@ -114,6 +114,8 @@ SIGNATURES = {
     "ops_geom": (ConvGeom, [_I, _I, _I]),
     "ops_conv_out": (_I, [_I, _I, _I, _I, _I]),
     "ops_conv2d": (None, [_O, Mem, _I, _I, _I, Mem, Mem, _I, C.POINTER(ConvGeom), Mem, Mem, Mem, _I, _F, Mem]),
+    "ops_conv2d_batch": (None, [_O, _I, Mem, _L, _I, _I, _I, Mem, Mem, _I, C.POINTER(ConvGeom),
+                                Mem, Mem, Mem, _I, _F, Mem, _L]),
     "ops_chan_stats": (None, [_O, Mem, _I, _I, _F, Mem, Mem]),
     "ops_chan_affine": (None, [_O, Mem, Mem, _I, _I, Mem, Mem, Mem, Mem, _I, _F]),
     "ops_prelu": (None, [_O, Mem, Mem, _I, _I, Mem]),

@@ -250,6 +250,13 @@ static cl_mem walloc(struct eloftr_model *m, size_t floats, const char *what)
     return ocl_alloc(m->ocl, floats * sizeof(float), what);
 }
 
+/* Image k's part of a pair buffer of 2 x floats. */
+static cl_mem view(cl_mem pair, int k, size_t floats)
+{
+    return ocl_wrap((float *)pair->ptr + (size_t)k * floats,
+                    floats * sizeof(float));
+}
+
 /* RoPE (cos, sin) table of the aggregated grid (eloftr.c:267-291):
  * position (i, j), 1-based, times pos_scale; pair p of the 256 channels
  * turns by i f(p / 2) for even p, j f(p / 2) for odd p, f(k) =
@@ -291,14 +298,18 @@ extern "C" void eloftr_alloc(struct eloftr_model *m, int H, int W)
     m->aw = m->w / 4;
     n = (size_t)m->h * m->w;
     na = (size_t)m->ah * m->aw;
-    m->img = walloc(m, hw, "image");
-    m->s_a = walloc(m, 16 * hw, "backbone");
-    m->s_b = walloc(m, 16 * hw, "backbone");
+    m->img = walloc(m, 2 * hw, "images");
+    m->s_a = walloc(m, 2 * 16 * hw, "backbone");
+    m->s_b = walloc(m, 2 * 16 * hw, "backbone");
+    m->f1p = walloc(m, 2 * 16 * hw, "1/2 features");
+    m->f2p = walloc(m, 2 * 8 * hw, "1/4 features");
+    m->xp = walloc(m, 2 * ELOFTR_DIM * n, "1/8 features");
+    m->finep = walloc(m, 2 * ELOFTR_FINE_DIM * hw, "fine features");
     for (int k = 0; k < 2; k++) {
-        m->f1[k] = walloc(m, 16 * hw, "1/2 features");
-        m->f2[k] = walloc(m, 8 * hw, "1/4 features");
-        m->x[k] = walloc(m, ELOFTR_DIM * n, "1/8 features");
-        m->fine[k] = walloc(m, ELOFTR_FINE_DIM * hw, "fine features");
+        m->f1[k] = view(m->f1p, k, 16 * hw);
+        m->f2[k] = view(m->f2p, k, 8 * hw);
+        m->x[k] = view(m->xp, k, ELOFTR_DIM * n);
+        m->fine[k] = view(m->finep, k, ELOFTR_FINE_DIM * hw);
     }
     m->t_q = walloc(m, ELOFTR_DIM * na, "aggregated");
     m->t_kv = walloc(m, ELOFTR_DIM * na, "aggregated");
@@ -327,9 +338,9 @@ extern "C" void eloftr_alloc(struct eloftr_model *m, int H, int W)
     m->col_max = walloc(m, n, "column max");
     m->row_arg = ocl_alloc(m->ocl, n * sizeof(int), "row argmax");
     m->col_arg = ocl_alloc(m->ocl, n * sizeof(int), "column argmax");
-    m->fu_a = walloc(m, 32 * hw, "fusion");
-    m->fu_b = walloc(m, 32 * hw, "fusion");
-    m->fu_c = walloc(m, 32 * hw, "fusion");
+    m->fu_a = walloc(m, 2 * 32 * hw, "fusion");
+    m->fu_b = walloc(m, 2 * 32 * hw, "fusion");
+    m->fu_c = walloc(m, 2 * 32 * hw, "fusion");
     m->nmax = (int)n;
     m->m_idx = ocl_alloc(m->ocl, n * 4 * sizeof(int), "match cells");
     m->m_out = walloc(m, n * 4, "fine matches");
@@ -343,40 +354,48 @@ extern "C" void eloftr_alloc(struct eloftr_model *m, int H, int W)
     ICOREG_API_END
 }
 
-static void conv3x3(struct eloftr_model *m, cl_mem in, int C, int H, int W,
-                    cl_mem w, cl_mem b, int K, int stride, int act, cl_mem out)
+/* 3 x 3 convolution of both images of a pair: in holds image 1 at
+ * in_stride floats after image 0, out likewise at out_stride. */
+static void conv3x3_pair(struct eloftr_model *m, cl_mem in, long in_stride,
+                         int C, int H, int W, cl_mem w, cl_mem b, int K,
+                         int stride, int act, cl_mem out, long out_stride)
 {
     struct conv_geom g = ops_geom(3, stride, 1);
 
-    ops_conv2d(m->ops, in, C, H, W, w, b, K, &g, NULL, NULL, NULL, act, LEAKY,
-               out);
+    ops_conv2d_batch(m->ops, 2, in, in_stride, C, H, W, w, b, K, &g, NULL,
+                     NULL, NULL, act, LEAKY, out, out_stride);
 }
 
-/* The RepVGG backbone on image in (1 x H x W) of image k: 1/2 features
- * into f1[k], 1/4 into f2[k], 1/8 into x[k]. eloftr.c:367-394. */
-static void backbone(struct eloftr_model *m, cl_mem img, int k)
+/* The RepVGG backbone on both images of the pair (m->img: image 1 at
+ * H W floats after image 0): 1/2 features into f1p, 1/4 into f2p, 1/8
+ * into xp, each layer one launch for the pair. eloftr.c:367-394. */
+static void backbone(struct eloftr_model *m)
 {
-    cl_mem in = img;
+    cl_mem in = m->img;
+    long in_stride = (long)m->H * m->W;
     int l = 0, Hc = m->H, Wc = m->W;
 
     for (int s = 0; s < 4; s++)
         for (int b = 0; b < stage_blocks[s]; b++, l++) {
             const int st = m->bstride[l], last = b == stage_blocks[s] - 1;
+            const int Ho = Hc / st, Wo = Wc / st;
+            const long out_stride = (long)m->bcout[l] * Ho * Wo;
             cl_mem out;
 
             if (last && s == 1)
-                out = m->f1[k];
+                out = m->f1p;
             else if (last && s == 2)
-                out = m->f2[k];
+                out = m->f2p;
             else if (last && s == 3)
-                out = m->x[k];
+                out = m->xp;
             else
                 out = in == m->s_a ? m->s_b : m->s_a;
-            conv3x3(m, in, m->bcin[l], Hc, Wc, m->bw[l], m->bb[l], m->bcout[l],
-                    st, ACT_RELU, out);
-            Hc /= st;
-            Wc /= st;
+            conv3x3_pair(m, in, in_stride, m->bcin[l], Hc, Wc, m->bw[l],
+                         m->bb[l], m->bcout[l], st, ACT_RELU, out, out_stride);
+            Hc = Ho;
+            Wc = Wo;
             in = out;
+            in_stride = out_stride;
         }
 }
 
@@ -501,34 +520,44 @@ static void coarse_match(struct eloftr_model *m)
     }
 }
 
-/* FPN fusion of image k into fine[k] (64, H, W). eloftr.c:573-604. */
-static void fusion(struct eloftr_model *m, int k)
+/* 1 x 1 convolution of both images: W (K, C) times X (C, HW) per image,
+ * images C HW / K HW floats apart in X / Y. */
+static void conv1x1_pair(struct eloftr_model *m, cl_mem X, int C, int HW,
+                         cl_mem Wt, int K, cl_mem Y)
+{
+    ops_gemm(m->ops, K, HW, C, ops_mat(Wt, 0, C),
+             ops_bmat(X, 0, HW, (long)C * HW, 0), 0,
+             ops_bmat(Y, 0, HW, (long)K * HW, 0), 2, 1, NULL, 1, NULL, 0, 1.0f,
+             ACT_NONE, 0);
+}
+
+/* FPN fusion of both images into finep (64, H, W) each, every layer one
+ * launch for the pair (the pair's channels are contiguous, so resizes and
+ * sums run over 2 C channels). eloftr.c:573-604. */
+static void fusion(struct eloftr_model *m)
 {
     struct ops *o = m->ops;
     const int h = m->h, w = m->w;
     const int H4 = 2 * h, W4 = 2 * w, H2 = 4 * h, W2 = 4 * w;
 
-    ops_conv1x1(o, m->x[k], 0, 256, h * w, m->f_out, NULL, 256, m->fu_a, 0,
-                ACT_NONE, 0);
-    ops_resize(o, m->fu_a, 256, h, w, m->fu_b, H4, W4, 0, 0, 2.0f);
-    ops_conv1x1(o, m->f2[k], 0, 128, H4 * W4, m->f1_w[0], NULL, 256, m->fu_c,
-                0, ACT_NONE, 0);
-    ops_axpby(o, m->fu_c, m->fu_c, 1.0f, m->fu_b, 1.0f, 256L * H4 * W4,
-              256L * H4 * W4);
-    conv3x3(m, m->fu_c, 256, H4, W4, m->f2_w[0], m->f2_b[0], 256, 1, ACT_LEAKY,
-            m->fu_a);
-    conv3x3(m, m->fu_a, 256, H4, W4, m->f3_w[0], NULL, 128, 1, ACT_NONE,
-            m->fu_b);
-    ops_resize(o, m->fu_b, 128, H4, W4, m->fu_c, H2, W2, 0, 0, 2.0f);
-    ops_conv1x1(o, m->f1[k], 0, 64, H2 * W2, m->f1_w[1], NULL, 128, m->fu_a, 0,
-                ACT_NONE, 0);
-    ops_axpby(o, m->fu_a, m->fu_a, 1.0f, m->fu_c, 1.0f, 128L * H2 * W2,
-              128L * H2 * W2);
-    conv3x3(m, m->fu_a, 128, H2, W2, m->f2_w[1], m->f2_b[1], 128, 1, ACT_LEAKY,
-            m->fu_b);
-    conv3x3(m, m->fu_b, 128, H2, W2, m->f3_w[1], NULL, 64, 1, ACT_NONE,
-            m->fu_c);
-    ops_resize(o, m->fu_c, 64, H2, W2, m->fine[k], m->H, m->W, 0, 0, 2.0f);
+    conv1x1_pair(m, m->xp, 256, h * w, m->f_out, 256, m->fu_a);
+    ops_resize(o, m->fu_a, 2 * 256, h, w, m->fu_b, H4, W4, 0, 0, 2.0f);
+    conv1x1_pair(m, m->f2p, 128, H4 * W4, m->f1_w[0], 256, m->fu_c);
+    ops_axpby(o, m->fu_c, m->fu_c, 1.0f, m->fu_b, 1.0f, 2 * 256L * H4 * W4,
+              2 * 256L * H4 * W4);
+    conv3x3_pair(m, m->fu_c, 256L * H4 * W4, 256, H4, W4, m->f2_w[0],
+                 m->f2_b[0], 256, 1, ACT_LEAKY, m->fu_a, 256L * H4 * W4);
+    conv3x3_pair(m, m->fu_a, 256L * H4 * W4, 256, H4, W4, m->f3_w[0], NULL,
+                 128, 1, ACT_NONE, m->fu_b, 128L * H4 * W4);
+    ops_resize(o, m->fu_b, 2 * 128, H4, W4, m->fu_c, H2, W2, 0, 0, 2.0f);
+    conv1x1_pair(m, m->f1p, 64, H2 * W2, m->f1_w[1], 128, m->fu_a);
+    ops_axpby(o, m->fu_a, m->fu_a, 1.0f, m->fu_c, 1.0f, 2 * 128L * H2 * W2,
+              2 * 128L * H2 * W2);
+    conv3x3_pair(m, m->fu_a, 128L * H2 * W2, 128, H2, W2, m->f2_w[1],
+                 m->f2_b[1], 128, 1, ACT_LEAKY, m->fu_b, 128L * H2 * W2);
+    conv3x3_pair(m, m->fu_b, 128L * H2 * W2, 128, H2, W2, m->f3_w[1], NULL, 64,
+                 1, ACT_NONE, m->fu_c, 64L * H2 * W2);
+    ops_resize(o, m->fu_c, 2 * 64, H2, W2, m->finep, m->H, m->W, 0, 0, 2.0f);
 }
 
 static void fine_match(struct eloftr_model *m)
@@ -578,8 +607,10 @@ static void match_stages(struct eloftr_model *m, cl_mem dev0, cl_mem dev1,
 
     need_floats(dev0, 0, (long long)hw, "eloftr_match", "image 0");
     need_floats(dev1, 0, (long long)hw, "eloftr_match", "image 1");
-    backbone(m, dev0, 0);
-    backbone(m, dev1, 1);
+    if (dev0 != m->img)
+        ocl_copy(m->ocl, dev0, 0, m->img, 0, hw * sizeof(float));
+    ocl_copy(m->ocl, dev1, 0, m->img, hw * sizeof(float), hw * sizeof(float));
+    backbone(m);
     if (dump) {
         dump_dev(m, dump, tile, "backbone_0", m->x[0], ELOFTR_DIM * n);
         dump_dev(m, dump, tile, "backbone_1", m->x[1], ELOFTR_DIM * n);
@@ -590,8 +621,7 @@ static void match_stages(struct eloftr_model *m, cl_mem dev0, cl_mem dev1,
         dump_dev(m, dump, tile, "coarse_1", m->x[1], ELOFTR_DIM * n);
     }
     coarse_match(m);
-    fusion(m, 0);
-    fusion(m, 1);
+    fusion(m);
     if (dump) {
         dump_dev(m, dump, tile, "fine_0", m->fine[0], ELOFTR_FINE_DIM * hw);
         dump_dev(m, dump, tile, "fine_1", m->fine[1], ELOFTR_FINE_DIM * hw);
@@ -613,7 +643,8 @@ extern "C" void eloftr_match(struct eloftr_model *m, const float *grey0,
     ICOREG_API_BEGIN
     const size_t hw = (size_t)m->H * m->W;
 
-    /* Image 1 goes into the first fusion buffer, free until fusion. */
+    /* Image 1 passes through the first fusion buffer, free until the
+     * fusion, on its way to the pair's input buffer. */
     ocl_write(m->ocl, m->img, 0, grey0, hw * sizeof(float));
     ocl_write(m->ocl, m->fu_a, 0, grey1, hw * sizeof(float));
     match_stages(m, m->img, m->fu_a, dump, tile);
@@ -623,9 +654,10 @@ extern "C" void eloftr_match(struct eloftr_model *m, const float *grey0,
 extern "C" void eloftr_free(struct eloftr_model *m)
 {
     cl_mem *all[] = {
-        &m->img,     &m->s_a,     &m->s_b,     &m->f1[0], &m->f1[1],
-        &m->f2[0],   &m->f2[1],   &m->x[0],    &m->x[1],  &m->fine[0],
-        &m->fine[1], &m->t_q,     &m->t_kv,    &m->t_qn,  &m->t_kvn,
+        &m->f1[0],   &m->f1[1],   &m->f2[0],   &m->f2[1], &m->x[0],
+        &m->x[1],    &m->fine[0], &m->fine[1], &m->img,   &m->s_a,
+        &m->s_b,     &m->f1p,     &m->f2p,     &m->xp,    &m->finep,
+        &m->t_q,     &m->t_kv,    &m->t_qn,    &m->t_kvn,
         &m->t_Q,     &m->t_K,     &m->t_V,     &m->t_O,   &m->t_O2,
         &m->t_cat,   &m->t_tok,   &m->t_h1,    &m->t_h2,  &m->rope,
         &m->s_blk,   &m->row_lse, &m->col_m,   &m->col_s, &m->row_max,

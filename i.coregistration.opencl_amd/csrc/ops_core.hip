@@ -14,6 +14,7 @@
 
 #include "act.h"
 #include "common.h"
+#include "conv.h"
 #include "gemm.h"
 #include "ops.h"
 
@@ -287,12 +288,13 @@ __global__ void __launch_bounds__(256)
     out[idx] = icoreg_act(acc, act, slope);
 }
 
-extern "C" void ops_conv2d(struct ops *o, cl_mem in, int C, int H, int W,
-                           cl_mem w, cl_mem b, int K,
-                           const struct conv_geom *g, cl_mem mean, cl_mem rstd,
-                           cl_mem alpha, int act, float slope, cl_mem out)
+/* ops_conv2d over nb images (in_stride / out_stride floats apart). */
+static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
+                      int C, int H, int W, cl_mem w, cl_mem b, int K,
+                      const struct conv_geom *g, cl_mem mean, cl_mem rstd,
+                      cl_mem alpha, int act, float slope, cl_mem out,
+                      long long out_stride)
 {
-    ICOREG_API_BEGIN
     const char *op = "ops_conv2d";
     int Ho, Wo, cg;
 
@@ -305,6 +307,8 @@ extern "C" void ops_conv2d(struct ops *o, cl_mem in, int C, int H, int W,
         icoreg_fatal("%s: unknown activation %d", op, act);
     if (mean && !rstd)
         icoreg_fatal("%s: mean given without rstd", op);
+    if (nb < 1 || nb > 65535 || in_stride < 0 || out_stride < 0)
+        icoreg_fatal("%s: invalid batch (%d images)", op, nb);
     Ho = ops_conv_out(H, g->kh, g->sy, g->py, g->dy);
     Wo = ops_conv_out(W, g->kw, g->sx, g->px, g->dx);
     if (Ho < 1 || Wo < 1 || C < 1 || K < 1)
@@ -312,9 +316,12 @@ extern "C" void ops_conv2d(struct ops *o, cl_mem in, int C, int H, int W,
     count32((long long)C * H * W, "convolution input");
     count32((long long)K * Ho * Wo, "convolution output");
     cg = C / g->groups;
-    need_floats(in, 0, (long long)C * H * W, op, "input");
+    need_floats(in, 0, (long long)(nb - 1) * in_stride + (long long)C * H * W,
+                op, "input");
     need_floats(w, 0, (long long)K * cg * g->kh * g->kw, op, "weights");
-    need_floats(out, 0, (long long)K * Ho * Wo, op, "output");
+    need_floats(out, 0,
+                (long long)(nb - 1) * out_stride + (long long)K * Ho * Wo, op,
+                "output");
     if (b)
         need_floats(b, 0, K, op, "bias");
     if (mean) {
@@ -322,6 +329,35 @@ extern "C" void ops_conv2d(struct ops *o, cl_mem in, int C, int H, int W,
         need_floats(rstd, 0, C, op, "rstd");
         if (alpha)
             need_floats(alpha, 0, C, op, "alpha");
+    }
+    if (conv_direct_supported(g->kh, g->kw, g->sy, g->sx, g->dy, g->dx,
+                              g->groups) &&
+        g->py == g->px) {
+        conv_args a;
+
+        a.in = cfptr(in);
+        a.w = cfptr(w);
+        a.bias = cfptr(b);
+        a.out = fptr(out);
+        a.in_stride = in_stride;
+        a.out_stride = out_stride;
+        a.C = C;
+        a.H = H;
+        a.W = W;
+        a.K = K;
+        a.Ho = Ho;
+        a.Wo = Wo;
+        a.pad = g->py;
+        a.mean = cfptr(mean);
+        a.rstd = cfptr(rstd);
+        a.gate = mean ? cfptr(alpha) : nullptr;
+        a.act = act;
+        a.slope = slope;
+        prof_scope ps(o->ocl, "conv_direct");
+        conv_direct_launch(a, g->kh, g->sy, nb, o->ocl->cu_count,
+                           stream_of(o->ocl));
+        launch_check("conv_direct");
+        return;
     }
     if (g->groups == 1) {
         gemm_args a;
@@ -335,8 +371,10 @@ extern "C" void ops_conv2d(struct ops *o, cl_mem in, int C, int H, int W,
         a.A = cfptr(w);
         a.lda = kred;
         a.B = cfptr(in);
+        a.sb0 = in_stride;
         a.C = fptr(out);
         a.ldc = (long long)Ho * Wo;
+        a.sc0 = out_stride;
         a.nb1 = 1;
         a.bias = cfptr(b);
         a.biasrow = 1;
@@ -358,26 +396,50 @@ extern "C" void ops_conv2d(struct ops *o, cl_mem in, int C, int H, int W,
         a.mean = cfptr(mean);
         a.rstd = cfptr(rstd);
         a.gate = mean ? cfptr(alpha) : nullptr;
-        pick_tile(K, Ho * Wo, 1, o->ocl->cu_count, &bm, &bn);
+        pick_tile(K, Ho * Wo, nb, o->ocl->cu_count, &bm, &bn);
         prof_scope ps(o->ocl, "conv_igemm");
-        gemm_launch(a, GEMM_B_CONV, 1, bm, bn,
+        gemm_launch(a, GEMM_B_CONV, nb, bm, bn,
                     kred % 4 == 0 && aligned16(w->ptr), false,
                     stream_of(o->ocl));
         launch_check("conv_igemm");
         return;
     }
-    {
+    for (int i = 0; i < nb; i++) {
         long long total = (long long)K * Ho * Wo;
         prof_scope ps(o->ocl, "conv2d_direct");
 
         hipLaunchKernelGGL(conv2d_direct, dim3((unsigned)((total + 255) / 256)),
-                           dim3(256), 0, stream_of(o->ocl), cfptr(in), C, H, W,
-                           cfptr(w), cfptr(b), K, Ho, Wo, g->kh, g->kw, g->sy,
-                           g->sx, g->py, g->px, g->dy, g->dx, g->groups,
-                           cfptr(mean), cfptr(rstd), cfptr(alpha), act, slope,
-                           fptr(out));
+                           dim3(256), 0, stream_of(o->ocl),
+                           cfptr(in) + i * in_stride, C, H, W, cfptr(w),
+                           cfptr(b), K, Ho, Wo, g->kh, g->kw, g->sy, g->sx,
+                           g->py, g->px, g->dy, g->dx, g->groups, cfptr(mean),
+                           cfptr(rstd), cfptr(alpha), act, slope,
+                           fptr(out) + i * out_stride);
         launch_check("conv2d_direct");
     }
+}
+
+extern "C" void ops_conv2d(struct ops *o, cl_mem in, int C, int H, int W,
+                           cl_mem w, cl_mem b, int K,
+                           const struct conv_geom *g, cl_mem mean, cl_mem rstd,
+                           cl_mem alpha, int act, float slope, cl_mem out)
+{
+    ICOREG_API_BEGIN
+    conv_impl(o, 1, in, 0, C, H, W, w, b, K, g, mean, rstd, alpha, act, slope,
+              out, 0);
+    ICOREG_API_END
+}
+
+extern "C" void ops_conv2d_batch(struct ops *o, int nb, cl_mem in,
+                                 long in_stride, int C, int H, int W,
+                                 cl_mem w, cl_mem b, int K,
+                                 const struct conv_geom *g, cl_mem mean,
+                                 cl_mem rstd, cl_mem alpha, int act,
+                                 float slope, cl_mem out, long out_stride)
+{
+    ICOREG_API_BEGIN
+    conv_impl(o, nb, in, in_stride, C, H, W, w, b, K, g, mean, rstd, alpha, act,
+              slope, out, out_stride);
     ICOREG_API_END
 }
 

@@ -51,8 +51,12 @@ struct eloftr_model {
      * side), set before eloftr_alloc. */
     float pos_scale;
     int H, W, h, w, ah, aw, nmax;
-    /* Work buffers (eloftr_alloc). */
-    cl_mem img, s_a, s_b, f1[2], f2[2], x[2], fine[2];
+    /* Work buffers (eloftr_alloc). Both images of the pair sit in one
+     * allocation (img, s_a, s_b, f1p, f2p, xp, finep, fu_*: image 1 right
+     * after image 0), so that the backbone and the fusion run each layer
+     * once for the pair; f1[k], f2[k], x[k], fine[k] are views of image k. */
+    cl_mem img, s_a, s_b, f1p, f2p, xp, finep;
+    cl_mem f1[2], f2[2], x[2], fine[2];
     cl_mem t_q, t_kv, t_qn, t_kvn, t_Q, t_K, t_V, t_O, t_O2, t_cat, t_tok,
         t_h1, t_h2, rope;
     cl_mem s_blk, row_lse, col_m, col_s, row_max, row_arg, col_max, col_arg;

@@ -100,13 +100,23 @@ int ops_conv_out(int n, int k, int s, int p, int d);
 /* in (C, H, W) into out (K, Ho, Wo), weights (K, C / groups, kh, kw).
  * mean/rstd/alpha (NULL for none) normalise and gate every input value,
  * prelu((x - mean[c]) * rstd[c], alpha[c]), before the zero padding, as
- * DISK's blocks (ops.h:84-92). One group: implicit-GEMM fp32 MFMA
- * kernel (any kernel size, stride, padding, dilation, with or without
- * the input normalisation). Groups = channels: depthwise kernel. Other
- * group counts: a direct kernel. */
+ * DISK's blocks (ops.h:84-92). One group, 3 x 3 or 5 x 5, stride 1
+ * or 2: direct fp32 MFMA kernel on LDS input patches; other one-group
+ * geometries: implicit-GEMM fp32 MFMA kernel; grouped: a direct
+ * kernel. */
 void ops_conv2d(struct ops *o, cl_mem in, int C, int H, int W, cl_mem w,
                 cl_mem b, int K, const struct conv_geom *g, cl_mem mean,
                 cl_mem rstd, cl_mem alpha, int act, float slope, cl_mem out);
+
+/* Extension with no counterpart in the reference: ops_conv2d over nb
+ * images stored in_stride / out_stride floats apart (the two images of
+ * a tile pair), in one launch; the same weights, bias and input
+ * normalisation for every image. */
+void ops_conv2d_batch(struct ops *o, int nb, cl_mem in, long in_stride, int C,
+                      int H, int W, cl_mem w, cl_mem b, int K,
+                      const struct conv_geom *g, cl_mem mean, cl_mem rstd,
+                      cl_mem alpha, int act, float slope, cl_mem out,
+                      long out_stride);
 
 /* Instance statistics of (C, HW): mean and 1 / sqrt(biased var + eps)
  * per channel. ops.h:96-97. */

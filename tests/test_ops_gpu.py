@@ -74,3 +74,48 @@ def test_attention_shapes(shape, dev, ic, orc):
     got = dev.read(O, Nq * E)
     err = opcases.rel_err(got, ref)
     assert err <= 1e-5, f"{shape}: {err:.2e}"
+
+
+CONV_SHAPES = [
+    # (nb, C, H, W, K, k, s, p, norm, act): ELoFTR backbone / fusion, VGG,
+    # DISK (5 x 5 with normalisation), stride 2, ragged sizes.
+    (2, 64, 40, 48, 64, 3, 1, 1, 0, 2),
+    (2, 128, 20, 24, 256, 3, 2, 1, 0, 2),
+    (1, 256, 20, 20, 256, 3, 1, 1, 0, 3),
+    (2, 1, 64, 96, 64, 3, 2, 1, 0, 2),
+    (1, 3, 37, 45, 129, 5, 1, 2, 1, 0),
+    (1, 80, 33, 31, 129, 5, 1, 2, 1, 0),
+    (1, 7, 21, 35, 10, 5, 2, 2, 1, 2),
+    (2, 130, 19, 70, 200, 3, 1, 1, 0, 1),
+]
+
+
+@pytest.mark.parametrize("shape", CONV_SHAPES, ids=[str(s) for s in CONV_SHAPES])
+def test_conv_shapes(shape, dev, ic, orc):
+    import ctypes as C
+    from oracle_lib import fp
+    nb, Cc, H, W, K, k, s, p, norm, act = shape
+    print(f"[conv] {shape}", flush=True)
+    rng = np.random.default_rng(100 + Cc + K)
+    x = rng.uniform(-1, 1, nb * Cc * H * W).astype(np.float32)
+    w = (rng.uniform(-1, 1, K * Cc * k * k) / np.sqrt(Cc * k * k)).astype(np.float32)
+    b = rng.uniform(-1, 1, K).astype(np.float32)
+    mean = rng.uniform(-0.5, 0.5, Cc).astype(np.float32) if norm else None
+    rstd = rng.uniform(0.5, 2, Cc).astype(np.float32) if norm else None
+    alpha = rng.uniform(0, 0.5, Cc).astype(np.float32) if norm else None
+    Ho, Wo = opcases.conv_out(H, k, s, p), opcases.conv_out(W, k, s, p)
+    ref = np.zeros(nb * K * Ho * Wo, np.float32)
+    for i in range(nb):
+        orc.orc_conv2d(fp(x[i * Cc * H * W:]), Cc, H, W, fp(w), fp(b), K, k, k, s, s, p, p, 1, 1,
+                       1, fp(mean), fp(rstd), fp(alpha), act, 0.1,
+                       fp(ref[i * K * Ho * Wo:]))
+    X, Wt, B = dev.upload(x), dev.upload(w), dev.upload(b)
+    Y = dev.zeros(nb * K * Ho * Wo)
+    mb = [dev.upload(v) if v is not None else None for v in (mean, rstd, alpha)]
+    g = ic.geom(k, k, s, s, p, p, 1, 1, 1)
+    dev.api.ops_conv2d_batch(dev.po, nb, X.mem, Cc * H * W, Cc, H, W, Wt.mem, B.mem, K,
+                             C.byref(g), *[ic.mem(v) for v in mb], act, 0.1, Y.mem,
+                             K * Ho * Wo)
+    got = dev.read(Y, nb * K * Ho * Wo)
+    err = opcases.rel_err(got, ref)
+    assert err <= 1e-5, f"{shape}: {err:.2e}"
