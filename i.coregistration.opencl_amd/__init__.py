@@ -153,6 +153,15 @@ SIGNATURES = {
     "eloftr_conf_row": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
     "eloftr_conf_col": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
     "eloftr_fine": (None, [_O, Mem, Mem, _I, _I, Mem, _I, _F, Mem]),
+    "roma_row_norm": (None, [_O, Mem, _I, _I, Mem]),
+    "roma_cos_exp": (None, [_O, Mem, Mem, Mem, _I, _I, _F, _F]),
+    "roma_cls_to_flow": (None, [_O, Mem, _I, _I, _I, _I, Mem, Mem]),
+    "roma_warp_sample": (None, [_O, Mem, _I, _I, _I, Mem, Mem, _I]),
+    "roma_local_corr": (None, [_O, Mem, Mem, _I, _I, _I, _I, Mem, Mem, _I]),
+    "roma_disp": (None, [_O, Mem, _I, _I, _F, _F, Mem]),
+    "roma_update": (None, [_O, Mem, Mem, Mem, _I, _F, _F, _F]),
+    "roma2_update": (None, [_O, Mem, Mem, Mem, _I, _F, _F]),
+    "roma_dwconv5": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem]),
     # binding glue (include/icoreg_glue.h)
     "icoreg_pth_new": (_P, []),
     "icoreg_eloftr_new": (_P, []),

@@ -50,6 +50,60 @@ void eloftr_conf_col(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse,
 void eloftr_fine(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
                  cl_mem cells, int M, float T, cl_mem out);
 
+/* ---- RoMa (roma_kernels.cl) ----------------------------------------------
+ * Warps are channel-major (2, n): x then y, normalised to -1..1 with
+ * align_corners = 0 (cell centres at -1 + (2 i + 1) / size). */
+
+/* Euclidean norm of each row of X (rows x C). roma_kernels.cl:9-23. */
+void roma_row_norm(struct ops *o, cl_mem X, int rows, int C, cl_mem out);
+
+/* In place on S (N x M): exp((S / (nx[i] ny[j] + eps) - 1) / T), RoMa's
+ * cosine kernel. roma_kernels.cl:25-38. */
+void roma_cos_exp(struct ops *o, cl_mem S, cl_mem nx, cl_mem ny, int N, int M,
+                  float T, float eps);
+
+/* Per token (row of L with ld floats: C = res^2 anchor logits, then the
+ * certainty logit): first argmax, softmax over the anchors, its mode and
+ * four neighbours (indices clamped to 0..C-1), probability-weighted mean
+ * anchor position into flow (2, n), certainty logit into cert (n).
+ * roma_kernels.cl:40-102. */
+void roma_cls_to_flow(struct ops *o, cl_mem L, int ld, int C, int res, int n,
+                      cl_mem flow, cl_mem cert);
+
+/* in (C, H, W) sampled bilinearly (zero padding) at the warp flow (2, n)
+ * of the same grid (n = H W) into channels coff.. of out (*, n).
+ * roma_kernels.cl:104-141. */
+void roma_warp_sample(struct ops *o, cl_mem in, int C, int H, int W,
+                      cl_mem flow, cl_mem out, int coff);
+
+/* Local correlation: for each cell and window offset k = (a, b) of
+ * (2 r + 1)^2 (a the row), f1 (C, n) / sqrt(C) dotted with f2 (C, H, W)
+ * sampled at the warp shifted by (b - r, a - r) cells, into channels
+ * coff + k of out. C <= 1024, r <= 7. roma_kernels.cl:143-192. */
+void roma_local_corr(struct ops *o, cl_mem f1, cl_mem f2, int C, int H, int W,
+                     int r, cl_mem flow, cl_mem out, int coff);
+
+/* Displacement input (fx, fy) * (warp - own cell centre) into out (2, n).
+ * roma_kernels.cl:194-208. */
+void roma_disp(struct ops *o, cl_mem flow, int H, int W, float fx, float fy,
+               cl_mem out);
+
+/* flow += scale d / (4 Wf, 4 Hf); cert += d2 (d: 3 x n).
+ * roma_kernels.cl:210-224. */
+void roma_update(struct ops *o, cl_mem flow, cl_mem cert, cl_mem d, int n,
+                 float scale, float Wf, float Hf);
+
+/* RoMa v2: flow += d / (4 W, 4 H); conf (4, n) += overlap logit and the
+ * precision (l00^2, l00 l10, l10^2 + l11^2) of the Cholesky factor with
+ * softplus diagonal (threshold 20) + 1e-6. roma_kernels.cl:226-250. */
+void roma2_update(struct ops *o, cl_mem flow, cl_mem conf, cl_mem d, int n,
+                  float W, float H);
+
+/* Depthwise 5 x 5, stride 1, zero padding 2, bias, ReLU on (C, H, W)
+ * (weights (C, 25)). roma_kernels.cl:252-284. */
+void roma_dwconv5(struct ops *o, cl_mem in, int C, int H, int W, cl_mem w,
+                  cl_mem bias, cl_mem out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -121,6 +121,27 @@ void orc_eloftr_fine(const float *f0, const float *f1, int H, int W,
                      const int *cells, int M, float T, float *out,
                      float *margin);
 
+/* ---- RoMa (roma_kernels.cl) -------------------------------------------- */
+
+void orc_roma_row_norm(const float *X, int rows, int C, float *out);
+void orc_roma_cos_exp(float *S, const float *nx, const float *ny, int N, int M,
+                      float T, float eps);
+void orc_roma_cls_to_flow(const float *L, int ld, int C, int res, int n,
+                          float *flow, float *cert);
+void orc_roma_warp_sample(const float *in, int C, int H, int W,
+                          const float *flow, float *out, int coff);
+void orc_roma_local_corr(const float *f1, const float *f2, int C, int H,
+                         int W, int r, const float *flow, float *out,
+                         int coff);
+void orc_roma_disp(const float *flow, int H, int W, float fx, float fy,
+                   float *out);
+void orc_roma_update(float *flow, float *cert, const float *d, int n,
+                     float scale, float Wf, float Hf);
+void orc_roma2_update(float *flow, float *conf, const float *d, int n, float W,
+                      float H);
+void orc_roma_dwconv5(const float *in, int C, int H, int W, const float *w,
+                      const float *bias, float *out);
+
 /* A named weight array (the safetensors tensors, float32). */
 struct orc_named {
     const char *name;

@@ -41,6 +41,15 @@ SIGS = {
     "orc_eloftr_coarse": (None, [_FP, _FP, _I, _I, _F, _I, _FP, _IP, _IP, _FP, _FP]),
     "orc_eloftr_select": (_I, [_FP, _IP, _IP, _I, _I, _F, _I, _IP, _IP, _FP]),
     "orc_eloftr_fine": (None, [_FP, _FP, _I, _I, _IP, _I, _F, _FP, _FP]),
+    "orc_roma_row_norm": (None, [_FP, _I, _I, _FP]),
+    "orc_roma_cos_exp": (None, [_FP, _FP, _FP, _I, _I, _F, _F]),
+    "orc_roma_cls_to_flow": (None, [_FP, _I, _I, _I, _I, _FP, _FP]),
+    "orc_roma_warp_sample": (None, [_FP, _I, _I, _I, _FP, _FP, _I]),
+    "orc_roma_local_corr": (None, [_FP, _FP, _I, _I, _I, _I, _FP, _FP, _I]),
+    "orc_roma_disp": (None, [_FP, _I, _I, _F, _F, _FP]),
+    "orc_roma_update": (None, [_FP, _FP, _FP, _I, _F, _F, _F]),
+    "orc_roma2_update": (None, [_FP, _FP, _FP, _I, _F, _F]),
+    "orc_roma_dwconv5": (None, [_FP, _I, _I, _I, _FP, _FP, _FP]),
 }
 
 class Named(C.Structure):

@@ -105,3 +105,24 @@ def test_bounds_checks_reject_out_of_range_views(ic):
         api.ops_conv2d(C.byref(ops), buf, 3, 4, 4, buf, None, 4, C.byref(g), None,
                        None, None, 0, 0.0, buf)
     lib.ocl_release(C.byref(buf))
+
+
+def test_roma_kernels_reject_bad_sizes(ic):
+    """RoMa launchers refuse sizes their LDS staging cannot hold (C above
+    1024 or r above 7 for local correlation) and views beyond a buffer,
+    on the host before any launch."""
+    api = ic.api()
+    lib = ic.lib()
+    buf = lib.ocl_wrap(None, 64)
+    ops = ic.Ops()
+    be = ic.OclBackend()
+    ops.ocl = C.pointer(be)
+    with pytest.raises(ic.IcoregError, match="roma_local_corr: invalid sizes C=1025"):
+        api.roma_local_corr(C.byref(ops), buf, buf, 1025, 1, 1, 1, buf, buf, 0)
+    with pytest.raises(ic.IcoregError, match="roma_local_corr: invalid sizes C=4 r=8"):
+        api.roma_local_corr(C.byref(ops), buf, buf, 4, 1, 1, 8, buf, buf, 0)
+    with pytest.raises(ic.IcoregError, match="roma_warp_sample"):
+        api.roma_warp_sample(C.byref(ops), buf, 4, 4, 4, buf, buf, 0)
+    with pytest.raises(ic.IcoregError, match="roma_cls_to_flow"):
+        api.roma_cls_to_flow(C.byref(ops), buf, 64, 64, 8, 1, buf, buf)
+    lib.ocl_release(C.byref(buf))

@@ -1,0 +1,163 @@
+# SPDX-License-Identifier: Unlicense
+"""GPU: RoMa's kernels (roma_kernels.cl contracts) on the HIP library
+against the oracle on the same float32 inputs. Tolerance 1e-5 of the
+largest reference magnitude (2e-5 where the sum runs over 1024 channels),
+cls_to_flow's certainty copied bit-exact; edge cases: warps on the
+border, far outside, a million cells off and non-finite, modes on the
+anchor grid's corners and ties, ragged tiles, the largest channel count
+and radius."""
+
+import numpy as np
+import pytest
+
+from oracle_lib import fp
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+    return np.abs(a - b).max() / max(np.abs(b).max(), 1e-30)
+
+
+def warps(rng, H, W):
+    gy = -1 + (2 * np.arange(H) + 1) / H
+    gx = -1 + (2 * np.arange(W) + 1) / W
+    gy, gx = np.meshgrid(gy, gx, indexing="ij")
+    f = np.stack([gx, gy]) + 0.3 * rng.standard_normal((2, H, W))
+    flat = f.reshape(2, -1)
+    k = rng.choice(H * W, 40, replace=False)
+    flat[:, k[:10]] *= 3.0
+    flat[0, k[10:15]] = 1.0
+    flat[1, k[15:20]] = -1.0
+    flat[0, k[20]] = 1e6
+    flat[1, k[21]] = -3e9
+    flat[0, k[22]] = np.nan
+    flat[1, k[23]] = np.inf
+    flat[0, k[24]] = -np.inf
+    return np.ascontiguousarray(f.astype(np.float32))
+
+
+def test_row_norm_cos_exp(dev, ic, orc):
+    print("[roma] row_norm / cos_exp", flush=True)
+    rng = np.random.default_rng(31)
+    N, M, C = 1000, 777, 512
+    X = rng.standard_normal((N, C)).astype(np.float32)
+    Y = rng.standard_normal((M, C)).astype(np.float32)
+    nx, ny = np.zeros(N, np.float32), np.zeros(M, np.float32)
+    orc.orc_roma_row_norm(fp(X), N, C, fp(nx))
+    orc.orc_roma_row_norm(fp(Y), M, C, fp(ny))
+    S = np.ascontiguousarray(X @ Y.T / 8)
+    Sref = S.copy()
+    orc.orc_roma_cos_exp(fp(Sref), fp(nx), fp(ny), N, M, 0.2, 1e-6)
+    bx, by, bnx, bny, bS = (dev.upload(X), dev.upload(Y), dev.zeros(N), dev.zeros(M),
+                            dev.upload(S))
+    a, m = dev.api, ic.mem
+    a.roma_row_norm(dev.po, m(bx), N, C, m(bnx))
+    a.roma_row_norm(dev.po, m(by), M, C, m(bny))
+    a.roma_cos_exp(dev.po, m(bS), m(bnx), m(bny), N, M, 0.2, 1e-6)
+    assert rel(dev.read(bnx), nx) < TOL
+    assert rel(dev.read(bny), ny) < TOL
+    assert rel(dev.read(bS), Sref) < 1e-4
+
+
+@pytest.mark.parametrize("res,n", [(64, 700), (8, 33)])
+def test_cls_to_flow(dev, ic, orc, res, n):
+    print(f"[roma] cls_to_flow res={res} n={n}", flush=True)
+    rng = np.random.default_rng(res)
+    C = res * res
+    ld = C + 1
+    L = (2 * rng.standard_normal((n, ld))).astype(np.float32)
+    for t, idx in enumerate([[0], [C - 1], [res - 1], [C - res], [5, 9], [C - 2, 1]]):
+        L[t, :C] = -5
+        L[t, idx] = 9
+    flow, cert = np.zeros(2 * n, np.float32), np.zeros(n, np.float32)
+    orc.orc_roma_cls_to_flow(fp(L), ld, C, res, n, fp(flow), fp(cert))
+    bL, bf, bc = dev.upload(L), dev.zeros(2 * n), dev.zeros(n)
+    dev.api.roma_cls_to_flow(dev.po, bL.mem, ld, C, res, n, bf.mem, bc.mem)
+    assert rel(dev.read(bf), flow) < TOL
+    assert np.array_equal(dev.read(bc), cert)
+
+
+@pytest.mark.parametrize("C,H,W", [(3, 37, 45), (64, 70, 70)])
+def test_warp_sample(dev, ic, orc, C, H, W):
+    print(f"[roma] warp_sample C={C} {H}x{W}", flush=True)
+    rng = np.random.default_rng(C)
+    x = rng.standard_normal((C, H, W)).astype(np.float32)
+    f = warps(rng, H, W)
+    n = H * W
+    ref = np.zeros((C + 1, n), np.float32)
+    orc.orc_roma_warp_sample(fp(x), C, H, W, fp(f), fp(ref), 1)
+    bx, bf = dev.upload(x), dev.upload(f)
+    out = dev.upload(np.full((C + 1, n), 7.0, np.float32))
+    dev.api.roma_warp_sample(dev.po, bx.mem, C, H, W, bf.mem, out.mem, 1)
+    got = dev.read(out).reshape(C + 1, n)
+    assert np.all(got[0] == 7.0)
+    assert rel(got[1:], ref[1:]) < TOL
+
+
+@pytest.mark.parametrize("C,H,W,r", [(512, 35, 35, 7), (1024, 20, 27, 3),
+                                     (256, 70, 70, 2), (24, 9, 13, 7)])
+def test_local_corr(dev, ic, orc, C, H, W, r):
+    print(f"[roma] local_corr C={C} {H}x{W} r={r}", flush=True)
+    rng = np.random.default_rng(C + r)
+    f0 = rng.standard_normal((C, H, W)).astype(np.float32)
+    f1 = rng.standard_normal((C, H, W)).astype(np.float32)
+    f = warps(rng, H, W)
+    n, K = H * W, (2 * r + 1) ** 2
+    ref = np.zeros((K + 2, n), np.float32)
+    orc.orc_roma_local_corr(fp(f0), fp(f1), C, H, W, r, fp(f), fp(ref), 2)
+    b0, b1, bf = dev.upload(f0), dev.upload(f1), dev.upload(f)
+    out = dev.upload(np.full((K + 2, n), 7.0, np.float32))
+    dev.api.roma_local_corr(dev.po, b0.mem, b1.mem, C, H, W, r, bf.mem, out.mem, 2)
+    got = dev.read(out).reshape(K + 2, n)
+    assert np.all(got[:2] == 7.0)
+    assert rel(got[2:], ref[2:]) < 2e-5
+
+
+def test_disp_updates(dev, ic, orc):
+    print("[roma] disp / update / update2", flush=True)
+    rng = np.random.default_rng(41)
+    H, W = 70, 93
+    n = H * W
+    flow = rng.uniform(-1, 1, (2, n)).astype(np.float32)
+    a, m = dev.api, ic.mem
+    ref = np.zeros((2, n), np.float32)
+    orc.orc_roma_disp(fp(flow), H, W, 35.0, 17.5, fp(ref))
+    bflow, bd = dev.upload(flow), dev.zeros(2 * n)
+    a.roma_disp(dev.po, m(bflow), H, W, 35.0, 17.5, m(bd))
+    assert rel(dev.read(bd), ref) < TOL
+
+    d = (4 * rng.standard_normal((6, n))).astype(np.float32)
+    d[3, :6] = [25.0, -30.0, 0.0, 19.9, 20.1, -90.0]
+    cert = rng.standard_normal(n).astype(np.float32)
+    rf, rc = flow.copy(), cert.copy()
+    orc.orc_roma_update(fp(rf), fp(rc), fp(d), n, 0.5, 280.0, 210.0)
+    bf, bc, bdd = dev.upload(flow), dev.upload(cert), dev.upload(d)
+    a.roma_update(dev.po, m(bf), m(bc), m(bdd), n, 0.5, 280.0, 210.0)
+    assert rel(dev.read(bf), rf) < TOL
+    assert rel(dev.read(bc), rc) < TOL
+
+    conf = rng.standard_normal((4, n)).astype(np.float32)
+    rf2, rc2 = flow.copy(), conf.copy()
+    orc.orc_roma2_update(fp(rf2), fp(rc2), fp(d), n, 93.0, 70.0)
+    bf2, bc2 = dev.upload(flow), dev.upload(conf)
+    a.roma2_update(dev.po, m(bf2), m(bc2), m(bdd), n, 93.0, 70.0)
+    assert rel(dev.read(bf2), rf2) < TOL
+    assert rel(dev.read(bc2), rc2) < TOL
+
+
+@pytest.mark.parametrize("C,H,W", [(5, 37, 70), (64, 140, 140), (2, 3, 4)])
+def test_dwconv5(dev, ic, orc, C, H, W):
+    print(f"[roma] dwconv5 C={C} {H}x{W}", flush=True)
+    rng = np.random.default_rng(C * H)
+    x = rng.standard_normal((C, H, W)).astype(np.float32)
+    w = rng.standard_normal((C, 25)).astype(np.float32)
+    b = rng.standard_normal(C).astype(np.float32)
+    ref = np.zeros((C, H, W), np.float32)
+    orc.orc_roma_dwconv5(fp(x), C, H, W, fp(w), fp(b), fp(ref))
+    bx, bw, bb, bo = dev.upload(x), dev.upload(w), dev.upload(b), dev.zeros(C * H * W)
+    dev.api.roma_dwconv5(dev.po, bx.mem, C, H, W, bw.mem, bb.mem, bo.mem)
+    assert rel(dev.read(bo), ref) < TOL

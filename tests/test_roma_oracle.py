@@ -1,0 +1,137 @@
+# SPDX-License-Identifier: Unlicense
+"""CPU: the oracle's restatement of roma_kernels.cl pinned against float64
+torch statements of RoMa's published operations (roma_ref.py): cosine
+kernel, cls_to_flow_refine, grid_sample, local_correlation, displacement,
+v1 / v2 updates, depthwise 5 x 5. Each check would fail on a swapped axis,
+a dropped term or an off-by-one cell offset."""
+
+import numpy as np
+import pytest
+import torch
+
+import roma_ref as R
+from oracle_lib import fp
+
+TOL = 2e-5
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+    return np.abs(a - b).max() / max(np.abs(b).max(), 1e-30)
+
+
+def test_row_norm_and_cos_exp(orc):
+    rng = np.random.default_rng(1)
+    N, M, C = 37, 53, 96
+    X = rng.standard_normal((N, C)).astype(np.float32)
+    Y = rng.standard_normal((M, C)).astype(np.float32)
+    nx, ny = np.zeros(N, np.float32), np.zeros(M, np.float32)
+    orc.orc_roma_row_norm(fp(X), N, C, fp(nx))
+    orc.orc_roma_row_norm(fp(Y), M, C, fp(ny))
+    assert rel(nx, torch.linalg.norm(R.t64(X), dim=1).numpy()) < TOL
+    S = np.ascontiguousarray(X @ Y.T)
+    T, eps = 0.2, 1e-6
+    orc.orc_roma_cos_exp(fp(S), fp(nx), fp(ny), N, M, T, eps)
+    x, y = R.t64(X), R.t64(Y)
+    cos = (x @ y.T) / (x.norm(dim=1)[:, None] * y.norm(dim=1)[None] + eps)
+    assert rel(S, torch.exp((cos - 1) / T).numpy()) < 1e-4
+
+
+@pytest.mark.parametrize("res", [8, 16])
+def test_cls_to_flow(orc, res):
+    rng = np.random.default_rng(res)
+    C, n = res * res, 300
+    ld = C + 3
+    L = (3 * rng.standard_normal((n, ld))).astype(np.float32)
+    # modes on the grid's edges and corners (clamped neighbours) and a tie
+    L[0, :C] = -5
+    L[0, 0] = 9
+    L[1, :C] = -5
+    L[1, C - 1] = 9
+    L[2, :C] = -5
+    L[2, res - 1] = 9
+    L[3, :C] = -5
+    L[3, 5] = L[3, 9] = 9
+    flow, cert = np.zeros(2 * n, np.float32), np.zeros(n, np.float32)
+    orc.orc_roma_cls_to_flow(fp(L), ld, C, res, n, fp(flow), fp(cert))
+    ref = R.cls_to_flow_refine(R.t64(L[:, :C]).T).numpy()
+    assert rel(flow, ref) < TOL
+    assert np.array_equal(cert, L[:, C])
+
+
+def warps(rng, H, W, n_out=40):
+    """Warps (2, H, W) around the identity, with some far outside, some
+    on the border and one a million cells off (non-finite warps are the
+    GPU tests' case: torch leaves them unspecified)."""
+    gy, gx = np.meshgrid(R.cell_centres(H).numpy(), R.cell_centres(W).numpy(), indexing="ij")
+    f = np.stack([gx, gy]) + 0.3 * rng.standard_normal((2, H, W))
+    flat = f.reshape(2, -1)
+    k = rng.choice(H * W, n_out, replace=False)
+    flat[:, k[:10]] *= 3.0
+    flat[0, k[10:15]] = 1.0
+    flat[1, k[15:20]] = -1.0
+    flat[0, k[20]] = 1e6
+    return f.astype(np.float32)
+
+
+def test_warp_sample(orc):
+    rng = np.random.default_rng(3)
+    C, H, W = 5, 19, 23
+    x = rng.standard_normal((C, H, W)).astype(np.float32)
+    f = warps(rng, H, W)
+    out = np.zeros((C + 2, H * W), np.float32)
+    orc.orc_roma_warp_sample(fp(x), C, H, W, fp(f), fp(out), 2)
+    ref = R.grid_sample_flow(R.t64(x), R.t64(f)).reshape(C, -1).numpy()
+    assert rel(out[2:], ref) < TOL
+    assert not out[:2].any()
+
+
+@pytest.mark.parametrize("C,H,W,r", [(16, 12, 17, 3), (32, 9, 11, 7), (8, 15, 13, 2)])
+def test_local_corr(orc, C, H, W, r):
+    rng = np.random.default_rng(C + r)
+    f0 = rng.standard_normal((C, H, W)).astype(np.float32)
+    f1 = rng.standard_normal((C, H, W)).astype(np.float32)
+    f = warps(rng, H, W, n_out=24)
+    K = (2 * r + 1) ** 2
+    out = np.zeros((K + 1, H * W), np.float32)
+    orc.orc_roma_local_corr(fp(f0), fp(f1), C, H, W, r, fp(f), fp(out), 1)
+    ref = R.local_correlation(R.t64(f0), R.t64(f1), R.t64(f), r).reshape(K, -1).numpy()
+    assert rel(out[1:], ref) < 1e-4
+    assert not out[0].any()
+
+
+def test_disp_and_updates(orc):
+    rng = np.random.default_rng(5)
+    H, W = 14, 22
+    n = H * W
+    flow = rng.uniform(-1, 1, (2, n)).astype(np.float32)
+    out = np.zeros((2, n), np.float32)
+    orc.orc_roma_disp(fp(flow), H, W, 11.0, 7.0, fp(out))
+    assert rel(out, R.disp(R.t64(flow), H, W, 11.0, 7.0).numpy()) < TOL
+
+    d = (4 * rng.standard_normal((6, n))).astype(np.float32)
+    d[3, :5] = [25.0, -30.0, 0.0, 19.9, 20.1]
+    f1, c1 = flow.copy(), rng.standard_normal(n).astype(np.float32)
+    c1_0 = c1.copy()
+    orc.orc_roma_update(fp(f1), fp(c1), fp(d), n, 0.5, 80.0, 60.0)
+    ref_f = R.t64(flow) + 0.5 * R.t64(d[:2]) / torch.tensor([[320.0], [240.0]], dtype=torch.float64)
+    assert rel(f1, ref_f.numpy()) < TOL
+    assert rel(c1, c1_0 + d[2]) < TOL
+
+    f2, conf = flow.copy(), rng.standard_normal((4, n)).astype(np.float32)
+    conf0 = conf.copy()
+    orc.orc_roma2_update(fp(f2), fp(conf), fp(d), n, 40.0, 30.0)
+    rf, rc = R.update2(R.t64(flow), R.t64(conf0), R.t64(d), 40.0, 30.0)
+    assert rel(f2, rf.numpy()) < TOL
+    assert rel(conf, rc.numpy()) < 1e-4
+
+
+def test_dwconv5(orc):
+    rng = np.random.default_rng(6)
+    C, H, W = 6, 21, 40
+    x = rng.standard_normal((C, H, W)).astype(np.float32)
+    w = rng.standard_normal((C, 25)).astype(np.float32)
+    b = rng.standard_normal(C).astype(np.float32)
+    out = np.zeros((C, H, W), np.float32)
+    orc.orc_roma_dwconv5(fp(x), C, H, W, fp(w), fp(b), fp(out))
+    assert rel(out, R.dwconv5_relu(R.t64(x), R.t64(w), R.t64(b)).numpy()) < TOL
