@@ -162,6 +162,16 @@ SIGNATURES = {
     "roma_update": (None, [_O, Mem, Mem, Mem, _I, _F, _F, _F]),
     "roma2_update": (None, [_O, Mem, Mem, Mem, _I, _F, _F]),
     "roma_dwconv5": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem]),
+    "roma_gp_work_bytes": (C.c_size_t, [_I, _I]),
+    "roma_gp_solve": (None, [_O, Mem, _I, _F, Mem, _I, Mem, Mem]),
+    # RoMa model (include/roma.h)
+    "roma_load": (None, [_P, _O, _P, _P]),
+    "roma_load_v2": (None, [_P, _P]),
+    "roma_set_coarse": (None, [_P, _I]),
+    "roma_alloc": (None, [_P, _I, _I]),
+    "roma_match": (None, [_P, _P, _P, _S, _I]),
+    "roma_coarse_device": (None, [_P, Mem]),
+    "roma_free": (None, [_P]),
     # binding glue (include/icoreg_glue.h)
     "icoreg_pth_new": (_P, []),
     "icoreg_eloftr_new": (_P, []),
@@ -172,6 +182,12 @@ SIGNATURES = {
                                         C.POINTER(C.POINTER(C.c_int)), C.POINTER(C.POINTER(C.c_int))]),
     "icoreg_eloftr_set_pos_scale": (None, [_P, _F]),
     "icoreg_eloftr_buffer": (Mem, [_P, _S]),
+    "icoreg_roma_new": (_P, []),
+    "icoreg_roma_result": (_I, [_P, C.POINTER(C.POINTER(C.c_float)), C.POINTER(C.POINTER(C.c_float)),
+                                C.POINTER(C.POINTER(C.c_float))]),
+    "icoreg_roma_buffer": (Mem, [_P, _S]),
+    "icoreg_roma_gp_info": (_I, [_P]),
+    "icoreg_roma_set_imagenet": (None, [_P, _I]),
 }
 
 # Entry points that never raise through the fatal path (no error check).
@@ -181,7 +197,9 @@ _NO_CHECK = {"icoreg_set_fatal_mode", "icoreg_last_error", "icoreg_clear_error",
              "pth_find", "pth_numel", "pth_bytes", "pth_strip_prefix",
              "icoreg_pth_new", "icoreg_eloftr_new", "icoreg_struct_delete",
              "icoreg_eloftr_result", "icoreg_eloftr_coarse_stats",
-             "icoreg_eloftr_set_pos_scale", "icoreg_eloftr_buffer"}
+             "icoreg_eloftr_set_pos_scale", "icoreg_eloftr_buffer", "roma_gp_work_bytes",
+             "icoreg_roma_new", "icoreg_roma_result", "icoreg_roma_buffer",
+             "icoreg_roma_set_imagenet"}
 
 _lib = None
 
@@ -409,3 +427,63 @@ class Eloftr:
             self.dev.api.pth_close(self.pf)
             lib().icoreg_struct_delete(self.pf)
             self.pf = None
+
+
+class Roma:
+    """RoMa on the device: roma_load (+ roma_load_v2) / roma_alloc /
+    roma_match of the C-ABI, weights from safetensors files."""
+
+    def __init__(self, dev, weights_path, dino_path, H, W, v2_path=None, coarse=560):
+        self.dev = dev
+        a = dev.api
+        self.pfs = []
+        for p in (weights_path, dino_path) + ((v2_path,) if v2_path else ()):
+            pf = lib().icoreg_pth_new()
+            a.pth_open(pf, str(p).encode())
+            self.pfs.append(pf)
+        self.m = lib().icoreg_roma_new()
+        a.roma_load(self.m, dev.po, self.pfs[0], self.pfs[1])
+        if v2_path:
+            a.roma_load_v2(self.m, self.pfs[2])
+        a.roma_set_coarse(self.m, coarse)
+        a.roma_alloc(self.m, H, W)
+        self.H, self.W, self.coarse, self.v2 = H, W, coarse, bool(v2_path)
+        self.c16 = coarse // 14
+
+    def match(self, imgA, imgB, dump=None, tile=1):
+        A = np.ascontiguousarray(imgA, np.float32)
+        B = np.ascontiguousarray(imgB, np.float32)
+        self.dev.api.roma_match(self.m, A.ctypes.data, B.ctypes.data,
+                                dump.encode() if dump else None, tile)
+        return self.result()
+
+    def coarse_device(self, pair):
+        self.dev.api.roma_coarse_device(self.m, pair.mem)
+
+    def result(self):
+        f, c, s = (C.POINTER(C.c_float)(), C.POINTER(C.c_float)(), C.POINTER(C.c_float)())
+        n = lib().icoreg_roma_result(self.m, C.byref(f), C.byref(c), C.byref(s))
+        out = {"flow": np.ctypeslib.as_array(f, (2 * n,)).copy().reshape(2, self.H, self.W),
+               "cert": np.ctypeslib.as_array(c, (n,)).copy().reshape(self.H, self.W)}
+        if self.v2:
+            out["sd"] = np.ctypeslib.as_array(s, (n,)).copy().reshape(self.H, self.W)
+        return out
+
+    def buffer(self, name, count, off=0):
+        mem = lib().icoreg_roma_buffer(self.m, name.encode())
+        out = np.empty(count, np.float32)
+        self.dev.api.ocl_read(self.dev.pb, mem, off * 4, out.ctypes.data, out.nbytes)
+        return out
+
+    def gp_info(self):
+        return lib().icoreg_roma_gp_info(self.m)
+
+    def close(self):
+        if self.m:
+            self.dev.api.roma_free(self.m)
+            lib().icoreg_struct_delete(self.m)
+            self.m = None
+        for pf in self.pfs:
+            self.dev.api.pth_close(pf)
+            lib().icoreg_struct_delete(pf)
+        self.pfs = []

@@ -71,3 +71,65 @@ extern "C" cl_mem icoreg_eloftr_buffer(const struct eloftr_model *m,
             return *(const cl_mem *)((const char *)m + tab[i].off);
     return NULL;
 }
+
+extern "C" struct roma_model *icoreg_roma_new(void)
+{
+    return (struct roma_model *)calloc(1, sizeof(struct roma_model));
+}
+
+extern "C" int icoreg_roma_result(const struct roma_model *m,
+                                  const float **flow, const float **cert,
+                                  const float **sd)
+{
+    *flow = m->flow;
+    *cert = m->cert;
+    *sd = m->sd;
+    return m->H * m->W;
+}
+
+extern "C" cl_mem icoreg_roma_buffer(const struct roma_model *m,
+                                     const char *name)
+{
+    static const struct {
+        const char *name;
+        size_t off;
+    } tab[] = {
+        {"fl0", offsetof(struct roma_model, fl[0])},
+        {"fl1", offsetof(struct roma_model, fl[1])},
+        {"ce0", offsetof(struct roma_model, ce[0])},
+        {"ce1", offsetof(struct roma_model, ce[1])},
+        {"cf0", offsetof(struct roma_model, cf[0])},
+        {"cf1", offsetof(struct roma_model, cf[1])},
+        {"t_out", offsetof(struct roma_model, t_out)},
+        {"t_x", offsetof(struct roma_model, t_x)},
+        {"t_n", offsetof(struct roma_model, t_n)},
+        {"g_y", offsetof(struct roma_model, g_y)},
+        {"g_f", offsetof(struct roma_model, g_f)},
+        {"g_kyy", offsetof(struct roma_model, g_kyy)},
+        {"cert16", offsetof(struct roma_model, cert16)},
+        {"img", offsetof(struct roma_model, img)},
+        {"P0", offsetof(struct roma_model, P[0])},
+        {"P1", offsetof(struct roma_model, P[1])},
+        {"P2", offsetof(struct roma_model, P[2])},
+        {"P3", offsetof(struct roma_model, P[3])},
+        {"P4", offsetof(struct roma_model, P[4])},
+    };
+
+    for (size_t i = 0; i < sizeof(tab) / sizeof(tab[0]); i++)
+        if (strcmp(tab[i].name, name) == 0)
+            return *(const cl_mem *)((const char *)m + tab[i].off);
+    return NULL;
+}
+
+extern "C" int icoreg_roma_gp_info(struct roma_model *m)
+{
+    int info = 0;
+
+    ocl_read(m->ocl, m->gp_info, 0, &info, sizeof(info));
+    return info;
+}
+
+extern "C" void icoreg_roma_set_imagenet(struct roma_model *m, int on)
+{
+    m->imagenet = on;
+}

@@ -180,3 +180,179 @@ def eloftr_weights_file(path, seed=BASE_SEED + CONFIG_ELOFTR):
     if not path.exists():
         save_safetensors(eloftr_weights_calibrated(seed), path)
     return path
+
+
+# ---- RoMa ---------------------------------------------------------------------
+
+CONFIG_ROMA = 2
+
+
+def tps_warp(rng, img, n_ctrl=4, disp=15.0):
+    """img (C, H, W) warped by a thin-plate spline through n_ctrl x n_ctrl
+    control points with displacements U(-disp, disp) px: output pixel p
+    samples img at p + d(p), bilinear, zeros outside. Returns the warped
+    image and d (2, H, W) (x, y)."""
+    from scipy.interpolate import RBFInterpolator
+    from scipy.ndimage import map_coordinates
+    C, H, W = img.shape
+    cy, cx = np.meshgrid(np.linspace(0, H - 1, n_ctrl), np.linspace(0, W - 1, n_ctrl),
+                         indexing="ij")
+    ctrl = np.stack([cx.ravel(), cy.ravel()], 1)
+    dd = rng.uniform(-disp, disp, ctrl.shape)
+    yy, xx = np.mgrid[0:H, 0:W].astype(np.float64)
+    pts = np.stack([xx.ravel(), yy.ravel()], 1)
+    d = RBFInterpolator(ctrl, dd, kernel="thin_plate_spline")(pts).T.reshape(2, H, W)
+    out = np.stack([map_coordinates(c.astype(np.float64), [yy + d[1], xx + d[0]], order=1,
+                                    mode="constant", cval=0.0) for c in img])
+    return out.astype(np.float32), d
+
+
+def roma_pair(H=560, W=560, seed=BASE_SEED + CONFIG_ROMA):
+    """RGB pair (3, H, W) in 0..1 for the RoMa configs: blurred noise A and
+    B = a TPS warp of A (16 control points, +-15 px)."""
+    rng = np.random.default_rng(seed)
+    a = smooth_noise(rng, (3, H, W))
+    b, d = tps_warp(rng, a)
+    return a, np.clip(b, 0.0, 1.0).astype(np.float32), d
+
+
+def _rn(rng, shape, std):
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+
+
+def _he32(rng, shape, gain=1.0):
+    fan_in = int(np.prod(shape[1:])) if len(shape) > 1 else shape[0]
+    return _rn(rng, shape, gain * np.sqrt(2.0 / fan_in))
+
+
+def _bias(rng, n, a=0.05):
+    return rng.uniform(-a, a, n).astype(np.float32)
+
+
+def _ln(rng, d, prefix, n):
+    d[f"{prefix}.weight"] = rng.uniform(0.8, 1.2, n).astype(np.float32)
+    d[f"{prefix}.bias"] = _bias(rng, n, 0.1)
+
+
+def _vit_block(rng, d, pre, D, qkv_bias, ls):
+    _ln(rng, d, f"{pre}.norm1", D)
+    d[f"{pre}.attn.qkv.weight"] = _he32(rng, (3 * D, D))
+    if qkv_bias:
+        d[f"{pre}.attn.qkv.bias"] = _bias(rng, 3 * D)
+    d[f"{pre}.attn.proj.weight"] = _he32(rng, (D, D))
+    d[f"{pre}.attn.proj.bias"] = _bias(rng, D)
+    _ln(rng, d, f"{pre}.norm2", D)
+    d[f"{pre}.mlp.fc1.weight"] = _he32(rng, (4 * D, D))
+    d[f"{pre}.mlp.fc1.bias"] = _bias(rng, 4 * D)
+    d[f"{pre}.mlp.fc2.weight"] = _he32(rng, (D, 4 * D))
+    d[f"{pre}.mlp.fc2.bias"] = _bias(rng, D)
+    if ls:
+        d[f"{pre}.ls1.gamma"] = rng.uniform(0.1, 0.5, D).astype(np.float32)
+        d[f"{pre}.ls2.gamma"] = rng.uniform(0.1, 0.5, D).astype(np.float32)
+
+
+def _vgg(rng, d, pre, nblk):
+    idx, cin = 0, 3
+    for blk, (nconv, co) in enumerate(zip((2, 2, 4, 4), (64, 128, 256, 512))):
+        if blk >= nblk:
+            break
+        for _ in range(nconv):
+            d[f"{pre}.{idx}.weight"] = _he32(rng, (co, cin, 3, 3))
+            d[f"{pre}.{idx}.bias"] = _bias(rng, co)
+            _bn(rng, d, f"{pre}.{idx + 1}", co)
+            cin = co
+            idx += 3
+        idx += 1
+
+
+def _refiner_blocks(rng, d, pre, cin, dw, bn, pw):
+    for b in range(9):
+        blk = f"{pre}.block1" if b == 0 else f"{pre}.hidden_blocks.{b - 1}"
+        d[f"{blk}.{dw}.weight"] = _he32(rng, (cin, 1, 5, 5))
+        d[f"{blk}.{dw}.bias"] = _bias(rng, cin)
+        _bn(rng, d, f"{blk}.{bn}", cin)
+        d[f"{blk}.{pw}.weight"] = _he32(rng, (cin, cin, 1, 1))
+        d[f"{blk}.{pw}.bias"] = _bias(rng, cin)
+
+
+ROMA_REFINERS = {16: (512, 128, 7), 8: (512, 64, 3), 4: (256, 32, 2), 2: (64, 16, 0), 1: (9, 6, 0)}
+ROMA_PROJ_IN = {16: 1024, 8: 512, 4: 256, 2: 128, 1: 64}
+ROMA2_REFINERS = {4: (256, 192, 79, 3), 2: (128, 48, 23, 1), 1: (64, 12, 8, 0)}
+
+
+def roma_weights(seed=BASE_SEED + CONFIG_ROMA):
+    """RoMa RegressionMatcher state dict (roma_outdoor names and shapes,
+    roma.c:213-436), seeded: He-normal weights, small random biases,
+    BatchNorm and LayerNorm parameters randomised around identity."""
+    rng = np.random.default_rng(seed + 1000)
+    d = {}
+    _vgg(rng, d, "encoder.cnn.layers", 4)
+    for s, (feat, _, _) in ROMA_REFINERS.items():
+        d[f"decoder.proj.{s}.0.weight"] = _he32(rng, (feat, ROMA_PROJ_IN[s], 1, 1))
+        d[f"decoder.proj.{s}.0.bias"] = _bias(rng, feat)
+        _bn(rng, d, f"decoder.proj.{s}.1", feat)
+    d["decoder.gps.16.pos_conv.weight"] = _rn(rng, (512, 2, 1, 1), 0.1)
+    d["decoder.gps.16.pos_conv.bias"] = _bias(rng, 512, 0.1)
+    for i in range(5):
+        _vit_block(rng, d, f"decoder.embedding_decoder.blocks.{i}", 1024, False, False)
+    d["decoder.embedding_decoder.to_out.weight"] = _he32(rng, (4097, 1024))
+    d["decoder.embedding_decoder.to_out.bias"] = _bias(rng, 4097)
+    for s, (feat, emb, rad) in ROMA_REFINERS.items():
+        cin = 2 * feat + emb + ((2 * rad + 1) ** 2 if rad else 0)
+        pre = f"decoder.conv_refiner.{s}"
+        _refiner_blocks(rng, d, pre, cin, "0", "1", "3")
+        d[f"{pre}.out_conv.weight"] = _he32(rng, (3, cin, 1, 1), 0.01)
+        d[f"{pre}.out_conv.bias"] = _bias(rng, 3)
+        d[f"{pre}.disp_emb.weight"] = _he32(rng, (emb, 2, 1, 1))
+        d[f"{pre}.disp_emb.bias"] = _bias(rng, emb)
+    return d
+
+
+def dino_weights(seed=BASE_SEED + CONFIG_ROMA):
+    """DINOv2 ViT-L/14 state dict (dinov2_vitl14_pretrain names and shapes,
+    roma.c:300-324), seeded."""
+    rng = np.random.default_rng(seed + 2000)
+    D = 1024
+    d = {"patch_embed.proj.weight": _he32(rng, (D, 3, 14, 14)),
+         "patch_embed.proj.bias": _bias(rng, D),
+         "cls_token": _rn(rng, (1, 1, D), 0.5),
+         "pos_embed": _rn(rng, (1, 37 * 37 + 1, D), 0.5)}
+    for i in range(24):
+        _vit_block(rng, d, f"blocks.{i}", D, True, True)
+    _ln(rng, d, "norm", D)
+    return d
+
+
+def roma2_weights(seed=BASE_SEED + CONFIG_ROMA):
+    """RoMa v2 refiners and their VGG19-BN (refiners.*, refiner_features.*
+    names and shapes, roma.c:452-544), seeded."""
+    rng = np.random.default_rng(seed + 3000)
+    d = {}
+    _vgg(rng, d, "refiner_features.layers", 3)
+    for s, (fin, feat, emb, rad) in ROMA2_REFINERS.items():
+        cin = 2 * feat + emb + ((2 * rad + 1) ** 2 if rad else 0)
+        pre = f"refiners.{s}"
+        d[f"{pre}.proj.weight"] = _he32(rng, (feat, fin))
+        d[f"{pre}.proj.bias"] = _bias(rng, feat)
+        _refiner_blocks(rng, d, pre, cin, "conv_depthwise", "norm", "conv_pointwise")
+        d[f"{pre}.disp_emb.weight"] = _he32(rng, (emb, 2, 1, 1))
+        d[f"{pre}.disp_emb.bias"] = _bias(rng, emb)
+        d[f"{pre}.warp_head.weight"] = _he32(rng, (2, cin, 1, 1), 0.01)
+        d[f"{pre}.warp_head.bias"] = _bias(rng, 2)
+        d[f"{pre}.confidence_head.weight"] = _he32(rng, (4, cin, 1, 1), 0.1)
+        d[f"{pre}.confidence_head.bias"] = _bias(rng, 4)
+    return d
+
+
+def roma_weights_files(folder, seed=BASE_SEED + CONFIG_ROMA):
+    """Write (once) and return the paths of the RoMa, DINOv2 and RoMa v2
+    weight files."""
+    folder = Path(folder)
+    out = []
+    for name, fn in (("roma_random", roma_weights), ("dinov2_random", dino_weights),
+                     ("romav2_random", roma2_weights)):
+        p = folder / f"{name}_{seed}.safetensors"
+        if not p.exists():
+            save_safetensors(fn(seed), p)
+        out.append(p)
+    return out

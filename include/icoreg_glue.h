@@ -11,6 +11,7 @@
 
 #include "eloftr.h"
 #include "pth_loader.h"
+#include "roma.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -35,6 +36,24 @@ void icoreg_eloftr_set_pos_scale(struct eloftr_model *m, float s);
  * n), "fine0", "fine1" (64 x H x W), "f1_0", "f2_0", ... Returns NULL for
  * an unknown name. */
 cl_mem icoreg_eloftr_buffer(const struct eloftr_model *m, const char *name);
+
+struct roma_model *icoreg_roma_new(void);
+
+/* Results of the last roma_match: H x W, host arrays owned by the model
+ * (sd NULL without v2). */
+int icoreg_roma_result(const struct roma_model *m, const float **flow,
+                       const float **cert, const float **sd);
+
+/* A named device buffer of the model: "fl0", "fl1", "ce0", "ce1", "cf0",
+ * "cf1", "t_out", "g_y", "g_f", "t_x", "cert16", "P0" .. "P4"; NULL for an
+ * unknown name. */
+cl_mem icoreg_roma_buffer(const struct roma_model *m, const char *name);
+
+/* 1 + the first failing GP pivot of the last solve, 0 if it succeeded
+ * (waits for the stream). */
+int icoreg_roma_gp_info(struct roma_model *m);
+
+void icoreg_roma_set_imagenet(struct roma_model *m, int on);
 
 #ifdef __cplusplus
 }

@@ -104,6 +104,18 @@ void roma2_update(struct ops *o, cl_mem flow, cl_mem conf, cl_mem d, int n,
 void roma_dwconv5(struct ops *o, cl_mem in, int C, int H, int W, cl_mem w,
                   cl_mem bias, cl_mem out);
 
+/* Extension with no counterpart among the reference's kernels: the
+ * Gaussian-process solve that roma.c:770-836 runs on the host in double
+ * precision, on the device in double precision. F (n x d floats) is
+ * replaced by (K + noise I)^-1 F, K (n x n floats, symmetric, its lower
+ * triangle read). work holds roma_gp_work_bytes(n, d) bytes; info (one
+ * int, cleared by the call) gets 1 + the first column whose pivot is
+ * not positive, the reference's "not positive definite" failure, for
+ * the caller to check once the stream has run. */
+size_t roma_gp_work_bytes(int n, int d);
+void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise, cl_mem F,
+                   int d, cl_mem work, cl_mem info);
+
 #ifdef __cplusplus
 }
 #endif

@@ -79,6 +79,20 @@ void orc_gemm(int M, int N, int K, const float *A, long aoff, int lda,
         const float *r = R ? R + roff + b0 * sc0 + b1 * sc1 + m * ldc : NULL;
         int n, k;
 
+        /* Without transb the row of C is accumulated k-outer over
+         * contiguous rows of B: the same fmaf sequence per output (k
+         * ascending) as the dot-product loop, so the same values. */
+        float *row = NULL;
+
+        if (!transb) {
+            row = calloc(N > 0 ? N : 1, sizeof(float));
+            for (k = 0; k < K; k++) {
+                const float ak = a[k], *bk = bb + (long)k * ldb;
+
+                for (n = 0; n < N; n++)
+                    row[n] = fmaf(ak, bk[n], row[n]);
+            }
+        }
         for (n = 0; n < N; n++) {
             float acc = 0.0f, v;
 
@@ -86,8 +100,7 @@ void orc_gemm(int M, int N, int K, const float *A, long aoff, int lda,
                 for (k = 0; k < K; k++)
                     acc = fmaf(a[k], bb[(long)n * ldb + k], acc);
             else
-                for (k = 0; k < K; k++)
-                    acc = fmaf(a[k], bb[(long)k * ldb + n], acc);
+                acc = row[n];
             v = alpha * acc;
             if (bias)
                 v += bias[biasrow ? m : n];
@@ -96,6 +109,7 @@ void orc_gemm(int M, int N, int K, const float *A, long aoff, int lda,
                 v += r[n];
             c[n] = v;
         }
+        free(row);
     }
 }
 

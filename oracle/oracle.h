@@ -167,6 +167,37 @@ int orc_eloftr_forward(const struct orc_named *weights, int nweights,
                        const float *grey0, const float *grey1, int H, int W,
                        float pos_scale, struct orc_eloftr_out *out);
 
+/* ---- RoMa network (roma.c) ------------------------------------------------ */
+
+/* Host input preparation, roma.c:1106-1186: (3, H, W) resampled to (3, h,
+ * w) with Pillow's antialiased bicubic filter, ImageNet-normalised when
+ * imagenet is set. */
+void orc_roma_prepare(const float *in, int H, int W, float *out, int h, int w,
+                      int imagenet);
+
+/* Outputs of orc_roma_forward; NULL pointers are skipped, flow (2 H W)
+ * and cert (H W) are required. scale_flow[p][s]: the warp after the
+ * refiner of scale index s (16, 8, 4, 2, 1) in pass p (0: coarse). */
+struct orc_roma_out {
+    float *dino[2];          /* 1024 x n16 normed patch tokens */
+    float *gp;               /* n16 x 512 posterior mean */
+    float *logits;           /* n16 x 4097 */
+    float *cls_flow, *cls_cert;
+    float *scale_flow[2][5];
+    float *flow, *cert, *sd; /* sd (v2 only) may be NULL */
+};
+
+/* RoMa's match (roma.c:1351-1435) on (3, H, W) images in 0..1 with a
+ * coarse pass of side coarse (a multiple of 56); v2 weights (nv2 > 0)
+ * switch to RoMa v2's refiners. cls_flow_in (2 n16, or NULL) replaces
+ * the decoder's coarse warp before the refiners. Returns 0, or 1 + the
+ * column at which the GP kernel was not positive definite. */
+int orc_roma_forward(const struct orc_named *weights, int nweights,
+                     const struct orc_named *dino, int ndino,
+                     const struct orc_named *v2, int nv2, const float *imgA,
+                     const float *imgB, int H, int W, int coarse, int imagenet,
+                     const float *cls_flow_in, struct orc_roma_out *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,20 @@ class EloftrOut(C.Structure):
 SIGS["orc_eloftr_forward"] = (_I, [C.POINTER(Named), _I, _FP, _FP, _I, _I, _F,
                                    C.POINTER(EloftrOut)])
 
+class RomaOut(C.Structure):
+    _fields_ = [
+        ("dino", _FP * 2), ("gp", _FP), ("logits", _FP),
+        ("cls_flow", _FP), ("cls_cert", _FP),
+        ("scale_flow", (_FP * 5) * 2),
+        ("flow", _FP), ("cert", _FP), ("sd", _FP),
+    ]
+
+
+SIGS["orc_roma_forward"] = (_I, [C.POINTER(Named), _I, C.POINTER(Named), _I,
+                                 C.POINTER(Named), _I, _FP, _FP, _I, _I, _I, _I, _FP,
+                                 C.POINTER(RomaOut)])
+SIGS["orc_roma_prepare"] = (None, [_FP, _I, _I, _FP, _I, _I, _I])
+
 _lib = None
 
 
@@ -116,6 +130,53 @@ def eloftr_forward(weights, g0, g1, pos_scale=1.0, backbone=False, coarse=False,
     nm = l.orc_eloftr_forward(arr, len(weights), fp(g0), fp(g1), H, W, pos_scale,
                               C.byref(st))
     out["nm"] = nm
+    return out
+
+
+ROMA_SCALES = (16, 8, 4, 2, 1)
+
+
+def roma_forward(wmain, wdino, wv2, imgA, imgB, coarse, imagenet=1, cls_flow_in=None):
+    """Run the oracle's RoMa match on (3, H, W) images; dict of outputs:
+    flow, cert, (sd), dino (2 x (1024, n16)), gp, logits, cls_flow,
+    cls_cert, scale_flow[(p, s)] and the GP status info."""
+    import numpy as np
+    l = oracle()
+    _, H, W = imgA.shape
+    c16 = coarse // 14
+    n16 = c16 * c16
+    a1, k1 = named_array(wmain)
+    a2, k2 = named_array(wdino)
+    a3, k3 = named_array(wv2) if wv2 else (None, [])
+    out = {"flow": np.zeros((2, H, W), np.float32), "cert": np.zeros((H, W), np.float32),
+           "dino": [np.zeros((1024, n16), np.float32) for _ in range(2)],
+           "gp": np.zeros((n16, 512), np.float32),
+           "logits": np.zeros((n16, 4097), np.float32),
+           "cls_flow": np.zeros((2, n16), np.float32), "cls_cert": np.zeros(n16, np.float32),
+           "scale_flow": {}}
+    st = RomaOut()
+    for k in ("flow", "cert", "gp", "logits", "cls_flow", "cls_cert"):
+        setattr(st, k, fp(out[k]))
+    st.dino[0], st.dino[1] = fp(out["dino"][0]), fp(out["dino"][1])
+    if wv2:
+        out["sd"] = np.zeros((H, W), np.float32)
+        st.sd = fp(out["sd"])
+    nsc = 2 if wv2 else 5
+    for p in range(2):
+        for si, s in enumerate(ROMA_SCALES):
+            if (p == 0 and si >= nsc) or (p == 1 and (wv2 or si == 0)):
+                continue
+            hs = (c16 if si == 0 else coarse // s) if p == 0 else H // s
+            ws = (c16 if si == 0 else coarse // s) if p == 0 else W // s
+            buf = np.zeros((2, hs, ws), np.float32)
+            out["scale_flow"][(p, s)] = buf
+            st.scale_flow[p][si] = fp(buf)
+    A = np.ascontiguousarray(imgA, np.float32)
+    B = np.ascontiguousarray(imgB, np.float32)
+    cf = None if cls_flow_in is None else np.ascontiguousarray(cls_flow_in, np.float32)
+    out["info"] = l.orc_roma_forward(a1, len(wmain), a2, len(wdino), a3,
+                                     len(wv2) if wv2 else 0, fp(A), fp(B), H, W, coarse,
+                                     imagenet, fp(cf), C.byref(st))
     return out
 
 

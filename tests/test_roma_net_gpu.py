@@ -1,0 +1,168 @@
+# SPDX-License-Identifier: Unlicense
+"""GPU: the RoMa network on the HIP library against the oracle.
+
+Tolerances: features and contractions <= 1e-3 of
+the largest reference magnitude; warps <= 1e-3 (normalised units); the
+anchor argmax of the coarse warp bit-exact (same cell) wherever the
+oracle's relative top-2 logit margin exceeds 1e-3. Where a near-tie
+decides the argmax differently, the oracle's refiners are re-run from
+the HIP coarse warp, so that the refiners are still compared on the
+same input.
+
+The Gaussian-process solve (device, double precision) is checked against
+numpy's float64 Cholesky solve, and at the full 560 x 560 size through
+its residual."""
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle_lib import roma_forward
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parents[1]
+sys.path.insert(0, str(ROOT / "i.coregistration.opencl_amd"))
+import synth  # noqa: E402
+
+COARSE, TILE = 112, 64
+
+
+def rel(a, b):
+    a, b = np.asarray(a, np.float64).ravel(), np.asarray(b, np.float64).ravel()
+    return np.abs(a - b).max() / max(np.abs(b).max(), 1e-30)
+
+
+def cos_kernel(rng, n, d=64):
+    x = rng.standard_normal((n, d))
+    x /= np.linalg.norm(x, axis=1, keepdims=True)
+    return np.exp((x @ x.T - 1) / 0.2).astype(np.float32)
+
+
+@pytest.mark.parametrize("n,d", [(1600, 512), (100, 512), (65, 7)])
+def test_gp_solve(dev, ic, n, d):
+    print(f"[roma] gp_solve n={n} d={d}", flush=True)
+    rng = np.random.default_rng(n)
+    K = cos_kernel(rng, n)
+    F = rng.standard_normal((n, d)).astype(np.float32)
+    ref = np.linalg.solve(K.astype(np.float64) + 0.1 * np.eye(n), F.astype(np.float64))
+    bK, bF = dev.upload(K), dev.upload(F)
+    work = dev.alloc(int(dev.api.roma_gp_work_bytes(n, d)))
+    info = dev.upload(np.full(1, 7, np.int32))
+    dev.api.roma_gp_solve(dev.po, bK.mem, n, 0.1, bF.mem, d, work.mem, info.mem)
+    got = dev.read(bF).reshape(n, d)
+    assert dev.read(info, 1, np.int32)[0] == 0
+    assert rel(got, ref) < 1e-5
+
+
+def test_gp_solve_reports_indefinite(dev, ic):
+    """A kernel that is not positive definite (here -I, so the first pivot
+    is -0.9) sets info to the failing column + 1; the factor is NaN from
+    there, no fault."""
+    n, d = 70, 3
+    K = -np.eye(n, dtype=np.float32)
+    bK, bF = dev.upload(K), dev.upload(np.ones((n, d), np.float32))
+    work = dev.alloc(int(dev.api.roma_gp_work_bytes(n, d)))
+    info = dev.zeros(1, np.int32)
+    dev.api.roma_gp_solve(dev.po, bK.mem, n, 0.1, bF.mem, d, work.mem, info.mem)
+    assert dev.read(info, 1, np.int32)[0] == 1
+
+
+@pytest.fixture(scope="module")
+def weights(tmp_path_factory):
+    d = tmp_path_factory.mktemp("roma_w")
+    files = synth.roma_weights_files(d)
+    return files, (synth.roma_weights(), synth.dino_weights(), synth.roma2_weights())
+
+
+def _margins(logits):
+    s = np.sort(logits[:, :4096], 1)
+    return (s[:, -1] - s[:, -2]) / np.maximum(np.abs(s[:, -1]), 1e-30)
+
+
+def _read_dump(folder, what, tile=1):
+    return np.fromfile(Path(folder) / f"tile{tile:03d}_roma_{what}.f32", np.float32)
+
+
+@pytest.mark.parametrize("v2", [False, True])
+def test_roma_match_vs_oracle(dev, ic, weights, tmp_path, v2):
+    print(f"[roma] match v2={v2} coarse={COARSE} tile={TILE}", flush=True)
+    (fm, fd, f2), (wm, wd, w2) = weights
+    a, b, _ = synth.roma_pair(TILE, TILE)
+    net = ic.Roma(dev, fm, fd, TILE, TILE, v2_path=f2 if v2 else None, coarse=COARSE)
+    try:
+        got = net.match(a, b, dump=str(tmp_path), tile=1)
+    finally:
+        net.close()
+    o = roma_forward(wm, wd, w2 if v2 else None, a, b, COARSE)
+    assert o["info"] == 0
+    n16 = (COARSE // 14) ** 2
+    for k in range(2):
+        assert rel(_read_dump(tmp_path, f"dino_{k}"), o["dino"][k]) < 1e-3
+    assert rel(_read_dump(tmp_path, "gp"), o["gp"]) < 1e-3
+    cls_flow = _read_dump(tmp_path, "cls_flow").reshape(2, n16)
+    sure = _margins(o["logits"]) > 1e-3
+    assert sure.mean() > 0.9
+    assert np.abs(cls_flow[:, sure] - o["cls_flow"][:, sure]).max() < 1e-4
+    assert rel(_read_dump(tmp_path, "cls_cert"), o["cls_cert"]) < 1e-3
+    if np.abs(cls_flow - o["cls_flow"]).max() > 1e-4:
+        print("[roma] near-tie anchors differ; oracle refiners re-run from the HIP warp",
+              flush=True)
+        o = roma_forward(wm, wd, w2 if v2 else None, a, b, COARSE, cls_flow_in=cls_flow)
+    for (p, s), f in o["scale_flow"].items():
+        g = _read_dump(tmp_path, f"p{p}_s{s}_flow").reshape(f.shape)
+        assert np.abs(g - f).max() < 1e-3, (p, s)
+    assert np.abs(got["flow"] - o["flow"]).max() < 1e-3
+    assert np.abs(got["cert"] - o["cert"]).max() < 1e-3
+    if v2:
+        both = np.isfinite(got["sd"]) & np.isfinite(o["sd"])
+        assert both.mean() > 0.99
+        assert rel(got["sd"][both], o["sd"][both]) < 1e-3
+
+
+def test_roma_coarse_560_properties(dev, ic, weights, tmp_path):
+    """The benchmark's unit at full size (DINOv2 x 2 on 560 x 560, GP on
+    1600 tokens, decoder): the GP solve's residual |(K + 0.1 I) X - B| /
+    |B| in float64 from the device's own K, X and basis, a finite warp
+    inside -1..1 on the 40 x 40 grid, and the same warp as the coarse
+    stage of roma_match on the same inputs."""
+    print("[roma] coarse 560 properties", flush=True)
+    (fm, fd, _), _ = weights
+    a, b, _ = synth.roma_pair(560, 560)
+    net = ic.Roma(dev, fm, fd, 560, 560)
+    try:
+        mean = np.array([0.485, 0.456, 0.406], np.float32)[:, None, None]
+        std = np.array([0.229, 0.224, 0.225], np.float32)[:, None, None]
+        pair = dev.upload(np.stack([(a - mean) / std, (b - mean) / std]))
+        net.coarse_device(pair)
+        dev.finish()
+        assert net.gp_info() == 0
+        n = 1600
+        K = net.buffer("g_kyy", n * n).reshape(n, n).astype(np.float64)
+        X = net.buffer("g_f", n * 512).reshape(n, 512).astype(np.float64)
+        flow = net.buffer("fl0", 2 * n).reshape(2, n)
+        cert = net.buffer("ce0", n)
+        assert np.isfinite(flow).all() and np.isfinite(cert).all()
+        assert np.abs(flow).max() <= 1.0
+        # The basis is what the solve started from: recompute it as the
+        # library does (roma.c:326-350) from the weights file.
+        w = synth.roma_weights()
+        c = 40
+        i = np.arange(n)
+        x = (-1.0 + 1.0 / c + (i % c) * (2.0 - 2.0 / c) / (c - 1)).astype(np.float32)
+        y = (-1.0 + 1.0 / c + (i // c) * (2.0 - 2.0 / c) / (c - 1)).astype(np.float32)
+        pw = w["decoder.gps.16.pos_conv.weight"][:, :, 0, 0]
+        v = (pw[:, 0][None] * x[:, None] + pw[:, 1][None] * y[:, None]
+             + w["decoder.gps.16.pos_conv.bias"][None]).astype(np.float32)
+        basis = np.cos(np.float32(8.0 * np.pi) * v).astype(np.float64)
+        res = (K + 0.1 * np.eye(n)) @ X - basis
+        assert np.abs(res).max() / np.abs(basis).max() < 1e-4
+        got = net.match(a, b, dump=str(tmp_path), tile=1)
+        assert np.isfinite(got["flow"]).all()
+        assert ((got["cert"] >= 0) & (got["cert"] <= 1)).all()
+        cls_full = _read_dump(tmp_path, "cls_flow").reshape(2, n)
+        assert np.abs(cls_full - flow).max() < 1e-5
+    finally:
+        net.close()

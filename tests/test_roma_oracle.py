@@ -135,3 +135,70 @@ def test_dwconv5(orc):
     out = np.zeros((C, H, W), np.float32)
     orc.orc_roma_dwconv5(fp(x), C, H, W, fp(w), fp(b), fp(out))
     assert rel(out, R.dwconv5_relu(R.t64(x), R.t64(w), R.t64(b)).numpy()) < TOL
+
+
+# ---- the network ---------------------------------------------------------------------
+
+import sys  # noqa: E402
+from pathlib import Path  # noqa: E402
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "i.coregistration.opencl_amd"))
+import synth  # noqa: E402
+from oracle_lib import roma_forward  # noqa: E402
+
+COARSE, TILE = 112, 64
+
+
+@pytest.mark.parametrize("H,W,h,w", [(112, 112, 56, 56), (64, 96, 112, 112), (90, 70, 56, 28)])
+def test_prepare_matches_antialiased_bicubic(orc, H, W, h, w):
+    """Host resampling (Pillow's antialiased bicubic, roma.c:1106-1186)
+    against torch's antialias=True bicubic, both directions, then the
+    ImageNet normalisation."""
+    rng = np.random.default_rng(H + w)
+    img = rng.uniform(0, 1, (3, H, W)).astype(np.float32)
+    out = np.zeros((3, h, w), np.float32)
+    orc.orc_roma_prepare(fp(img), H, W, fp(out), h, w, 1)
+    ref = R.prepare(img, h, w).numpy()
+    assert np.abs(out - ref).max() < 2e-5
+
+
+@pytest.fixture(scope="module")
+def roma_weights():
+    return synth.roma_weights(), synth.dino_weights(), synth.roma2_weights()
+
+
+def _margins(logits):
+    s = np.sort(logits[:, :4096], 1)
+    return (s[:, -1] - s[:, -2]) / np.maximum(np.abs(s[:, -1]), 1e-30)
+
+
+@pytest.mark.parametrize("v2", [False, True])
+def test_roma_forward_matches_float64_restatement(roma_weights, v2):
+    """The oracle's whole RoMa match (float32, the reference's schedule)
+    against a float64 torch statement built from library routines:
+    transformers' Dinov2Layer for the 24 DINOv2 blocks and the 5 decoder
+    blocks, torch.linalg.cholesky for the GP, F.grid_sample /
+    local_correlation / depthwise F.conv2d + F.batch_norm for the
+    refiners, antialiased bicubic resizes. Stage by stage; the refiners
+    start from the oracle's coarse warp so that an anchor argmax decided
+    by a near-tie cannot hide a refiner difference."""
+    wm, wd, w2 = roma_weights
+    a, b, _ = synth.roma_pair(TILE, TILE)
+    o = roma_forward(wm, wd, w2 if v2 else None, a, b, COARSE)
+    assert o["info"] == 0
+    r = R.roma_match(wm, wd, w2 if v2 else None, a, b, COARSE, cls_flow_in=o["cls_flow"])
+    for k in range(2):
+        assert rel(o["dino"][k], r["dino"][k]) < 1e-3
+    assert rel(o["gp"], r["gp"]) < 1e-3
+    assert rel(o["logits"], r["logits"]) < 1e-3
+    sure = _margins(o["logits"]) > 1e-3
+    assert sure.mean() > 0.9
+    assert np.abs(o["cls_flow"][:, sure] - r["cls_flow"][:, sure]).max() < 1e-4
+    for key, f in o["scale_flow"].items():
+        assert np.abs(f - r["scale_flow"][key]).max() < 1e-3, key
+    assert np.abs(o["flow"] - r["flow"]).max() < 1e-3
+    assert np.abs(o["cert"] - r["cert"]).max() < 1e-3
+    if v2:
+        both = np.isfinite(o["sd"]) & np.isfinite(r["sd"])
+        assert both.mean() > 0.99
+        assert rel(o["sd"][both], r["sd"][both]) < 1e-3
