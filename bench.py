@@ -1,12 +1,17 @@
 # SPDX-License-Identifier: Unlicense
 """Benchmark of the MI355X matcher tensor path (BASELINE.json metric).
 
-One step = one Efficient LoFTR 640 x 640 grey tile pair through the whole
-device stage of the reference's eloftr_match (eloftr.c:654-681):
+The metric names two workloads. `value` is the first: one step = one
+Efficient LoFTR 640 x 640 grey tile pair through the whole device stage of
+the reference's eloftr_match (eloftr.c:654-681):
 backbone x 2, 4 x (self, self, cross, cross) aggregated attention, coarse
 dual-softmax matching with the host mutual selection, FPN fusion x 2 and
 two-stage fine matching; seeded synthetic pair and seeded random-init
 weights (synth.py), both images resident in HBM before timing.
+
+The second, RoMa's coarse forward on a 560 x 560 RGB pair (DINOv2 ViT-L/14
+x 2, Gaussian process, coordinate decoder; roma.c:715-919), is reported
+under "roma560" with its own throughput and GEMM roofline.
 
 Prints one JSON line (the driver's contract) with the per-kernel roofline
 of the dominant kernel (the 3 x 3 convolution on the fp32 matrix cores:
@@ -15,6 +20,7 @@ baseline (the oracle, a C port of the reference kernels, on a bounded
 sample timed on this host).
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+                    [--no-roma] [--roma-steps 10] [--copy-calib MiB]
 """
 
 import argparse
@@ -78,6 +84,83 @@ def eloftr_flops(H, W, nm=0):
             "total": conv + gemm + attn + other}
 
 
+def roma_coarse_flops(coarse=560):
+    """Algorithmic FLOPs of RoMa's coarse forward on one pair (DINOv2 x 2,
+    GP, decoder), by kernel family; the GP's double-precision Cholesky
+    (n^3 / 3) and solves (2 n^2 d) are reported apart as fp64."""
+    c16 = coarse // 14
+    n, nt, D = c16 * c16, c16 * c16 + 1, 1024
+    gemm = attn = 0.0
+    gemm += 2 * 2.0 * D * n * 3 * 14 * 14                        # patch embedding
+    blk = 2.0 * nt * D * (3 * D + D + 4 * D + 4 * D)
+    gemm += 2 * 24 * blk
+    attn += 2 * 24 * 4.0 * 16 * nt * nt * 64
+    gemm += 2 * 2.0 * n * 512 * D                                 # proj to 512
+    gemm += 3 * 2.0 * n * n * 512                                 # K_yy, K_xy, K_xy X
+    gemm += 5 * 2.0 * n * D * (3 * D + D + 4 * D + 4 * D)
+    attn += 5 * 4.0 * 8 * n * n * 128
+    gemm += 2.0 * n * 4097 * D                                    # to_out
+    fp64 = n ** 3 / 3.0 + 2.0 * n * n * 512
+    return {"gemm": gemm, "attention": attn, "fp64": fp64, "total": gemm + attn}
+
+
+def bench_roma(ic, dev, synth, wdir, steps, warmup, profile_steps):
+    """RoMa coarse forward (DINOv2 ViT-L/14 x 2 at 560 x 560, GP on 1600
+    tokens, coordinate decoder, cls_to_flow) of one pair already in HBM."""
+    fm, fd, _ = synth.roma_weights_files(wdir)
+    a, b, _ = synth.roma_pair(560, 560)
+    net = ic.Roma(dev, fm, fd, 560, 560)
+    mean = np.array([0.485, 0.456, 0.406], np.float32)[:, None, None]
+    std = np.array([0.229, 0.224, 0.225], np.float32)[:, None, None]
+    pair = dev.upload(np.stack([(a - mean) / std, (b - mean) / std]))
+    for _ in range(warmup):
+        net.coarse_device(pair)
+    dev.finish()
+    dev.reset_events()
+    t0 = time.perf_counter()
+    e0 = dev.event()
+    for _ in range(steps):
+        net.coarse_device(pair)
+    e1 = dev.event()
+    dev.finish()
+    wall = time.perf_counter() - t0
+    ms = max(dev.elapsed_ms(e0, e1), wall * 1e3) / steps
+    if net.gp_info() != 0:
+        raise RuntimeError("RoMa GP kernel not positive definite")
+    dev.profile_reset()
+    dev.set_profile(2)
+    for _ in range(profile_steps):
+        net.coarse_device(pair)
+    dev.finish()
+    table = dev.profile_table()
+    dev.set_profile(0)
+    net.close()
+    fl = roma_coarse_flops()
+    ps = profile_steps
+    gemm_ms = table.get("gemm", (0.0, 0))[0] / ps
+    attn_ms = table.get("attention", (0.0, 0))[0] / ps
+    kernels = {k: {"ms_per_step": round(v[0] / ps, 4), "launches_per_step": v[1] / ps}
+               for k, v in sorted(table.items(), key=lambda kv: -kv[1][0])}
+    print("[bench] RoMa per-kernel ms per pair: " + json.dumps(kernels), file=sys.stderr,
+          flush=True)
+    g_tf = fl["gemm"] / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
+    a_tf = fl["attention"] / (attn_ms * 1e-3) / 1e12 if attn_ms > 0 else 0.0
+    return {
+        "workload": "RoMa coarse forward, 560x560 RGB pair: DINOv2 ViT-L/14 x 2 (1601 tokens), "
+                    "GP on 1600 tokens (device fp64 solve), coordinate decoder, cls_to_flow",
+        "pairs_per_s": round(1000.0 / ms, 3), "ms_per_pair": round(ms, 4),
+        "gflop_per_pair": round(fl["total"] / 1e9, 1),
+        "pipeline_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
+        "roofline": {"kernel": "gemm_mfma (fp32 MFMA GEMM: qkv, proj, MLP, GP, to_out)",
+                     "bound": "mfma", "achieved": round(g_tf, 2), "peak": PEAK_FP32_MFMA,
+                     "unit": "TFLOP/s", "frac": round(g_tf / PEAK_FP32_MFMA, 4),
+                     "gflop_per_step": round(fl["gemm"] / 1e9, 1)},
+        "attention": {"achieved": round(a_tf, 2), "unit": "TFLOP/s",
+                      "frac": round(a_tf / PEAK_FP32_MFMA, 4),
+                      "gflop_per_step": round(fl["attention"] / 1e9, 1)},
+    }
+
+
 def cpu_baseline(weights, size=256):
     """The oracle (C port of the reference kernels and schedule, OpenMP)
     on one size x size pair, scaled to a 640 x 640 pair by algorithmic
@@ -106,6 +189,11 @@ def main():
     ap.add_argument("--size", type=int, default=640)
     ap.add_argument("--profile-steps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-roma", action="store_true")
+    ap.add_argument("--roma-steps", type=int, default=10)
+    ap.add_argument("--copy-calib", type=int, default=0,
+                    help="MiB: one device-to-device copy of this size, the known-size "
+                         "reference for HBM byte counters under rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus}: this build runs on one GPU only (tiles are "
@@ -142,6 +230,17 @@ def main():
     res = net.result()
     nm = int(res["nm"])
 
+    if args.copy_calib:
+        nb = args.copy_calib << 20
+        src, dst = dev.alloc(nb, "calibration"), dev.alloc(nb, "calibration")
+        dev.api.ocl_fill(dev.pb, src.mem, 0, nb // 4, 1.0)
+        dev.finish()
+        dev.api.ocl_copy(dev.pb, src.mem, 0, dst.mem, 0, nb)
+        dev.finish()
+        print(f"[bench] calibration copy of {args.copy_calib} MiB done", file=sys.stderr, flush=True)
+        src.release()
+        dst.release()
+
     # Per-kernel times over a few more steps (event pairs, no sync).
     dev.profile_reset()
     dev.set_profile(2)
@@ -177,6 +276,11 @@ def main():
     eb = dev.event()
     fine_nmax_ms = dev.elapsed_ms(ea, eb) / 5
 
+    net.close()
+    roma = None
+    if not args.no_roma:
+        roma = bench_roma(ic, dev, synth, wdir, args.roma_steps, 2, args.profile_steps)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(synth.eloftr_weights_calibrated())
@@ -208,9 +312,9 @@ def main():
         "pipeline_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
         "fine_ms_at_max_matches": round(fine_nmax_ms, 4),
         "cpu_baseline": cpu,
+        "roma560": roma,
     }
     print(json.dumps(line), flush=True)
-    net.close()
     dev.close()
 
 
