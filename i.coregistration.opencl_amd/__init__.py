@@ -164,6 +164,13 @@ SIGNATURES = {
     "roma_dwconv5": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem]),
     "roma_gp_work_bytes": (C.c_size_t, [_I, _I]),
     "roma_gp_solve": (None, [_O, Mem, _I, _F, Mem, _I, Mem, Mem]),
+    "disk_nms5x5": (None, [_O, Mem, _L, _I, _I, _I, _F, Mem]),
+    "disk_gather_desc": (None, [_O, Mem, _I, _I, _I, Mem, _I, Mem]),
+    # DISK model (include/disk.h)
+    "disk_load": (None, [_P, _O, _P]),
+    "disk_alloc": (None, [_P, _I, _I, _I]),
+    "disk_detect": (_I, [_P, _P, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P]),
+    "disk_free": (None, [_P]),
     # RoMa model (include/roma.h)
     "roma_load": (None, [_P, _O, _P, _P]),
     "roma_load_v2": (None, [_P, _P]),
@@ -183,6 +190,8 @@ SIGNATURES = {
     "icoreg_eloftr_set_pos_scale": (None, [_P, _F]),
     "icoreg_eloftr_buffer": (Mem, [_P, _S]),
     "icoreg_roma_new": (_P, []),
+    "icoreg_disk_new": (_P, []),
+    "icoreg_disk_buffer": (Mem, [_P, _S]),
     "icoreg_roma_result": (_I, [_P, C.POINTER(C.POINTER(C.c_float)), C.POINTER(C.POINTER(C.c_float)),
                                 C.POINTER(C.POINTER(C.c_float))]),
     "icoreg_roma_buffer": (Mem, [_P, _S]),
@@ -199,7 +208,7 @@ _NO_CHECK = {"icoreg_set_fatal_mode", "icoreg_last_error", "icoreg_clear_error",
              "icoreg_eloftr_result", "icoreg_eloftr_coarse_stats",
              "icoreg_eloftr_set_pos_scale", "icoreg_eloftr_buffer", "roma_gp_work_bytes",
              "icoreg_roma_new", "icoreg_roma_result", "icoreg_roma_buffer",
-             "icoreg_roma_set_imagenet"}
+             "icoreg_roma_set_imagenet", "icoreg_disk_new", "icoreg_disk_buffer"}
 
 _lib = None
 
@@ -487,3 +496,51 @@ class Roma:
             self.dev.api.pth_close(pf)
             lib().icoreg_struct_delete(pf)
         self.pfs = []
+
+
+class Disk:
+    """DISK on the device: disk_load / disk_alloc / disk_detect of the
+    C-ABI, weights from a safetensors file."""
+
+    def __init__(self, dev, weights_path, H, W, nmax=2048):
+        self.dev = dev
+        a = dev.api
+        self.pf = lib().icoreg_pth_new()
+        a.pth_open(self.pf, str(weights_path).encode())
+        self.m = lib().icoreg_disk_new()
+        a.disk_load(self.m, dev.po, self.pf)
+        a.disk_alloc(self.m, H, W, nmax)
+        self.H, self.W, self.nmax = H, W, nmax
+
+    def detect(self, img, h=None, w=None, n=2048, thresh=0.0, valid=None):
+        _, H, W = img.shape
+        h = H if h is None else h
+        w = W if w is None else w
+        img = np.ascontiguousarray(img, np.float32)
+        n = min(n, self.nmax)
+        xy = np.zeros(2 * n, np.int32)
+        score = np.zeros(n, np.float32)
+        desc = np.zeros((n, 128), np.float32)
+        v = None if valid is None else np.ascontiguousarray(valid, np.uint8)
+        nk = self.dev.api.disk_detect(self.m, img.ctypes.data, H, W, h, w, n, thresh,
+                                      v.ctypes.data if v is not None else None,
+                                      xy.ctypes.data, score.ctypes.data, desc.ctypes.data)
+        return {"n": nk, "xy": xy[:2 * nk].reshape(-1, 2), "score": score[:nk],
+                "desc": desc[:nk]}
+
+    def buffer(self, name, count, dtype=np.float32, off=0):
+        mem = lib().icoreg_disk_buffer(self.m, name.encode())
+        out = np.empty(count, dtype)
+        self.dev.api.ocl_read(self.dev.pb, mem, off * out.itemsize, out.ctypes.data,
+                              out.nbytes)
+        return out
+
+    def close(self):
+        if self.m:
+            self.dev.api.disk_free(self.m)
+            lib().icoreg_struct_delete(self.m)
+            self.m = None
+        if self.pf:
+            self.dev.api.pth_close(self.pf)
+            lib().icoreg_struct_delete(self.pf)
+            self.pf = None

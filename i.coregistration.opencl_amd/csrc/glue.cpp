@@ -133,3 +133,18 @@ extern "C" void icoreg_roma_set_imagenet(struct roma_model *m, int on)
 {
     m->imagenet = on;
 }
+
+extern "C" struct disk_model *icoreg_disk_new(void)
+{
+    return (struct disk_model *)calloc(1, sizeof(struct disk_model));
+}
+
+extern "C" cl_mem icoreg_disk_buffer(const struct disk_model *m,
+                                     const char *name)
+{
+    if (strcmp(name, "out") == 0)
+        return m->out;
+    if (strcmp(name, "mask") == 0)
+        return m->mask;
+    return NULL;
+}

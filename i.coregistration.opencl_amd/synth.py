@@ -356,3 +356,37 @@ def roma_weights_files(folder, seed=BASE_SEED + CONFIG_ROMA):
             save_safetensors(fn(seed), p)
         out.append(p)
     return out
+
+
+# ---- DISK ---------------------------------------------------------------------
+
+CONFIG_DISK = 0
+DISK_CIN = (3, 16, 32, 64, 64, 128, 128, 96, 80)
+DISK_COUT = (16, 32, 64, 64, 64, 64, 64, 64, 129)
+
+
+def disk_image(H=512, W=512, seed=BASE_SEED + CONFIG_DISK):
+    """(3, H, W) blurred noise in 0..1, the DISK config's input."""
+    return smooth_noise(np.random.default_rng(seed), (3, H, W))
+
+
+def disk_weights(seed=BASE_SEED + CONFIG_DISK):
+    """DISK U-Net state dict (kornia DISK names and shapes, disk.c:43-82),
+    seeded: He-normal 5 x 5 convolutions, small biases, PReLU slopes
+    U(0.1, 0.3)."""
+    rng = np.random.default_rng(seed + 1000)
+    d = {}
+    for l in range(9):
+        pre = f"unet.path_down.{l}.1" if l < 5 else f"unet.path_up.{l - 5}.conv"
+        d[f"{pre}.3.weight"] = _he32(rng, (DISK_COUT[l], DISK_CIN[l], 5, 5))
+        d[f"{pre}.3.bias"] = _bias(rng, DISK_COUT[l])
+        if l > 0:
+            d[f"{pre}.1.weight"] = rng.uniform(0.1, 0.3, DISK_CIN[l]).astype(np.float32)
+    return d
+
+
+def disk_weights_file(path, seed=BASE_SEED + CONFIG_DISK):
+    path = Path(path)
+    if not path.exists():
+        save_safetensors(disk_weights(seed), path)
+    return path

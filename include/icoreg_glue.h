@@ -9,6 +9,7 @@
 #ifndef ICOREG_GLUE_H
 #define ICOREG_GLUE_H
 
+#include "disk.h"
 #include "eloftr.h"
 #include "pth_loader.h"
 #include "roma.h"
@@ -38,6 +39,11 @@ void icoreg_eloftr_set_pos_scale(struct eloftr_model *m, float s);
 cl_mem icoreg_eloftr_buffer(const struct eloftr_model *m, const char *name);
 
 struct roma_model *icoreg_roma_new(void);
+struct disk_model *icoreg_disk_new(void);
+
+/* A named device buffer of a DISK model: "out" (129 x H x W: descriptor
+ * channels then the heatmap), "mask" (NMS bytes); NULL otherwise. */
+cl_mem icoreg_disk_buffer(const struct disk_model *m, const char *name);
 
 /* Results of the last roma_match: H x W, host arrays owned by the model
  * (sd NULL without v2). */

@@ -104,6 +104,21 @@ void roma2_update(struct ops *o, cl_mem flow, cl_mem conf, cl_mem d, int n,
 void roma_dwconv5(struct ops *o, cl_mem in, int C, int H, int W, cl_mem w,
                   cl_mem bias, cl_mem out);
 
+/* ---- DISK (disk_kernels.cl) -------------------------------------------- */
+
+/* Keypoint candidates of the heatmap (float offset off of heat, row
+ * stride W) cropped to h x w: mask (h x w bytes) = 1 where the cell is
+ * strictly greater than its 24 neighbours in the 5 x 5 window and than
+ * thresh; the 2-cell border never. disk_kernels.cl:8-35. */
+void disk_nms5x5(struct ops *o, cl_mem heat, long off, int W, int h, int w,
+                 float thresh, cl_mem mask);
+
+/* Descriptors: channels 0..D-1 of feat (D + 1, H, W) at the n keypoints
+ * xy (int x, y pairs), L2-normalised (eps 1e-12) into desc (n x D).
+ * disk_kernels.cl:37-60. */
+void disk_gather_desc(struct ops *o, cl_mem feat, int H, int W, int D,
+                      cl_mem xy, int n, cl_mem desc);
+
 /* Extension with no counterpart among the reference's kernels: the
  * Gaussian-process solve that roma.c:770-836 runs on the host in double
  * precision, on the device in double precision. F (n x d floats) is

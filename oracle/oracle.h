@@ -167,6 +167,22 @@ int orc_eloftr_forward(const struct orc_named *weights, int nweights,
                        const float *grey0, const float *grey1, int H, int W,
                        float pos_scale, struct orc_eloftr_out *out);
 
+/* ---- DISK (disk_kernels.cl, disk.c) ------------------------------------ */
+
+/* disk_kernels.cl:8-35: mask (h x w) of strict 5 x 5 maxima above
+ * thresh of heat (row stride W), border 2 never. */
+void orc_disk_nms5x5(const float *heat, int W, int h, int w, float thresh,
+                     unsigned char *mask);
+/* disk_kernels.cl:37-60. */
+void orc_disk_gather_desc(const float *feat, int H, int W, int D,
+                          const int *xy, int n, float *desc);
+/* disk_detect (disk.c:164-273) on a (3, H, W) image: returns the keypoint
+ * count; out_full (129 x H x W, or NULL) gets the U-Net output. */
+int orc_disk_detect(const struct orc_named *weights, int nweights,
+                    const float *img, int H, int W, int h, int w, int n,
+                    float thresh, const unsigned char *valid, int *xy,
+                    float *score, float *desc, float *out_full);
+
 /* ---- RoMa network (roma.c) ------------------------------------------------ */
 
 /* Host input preparation, roma.c:1106-1186: (3, H, W) resampled to (3, h,

@@ -82,6 +82,11 @@ class RomaOut(C.Structure):
 SIGS["orc_roma_forward"] = (_I, [C.POINTER(Named), _I, C.POINTER(Named), _I,
                                  C.POINTER(Named), _I, _FP, _FP, _I, _I, _I, _I, _FP,
                                  C.POINTER(RomaOut)])
+_UP = C.POINTER(C.c_ubyte)
+SIGS["orc_disk_nms5x5"] = (None, [_FP, _I, _I, _I, _F, _UP])
+SIGS["orc_disk_gather_desc"] = (None, [_FP, _I, _I, _I, _IP, _I, _FP])
+SIGS["orc_disk_detect"] = (_I, [C.POINTER(Named), _I, _FP, _I, _I, _I, _I, _I, _F, _UP,
+                                _IP, _FP, _FP, _FP])
 SIGS["orc_roma_prepare"] = (None, [_FP, _I, _I, _FP, _I, _I, _I])
 
 _lib = None
@@ -178,6 +183,30 @@ def roma_forward(wmain, wdino, wv2, imgA, imgB, coarse, imagenet=1, cls_flow_in=
                                      len(wv2) if wv2 else 0, fp(A), fp(B), H, W, coarse,
                                      imagenet, fp(cf), C.byref(st))
     return out
+
+
+def disk_detect(weights, img, h=None, w=None, n=2048, thresh=0.0, valid=None,
+                full=False):
+    """Run the oracle's DISK detection on a (3, H, W) image."""
+    import numpy as np
+    l = oracle()
+    _, H, W = img.shape
+    h = H if h is None else h
+    w = W if w is None else w
+    arr, keep = named_array(weights)
+    xy = np.zeros(2 * n, np.int32)
+    score = np.zeros(n, np.float32)
+    desc = np.zeros((n, 128), np.float32)
+    out = np.zeros((129, H, W), np.float32) if full else None
+    img = np.ascontiguousarray(img, np.float32)
+    v = None if valid is None else np.ascontiguousarray(valid, np.uint8)
+    nk = l.orc_disk_detect(arr, len(weights), fp(img), H, W, h, w, n, thresh,
+                           v.ctypes.data_as(_UP) if v is not None else None, ip(xy),
+                           fp(score), fp(desc), fp(out))
+    r = {"n": nk, "xy": xy[:2 * nk].reshape(-1, 2), "score": score[:nk], "desc": desc[:nk]}
+    if full:
+        r["out"] = out
+    return r
 
 
 def oracle():
