@@ -64,36 +64,38 @@ __global__ void __launch_bounds__(256) dgemm_kernel(dg_args a)
             acc[p][q] = 0.0;
     for (int k0 = 0; k0 < a.K; k0 += DG_K) {
         /* 32 x 64 of A and of B, 8 values per thread, the unit-stride
-         * index fastest across threads. */
+         * index fastest across threads. Every load reads a valid address
+         * (indices clamped to the last row / column) and the value is
+         * selected afterwards, so that the 16 loads are all in flight
+         * together instead of one per guarded branch. */
+        double va[8], vb[8];
+        bool oka[8], okb[8];
+
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const int e = tid + 256 * t;
-            int i, q, j, qb;
+            const int i = a.a_rk == 1 ? e / DG_K : (e & (DG_T - 1));
+            const int q = a.a_rk == 1 ? (e & (DG_K - 1)) : e / DG_T;
+            const int j = a.b_rj == 1 ? (e & (DG_T - 1)) : e / DG_K;
+            const int qb = a.b_rj == 1 ? e / DG_T : (e & (DG_K - 1));
 
-            if (a.a_rk == 1) {
-                q = e & (DG_K - 1);
-                i = e / DG_K;
-            }
-            else {
-                i = e & (DG_T - 1);
-                q = e / DG_T;
-            }
-            As[q][i] = i0 + i < a.M && k0 + q < a.K
-                           ? a.A[(long long)(i0 + i) * a.a_ri +
-                                 (long long)(k0 + q) * a.a_rk]
-                           : 0.0;
-            if (a.b_rj == 1) {
-                j = e & (DG_T - 1);
-                qb = e / DG_T;
-            }
-            else {
-                qb = e & (DG_K - 1);
-                j = e / DG_K;
-            }
-            Bs[qb][j] = j0 + j < a.N && k0 + qb < a.K
-                            ? a.B[(long long)(k0 + qb) * a.b_rk +
-                                  (long long)(j0 + j) * a.b_rj]
-                            : 0.0;
+            oka[t] = i0 + i < a.M && k0 + q < a.K;
+            okb[t] = j0 + j < a.N && k0 + qb < a.K;
+            va[t] = a.A[(long long)min(i0 + i, a.M - 1) * a.a_ri +
+                        (long long)min(k0 + q, a.K - 1) * a.a_rk];
+            vb[t] = a.B[(long long)min(k0 + qb, a.K - 1) * a.b_rk +
+                        (long long)min(j0 + j, a.N - 1) * a.b_rj];
+        }
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const int e = tid + 256 * t;
+            const int i = a.a_rk == 1 ? e / DG_K : (e & (DG_T - 1));
+            const int q = a.a_rk == 1 ? (e & (DG_K - 1)) : e / DG_T;
+            const int j = a.b_rj == 1 ? (e & (DG_T - 1)) : e / DG_K;
+            const int qb = a.b_rj == 1 ? e / DG_T : (e & (DG_K - 1));
+
+            As[q][i] = oka[t] ? va[t] : 0.0;
+            Bs[qb][j] = okb[t] ? vb[t] : 0.0;
         }
         __syncthreads();
 #pragma unroll 8
@@ -134,69 +136,101 @@ __global__ void __launch_bounds__(256) dgemm_kernel(dg_args a)
 
 /* Cholesky factor of the nb x nb diagonal block at (k, k) of A (n x n)
  * into L, and the inverse of that factor into Linv (nb x nb, row-major,
- * GP_NB apart). info gets 1 + the first column whose pivot is not
- * positive (the factor then holds NaN from there on). */
+ * GP_NB apart), both in one pass over the columns. info gets 1 + the
+ * first column whose pivot is not positive (the factor then holds NaN
+ * from there on).
+ *
+ * LDS holds the block: its lower triangle becomes L, its strictly upper
+ * triangle holds the inverse transposed (Linv[r][c] at s[c][r], c < r,
+ * starting as the identity's zeros), the inverse's diagonal is dinv.
+ * Column j: one wave takes the pivot's square root and divides column j
+ * below it (L) and above it (row j of the inverse, in transposed
+ * storage) by it; then every thread updates the cells it owns (rows
+ * ty + 16 a, columns tx + 16 b): the trailing lower triangle of A
+ * (A[r][c] -= L[r][j] L[c][j], c > j) and the inverse's rows below j
+ * (B[r][c] -= L[r][j] Linv[j][c], c <= j), branch-free so that all its
+ * LDS reads issue together. */
 __global__ void __launch_bounds__(256)
     chol_diag_kernel(const double *__restrict__ A, double *__restrict__ L,
                      double *__restrict__ Linv, int n, int k, int nb,
                      int *__restrict__ info)
 {
     __shared__ double s[GP_NB][GP_NB + 1];
-    const int tid = threadIdx.x;
+    __shared__ double dinv[GP_NB];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
 
-    for (int e = tid; e < nb * nb; e += 256) {
-        const int r = e / nb, c = e % nb;
+    {
+        double v[16];
 
-        s[r][c] = A[(long long)(k + r) * n + k + c];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int e = tid + 256 * i, r = e >> 6, c = e & 63;
+
+            v[i] = A[(long long)(k + min(r, nb - 1)) * n + k + min(c, nb - 1)];
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int e = tid + 256 * i, r = e >> 6, c = e & 63;
+
+            s[r][c] = r < nb && c <= r ? v[i] : 0.0;
+        }
     }
     __syncthreads();
     for (int j = 0; j < nb; j++) {
-        if (tid == 0) {
+        if (tid < 64) {
             const double d = s[j][j];
+            const double sq = sqrt(d);
 
-            if (!(d > 0.0) && *info == 0)
+            if (tid == 0 && !(d > 0.0) && *info == 0)
                 *info = k + j + 1;
-            s[j][j] = sqrt(d);
+            if (tid == j) {
+                s[j][j] = sq;
+                dinv[j] = 1.0 / sq;
+            }
+            else if (tid < nb)
+                s[tid][j] /= sq;
         }
-        __syncthreads();
-        for (int r = j + 1 + tid; r < nb; r += 256)
-            s[r][j] /= s[j][j];
         __syncthreads();
         {
-            const int m = nb - j - 1;
+            const double dj = dinv[j];
+            double lr[4], lc[4], v[4][4];
 
-            for (int e = tid; e < m * m; e += 256) {
-                const int r = j + 1 + e / m, c = j + 1 + e % m;
-
-                if (c <= r)
-                    s[r][c] -= s[r][j] * s[c][j];
+#pragma unroll
+            for (int a4 = 0; a4 < 4; a4++) {
+                lr[a4] = s[ty + 16 * a4][j];
+                lc[a4] = s[tx + 16 * a4][j];
             }
+#pragma unroll
+            for (int a4 = 0; a4 < 4; a4++)
+#pragma unroll
+                for (int b4 = 0; b4 < 4; b4++)
+                    v[a4][b4] = s[ty + 16 * a4][tx + 16 * b4];
+#pragma unroll
+            for (int a4 = 0; a4 < 4; a4++)
+#pragma unroll
+                for (int b4 = 0; b4 < 4; b4++) {
+                    const int r = ty + 16 * a4, c = tx + 16 * b4;
+                    /* lower: factor update; upper (r < c): inverse cell
+                     * (c, r), updated for r <= j < c. */
+                    const bool low = r < nb && c > j && c <= r;
+                    const bool inv = c < nb && r <= j && j < c;
+                    const double f = r == j ? dj : lr[a4];
+
+                    s[r][c] = low ? fma(-lr[a4], lc[b4], v[a4][b4])
+                              : inv ? fma(-lc[b4], f, v[a4][b4])
+                                    : v[a4][b4];
+                }
         }
         __syncthreads();
     }
-    /* Inverse of the lower factor, one column per thread, written
-     * straight to Linv (each thread reads back only its own column):
-     * v[c][c] = 1 / s[c][c], v[r][c] = -sum_{c <= q < r} s[r][q] v[q][c]
-     * / s[r][r]. */
-    if (tid < nb) {
-        const int c = tid;
-        double *v = Linv + c;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int e = tid + 256 * i, r = e >> 6, c = e & 63;
 
-        for (int r = 0; r < c; r++)
-            v[r * GP_NB] = 0.0;
-        v[c * GP_NB] = 1.0 / s[c][c];
-        for (int r = c + 1; r < nb; r++) {
-            double t = 0.0;
-
-            for (int q = c; q < r; q++)
-                t = fma(s[r][q], v[q * GP_NB], t);
-            v[r * GP_NB] = -t / s[r][r];
+        if (r < nb && c < nb) {
+            L[(long long)(k + r) * n + k + c] = c <= r ? s[r][c] : 0.0;
+            Linv[r * GP_NB + c] = r == c ? dinv[c] : r > c ? s[c][r] : 0.0;
         }
-    }
-    for (int e = tid; e < nb * nb; e += 256) {
-        const int r = e / nb, c = e % nb;
-
-        L[(long long)(k + r) * n + k + c] = c <= r ? s[r][c] : 0.0;
     }
 }
 
