@@ -84,6 +84,43 @@ def eloftr_flops(H, W, nm=0):
             "total": conv + gemm + attn + other}
 
 
+def eloftr_conv_layers(H, W):
+    """(ci, co, hin, win, stride) of the 25 direct 3 x 3 convolution
+    launches of one pair (each launch covers both images): 21 backbone
+    layers (eloftr.c:367-394), 4 fusion layers (eloftr.c:573-604)."""
+    out, Hc, Wc = [], H, W
+    for ci, co, st in [(1, 64, 2)] + [(64, 64, 1)] * 2 + [(64, 128, 2)] + [(128, 128, 1)] * 3 + \
+            [(128, 256, 2)] + [(256, 256, 1)] * 13:
+        out.append((ci, co, Hc, Wc, st))
+        Hc, Wc = Hc // st, Wc // st
+    H4, W4, H2, W2 = H // 4, W // 4, H // 2, W // 2
+    out += [(256, 256, H4, W4, 1), (256, 128, H4, W4, 1), (128, 128, H2, W2, 1),
+            (128, 64, H2, W2, 1)]
+    return out
+
+
+def eloftr_conv_bytes(H, W):
+    """Algorithmic HBM bytes of the 25 convolution launches of one pair:
+    both images' input and output read / written once, weights and bias
+    once per launch."""
+    b = 0
+    for ci, co, h, w, st in eloftr_conv_layers(H, W):
+        b += 4 * (2 * (ci * h * w + co * (h // st) * (w // st)) + co * ci * 9 + co)
+    return b
+
+
+def conv_traffic(profile=ROOT / "profiles" / "eloftr_640_conv_traffic.md"):
+    """Measured HBM bytes per convolution launch, from the committed
+    rocprofv3 counter summary (the line 'traffic_bytes_per_launch: N'),
+    or None."""
+    import re
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", profile.read_text())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def roma_coarse_flops(coarse=560):
     """Algorithmic FLOPs of RoMa's coarse forward on one pair (DINOv2 x 2,
     GP, decoder), by kernel family; the GP's double-precision Cholesky
@@ -190,6 +227,8 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roma", action="store_true")
+    ap.add_argument("--roma-only", action="store_true",
+                    help="run only the RoMa leg and print its JSON object (for profiling)")
     ap.add_argument("--roma-steps", type=int, default=10)
     ap.add_argument("--copy-calib", type=int, default=0,
                     help="MiB: one device-to-device copy of this size, the known-size "
@@ -209,6 +248,11 @@ def main():
     dev = ic.Device("auto")
     print(f"[bench] {dev.name} ({dev.arch}), {dev.ocl.cu_count} CUs", file=sys.stderr, flush=True)
     wdir = Path(tempfile.gettempdir()) / "icoreg_bench"
+    if args.roma_only:
+        print(json.dumps(bench_roma(ic, dev, synth, wdir, args.roma_steps, 2,
+                                    args.profile_steps)), flush=True)
+        dev.close()
+        return
     wfile = synth.eloftr_weights_file(wdir / "eloftr_random_calibrated.safetensors")
     g0, g1, _ = synth.eloftr_pair(H, W)
     net = ic.Eloftr(dev, wfile, H, W)
@@ -306,7 +350,9 @@ def main():
         "roofline": {"kernel": "conv_direct (3x3 convolution, fp32 MFMA on LDS patches)",
                      "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4),
+                     "traffic": conv_traffic() if H == W == 640 else None,
+                     "algorithmic_bytes_per_launch": round(eloftr_conv_bytes(H, W) / 25),
                      "launches_per_step": conv_calls,
                      "gflop_per_step": round(fl["conv"] / 1e9, 2)},
         "pipeline_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
