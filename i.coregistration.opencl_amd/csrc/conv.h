@@ -25,6 +25,10 @@ struct conv_args {
 bool conv_direct_supported(int kh, int kw, int sy, int sx, int dy, int dx,
                            int groups);
 
+/* True if the tensors are small enough for the kernel's 32-bit buffer
+ * offsets (per-image input and the weights below 2 GiB). */
+bool conv_direct_fits(long long in_floats, long long w_floats);
+
 void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,
                         int cus, hipStream_t s);
 

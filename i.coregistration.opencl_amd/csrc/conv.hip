@@ -6,22 +6,26 @@
  * i.coregistration.opencl): out = act(W * in + bias), optional input
  * normalisation and PReLU gate before the zero padding.
  *
- * A block computes 128 output pixels (a 4 x 32 tile of one image) for
- * BM output channels as an implicit GEMM (M = channels, N = pixels,
- * K = C k k). The K loop walks CC input channels at a time:
+ * A block computes 128 output pixels (a TH x TW tile of one image, 4 x 32
+ * or 8 x 16, whichever wastes less of the image) for BM output channels
+ * as an implicit GEMM (M = channels, N = pixels, K = C k k). The K loop
+ * walks CC input channels at a time:
  *  - the weights of the slice (BM x CC k k, contiguous per output
  *    channel) go to LDS k-major;
- *  - the input patch under the tile (CC x (4 s + k - s) x (32 s + k - s)
+ *  - the input patch under the tile (CC x ((TH-1) s + k) x ((TW-1) s + k)
  *    floats, zero outside the image) goes to LDS once, normalised and
- *    gated there (once per input value rather than once per tap);
+ *    gated there (once per input value rather than once per tap); at
+ *    stride 2 its even and odd columns are stored apart, so that the
+ *    lanes of one output row read consecutive words;
  *  - each MFMA step (v_mfma_f32_32x32x2f32, K = 2) reads its B operand
- *    straight from the patch at the tap's (channel, row, column) shift,
- *    consecutive lanes on consecutive pixels of one output row; the
- *    shifts are compile-time constants, so the inner loop has no index
- *    arithmetic beyond one select per step for the lane half.
- * Double-buffered: the next slice is fetched into registers while the
- * matrix cores work on the current one. Images of a batch run on the
- * grid's z dimension. */
+ *    straight from the patch at the tap's (channel, row, column) shift;
+ *    the shifts are compile-time constants.
+ * Global reads are buffer loads: the zero padding, the channel and
+ * output-channel tails come from the buffer's range check (an offset
+ * past the end reads 0), so a fetch is one load per value with offsets
+ * computed once per thread. Double-buffered: the next slice is fetched
+ * into registers while the matrix cores work on the current one. Images
+ * of a batch run on the grid's z dimension. */
 
 #include <hip/hip_runtime.h>
 
@@ -30,38 +34,65 @@
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-#define TILE_H 4
-#define TILE_W 32
+/* Offset past the end of every buffer the kernel reads (each is below
+ * 2 GiB): its load returns 0. */
+#define CONV_OOB 0x80000000u
 
-template <int KS, int ST, int BM>
+/* Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data. */
+#define CONV_RSRC_FLAGS 0x00020000
+
+static __device__ __forceinline__ __amdgpu_buffer_rsrc_t
+conv_rsrc(const float *p, unsigned long long bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0,
+                                             (int)(unsigned)bytes,
+                                             CONV_RSRC_FLAGS);
+}
+
+static __device__ __forceinline__ float conv_load(__amdgpu_buffer_rsrc_t r,
+                                                  unsigned off)
+{
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+template <int KS, int ST, int BM, int TW>
 __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
 {
-    /* Input channels per K slice: 36 or 18 taps for 3 x 3, 50 for 5 x 5. */
-    constexpr int CC = KS == 3 ? (BM == 128 ? 2 : 4) : 2;
+    constexpr int TH = 128 / TW;
+    /* Input channels per K slice: K = 36 or 72 per slice for 3 x 3,
+     * 50 or 100 for 5 x 5. */
+    constexpr int CC = (KS == 3 ? 4 : 2) * (BM == 128 ? 1 : 2);
     constexpr int KK = KS * KS;
-    constexpr int KT = CC * KK;          /* K per slice (even) */
-    constexpr int PH = (TILE_H - 1) * ST + KS;
-    constexpr int PW = (TILE_W - 1) * ST + KS;
+    constexpr int KT = CC * KK;
+    constexpr int PH = (TH - 1) * ST + KS;
+    constexpr int PW = (TW - 1) * ST + KS;
+    constexpr int HALF = (PW + 1) / 2;   /* stride 2: even columns first */
     constexpr int PWP = PW + 1;
     constexpr int PCH = PH * PWP;        /* LDS floats per patch channel */
+    constexpr int PN = CC * PH * PW;     /* patch values per slice */
     constexpr int LDA = BM + 4;
     constexpr int TM = BM / 64;
-    constexpr int NA = (BM * KT + 255) / 256;
-    constexpr int NP = (CC * PH * PW + 255) / 256;
-    static_assert(KT % 2 == 0, "K slice must be even");
+    constexpr int NA = BM * KT / 256;
+    constexpr int NP = (PN + 255) / 256;
+    constexpr int RJ = 32 / TW;          /* tile rows per 32 pixels */
+    static_assert(KT % 2 == 0 && BM * KT % 256 == 0, "slice shape");
     __shared__ float As[2][KT * LDA];
-    __shared__ float Ps[2][CC * PCH];
+    __shared__ float Ps[2][CC * PCH + 1]; /* + one slot for idle lanes */
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, half = lane >> 5, col = lane & 31;
-    const int tiles_w = (a.Wo + TILE_W - 1) / TILE_W;
-    const int oy0 = (blockIdx.x / tiles_w) * TILE_H;
-    const int ox0 = (blockIdx.x % tiles_w) * TILE_W;
+    const int tiles_w = (a.Wo + TW - 1) / TW;
+    const int oy0 = (blockIdx.x / tiles_w) * TH;
+    const int ox0 = (blockIdx.x % tiles_w) * TW;
     const int m0 = blockIdx.y * BM;
     const int iy0 = oy0 * ST - a.pad, ix0 = ox0 * ST - a.pad;
     const int C = a.C, H = a.H, W = a.W, K = a.K;
+    const long long HW = (long long)H * W;
     const float *in = a.in + (long long)blockIdx.z * a.in_stride;
     const long long wrow = (long long)C * KK;
+    unsigned woff[NA], poff[NP];
+    int lda_[NA], ldp[NP];
     float ra[NA], rp[NP];
     floatx16 acc[TM][2];
 
@@ -73,55 +104,80 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
             for (int r = 0; r < 16; r++)
                 acc[i][j][r] = 0.0f;
 
+    /* Per-thread offsets, the same for every slice: weights of output
+     * channel m0 + m at slice tap t; patch value (c, py, px). */
+#pragma unroll
+    for (int q = 0; q < NA; q++) {
+        const int e = tid + 256 * q, m = e / KT, t = e - m * KT;
+
+        woff[q] = m0 + m < K ? (unsigned)(((m0 + m) * wrow + t) * 4)
+                             : CONV_OOB;
+        lda_[q] = t * LDA + m;
+    }
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+        const int e = tid + 256 * q, c = e / (PH * PW);
+        const int rem = e - c * (PH * PW), py = rem / PW, px = rem - py * PW;
+        const int iy = iy0 + py, ix = ix0 + px;
+        const int lc = ST == 1 ? px : (px & 1) * HALF + (px >> 1);
+
+        poff[q] = e < PN && iy >= 0 && iy < H && ix >= 0 && ix < W
+                      ? (unsigned)((c * HW + (long long)iy * W + ix) * 4)
+                      : CONV_OOB;
+        ldp[q] = e < PN ? c * PCH + py * PWP + lc : CC * PCH;
+    }
+
+    const unsigned long long wbytes = (unsigned long long)K * wrow * 4;
+    const unsigned long long ibytes = (unsigned long long)C * HW * 4;
+
     auto fetch = [&](int c0) {
-#pragma unroll
-        for (int q = 0; q < NA; q++) {
-            const int e = tid + 256 * q, m = e / KT, t = e - m * KT;
-            const int c = c0 + t / KK;
-            float v = 0.0f;
+        const __amdgpu_buffer_rsrc_t rw =
+            conv_rsrc(a.w + (long long)c0 * KK, wbytes - (unsigned long long)c0 * KK * 4);
+        const __amdgpu_buffer_rsrc_t ri =
+            conv_rsrc(in + c0 * HW, ibytes - (unsigned long long)c0 * HW * 4);
 
-            if (e < BM * KT && m0 + m < K && c < C)
-                v = a.w[(long long)(m0 + m) * wrow + (long long)c0 * KK + t];
-            ra[q] = v;
-        }
 #pragma unroll
-        for (int q = 0; q < NP; q++) {
-            const int e = tid + 256 * q, c = e / (PH * PW);
-            const int rem = e - c * (PH * PW), py = rem / PW, px = rem - py * PW;
-            const int iy = iy0 + py, ix = ix0 + px, cg = c0 + c;
-            float v = 0.0f;
+        for (int q = 0; q < NA; q++)
+            ra[q] = conv_load(rw, woff[q]);
+#pragma unroll
+        for (int q = 0; q < NP; q++)
+            rp[q] = conv_load(ri, poff[q]);
+        if (c0 + CC > C) {
+            /* Ragged last slice: the weight rows run on into the next
+             * output channel, so mask the taps of missing channels. */
+#pragma unroll
+            for (int q = 0; q < NA; q++) {
+                const int e = tid + 256 * q, t = e - (e / KT) * KT;
 
-            if (e < CC * PH * PW && cg < C && iy >= 0 && iy < H && ix >= 0 &&
-                ix < W) {
-                v = in[((long long)cg * H + iy) * W + ix];
-                if (a.mean) {
-                    v = (v - a.mean[cg]) * a.rstd[cg];
-                    if (a.gate)
-                        v = v >= 0.0f ? v : a.gate[cg] * v;
-                }
+                ra[q] = c0 + t / KK < C ? ra[q] : 0.0f;
             }
-            rp[q] = v;
+        }
+        if (a.mean) {
+#pragma unroll
+            for (int q = 0; q < NP; q++) {
+                const int cg = c0 + (tid + 256 * q) / (PH * PW);
+                const int cc = cg < C ? cg : C - 1;
+                float v = (rp[q] - a.mean[cc]) * a.rstd[cc];
+
+                if (a.gate)
+                    v = v >= 0.0f ? v : a.gate[cc] * v;
+                rp[q] = poff[q] != CONV_OOB && cg < C ? v : 0.0f;
+            }
         }
     };
     auto stash = [&](int buf) {
 #pragma unroll
-        for (int q = 0; q < NA; q++) {
-            const int e = tid + 256 * q, m = e / KT, t = e - m * KT;
-
-            if (e < BM * KT)
-                As[buf][t * LDA + m] = ra[q];
-        }
+        for (int q = 0; q < NA; q++)
+            As[buf][lda_[q]] = ra[q];
 #pragma unroll
-        for (int q = 0; q < NP; q++) {
-            const int e = tid + 256 * q, c = e / (PH * PW);
-            const int rem = e - c * (PH * PW), py = rem / PW, px = rem - py * PW;
-
-            if (e < CC * PH * PW)
-                Ps[buf][c * PCH + py * PWP + px] = rp[q];
-        }
+        for (int q = 0; q < NP; q++)
+            Ps[buf][ldp[q]] = rp[q];
     };
 
     const int nk = (C + CC - 1) / CC;
+    /* This lane's first pixel: row r of the tile, column x. */
+    const int pr = (wn * 64 + col) / TW, px0 = col % TW;
+    const int pbase = pr * ST * PWP + px0;
 
     fetch(0);
     stash(0);
@@ -133,14 +189,18 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
             fetch((kt + 1) * CC);
         {
             const float *as = As[cur] + wm * (BM / 2) + col;
-            const float *ps = Ps[cur] + (wn * 2 * ST) * PWP + col * ST;
+            const float *ps = Ps[cur] + pbase;
 
 #pragma unroll
             for (int s = 0; s < KT / 2; s++) {
                 /* Taps t = 2 s (lane half 0) and 2 s + 1 (half 1). */
                 const int t0 = 2 * s, t1 = 2 * s + 1;
-                const int p0 = (t0 / KK) * PCH + ((t0 % KK) / KS) * PWP + t0 % KS;
-                const int p1 = (t1 / KK) * PCH + ((t1 % KK) / KS) * PWP + t1 % KS;
+                const int c_0 = t0 / KK, y_0 = (t0 % KK) / KS, x_0 = t0 % KS;
+                const int c_1 = t1 / KK, y_1 = (t1 % KK) / KS, x_1 = t1 % KS;
+                const int p0 = c_0 * PCH + y_0 * PWP +
+                               (ST == 1 ? x_0 : (x_0 & 1) * HALF + (x_0 >> 1));
+                const int p1 = c_1 * PCH + y_1 * PWP +
+                               (ST == 1 ? x_1 : (x_1 & 1) * HALF + (x_1 >> 1));
                 const int po = half ? p1 : p0;
                 const int ao = (2 * s + half) * LDA;
                 float av[TM], bv[2];
@@ -150,7 +210,7 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
                     av[i] = as[ao + i * 32];
 #pragma unroll
                 for (int j = 0; j < 2; j++)
-                    bv[j] = ps[po + j * ST * PWP];
+                    bv[j] = ps[po + j * RJ * ST * PWP];
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -169,7 +229,7 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
 
 #pragma unroll
         for (int j = 0; j < 2; j++) {
-            const int oy = oy0 + wn * 2 + j, ox = ox0 + col;
+            const int oy = oy0 + pr + j * RJ, ox = ox0 + px0;
 
             if (oy >= a.Ho || ox >= a.Wo)
                 continue;
@@ -200,20 +260,43 @@ bool conv_direct_supported(int kh, int kw, int sy, int sx, int dy, int dx,
            (sy == 1 || sy == 2) && dy == 1 && dx == 1;
 }
 
-template <int KS, int ST>
-static void launch_ks(const conv_args &a, int nb, hipStream_t s)
+bool conv_direct_fits(long long in_floats, long long w_floats)
 {
-    const int tiles = ((a.Wo + TILE_W - 1) / TILE_W) *
-                      ((a.Ho + TILE_H - 1) / TILE_H);
+    /* Buffer offsets are 32-bit byte offsets below the value that marks
+     * padding. */
+    return in_floats * 4 < 0x80000000LL && w_floats * 4 < 0x80000000LL;
+}
+
+/* Padded output area of a TW-wide tiling. */
+static long long tiled_area(int Ho, int Wo, int tw)
+{
+    const int th = 128 / tw;
+
+    return (long long)((Ho + th - 1) / th) * th * ((Wo + tw - 1) / tw) * tw;
+}
+
+template <int KS, int ST, int TW>
+static void launch_tw(const conv_args &a, int nb, hipStream_t s)
+{
+    const int tiles = ((a.Wo + TW - 1) / TW) * ((a.Ho + 128 / TW - 1) / (128 / TW));
 
     if (a.K <= 64)
-        hipLaunchKernelGGL((conv_mfma<KS, ST, 64>),
+        hipLaunchKernelGGL((conv_mfma<KS, ST, 64, TW>),
                            dim3(tiles, (a.K + 63) / 64, nb), dim3(256), 0, s,
                            a);
     else
-        hipLaunchKernelGGL((conv_mfma<KS, ST, 128>),
+        hipLaunchKernelGGL((conv_mfma<KS, ST, 128, TW>),
                            dim3(tiles, (a.K + 127) / 128, nb), dim3(256), 0,
                            s, a);
+}
+
+template <int KS, int ST>
+static void launch_ks(const conv_args &a, int nb, hipStream_t s)
+{
+    if (tiled_area(a.Ho, a.Wo, 16) < tiled_area(a.Ho, a.Wo, 32))
+        launch_tw<KS, ST, 16>(a, nb, s);
+    else
+        launch_tw<KS, ST, 32>(a, nb, s);
 }
 
 void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,

@@ -332,7 +332,9 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
     }
     if (conv_direct_supported(g->kh, g->kw, g->sy, g->sx, g->dy, g->dx,
                               g->groups) &&
-        g->py == g->px) {
+        g->py == g->px &&
+        conv_direct_fits((long long)C * H * W,
+                         (long long)K * C * g->kh * g->kw)) {
         conv_args a;
 
         a.in = cfptr(in);

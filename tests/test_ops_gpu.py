@@ -87,6 +87,11 @@ CONV_SHAPES = [
     (1, 80, 33, 31, 129, 5, 1, 2, 1, 0),
     (1, 7, 21, 35, 10, 5, 2, 2, 1, 2),
     (2, 130, 19, 70, 200, 3, 1, 1, 0, 1),
+    # Widths where 8 x 16 output tiles waste less than 4 x 32 ones.
+    (1, 64, 40, 80, 96, 3, 1, 1, 0, 2),
+    (2, 20, 60, 90, 40, 3, 2, 1, 0, 3),
+    (1, 7, 30, 90, 70, 5, 2, 2, 1, 2),
+    (1, 9, 17, 48, 20, 5, 1, 2, 1, 1),
 ]
 
 
