@@ -56,13 +56,12 @@ static __device__ __forceinline__ float conv_load(__amdgpu_buffer_rsrc_t r,
         float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
 }
 
-template <int KS, int ST, int BM, int TW>
+/* KS x KS taps, stride ST, BM output channels and a 128 / TW x TW pixel
+ * tile per block, CC input channels per K slice. */
+template <int KS, int ST, int BM, int TW, int CC>
 __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
 {
     constexpr int TH = 128 / TW;
-    /* Input channels per K slice: K = 36 or 72 per slice for 3 x 3,
-     * 50 or 100 for 5 x 5. */
-    constexpr int CC = (KS == 3 ? 4 : 2) * (BM == 128 ? 1 : 2);
     constexpr int KK = KS * KS;
     constexpr int KT = CC * KK;
     constexpr int PH = (TH - 1) * ST + KS;
@@ -190,10 +189,9 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
         {
             const float *as = As[cur] + wm * (BM / 2) + col;
             const float *ps = Ps[cur] + pbase;
-
-#pragma unroll
-            for (int s = 0; s < KT / 2; s++) {
-                /* Taps t = 2 s (lane half 0) and 2 s + 1 (half 1). */
+            /* Operands of step s: taps t = 2 s (lane half 0) and 2 s + 1
+             * (half 1). */
+            auto operands = [&](int s, float *av, float *bv) {
                 const int t0 = 2 * s, t1 = 2 * s + 1;
                 const int c_0 = t0 / KK, y_0 = (t0 % KK) / KS, x_0 = t0 % KS;
                 const int c_1 = t1 / KK, y_1 = (t1 % KK) / KS, x_1 = t1 % KS;
@@ -203,7 +201,6 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
                                (ST == 1 ? x_1 : (x_1 & 1) * HALF + (x_1 >> 1));
                 const int po = half ? p1 : p0;
                 const int ao = (2 * s + half) * LDA;
-                float av[TM], bv[2];
 
 #pragma unroll
                 for (int i = 0; i < TM; i++)
@@ -211,16 +208,38 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
 #pragma unroll
                 for (int j = 0; j < 2; j++)
                     bv[j] = ps[po + j * RJ * ST * PWP];
+            };
+            constexpr int NS = KT / 2;
+            /* LDS reads run PF steps ahead of the MFMAs that use them. */
+            constexpr int PF = 2;
+            float av[PF + 1][TM], bv[PF + 1][2];
+
+            /* The scheduling barriers keep the reads of step s + PF ahead
+             * of the MFMAs of step s, so their latency hides behind the
+             * matrix pipe; the next slice goes to the other LDS buffer a
+             * few steps before the end. */
+#pragma unroll
+            for (int s = 0; s < PF; s++)
+                operands(s, av[s], bv[s]);
+#pragma unroll
+            for (int s = 0; s < NS; s++) {
+                constexpr int NB = PF + 1;
+
+                if (s + PF < NS)
+                    operands(s + PF, av[(s + PF) % NB], bv[(s + PF) % NB]);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
                     for (int j = 0; j < 2; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                            av[i], bv[j], acc[i][j], 0, 0, 0);
+                            av[s % NB][i], bv[s % NB][j], acc[i][j], 0, 0,
+                            0);
+                if (s == NS - 4 && kt + 1 < nk)
+                    stash(cur ^ 1);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if (kt + 1 < nk)
-            stash(cur ^ 1);
         __syncthreads();
     }
 
@@ -275,40 +294,55 @@ static long long tiled_area(int Ho, int Wo, int tw)
     return (long long)((Ho + th - 1) / th) * th * ((Wo + tw - 1) / tw) * tw;
 }
 
+template <int KS, int ST, int BM, int TW>
+static void launch_cfg(const conv_args &a, int tiles, int nb, hipStream_t s)
+{
+    /* K = 100 (5 x 5) or 36 (3 x 3) per slice at 64 channels per block,
+     * 50 at 128. */
+    constexpr int CC = BM == 128 ? 2 : 4;
+
+    hipLaunchKernelGGL((conv_mfma<KS, ST, BM, TW, CC>),
+                       dim3(tiles, (a.K + BM - 1) / BM, nb), dim3(256), 0, s,
+                       a);
+}
+
 template <int KS, int ST, int TW>
-static void launch_tw(const conv_args &a, int nb, hipStream_t s)
+static void launch_tw(const conv_args &a, int nb, int cus, hipStream_t s)
 {
     const int tiles = ((a.Wo + TW - 1) / TW) * ((a.Ho + 128 / TW - 1) / (128 / TW));
 
-    if (a.K <= 64)
-        hipLaunchKernelGGL((conv_mfma<KS, ST, 64, TW>),
-                           dim3(tiles, (a.K + 63) / 64, nb), dim3(256), 0, s,
-                           a);
-    else
-        hipLaunchKernelGGL((conv_mfma<KS, ST, 128, TW>),
-                           dim3(tiles, (a.K + 127) / 128, nb), dim3(256), 0,
-                           s, a);
+    /* 3 x 3: 64 output channels per block at every size measured (the
+     * smaller block keeps more waves per CU in flight). 5 x 5: 128
+     * channels unless that grid would leave CUs with fewer than two
+     * blocks each. */
+    if constexpr (KS == 5) {
+        if (a.K > 64 &&
+            (long long)tiles * ((a.K + 127) / 128) * nb >= 2LL * cus) {
+            launch_cfg<KS, ST, 128, TW>(a, tiles, nb, s);
+            return;
+        }
+    }
+    launch_cfg<KS, ST, 64, TW>(a, tiles, nb, s);
 }
 
 template <int KS, int ST>
-static void launch_ks(const conv_args &a, int nb, hipStream_t s)
+static void launch_ks(const conv_args &a, int nb, int cus, hipStream_t s)
 {
     if (tiled_area(a.Ho, a.Wo, 16) < tiled_area(a.Ho, a.Wo, 32))
-        launch_tw<KS, ST, 16>(a, nb, s);
+        launch_tw<KS, ST, 16>(a, nb, cus, s);
     else
-        launch_tw<KS, ST, 32>(a, nb, s);
+        launch_tw<KS, ST, 32>(a, nb, cus, s);
 }
 
 void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,
                         int cus, hipStream_t s)
 {
-    (void)cus;
     if (ks == 3 && stride == 1)
-        launch_ks<3, 1>(a, nb, s);
+        launch_ks<3, 1>(a, nb, cus, s);
     else if (ks == 3)
-        launch_ks<3, 2>(a, nb, s);
+        launch_ks<3, 2>(a, nb, cus, s);
     else if (stride == 1)
-        launch_ks<5, 1>(a, nb, s);
+        launch_ks<5, 1>(a, nb, cus, s);
     else
-        launch_ks<5, 2>(a, nb, s);
+        launch_ks<5, 2>(a, nb, cus, s);
 }
