@@ -14,7 +14,12 @@
  *    single block the second pass reuses the scores instead of
  *    recomputing the identical GEMM;
  *  - statistics buffers are initialised by device fills, not host
- *    writes. */
+ *    writes;
+ *  - the two self-attention blocks of a layer run as one batch, and the
+ *    MLP of every attention block runs on channel-major maps (products
+ *    W * [x; message] instead of token-major linears between
+ *    transposes, the MLP LayerNorm fused with the residual add): the
+ *    same sums per output value, in another memory layout. */
 
 #include <math.h>
 #include <stdio.h>
@@ -23,6 +28,7 @@
 
 #include "common.h"
 #include "eloftr.h"
+#include "eloftr_fused.h"
 #include "icoreg_kernels.h"
 
 using namespace icoreg;
@@ -311,19 +317,23 @@ extern "C" void eloftr_alloc(struct eloftr_model *m, int H, int W)
         m->x[k] = view(m->xp, k, ELOFTR_DIM * n);
         m->fine[k] = view(m->finep, k, ELOFTR_FINE_DIM * hw);
     }
-    m->t_q = walloc(m, ELOFTR_DIM * na, "aggregated");
-    m->t_kv = walloc(m, ELOFTR_DIM * na, "aggregated");
-    m->t_qn = walloc(m, ELOFTR_DIM * na, "tokens");
-    m->t_kvn = walloc(m, ELOFTR_DIM * na, "tokens");
-    m->t_Q = walloc(m, ELOFTR_DIM * na, "queries");
-    m->t_K = walloc(m, ELOFTR_DIM * na, "keys");
-    m->t_V = walloc(m, ELOFTR_DIM * na, "values");
-    m->t_O = walloc(m, ELOFTR_DIM * na, "attention");
-    m->t_O2 = walloc(m, ELOFTR_DIM * na, "attention");
-    m->t_cat = walloc(m, 2 * ELOFTR_DIM * n, "concatenation");
-    m->t_tok = walloc(m, 2 * ELOFTR_DIM * n, "tokens");
-    m->t_h1 = walloc(m, MLP * n, "mlp");
-    m->t_h2 = walloc(m, ELOFTR_DIM * n, "mlp");
+    /* Transformer work buffers hold both images (self-attention runs the
+     * pair as one batch). */
+    m->t_q = walloc(m, 2 * ELOFTR_DIM * na, "aggregated");
+    m->t_kv = walloc(m, 2 * ELOFTR_DIM * na, "aggregated");
+    m->t_qn = walloc(m, 2 * ELOFTR_DIM * na, "tokens");
+    m->t_kvn = walloc(m, 2 * ELOFTR_DIM * na, "tokens");
+    m->t_Q = walloc(m, 2 * ELOFTR_DIM * na, "queries");
+    m->t_K = walloc(m, 2 * ELOFTR_DIM * na, "keys");
+    m->t_V = walloc(m, 2 * ELOFTR_DIM * na, "values");
+    m->t_O = walloc(m, 2 * ELOFTR_DIM * na, "attention");
+    m->t_O2 = walloc(m, 2 * ELOFTR_DIM * na, "attention");
+    for (int k = 0; k < 2; k++)
+        m->t_O2v[k] = view(m->t_O2, k, ELOFTR_DIM * na);
+    m->t_cat = walloc(m, 4 * ELOFTR_DIM * n, "concatenation");
+    m->t_tok = walloc(m, ELOFTR_DIM * n, "tokens");
+    m->t_h1 = walloc(m, 2 * MLP * n, "mlp");
+    m->t_h2 = walloc(m, 2 * ELOFTR_DIM * n, "mlp");
     rope_table(m);
     m->blk_rows = (int)(SCORE_BLOCK_FLOATS / n);
     if (m->blk_rows > (int)n)
@@ -406,61 +416,86 @@ static void copyf(struct eloftr_model *m, cl_mem src, size_t soff, cl_mem dst,
              floats * sizeof(float));
 }
 
-/* One aggregated attention block: X (256 x h x w) attends to Y, X
- * updated in place (eloftr.c:405-449). */
+/* One aggregated attention block (eloftr.c:405-449) for nimg images at
+ * once: image i of X (256 x h x w maps, nimg of them one after the other)
+ * attends to image i of Y and is updated in place. The self-attention
+ * blocks of a pair run with nimg = 2 (both images' maps are contiguous
+ * in xp); cross-attention runs image by image, as the reference orders
+ * it.
+ *
+ * Up to the attention message this is the reference's sequence on
+ * token-major rows. The MLP then runs on channel-major maps: fc1 and fc2
+ * as W * [x; message] products on the (2 D, n) concatenation, so the
+ * reference's transposes of the concatenation and of the MLP output are
+ * not needed, and the MLP LayerNorm and the residual add are one
+ * channel-wise kernel. */
 static void agg_attn(struct eloftr_model *m, const struct eloftr_attn *a,
-                     cl_mem X, cl_mem Y, int use_rope)
+                     cl_mem X, cl_mem Y, int nimg, int use_rope)
 {
     struct ops *o = m->ops;
     struct conv_geom g = {4, 4, 4, 4, 0, 0, 1, 1, ELOFTR_DIM};
     const int D = ELOFTR_DIM, n = m->h * m->w, na = m->ah * m->aw;
-    const int hd = D / HEADS;
+    const int hd = D / HEADS, rows = nimg * na;
 
-    ops_conv2d(o, X, D, m->h, m->w, a->q_agg, NULL, D, &g, NULL, NULL, NULL,
-               ACT_NONE, 0, m->t_q);
-    ops_pool2d(o, Y, D, m->h, m->w, 4, 4, 0, 1, m->t_kv);
-    ops_transpose(o, m->t_q, m->t_qn, 1, D, na);
-    ops_transpose(o, m->t_kv, m->t_kvn, 1, D, na);
-    ops_layernorm(o, na, D, m->t_qn, m->t_qn, a->norm_g, a->norm_b, EPS_LN,
+    ops_conv2d_batch(o, nimg, X, (long)D * n, D, m->h, m->w, a->q_agg, NULL,
+                     D, &g, NULL, NULL, NULL, ACT_NONE, 0, m->t_q,
+                     (long)D * na);
+    ops_pool2d(o, Y, nimg * D, m->h, m->w, 4, 4, 0, 1, m->t_kv);
+    ops_transpose(o, m->t_q, m->t_qn, nimg, D, na);
+    ops_transpose(o, m->t_kv, m->t_kvn, nimg, D, na);
+    ops_layernorm(o, rows, D, m->t_qn, m->t_qn, a->norm_g, a->norm_b, EPS_LN,
                   ACT_NONE, 0);
-    ops_layernorm(o, na, D, m->t_kvn, m->t_kvn, a->norm_g, a->norm_b, EPS_LN,
-                  ACT_NONE, 0);
-    ops_linear(o, na, D, D, m->t_qn, 0, a->wq, NULL, m->t_Q, 0, ACT_NONE, 0, 0);
-    ops_linear(o, na, D, D, m->t_kvn, 0, a->wk, NULL, m->t_K, 0, ACT_NONE, 0,
+    ops_layernorm(o, rows, D, m->t_kvn, m->t_kvn, a->norm_g, a->norm_b,
+                  EPS_LN, ACT_NONE, 0);
+    ops_linear(o, rows, D, D, m->t_qn, 0, a->wq, NULL, m->t_Q, 0, ACT_NONE, 0,
                0);
-    ops_linear(o, na, D, D, m->t_kvn, 0, a->wv, NULL, m->t_V, 0, ACT_NONE, 0,
-               0);
+    ops_linear(o, rows, D, D, m->t_kvn, 0, a->wk, NULL, m->t_K, 0, ACT_NONE,
+               0, 0);
+    ops_linear(o, rows, D, D, m->t_kvn, 0, a->wv, NULL, m->t_V, 0, ACT_NONE,
+               0, 0);
     if (use_rope) {
-        ops_rope(o, m->t_Q, 0, D, na, 1, D, na, m->rope, 1);
-        ops_rope(o, m->t_K, 0, D, na, 1, D, na, m->rope, 1);
+        /* Row r takes table row r % na: the same positions per image. */
+        ops_rope(o, m->t_Q, 0, D, rows, 1, D, na, m->rope, 1);
+        ops_rope(o, m->t_K, 0, D, rows, 1, D, na, m->rope, 1);
     }
-    ops_attention(o, ops_mat(m->t_Q, 0, D), ops_mat(m->t_K, 0, D),
-                  ops_mat(m->t_V, 0, D), ops_mat(m->t_O, 0, D), na, na, HEADS,
-                  hd, 1.0f / sqrtf((float)hd), NULL);
-    ops_linear(o, na, D, D, m->t_O, 0, a->wo, NULL, m->t_Q, 0, ACT_NONE, 0, 0);
-    ops_transpose(o, m->t_Q, m->t_O2, 1, na, D);
-    copyf(m, X, 0, m->t_cat, 0, (size_t)D * n);
-    ops_resize(o, m->t_O2, D, m->ah, m->aw, m->t_cat, m->h, m->w, D, 0, 4.0f);
-    ops_transpose(o, m->t_cat, m->t_tok, 1, 2 * D, n);
-    ops_linear(o, n, 2 * D, MLP, m->t_tok, 0, a->fc1, NULL, m->t_h1, 0,
-               ACT_LEAKY, LEAKY, 0);
-    ops_linear(o, n, MLP, D, m->t_h1, 0, a->fc2, NULL, m->t_h2, 0, ACT_NONE, 0,
+    for (int i = 0; i < nimg; i++) {
+        const long off = (long)i * na * D;
+
+        ops_attention(o, ops_mat(m->t_Q, off, D), ops_mat(m->t_K, off, D),
+                      ops_mat(m->t_V, off, D), ops_mat(m->t_O, off, D), na, na,
+                      HEADS, hd, 1.0f / sqrtf((float)hd), NULL);
+    }
+    ops_linear(o, rows, D, D, m->t_O, 0, a->wo, NULL, m->t_Q, 0, ACT_NONE, 0,
                0);
-    ops_layernorm(o, n, D, m->t_h2, m->t_h2, a->mlp_g, a->mlp_b, EPS_LN,
-                  ACT_NONE, 0);
-    ops_transpose(o, m->t_h2, m->t_cat, 1, n, D);
-    ops_axpby(o, X, X, 1.0f, m->t_cat, 1.0f, (long)D * n, (long)D * n);
+    ops_transpose(o, m->t_Q, m->t_O2, nimg, na, D);
+    for (int i = 0; i < nimg; i++) {
+        copyf(m, X, (size_t)i * D * n, m->t_cat, (size_t)i * 2 * D * n,
+              (size_t)D * n);
+        ops_resize(o, m->t_O2v[i], D, m->ah, m->aw, m->t_cat, m->h, m->w,
+                   (2 * i + 1) * D, 0, 4.0f);
+    }
+    /* h1 (MLP x n) = leaky(fc1 (MLP x 2D) * cat (2D x n)), per image. */
+    ops_gemm(o, MLP, n, 2 * D, ops_mat(a->fc1, 0, 2 * D),
+             ops_bmat(m->t_cat, 0, n, 2L * D * n, 0), 0,
+             ops_bmat(m->t_h1, 0, n, (long)MLP * n, 0), nimg, 1, NULL, 1,
+             NULL, 0, 1.0f, ACT_LEAKY, LEAKY);
+    /* h2 (D x n) = fc2 (D x MLP) * h1. */
+    ops_gemm(o, D, n, MLP, ops_mat(a->fc2, 0, MLP),
+             ops_bmat(m->t_h1, 0, n, (long)MLP * n, 0), 0,
+             ops_bmat(m->t_h2, 0, n, (long)D * n, 0), nimg, 1, NULL, 1, NULL,
+             0, 1.0f, ACT_NONE, 0);
+    eloftr_ln_residual(o, m->t_h2, nimg, D, n, a->mlp_g, a->mlp_b, EPS_LN, X);
 }
 
 /* eloftr.c:451-463: image 1's cross attention sees image 0's features
- * already updated by this layer. */
+ * already updated by this layer. The two self-attention blocks of a layer
+ * are independent and run as one. */
 static void transformer(struct eloftr_model *m)
 {
     for (int l = 0; l < ELOFTR_LAYERS; l++) {
-        agg_attn(m, &m->self_attn[l], m->x[0], m->x[0], 1);
-        agg_attn(m, &m->self_attn[l], m->x[1], m->x[1], 1);
-        agg_attn(m, &m->cross_attn[l], m->x[0], m->x[1], 0);
-        agg_attn(m, &m->cross_attn[l], m->x[1], m->x[0], 0);
+        agg_attn(m, &m->self_attn[l], m->xp, m->xp, 2, 1);
+        agg_attn(m, &m->cross_attn[l], m->x[0], m->x[1], 1, 0);
+        agg_attn(m, &m->cross_attn[l], m->x[1], m->x[0], 1, 0);
     }
 }
 
@@ -658,7 +693,8 @@ extern "C" void eloftr_free(struct eloftr_model *m)
         &m->x[1],    &m->fine[0], &m->fine[1], &m->img,   &m->s_a,
         &m->s_b,     &m->f1p,     &m->f2p,     &m->xp,    &m->finep,
         &m->t_q,     &m->t_kv,    &m->t_qn,    &m->t_kvn,
-        &m->t_Q,     &m->t_K,     &m->t_V,     &m->t_O,   &m->t_O2,
+        &m->t_Q,     &m->t_K,     &m->t_V,     &m->t_O,   &m->t_O2v[0],
+        &m->t_O2v[1], &m->t_O2,
         &m->t_cat,   &m->t_tok,   &m->t_h1,    &m->t_h2,  &m->rope,
         &m->s_blk,   &m->row_lse, &m->col_m,   &m->col_s, &m->row_max,
         &m->row_arg, &m->col_max, &m->col_arg, &m->fu_a,  &m->fu_b,

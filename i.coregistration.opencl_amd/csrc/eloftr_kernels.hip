@@ -533,3 +533,84 @@ extern "C" void eloftr_fine(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
     launch_check(op);
     ICOREG_API_END
 }
+
+/* ---- MLP output LayerNorm + residual on channel-major maps -------------- */
+
+/* X[b][c][j] += LayerNorm over c of M[b][c][j] (gain g, bias bt): the end
+ * of an aggregated-attention block (eloftr.c:445-448: LayerNorm of the
+ * MLP output per token, then x + message), on channel-major maps so that
+ * neither operand is transposed. A block takes 64 tokens, one per lane;
+ * its 4 waves split the C <= 256 channels, each lane holding its token's
+ * share in registers, so M is read once; the per-token sums are combined
+ * across the waves in LDS. Reads of one channel row are 256 contiguous
+ * bytes per wave. */
+#define LNR_MAXC 256
+__global__ void __launch_bounds__(256)
+    chan_ln_add_kernel(const float *__restrict__ Mm, float *__restrict__ X,
+                       const float *__restrict__ g,
+                       const float *__restrict__ bt, int C, int n, float eps)
+{
+    constexpr int CPW = LNR_MAXC / 4;
+    __shared__ float part[2][4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + lane;
+    const int cw = (C + 3) / 4, c0 = wave * cw;
+    const int nc = max(0, min(cw, C - c0));
+    const long long base = (long long)blockIdx.y * C * n;
+    const bool on = j < n;
+    float v[CPW];
+    float s = 0.0f, mean, r;
+
+#pragma unroll
+    for (int k = 0; k < CPW; k++) {
+        v[k] = on && k < nc ? Mm[base + (long long)(c0 + k) * n + j] : 0.0f;
+        s += v[k];
+    }
+    part[0][wave][lane] = s;
+    __syncthreads();
+    mean = (part[0][0][lane] + part[0][1][lane] + part[0][2][lane] +
+            part[0][3][lane]) / C;
+    s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < CPW; k++) {
+        const float d = v[k] - mean;
+
+        if (k < nc)
+            s = fmaf(d, d, s);
+    }
+    part[1][wave][lane] = s;
+    __syncthreads();
+    r = 1.0f / sqrtf((part[1][0][lane] + part[1][1][lane] + part[1][2][lane] +
+                      part[1][3][lane]) / C + eps);
+    if (!on)
+        return;
+#pragma unroll
+    for (int k = 0; k < CPW; k++) {
+        if (k < nc) {
+            const int c = c0 + k;
+            float u = (v[k] - mean) * r;
+
+            u = u * g[c] + bt[c];
+            X[base + (long long)c * n + j] += u;
+        }
+    }
+}
+
+void eloftr_ln_residual(struct ops *o, cl_mem M, int nb, int C, int n,
+                        cl_mem g, cl_mem b, float eps, cl_mem X)
+{
+    const char *op = "eloftr_ln_residual";
+
+    if (nb < 1 || nb > 65535 || C < 1 || C > LNR_MAXC || n < 1)
+        icoreg_fatal("%s: invalid sizes nb=%d C=%d n=%d", op, nb, C, n);
+    count32((long long)C * n, "channel map");
+    need_floats(M, 0, (long long)nb * C * n, op, "M");
+    need_floats(X, 0, (long long)nb * C * n, op, "X");
+    need_floats(g, 0, C, op, "g");
+    need_floats(b, 0, C, op, "b");
+    prof_scope ps(o->ocl, "ln_residual");
+    hipLaunchKernelGGL(chan_ln_add_kernel, dim3((n + 63) / 64, nb),
+                       dim3(256), 0, stream_of(o->ocl), cfptr(M), fptr(X),
+                       cfptr(g), cfptr(b), C, n, eps);
+    launch_check(op);
+}

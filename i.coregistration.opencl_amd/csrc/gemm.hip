@@ -14,7 +14,13 @@
  *  - BK = 16 slices of A and B staged through LDS, double-buffered: the
  *    next slice is fetched from HBM/L2 into registers (16-byte loads
  *    when rows are aligned) while the matrix cores work on the current
- *    one, then written to the other LDS buffer; one barrier per slice;
+ *    one, then written to the other LDS buffer two MFMA steps before
+ *    the slice ends; one barrier per slice;
+ *  - operands are read through buffer windows over the tile's rows, so
+ *    rows and columns past the matrix edge read 0 from the window's
+ *    range check instead of a branch per load, and the per-thread
+ *    offsets are computed once;
+ *  - LDS operand reads run two MFMA steps ahead of their use;
  *  - LDS holds both operands k-major ([k][m], [k][n]) so that the 32
  *    lanes of an MFMA operand read 32 consecutive floats;
  *  - the B operand of a convolution is gathered from the (C, H, W) input
@@ -31,26 +37,51 @@
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-#define GEMM_BK 16
 #define GEMM_PAD 4
 
-/* Four floats of a row at column k (k, k+1, k+2, k+3 < K), zero past K;
- * one 16-byte load when allowed and the whole vector is inside. */
-template <bool VEC>
-__device__ __forceinline__ float4 load_row4(const float *p, int k, int K)
-{
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+/* Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data. */
+#define GEMM_RSRC_FLAGS 0x00020000
 
-    if (VEC && k + 3 < K)
-        return *(const float4 *)p;
-    if (k < K)
-        v.x = p[0];
-    if (k + 1 < K)
-        v.y = p[1];
-    if (k + 2 < K)
-        v.z = p[2];
-    if (k + 3 < K)
-        v.w = p[3];
+/* Buffer window of `bytes` bytes from p: loads at byte offsets at or past
+ * its end return 0. */
+static __device__ __forceinline__ __amdgpu_buffer_rsrc_t
+gemm_rsrc(const float *p, long long bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0,
+                                             (int)(unsigned)bytes,
+                                             GEMM_RSRC_FLAGS);
+}
+
+/* Four consecutive floats at byte offset off of window r: one 16-byte
+ * load (VEC: the four are either all inside the window or all past its
+ * end), else four 4-byte loads. */
+template <bool VEC>
+__device__ __forceinline__ float4 gemm_load4(__amdgpu_buffer_rsrc_t r,
+                                             unsigned off)
+{
+    if (VEC)
+        return __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+    float4 v;
+
+    v.x = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+    v.y = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off + 4, 0, 0));
+    v.z = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off + 8, 0, 0));
+    v.w = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off + 12, 0, 0));
+    return v;
+}
+
+/* Components i of v with lo + i >= hi set to 0. */
+__device__ __forceinline__ float4 mask4(float4 v, int lo, int hi)
+{
+    v.x = lo < hi ? v.x : 0.0f;
+    v.y = lo + 1 < hi ? v.y : 0.0f;
+    v.z = lo + 2 < hi ? v.z : 0.0f;
+    v.w = lo + 3 < hi ? v.w : 0.0f;
     return v;
 }
 
@@ -64,15 +95,18 @@ __device__ __forceinline__ int xcd_tile(int L, int T)
     return (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + idx;
 }
 
-template <int BM, int BN, int MODE, bool VA, bool VB>
+template <int BM, int BN, int BK, int MODE, bool VA, bool VB>
 __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
 {
-    constexpr int BK = GEMM_BK;
     constexpr int LDSA = BM + GEMM_PAD, LDSB = BN + GEMM_PAD;
     constexpr int TM = BM / 64, TN = BN / 64;
+    constexpr int KQ = BK / 4;            /* float4 per row of a slice */
     constexpr int A4 = BM * BK / 4 / 256; /* float4 loads of A per thread */
     constexpr int B4 = BN * BK / 4 / 256; /* dense B */
     constexpr int BE = BN * BK / 256;     /* gathered B elements */
+    constexpr int NS = BK / 2;            /* MFMA steps per slice */
+    constexpr int PF = 2;                 /* LDS reads run PF steps ahead */
+    static_assert(A4 >= 1 && BN * BK % 1024 == 0, "tile shape");
     __shared__ float As[2][BK * LDSA];
     __shared__ float Bs[2][BK * LDSB];
 
@@ -86,10 +120,42 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
     const float *A = g.A + b0 * g.sa0 + b1 * g.sa1;
     const float *B = g.B + b0 * g.sb0 + b1 * g.sb1;
     const int M = g.M, N = g.N, K = g.K;
+    const long long lda = g.lda, ldb = g.ldb;
+    /* Rows of A and columns of B inside the matrix for this tile. */
+    const int rows_a = min(BM, M - m0), cols_b = min(BN, N - n0);
+    const float *Ablk = A + m0 * lda;
 
     float4 ra[A4], rb[B4 > 0 ? B4 : 1];
     float rg[MODE == GEMM_B_CONV ? BE : 1];
+    unsigned aoff[A4], boff[B4 > 0 ? B4 : 1];
     floatx16 acc[TM][TN];
+
+    /* Byte offsets inside the windows, the same for every slice: A rows
+     * past rows_a (and B rows past cols_b for B given N x K) land past
+     * the window's end and read 0. */
+#pragma unroll
+    for (int e = 0; e < A4; e++) {
+        const int q = tid + 256 * e, row = q / KQ, kq = (q % KQ) * 4;
+
+        aoff[e] = (unsigned)((row * lda + kq) * 4);
+    }
+    if (MODE == GEMM_B_NK) {
+#pragma unroll
+        for (int e = 0; e < B4; e++) {
+            const int q = tid + 256 * e, row = q / KQ, kq = (q % KQ) * 4;
+
+            boff[e] = (unsigned)((row * ldb + kq) * 4);
+        }
+    }
+    else if (MODE == GEMM_B_KN) {
+#pragma unroll
+        for (int e = 0; e < B4; e++) {
+            const int q = tid + 256 * e, kk = q / (BN / 4);
+            const int nq = (q % (BN / 4)) * 4;
+
+            boff[e] = (unsigned)((kk * ldb + nq) * 4);
+        }
+    }
 
     /* Convolution gather: this thread's output column is fixed. */
     const int cn = tid % BN, ck0 = tid / BN;
@@ -109,37 +175,38 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
                 acc[i][j][r] = 0.0f;
 
     auto fetch = [&](int k0) {
-#pragma unroll
-        for (int e = 0; e < A4; e++) {
-            const int q = tid + 256 * e, row = q >> 2, kq = (q & 3) * 4;
-            const int gm = m0 + row;
+        const bool ktail = k0 + BK > K;
+        const __amdgpu_buffer_rsrc_t wa =
+            gemm_rsrc(Ablk + k0, ((rows_a - 1) * lda + K - k0) * 4);
 
-            ra[e] = gm < M ? load_row4<VA>(A + (long long)gm * g.lda + k0 + kq,
-                                           k0 + kq, K)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+#pragma unroll
+        for (int e = 0; e < A4; e++)
+            ra[e] = gemm_load4<VA>(wa, aoff[e]);
         if (MODE == GEMM_B_NK) {
-#pragma unroll
-            for (int e = 0; e < B4; e++) {
-                const int q = tid + 256 * e, row = q >> 2, kq = (q & 3) * 4;
-                const int gn = n0 + row;
+            const __amdgpu_buffer_rsrc_t wb = gemm_rsrc(
+                B + n0 * ldb + k0, ((cols_b - 1) * ldb + K - k0) * 4);
 
-                rb[e] = gn < N ? load_row4<VB>(B + (long long)gn * g.ldb + k0 +
-                                                   kq,
-                                               k0 + kq, K)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+#pragma unroll
+            for (int e = 0; e < B4; e++)
+                rb[e] = gemm_load4<VB>(wb, boff[e]);
         }
         else if (MODE == GEMM_B_KN) {
-#pragma unroll
-            for (int e = 0; e < B4; e++) {
-                const int q = tid + 256 * e, kk = q / (BN / 4);
-                const int nq = (q % (BN / 4)) * 4, gk = k0 + kk;
+            const int kv = min(BK, K - k0);
+            const __amdgpu_buffer_rsrc_t wb = gemm_rsrc(
+                B + k0 * ldb + n0, ((kv - 1) * ldb + cols_b) * 4);
 
-                rb[e] = gk < K ? load_row4<VB>(B + (long long)gk * g.ldb + n0 +
-                                                   nq,
-                                               n0 + nq, N)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int e = 0; e < B4; e++)
+                rb[e] = gemm_load4<VB>(wb, boff[e]);
+            if (cols_b < BN) {
+                /* Columns past N of rows before the window's last read
+                 * the next row: zero them. */
+#pragma unroll
+                for (int e = 0; e < B4; e++) {
+                    const int q = tid + 256 * e, nq = (q % (BN / 4)) * 4;
+
+                    rb[e] = mask4(rb[e], nq, cols_b);
+                }
             }
         }
         else {
@@ -166,6 +233,24 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
                 rg[e] = v;
             }
         }
+        if (ktail) {
+            /* Last slice of a K that BK does not divide: columns past K
+             * of rows before the window's last read the next row. */
+#pragma unroll
+            for (int e = 0; e < A4; e++) {
+                const int q = tid + 256 * e, kq = (q % KQ) * 4;
+
+                ra[e] = mask4(ra[e], k0 + kq, K);
+            }
+            if (MODE == GEMM_B_NK) {
+#pragma unroll
+                for (int e = 0; e < B4; e++) {
+                    const int q = tid + 256 * e, kq = (q % KQ) * 4;
+
+                    rb[e] = mask4(rb[e], k0 + kq, K);
+                }
+            }
+        }
     };
 
     auto stash = [&](int buf) {
@@ -173,7 +258,7 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
 
 #pragma unroll
         for (int e = 0; e < A4; e++) {
-            const int q = tid + 256 * e, row = q >> 2, kq = (q & 3) * 4;
+            const int q = tid + 256 * e, row = q / KQ, kq = (q % KQ) * 4;
 
             as[(kq + 0) * LDSA + row] = ra[e].x;
             as[(kq + 1) * LDSA + row] = ra[e].y;
@@ -183,7 +268,7 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
         if (MODE == GEMM_B_NK) {
 #pragma unroll
             for (int e = 0; e < B4; e++) {
-                const int q = tid + 256 * e, row = q >> 2, kq = (q & 3) * 4;
+                const int q = tid + 256 * e, row = q / KQ, kq = (q % KQ) * 4;
 
                 bs[(kq + 0) * LDSB + row] = rb[e].x;
                 bs[(kq + 1) * LDSB + row] = rb[e].y;
@@ -223,11 +308,8 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
             const float *as = As[cur] + wm * (BM / 2) + (lane & 31);
             const float *bs = Bs[cur] + wn * (BN / 2) + (lane & 31);
             const int kh = lane >> 5;
-
-#pragma unroll
-            for (int ks = 0; ks < BK / 2; ks++) {
+            auto operands = [&](int ks, float *a, float *b) {
                 const int kr = 2 * ks + kh;
-                float a[TM], b[TN];
 
 #pragma unroll
                 for (int i = 0; i < TM; i++)
@@ -235,16 +317,33 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
 #pragma unroll
                 for (int j = 0; j < TN; j++)
                     b[j] = bs[kr * LDSB + j * 32];
+            };
+            float a[PF + 1][TM], b[PF + 1][TN];
+
+            /* The scheduling barriers keep the LDS reads of step ks + PF
+             * ahead of the MFMAs of step ks; the next slice goes to the
+             * other LDS buffer two steps before the end. */
+#pragma unroll
+            for (int ks = 0; ks < PF; ks++)
+                operands(ks, a[ks], b[ks]);
+#pragma unroll
+            for (int ks = 0; ks < NS; ks++) {
+                constexpr int NB = PF + 1;
+
+                if (ks + PF < NS)
+                    operands(ks + PF, a[(ks + PF) % NB], b[(ks + PF) % NB]);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
                     for (int j = 0; j < TN; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                            a[i], b[j], acc[i][j], 0, 0, 0);
+                            a[ks % NB][i], b[ks % NB][j], acc[i][j], 0, 0, 0);
+                if (ks == NS - 2 && kt + 1 < nk)
+                    stash(cur ^ 1);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if (kt + 1 < nk)
-            stash(cur ^ 1);
         __syncthreads();
     }
 
@@ -286,29 +385,30 @@ template <int BM, int BN, int MODE>
 static void launch_mode(const gemm_args &g, int nb, bool va, bool vb,
                         hipStream_t s)
 {
+    constexpr int BK = 16;
     const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
     dim3 grid(tiles, nb), block(256);
 
     if (MODE == GEMM_B_CONV) {
         if (va)
-            hipLaunchKernelGGL((gemm_mfma<BM, BN, MODE, true, false>), grid,
+            hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, true, false>), grid,
                                block, 0, s, g);
         else
-            hipLaunchKernelGGL((gemm_mfma<BM, BN, MODE, false, false>), grid,
+            hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, false, false>), grid,
                                block, 0, s, g);
         return;
     }
     if (va && vb)
-        hipLaunchKernelGGL((gemm_mfma<BM, BN, MODE, true, true>), grid, block, 0,
+        hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, true, true>), grid, block, 0,
                            s, g);
     else if (va)
-        hipLaunchKernelGGL((gemm_mfma<BM, BN, MODE, true, false>), grid, block,
+        hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, true, false>), grid, block,
                            0, s, g);
     else if (vb)
-        hipLaunchKernelGGL((gemm_mfma<BM, BN, MODE, false, true>), grid, block,
+        hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, false, true>), grid, block,
                            0, s, g);
     else
-        hipLaunchKernelGGL((gemm_mfma<BM, BN, MODE, false, false>), grid, block,
+        hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, false, false>), grid, block,
                            0, s, g);
 }
 
@@ -329,9 +429,29 @@ static void launch_tile(const gemm_args &g, int bmode, int nb, bool va,
     }
 }
 
+bool gemm_shape_ok(const gemm_args &g, int bmode)
+{
+    /* Buffer windows span at most 128 rows of an operand (32-bit byte
+     * offsets below 2 GiB), and rows must not overlap. */
+    const long long lim = (1LL << 31) / (4 * 128);
+
+    if (g.lda < g.K || g.lda >= lim)
+        return false;
+    if (bmode == GEMM_B_NK)
+        return g.ldb >= g.K && g.ldb < lim;
+    if (bmode == GEMM_B_KN)
+        return g.ldb >= g.N && g.ldb < lim;
+    return true;
+}
+
 void gemm_launch(const gemm_args &g, int bmode, int nb, int bm, int bn,
                  bool va, bool vb, hipStream_t s)
 {
+    /* 16-byte loads need every four-float group wholly inside or wholly
+     * past the matrix edge: K (A, and B given N x K) or N (B given
+     * K x N) a multiple of 4. */
+    va = va && g.K % 4 == 0;
+    vb = vb && (bmode == GEMM_B_KN ? g.N % 4 == 0 : g.K % 4 == 0);
     if (bm == 128 && bn == 128)
         launch_tile<128, 128>(g, bmode, nb, va, vb, s);
     else if (bm == 64 && bn == 128)

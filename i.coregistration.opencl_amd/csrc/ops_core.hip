@@ -195,6 +195,10 @@ extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
     g.act = act;
     g.slope = slope;
     pick_tile(M, N, nb, o->ocl->cu_count, &bm, &bn);
+    if (!gemm_shape_ok(g, transb ? GEMM_B_NK : GEMM_B_KN))
+        icoreg_fatal("%s: leading dimensions lda=%d ldb=%d not supported "
+                     "(each at least its row length, below 4 Mi floats)",
+                     op, A.ld, B.ld);
     {
         prof_scope ps(o->ocl, "gemm");
 
@@ -399,6 +403,8 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
         a.rstd = cfptr(rstd);
         a.gate = mean ? cfptr(alpha) : nullptr;
         pick_tile(K, Ho * Wo, nb, o->ocl->cu_count, &bm, &bn);
+        if (!gemm_shape_ok(a, GEMM_B_CONV))
+            icoreg_fatal("%s: reduction of %d too long", op, kred);
         prof_scope ps(o->ocl, "conv_igemm");
         gemm_launch(a, GEMM_B_CONV, nb, bm, bn,
                     kred % 4 == 0 && aligned16(w->ptr), false,

@@ -18,22 +18,23 @@ using namespace icoreg;
 
 /* ---- bilinear resize --------------------------------------------------- */
 
+/* One thread per output pixel; grid y runs over the channels, so the
+ * pixel's row and column come from one 32-bit division. */
 __global__ void __launch_bounds__(256)
     resize_kernel(const float *__restrict__ in, int h, int w,
                   float *__restrict__ out, int H, int W, int coff, int align,
-                  float sy, float sx, int C)
+                  float sy, float sx)
 {
-    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-    const long long total = (long long)C * H * W;
-    int x, y, c, x0, y0, x1, y1;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    const int c = blockIdx.y;
+    int x, y, x0, y0, x1, y1;
     float ux, uy, fx, fy;
     const float *p;
 
-    if (idx >= total)
+    if (idx >= H * W)
         return;
-    x = (int)(idx % W);
-    y = (int)((idx / W) % H);
-    c = (int)(idx / ((long long)W * H));
+    y = idx / W;
+    x = idx - y * W;
     if (align) {
         ux = W > 1 ? (float)x * (float)(w - 1) / (float)(W - 1) : 0.0f;
         uy = H > 1 ? (float)y * (float)(h - 1) / (float)(H - 1) : 0.0f;
@@ -72,10 +73,13 @@ extern "C" void ops_resize(struct ops *o, cl_mem in, int C, int h, int w,
     count32((long long)(C + coff) * H * W, "resize output");
     need_floats(in, 0, (long long)C * h * w, op, "in");
     need_floats(out, (long long)coff * H * W, total, op, "out");
+    if (C > 65535)
+        icoreg_fatal("%s: %d channels (at most 65535)", op, C);
     prof_scope ps(o->ocl, "resize_bilinear");
-    hipLaunchKernelGGL(resize_kernel, dim3((unsigned)((total + 255) / 256)),
+    hipLaunchKernelGGL(resize_kernel,
+                       dim3((unsigned)((H * W + 255) / 256), (unsigned)C),
                        dim3(256), 0, stream_of(o->ocl), cfptr(in), h, w,
-                       fptr(out), H, W, coff, align_corners, sy, sx, C);
+                       fptr(out), H, W, coff, align_corners, sy, sx);
     launch_check("resize_bilinear");
     ICOREG_API_END
 }
