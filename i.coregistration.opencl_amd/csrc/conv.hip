@@ -6,9 +6,9 @@
  * i.coregistration.opencl): out = act(W * in + bias), optional input
  * normalisation and PReLU gate before the zero padding.
  *
- * A block computes 128 output pixels (a TH x TW tile of one image, 4 x 32
- * or 8 x 16, whichever wastes less of the image) for BM output channels
- * as an implicit GEMM (M = channels, N = pixels, K = C k k). The K loop
+ * A block computes 64 or 128 output pixels (a TH x TW tile of one image,
+ * 32 or 16 wide, whichever wastes less of the image) for BM output
+ * channels as an implicit GEMM (M = channels, N = pixels, K = C k k). The K loop
  * walks CC input channels at a time:
  *  - the weights of the slice (BM x CC k k, contiguous per output
  *    channel) go to LDS k-major;
@@ -56,12 +56,13 @@ static __device__ __forceinline__ float conv_load(__amdgpu_buffer_rsrc_t r,
         float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
 }
 
-/* KS x KS taps, stride ST, BM output channels and a 128 / TW x TW pixel
- * tile per block, CC input channels per K slice. */
-template <int KS, int ST, int BM, int TW, int CC>
+/* KS x KS taps, stride ST, BM output channels and a TH x TW tile of
+ * 64 NJ pixels per block (each wave NJ 32-pixel MFMA tiles), CC input
+ * channels per K slice. */
+template <int KS, int ST, int BM, int TW, int CC, int NJ>
 __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
 {
-    constexpr int TH = 128 / TW;
+    constexpr int TH = 64 * NJ / TW;
     constexpr int KK = KS * KS;
     constexpr int KT = CC * KK;
     constexpr int PH = (TH - 1) * ST + KS;
@@ -93,12 +94,12 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
     unsigned woff[NA], poff[NP];
     int lda_[NA], ldp[NP];
     float ra[NA], rp[NP];
-    floatx16 acc[TM][2];
+    floatx16 acc[TM][NJ];
 
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < NJ; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++)
                 acc[i][j][r] = 0.0f;
@@ -175,7 +176,7 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
 
     const int nk = (C + CC - 1) / CC;
     /* This lane's first pixel: row r of the tile, column x. */
-    const int pr = (wn * 64 + col) / TW, px0 = col % TW;
+    const int pr = (wn * 32 * NJ + col) / TW, px0 = col % TW;
     const int pbase = pr * ST * PWP + px0;
 
     fetch(0);
@@ -206,13 +207,13 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
                 for (int i = 0; i < TM; i++)
                     av[i] = as[ao + i * 32];
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                for (int j = 0; j < NJ; j++)
                     bv[j] = ps[po + j * RJ * ST * PWP];
             };
             constexpr int NS = KT / 2;
             /* LDS reads run PF steps ahead of the MFMAs that use them. */
             constexpr int PF = 2;
-            float av[PF + 1][TM], bv[PF + 1][2];
+            float av[PF + 1][TM], bv[PF + 1][NJ];
 
             /* The scheduling barriers keep the reads of step s + PF ahead
              * of the MFMAs of step s, so their latency hides behind the
@@ -231,7 +232,7 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
 #pragma unroll
                 for (int i = 0; i < TM; i++)
 #pragma unroll
-                    for (int j = 0; j < 2; j++)
+                    for (int j = 0; j < NJ; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
                             av[s % NB][i], bv[s % NB][j], acc[i][j], 0, 0,
                             0);
@@ -247,7 +248,7 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
         float *out = a.out + (long long)blockIdx.z * a.out_stride;
 
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NJ; j++) {
             const int oy = oy0 + pr + j * RJ, ox = ox0 + px0;
 
             if (oy >= a.Ho || ox >= a.Wo)
@@ -286,52 +287,57 @@ bool conv_direct_fits(long long in_floats, long long w_floats)
     return in_floats * 4 < 0x80000000LL && w_floats * 4 < 0x80000000LL;
 }
 
-/* Padded output area of a TW-wide tiling. */
-static long long tiled_area(int Ho, int Wo, int tw)
+/* Padded output area of a th x tw tiling. */
+static long long tiled_area(int Ho, int Wo, int th, int tw)
 {
-    const int th = 128 / tw;
-
     return (long long)((Ho + th - 1) / th) * th * ((Wo + tw - 1) / tw) * tw;
 }
 
-template <int KS, int ST, int BM, int TW>
-static void launch_cfg(const conv_args &a, int tiles, int nb, hipStream_t s)
+template <int KS, int ST, int BM, int TW, int NJ>
+static void launch_cfg(const conv_args &a, int nb, hipStream_t s)
 {
     /* K = 100 (5 x 5) or 36 (3 x 3) per slice at 64 channels per block,
      * 50 at 128. */
     constexpr int CC = BM == 128 ? 2 : 4;
+    constexpr int TH = 64 * NJ / TW;
+    const int tiles = ((a.Wo + TW - 1) / TW) * ((a.Ho + TH - 1) / TH);
 
-    hipLaunchKernelGGL((conv_mfma<KS, ST, BM, TW, CC>),
+    hipLaunchKernelGGL((conv_mfma<KS, ST, BM, TW, CC, NJ>),
                        dim3(tiles, (a.K + BM - 1) / BM, nb), dim3(256), 0, s,
                        a);
 }
 
-template <int KS, int ST, int TW>
-static void launch_tw(const conv_args &a, int nb, int cus, hipStream_t s)
-{
-    const int tiles = ((a.Wo + TW - 1) / TW) * ((a.Ho + 128 / TW - 1) / (128 / TW));
-
-    /* 3 x 3: 64 output channels per block at every size measured (the
-     * smaller block keeps more waves per CU in flight). 5 x 5: 128
-     * channels unless that grid would leave CUs with fewer than two
-     * blocks each. */
-    if constexpr (KS == 5) {
-        if (a.K > 64 &&
-            (long long)tiles * ((a.K + 127) / 128) * nb >= 2LL * cus) {
-            launch_cfg<KS, ST, 128, TW>(a, tiles, nb, s);
-            return;
-        }
-    }
-    launch_cfg<KS, ST, 64, TW>(a, tiles, nb, s);
-}
-
+/* 3 x 3: blocks of 64 channels x 64 pixels, the fastest of the 64 / 128
+ * channel x 64 / 128 pixel blocks at every ELoFTR layer measured (the
+ * small block keeps the most waves per CU in flight). 5 x 5: 128 pixels,
+ * and 128 channels unless that grid would leave CUs with fewer than two
+ * blocks each. The tile is 2 x 32 / 4 x 32 or 4 x 16 / 8 x 16 pixels,
+ * whichever pads the image less. */
 template <int KS, int ST>
 static void launch_ks(const conv_args &a, int nb, int cus, hipStream_t s)
 {
-    if (tiled_area(a.Ho, a.Wo, 16) < tiled_area(a.Ho, a.Wo, 32))
-        launch_tw<KS, ST, 16>(a, nb, cus, s);
+    constexpr int NJ = KS == 3 ? 1 : 2;
+    constexpr int P = 64 * NJ;
+    const bool narrow = tiled_area(a.Ho, a.Wo, P / 16, 16) <
+                        tiled_area(a.Ho, a.Wo, P / 32, 32);
+
+    if constexpr (KS == 5) {
+        const long long tiles =
+            narrow ? (long long)((a.Wo + 15) / 16) * ((a.Ho + 7) / 8)
+                   : (long long)((a.Wo + 31) / 32) * ((a.Ho + 3) / 4);
+
+        if (a.K > 64 && tiles * ((a.K + 127) / 128) * nb >= 2LL * cus) {
+            if (narrow)
+                launch_cfg<KS, ST, 128, 16, NJ>(a, nb, s);
+            else
+                launch_cfg<KS, ST, 128, 32, NJ>(a, nb, s);
+            return;
+        }
+    }
+    if (narrow)
+        launch_cfg<KS, ST, 64, 16, NJ>(a, nb, s);
     else
-        launch_tw<KS, ST, 32>(a, nb, cus, s);
+        launch_cfg<KS, ST, 64, 32, NJ>(a, nb, s);
 }
 
 void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,

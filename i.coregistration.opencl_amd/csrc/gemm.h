@@ -40,9 +40,9 @@ struct gemm_args {
  * row length and below 4 Mi floats. */
 bool gemm_shape_ok(const gemm_args &g, int bmode);
 
-/* Launch on stream s over nb batches. bm/bn: 128 or 64 (tile). va/vb:
- * 16-byte vector loads allowed for A / B (every row start aligned). */
-void gemm_launch(const gemm_args &g, int bmode, int nb, int bm, int bn,
-                 bool va, bool vb, hipStream_t s);
+/* Launch on stream s over nb batches. va/vb: 16-byte vector loads
+ * allowed for A / B (every row start aligned). */
+void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
+                 hipStream_t s);
 
 #endif /* ICOREG_GEMM_H */

@@ -119,29 +119,6 @@ static bool vec_ok(const struct opnd &x)
            x.s0 % 4 == 0 && x.s1 % 4 == 0;
 }
 
-/* Tile choice: the 128 x 128 tile when it still gives every CU a block,
- * else smaller tiles for more blocks. */
-static void pick_tile(int M, int N, int nb, int cus, int *bm, int *bn)
-{
-    long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128) * nb;
-    long long t64 = (long long)((M + 63) / 64) * ((N + 127) / 128) * nb;
-
-    if (M > 64 && t128 >= cus) {
-        *bm = 128;
-        *bn = 128;
-    }
-    else if (t64 >= cus || M <= 64) {
-        *bm = 64;
-        *bn = N > 64 ? 128 : 64;
-        if (*bn == 128 && t64 < cus)
-            *bn = 64;
-    }
-    else {
-        *bm = 64;
-        *bn = 64;
-    }
-}
-
 extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
                          struct opnd B, int transb, struct opnd C, int nb,
                          int nb1, cl_mem bias, int biasrow, cl_mem R, long roff,
@@ -150,7 +127,6 @@ extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
     ICOREG_API_BEGIN
     const char *op = "ops_gemm";
     gemm_args g;
-    int bm, bn;
 
     if (M < 0 || N < 0 || K < 0 || nb < 1 || nb1 < 1 || nb > 65535)
         icoreg_fatal("%s: invalid sizes M=%d N=%d K=%d nb=%d nb1=%d", op, M, N,
@@ -194,7 +170,6 @@ extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
     g.alpha = alpha;
     g.act = act;
     g.slope = slope;
-    pick_tile(M, N, nb, o->ocl->cu_count, &bm, &bn);
     if (!gemm_shape_ok(g, transb ? GEMM_B_NK : GEMM_B_KN))
         icoreg_fatal("%s: leading dimensions lda=%d ldb=%d not supported "
                      "(each at least its row length, below 4 Mi floats)",
@@ -202,7 +177,7 @@ extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
     {
         prof_scope ps(o->ocl, "gemm");
 
-        gemm_launch(g, transb ? GEMM_B_NK : GEMM_B_KN, nb, bm, bn, vec_ok(A),
+        gemm_launch(g, transb ? GEMM_B_NK : GEMM_B_KN, nb, vec_ok(A),
                     vec_ok(B), stream_of(o->ocl));
         launch_check("gemm");
     }
@@ -367,7 +342,7 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
     }
     if (g->groups == 1) {
         gemm_args a;
-        int bm, bn, kred = C * g->kh * g->kw;
+        int kred = C * g->kh * g->kw;
 
         count32((long long)kred * 128, "convolution reduction");
         memset(&a, 0, sizeof(a));
@@ -402,11 +377,10 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
         a.mean = cfptr(mean);
         a.rstd = cfptr(rstd);
         a.gate = mean ? cfptr(alpha) : nullptr;
-        pick_tile(K, Ho * Wo, nb, o->ocl->cu_count, &bm, &bn);
         if (!gemm_shape_ok(a, GEMM_B_CONV))
             icoreg_fatal("%s: reduction of %d too long", op, kred);
         prof_scope ps(o->ocl, "conv_igemm");
-        gemm_launch(a, GEMM_B_CONV, nb, bm, bn,
+        gemm_launch(a, GEMM_B_CONV, nb,
                     kred % 4 == 0 && aligned16(w->ptr), false,
                     stream_of(o->ocl));
         launch_check("conv_igemm");
