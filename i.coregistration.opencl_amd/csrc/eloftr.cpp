@@ -19,7 +19,10 @@
  *    MLP of every attention block runs on channel-major maps (products
  *    W * [x; message] instead of token-major linears between
  *    transposes, the MLP LayerNorm fused with the residual add): the
- *    same sums per output value, in another memory layout. */
+ *    same sums per output value, in another memory layout;
+ *  - k_proj and v_proj run as one product with their weights stacked;
+ *  - the fusion's "1 x 1 convolution + upsampled coarser level" sums are
+ *    the 1 x 1 products' residual inputs instead of separate adds. */
 
 #include <math.h>
 #include <stdio.h>
@@ -176,14 +179,31 @@ static void load_attn(struct eloftr_model *m, struct pth_file *pf, int layer,
     LD(norm_g, "aggregation.norm.weight", 1, v1);
     LD(norm_b, "aggregation.norm.bias", 1, v1);
     LD(wq, "attention.q_proj.weight", 2, sq);
-    LD(wk, "attention.k_proj.weight", 2, sq);
-    LD(wv, "attention.v_proj.weight", 2, sq);
     LD(wo, "attention.o_proj.weight", 2, sq);
     LD(fc1, "mlp.fc1.weight", 2, s1);
     LD(fc2, "mlp.fc2.weight", 2, s2);
     LD(mlp_g, "mlp.layer_norm.weight", 1, v1);
     LD(mlp_b, "mlp.layer_norm.bias", 1, v1);
 #undef LD
+    {
+        /* k_proj and v_proj stacked into one (512, 256) weight, so that
+         * keys and values come from one product with the shared input. */
+        const size_t dd = (size_t)ELOFTR_DIM * ELOFTR_DIM;
+        float *kv = (float *)malloc(2 * dd * sizeof(float)), *w;
+
+        if (!kv)
+            icoreg_fatal("ELoFTR: out of host memory");
+        snprintf(name, sizeof(name), "%s.attention.k_proj.weight", pre);
+        w = read_host(pf, name, 2, sq);
+        memcpy(kv, w, dd * sizeof(float));
+        free(w);
+        snprintf(name, sizeof(name), "%s.attention.v_proj.weight", pre);
+        w = read_host(pf, name, 2, sq);
+        memcpy(kv + dd, w, dd * sizeof(float));
+        free(w);
+        a->wkv = upload(m, kv, 2 * dd, "attention.kv_proj");
+        free(kv);
+    }
 }
 
 static void load_fusion(struct eloftr_model *m, struct pth_file *pf)
@@ -324,8 +344,7 @@ extern "C" void eloftr_alloc(struct eloftr_model *m, int H, int W)
     m->t_qn = walloc(m, 2 * ELOFTR_DIM * na, "tokens");
     m->t_kvn = walloc(m, 2 * ELOFTR_DIM * na, "tokens");
     m->t_Q = walloc(m, 2 * ELOFTR_DIM * na, "queries");
-    m->t_K = walloc(m, 2 * ELOFTR_DIM * na, "keys");
-    m->t_V = walloc(m, 2 * ELOFTR_DIM * na, "values");
+    m->t_KV = walloc(m, 4 * ELOFTR_DIM * na, "keys and values");
     m->t_O = walloc(m, 2 * ELOFTR_DIM * na, "attention");
     m->t_O2 = walloc(m, 2 * ELOFTR_DIM * na, "attention");
     for (int k = 0; k < 2; k++)
@@ -449,21 +468,22 @@ static void agg_attn(struct eloftr_model *m, const struct eloftr_attn *a,
                   EPS_LN, ACT_NONE, 0);
     ops_linear(o, rows, D, D, m->t_qn, 0, a->wq, NULL, m->t_Q, 0, ACT_NONE, 0,
                0);
-    ops_linear(o, rows, D, D, m->t_kvn, 0, a->wk, NULL, m->t_K, 0, ACT_NONE,
-               0, 0);
-    ops_linear(o, rows, D, D, m->t_kvn, 0, a->wv, NULL, m->t_V, 0, ACT_NONE,
-               0, 0);
+    /* Keys (columns 0..D-1) and values (D..2D-1) of t_KV in one
+     * product. */
+    ops_linear(o, rows, D, 2 * D, m->t_kvn, 0, a->wkv, NULL, m->t_KV, 0,
+               ACT_NONE, 0, 0);
     if (use_rope) {
         /* Row r takes table row r % na: the same positions per image. */
         ops_rope(o, m->t_Q, 0, D, rows, 1, D, na, m->rope, 1);
-        ops_rope(o, m->t_K, 0, D, rows, 1, D, na, m->rope, 1);
+        ops_rope(o, m->t_KV, 0, 2 * D, rows, 1, D, na, m->rope, 1);
     }
     for (int i = 0; i < nimg; i++) {
-        const long off = (long)i * na * D;
+        const long off = (long)i * na * D, kv = 2 * off;
 
-        ops_attention(o, ops_mat(m->t_Q, off, D), ops_mat(m->t_K, off, D),
-                      ops_mat(m->t_V, off, D), ops_mat(m->t_O, off, D), na, na,
-                      HEADS, hd, 1.0f / sqrtf((float)hd), NULL);
+        ops_attention(o, ops_mat(m->t_Q, off, D), ops_mat(m->t_KV, kv, 2 * D),
+                      ops_mat(m->t_KV, kv + D, 2 * D),
+                      ops_mat(m->t_O, off, D), na, na, HEADS, hd,
+                      1.0f / sqrtf((float)hd), NULL);
     }
     ops_linear(o, rows, D, D, m->t_O, 0, a->wo, NULL, m->t_Q, 0, ACT_NONE, 0,
                0);
@@ -556,13 +576,14 @@ static void coarse_match(struct eloftr_model *m)
 }
 
 /* 1 x 1 convolution of both images: W (K, C) times X (C, HW) per image,
- * images C HW / K HW floats apart in X / Y. */
+ * images C HW / K HW floats apart in X / Y; R (Y's layout) is added when
+ * given. */
 static void conv1x1_pair(struct eloftr_model *m, cl_mem X, int C, int HW,
-                         cl_mem Wt, int K, cl_mem Y)
+                         cl_mem Wt, int K, cl_mem Y, cl_mem R = NULL)
 {
     ops_gemm(m->ops, K, HW, C, ops_mat(Wt, 0, C),
              ops_bmat(X, 0, HW, (long)C * HW, 0), 0,
-             ops_bmat(Y, 0, HW, (long)K * HW, 0), 2, 1, NULL, 1, NULL, 0, 1.0f,
+             ops_bmat(Y, 0, HW, (long)K * HW, 0), 2, 1, NULL, 1, R, 0, 1.0f,
              ACT_NONE, 0);
 }
 
@@ -577,17 +598,13 @@ static void fusion(struct eloftr_model *m)
 
     conv1x1_pair(m, m->xp, 256, h * w, m->f_out, 256, m->fu_a);
     ops_resize(o, m->fu_a, 2 * 256, h, w, m->fu_b, H4, W4, 0, 0, 2.0f);
-    conv1x1_pair(m, m->f2p, 128, H4 * W4, m->f1_w[0], 256, m->fu_c);
-    ops_axpby(o, m->fu_c, m->fu_c, 1.0f, m->fu_b, 1.0f, 2 * 256L * H4 * W4,
-              2 * 256L * H4 * W4);
+    conv1x1_pair(m, m->f2p, 128, H4 * W4, m->f1_w[0], 256, m->fu_c, m->fu_b);
     conv3x3_pair(m, m->fu_c, 256L * H4 * W4, 256, H4, W4, m->f2_w[0],
                  m->f2_b[0], 256, 1, ACT_LEAKY, m->fu_a, 256L * H4 * W4);
     conv3x3_pair(m, m->fu_a, 256L * H4 * W4, 256, H4, W4, m->f3_w[0], NULL,
                  128, 1, ACT_NONE, m->fu_b, 128L * H4 * W4);
     ops_resize(o, m->fu_b, 2 * 128, H4, W4, m->fu_c, H2, W2, 0, 0, 2.0f);
-    conv1x1_pair(m, m->f1p, 64, H2 * W2, m->f1_w[1], 128, m->fu_a);
-    ops_axpby(o, m->fu_a, m->fu_a, 1.0f, m->fu_c, 1.0f, 2 * 128L * H2 * W2,
-              2 * 128L * H2 * W2);
+    conv1x1_pair(m, m->f1p, 64, H2 * W2, m->f1_w[1], 128, m->fu_a, m->fu_c);
     conv3x3_pair(m, m->fu_a, 128L * H2 * W2, 128, H2, W2, m->f2_w[1],
                  m->f2_b[1], 128, 1, ACT_LEAKY, m->fu_b, 128L * H2 * W2);
     conv3x3_pair(m, m->fu_b, 128L * H2 * W2, 128, H2, W2, m->f3_w[1], NULL, 64,
@@ -693,7 +710,7 @@ extern "C" void eloftr_free(struct eloftr_model *m)
         &m->x[1],    &m->fine[0], &m->fine[1], &m->img,   &m->s_a,
         &m->s_b,     &m->f1p,     &m->f2p,     &m->xp,    &m->finep,
         &m->t_q,     &m->t_kv,    &m->t_qn,    &m->t_kvn,
-        &m->t_Q,     &m->t_K,     &m->t_V,     &m->t_O,   &m->t_O2v[0],
+        &m->t_Q,     &m->t_KV,    &m->t_O,   &m->t_O2v[0],
         &m->t_O2v[1], &m->t_O2,
         &m->t_cat,   &m->t_tok,   &m->t_h1,    &m->t_h2,  &m->rope,
         &m->s_blk,   &m->row_lse, &m->col_m,   &m->col_s, &m->row_max,
@@ -713,7 +730,7 @@ extern "C" void eloftr_free(struct eloftr_model *m)
 
         for (int j = 0; j < 2; j++) {
             cl_mem *f[] = {&a[j]->q_agg, &a[j]->norm_g, &a[j]->norm_b,
-                           &a[j]->wq,    &a[j]->wk,     &a[j]->wv,
+                           &a[j]->wq,    &a[j]->wkv,
                            &a[j]->wo,    &a[j]->fc1,    &a[j]->fc2,
                            &a[j]->mlp_g, &a[j]->mlp_b};
 

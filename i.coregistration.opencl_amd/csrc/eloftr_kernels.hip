@@ -540,21 +540,22 @@ extern "C" void eloftr_fine(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
  * of an aggregated-attention block (eloftr.c:445-448: LayerNorm of the
  * MLP output per token, then x + message), on channel-major maps so that
  * neither operand is transposed. A block takes 64 tokens, one per lane;
- * its 4 waves split the C <= 256 channels, each lane holding its token's
- * share in registers, so M is read once; the per-token sums are combined
- * across the waves in LDS. Reads of one channel row are 256 contiguous
- * bytes per wave. */
+ * its LNR_NW waves split the C <= 256 channels, each lane holding its
+ * token's share in registers, so M is read once; the per-token sums are
+ * combined across the waves in LDS. Reads of one channel row are 256
+ * contiguous bytes per wave. */
 #define LNR_MAXC 256
-__global__ void __launch_bounds__(256)
+#define LNR_NW 16
+__global__ void __launch_bounds__(64 * LNR_NW)
     chan_ln_add_kernel(const float *__restrict__ Mm, float *__restrict__ X,
                        const float *__restrict__ g,
                        const float *__restrict__ bt, int C, int n, float eps)
 {
-    constexpr int CPW = LNR_MAXC / 4;
-    __shared__ float part[2][4][64];
+    constexpr int CPW = LNR_MAXC / LNR_NW;
+    __shared__ float part[2][LNR_NW][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = blockIdx.x * 64 + lane;
-    const int cw = (C + 3) / 4, c0 = wave * cw;
+    const int cw = (C + LNR_NW - 1) / LNR_NW, c0 = wave * cw;
     const int nc = max(0, min(cw, C - c0));
     const long long base = (long long)blockIdx.y * C * n;
     const bool on = j < n;
@@ -568,8 +569,11 @@ __global__ void __launch_bounds__(256)
     }
     part[0][wave][lane] = s;
     __syncthreads();
-    mean = (part[0][0][lane] + part[0][1][lane] + part[0][2][lane] +
-            part[0][3][lane]) / C;
+    s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < LNR_NW; w++)
+        s += part[0][w][lane];
+    mean = s / C;
     s = 0.0f;
 #pragma unroll
     for (int k = 0; k < CPW; k++) {
@@ -580,8 +584,11 @@ __global__ void __launch_bounds__(256)
     }
     part[1][wave][lane] = s;
     __syncthreads();
-    r = 1.0f / sqrtf((part[1][0][lane] + part[1][1][lane] + part[1][2][lane] +
-                      part[1][3][lane]) / C + eps);
+    s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < LNR_NW; w++)
+        s += part[1][w][lane];
+    r = 1.0f / sqrtf(s / C + eps);
     if (!on)
         return;
 #pragma unroll
@@ -610,7 +617,7 @@ void eloftr_ln_residual(struct ops *o, cl_mem M, int nb, int C, int n,
     need_floats(b, 0, C, op, "b");
     prof_scope ps(o->ocl, "ln_residual");
     hipLaunchKernelGGL(chan_ln_add_kernel, dim3((n + 63) / 64, nb),
-                       dim3(256), 0, stream_of(o->ocl), cfptr(M), fptr(X),
+                       dim3(64 * LNR_NW), 0, stream_of(o->ocl), cfptr(M), fptr(X),
                        cfptr(g), cfptr(b), C, n, eps);
     launch_check(op);
 }

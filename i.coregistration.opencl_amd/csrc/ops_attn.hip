@@ -8,15 +8,18 @@
  * key left gets zeros.
  *
  * A block holds 4 waves of 32 queries each (128 queries of one head)
- * and streams its range of keys in tiles of 32 through LDS, shared by
- * the 4 waves; with 16-byte aligned rows the next tile is read into
- * registers while the current one is used:
+ * and streams its range of keys in tiles of 32 through double-buffered
+ * LDS, shared by the 4 waves, one barrier per tile; with 16-byte
+ * aligned rows the next tile is read into registers a tile ahead:
  *  - the scores are computed transposed, S^T = K Q^T, with
  *    v_mfma_f32_32x32x2f32 (A = K from LDS, B = the wave's queries,
  *    pre-scaled and held in registers for the whole kernel), so that
  *    each lane holds 16 keys of one query (its column);
  *  - the online softmax runs per lane on those registers, the two lane
- *    halves of a query combined with one cross-lane exchange;
+ *    halves of a query combined with one cross-lane exchange; scores are
+ *    kept in base 2 (log2 e folded into the query scale, one v_exp_f32
+ *    per probability) and the running maximum is raised lazily, only
+ *    when a tile exceeds it by 2^8, so the accumulator rescale is rare;
  *  - the output is accumulated transposed, O^T += V^T P^T, with the
  *    probabilities fed to the MFMA straight from the score registers:
  *    MFMA step r pairs, for lane half h, key (r / 4) * 8 + h * 4 + r % 4,
@@ -40,6 +43,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 #define ATT_KT 32 /* keys per tile */
 #define ATT_NW 4  /* waves per block, 32 queries each */
+#define ATT_TAU 8.0f /* lazy rescaling threshold, base-2 units */
+#define ATT_PF 2     /* LDS operand reads ahead of their MFMA */
 
 /* Registers <- the key tile from key k0 (zeros past Nk and d), 16-byte
  * loads, consecutive threads along a key row. */
@@ -73,14 +78,55 @@ __device__ __forceinline__ void att_fetch(float4 (&kr)[NL], float4 (&vr)[NL],
     }
 }
 
+/* Tile t of keys into LDS buffers ks / vs from the registers of a VEC
+ * fetch (K stored with an odd row pitch, V with 16-byte rows). */
+template <int NL, int DP, int KP, int VP>
+__device__ __forceinline__ void att_stash(const float4 (&kr)[NL],
+                                          const float4 (&vr)[NL], float *ks,
+                                          float *vs, int tid)
+{
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int e = tid + 64 * ATT_NW * i, key = e / (DP / 4);
+        const int dd = (e - key * (DP / 4)) * 4;
+        float *kd = ks + key * KP + dd;
+
+        kd[0] = kr[i].x;
+        kd[1] = kr[i].y;
+        kd[2] = kr[i].z;
+        kd[3] = kr[i].w;
+        *(float4 *)(vs + key * VP + dd) = vr[i];
+    }
+}
+
+/* The same straight from global memory, one float per thread and load
+ * (rows not 16-byte aligned). */
+template <int NL, int DP, int KP, int VP>
+__device__ __forceinline__ void att_stash_direct(const float *K, int ldk,
+                                                 const float *V, int ldv,
+                                                 int k0, int Nk, int d,
+                                                 float *ks, float *vs, int tid)
+{
+    for (int i = 0; i < NL; i++) {
+        const int e = tid + 64 * ATT_NW * i, key = e / DP;
+        const int dd = e - key * DP, kk = k0 + key;
+        const bool ok = kk < Nk && dd < d;
+
+        ks[key * KP + dd] = ok ? K[(long long)kk * ldk + dd] : 0.0f;
+        vs[key * VP + dd] = ok ? V[(long long)kk * ldv + dd] : 0.0f;
+    }
+}
+
 /* One block: 128 queries (4 waves x 32) of one head against the key
- * tiles [t0, t1) of 32 keys; the block's K and V tiles are shared through
- * LDS, the next tile is loaded into registers while the current one is
- * used. With nsplit > 1 (blockIdx.z picks the key range) the
- * unnormalised output and the running (max, sum) go to part_o / part_ml
- * for attn_merge_kernel; with one split the normalised output goes to O
- * directly. */
-template <int ND, bool VEC>
+ * tiles [t0, t1) of 32 keys. K and V tiles are double-buffered in LDS
+ * and shared by the 4 waves: the next tile (fetched into registers one
+ * tile earlier) is written to the other buffer between the score and
+ * the output MFMAs, so one barrier per tile suffices. With nsplit > 1
+ * (blockIdx.z picks the key range) the unnormalised output and the
+ * running (max, sum) go to part_o / part_ml for attn_merge_kernel; with
+ * one split the normalised output goes to O directly. MASK: a key mask
+ * is given. */
+template <int ND, bool VEC, bool MASK>
 __global__ void __launch_bounds__(64 * ATT_NW)
     attention_kernel(const float *__restrict__ Q, int ldq,
                      const float *__restrict__ K, int ldk,
@@ -96,8 +142,8 @@ __global__ void __launch_bounds__(64 * ATT_NW)
     constexpr int NS = DP / 2;      /* score MFMA steps */
     constexpr int NL = VEC ? ATT_KT * DP / 4 / (64 * ATT_NW)
                            : ATT_KT * DP / (64 * ATT_NW); /* loads / thread */
-    __shared__ __align__(16) float Ks[ATT_KT * KP];
-    __shared__ __align__(16) float Vs[ATT_KT * VP];
+    __shared__ __align__(16) float Ks[2][ATT_KT * KP];
+    __shared__ __align__(16) float Vs[2][ATT_KT * VP];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.y, half = lane >> 5, col = lane & 31;
@@ -110,6 +156,11 @@ __global__ void __launch_bounds__(64 * ATT_NW)
     float m = -INFINITY, l = 0.0f;
     float4 kr4[VEC ? NL : 1], vr4[VEC ? NL : 1];
 
+    /* Scores in the base-2 domain: softmax(x) = 2^(x log2 e - max) / sum,
+     * so log2 e is folded into the query scale and every exponential is
+     * one v_exp_f32. */
+    const float qscale = scale * 1.4426950408889634f;
+
     Q += (long long)h * d;
     K += (long long)h * d;
     V += (long long)h * d;
@@ -117,7 +168,8 @@ __global__ void __launch_bounds__(64 * ATT_NW)
     for (int s = 0; s < NS; s++) {
         const int dd = 2 * s + half;
 
-        q[s] = (qi < Nq && dd < d) ? Q[(long long)qi * ldq + dd] * scale : 0.0f;
+        q[s] = (qi < Nq && dd < d) ? Q[(long long)qi * ldq + dd] * qscale
+                                   : 0.0f;
     }
 #pragma unroll
     for (int t = 0; t < ND; t++)
@@ -125,108 +177,162 @@ __global__ void __launch_bounds__(64 * ATT_NW)
         for (int r = 0; r < 16; r++)
             o[t][r] = 0.0f;
 
-    if constexpr (VEC) {
-        if (t0 < t1) {
-            att_fetch<NL, DP>(kr4, vr4, K, ldk, V, ldv, t0 * ATT_KT, Nk, d, tid);
-        }
-    }
-    for (int t = t0; t < t1; t++) {
-        const int k0 = t * ATT_KT;
-        floatx16 s;
-
-        __syncthreads();
+    if (t0 < t1) {
         if constexpr (VEC) {
-#pragma unroll
-            for (int i = 0; i < NL; i++) {
-                const int e = tid + 64 * ATT_NW * i, key = e / (DP / 4);
-                const int dd = (e - key * (DP / 4)) * 4;
-                float *kd = Ks + key * KP + dd;
-
-                kd[0] = kr4[i].x;
-                kd[1] = kr4[i].y;
-                kd[2] = kr4[i].z;
-                kd[3] = kr4[i].w;
-                *(float4 *)(Vs + key * VP + dd) = vr4[i];
-            }
+            att_fetch<NL, DP>(kr4, vr4, K, ldk, V, ldv, t0 * ATT_KT, Nk, d,
+                              tid);
+            att_stash<NL, DP, KP, VP>(kr4, vr4, Ks[0], Vs[0], tid);
+            if (t0 + 1 < t1)
+                att_fetch<NL, DP>(kr4, vr4, K, ldk, V, ldv,
+                                  (t0 + 1) * ATT_KT, Nk, d, tid);
         }
         else {
-            for (int i = 0; i < NL; i++) {
-                const int e = tid + 64 * ATT_NW * i, key = e / DP;
-                const int dd = e - key * DP, kk = k0 + key;
-                const bool ok = kk < Nk && dd < d;
-
-                Ks[key * KP + dd] = ok ? K[(long long)kk * ldk + dd] : 0.0f;
-                Vs[key * VP + dd] = ok ? V[(long long)kk * ldv + dd] : 0.0f;
-            }
+            att_stash_direct<NL, DP, KP, VP>(K, ldk, V, ldv, t0 * ATT_KT, Nk,
+                                             d, Ks[0], Vs[0], tid);
         }
-        __syncthreads();
-        if constexpr (VEC) {
-            if (t + 1 < t1) {
-                att_fetch<NL, DP>(kr4, vr4, K, ldk, V, ldv, (t + 1) * ATT_KT, Nk,
-                                  d, tid);
-            }
-        }
+    }
+    __syncthreads();
+    for (int t = t0; t < t1; t++) {
+        const int k0 = t * ATT_KT, cur = (t - t0) & 1;
+        const float *ks = Ks[cur], *vs = Vs[cur];
+        floatx16 s;
 
 #pragma unroll
         for (int r = 0; r < 16; r++)
             s[r] = 0.0f;
+        {
+            /* K operands read ATT_PF steps ahead of their MFMA; the
+             * scheduling barriers keep the reads there. */
+            const float *kb = ks + col * KP + half;
+            float kv[ATT_PF + 1];
+
 #pragma unroll
-        for (int st = 0; st < NS; st++)
-            s = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                Ks[col * KP + 2 * st + half], q[st], s, 0, 0, 0);
+            for (int st = 0; st < ATT_PF; st++)
+                kv[st] = kb[2 * st];
+#pragma unroll
+            for (int st = 0; st < NS; st++) {
+                if (st + ATT_PF < NS)
+                    kv[(st + ATT_PF) % (ATT_PF + 1)] = kb[2 * (st + ATT_PF)];
+                __builtin_amdgcn_sched_barrier(0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                    kv[st % (ATT_PF + 1)], q[st], s, 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
 
         /* Scores out of the accumulator into plain registers; keys past
-         * Nk or masked out become -inf by a select on a flag computed
-         * first (no conditional writes into the accumulator vector). */
+         * Nk (last tile only) or masked out become -inf by a select on a
+         * flag computed first (no conditional writes into the accumulator
+         * vector). */
         float p[16];
         float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int kk = k0 + (r >> 2) * 8 + half * 4 + (r & 3);
-            bool keep = kk < Nk;
 
-            if (kmask && keep)
-                keep = kmask[kk] != 0;
-            p[r] = keep ? s[r] : -INFINITY;
-            mx = fmaxf(mx, p[r]);
+        if (MASK || k0 + ATT_KT > Nk) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int kk = k0 + (r >> 2) * 8 + half * 4 + (r & 3);
+                bool keep = kk < Nk;
+
+                if (MASK)
+                    keep = keep && kmask[min(kk, Nk - 1)] != 0;
+                p[r] = keep ? s[r] : -INFINITY;
+                mx = fmaxf(mx, p[r]);
+            }
+        }
+        else {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                p[r] = s[r];
+                mx = fmaxf(mx, p[r]);
+            }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         {
-            const float mn = fmaxf(m, mx);
-            float corr, sum = 0.0f;
+            /* Lazy rescaling: the reference maximum m moves only when a
+             * tile's maximum exceeds it by more than ATT_TAU (so the
+             * probabilities stay below 2^ATT_TAU), and the accumulated
+             * output and sum are rescaled only then, by a wave-uniform
+             * branch. Output and sum always share the same m, so the
+             * normalised result is the same. */
+            const bool need = mx > m + ATT_TAU;
+            float sum = 0.0f;
 
-            if (mn == -INFINITY) {
-                corr = 1.0f;
+            if (__any(need)) {
+                const float mn = need ? mx : m;
+                const float corr =
+                    need ? (m == -INFINITY ? 0.0f
+                                           : __builtin_amdgcn_exp2f(m - mn))
+                         : 1.0f;
+
+                m = mn;
+                l *= corr;
+#pragma unroll
+                for (int tt = 0; tt < ND; tt++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        o[tt][r] *= corr;
+            }
+            if (m == -INFINITY) {
 #pragma unroll
                 for (int r = 0; r < 16; r++)
                     p[r] = 0.0f;
             }
             else {
-                corr = m == -INFINITY ? 0.0f : expf(m - mn);
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    p[r] = expf(p[r] - mn);
+                    p[r] = __builtin_amdgcn_exp2f(p[r] - m);
                     sum += p[r];
                 }
-                m = mn;
             }
             sum += __shfl_xor(sum, 32, 64);
-            l = l * corr + sum;
-#pragma unroll
-            for (int tt = 0; tt < ND; tt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++)
-                    o[tt][r] *= corr;
+            l += sum;
         }
+
+        /* The next tile into the other buffer (last read one tile ago,
+         * before the previous barrier), then its successor's loads. */
+        if (t + 1 < t1) {
+            if constexpr (VEC) {
+                att_stash<NL, DP, KP, VP>(kr4, vr4, Ks[cur ^ 1], Vs[cur ^ 1],
+                                          tid);
+                if (t + 2 < t1)
+                    att_fetch<NL, DP>(kr4, vr4, K, ldk, V, ldv,
+                                      (t + 2) * ATT_KT, Nk, d, tid);
+            }
+            else {
+                att_stash_direct<NL, DP, KP, VP>(K, ldk, V, ldv,
+                                                 (t + 1) * ATT_KT, Nk, d,
+                                                 Ks[cur ^ 1], Vs[cur ^ 1],
+                                                 tid);
+            }
+        }
+
+        {
+            /* V operands of step r (key (r / 4) * 8 + half * 4 + r % 4)
+             * read ATT_PF steps ahead, as for K. */
+            const float *vb = vs + half * 4 * VP + col;
+            float vv[ATT_PF + 1][ND];
+            auto vread = [&](int r, float *v) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int key = (r >> 2) * 8 + half * 4 + (r & 3);
+                for (int tt = 0; tt < ND; tt++)
+                    v[tt] = vb[((r >> 2) * 8 + (r & 3)) * VP + tt * 32];
+            };
 
 #pragma unroll
-            for (int tt = 0; tt < ND; tt++)
-                o[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                    Vs[key * VP + tt * 32 + col], p[r], o[tt], 0, 0, 0);
+            for (int r = 0; r < ATT_PF; r++)
+                vread(r, vv[r]);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                if (r + ATT_PF < 16)
+                    vread(r + ATT_PF, vv[(r + ATT_PF) % (ATT_PF + 1)]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int tt = 0; tt < ND; tt++)
+                    o[tt] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                        vv[r % (ATT_PF + 1)][tt], p[r], o[tt], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
+        __syncthreads();
     }
 
     if (qi >= Nq)
@@ -261,8 +367,9 @@ __global__ void __launch_bounds__(64 * ATT_NW)
 }
 
 /* Combine nsplit partial results per (query, head): weights
- * exp(m_s - max m), O = sum_s w_s O_s / sum_s w_s l_s (zeros when no key
- * was kept). One thread per output value. */
+ * 2^(m_s - max m) (the maxima are in the base-2 domain), O = sum_s w_s O_s
+ * / sum_s w_s l_s (zeros when no key was kept). One thread per output
+ * value. */
 __global__ void __launch_bounds__(256)
     attn_merge_kernel(const float *__restrict__ part_o,
                       const float2 *__restrict__ part_ml, int nsplit, int nh,
@@ -284,7 +391,8 @@ __global__ void __launch_bounds__(256)
         for (int s = 0; s < nsplit; s++) {
             const long long row = ((long long)s * nh + h) * Nq + qi;
             const float2 ml = part_ml[row];
-            const float w = ml.x == -INFINITY ? 0.0f : expf(ml.x - mx);
+            const float w =
+                ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - mx);
 
             L += w * ml.y;
             acc += w * part_o[row * DP + dd];
@@ -292,7 +400,7 @@ __global__ void __launch_bounds__(256)
     O[(long long)qi * ldo + (long long)h * d + dd] = L > 0.0f ? acc / L : 0.0f;
 }
 
-template <int ND, bool VEC>
+template <int ND, bool VEC, bool MASK>
 static void launch_nd(struct ops *ops, hipStream_t st, int nh, const float *Q,
                       int ldq, const float *K, int ldk, const float *V, int ldv,
                       float *O, int ldo, int Nq, int Nk, int d, float scale,
@@ -310,7 +418,7 @@ static void launch_nd(struct ops *ops, hipStream_t st, int nh, const float *Q,
     tps = ntiles > 0 ? (ntiles + nsplit - 1) / nsplit : 0;
     nsplit = tps > 0 ? (ntiles + tps - 1) / tps : 1;
     if (nsplit == 1) {
-        hipLaunchKernelGGL((attention_kernel<ND, VEC>),
+        hipLaunchKernelGGL((attention_kernel<ND, VEC, MASK>),
                            dim3((unsigned)qb, (unsigned)nh, 1),
                            dim3(64 * ATT_NW), 0, st, Q, ldq, K, ldk, V, ldv,
                            O, ldo, Nq, Nk, d, scale, kmask, tps, nullptr,
@@ -325,7 +433,7 @@ static void launch_nd(struct ops *ops, hipStream_t st, int nh, const float *Q,
         float2 *pml = (float2 *)((char *)sc->ptr + ob);
         const long long total = (long long)Nq * nh * d;
 
-        hipLaunchKernelGGL((attention_kernel<ND, VEC>),
+        hipLaunchKernelGGL((attention_kernel<ND, VEC, MASK>),
                            dim3((unsigned)qb, (unsigned)nh, (unsigned)nsplit),
                            dim3(64 * ATT_NW), 0, st, Q, ldq, K, ldk, V, ldv,
                            O, ldo, Nq, Nk, d, scale, kmask, tps, po, pml);
@@ -379,14 +487,26 @@ extern "C" void ops_attention(struct ops *o, struct opnd Q, struct opnd K,
                          ((uintptr_t)K.buf->ptr & 15) == 0 &&
                          ((uintptr_t)V.buf->ptr & 15) == 0;
 
-        if (d <= 32)
-            vec ? launch_nd<1, true>(ARGS) : launch_nd<1, false>(ARGS);
-        else if (d <= 64)
-            vec ? launch_nd<2, true>(ARGS) : launch_nd<2, false>(ARGS);
-        else if (d <= 96)
-            vec ? launch_nd<3, true>(ARGS) : launch_nd<3, false>(ARGS);
-        else
-            vec ? launch_nd<4, true>(ARGS) : launch_nd<4, false>(ARGS);
+#define DISPATCH(ND)                                                           \
+    if (kmask)                                                                 \
+        vec ? launch_nd<ND, true, true>(ARGS)                                  \
+            : launch_nd<ND, false, true>(ARGS);                                \
+    else                                                                       \
+        vec ? launch_nd<ND, true, false>(ARGS)                                 \
+            : launch_nd<ND, false, false>(ARGS)
+        if (d <= 32) {
+            DISPATCH(1);
+        }
+        else if (d <= 64) {
+            DISPATCH(2);
+        }
+        else if (d <= 96) {
+            DISPATCH(3);
+        }
+        else {
+            DISPATCH(4);
+        }
+#undef DISPATCH
     }
 #undef ARGS
     launch_check("attention");

@@ -18,41 +18,61 @@ using namespace icoreg;
 
 /* ---- bilinear resize --------------------------------------------------- */
 
-/* One thread per output pixel; grid y runs over the channels, so the
- * pixel's row and column come from one 32-bit division. */
+/* Four consecutive outputs of one row per thread: the row's source rows
+ * and weight are found once for the four, and with W % 4 == 0 (and an
+ * aligned output) the four go out as one 16-byte store. */
 __global__ void __launch_bounds__(256)
     resize_kernel(const float *__restrict__ in, int h, int w,
                   float *__restrict__ out, int H, int W, int coff, int align,
-                  float sy, float sx)
+                  float sy, float sx, int C, int X4, int vec)
 {
-    const int idx = blockIdx.x * 256 + threadIdx.x;
-    const int c = blockIdx.y;
-    int x, y, x0, y0, x1, y1;
-    float ux, uy, fx, fy;
-    const float *p;
+    const long long item = (long long)blockIdx.x * 256 + threadIdx.x;
+    int it, x4, row, y, c, y0, y1;
+    float uy, fy, v[4];
+    const float *r0, *r1;
+    float *o;
 
-    if (idx >= H * W)
+    if (item >= (long long)C * H * X4)
         return;
-    y = idx / W;
-    x = idx - y * W;
-    if (align) {
-        ux = W > 1 ? (float)x * (float)(w - 1) / (float)(W - 1) : 0.0f;
+    it = (int)item;
+    row = it / X4;
+    x4 = it - row * X4;
+    c = row / H;
+    y = row - c * H;
+    if (align)
         uy = H > 1 ? (float)y * (float)(h - 1) / (float)(H - 1) : 0.0f;
-    }
-    else {
-        ux = fmaxf(((float)x + 0.5f) * sx - 0.5f, 0.0f);
+    else
         uy = fmaxf(((float)y + 0.5f) * sy - 0.5f, 0.0f);
-    }
-    x0 = min((int)ux, w - 1);
     y0 = min((int)uy, h - 1);
-    x1 = min(x0 + 1, w - 1);
     y1 = min(y0 + 1, h - 1);
-    fx = ux - x0;
     fy = uy - y0;
-    p = in + (long long)c * h * w;
-    out[((long long)(c + coff) * H + y) * W + x] =
-        (1.0f - fy) * ((1.0f - fx) * p[y0 * w + x0] + fx * p[y0 * w + x1]) +
-        fy * ((1.0f - fx) * p[y1 * w + x0] + fx * p[y1 * w + x1]);
+    r0 = in + ((long long)c * h + y0) * w;
+    r1 = in + ((long long)c * h + y1) * w;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int x = min(4 * x4 + k, W - 1);
+        float ux, fx;
+        int x0, x1;
+
+        if (align)
+            ux = W > 1 ? (float)x * (float)(w - 1) / (float)(W - 1) : 0.0f;
+        else
+            ux = fmaxf(((float)x + 0.5f) * sx - 0.5f, 0.0f);
+        x0 = min((int)ux, w - 1);
+        x1 = min(x0 + 1, w - 1);
+        fx = ux - x0;
+        v[k] = (1.0f - fy) * ((1.0f - fx) * r0[x0] + fx * r0[x1]) +
+               fy * ((1.0f - fx) * r1[x0] + fx * r1[x1]);
+    }
+    o = out + ((long long)(c + coff) * H + y) * W + 4 * x4;
+    if (vec) {
+        *(float4 *)o = make_float4(v[0], v[1], v[2], v[3]);
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+        if (4 * x4 + k < W)
+            o[k] = v[k];
 }
 
 extern "C" void ops_resize(struct ops *o, cl_mem in, int C, int h, int w,
@@ -73,13 +93,17 @@ extern "C" void ops_resize(struct ops *o, cl_mem in, int C, int h, int w,
     count32((long long)(C + coff) * H * W, "resize output");
     need_floats(in, 0, (long long)C * h * w, op, "in");
     need_floats(out, (long long)coff * H * W, total, op, "out");
-    if (C > 65535)
-        icoreg_fatal("%s: %d channels (at most 65535)", op, C);
-    prof_scope ps(o->ocl, "resize_bilinear");
-    hipLaunchKernelGGL(resize_kernel,
-                       dim3((unsigned)((H * W + 255) / 256), (unsigned)C),
-                       dim3(256), 0, stream_of(o->ocl), cfptr(in), h, w,
-                       fptr(out), H, W, coff, align_corners, sy, sx);
+    {
+        const int X4 = (W + 3) / 4;
+        const long long items = (long long)C * H * X4;
+        const int vec = W % 4 == 0 && ((uintptr_t)fptr(out) & 15) == 0;
+
+        prof_scope ps(o->ocl, "resize_bilinear");
+        hipLaunchKernelGGL(resize_kernel,
+                           dim3((unsigned)((items + 255) / 256)), dim3(256),
+                           0, stream_of(o->ocl), cfptr(in), h, w, fptr(out),
+                           H, W, coff, align_corners, sy, sx, C, X4, vec);
+    }
     launch_check("resize_bilinear");
     ICOREG_API_END
 }

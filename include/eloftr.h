@@ -31,7 +31,8 @@ extern "C" {
 struct eloftr_attn {
     cl_mem q_agg;          /* Depthwise 4 x 4 (256, 1, 4, 4). */
     cl_mem norm_g, norm_b; /* LayerNorm of the aggregated tokens. */
-    cl_mem wq, wk, wv, wo; /* (256, 256), no bias. */
+    cl_mem wq, wo;         /* (256, 256), no bias. */
+    cl_mem wkv;            /* k_proj over v_proj: (512, 256), no bias. */
     cl_mem fc1, fc2;       /* (512, 512), (256, 512), no bias. */
     cl_mem mlp_g, mlp_b;   /* LayerNorm after the MLP. */
 };
@@ -57,7 +58,7 @@ struct eloftr_model {
      * once for the pair; f1[k], f2[k], x[k], fine[k] are views of image k. */
     cl_mem img, s_a, s_b, f1p, f2p, xp, finep;
     cl_mem f1[2], f2[2], x[2], fine[2];
-    cl_mem t_q, t_kv, t_qn, t_kvn, t_Q, t_K, t_V, t_O, t_O2, t_cat, t_tok,
+    cl_mem t_q, t_kv, t_qn, t_kvn, t_Q, t_KV, t_O, t_O2, t_cat, t_tok,
         t_h1, t_h2, rope;
     cl_mem t_O2v[2]; /* image k's part of t_O2 */
     cl_mem s_blk, row_lse, col_m, col_s, row_max, row_arg, col_max, col_arg;
