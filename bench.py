@@ -14,10 +14,12 @@ x 2, Gaussian process, coordinate decoder; roma.c:715-919), is reported
 under "roma560" with its own throughput and GEMM roofline.
 
 Prints one JSON line (the driver's contract) with the per-kernel roofline
-of the dominant kernel (the 3 x 3 convolution on the fp32 matrix cores:
-HIP events around each of its launches over the profiled steps) and the CPU
-baseline (the oracle, a C port of the reference kernels, on a bounded
-sample timed on this host).
+of the dominant kernel (the same-size 3 x 3 convolutions as Winograd
+F(2 x 2, 3 x 3) on the fp32 matrix cores: HIP events around each of its
+launches over the profiled steps; its FLOPs are the 16 transform-domain
+products it performs, and the direct-convolution rate of the same layers is
+reported beside it) and the CPU baseline (the oracle, a C port of the
+reference kernels, on a bounded sample timed on this host).
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
                     [--no-roma] [--roma-steps 10] [--copy-calib MiB]
@@ -99,20 +101,43 @@ def eloftr_conv_layers(H, W):
     return out
 
 
-def eloftr_conv_bytes(H, W):
-    """Algorithmic HBM bytes of the 25 convolution launches of one pair:
-    both images' input and output read / written once, weights and bias
-    once per launch."""
+def eloftr_wino_layers(H, W):
+    """The stride-1 layers, which run as Winograd F(2 x 2, 3 x 3)
+    (conv_wino, 22 launches per pair); the 3 stride-2 layers run direct."""
+    return [l for l in eloftr_conv_layers(H, W) if l[4] == 1]
+
+
+def eloftr_wino_flops(H, W):
+    """Algorithmic matrix FLOPs of the Winograd launches of one pair: per
+    image, 2 x 16 x K x C per 2 x 2 output tile (the 16 transform-domain
+    products), ceil(Ho / 2) ceil(Wo / 2) tiles. The input and output
+    transforms (additions on the vector ALUs) are not counted."""
+    f = 0.0
+    for ci, co, h, w, _ in eloftr_wino_layers(H, W):
+        f += 2 * 2.0 * 16 * co * ci * ((h + 1) // 2) * ((w + 1) // 2)
+    return f
+
+
+def eloftr_wino_direct_flops(H, W):
+    """The same layers' direct-convolution FLOPs (2 K Ho Wo C 9 per image):
+    the work a direct kernel would do for the same outputs."""
+    return sum(2 * 2.0 * co * h * w * ci * 9 for ci, co, h, w, _ in eloftr_wino_layers(H, W))
+
+
+def eloftr_wino_bytes(H, W):
+    """Algorithmic HBM bytes of the Winograd launches of one pair: both
+    images' input and output read / written once, the transformed filters
+    (16 K C) and bias once per launch."""
     b = 0
-    for ci, co, h, w, st in eloftr_conv_layers(H, W):
-        b += 4 * (2 * (ci * h * w + co * (h // st) * (w // st)) + co * ci * 9 + co)
+    for ci, co, h, w, _ in eloftr_wino_layers(H, W):
+        b += 4 * (2 * (ci * h * w + co * h * w) + 16 * co * ci + co)
     return b
 
 
-def conv_traffic(profile=ROOT / "profiles" / "eloftr_640_conv_traffic.md"):
-    """Measured HBM bytes per convolution launch, from the committed
-    rocprofv3 counter summary (the line 'traffic_bytes_per_launch: N'),
-    or None."""
+def conv_traffic(profile=ROOT / "profiles" / "eloftr_640_wino_traffic.md"):
+    """Measured HBM bytes per Winograd convolution launch, from the
+    committed rocprofv3 counter summary (the line
+    'traffic_bytes_per_launch: N'), or None."""
     import re
     try:
         m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", profile.read_text())
@@ -295,10 +320,11 @@ def main():
     dev.set_profile(0)
     ps = args.profile_steps
     fl = eloftr_flops(H, W, nm)
-    conv_names = ("conv_direct", "conv_igemm")
-    conv_ms = sum(table.get(k, (0.0, 0))[0] for k in conv_names) / ps
-    conv_calls = sum(table.get(k, (0.0, 0))[1] for k in conv_names) / ps
-    achieved = fl["conv"] / (conv_ms * 1e-3) / 1e12 if conv_ms > 0 else 0.0
+    wino_ms = table.get("conv_wino", (0.0, 0))[0] / ps
+    wino_calls = table.get("conv_wino", (0.0, 0))[1] / ps
+    wino_fl = eloftr_wino_flops(H, W)
+    achieved = wino_fl / (wino_ms * 1e-3) / 1e12 if wino_ms > 0 else 0.0
+    direct_eq = eloftr_wino_direct_flops(H, W) / (wino_ms * 1e-3) / 1e12 if wino_ms > 0 else 0.0
     kernels = {k: {"ms_per_step": round(v[0] / ps, 4), "launches_per_step": v[1] / ps}
                for k, v in sorted(table.items(), key=lambda kv: -kv[1][0])}
     print("[bench] per-kernel ms per pair: " + json.dumps(kernels), file=sys.stderr, flush=True)
@@ -347,14 +373,16 @@ def main():
                                "transformer, coarse match, fusion, fine match)",
                    "tile": [H, W], "coarse_matches": nm,
                    "gflop_per_pair": round(fl["total"] / 1e9, 1)},
-        "roofline": {"kernel": "conv_direct (3x3 convolution, fp32 MFMA on LDS patches)",
+        "roofline": {"kernel": "conv_wino (3x3 stride-1 convolution, Winograd F(2x2,3x3), "
+                               "fp32 MFMA on the 16 transform-domain products)",
                      "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4),
                      "traffic": conv_traffic() if H == W == 640 else None,
-                     "algorithmic_bytes_per_launch": round(eloftr_conv_bytes(H, W) / 25),
-                     "launches_per_step": conv_calls,
-                     "gflop_per_step": round(fl["conv"] / 1e9, 2)},
+                     "algorithmic_bytes_per_launch": round(eloftr_wino_bytes(H, W) / 22),
+                     "launches_per_step": wino_calls,
+                     "gflop_per_step": round(wino_fl / 1e9, 2),
+                     "direct_equivalent_tflops": round(direct_eq, 2)},
         "pipeline_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
         "fine_ms_at_max_matches": round(fine_nmax_ms, 4),
         "cpu_baseline": cpu,

@@ -1,13 +1,16 @@
 /* SPDX-License-Identifier: Unlicense */
 
-/* Direct k x k convolution on the fp32 matrix cores (LDS input patches):
- * the fast path of ops_conv2d for one group, dilation 1, k = 3 or 5,
+/* The fast paths of ops_conv2d on the fp32 matrix cores: Winograd
+ * F(2 x 2, 3 x 3) for same-size 3 x 3 convolutions, and the direct k x k
+ * convolution (LDS input patches) for one group, dilation 1, k = 3 or 5,
  * stride 1 or 2. */
 
 #ifndef ICOREG_CONV_H
 #define ICOREG_CONV_H
 
 #include <hip/hip_runtime.h>
+
+#include "ops.h"
 
 struct conv_args {
     const float *in;  /* (nb, C, H, W) with image stride in_stride */
@@ -31,5 +34,28 @@ bool conv_direct_fits(long long in_floats, long long w_floats);
 
 void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,
                         int cus, hipStream_t s);
+
+/* Winograd F(2 x 2, 3 x 3) path (conv_wino.hip): 3 x 3, stride 1,
+ * padding 1, one group, K % 4 == 0, at least 32 channels in and out. */
+bool conv_wino_supported(int kh, int kw, int sy, int sx, int py, int px,
+                         int dy, int dx, int groups, int C, int K);
+/* Floats of the transformed filters U ([16][C][K]). */
+size_t conv_wino_weight_floats(int K, int C);
+/* U from w (K, C, 3, 3). */
+void conv_wino_weights(const float *w, int K, int C, float *U, hipStream_t s);
+/* The convolution of a (a.w unused) with filters U, nb images. */
+void conv_wino_launch(const conv_args &a, const float *U, int nb,
+                      hipStream_t s);
+
+/* Filters of a 3 x 3 convolution transformed once (a new buffer), for
+ * callers that run the same weights many times. */
+cl_mem conv_wino_prepare(struct ops *o, cl_mem w, int K, int C);
+/* ops_conv2d_batch for 3 x 3, stride 1, padding 1, one group, with U
+ * from conv_wino_prepare (w is used only when the Winograd path does not
+ * take the shape). */
+void conv3x3_wino_batch(struct ops *o, int nb, cl_mem in, long in_stride,
+                        int C, int H, int W, cl_mem w, cl_mem U, cl_mem b,
+                        int K, int act, float slope, cl_mem out,
+                        long out_stride);
 
 #endif /* ICOREG_CONV_H */

@@ -1,0 +1,355 @@
+/* SPDX-License-Identifier: Unlicense */
+
+/* 3 x 3, stride 1, padding 1 convolution by Winograd's minimal filtering
+ * F(2 x 2, 3 x 3) on the CDNA4 matrix cores: the same result as the
+ * reference's direct and im2col + GEMM paths of ops_conv2d (ops.cl:319-387,
+ * ops.c:236-336 of i.coregistration.opencl), with 16 multiplications per
+ * 2 x 2 output tile and input channel instead of 36.
+ *
+ * For a tile d (4 x 4 input values, padding zeros included) and a filter g
+ * (3 x 3):
+ *   V = B^T d B,  U = G g G^T,  Y = A^T (sum over channels of U . V) A,
+ * with B^T = [1 0 -1 0; 0 1 1 0; 0 -1 1 0; 0 1 0 -1],
+ *      G   = [1 0 0; 1/2 1/2 1/2; 1/2 -1/2 1/2; 0 0 1],
+ *      A^T = [1 1 1 0; 0 1 -1 -1]
+ * (Lavin and Gray, "Fast Algorithms for Convolutional Neural Networks",
+ * 2016). The channel sums are 16 GEMMs, one per position (xi, nu) of the
+ * 4 x 4 transform: M[xi nu](k, t) = sum_c U[xi nu](k, c) V[xi nu](c, t).
+ *
+ * wino_weights_kernel writes U as [16][C][K]. conv_wino_kernel: a block
+ * takes 32 tiles (a 4 x 8 grid of 2 x 2 output tiles, 8 x 16 pixels) of
+ * one image and 32 output channels, and walks the input channels WG_CC
+ * at a time:
+ *  - the input patch under the tiles (WG_CC x 10 x 18, zero outside the
+ *    image, normalised and gated when asked) and the U slice go to LDS;
+ *    the next slice is fetched into registers while the matrix cores
+ *    work on the current one;
+ *  - each thread transforms two (channel, tile) patches into V in LDS;
+ *  - wave w runs the 4 GEMMs of row xi = w of the transform
+ *    (v_mfma_f32_32x32x2f32, 32 channels x 32 tiles each);
+ *  - at the end each wave applies A over nu in registers, the rows over
+ *    xi are combined through LDS, and bias and activation are applied on
+ *    the 2 x 2 outputs. */
+
+#include <hip/hip_runtime.h>
+
+#include "act.h"
+#include "conv.h"
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+#define WG_TR 4  /* tile rows per block */
+#define WG_TC 8  /* tile columns per block */
+#define WG_BK 32 /* output channels per block */
+#define WG_CC 16 /* input channels per K slice */
+
+/* Offset past the end of every buffer read (each below 2 GiB): 0. */
+#define WG_OOB 0x80000000u
+#define WG_RSRC_FLAGS 0x00020000
+
+static __device__ __forceinline__ __amdgpu_buffer_rsrc_t
+wg_rsrc(const float *p, unsigned long long bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0,
+                                             (int)(unsigned)bytes,
+                                             WG_RSRC_FLAGS);
+}
+
+/* U[xi nu][c][k] = (G g G^T)[xi][nu] of filter g = w[k][c]. */
+__global__ void __launch_bounds__(256)
+    wino_weights_kernel(const float *__restrict__ w, int K, int C,
+                        float *__restrict__ U)
+{
+    const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
+    const long long kc = (long long)K * C;
+    float g[9], t[4][3];
+
+    if (id >= kc)
+        return;
+    {
+        const int k = (int)(id % K), c = (int)(id / K);
+        const float *src = w + ((long long)k * C + c) * 9;
+
+#pragma unroll
+        for (int i = 0; i < 9; i++)
+            g[i] = src[i];
+        /* t = G g (4 x 3). */
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const float g0 = g[j], g1 = g[3 + j], g2 = g[6 + j];
+
+            t[0][j] = g0;
+            t[1][j] = 0.5f * (g0 + g1 + g2);
+            t[2][j] = 0.5f * (g0 - g1 + g2);
+            t[3][j] = g2;
+        }
+        /* U = t G^T (4 x 4). */
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float a0 = t[i][0], a1 = t[i][1], a2 = t[i][2];
+            const float u[4] = {a0, 0.5f * (a0 + a1 + a2),
+                                0.5f * (a0 - a1 + a2), a2};
+
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                U[(long long)(i * 4 + j) * kc + (long long)c * K + k] = u[j];
+        }
+    }
+}
+
+template <bool NORM>
+__global__ void __launch_bounds__(256)
+    conv_wino_kernel(const conv_args a, const float *__restrict__ U)
+{
+    constexpr int PH = 2 * WG_TR + 2, PW = 2 * WG_TC + 2; /* 10 x 18 */
+    constexpr int PWP = PW + 1;
+    constexpr int PCH = PH * PWP;
+    constexpr int PN = WG_CC * PH * PW;      /* patch values per slice */
+    constexpr int NP = (PN + 255) / 256;     /* per thread */
+    constexpr int NU = 16 * WG_CC * WG_BK / 4 / 256; /* float4 of U */
+    constexpr int NT = WG_TR * WG_TC;        /* 32 tiles */
+    __shared__ float Ps[WG_CC * PCH + 1];    /* + one slot for idle lanes */
+    __shared__ __align__(16) float Vs[16 * WG_CC * NT];
+    __shared__ __align__(16) float Us[16 * WG_CC * WG_BK];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int half = lane >> 5, col = lane & 31;
+    const int C = a.C, H = a.H, W = a.W, K = a.K;
+    const int tiles_w = (W + 1) / 2, bw = (tiles_w + WG_TC - 1) / WG_TC;
+    const int ty0 = (blockIdx.x / bw) * WG_TR, tx0 = (blockIdx.x % bw) * WG_TC;
+    const int k0 = blockIdx.y * WG_BK;
+    const int iy0 = 2 * ty0 - 1, ix0 = 2 * tx0 - 1;
+    const long long HW = (long long)H * W;
+    const float *in = a.in + (long long)blockIdx.z * a.in_stride;
+    const unsigned long long ibytes = (unsigned long long)C * HW * 4;
+    const unsigned long long ubytes = 16ULL * C * K * 4;
+    unsigned poff[NP], uoff[NU];
+    int ldp[NP];
+    float rp[NP];
+    float4 ru[NU];
+    floatx16 acc[4];
+
+#pragma unroll
+    for (int v = 0; v < 4; v++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            acc[v][r] = 0.0f;
+
+    /* Per-thread offsets, the same for every slice. Patch value
+     * (c, py, px); U float4 (position, c, k quad). */
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+        const int e = tid + 256 * q, c = e / (PH * PW);
+        const int rem = e - c * (PH * PW), py = rem / PW, px = rem - py * PW;
+        const int iy = iy0 + py, ix = ix0 + px;
+
+        poff[q] = e < PN && iy >= 0 && iy < H && ix >= 0 && ix < W
+                      ? (unsigned)((c * HW + (long long)iy * W + ix) * 4)
+                      : WG_OOB;
+        ldp[q] = e < PN ? c * PCH + py * PWP + px : WG_CC * PCH;
+    }
+#pragma unroll
+    for (int q = 0; q < NU; q++) {
+        const int e = tid + 256 * q, kq = e % (WG_BK / 4);
+        const int pc = e / (WG_BK / 4), pos = pc / WG_CC, c = pc % WG_CC;
+
+        uoff[q] = k0 + 4 * kq < K
+                      ? (unsigned)((((long long)pos * C + c) * K + k0 + 4 * kq) *
+                                   4)
+                      : WG_OOB;
+    }
+
+    auto fetch = [&](int c0) {
+        const __amdgpu_buffer_rsrc_t ri =
+            wg_rsrc(in + c0 * HW, ibytes - (unsigned long long)c0 * HW * 4);
+        /* U rows of this slice start c0 rows on; rows past C (and past
+         * the last position's end) read 0 or are multiplied by V = 0. */
+        const __amdgpu_buffer_rsrc_t ru_ =
+            wg_rsrc(U + (long long)c0 * K, ubytes - (unsigned long long)c0 * K * 4);
+
+#pragma unroll
+        for (int q = 0; q < NP; q++)
+            rp[q] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(ri, (int)poff[q],
+                                                            0, 0));
+#pragma unroll
+        for (int q = 0; q < NU; q++)
+            ru[q] = __builtin_bit_cast(
+                float4, __builtin_amdgcn_raw_buffer_load_b128(
+                            ru_, (int)uoff[q], 0, 0));
+        if (NORM) {
+#pragma unroll
+            for (int q = 0; q < NP; q++) {
+                const int cg = c0 + (tid + 256 * q) / (PH * PW);
+                const int cc = cg < C ? cg : C - 1;
+                float v = (rp[q] - a.mean[cc]) * a.rstd[cc];
+
+                if (a.gate)
+                    v = v >= 0.0f ? v : a.gate[cc] * v;
+                rp[q] = poff[q] != WG_OOB && cg < C ? v : 0.0f;
+            }
+        }
+    };
+    auto stash = [&]() {
+#pragma unroll
+        for (int q = 0; q < NP; q++)
+            Ps[ldp[q]] = rp[q];
+#pragma unroll
+        for (int q = 0; q < NU; q++)
+            *(float4 *)&Us[(tid + 256 * q) * 4] = ru[q];
+    };
+    /* V of (channel c, tile t) for the two pairs of this thread. */
+    auto transform = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int c = (tid >> 5) + 8 * i, t = tid & 31;
+            const int tr = t / WG_TC, tc = t % WG_TC;
+            const float *p = Ps + c * PCH + 2 * tr * PWP + 2 * tc;
+            float d[4][4], u[4][4];
+
+#pragma unroll
+            for (int y = 0; y < 4; y++)
+#pragma unroll
+                for (int x = 0; x < 4; x++)
+                    d[y][x] = p[y * PWP + x];
+            /* Rows: u = B^T d. */
+#pragma unroll
+            for (int x = 0; x < 4; x++) {
+                u[0][x] = d[0][x] - d[2][x];
+                u[1][x] = d[1][x] + d[2][x];
+                u[2][x] = d[2][x] - d[1][x];
+                u[3][x] = d[1][x] - d[3][x];
+            }
+            /* Columns: V = u B. */
+#pragma unroll
+            for (int y = 0; y < 4; y++) {
+                const float v0 = u[y][0] - u[y][2], v1 = u[y][1] + u[y][2];
+                const float v2 = u[y][2] - u[y][1], v3 = u[y][1] - u[y][3];
+                float *o = Vs + (y * 4) * WG_CC * NT + c * NT + t;
+
+                o[0] = v0;
+                o[WG_CC * NT] = v1;
+                o[2 * WG_CC * NT] = v2;
+                o[3 * WG_CC * NT] = v3;
+            }
+        }
+    };
+
+    const int nk = (C + WG_CC - 1) / WG_CC;
+
+    fetch(0);
+    for (int kt = 0; kt < nk; kt++) {
+        stash();
+        __syncthreads();
+        if (kt + 1 < nk)
+            fetch((kt + 1) * WG_CC);
+        transform();
+        __syncthreads();
+        {
+            /* Wave w: positions (w, nu), nu = 0..3; A = U (channels k on
+             * lanes), B = V (tiles on lanes), K = input channels. */
+#pragma unroll
+            for (int s = 0; s < WG_CC / 2; s++) {
+                const int c = 2 * s + half;
+                float av[4], bv[4];
+
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int pos = wave * 4 + v;
+
+                    av[v] = Us[(pos * WG_CC + c) * WG_BK + col];
+                    bv[v] = Vs[(pos * WG_CC + c) * NT + col];
+                }
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    acc[v] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                        av[v], bv[v], acc[v], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+
+    /* Z[xi][j] = (M A)[xi][j] for xi = wave, in registers; then
+     * Y[i][j] = (A^T Z)[i][j] through LDS. Register r of a 32 x 32
+     * accumulator holds channel (r / 4) * 8 + half * 4 + r % 4, tile
+     * col. */
+    {
+        float *Zs = Vs; /* [xi][j][k][t], 4 * 2 * 32 * 32 floats */
+
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int k = (r >> 2) * 8 + half * 4 + (r & 3);
+            const float z0 = acc[0][r] + acc[1][r] + acc[2][r];
+            const float z1 = acc[1][r] - acc[2][r] - acc[3][r];
+
+            Zs[((wave * 2 + 0) * WG_BK + k) * NT + col] = z0;
+            Zs[((wave * 2 + 1) * WG_BK + k) * NT + col] = z1;
+        }
+        __syncthreads();
+        {
+            float *out = a.out + (long long)blockIdx.z * a.out_stride;
+            const int t = tid & 31, tr = t / WG_TC, tc = t % WG_TC;
+            const int oy = 2 * (ty0 + tr), ox = 2 * (tx0 + tc);
+
+#pragma unroll
+            for (int i = 0; i < WG_BK / 8; i++) {
+                const int k = (tid >> 5) + 8 * i, kg = k0 + k;
+                const float bias = a.bias && kg < K ? a.bias[kg] : 0.0f;
+
+                if (kg >= K)
+                    continue;
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float z0 = Zs[((0 * 2 + j) * WG_BK + k) * NT + t];
+                    const float z1 = Zs[((1 * 2 + j) * WG_BK + k) * NT + t];
+                    const float z2 = Zs[((2 * 2 + j) * WG_BK + k) * NT + t];
+                    const float z3 = Zs[((3 * 2 + j) * WG_BK + k) * NT + t];
+                    const float y0 = z0 + z1 + z2, y1 = z1 - z2 - z3;
+
+                    if (ox + j >= a.Wo)
+                        continue;
+                    if (oy < a.Ho)
+                        out[((long long)kg * a.Ho + oy) * a.Wo + ox + j] =
+                            icoreg_act(y0 + bias, a.act, a.slope);
+                    if (oy + 1 < a.Ho)
+                        out[((long long)kg * a.Ho + oy + 1) * a.Wo + ox + j] =
+                            icoreg_act(y1 + bias, a.act, a.slope);
+                }
+            }
+        }
+    }
+}
+
+bool conv_wino_supported(int kh, int kw, int sy, int sx, int py, int px,
+                         int dy, int dx, int groups, int C, int K)
+{
+    return kh == 3 && kw == 3 && sy == 1 && sx == 1 && py == 1 && px == 1 &&
+           dy == 1 && dx == 1 && groups == 1 && K % 4 == 0 && C >= 32 &&
+           K >= 32;
+}
+
+size_t conv_wino_weight_floats(int K, int C) { return 16ULL * K * C; }
+
+void conv_wino_weights(const float *w, int K, int C, float *U, hipStream_t s)
+{
+    const long long n = (long long)K * C;
+
+    hipLaunchKernelGGL(wino_weights_kernel, dim3((unsigned)((n + 255) / 256)),
+                       dim3(256), 0, s, w, K, C, U);
+}
+
+void conv_wino_launch(const conv_args &a, const float *U, int nb,
+                      hipStream_t s)
+{
+    const int tiles_h = (a.Ho + 1) / 2, tiles_w = (a.Wo + 1) / 2;
+    const int blocks = ((tiles_h + WG_TR - 1) / WG_TR) *
+                       ((tiles_w + WG_TC - 1) / WG_TC);
+    const dim3 grid(blocks, (a.K + WG_BK - 1) / WG_BK, nb);
+
+    if (a.mean)
+        hipLaunchKernelGGL(conv_wino_kernel<true>, grid, dim3(256), 0, s, a,
+                           U);
+    else
+        hipLaunchKernelGGL(conv_wino_kernel<false>, grid, dim3(256), 0, s, a,
+                           U);
+}

@@ -22,7 +22,11 @@
  *    same sums per output value, in another memory layout;
  *  - k_proj and v_proj run as one product with their weights stacked;
  *  - the fusion's "1 x 1 convolution + upsampled coarser level" sums are
- *    the 1 x 1 products' residual inputs instead of separate adds. */
+ *    the 1 x 1 products' residual inputs instead of separate adds;
+ *  - the same-size 3 x 3 convolutions run as Winograd F(2 x 2, 3 x 3)
+ *    with the filters transformed once at load: the same sums, regrouped
+ *    (16 instead of 36 multiplications per 2 x 2 output tile and input
+ *    channel), equal to the direct sums within float rounding. */
 
 #include <math.h>
 #include <stdio.h>
@@ -30,6 +34,7 @@
 #include <string.h>
 
 #include "common.h"
+#include "conv.h"
 #include "eloftr.h"
 #include "eloftr_fused.h"
 #include "icoreg_kernels.h"
@@ -268,6 +273,19 @@ extern "C" void eloftr_load(struct eloftr_model *m, struct ops *ops,
         load_attn(m, pf, i, "cross_attention", &m->cross_attn[i]);
     }
     load_fusion(m, pf);
+    /* Same-size 3 x 3 filters in Winograd form, once. */
+    for (l = 0; l < ELOFTR_BLOCKS; l++)
+        if (m->bstride[l] == 1 &&
+            conv_wino_supported(3, 3, 1, 1, 1, 1, 1, 1, 1, m->bcin[l],
+                                m->bcout[l]))
+            m->bU[l] = conv_wino_prepare(ops, m->bw[l], m->bcout[l],
+                                         m->bcin[l]);
+    for (int i = 0; i < 2; i++) {
+        const int d = i ? 128 : 256, d3 = i ? 64 : 128;
+
+        m->f2_U[i] = conv_wino_prepare(ops, m->f2_w[i], d, d);
+        m->f3_U[i] = conv_wino_prepare(ops, m->f3_w[i], d3, d);
+    }
     ICOREG_API_END
 }
 
@@ -387,12 +405,17 @@ extern "C" void eloftr_alloc(struct eloftr_model *m, int H, int W)
  * in_stride floats after image 0, out likewise at out_stride. */
 static void conv3x3_pair(struct eloftr_model *m, cl_mem in, long in_stride,
                          int C, int H, int W, cl_mem w, cl_mem b, int K,
-                         int stride, int act, cl_mem out, long out_stride)
+                         int stride, int act, cl_mem out, long out_stride,
+                         cl_mem U = NULL)
 {
     struct conv_geom g = ops_geom(3, stride, 1);
 
-    ops_conv2d_batch(m->ops, 2, in, in_stride, C, H, W, w, b, K, &g, NULL,
-                     NULL, NULL, act, LEAKY, out, out_stride);
+    if (U)
+        conv3x3_wino_batch(m->ops, 2, in, in_stride, C, H, W, w, U, b, K, act,
+                           LEAKY, out, out_stride);
+    else
+        ops_conv2d_batch(m->ops, 2, in, in_stride, C, H, W, w, b, K, &g, NULL,
+                         NULL, NULL, act, LEAKY, out, out_stride);
 }
 
 /* The RepVGG backbone on both images of the pair (m->img: image 1 at
@@ -420,7 +443,8 @@ static void backbone(struct eloftr_model *m)
             else
                 out = in == m->s_a ? m->s_b : m->s_a;
             conv3x3_pair(m, in, in_stride, m->bcin[l], Hc, Wc, m->bw[l],
-                         m->bb[l], m->bcout[l], st, ACT_RELU, out, out_stride);
+                         m->bb[l], m->bcout[l], st, ACT_RELU, out, out_stride,
+                         m->bU[l]);
             Hc = Ho;
             Wc = Wo;
             in = out;
@@ -600,15 +624,17 @@ static void fusion(struct eloftr_model *m)
     ops_resize(o, m->fu_a, 2 * 256, h, w, m->fu_b, H4, W4, 0, 0, 2.0f);
     conv1x1_pair(m, m->f2p, 128, H4 * W4, m->f1_w[0], 256, m->fu_c, m->fu_b);
     conv3x3_pair(m, m->fu_c, 256L * H4 * W4, 256, H4, W4, m->f2_w[0],
-                 m->f2_b[0], 256, 1, ACT_LEAKY, m->fu_a, 256L * H4 * W4);
+                 m->f2_b[0], 256, 1, ACT_LEAKY, m->fu_a, 256L * H4 * W4,
+                 m->f2_U[0]);
     conv3x3_pair(m, m->fu_a, 256L * H4 * W4, 256, H4, W4, m->f3_w[0], NULL,
-                 128, 1, ACT_NONE, m->fu_b, 128L * H4 * W4);
+                 128, 1, ACT_NONE, m->fu_b, 128L * H4 * W4, m->f3_U[0]);
     ops_resize(o, m->fu_b, 2 * 128, H4, W4, m->fu_c, H2, W2, 0, 0, 2.0f);
     conv1x1_pair(m, m->f1p, 64, H2 * W2, m->f1_w[1], 128, m->fu_a, m->fu_c);
     conv3x3_pair(m, m->fu_a, 128L * H2 * W2, 128, H2, W2, m->f2_w[1],
-                 m->f2_b[1], 128, 1, ACT_LEAKY, m->fu_b, 128L * H2 * W2);
+                 m->f2_b[1], 128, 1, ACT_LEAKY, m->fu_b, 128L * H2 * W2,
+                 m->f2_U[1]);
     conv3x3_pair(m, m->fu_b, 128L * H2 * W2, 128, H2, W2, m->f3_w[1], NULL, 64,
-                 1, ACT_NONE, m->fu_c, 64L * H2 * W2);
+                 1, ACT_NONE, m->fu_c, 64L * H2 * W2, m->f3_U[1]);
     ops_resize(o, m->fu_c, 2 * 64, H2, W2, m->finep, m->H, m->W, 0, 0, 2.0f);
 }
 
@@ -724,6 +750,7 @@ extern "C" void eloftr_free(struct eloftr_model *m)
     for (int l = 0; l < ELOFTR_BLOCKS; l++) {
         ocl_release(&m->bw[l]);
         ocl_release(&m->bb[l]);
+        ocl_release(&m->bU[l]);
     }
     for (int l = 0; l < ELOFTR_LAYERS; l++) {
         struct eloftr_attn *a[2] = {&m->self_attn[l], &m->cross_attn[l]};
@@ -743,6 +770,8 @@ extern "C" void eloftr_free(struct eloftr_model *m)
         ocl_release(&m->f2_w[i]);
         ocl_release(&m->f2_b[i]);
         ocl_release(&m->f3_w[i]);
+        ocl_release(&m->f2_U[i]);
+        ocl_release(&m->f3_U[i]);
     }
     free(m->mi);
     free(m->mj);

@@ -268,11 +268,12 @@ __global__ void __launch_bounds__(256)
 }
 
 /* ops_conv2d over nb images (in_stride / out_stride floats apart). */
+/* U: the filters already in Winograd form (conv_wino_prepare) or NULL. */
 static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
                       int C, int H, int W, cl_mem w, cl_mem b, int K,
                       const struct conv_geom *g, cl_mem mean, cl_mem rstd,
                       cl_mem alpha, int act, float slope, cl_mem out,
-                      long long out_stride)
+                      long long out_stride, cl_mem U = nullptr)
 {
     const char *op = "ops_conv2d";
     int Ho, Wo, cg;
@@ -308,6 +309,46 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
         need_floats(rstd, 0, C, op, "rstd");
         if (alpha)
             need_floats(alpha, 0, C, op, "alpha");
+    }
+    if (conv_wino_supported(g->kh, g->kw, g->sy, g->sx, g->py, g->px, g->dy,
+                            g->dx, g->groups, C, K) &&
+        conv_direct_fits((long long)C * H * W,
+                         (long long)conv_wino_weight_floats(K, C))) {
+        /* 3 x 3, stride 1, same size: Winograd F(2 x 2, 3 x 3). */
+        conv_args a;
+
+        a.in = cfptr(in);
+        a.w = nullptr;
+        a.bias = cfptr(b);
+        a.out = fptr(out);
+        a.in_stride = in_stride;
+        a.out_stride = out_stride;
+        a.C = C;
+        a.H = H;
+        a.W = W;
+        a.K = K;
+        a.Ho = Ho;
+        a.Wo = Wo;
+        a.pad = 1;
+        a.mean = cfptr(mean);
+        a.rstd = cfptr(rstd);
+        a.gate = mean ? cfptr(alpha) : nullptr;
+        a.act = act;
+        a.slope = slope;
+        if (!U) {
+            U = scratch_get(o, conv_wino_weight_floats(K, C) * sizeof(float));
+            prof_scope ps(o->ocl, "conv_wino_weights");
+            conv_wino_weights(cfptr(w), K, C, fptr(U), stream_of(o->ocl));
+            launch_check("conv_wino_weights");
+        }
+        else {
+            need_floats(U, 0, (long long)conv_wino_weight_floats(K, C), op,
+                        "Winograd filters");
+        }
+        prof_scope ps(o->ocl, "conv_wino");
+        conv_wino_launch(a, cfptr(U), nb, stream_of(o->ocl));
+        launch_check("conv_wino");
+        return;
     }
     if (conv_direct_supported(g->kh, g->kw, g->sy, g->sx, g->dy, g->dx,
                               g->groups) &&
@@ -423,6 +464,29 @@ extern "C" void ops_conv2d_batch(struct ops *o, int nb, cl_mem in,
     conv_impl(o, nb, in, in_stride, C, H, W, w, b, K, g, mean, rstd, alpha, act,
               slope, out, out_stride);
     ICOREG_API_END
+}
+
+cl_mem conv_wino_prepare(struct ops *o, cl_mem w, int K, int C)
+{
+    cl_mem U;
+
+    need_floats(w, 0, (long long)K * C * 9, "conv_wino_prepare", "weights");
+    U = ocl_alloc(o->ocl, conv_wino_weight_floats(K, C) * sizeof(float),
+                  "Winograd filters");
+    conv_wino_weights(cfptr(w), K, C, fptr(U), stream_of(o->ocl));
+    launch_check("conv_wino_weights");
+    return U;
+}
+
+void conv3x3_wino_batch(struct ops *o, int nb, cl_mem in, long in_stride,
+                        int C, int H, int W, cl_mem w, cl_mem U, cl_mem b,
+                        int K, int act, float slope, cl_mem out,
+                        long out_stride)
+{
+    const struct conv_geom g = {3, 3, 1, 1, 1, 1, 1, 1, 1};
+
+    conv_impl(o, nb, in, in_stride, C, H, W, w, b, K, &g, nullptr, nullptr,
+              nullptr, act, slope, out, out_stride, U);
 }
 
 extern "C" void ops_fold_bn(float *w, float *b, int K, long per,

@@ -47,6 +47,9 @@ struct eloftr_model {
     /* Fine fusion: out_conv (x / 16 folded), then per block out_conv1
      * 1 x 1, out_conv2 3 x 3 with BatchNorm folded, out_conv3 3 x 3. */
     cl_mem f_out, f1_w[2], f2_w[2], f2_b[2], f3_w[2];
+    /* The stride-1 3 x 3 filters in Winograd form (NULL where the
+     * convolution runs direct): backbone blocks, then f2_w, f3_w. */
+    cl_mem bU[ELOFTR_BLOCKS], f2_U[2], f3_U[2];
 
     /* Scale of the RoPE positions (1; the authors' "npe": 832 / long
      * side), set before eloftr_alloc. */

@@ -92,6 +92,10 @@ CONV_SHAPES = [
     (2, 20, 60, 90, 40, 3, 2, 1, 0, 3),
     (1, 7, 30, 90, 70, 5, 2, 2, 1, 2),
     (1, 9, 17, 48, 20, 5, 1, 2, 1, 1),
+    # Winograd F(2 x 2, 3 x 3): normalised input, ragged channels, odd
+    # sizes, a partial block of output channels.
+    (2, 50, 31, 35, 44, 3, 1, 1, 1, 2),
+    (1, 33, 9, 7, 36, 3, 1, 1, 0, 0),
 ]
 
 
