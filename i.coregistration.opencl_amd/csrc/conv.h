@@ -36,9 +36,11 @@ void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,
                         int cus, hipStream_t s);
 
 /* Winograd F(2 x 2, 3 x 3) path (conv_wino.hip): 3 x 3, stride 1,
- * padding 1, one group, K % 4 == 0, at least 32 channels in and out. */
+ * padding 1, one group, K % 4 == 0, at least 32 channels in and out, an
+ * Ho x Wo output of at most 65535 blocks of 8 x 16 pixels. */
 bool conv_wino_supported(int kh, int kw, int sy, int sx, int py, int px,
-                         int dy, int dx, int groups, int C, int K);
+                         int dy, int dx, int groups, int C, int K, int Ho,
+                         int Wo);
 /* Floats of the transformed filters U ([16][C][K]). */
 size_t conv_wino_weight_floats(int K, int C);
 /* U from w (K, C, 3, 3). */

@@ -277,7 +277,7 @@ extern "C" void eloftr_load(struct eloftr_model *m, struct ops *ops,
     for (l = 0; l < ELOFTR_BLOCKS; l++)
         if (m->bstride[l] == 1 &&
             conv_wino_supported(3, 3, 1, 1, 1, 1, 1, 1, 1, m->bcin[l],
-                                m->bcout[l]))
+                                m->bcout[l], 1, 1))
             m->bU[l] = conv_wino_prepare(ops, m->bw[l], m->bcout[l],
                                          m->bcin[l]);
     for (int i = 0; i < 2; i++) {

@@ -311,7 +311,7 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
             need_floats(alpha, 0, C, op, "alpha");
     }
     if (conv_wino_supported(g->kh, g->kw, g->sy, g->sx, g->py, g->px, g->dy,
-                            g->dx, g->groups, C, K) &&
+                            g->dx, g->groups, C, K, Ho, Wo) &&
         conv_direct_fits((long long)C * H * W,
                          (long long)conv_wino_weight_floats(K, C))) {
         /* 3 x 3, stride 1, same size: Winograd F(2 x 2, 3 x 3). */
