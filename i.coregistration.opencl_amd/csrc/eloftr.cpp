@@ -21,6 +21,10 @@
  *    transposes, the MLP LayerNorm fused with the residual add): the
  *    same sums per output value, in another memory layout;
  *  - k_proj and v_proj run as one product with their weights stacked;
+ *  - an attention block's aggregation, pooling, transposes to tokens and
+ *    both LayerNorms are one kernel, o_proj writes the message
+ *    channel-major directly, and fc1 reads [x; message] as two row
+ *    blocks instead of a copied concatenation;
  *  - the fusion's "1 x 1 convolution + upsampled coarser level" sums are
  *    the 1 x 1 products' residual inputs instead of separate adds;
  *  - the same-size 3 x 3 convolutions run as Winograd F(2 x 2, 3 x 3)
@@ -37,6 +41,7 @@
 #include "conv.h"
 #include "eloftr.h"
 #include "eloftr_fused.h"
+#include "gemm.h"
 #include "icoreg_kernels.h"
 
 using namespace icoreg;
@@ -357,17 +362,13 @@ extern "C" void eloftr_alloc(struct eloftr_model *m, int H, int W)
     }
     /* Transformer work buffers hold both images (self-attention runs the
      * pair as one batch). */
-    m->t_q = walloc(m, 2 * ELOFTR_DIM * na, "aggregated");
-    m->t_kv = walloc(m, 2 * ELOFTR_DIM * na, "aggregated");
     m->t_qn = walloc(m, 2 * ELOFTR_DIM * na, "tokens");
     m->t_kvn = walloc(m, 2 * ELOFTR_DIM * na, "tokens");
     m->t_Q = walloc(m, 2 * ELOFTR_DIM * na, "queries");
     m->t_KV = walloc(m, 4 * ELOFTR_DIM * na, "keys and values");
     m->t_O = walloc(m, 2 * ELOFTR_DIM * na, "attention");
     m->t_O2 = walloc(m, 2 * ELOFTR_DIM * na, "attention");
-    for (int k = 0; k < 2; k++)
-        m->t_O2v[k] = view(m->t_O2, k, ELOFTR_DIM * na);
-    m->t_cat = walloc(m, 4 * ELOFTR_DIM * n, "concatenation");
+    m->t_cat = walloc(m, 2 * ELOFTR_DIM * n, "messages");
     m->t_tok = walloc(m, ELOFTR_DIM * n, "tokens");
     m->t_h1 = walloc(m, 2 * MLP * n, "mlp");
     m->t_h2 = walloc(m, 2 * ELOFTR_DIM * n, "mlp");
@@ -452,13 +453,6 @@ static void backbone(struct eloftr_model *m)
         }
 }
 
-static void copyf(struct eloftr_model *m, cl_mem src, size_t soff, cl_mem dst,
-                  size_t doff, size_t floats)
-{
-    ocl_copy(m->ocl, src, soff * sizeof(float), dst, doff * sizeof(float),
-             floats * sizeof(float));
-}
-
 /* One aggregated attention block (eloftr.c:405-449) for nimg images at
  * once: image i of X (256 x h x w maps, nimg of them one after the other)
  * attends to image i of Y and is updated in place. The self-attention
@@ -466,30 +460,22 @@ static void copyf(struct eloftr_model *m, cl_mem src, size_t soff, cl_mem dst,
  * in xp); cross-attention runs image by image, as the reference orders
  * it.
  *
- * Up to the attention message this is the reference's sequence on
- * token-major rows. The MLP then runs on channel-major maps: fc1 and fc2
- * as W * [x; message] products on the (2 D, n) concatenation, so the
- * reference's transposes of the concatenation and of the MLP output are
- * not needed, and the MLP LayerNorm and the residual add are one
- * channel-wise kernel. */
+ * The reference's sequence, with its layout changes folded away: the
+ * aggregation, pooling, transposes to tokens and LayerNorms are one
+ * kernel; o_proj writes the message channel-major (a product with the
+ * token-major output as the transposed operand) for the 4x upsampling;
+ * the MLP runs on channel-major maps, fc1 reading [x; message] as two row
+ * blocks of one operand, and the MLP LayerNorm is fused with the residual
+ * add. */
 static void agg_attn(struct eloftr_model *m, const struct eloftr_attn *a,
                      cl_mem X, cl_mem Y, int nimg, int use_rope)
 {
     struct ops *o = m->ops;
-    struct conv_geom g = {4, 4, 4, 4, 0, 0, 1, 1, ELOFTR_DIM};
     const int D = ELOFTR_DIM, n = m->h * m->w, na = m->ah * m->aw;
     const int hd = D / HEADS, rows = nimg * na;
 
-    ops_conv2d_batch(o, nimg, X, (long)D * n, D, m->h, m->w, a->q_agg, NULL,
-                     D, &g, NULL, NULL, NULL, ACT_NONE, 0, m->t_q,
-                     (long)D * na);
-    ops_pool2d(o, Y, nimg * D, m->h, m->w, 4, 4, 0, 1, m->t_kv);
-    ops_transpose(o, m->t_q, m->t_qn, nimg, D, na);
-    ops_transpose(o, m->t_kv, m->t_kvn, nimg, D, na);
-    ops_layernorm(o, rows, D, m->t_qn, m->t_qn, a->norm_g, a->norm_b, EPS_LN,
-                  ACT_NONE, 0);
-    ops_layernorm(o, rows, D, m->t_kvn, m->t_kvn, a->norm_g, a->norm_b,
-                  EPS_LN, ACT_NONE, 0);
+    eloftr_aggregate(o, X, Y, nimg, D, m->h, m->w, a->q_agg, a->norm_g,
+                     a->norm_b, EPS_LN, m->t_qn, m->t_kvn);
     ops_linear(o, rows, D, D, m->t_qn, 0, a->wq, NULL, m->t_Q, 0, ACT_NONE, 0,
                0);
     /* Keys (columns 0..D-1) and values (D..2D-1) of t_KV in one
@@ -509,20 +495,20 @@ static void agg_attn(struct eloftr_model *m, const struct eloftr_attn *a,
                       ops_mat(m->t_O, off, D), na, na, HEADS, hd,
                       1.0f / sqrtf((float)hd), NULL);
     }
-    ops_linear(o, rows, D, D, m->t_O, 0, a->wo, NULL, m->t_Q, 0, ACT_NONE, 0,
-               0);
-    ops_transpose(o, m->t_Q, m->t_O2, nimg, na, D);
-    for (int i = 0; i < nimg; i++) {
-        copyf(m, X, (size_t)i * D * n, m->t_cat, (size_t)i * 2 * D * n,
-              (size_t)D * n);
-        ops_resize(o, m->t_O2v[i], D, m->ah, m->aw, m->t_cat, m->h, m->w,
-                   (2 * i + 1) * D, 0, 4.0f);
-    }
-    /* h1 (MLP x n) = leaky(fc1 (MLP x 2D) * cat (2D x n)), per image. */
-    ops_gemm(o, MLP, n, 2 * D, ops_mat(a->fc1, 0, 2 * D),
-             ops_bmat(m->t_cat, 0, n, 2L * D * n, 0), 0,
-             ops_bmat(m->t_h1, 0, n, (long)MLP * n, 0), nimg, 1, NULL, 1,
-             NULL, 0, 1.0f, ACT_LEAKY, LEAKY);
+    /* message (D x na per image) = o_proj (D x D) * O^T, O token-major. */
+    ops_gemm(o, D, na, D, ops_mat(a->wo, 0, D),
+             ops_bmat(m->t_O, 0, D, (long)na * D, 0), 1,
+             ops_bmat(m->t_O2, 0, na, (long)D * na, 0), nimg, 1, NULL, 0,
+             NULL, 0, 1.0f, ACT_NONE, 0);
+    /* Upsampled messages of all images, (nimg D, h, w). */
+    ops_resize(o, m->t_O2, nimg * D, m->ah, m->aw, m->t_cat, m->h, m->w, 0, 0,
+               4.0f);
+    /* h1 (MLP x n) = leaky(fc1 (MLP x 2D) * [x; message] (2D x n)). */
+    ops_gemm_cat(o, MLP, n, 2 * D, ops_mat(a->fc1, 0, 2 * D),
+                 ops_bmat(X, 0, n, (long)D * n, 0),
+                 ops_bmat(m->t_cat, 0, n, (long)D * n, 0), D,
+                 ops_bmat(m->t_h1, 0, n, (long)MLP * n, 0), nimg, ACT_LEAKY,
+                 LEAKY);
     /* h2 (D x n) = fc2 (D x MLP) * h1. */
     ops_gemm(o, D, n, MLP, ops_mat(a->fc2, 0, MLP),
              ops_bmat(m->t_h1, 0, n, (long)MLP * n, 0), 0,
@@ -735,9 +721,8 @@ extern "C" void eloftr_free(struct eloftr_model *m)
         &m->f1[0],   &m->f1[1],   &m->f2[0],   &m->f2[1], &m->x[0],
         &m->x[1],    &m->fine[0], &m->fine[1], &m->img,   &m->s_a,
         &m->s_b,     &m->f1p,     &m->f2p,     &m->xp,    &m->finep,
-        &m->t_q,     &m->t_kv,    &m->t_qn,    &m->t_kvn,
-        &m->t_Q,     &m->t_KV,    &m->t_O,   &m->t_O2v[0],
-        &m->t_O2v[1], &m->t_O2,
+        &m->t_qn,    &m->t_kvn,   &m->t_Q,     &m->t_KV,  &m->t_O,
+        &m->t_O2,
         &m->t_cat,   &m->t_tok,   &m->t_h1,    &m->t_h2,  &m->rope,
         &m->s_blk,   &m->row_lse, &m->col_m,   &m->col_s, &m->row_max,
         &m->row_arg, &m->col_max, &m->col_arg, &m->fu_a,  &m->fu_b,

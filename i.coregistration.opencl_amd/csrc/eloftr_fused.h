@@ -17,4 +17,15 @@
 void eloftr_ln_residual(struct ops *o, cl_mem M, int nb, int C, int n,
                         cl_mem g, cl_mem b, float eps, cl_mem X);
 
+/* Tokens of an aggregated-attention block for nb images of C = 256
+ * channels (h x w maps, multiples of 4; image k of X and Y C h w floats
+ * after image k - 1): Q (nb, h/4 * w/4, C) = LayerNorm of the depthwise
+ * 4 x 4 stride-4 aggregation of X with wq (C, 1, 4, 4); KV (same shape)
+ * = LayerNorm of the 4 x 4 max pooling of Y; the LayerNorm's gain g and
+ * bias b shared (eloftr.c:411-423: ops_conv2d, ops_pool2d, two
+ * transposes, two ops_layernorm). */
+void eloftr_aggregate(struct ops *o, cl_mem X, cl_mem Y, int nb, int C, int h,
+                      int w, cl_mem wq, cl_mem g, cl_mem b, float eps,
+                      cl_mem Q, cl_mem KV);
+
 #endif /* ICOREG_ELOFTR_FUSED_H */

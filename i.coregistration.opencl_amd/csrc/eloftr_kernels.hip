@@ -621,3 +621,115 @@ void eloftr_ln_residual(struct ops *o, cl_mem M, int nb, int C, int n,
                        cfptr(g), cfptr(b), C, n, eps);
     launch_check(op);
 }
+
+/* ---- token aggregation of an attention block ------------------------- */
+
+/* For tokens p = (ay, ax) of image b and channels c:
+ *   q[p][c]  = sum_{i,j<4} wq[c][i][j] X[b][c][4 ay + i][4 ax + j]
+ *   kv[p][c] = max_{i,j<4}          Y[b][c][4 ay + i][4 ax + j]
+ * then each row LayerNorm over the channels (gain g, bias bt), written
+ * token-major: eloftr.c:411-423 (depthwise 4 x 4 aggregation, 4 x 4 max
+ * pooling, transposes to tokens, LayerNorm) in one launch. A block takes
+ * AGG_T consecutive tokens; thread c reads its channel's 4 x 4 windows as
+ * 16-byte rows (consecutive tokens of a row share cache lines), the
+ * values go to LDS token-major, and wave t normalises token t of both
+ * outputs. */
+#define AGG_D 256
+#define AGG_T 4
+__global__ void __launch_bounds__(AGG_D)
+    aggregate_kernel(const float *__restrict__ X, const float *__restrict__ Y,
+                     long long img, const float *__restrict__ wq,
+                     const float *__restrict__ g, const float *__restrict__ bt,
+                     int h, int w, int aw, float eps, float *__restrict__ Q,
+                     float *__restrict__ KV)
+{
+    static_assert(AGG_D / 64 == AGG_T, "one wave per token");
+    __shared__ float sv[2][AGG_T][AGG_D];
+    const int c = threadIdx.x, b = blockIdx.y, na = (h / 4) * aw;
+    const int p0 = blockIdx.x * AGG_T;
+    float4 wr[4];
+
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        wr[i] = *(const float4 *)(wq + c * 16 + i * 4);
+#pragma unroll
+    for (int t = 0; t < AGG_T; t++) {
+        const int p = min(p0 + t, na - 1), ay = p / aw, ax = p - ay * aw;
+        const long long base = (long long)b * img + (long long)c * h * w +
+                               (long long)(4 * ay) * w + 4 * ax;
+        float q = 0.0f, kv = -INFINITY;
+
+        /* Rows of a window are 16-byte aligned (w % 4 == 0). */
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 xr = *(const float4 *)(X + base + i * w);
+            const float4 yr = *(const float4 *)(Y + base + i * w);
+
+            q = fmaf(wr[i].x, xr.x, q);
+            q = fmaf(wr[i].y, xr.y, q);
+            q = fmaf(wr[i].z, xr.z, q);
+            q = fmaf(wr[i].w, xr.w, q);
+            kv = fmaxf(kv, fmaxf(fmaxf(yr.x, yr.y), fmaxf(yr.z, yr.w)));
+        }
+        sv[0][t][c] = q;
+        sv[1][t][c] = kv;
+    }
+    __syncthreads();
+    if (p0 + (c >> 6) < na) {
+        const int lane = c & 63, t = c >> 6;
+        const long long row = (long long)b * na + p0 + t;
+
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            float v[AGG_D / 64], s = 0.0f, mean, r;
+
+#pragma unroll
+            for (int u = 0; u < AGG_D / 64; u++) {
+                v[u] = sv[k][t][lane + 64 * u];
+                s += v[u];
+            }
+            mean = wave_sum(s) / AGG_D;
+            s = 0.0f;
+#pragma unroll
+            for (int u = 0; u < AGG_D / 64; u++) {
+                v[u] -= mean;
+                s = fmaf(v[u], v[u], s);
+            }
+            r = 1.0f / sqrtf(wave_sum(s) / AGG_D + eps);
+#pragma unroll
+            for (int u = 0; u < AGG_D / 64; u++) {
+                const int cc = lane + 64 * u;
+
+                (k ? KV : Q)[row * AGG_D + cc] = v[u] * r * g[cc] + bt[cc];
+            }
+        }
+    }
+}
+
+void eloftr_aggregate(struct ops *o, cl_mem X, cl_mem Y, int nb, int C, int h,
+                      int w, cl_mem wq, cl_mem g, cl_mem b, float eps,
+                      cl_mem Q, cl_mem KV)
+{
+    const char *op = "eloftr_aggregate";
+    const int ah = h / 4, aw = w / 4;
+    const long long img = (long long)C * h * w;
+
+    if (C != AGG_D || nb < 1 || nb > 65535 || h < 4 || w < 4 || h % 4 ||
+        w % 4)
+        icoreg_fatal("%s: invalid sizes C=%d nb=%d %dx%d", op, C, nb, h, w);
+    if (((uintptr_t)X->ptr | (uintptr_t)Y->ptr | (uintptr_t)wq->ptr) & 15)
+        icoreg_fatal("%s: X, Y and wq must be 16-byte aligned", op);
+    need_floats(X, 0, nb * img, op, "X");
+    need_floats(Y, 0, nb * img, op, "Y");
+    need_floats(wq, 0, (long long)C * 16, op, "wq");
+    need_floats(g, 0, C, op, "g");
+    need_floats(b, 0, C, op, "b");
+    need_floats(Q, 0, (long long)nb * ah * aw * C, op, "Q");
+    need_floats(KV, 0, (long long)nb * ah * aw * C, op, "KV");
+    prof_scope ps(o->ocl, "aggregate");
+    hipLaunchKernelGGL(aggregate_kernel, dim3((ah * aw + AGG_T - 1) / AGG_T, nb),
+                       dim3(AGG_D), 0,
+                       stream_of(o->ocl), cfptr(X), cfptr(Y), img, cfptr(wq),
+                       cfptr(g), cfptr(b), h, w, aw, eps, fptr(Q), fptr(KV));
+    launch_check(op);
+}

@@ -34,6 +34,11 @@ struct gemm_args {
      * input normalisation and PReLU gate per input channel. */
     int cc, ch, cw, kh, kw, sy, sx, py, px, dy, dx, wo;
     const float *mean, *rstd, *gate;
+    /* GEMM_B_KN with ksplit > 0 (a multiple of 16): rows k >= ksplit of
+     * B are rows k - ksplit of B2 (same ldb and batch strides), i.e. B is
+     * the concatenation [B; B2] without being materialised. */
+    const float *B2;
+    int ksplit;
 };
 
 /* True if the kernel takes these leading dimensions: each at least its
@@ -44,5 +49,14 @@ bool gemm_shape_ok(const gemm_args &g, int bmode);
  * allowed for A / B (every row start aligned). */
 void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
                  hipStream_t s);
+
+#include "ops.h"
+
+/* ops_gemm with B (K x N, not transposed) given as two row blocks: rows
+ * 0..ksplit-1 in B1, the rest in B2 (same ld and batch stride s0; ksplit a
+ * multiple of 16); nb batches over s0, no bias or residual. */
+void ops_gemm_cat(struct ops *o, int M, int N, int K, struct opnd A,
+                  struct opnd B1, struct opnd B2, int ksplit, struct opnd C,
+                  int nb, int act, float slope);
 
 #endif /* ICOREG_GEMM_H */

@@ -119,6 +119,7 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
     const long long bt = blockIdx.y, b0 = bt / g.nb1, b1 = bt % g.nb1;
     const float *A = g.A + b0 * g.sa0 + b1 * g.sa1;
     const float *B = g.B + b0 * g.sb0 + b1 * g.sb1;
+    const float *B2 = g.B2 ? g.B2 + b0 * g.sb0 + b1 * g.sb1 : nullptr;
     const int M = g.M, N = g.N, K = g.K;
     const long long lda = g.lda, ldb = g.ldb;
     /* Rows of A and columns of B inside the matrix for this tile. */
@@ -191,9 +192,15 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
                 rb[e] = gemm_load4<VB>(wb, boff[e]);
         }
         else if (MODE == GEMM_B_KN) {
-            const int kv = min(BK, K - k0);
-            const __amdgpu_buffer_rsrc_t wb = gemm_rsrc(
-                B + k0 * ldb + n0, ((kv - 1) * ldb + cols_b) * 4);
+            /* Rows of a slice come from B or, past ksplit, from B2 (BK
+             * divides ksplit, so a slice never straddles the two). */
+            const bool second = g.ksplit > 0 && k0 >= g.ksplit;
+            const float *Bk = second ? B2 + (long long)(k0 - g.ksplit) * ldb
+                                     : B + (long long)k0 * ldb;
+            const int kend = g.ksplit > 0 && !second ? g.ksplit : K;
+            const int kv = min(BK, kend - k0);
+            const __amdgpu_buffer_rsrc_t wb =
+                gemm_rsrc(Bk + n0, ((kv - 1) * ldb + cols_b) * 4);
 
 #pragma unroll
             for (int e = 0; e < B4; e++)

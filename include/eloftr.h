@@ -61,9 +61,8 @@ struct eloftr_model {
      * once for the pair; f1[k], f2[k], x[k], fine[k] are views of image k. */
     cl_mem img, s_a, s_b, f1p, f2p, xp, finep;
     cl_mem f1[2], f2[2], x[2], fine[2];
-    cl_mem t_q, t_kv, t_qn, t_kvn, t_Q, t_KV, t_O, t_O2, t_cat, t_tok,
-        t_h1, t_h2, rope;
-    cl_mem t_O2v[2]; /* image k's part of t_O2 */
+    cl_mem t_qn, t_kvn, t_Q, t_KV, t_O, t_O2, t_cat, t_tok, t_h1, t_h2,
+        rope;
     cl_mem s_blk, row_lse, col_m, col_s, row_max, row_arg, col_max, col_arg;
     cl_mem fu_a, fu_b, fu_c, m_idx, m_out;
     int blk_rows;
