@@ -17,14 +17,15 @@
  * 4 x 4 transform: M[xi nu](k, t) = sum_c U[xi nu](k, c) V[xi nu](c, t).
  *
  * wino_weights_kernel writes U as [16][C][K]. conv_wino_kernel: a block
- * takes 32 or 64 tiles (a 4 x 8 or 8 x 8 grid of 2 x 2 output tiles) of
- * one image and 32 output channels, and walks the input channels WG_CC
- * at a time:
+ * takes 32 tiles (a 4 x 8 grid of 2 x 2 output tiles, 8 x 16 pixels; the
+ * template also allows 8 x 8 tiles) of one image and 32 output channels,
+ * and walks the input channels WG_CC at a time:
  *  - the input patch under the tiles (WG_CC x (2 WG_TR + 2) x 18, zero
  *    outside the image, normalised and gated when asked) and the U slice
  *    go to LDS; the next slice is fetched into registers while the
  *    matrix cores work on the current one;
- *  - each thread transforms two (channel, tile) patches into V in LDS;
+ *  - each thread transforms WG_CC NT / 256 (channel, tile) patches into V
+ *    in LDS;
  *  - wave w runs the 4 GEMMs of row xi = w of the transform
  *    (v_mfma_f32_32x32x2f32, 32 channels x 32 tiles per MFMA column);
  *  - at the end each wave applies A over nu in registers, the rows over
@@ -111,11 +112,14 @@ __global__ void __launch_bounds__(256, MINW)
     constexpr int NT = WG_TR * WG_TC;        /* tiles per block */
     constexpr int NH = NT / 32;              /* 32-tile MFMA columns */
     constexpr int NV = WG_CC * NT / 256;     /* (c, t) transforms each */
-    static_assert(16 * WG_CC * NT >= 8 * WG_BK * 32,
-                  "the output transform reuses the V buffer");
-    __shared__ float Ps[WG_CC * PCH + 1];    /* + one slot for idle lanes */
-    __shared__ __align__(16) float Vs[16 * WG_CC * NT];
-    __shared__ __align__(16) float Us[16 * WG_CC * WG_BK];
+    static_assert(16 * WG_CC * (NT + WG_BK) >= 8 * WG_BK * 32,
+                  "the output transform reuses the V and U buffers");
+    /* [Vs | Us | Ps]: V [pos][c][t], U [pos][c][k], the patch (+ one slot
+     * for idle lanes); the output transform reuses Vs and Us. */
+    __shared__ __align__(16) float lds[16 * WG_CC * (NT + WG_BK) +
+                                        WG_CC * PCH + 1];
+    float *const Vs = lds, *const Us = lds + 16 * WG_CC * NT;
+    float *const Ps = Us + 16 * WG_CC * WG_BK;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int half = lane >> 5, col = lane & 31;
@@ -288,7 +292,7 @@ __global__ void __launch_bounds__(256, MINW)
      * Register r of a 32 x 32 accumulator holds channel
      * (r / 4) * 8 + half * 4 + r % 4, tile col. */
     {
-        float *Zs = Vs; /* [xi][j][k][t32], 4 * 2 * 32 * 32 floats */
+        float *Zs = lds; /* [xi][j][k][t32], 4 * 2 * 32 * 32 floats */
         float *out = a.out + (long long)blockIdx.z * a.out_stride;
 
 #pragma unroll
@@ -385,12 +389,9 @@ static void wino_launch(const conv_args &a, const float *U, int nb,
 void conv_wino_launch(const conv_args &a, const float *U, int nb,
                       hipStream_t s)
 {
-    /* 64 tiles per block (twice the output tiles per filter slice read,
-     * 8 channels per slice) where the image gives at least 256 such
-     * blocks: 5-8 % faster on the ELoFTR layers; 32 tiles, 16 channels
-     * per slice on smaller images. */
-    if (wino_blocks(a.Ho, a.Wo, 8) * nb * ((a.K + WG_BK - 1) / WG_BK) >= 256)
-        wino_launch<8, 8, 2>(a, U, nb, s);
-    else
-        wino_launch<4, 16, 1>(a, U, nb, s);
+    /* 32 tiles x 32 channels per block, 8 input channels per slice,
+     * registers capped for 4 waves per SIMD: the 38 KB of LDS and the
+     * extra waves in flight beat the larger blocks (64 tiles, or 16
+     * channels per slice) on every ELoFTR layer measured. */
+    wino_launch<4, 8, 4>(a, U, nb, s);
 }
