@@ -45,10 +45,10 @@ struct gemm_args {
  * row length and below 4 Mi floats. */
 bool gemm_shape_ok(const gemm_args &g, int bmode);
 
-/* Launch on stream s over nb batches. va/vb: 16-byte vector loads
- * allowed for A / B (every row start aligned). */
+/* Launch on stream s over nb batches on a device of cus CUs. va/vb:
+ * 16-byte vector loads allowed for A / B (every row start aligned). */
 void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
-                 hipStream_t s);
+                 int cus, hipStream_t s);
 
 #include "ops.h"
 

@@ -7,11 +7,11 @@
  * strides per operand, B either K x N or N x K, bias per row or column,
  * activation, residual that may alias C. The design is gfx950's own:
  *
- *  - 256 threads = 4 wave64s in a 2 x 2 arrangement; each wave owns a
- *    (BM/2) x (BN/2) block of the output as 32 x 32 tiles accumulated by
- *    v_mfma_f32_32x32x2f32 (4096 flop per instruction, full fp32 matrix
- *    rate), so the accumulators live in the matrix unit's registers;
- *  - BK = 16 slices of A and B staged through LDS, double-buffered: the
+ *  - 4, 8 or 16 wave64s in a WGM x WGN arrangement; each wave owns a
+ *    (BM/WGM) x (BN/WGN) block of the output as 32 x 32 tiles
+ *    accumulated by v_mfma_f32_32x32x2f32 (4096 flop per instruction,
+ *    full fp32 matrix rate);
+ *  - BK = 16 or 32 slices of A and B staged through LDS, double-buffered: the
  *    next slice is fetched from HBM/L2 into registers (16-byte loads
  *    when rows are aligned) while the matrix cores work on the current
  *    one, then written to the other LDS buffer two MFMA steps before
@@ -95,23 +95,29 @@ __device__ __forceinline__ int xcd_tile(int L, int T)
     return (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + idx;
 }
 
-template <int BM, int BN, int BK, int MODE, bool VA, bool VB>
-__global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
+/* BM x BN output tile, BK slice, WGM x WGN waves (each a
+ * BM / WGM x BN / WGN block of 32 x 32 MFMA tiles). */
+template <int BM, int BN, int BK, int MODE, bool VA, bool VB, int WGM = 2,
+          int WGN = 2>
+__global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
 {
+    constexpr int NTH = 64 * WGM * WGN;
     constexpr int LDSA = BM + GEMM_PAD, LDSB = BN + GEMM_PAD;
-    constexpr int TM = BM / 64, TN = BN / 64;
+    constexpr int TM = BM / WGM / 32, TN = BN / WGN / 32;
     constexpr int KQ = BK / 4;            /* float4 per row of a slice */
-    constexpr int A4 = BM * BK / 4 / 256; /* float4 loads of A per thread */
-    constexpr int B4 = BN * BK / 4 / 256; /* dense B */
-    constexpr int BE = BN * BK / 256;     /* gathered B elements */
+    constexpr int A4 = BM * BK / 4 / NTH; /* float4 loads of A per thread */
+    constexpr int B4 = BN * BK / 4 / NTH; /* dense B */
+    constexpr int BE = BN * BK / NTH;     /* gathered B elements */
     constexpr int NS = BK / 2;            /* MFMA steps per slice */
     constexpr int PF = 2;                 /* LDS reads run PF steps ahead */
-    static_assert(A4 >= 1 && BN * BK % 1024 == 0, "tile shape");
+    static_assert(A4 >= 1 && BM * BK % (4 * NTH) == 0 &&
+                      BN * BK % (4 * NTH) == 0 && NTH % BN == 0,
+                  "tile shape");
     __shared__ float As[2][BK * LDSA];
     __shared__ float Bs[2][BK * LDSB];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WGN, wn = wave % WGN;
     const int tiles_n = (g.N + BN - 1) / BN;
     const int tiles = tiles_n * ((g.M + BM - 1) / BM);
     const int tile = xcd_tile(blockIdx.x, tiles);
@@ -136,14 +142,14 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
      * the window's end and read 0. */
 #pragma unroll
     for (int e = 0; e < A4; e++) {
-        const int q = tid + 256 * e, row = q / KQ, kq = (q % KQ) * 4;
+        const int q = tid + NTH * e, row = q / KQ, kq = (q % KQ) * 4;
 
         aoff[e] = (unsigned)((row * lda + kq) * 4);
     }
     if (MODE == GEMM_B_NK) {
 #pragma unroll
         for (int e = 0; e < B4; e++) {
-            const int q = tid + 256 * e, row = q / KQ, kq = (q % KQ) * 4;
+            const int q = tid + NTH * e, row = q / KQ, kq = (q % KQ) * 4;
 
             boff[e] = (unsigned)((row * ldb + kq) * 4);
         }
@@ -151,7 +157,7 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
     else if (MODE == GEMM_B_KN) {
 #pragma unroll
         for (int e = 0; e < B4; e++) {
-            const int q = tid + 256 * e, kk = q / (BN / 4);
+            const int q = tid + NTH * e, kk = q / (BN / 4);
             const int nq = (q % (BN / 4)) * 4;
 
             boff[e] = (unsigned)((kk * ldb + nq) * 4);
@@ -210,7 +216,7 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
                  * the next row: zero them. */
 #pragma unroll
                 for (int e = 0; e < B4; e++) {
-                    const int q = tid + 256 * e, nq = (q % (BN / 4)) * 4;
+                    const int q = tid + NTH * e, nq = (q % (BN / 4)) * 4;
 
                     rb[e] = mask4(rb[e], nq, cols_b);
                 }
@@ -220,7 +226,7 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
             const int khw = g.kh * g.kw;
 #pragma unroll
             for (int e = 0; e < BE; e++) {
-                const int r = k0 + ck0 + e * (256 / BN);
+                const int r = k0 + ck0 + e * (NTH / BN);
                 float v = 0.0f;
 
                 if (cvalid && r < K) {
@@ -245,14 +251,14 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
              * of rows before the window's last read the next row. */
 #pragma unroll
             for (int e = 0; e < A4; e++) {
-                const int q = tid + 256 * e, kq = (q % KQ) * 4;
+                const int q = tid + NTH * e, kq = (q % KQ) * 4;
 
                 ra[e] = mask4(ra[e], k0 + kq, K);
             }
             if (MODE == GEMM_B_NK) {
 #pragma unroll
                 for (int e = 0; e < B4; e++) {
-                    const int q = tid + 256 * e, kq = (q % KQ) * 4;
+                    const int q = tid + NTH * e, kq = (q % KQ) * 4;
 
                     rb[e] = mask4(rb[e], k0 + kq, K);
                 }
@@ -265,7 +271,7 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
 
 #pragma unroll
         for (int e = 0; e < A4; e++) {
-            const int q = tid + 256 * e, row = q / KQ, kq = (q % KQ) * 4;
+            const int q = tid + NTH * e, row = q / KQ, kq = (q % KQ) * 4;
 
             as[(kq + 0) * LDSA + row] = ra[e].x;
             as[(kq + 1) * LDSA + row] = ra[e].y;
@@ -275,7 +281,7 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
         if (MODE == GEMM_B_NK) {
 #pragma unroll
             for (int e = 0; e < B4; e++) {
-                const int q = tid + 256 * e, row = q / KQ, kq = (q % KQ) * 4;
+                const int q = tid + NTH * e, row = q / KQ, kq = (q % KQ) * 4;
 
                 bs[(kq + 0) * LDSB + row] = rb[e].x;
                 bs[(kq + 1) * LDSB + row] = rb[e].y;
@@ -286,7 +292,7 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
         else if (MODE == GEMM_B_KN) {
 #pragma unroll
             for (int e = 0; e < B4; e++) {
-                const int q = tid + 256 * e, kk = q / (BN / 4);
+                const int q = tid + NTH * e, kk = q / (BN / 4);
                 const int nq = (q % (BN / 4)) * 4;
 
                 *(float4 *)&bs[kk * LDSB + nq] = rb[e];
@@ -295,7 +301,7 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
         else {
 #pragma unroll
             for (int e = 0; e < BE; e++)
-                bs[(ck0 + e * (256 / BN)) * LDSB + cn] = rg[e];
+                bs[(ck0 + e * (NTH / BN)) * LDSB + cn] = rg[e];
         }
     };
 
@@ -312,8 +318,8 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
         if (kt + 1 < nk)
             fetch((kt + 1) * BK);
         {
-            const float *as = As[cur] + wm * (BM / 2) + (lane & 31);
-            const float *bs = Bs[cur] + wn * (BN / 2) + (lane & 31);
+            const float *as = As[cur] + wm * (BM / WGM) + (lane & 31);
+            const float *bs = Bs[cur] + wn * (BN / WGN) + (lane & 31);
             const int kh = lane >> 5;
             auto operands = [&](int ks, float *a, float *b) {
                 const int kr = 2 * ks + kh;
@@ -364,13 +370,13 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++) {
-                const int col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
+                const int col = n0 + wn * (BN / WGN) + j * 32 + (lane & 31);
 
                 if (col >= N)
                     continue;
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * (BM / 2) + i * 32 + (r >> 2) * 8 +
+                    const int row = m0 + wm * (BM / WGM) + i * 32 + (r >> 2) * 8 +
                                     (lane >> 5) * 4 + (r & 3);
                     float v;
 
@@ -388,35 +394,48 @@ __global__ void __launch_bounds__(256) gemm_mfma(const gemm_args g)
     }
 }
 
-template <int BM, int BN, int MODE>
+template <int BM, int BN, int BK, int WGM, int WGN, int MODE>
 static void launch_mode(const gemm_args &g, int nb, bool va, bool vb,
                         hipStream_t s)
 {
-    constexpr int BK = 16;
     const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-    dim3 grid(tiles, nb), block(256);
+    dim3 grid(tiles, nb), block(64 * WGM * WGN);
 
+#define GEMM_LAUNCH(VA_, VB_)                                                  \
+    hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, VA_, VB_, WGM, WGN>),      \
+                       grid, block, 0, s, g)
     if (MODE == GEMM_B_CONV) {
         if (va)
-            hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, true, false>), grid,
-                               block, 0, s, g);
+            GEMM_LAUNCH(true, false);
         else
-            hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, false, false>), grid,
-                               block, 0, s, g);
-        return;
+            GEMM_LAUNCH(false, false);
     }
-    if (va && vb)
-        hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, true, true>), grid, block, 0,
-                           s, g);
+    else if (va && vb)
+        GEMM_LAUNCH(true, true);
     else if (va)
-        hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, true, false>), grid, block,
-                           0, s, g);
+        GEMM_LAUNCH(true, false);
     else if (vb)
-        hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, false, true>), grid, block,
-                           0, s, g);
+        GEMM_LAUNCH(false, true);
     else
-        hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, false, false>), grid, block,
-                           0, s, g);
+        GEMM_LAUNCH(false, false);
+#undef GEMM_LAUNCH
+}
+
+template <int BM, int BN, int BK, int WGM, int WGN>
+static void launch_cfg(const gemm_args &g, int bmode, int nb, bool va,
+                       bool vb, hipStream_t s)
+{
+    switch (bmode) {
+    case GEMM_B_KN:
+        launch_mode<BM, BN, BK, WGM, WGN, GEMM_B_KN>(g, nb, va, vb, s);
+        break;
+    case GEMM_B_NK:
+        launch_mode<BM, BN, BK, WGM, WGN, GEMM_B_NK>(g, nb, va, vb, s);
+        break;
+    default:
+        launch_mode<BM, BN, BK, WGM, WGN, GEMM_B_CONV>(g, nb, va, vb, s);
+        break;
+    }
 }
 
 bool gemm_shape_ok(const gemm_args &g, int bmode)
@@ -435,27 +454,20 @@ bool gemm_shape_ok(const gemm_args &g, int bmode)
 }
 
 void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
-                 hipStream_t s)
+                 int cus, hipStream_t s)
 {
     /* 16-byte loads need every four-float group wholly inside or wholly
      * past the matrix edge: K (A, and B given N x K) or N (B given
      * K x N) a multiple of 4. */
     va = va && g.K % 4 == 0;
     vb = vb && (bmode == GEMM_B_KN ? g.N % 4 == 0 : g.K % 4 == 0);
-    /* 64 x 64 tiles at every shape measured on gfx950 (transformer and
-     * ViT products, score blocks, 1 x 1 and implicit convolutions): the
-     * small tile's 17 KB of LDS and few registers keep up to 8 waves per
-     * SIMD in flight, which hides operand latency better than the
-     * operand reuse of 64 x 128 or 128 x 128 tiles. */
-    switch (bmode) {
-    case GEMM_B_KN:
-        launch_mode<64, 64, GEMM_B_KN>(g, nb, va, vb, s);
-        break;
-    case GEMM_B_NK:
-        launch_mode<64, 64, GEMM_B_NK>(g, nb, va, vb, s);
-        break;
-    default:
-        launch_mode<64, 64, GEMM_B_CONV>(g, nb, va, vb, s);
-        break;
-    }
+    /* 64 x 64 tiles, 4 waves, BK = 16 at every shape: 17 KB of LDS and
+     * few registers keep up to 8 waves per SIMD in flight. In isolated
+     * sweeps 64 x 128 (8 waves, BK = 32) and 128 x 128 (16 waves) tiles
+     * ran some ViT shapes up to 15 % faster, but inside the RoMa and
+     * ELoFTR pipelines (operands fresh from the previous kernel) they
+     * were 5-70 % slower on the same shapes, so the kernel's WGM x WGN
+     * generality is not used here. */
+    (void)cus;
+    launch_cfg<64, 64, 16, 2, 2>(g, bmode, nb, va, vb, s);
 }

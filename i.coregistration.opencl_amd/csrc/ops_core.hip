@@ -178,7 +178,7 @@ extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
         prof_scope ps(o->ocl, "gemm");
 
         gemm_launch(g, transb ? GEMM_B_NK : GEMM_B_KN, nb, vec_ok(A),
-                    vec_ok(B), stream_of(o->ocl));
+                    vec_ok(B), o->ocl->cu_count, stream_of(o->ocl));
         launch_check("gemm");
     }
     ICOREG_API_END
@@ -231,7 +231,7 @@ void ops_gemm_cat(struct ops *o, int M, int N, int K, struct opnd A,
         prof_scope ps(o->ocl, "gemm");
 
         gemm_launch(g, GEMM_B_KN, nb, vec_ok(A), vec_ok(B1) && vec_ok(B2),
-                    stream_of(o->ocl));
+                    o->ocl->cu_count, stream_of(o->ocl));
         launch_check("gemm");
     }
 }
@@ -475,7 +475,7 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
         prof_scope ps(o->ocl, "conv_igemm");
         gemm_launch(a, GEMM_B_CONV, nb,
                     kred % 4 == 0 && aligned16(w->ptr), false,
-                    stream_of(o->ocl));
+                    o->ocl->cu_count, stream_of(o->ocl));
         launch_check("conv_igemm");
         return;
     }
