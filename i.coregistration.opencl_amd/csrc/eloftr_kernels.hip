@@ -35,6 +35,9 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 /* ---- rows ----------------------------------------------------------------- */
 
+/* One wave per row, one pass over it: each lane keeps a running
+ * (max, sum of exp(x - max)) over its elements, taken 4 at a time (one
+ * rescale per 4), and the lanes are merged at the end. */
 __global__ void __launch_bounds__(256)
     row_lse_kernel(const float *__restrict__ S, int rows, int N, int r0,
                    float *__restrict__ lse)
@@ -42,19 +45,31 @@ __global__ void __launch_bounds__(256)
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     const float *s;
-    float m = -INFINITY, sum = 0.0f;
+    float m = -INFINITY, sum = 0.0f, mw, sw;
 
     if (r >= rows)
         return;
     s = S + (long long)r * N;
-    for (int j = lane; j < N; j += 64)
-        m = fmaxf(m, s[j]);
-    m = wave_max(m);
-    for (int j = lane; j < N; j += 64)
-        sum += expf(s[j] - m);
-    sum = wave_sum(sum);
+    for (int j0 = 4 * lane; j0 < N; j0 += 256) {
+        float v[4], cm = -INFINITY;
+
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            v[u] = j0 + u < N ? s[j0 + u] : -INFINITY;
+            cm = fmaxf(cm, v[u]);
+        }
+        if (cm > m) {
+            sum = m == -INFINITY ? 0.0f : sum * expf(m - cm);
+            m = cm;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            sum += v[u] == -INFINITY ? 0.0f : expf(v[u] - m);
+    }
+    mw = wave_max(m);
+    sw = wave_sum(m == -INFINITY ? 0.0f : sum * expf(m - mw));
     if (lane == 0)
-        lse[r0 + r] = m + logf(sum);
+        lse[r0 + r] = mw + logf(sw);
 }
 
 /* lc[j] = cm[j] + log(cs[j]): the column log-sum-exp, as dual_conf
@@ -106,26 +121,33 @@ __global__ void __launch_bounds__(256)
 
 /* ---- columns ---------------------------------------------------------------- */
 
-/* Chunk c of the block's rows: column maximum and sum of exp(x - max). */
+/* Chunk c of the block's rows: column maximum and sum of exp(x - max),
+ * the chunk's values read once into registers. */
 __global__ void __launch_bounds__(256)
     col_lse_part_kernel(const float *__restrict__ S, int R, int N,
                         float2 *__restrict__ part)
 {
     const int j = blockIdx.x * 256 + threadIdx.x, c = blockIdx.y;
-    const int ra = c * COL_CHUNK, rb = min(R, ra + COL_CHUNK);
-    float m = -INFINITY, s = 0.0f;
+    const int ra = c * COL_CHUNK, nr = min(R - ra, COL_CHUNK);
+    float v[COL_CHUNK], m = -INFINITY, s = 0.0f;
 
     if (j >= N)
         return;
-    for (int r = ra; r < rb; r++)
-        m = fmaxf(m, S[(long long)r * N + j]);
-    for (int r = ra; r < rb; r++)
-        s += expf(S[(long long)r * N + j] - m);
+#pragma unroll
+    for (int r = 0; r < COL_CHUNK; r++) {
+        v[r] = r < nr ? S[(long long)(ra + r) * N + j] : -INFINITY;
+        m = fmaxf(m, v[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < COL_CHUNK; r++)
+        s += r < nr ? expf(v[r] - m) : 0.0f;
     part[(long long)c * N + j] = make_float2(m, s);
 }
 
-/* Chunks merged in order into the block's (max, sum), then into the
- * running (cm, cs) as eloftr_col_lse does (eloftr_kernels.cl:62-65). */
+/* Chunks merged into the block's (max, sum) in two passes (the maximum
+ * of the chunk maxima, then the rescaled sums: independent loads, no
+ * serial chain), then into the running (cm, cs) as eloftr_col_lse does
+ * (eloftr_kernels.cl:62-65). */
 __global__ void __launch_bounds__(256)
     col_lse_merge_kernel(const float2 *__restrict__ part, int nchunks, int N,
                          float *__restrict__ cm, float *__restrict__ cs)
@@ -135,19 +157,23 @@ __global__ void __launch_bounds__(256)
 
     if (j >= N)
         return;
-    for (int c = 0; c < nchunks; c++) {
-        const float2 p = part[(long long)c * N + j];
-        const float m2 = fmaxf(m, p.x);
+#pragma unroll 8
+    for (int c = 0; c < nchunks; c++)
+        m = fmaxf(m, part[(long long)c * N + j].x);
+    if (m != -INFINITY) {
+#pragma unroll 8
+        for (int c = 0; c < nchunks; c++) {
+            const float2 p = part[(long long)c * N + j];
 
-        if (m2 == -INFINITY)
-            continue;
-        s = (m == -INFINITY ? 0.0f : s * expf(m - m2)) +
-            (p.x == -INFINITY ? 0.0f : p.y * expf(p.x - m2));
-        m = m2;
+            s += p.x == -INFINITY ? 0.0f : p.y * expf(p.x - m);
+        }
     }
     mo = cm[j];
     mn = fmaxf(mo, m);
-    cs[j] = (mo == -INFINITY ? 0.0f : cs[j] * expf(mo - mn)) + s * expf(m - mn);
+    if (mn == -INFINITY)
+        return;
+    cs[j] = (mo == -INFINITY ? 0.0f : cs[j] * expf(mo - mn)) +
+            (m == -INFINITY ? 0.0f : s * expf(m - mn));
     cm[j] = mn;
 }
 
@@ -194,6 +220,7 @@ __global__ void __launch_bounds__(256)
         return;
     best = cmax[j];
     bi = carg[j];
+#pragma unroll 8
     for (int c = 0; c < nchunks; c++) {
         const float v = pv[(long long)c * N + j];
 
