@@ -408,13 +408,15 @@ static void launch_nd(struct ops *ops, hipStream_t st, int nh, const float *Q,
 {
     const int qb = (Nq + 32 * ATT_NW - 1) / (32 * ATT_NW);
     const int ntiles = (Nk + ATT_KT - 1) / ATT_KT;
-    /* Key splits so that about 16 waves per CU are resident. */
-    const long long want = 16LL * (ops->ocl->cu_count > 0 ? ops->ocl->cu_count : 256);
+    /* Key splits so that about 8 waves per CU are resident, each split at
+     * least 2 key tiles (measured: more splits cost more in the merge
+     * than they gain in occupancy). */
+    const long long want = 8LL * (ops->ocl->cu_count > 0 ? ops->ocl->cu_count : 256);
     const long long base = (long long)qb * ATT_NW * nh;
     int nsplit = (int)((want + base - 1) / base);
     int tps;
 
-    nsplit = max(1, min(nsplit, min(ntiles, 64)));
+    nsplit = max(1, min(nsplit, min(ntiles / 2, 64)));
     tps = ntiles > 0 ? (ntiles + nsplit - 1) / nsplit : 0;
     nsplit = tps > 0 ? (ntiles + tps - 1) / tps : 1;
     if (nsplit == 1) {
