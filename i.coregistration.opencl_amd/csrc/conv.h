@@ -41,16 +41,19 @@ void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,
 bool conv_wino_supported(int kh, int kw, int sy, int sx, int py, int px,
                          int dy, int dx, int groups, int C, int K, int Ho,
                          int Wo);
-/* Floats of the transformed filters U ([16][C][K]). */
-size_t conv_wino_weight_floats(int K, int C);
-/* U from w (K, C, 3, 3). */
-void conv_wino_weights(const float *w, int K, int C, float *U, hipStream_t s);
-/* The convolution of a (a.w unused) with filters U, nb images. */
+/* Floats of the transformed filters U for a convolution with (norm) or
+ * without input normalisation: MFMA fragment order when C % 8 == 0 and no
+ * normalisation, else [16][C][K]. */
+size_t conv_wino_weight_floats(int K, int C, bool norm);
+/* U from w (K, C, 3, 3), in the order conv_wino_weight_floats names. */
+void conv_wino_weights(const float *w, int K, int C, bool norm, float *U, hipStream_t s);
+/* The convolution of a (a.w unused) with filters U from conv_wino_weights
+ * with norm = (a.mean != NULL), nb images. */
 void conv_wino_launch(const conv_args &a, const float *U, int nb,
                       hipStream_t s);
 
-/* Filters of a 3 x 3 convolution transformed once (a new buffer), for
- * callers that run the same weights many times. */
+/* Filters of a 3 x 3 convolution without input normalisation transformed
+ * once (a new buffer), for callers that run the same weights many times. */
 cl_mem conv_wino_prepare(struct ops *o, cl_mem w, int K, int C);
 /* ops_conv2d_batch for 3 x 3, stride 1, padding 1, one group, with U
  * from conv_wino_prepare (w is used only when the Winograd path does not

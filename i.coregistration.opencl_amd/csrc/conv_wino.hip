@@ -16,6 +16,11 @@
  * 2016). The channel sums are 16 GEMMs, one per position (xi, nu) of the
  * 4 x 4 transform: M[xi nu](k, t) = sum_c U[xi nu](k, c) V[xi nu](c, t).
  *
+ * Two kernels. conv_wino_rows_kernel (further down) takes convolutions
+ * without input normalisation over whole 8-channel slices: each wave forms
+ * its own row of the transform in registers. conv_wino_kernel, the staged
+ * form, takes the rest:
+ *
  * wino_weights_kernel writes U as [16][C][K]. conv_wino_kernel: a block
  * takes 32 tiles (a 4 x 8 grid of 2 x 2 output tiles, 8 x 16 pixels; the
  * template also allows 8 x 8 tiles) of one image and 32 output channels,
@@ -344,6 +349,332 @@ __global__ void __launch_bounds__(256, MINW)
     }
 }
 
+/* ---- Row-split form -------------------------------------------------
+ *
+ * Row xi of V = B^T d B needs only two rows of the tile (B^T row xi has two
+ * non-zeros), so wave xi of a block forms the transform values of its own
+ * four GEMMs (positions (xi, nu)) directly from the input patch in LDS, in
+ * the lane order of the MFMA B operand, and never writes V back: no V
+ * round trip through LDS and no barrier between transform and product. The
+ * transformed filters come from global memory (L2) straight into the A
+ * operand registers, stored in that operand's lane order (wino_frag_kernel);
+ * the input patch goes to LDS by LDS DMA (buffer_load ... lds), two slices
+ * in flight (double buffer), one barrier per slice of 8 input channels.
+ *
+ * Patch layouts in LDS (per slice: 8 channels x 10 rows x 18 columns used):
+ *  - 16-byte DMA (W % 4 == 0, 16-byte aligned input): columns fetched in
+ *    aligned groups of 4 from 2 tx0 - 4 (a group lies wholly inside or
+ *    wholly outside the image row, so zero padding is exact), 24 floats a
+ *    row, 240 a channel; the patch column -1 is at offset 3;
+ *  - 4-byte DMA (other widths): one load per row pair (lanes 0-31 row 2i,
+ *    32-63 row 2i + 1), pairs 80 floats apart so the four tile rows of a
+ *    wave read from different banks, 400 floats a channel.
+ *
+ * Filter fragments Uf[kb][sl][xi][nu][lane][s]: lane = (c & 1) * 32 + k % 32,
+ * s = (c % 8) / 2, output channel block kb = k / 32, slice sl = c / 8; zero
+ * for k >= K. Row xi = 2 is stored negated, which lets every wave form its
+ * row as u = d[ra] + be * d[rb] with one FMA. */
+
+#define WR_CC 8
+
+static __device__ __forceinline__ int wr_nslices(int C) { return (C + WR_CC - 1) / WR_CC; }
+
+__global__ void __launch_bounds__(256)
+    wino_frag_kernel(const float *__restrict__ w, int K, int C, int Kp,
+                     float *__restrict__ Uf)
+{
+    const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int nsl = wr_nslices(C);
+
+    if (id >= (long long)Kp * nsl * WR_CC)
+        return;
+    {
+        const int k = (int)(id % Kp), c = (int)(id / Kp);
+        float u[16];
+
+        if (k < K && c < C) {
+            const float *src = w + ((long long)k * C + c) * 9;
+            float g[9], t[4][3];
+
+#pragma unroll
+            for (int i = 0; i < 9; i++)
+                g[i] = src[i];
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                const float g0 = g[j], g1 = g[3 + j], g2 = g[6 + j];
+
+                t[0][j] = g0;
+                t[1][j] = 0.5f * (g0 + g1 + g2);
+                t[2][j] = 0.5f * (g0 - g1 + g2);
+                t[3][j] = g2;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float a0 = t[i][0], a1 = t[i][1], a2 = t[i][2];
+                const float sg = i == 2 ? -1.0f : 1.0f;
+
+                u[i * 4 + 0] = sg * a0;
+                u[i * 4 + 1] = sg * 0.5f * (a0 + a1 + a2);
+                u[i * 4 + 2] = sg * 0.5f * (a0 - a1 + a2);
+                u[i * 4 + 3] = sg * a2;
+            }
+        }
+        else {
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                u[i] = 0.0f;
+        }
+        {
+            const int kb = k / 32, col = k % 32, sl = c / WR_CC, cc = c % WR_CC;
+            const int s = cc / 2, lane = (cc & 1) * 32 + col;
+            float *dst = Uf + ((long long)kb * nsl + sl) * 16 * 256 + lane * 4 + s;
+
+#pragma unroll
+            for (int p = 0; p < 16; p++)
+                dst[p * 256] = u[p];
+        }
+    }
+}
+
+/* gfx9 s_waitcnt immediates: vmcnt(0) alone; vmcnt(0) and lgkmcnt(0). */
+#define WR_WAIT_VM0 0x0F70
+#define WR_WAIT_VM0_LGKM0 0x0070
+
+template <bool X4>
+__global__ void __launch_bounds__(256, 4)
+    conv_wino_rows_kernel(const conv_args a, const float *__restrict__ Uf)
+{
+    constexpr int TR = 4, TC = 8, BK = 32;
+    /* Per-slice patch buffer (floats) and pitches of the two layouts. */
+    constexpr int PSZ = X4 ? 2048 : WR_CC * 400;
+    constexpr int CPITCH = X4 ? 240 : 400;
+    /* Two patch buffers; the output transform reuses the first 8192. */
+    __shared__ __align__(16) float lds[2 * PSZ > 8192 ? 2 * PSZ : 8192];
+    float *const P0 = lds, *const P1 = lds + PSZ;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int half = lane >> 5, col = lane & 31;
+    const int tr = col >> 3, tc = col & 7;
+    const int C = a.C, H = a.H, W = a.W, K = a.K;
+    const int tiles_w = (W + 1) / 2, bw = (tiles_w + TC - 1) / TC;
+    const int ty0 = (blockIdx.y / bw) * TR, tx0 = (blockIdx.y % bw) * TC;
+    const int k0 = blockIdx.x * BK;
+    const int iy0 = 2 * ty0 - 1, ix0 = 2 * tx0 - 1;
+    const long long HW = (long long)H * W;
+    const float *in = a.in + (long long)blockIdx.z * a.in_stride;
+    const unsigned long long ibytes = (unsigned long long)C * HW * 4;
+    const int nk = (C + WR_CC - 1) / WR_CC;
+    /* This wave's filter fragments: 16 floats a lane, 4096 a slice. */
+    const float *uf = Uf + ((long long)blockIdx.x * nk * 16 + wave * 4) * 256 + lane * 4;
+    /* Rows of the tile that row xi of B^T combines: u = d[ra] + be d[rb]
+     * (row 2 negated in the filters). */
+    const int ra = wave == 0 ? 0 : 1, rb = wave == 3 ? 3 : 2;
+    const float be = wave == 1 ? 1.0f : -1.0f;
+    floatx16 acc[4];
+    float ruA[16], ruB[16];
+    unsigned doff[2], rmask = 0;
+
+#pragma unroll
+    for (int v = 0; v < 4; v++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+            acc[v][r] = 0.0f;
+
+    if (X4) {
+        /* 16-byte chunk e of the slice: channel e / 60, row (e % 60) / 6,
+         * group e % 6 of 4 columns from 2 tx0 - 4; to floats 4e. */
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int e = tid + 256 * q, c = e / 60, rem = e - c * 60;
+            const int r = rem / 6, g = rem - r * 6;
+            const int iy = iy0 + r, ix = 2 * tx0 - 4 + 4 * g;
+
+            doff[q] = c < WR_CC && iy >= 0 && iy < H && ix >= 0 && ix < W
+                          ? (unsigned)((c * HW + (long long)iy * W + ix) * 4)
+                          : WG_OOB;
+        }
+    }
+    else {
+        /* Lane: row 2 i + half of pair i, patch column col; the offset is
+         * taken from a window W + 1 floats before the slice (never
+         * negative), the channel and pair terms go in soffset. */
+        const bool col_ok = col < 2 * TC + 2 && ix0 + col >= 0 && ix0 + col < W;
+
+#pragma unroll
+        for (int i = 0; i < 5; i++) {
+            const int iy = iy0 + 2 * i + half;
+
+            rmask |= col_ok && iy >= 0 && iy < H ? 1u << i : 0u;
+        }
+        doff[0] = (unsigned)(((iy0 + half) * W + ix0 + col + W + 1) * 4);
+        doff[1] = 0;
+    }
+
+    auto load_patch = [&](int c0, float *P) {
+        if (X4) {
+            const __amdgpu_buffer_rsrc_t ri =
+                wg_rsrc(in + (long long)c0 * HW, ibytes - (unsigned long long)c0 * HW * 4);
+
+#pragma unroll
+            for (int q = 0; q < 2; q++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ri, (__attribute__((address_space(3))) void *)(P + 1024 * q + 256 * wave),
+                    16, (int)doff[q], 0, 0, 0);
+        }
+        else {
+            const __amdgpu_buffer_rsrc_t ri =
+                wg_rsrc(in + (long long)c0 * HW - (W + 1),
+                        ibytes - (unsigned long long)c0 * HW * 4 + (unsigned long long)(W + 1) * 4);
+
+#pragma unroll
+            for (int cc = 0; cc < 2; cc++)
+#pragma unroll
+                for (int i = 0; i < 5; i++) {
+                    const int c = 2 * wave + cc;
+
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        ri, (__attribute__((address_space(3))) void *)(P + c * 400 + i * 80), 4,
+                        (int)((rmask >> i) & 1u ? doff[0] : WG_OOB),
+                        (int)((c * HW + 2 * i * W) * 4), 0, 0);
+                }
+        }
+    };
+    auto load_u = [&](int kt, float *ru) {
+        const float *p = uf + (long long)kt * 16 * 256;
+
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const float4 t = *(const float4 *)(p + v * 256);
+
+            ru[v * 4 + 0] = t.x;
+            ru[v * 4 + 1] = t.y;
+            ru[v * 4 + 2] = t.z;
+            ru[v * 4 + 3] = t.w;
+        }
+    };
+    /* Slice kt from patch buffer Pc, filters ru; the next slice's patch
+     * (to Pn) and filters (to rn) are loaded meanwhile. */
+    auto step = [&](int kt, const float *__restrict__ Pc, float *__restrict__ Pn, float *ru,
+                    float *rn) {
+        const bool more = kt + 1 < nk;
+        float bv[4][4];
+
+        /* ru arrived before the last barrier. Redefining it here (an empty
+         * asm) keeps the compiler from placing a wait for the loads issued
+         * below in front of the products. */
+        asm volatile(""
+                     : "+v"(ru[0]), "+v"(ru[1]), "+v"(ru[2]), "+v"(ru[3]), "+v"(ru[4]),
+                       "+v"(ru[5]), "+v"(ru[6]), "+v"(ru[7]), "+v"(ru[8]), "+v"(ru[9]),
+                       "+v"(ru[10]), "+v"(ru[11]), "+v"(ru[12]), "+v"(ru[13]), "+v"(ru[14]),
+                       "+v"(ru[15]));
+        if (more) {
+            load_patch((kt + 1) * WR_CC, Pn);
+            load_u(kt + 1, rn);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const int c = 2 * s + half;
+            float da[4], db[4], u[4];
+
+            if (X4) {
+                const float *p = Pc + c * CPITCH + 2 * tr * 24 + 3 + 2 * tc;
+
+#pragma unroll
+                for (int x = 0; x < 4; x++) {
+                    da[x] = p[ra * 24 + x];
+                    db[x] = p[rb * 24 + x];
+                }
+            }
+            else {
+                const float *p = Pc + c * CPITCH + tr * 80 + 2 * tc;
+                const float *pa = p + (ra >> 1) * 80 + (ra & 1) * 32;
+                const float *pb = p + (rb >> 1) * 80 + (rb & 1) * 32;
+                const float2 a0 = *(const float2 *)pa, a1 = *(const float2 *)(pa + 2);
+                const float2 b0 = *(const float2 *)pb, b1 = *(const float2 *)(pb + 2);
+
+                da[0] = a0.x, da[1] = a0.y, da[2] = a1.x, da[3] = a1.y;
+                db[0] = b0.x, db[1] = b0.y, db[2] = b1.x, db[3] = b1.y;
+            }
+#pragma unroll
+            for (int x = 0; x < 4; x++)
+                u[x] = __builtin_fmaf(be, db[x], da[x]);
+            bv[s][0] = u[0] - u[2];
+            bv[s][1] = u[1] + u[2];
+            bv[s][2] = u[2] - u[1];
+            bv[s][3] = u[1] - u[3];
+        }
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                acc[v] = __builtin_amdgcn_mfma_f32_32x32x2f32(ru[v * 4 + s], bv[s][v], acc[v], 0,
+                                                              0, 0);
+        /* The next slice's patch and filters have landed (LDS DMA is
+         * counted in vmcnt), then everyone's reads of Pc are done. */
+        __builtin_amdgcn_s_waitcnt(WR_WAIT_VM0);
+        __syncthreads();
+    };
+
+    load_patch(0, P0);
+    load_u(0, ruA);
+    __builtin_amdgcn_s_waitcnt(WR_WAIT_VM0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(kt, P0, P1, ruA, ruB);
+        if (kt + 1 < nk)
+            step(kt + 1, P1, P0, ruB, ruA);
+    }
+
+    /* Output transform as in conv_wino_kernel: Z = M A over nu in
+     * registers, Y = A^T Z over xi through LDS. */
+    {
+        float *Zs = lds; /* [xi][j][k][t32] */
+        float *out = a.out + (long long)blockIdx.z * a.out_stride;
+
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int k = (r >> 2) * 8 + half * 4 + (r & 3);
+            const float z0 = acc[0][r] + acc[1][r] + acc[2][r];
+            const float z1 = acc[1][r] - acc[2][r] - acc[3][r];
+
+            Zs[((wave * 2 + 0) * BK + k) * 32 + col] = z0;
+            Zs[((wave * 2 + 1) * BK + k) * 32 + col] = z1;
+        }
+        __syncthreads();
+        {
+            const int ts = tid & 31, otr = ts / TC, otc = ts % TC;
+            const int oy = 2 * (ty0 + otr), ox = 2 * (tx0 + otc);
+
+#pragma unroll
+            for (int i = 0; i < BK / 8; i++) {
+                const int k = (tid >> 5) + 8 * i, kg = k0 + k;
+                const float bias = a.bias && kg < K ? a.bias[kg] : 0.0f;
+
+                if (kg >= K)
+                    continue;
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float z0 = Zs[((0 * 2 + j) * BK + k) * 32 + ts];
+                    const float z1 = Zs[((1 * 2 + j) * BK + k) * 32 + ts];
+                    const float z2 = Zs[((2 * 2 + j) * BK + k) * 32 + ts];
+                    const float z3 = Zs[((3 * 2 + j) * BK + k) * 32 + ts];
+                    const float y0 = z0 + z1 + z2, y1 = z1 - z2 - z3;
+
+                    if (ox + j >= a.Wo)
+                        continue;
+                    if (oy < a.Ho)
+                        out[((long long)kg * a.Ho + oy) * a.Wo + ox + j] =
+                            icoreg_act(y0 + bias, a.act, a.slope);
+                    if (oy + 1 < a.Ho)
+                        out[((long long)kg * a.Ho + oy + 1) * a.Wo + ox + j] =
+                            icoreg_act(y1 + bias, a.act, a.slope);
+                }
+            }
+        }
+    }
+}
+
 /* Blocks of 8 x 16 output pixels (the larger block's 16 x 16 on a
  * different grid, always fewer). */
 static long long wino_blocks(int Ho, int Wo, int tr)
@@ -361,14 +692,30 @@ bool conv_wino_supported(int kh, int kw, int sy, int sx, int py, int px,
            K >= 32 && wino_blocks(Ho, Wo, 4) <= 65535;
 }
 
-size_t conv_wino_weight_floats(int K, int C) { return 16ULL * K * C; }
+/* The row-split kernel takes whole 8-channel slices and no input
+ * normalisation; the staged kernel takes the rest. */
+static bool wino_rows(int C, bool norm) { return C % WR_CC == 0 && !norm; }
 
-void conv_wino_weights(const float *w, int K, int C, float *U, hipStream_t s)
+size_t conv_wino_weight_floats(int K, int C, bool norm)
 {
-    const long long n = (long long)K * C;
+    return wino_rows(C, norm) ? (size_t)((K + 31) / 32 * 32) * C * 16 : 16ULL * K * C;
+}
 
-    hipLaunchKernelGGL(wino_weights_kernel, dim3((unsigned)((n + 255) / 256)),
-                       dim3(256), 0, s, w, K, C, U);
+void conv_wino_weights(const float *w, int K, int C, bool norm, float *U, hipStream_t s)
+{
+    if (wino_rows(C, norm)) {
+        const int Kp = (K + 31) / 32 * 32;
+        const long long n = (long long)Kp * C;
+
+        hipLaunchKernelGGL(wino_frag_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                           w, K, C, Kp, U);
+    }
+    else {
+        const long long n = (long long)K * C;
+
+        hipLaunchKernelGGL(wino_weights_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                           s, w, K, C, U);
+    }
 }
 
 template <int TR, int CC, int MINW>
@@ -389,6 +736,19 @@ static void wino_launch(const conv_args &a, const float *U, int nb,
 void conv_wino_launch(const conv_args &a, const float *U, int nb,
                       hipStream_t s)
 {
+    if (wino_rows(a.C, a.mean != nullptr)) {
+        /* Row-split kernel; 16-byte patch loads when every image row
+         * starts 16-byte aligned. */
+        const dim3 grid((a.K + 31) / 32, (unsigned)wino_blocks(a.Ho, a.Wo, 4), nb);
+        const bool x4 = a.W % 4 == 0 && a.in_stride % 4 == 0 &&
+                        ((unsigned long long)(size_t)a.in) % 16 == 0;
+
+        if (x4)
+            hipLaunchKernelGGL(conv_wino_rows_kernel<true>, grid, dim3(256), 0, s, a, U);
+        else
+            hipLaunchKernelGGL(conv_wino_rows_kernel<false>, grid, dim3(256), 0, s, a, U);
+        return;
+    }
     /* 32 tiles x 32 channels per block, 8 input channels per slice,
      * registers capped for 4 waves per SIMD: the 38 KB of LDS and the
      * extra waves in flight beat the larger blocks (64 tiles, or 16

@@ -365,7 +365,7 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
     if (conv_wino_supported(g->kh, g->kw, g->sy, g->sx, g->py, g->px, g->dy,
                             g->dx, g->groups, C, K, Ho, Wo) &&
         conv_direct_fits((long long)C * H * W,
-                         (long long)conv_wino_weight_floats(K, C))) {
+                         (long long)conv_wino_weight_floats(K, C, mean != nullptr))) {
         /* 3 x 3, stride 1, same size: Winograd F(2 x 2, 3 x 3). */
         conv_args a;
 
@@ -388,14 +388,21 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
         a.act = act;
         a.slope = slope;
         if (!U) {
-            U = scratch_get(o, conv_wino_weight_floats(K, C) * sizeof(float));
+            U = scratch_get(o, conv_wino_weight_floats(K, C, mean != nullptr) *
+                                   sizeof(float));
             prof_scope ps(o->ocl, "conv_wino_weights");
-            conv_wino_weights(cfptr(w), K, C, fptr(U), stream_of(o->ocl));
+            conv_wino_weights(cfptr(w), K, C, mean != nullptr, fptr(U),
+                              stream_of(o->ocl));
             launch_check("conv_wino_weights");
         }
         else {
-            need_floats(U, 0, (long long)conv_wino_weight_floats(K, C), op,
-                        "Winograd filters");
+            /* Prepared filters are in the order of a convolution without
+             * input normalisation. */
+            if (mean)
+                icoreg_fatal("%s: prepared Winograd filters with input "
+                             "normalisation", op);
+            need_floats(U, 0, (long long)conv_wino_weight_floats(K, C, false),
+                        op, "Winograd filters");
         }
         prof_scope ps(o->ocl, "conv_wino");
         conv_wino_launch(a, cfptr(U), nb, stream_of(o->ocl));
@@ -523,9 +530,9 @@ cl_mem conv_wino_prepare(struct ops *o, cl_mem w, int K, int C)
     cl_mem U;
 
     need_floats(w, 0, (long long)K * C * 9, "conv_wino_prepare", "weights");
-    U = ocl_alloc(o->ocl, conv_wino_weight_floats(K, C) * sizeof(float),
+    U = ocl_alloc(o->ocl, conv_wino_weight_floats(K, C, false) * sizeof(float),
                   "Winograd filters");
-    conv_wino_weights(cfptr(w), K, C, fptr(U), stream_of(o->ocl));
+    conv_wino_weights(cfptr(w), K, C, false, fptr(U), stream_of(o->ocl));
     launch_check("conv_wino_weights");
     return U;
 }

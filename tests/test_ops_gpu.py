@@ -96,6 +96,10 @@ CONV_SHAPES = [
     # sizes, a partial block of output channels.
     (2, 50, 31, 35, 44, 3, 1, 1, 1, 2),
     (1, 33, 9, 7, 36, 3, 1, 1, 0, 0),
+    # Row-split Winograd: 4-byte patch loads (W % 4 != 0) and 16-byte ones,
+    # an odd number of 8-channel slices, a partial block of output channels.
+    (2, 40, 23, 37, 40, 3, 1, 1, 0, 2),
+    (1, 72, 18, 28, 36, 3, 1, 1, 0, 1),
 ]
 
 
