@@ -394,6 +394,142 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
     }
 }
 
+/* Small products (few output tiles, K <= 256): one 32 x 32 output tile per
+ * block of 8 waves. Both operand panels (32 x K of A, K x 32 of B) are
+ * loaded to LDS at once, the 8 waves split K into eighths and their
+ * partial tiles are summed through LDS. For the q / kv / o projections of
+ * aggregated attention (a few hundred tokens, K = 256) the main kernel
+ * leaves most CUs idle and waits on 16 dependent slice loads per tile;
+ * here every block has one load round trip and K / 16 MFMA steps. */
+#define GEMM_SK_MAXK 256
+
+template <int MODE>
+__global__ void __launch_bounds__(512) gemm_smallk(const gemm_args g)
+{
+    constexpr int NTH = 512, T = 32;
+    /* Row-major panels as loaded (no transposing stores): A [m][k] and B
+     * given N x K as [n][k], K + 2 floats a row, so the 32 lanes of an
+     * MFMA operand (32 rows, one k) fall in 32 different even banks and
+     * lanes 32-63 (k + 1) in the odd ones; B given K x N as [k][n]. */
+    constexpr int P = GEMM_SK_MAXK + 2;
+    __shared__ __align__(16) float As[T * P], Bs[T * P];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tiles_n = (g.N + T - 1) / T;
+    const int m0 = (blockIdx.x / tiles_n) * T, n0 = (blockIdx.x % tiles_n) * T;
+    const long long bt = blockIdx.y, b0 = bt / g.nb1, b1 = bt % g.nb1;
+    const float *A = g.A + b0 * g.sa0 + b1 * g.sa1;
+    const float *B = g.B + b0 * g.sb0 + b1 * g.sb1;
+    const int M = g.M, N = g.N, K = g.K, KQ = K / 4, pk = K + 2;
+    const int rows_a = min(T, M - m0), cols_b = min(T, N - n0);
+    const long long lda = g.lda, ldb = g.ldb;
+    floatx16 acc;
+
+    /* Panels: 16-byte loads through windows ending at the last row inside
+     * the matrix (rows past it read 0), all issued before the first LDS
+     * store. At most 32 x 256 / 4 / 512 = 4 per thread and operand. */
+    {
+        constexpr int NL = GEMM_SK_MAXK * T / 4 / NTH;
+        const __amdgpu_buffer_rsrc_t wa =
+            gemm_rsrc(A + m0 * lda, ((rows_a - 1) * lda + K) * 4);
+        const __amdgpu_buffer_rsrc_t wb =
+            MODE == GEMM_B_NK ? gemm_rsrc(B + n0 * ldb, ((cols_b - 1) * ldb + K) * 4)
+                              : gemm_rsrc(B + n0, ((K - 1) * ldb + cols_b) * 4);
+        const int nq4 = T * KQ; /* float4 groups per panel */
+        float4 va[NL], vb[NL];
+
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const int q = tid + i * NTH, row = q / KQ, kq = (q % KQ) * 4;
+
+            va[i] = q < nq4 ? gemm_load4<true>(wa, (unsigned)((row * lda + kq) * 4))
+                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (MODE == GEMM_B_NK) {
+                vb[i] = q < nq4 ? gemm_load4<true>(wb, (unsigned)((row * ldb + kq) * 4))
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+            else {
+                const int kk = q / (T / 4), nq = (q % (T / 4)) * 4;
+
+                /* Columns past N of rows before the window's last read
+                 * the next row. */
+                vb[i] = q < nq4 ? mask4(gemm_load4<true>(wb, (unsigned)((kk * ldb + nq) * 4)),
+                                        nq, cols_b)
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const int q = tid + i * NTH, row = q / KQ, kq = (q % KQ) * 4;
+
+            if (q >= nq4)
+                continue;
+            *(float2 *)&As[row * pk + kq] = make_float2(va[i].x, va[i].y);
+            *(float2 *)&As[row * pk + kq + 2] = make_float2(va[i].z, va[i].w);
+            if (MODE == GEMM_B_NK) {
+                *(float2 *)&Bs[row * pk + kq] = make_float2(vb[i].x, vb[i].y);
+                *(float2 *)&Bs[row * pk + kq + 2] = make_float2(vb[i].z, vb[i].w);
+            }
+            else {
+                const int kk = q / (T / 4), nq = (q % (T / 4)) * 4;
+
+                *(float4 *)&Bs[kk * T + nq] = vb[i];
+            }
+        }
+    }
+    __syncthreads();
+
+    /* Wave w: k in [w K / 8, (w + 1) K / 8). */
+    for (int r = 0; r < 16; r++)
+        acc[r] = 0.0f;
+    {
+        const int kw = K / 8, kb = wave * kw, kh = lane >> 5, c = lane & 31;
+
+        for (int ks = 0; ks < kw; ks += 2) {
+            const int kr = kb + ks + kh;
+            const float bvl = MODE == GEMM_B_NK ? Bs[c * pk + kr] : Bs[kr * T + c];
+
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[c * pk + kr], bvl, acc, 0, 0, 0);
+        }
+    }
+    __syncthreads();
+    /* Partial tiles [w][row][col] over the A panel, then the sum of the 8
+     * per output in the fixed order w = 0..7. */
+    {
+        float *Ps = As;
+
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+
+            Ps[(wave * T + row) * T + (lane & 31)] = acc[r];
+        }
+    }
+    __syncthreads();
+    {
+        float *C = g.C + b0 * g.sc0 + b1 * g.sc1;
+        const float *R = g.R ? g.R + b0 * g.sc0 + b1 * g.sc1 : nullptr;
+
+        for (int e = tid; e < T * T; e += NTH) {
+            const int row = e / T, col = e % T, gr = m0 + row, gc = n0 + col;
+            float v = 0.0f;
+
+            if (gr >= M || gc >= N)
+                continue;
+#pragma unroll
+            for (int w = 0; w < 8; w++)
+                v += As[(w * T + row) * T + col];
+            v *= g.alpha;
+            if (g.bias)
+                v += g.bias[g.biasrow ? gr : gc];
+            v = icoreg_act(v, g.act, g.slope);
+            if (R)
+                v += R[(long long)gr * g.ldc + gc];
+            C[(long long)gr * g.ldc + gc] = v;
+        }
+    }
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, int MODE>
 static void launch_mode(const gemm_args &g, int nb, bool va, bool vb,
                         hipStream_t s)
@@ -468,6 +604,22 @@ void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
      * ELoFTR pipelines (operands fresh from the previous kernel) they
      * were 5-70 % slower on the same shapes, so the kernel's WGM x WGN
      * generality is not used here. */
-    (void)cus;
+    {
+        /* Small products that would fill under half of the CUs with 64 x
+         * 64 tiles: the one-shot small-K kernel. */
+        const long long tiles64 =
+            (long long)((g.M + 63) / 64) * ((g.N + 63) / 64) * nb;
+
+        if (bmode != GEMM_B_CONV && va && vb && g.K <= GEMM_SK_MAXK && g.K % 16 == 0 &&
+            g.ksplit == 0 && 2 * tiles64 <= cus) {
+            const dim3 grid(((g.M + 31) / 32) * ((g.N + 31) / 32), nb);
+
+            if (bmode == GEMM_B_NK)
+                hipLaunchKernelGGL(gemm_smallk<GEMM_B_NK>, grid, dim3(512), 0, s, g);
+            else
+                hipLaunchKernelGGL(gemm_smallk<GEMM_B_KN>, grid, dim3(512), 0, s, g);
+            return;
+        }
+    }
     launch_cfg<64, 64, 16, 2, 2>(g, bmode, nb, va, vb, s);
 }
