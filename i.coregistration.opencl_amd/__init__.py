@@ -153,6 +153,7 @@ SIGNATURES = {
     "eloftr_conf_row": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
     "eloftr_conf_col": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
     "eloftr_fine": (None, [_O, Mem, Mem, _I, _I, Mem, _I, _F, Mem]),
+    "eloftr_fine_half": (None, [_O, Mem, Mem, _I, _I, Mem, _I, _F, Mem]),
     "roma_row_norm": (None, [_O, Mem, _I, _I, Mem]),
     "roma_cos_exp": (None, [_O, Mem, Mem, Mem, _I, _I, _F, _F]),
     "roma_cls_to_flow": (None, [_O, Mem, _I, _I, _I, _I, Mem, Mem]),

@@ -389,6 +389,8 @@ extern "C" void eloftr_alloc(struct eloftr_model *m, int H, int W)
     m->fu_a = walloc(m, 2 * 32 * hw, "fusion");
     m->fu_b = walloc(m, 2 * 32 * hw, "fusion");
     m->fu_c = walloc(m, 2 * 32 * hw, "fusion");
+    for (int k = 0; k < 2; k++)
+        m->fine_h[k] = view(m->fu_c, k, (size_t)ELOFTR_FINE_DIM * (m->H / 2) * (m->W / 2));
     m->nmax = (int)n;
     m->m_idx = ocl_alloc(m->ocl, n * 4 * sizeof(int), "match cells");
     m->m_out = walloc(m, n * 4, "fine matches");
@@ -597,31 +599,52 @@ static void conv1x1_pair(struct eloftr_model *m, cl_mem X, int C, int HW,
              ACT_NONE, 0);
 }
 
-/* FPN fusion of both images into finep (64, H, W) each, every layer one
- * launch for the pair (the pair's channels are contiguous, so resizes and
- * sums run over 2 C channels). eloftr.c:573-604. */
+/* conv1x1_pair plus the 2x bilinear resize of Rlow (K x HW / 4 per image,
+ * K HW / 4 floats apart) as the residual: the reference's ops_resize and
+ * residual add after the 1 x 1 convolution, without the upsampled map. */
+static void conv1x1_up2_pair(struct eloftr_model *m, cl_mem X, int C, int H, int W,
+                             cl_mem Wt, int K, cl_mem Y, cl_mem Rlow)
+{
+    const long HW = (long)H * W;
+
+    ops_gemm_up2res(m->ops, K, (int)HW, C, ops_mat(Wt, 0, C),
+                    ops_bmat(X, 0, HW, (long)C * HW, 0), ops_bmat(Y, 0, HW, (long)K * HW, 0),
+                    2, Rlow, (long)K * (HW / 4), H, W);
+}
+
+/* FPN fusion of both images (eloftr.c:573-604), every layer one launch for
+ * the pair (the pair's channels are contiguous). The reference's three 2x
+ * resizes are sampled on the fly by their consumers, with the resize's
+ * arithmetic: the residuals of the two 1 x 1 convolutions
+ * (ops_gemm_up2res) and fine matching (eloftr_fine_half). The result is
+ * fu_c, the fine maps at half resolution (64, H / 2, W / 2) per image. */
 static void fusion(struct eloftr_model *m)
 {
-    struct ops *o = m->ops;
     const int h = m->h, w = m->w;
     const int H4 = 2 * h, W4 = 2 * w, H2 = 4 * h, W2 = 4 * w;
 
     conv1x1_pair(m, m->xp, 256, h * w, m->f_out, 256, m->fu_a);
-    ops_resize(o, m->fu_a, 2 * 256, h, w, m->fu_b, H4, W4, 0, 0, 2.0f);
-    conv1x1_pair(m, m->f2p, 128, H4 * W4, m->f1_w[0], 256, m->fu_c, m->fu_b);
+    conv1x1_up2_pair(m, m->f2p, 128, H4, W4, m->f1_w[0], 256, m->fu_c, m->fu_a);
     conv3x3_pair(m, m->fu_c, 256L * H4 * W4, 256, H4, W4, m->f2_w[0],
                  m->f2_b[0], 256, 1, ACT_LEAKY, m->fu_a, 256L * H4 * W4,
                  m->f2_U[0]);
     conv3x3_pair(m, m->fu_a, 256L * H4 * W4, 256, H4, W4, m->f3_w[0], NULL,
                  128, 1, ACT_NONE, m->fu_b, 128L * H4 * W4, m->f3_U[0]);
-    ops_resize(o, m->fu_b, 2 * 128, H4, W4, m->fu_c, H2, W2, 0, 0, 2.0f);
-    conv1x1_pair(m, m->f1p, 64, H2 * W2, m->f1_w[1], 128, m->fu_a, m->fu_c);
+    conv1x1_up2_pair(m, m->f1p, 64, H2, W2, m->f1_w[1], 128, m->fu_a, m->fu_b);
     conv3x3_pair(m, m->fu_a, 128L * H2 * W2, 128, H2, W2, m->f2_w[1],
                  m->f2_b[1], 128, 1, ACT_LEAKY, m->fu_b, 128L * H2 * W2,
                  m->f2_U[1]);
     conv3x3_pair(m, m->fu_b, 128L * H2 * W2, 128, H2, W2, m->f3_w[1], NULL, 64,
                  1, ACT_NONE, m->fu_c, 64L * H2 * W2, m->f3_U[1]);
-    ops_resize(o, m->fu_c, 2 * 64, H2, W2, m->finep, m->H, m->W, 0, 0, 2.0f);
+    /* The reference resizes fu_c 2x into the fine maps here; fine
+     * matching samples that resize on the fly instead, and finep is
+     * written only when asked for (eloftr_fine_maps). */
+}
+
+extern "C" void eloftr_fine_maps(struct eloftr_model *m)
+{
+    ops_resize(m->ops, m->fu_c, 2 * ELOFTR_FINE_DIM, m->H / 2, m->W / 2, m->finep, m->H,
+               m->W, 0, 0, 2.0f);
 }
 
 static void fine_match(struct eloftr_model *m)
@@ -639,8 +662,8 @@ static void fine_match(struct eloftr_model *m)
     }
     ocl_write(m->ocl, m->m_idx, 0, cells, (size_t)m->nm * 4 * sizeof(int));
     free(cells);
-    eloftr_fine(m->ops, m->fine[0], m->fine[1], m->H, m->W, m->m_idx, m->nm,
-                FINE_T, m->m_out);
+    eloftr_fine_half(m->ops, m->fine_h[0], m->fine_h[1], m->H, m->W, m->m_idx, m->nm,
+                     FINE_T, m->m_out);
     ocl_read(m->ocl, m->m_out, 0, m->kp, (size_t)m->nm * 4 * sizeof(float));
 }
 
@@ -687,6 +710,7 @@ static void match_stages(struct eloftr_model *m, cl_mem dev0, cl_mem dev1,
     coarse_match(m);
     fusion(m);
     if (dump) {
+        eloftr_fine_maps(m);
         dump_dev(m, dump, tile, "fine_0", m->fine[0], ELOFTR_FINE_DIM * hw);
         dump_dev(m, dump, tile, "fine_1", m->fine[1], ELOFTR_FINE_DIM * hw);
     }
@@ -719,7 +743,8 @@ extern "C" void eloftr_free(struct eloftr_model *m)
 {
     cl_mem *all[] = {
         &m->f1[0],   &m->f1[1],   &m->f2[0],   &m->f2[1], &m->x[0],
-        &m->x[1],    &m->fine[0], &m->fine[1], &m->img,   &m->s_a,
+        &m->x[1],    &m->fine[0], &m->fine[1], &m->fine_h[0], &m->fine_h[1],
+        &m->img,     &m->s_a,
         &m->s_b,     &m->f1p,     &m->f2p,     &m->xp,    &m->finep,
         &m->t_qn,    &m->t_kvn,   &m->t_Q,     &m->t_KV,  &m->t_O,
         &m->t_O2,

@@ -23,6 +23,7 @@
 
 #include <math.h>
 
+#include "bilinear.h"
 #include "common.h"
 #include "icoreg_kernels.h"
 #include "reduce.h"
@@ -362,6 +363,10 @@ extern "C" void eloftr_conf_col(struct ops *o, cl_mem S, int R, int N, int r0,
 #define WP (FC + 1)    /* LDS row pitch of the windows */
 #define SP (NQ + 1)    /* LDS row pitch of the scores */
 
+/* UP2: f0 and f1 hold the features at half resolution (H / 2 x W / 2)
+ * and each window value is their 2x bilinear resize (bl_up2, the resize
+ * kernel's arithmetic), so the full-resolution maps need not exist. */
+template <bool UP2>
 __global__ void __launch_bounds__(256)
     fine_kernel(const float *__restrict__ f0, const float *__restrict__ f1,
                 int H, int W, const int4 *__restrict__ cells, int M, float T,
@@ -375,7 +380,7 @@ __global__ void __launch_bounds__(256)
     __shared__ int ri[4];
     const int k = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wave = tid >> 6, half = lane >> 5, col = lane & 31;
-    const long long plane = (long long)H * W;
+    const long long plane = UP2 ? (long long)(H / 2) * (W / 2) : (long long)H * W;
     int4 cl;
 
     if (k >= M)
@@ -388,7 +393,8 @@ __global__ void __launch_bounds__(256)
         const int x = cl.x * FW + p % FW, y = cl.y * FW + p / FW;
 
         A[p * WP + c] = (x >= 0 && y >= 0 && x < W && y < H)
-                            ? f0[c * plane + (long long)y * W + x]
+                            ? (UP2 ? bl_up2(f0 + c * plane, H / 2, W / 2, y, x)
+                                   : f0[c * plane + (long long)y * W + x])
                             : 0.0f;
     }
     for (int e = tid; e < FC * NQ; e += 256) {
@@ -396,7 +402,8 @@ __global__ void __launch_bounds__(256)
         const int x = cl.z * FW - 1 + q % FW1, y = cl.w * FW - 1 + q / FW1;
 
         B[q * WP + c] = (x >= 0 && y >= 0 && x < W && y < H)
-                            ? f1[c * plane + (long long)y * W + x]
+                            ? (UP2 ? bl_up2(f1 + c * plane, H / 2, W / 2, y, x)
+                                   : f1[c * plane + (long long)y * W + x])
                             : 0.0f;
     }
     __syncthreads();
@@ -554,9 +561,33 @@ extern "C" void eloftr_fine(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
     if (((uintptr_t)cells->ptr & 15) || ((uintptr_t)out->ptr & 15))
         icoreg_fatal("%s: cells and out must be 16-byte aligned", op);
     prof_scope ps(o->ocl, op);
-    hipLaunchKernelGGL(fine_kernel, dim3(M), dim3(256), 0, stream_of(o->ocl),
+    hipLaunchKernelGGL(fine_kernel<false>, dim3(M), dim3(256), 0, stream_of(o->ocl),
                        cfptr(f0), cfptr(f1), H, W, (const int4 *)cells->ptr, M,
                        T, (float4 *)out->ptr);
+    launch_check(op);
+    ICOREG_API_END
+}
+
+extern "C" void eloftr_fine_half(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
+                                 cl_mem cells, int M, float T, cl_mem out)
+{
+    ICOREG_API_BEGIN
+    const char *op = "eloftr_fine_half";
+
+    if (M < 0 || H < 2 || W < 2 || H % 2 || W % 2)
+        icoreg_fatal("%s: invalid sizes M=%d H=%d W=%d", op, M, H, W);
+    if (M == 0)
+        return;
+    need_floats(f0, 0, (long long)FC * (H / 2) * (W / 2), op, "f0");
+    need_floats(f1, 0, (long long)FC * (H / 2) * (W / 2), op, "f1");
+    need_bytes(cells, 0, 16LL * M, op, "cells");
+    need_floats(out, 0, 4LL * M, op, "out");
+    if (((uintptr_t)cells->ptr & 15) || ((uintptr_t)out->ptr & 15))
+        icoreg_fatal("%s: cells and out must be 16-byte aligned", op);
+    prof_scope ps(o->ocl, op);
+    hipLaunchKernelGGL(fine_kernel<true>, dim3(M), dim3(256), 0, stream_of(o->ocl),
+                       cfptr(f0), cfptr(f1), H, W, (const int4 *)cells->ptr, M, T,
+                       (float4 *)out->ptr);
     launch_check(op);
     ICOREG_API_END
 }

@@ -39,6 +39,12 @@ struct gemm_args {
      * the concatenation [B; B2] without being materialised. */
     const float *B2;
     int ksplit;
+    /* rup = 2: R is not in C's layout but (nb0 batches rs0 floats apart)
+     * M rows of rh x rw planes, and C's column n = y * rwo + x (rwo =
+     * 2 rw) receives R's 2x bilinear resize at (y, x) (ops_resize, pixel
+     * centres), sampled on the fly. */
+    int rup, rh, rw, rwo;
+    long long rs0;
 };
 
 /* True if the kernel takes these leading dimensions: each at least its
@@ -58,5 +64,14 @@ void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
 void ops_gemm_cat(struct ops *o, int M, int N, int K, struct opnd A,
                   struct opnd B1, struct opnd B2, int ksplit, struct opnd C,
                   int nb, int act, float slope);
+
+/* C (M x N, nb batches C.s0 apart) = A (M x K) B (K x N, not transposed)
+ * + the 2x bilinear resize of R, R holding nb batches (M, H / 2, W / 2)
+ * rstride floats apart and N = H W: a product whose residual is an
+ * upsampled map (ops_resize, then ops_gemm with residual), without
+ * writing the upsampled map. */
+void ops_gemm_up2res(struct ops *o, int M, int N, int K, struct opnd A,
+                     struct opnd B, struct opnd C, int nb, cl_mem R,
+                     long rstride, int H, int W);
 
 #endif /* ICOREG_GEMM_H */

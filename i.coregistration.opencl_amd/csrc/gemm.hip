@@ -33,6 +33,7 @@
 #include <hip/hip_runtime.h>
 
 #include "act.h"
+#include "bilinear.h"
 #include "gemm.h"
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -364,13 +365,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
      * (lane / 32) * 4 + r % 4, column lane % 32. */
     {
         float *C = g.C + b0 * g.sc0 + b1 * g.sc1;
-        const float *R = g.R ? g.R + b0 * g.sc0 + b1 * g.sc1 : nullptr;
+        const float *R = g.R ? (g.rup ? g.R + b0 * g.rs0 : g.R + b0 * g.sc0 + b1 * g.sc1)
+                             : nullptr;
 
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const int col = n0 + wn * (BN / WGN) + j * 32 + (lane & 31);
+                const int ry = g.rup ? col / g.rwo : 0, rx = g.rup ? col - ry * g.rwo : 0;
 
                 if (col >= N)
                     continue;
@@ -387,7 +390,9 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
                         v += g.bias[g.biasrow ? row : col];
                     v = icoreg_act(v, g.act, g.slope);
                     if (R)
-                        v += R[(long long)row * g.ldc + col];
+                        v += g.rup ? bl_up2(R + (long long)row * g.rh * g.rw, g.rh, g.rw,
+                                            ry, rx)
+                                   : R[(long long)row * g.ldc + col];
                     C[(long long)row * g.ldc + col] = v;
                 }
             }
@@ -611,7 +616,7 @@ void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
             (long long)((g.M + 63) / 64) * ((g.N + 63) / 64) * nb;
 
         if (bmode != GEMM_B_CONV && va && vb && g.K <= GEMM_SK_MAXK && g.K % 16 == 0 &&
-            g.ksplit == 0 && 2 * tiles64 <= cus) {
+            g.ksplit == 0 && g.rup == 0 && 2 * tiles64 <= cus) {
             const dim3 grid(((g.M + 31) / 32) * ((g.N + 31) / 32), nb);
 
             if (bmode == GEMM_B_NK)

@@ -46,8 +46,7 @@ extern "C" void icoreg_eloftr_set_pos_scale(struct eloftr_model *m, float s)
     m->pos_scale = s;
 }
 
-extern "C" cl_mem icoreg_eloftr_buffer(const struct eloftr_model *m,
-                                       const char *name)
+extern "C" cl_mem icoreg_eloftr_buffer(struct eloftr_model *m, const char *name)
 {
     static const struct {
         const char *name;
@@ -66,6 +65,9 @@ extern "C" cl_mem icoreg_eloftr_buffer(const struct eloftr_model *m,
         {"col_s", offsetof(struct eloftr_model, col_s)},
     };
 
+    /* The full-resolution fine maps are written on request only. */
+    if (strncmp(name, "fine", 4) == 0 && m->fu_c && m->finep)
+        eloftr_fine_maps(m);
     for (size_t i = 0; i < sizeof(tab) / sizeof(tab[0]); i++)
         if (strcmp(tab[i].name, name) == 0)
             return *(const cl_mem *)((const char *)m + tab[i].off);

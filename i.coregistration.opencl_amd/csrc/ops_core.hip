@@ -236,6 +236,59 @@ void ops_gemm_cat(struct ops *o, int M, int N, int K, struct opnd A,
     }
 }
 
+void ops_gemm_up2res(struct ops *o, int M, int N, int K, struct opnd A,
+                     struct opnd B, struct opnd C, int nb, cl_mem R,
+                     long rstride, int H, int W)
+{
+    const char *op = "ops_gemm_up2res";
+    gemm_args g;
+
+    if (M < 1 || N < 1 || K < 1 || nb < 1 || nb > 65535 || H < 2 || W < 2 ||
+        H % 2 || W % 2 || (long long)H * W != N || rstride < (long long)M * (H / 2) * (W / 2))
+        icoreg_fatal("%s: invalid sizes M=%d N=%d K=%d H=%d W=%d nb=%d", op, M, N, K, H,
+                     W, nb);
+    need_matrix(A.buf, A.off, A.ld, A.s0, A.s1, M, K, nb, 1, op, "A");
+    need_matrix(B.buf, B.off, B.ld, B.s0, B.s1, K, N, nb, 1, op, "B");
+    need_matrix(C.buf, C.off, C.ld, C.s0, C.s1, M, N, nb, 1, op, "C");
+    need_floats(R, 0, (long long)(nb - 1) * rstride + (long long)M * (H / 2) * (W / 2), op,
+                "R");
+    if (C.ld != N)
+        icoreg_fatal("%s: C rows must be whole planes (ld %ld, N %d)", op, C.ld, N);
+    count32((long long)M * N, "gemm output");
+
+    memset(&g, 0, sizeof(g));
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    g.A = cfptr(A.buf) + A.off;
+    g.lda = A.ld;
+    g.sa0 = A.s0;
+    g.B = cfptr(B.buf) + B.off;
+    g.ldb = B.ld;
+    g.sb0 = B.s0;
+    g.C = fptr(C.buf) + C.off;
+    g.ldc = C.ld;
+    g.sc0 = C.s0;
+    g.nb1 = 1;
+    g.alpha = 1.0f;
+    g.act = ACT_NONE;
+    g.R = cfptr(R);
+    g.rup = 2;
+    g.rh = H / 2;
+    g.rw = W / 2;
+    g.rwo = W;
+    g.rs0 = rstride;
+    if (!gemm_shape_ok(g, GEMM_B_KN))
+        icoreg_fatal("%s: leading dimensions not supported", op);
+    {
+        prof_scope ps(o->ocl, "gemm");
+
+        gemm_launch(g, GEMM_B_KN, nb, vec_ok(A), vec_ok(B), o->ocl->cu_count,
+                    stream_of(o->ocl));
+        launch_check("gemm");
+    }
+}
+
 extern "C" void ops_linear(struct ops *o, int rows, int in, int out, cl_mem X,
                            long xoff, cl_mem W, cl_mem b, cl_mem Y, long yoff,
                            int act, float slope, int residual)

@@ -11,6 +11,7 @@
 
 #include <math.h>
 
+#include "bilinear.h"
 #include "common.h"
 #include "ops.h"
 
@@ -28,7 +29,7 @@ __global__ void __launch_bounds__(256)
 {
     const long long item = (long long)blockIdx.x * 256 + threadIdx.x;
     int it, x4, row, y, c, y0, y1;
-    float uy, fy, v[4];
+    float fy, v[4];
     const float *r0, *r1;
     float *o;
 
@@ -39,30 +40,17 @@ __global__ void __launch_bounds__(256)
     x4 = it - row * X4;
     c = row / H;
     y = row - c * H;
-    if (align)
-        uy = H > 1 ? (float)y * (float)(h - 1) / (float)(H - 1) : 0.0f;
-    else
-        uy = fmaxf(((float)y + 0.5f) * sy - 0.5f, 0.0f);
-    y0 = min((int)uy, h - 1);
-    y1 = min(y0 + 1, h - 1);
-    fy = uy - y0;
+    bl_taps(y, H, h, align, sy, y0, y1, fy);
     r0 = in + ((long long)c * h + y0) * w;
     r1 = in + ((long long)c * h + y1) * w;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const int x = min(4 * x4 + k, W - 1);
-        float ux, fx;
+        float fx;
         int x0, x1;
 
-        if (align)
-            ux = W > 1 ? (float)x * (float)(w - 1) / (float)(W - 1) : 0.0f;
-        else
-            ux = fmaxf(((float)x + 0.5f) * sx - 0.5f, 0.0f);
-        x0 = min((int)ux, w - 1);
-        x1 = min(x0 + 1, w - 1);
-        fx = ux - x0;
-        v[k] = (1.0f - fy) * ((1.0f - fx) * r0[x0] + fx * r0[x1]) +
-               fy * ((1.0f - fx) * r1[x0] + fx * r1[x1]);
+        bl_taps(x, W, w, align, sx, x0, x1, fx);
+        v[k] = bl_mix(r0, r1, x0, x1, fx, fy);
     }
     o = out + ((long long)(c + coff) * H + y) * W + 4 * x4;
     if (vec) {

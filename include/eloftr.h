@@ -58,9 +58,11 @@ struct eloftr_model {
     /* Work buffers (eloftr_alloc). Both images of the pair sit in one
      * allocation (img, s_a, s_b, f1p, f2p, xp, finep, fu_*: image 1 right
      * after image 0), so that the backbone and the fusion run each layer
-     * once for the pair; f1[k], f2[k], x[k], fine[k] are views of image k. */
+     * once for the pair; f1[k], f2[k], x[k], fine[k] are views of image k.
+     * finep is written only on request (eloftr_fine_maps); fine matching
+     * reads the half-resolution maps fine_h[k] (views of fu_c). */
     cl_mem img, s_a, s_b, f1p, f2p, xp, finep;
-    cl_mem f1[2], f2[2], x[2], fine[2];
+    cl_mem f1[2], f2[2], x[2], fine[2], fine_h[2];
     cl_mem t_qn, t_kvn, t_Q, t_KV, t_O, t_O2, t_cat, t_tok, t_h1, t_h2,
         rope;
     cl_mem s_blk, row_lse, col_m, col_s, row_max, row_arg, col_max, col_arg;
@@ -101,6 +103,10 @@ void eloftr_match(struct eloftr_model *m, const float *grey0,
 void eloftr_match_device(struct eloftr_model *m, cl_mem dev0, cl_mem dev1);
 
 void eloftr_free(struct eloftr_model *m);
+/* Write finep (fine[0], fine[1]: 64 x H x W each), the 2x bilinear resize
+ * of the last match's half-resolution fine maps (eloftr.c:604); the
+ * matcher itself samples that resize on the fly and does not need it. */
+void eloftr_fine_maps(struct eloftr_model *m);
 
 #ifdef __cplusplus
 }

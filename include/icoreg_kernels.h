@@ -50,6 +50,15 @@ void eloftr_conf_col(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse,
 void eloftr_fine(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
                  cl_mem cells, int M, float T, cl_mem out);
 
+/* No counterpart in the reference: eloftr_fine on the fine features at
+ * half resolution, for the ELoFTR driver. f0, f1 (64, H / 2, W / 2) stand
+ * for their 2x bilinear resize (64, H, W) (ops_resize, pixel centres),
+ * sampled in the windows with the resize's own arithmetic, so that the
+ * result is eloftr_fine's on the resized maps without writing them (the
+ * reference resizes before fine matching, eloftr.c:604). H and W even. */
+void eloftr_fine_half(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
+                      cl_mem cells, int M, float T, cl_mem out);
+
 /* ---- RoMa (roma_kernels.cl) ----------------------------------------------
  * Warps are channel-major (2, n): x then y, normalised to -1..1 with
  * align_corners = 0 (cell centres at -1 + (2 i + 1) / size). */

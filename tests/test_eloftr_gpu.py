@@ -114,6 +114,32 @@ def test_fine_kernel(dev, ic, orc):
     np.testing.assert_allclose(got[sure], ref[sure], atol=1e-3, rtol=0)
 
 
+def test_fine_half_resolution(dev, ic):
+    """eloftr_fine_half on half-resolution maps is bit for bit eloftr_fine on
+    their 2x resize (ops_resize), including windows at the image border."""
+    print("[eloftr] fine kernel, half-resolution maps", flush=True)
+    rng = np.random.default_rng(23)
+    H, W = 48, 64
+    h, w = H // 8, W // 8
+    f0 = rng.standard_normal((64, H // 2, W // 2)).astype(np.float32)
+    f1 = rng.standard_normal((64, H // 2, W // 2)).astype(np.float32)
+    Mn = 300
+    cells = np.stack([rng.integers(0, w, Mn), rng.integers(0, h, Mn),
+                      rng.integers(0, w, Mn), rng.integers(0, h, Mn)], 1).astype(np.int32)
+    cells[:3] = [[0, 0, 0, 0], [w - 1, h - 1, w - 1, h - 1], [0, h - 1, w - 1, 0]]
+    cells = np.ascontiguousarray(cells)
+    b0, b1, bc = dev.upload(f0), dev.upload(f1), dev.upload(cells)
+    u0, u1 = dev.zeros(64 * H * W), dev.zeros(64 * H * W)
+    dev.api.ops_resize(dev.po, b0.mem, 64, H // 2, W // 2, u0.mem, H, W, 0, 0, 2.0)
+    dev.api.ops_resize(dev.po, b1.mem, 64, H // 2, W // 2, u1.mem, H, W, 0, 0, 2.0)
+    full, half = dev.zeros(4 * Mn), dev.zeros(4 * Mn)
+    dev.api.eloftr_fine(dev.po, u0.mem, u1.mem, H, W, bc.mem, Mn, 10.0, full.mem)
+    dev.api.eloftr_fine_half(dev.po, b0.mem, b1.mem, H, W, bc.mem, Mn, 10.0, half.mem)
+    a, b = dev.read(full, 4 * Mn), dev.read(half, 4 * Mn)
+    assert np.isfinite(a).all()
+    assert np.array_equal(a, b)
+
+
 def test_network_small_vs_oracle_and_transformers(dev, ic, weights, weights_file, tmp_path):
     print("[eloftr] network 64x96", flush=True)
     g = np.load(GOLDEN)
