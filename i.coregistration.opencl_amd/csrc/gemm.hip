@@ -40,6 +40,11 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 #define GEMM_PAD 4
 
+/* Offset past the end of every window: the load reads 0. */
+#define GEMM_OOB 0x80000000u
+/* gfx9 s_waitcnt immediate: vmcnt(0), expcnt and lgkmcnt not waited on. */
+#define GEMM_WAIT_VM0 0x0F70
+
 /* Word 3 of a raw buffer resource on gfx9-family parts: 32-bit data. */
 #define GEMM_RSRC_FLAGS 0x00020000
 
@@ -94,6 +99,46 @@ __device__ __forceinline__ int xcd_tile(int L, int T)
     const int q = T >> 3, rem = T & 7, x = L & 7, idx = L >> 3;
 
     return (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + idx;
+}
+
+/* C = act(alpha acc + bias) + R for the TM x TN 32 x 32 tiles of a wave
+ * whose block of C starts at (r0, c0), batch (b0, b1). Register r of a
+ * tile holds row (r / 4) * 8 + (lane / 32) * 4 + r % 4, column lane % 32. */
+template <int TM, int TN>
+__device__ __forceinline__ void gemm_epilogue(const gemm_args &g, const floatx16 (&acc)[TM][TN],
+                                              long long b0, long long b1, int r0, int c0,
+                                              int lane)
+{
+    float *C = g.C + b0 * g.sc0 + b1 * g.sc1;
+    const float *R =
+        g.R ? (g.rup ? g.R + b0 * g.rs0 : g.R + b0 * g.sc0 + b1 * g.sc1) : nullptr;
+
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int col = c0 + j * 32 + (lane & 31);
+            const int ry = g.rup ? col / g.rwo : 0, rx = g.rup ? col - ry * g.rwo : 0;
+
+            if (col >= g.N)
+                continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = r0 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                float v;
+
+                if (row >= g.M)
+                    continue;
+                v = g.alpha * acc[i][j][r];
+                if (g.bias)
+                    v += g.bias[g.biasrow ? row : col];
+                v = icoreg_act(v, g.act, g.slope);
+                if (R)
+                    v += g.rup ? bl_up2(R + (long long)row * g.rh * g.rw, g.rh, g.rw, ry, rx)
+                               : R[(long long)row * g.ldc + col];
+                C[(long long)row * g.ldc + col] = v;
+            }
+        }
 }
 
 /* BM x BN output tile, BK slice, WGM x WGN waves (each a
@@ -361,42 +406,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
         __syncthreads();
     }
 
-    /* Epilogue: register r of a 32 x 32 tile holds row (r / 4) * 8 +
-     * (lane / 32) * 4 + r % 4, column lane % 32. */
-    {
-        float *C = g.C + b0 * g.sc0 + b1 * g.sc1;
-        const float *R = g.R ? (g.rup ? g.R + b0 * g.rs0 : g.R + b0 * g.sc0 + b1 * g.sc1)
-                             : nullptr;
-
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const int col = n0 + wn * (BN / WGN) + j * 32 + (lane & 31);
-                const int ry = g.rup ? col / g.rwo : 0, rx = g.rup ? col - ry * g.rwo : 0;
-
-                if (col >= N)
-                    continue;
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int row = m0 + wm * (BM / WGM) + i * 32 + (r >> 2) * 8 +
-                                    (lane >> 5) * 4 + (r & 3);
-                    float v;
-
-                    if (row >= M)
-                        continue;
-                    v = g.alpha * acc[i][j][r];
-                    if (g.bias)
-                        v += g.bias[g.biasrow ? row : col];
-                    v = icoreg_act(v, g.act, g.slope);
-                    if (R)
-                        v += g.rup ? bl_up2(R + (long long)row * g.rh * g.rw, g.rh, g.rw,
-                                            ry, rx)
-                                   : R[(long long)row * g.ldc + col];
-                    C[(long long)row * g.ldc + col] = v;
-                }
-            }
-    }
+    gemm_epilogue<TM, TN>(g, acc, b0, b1, m0 + wm * (BM / WGM), n0 + wn * (BN / WGN), lane);
 }
 
 /* Small products (few output tiles, K <= 256): one 32 x 32 output tile per
@@ -535,6 +545,180 @@ __global__ void __launch_bounds__(512) gemm_smallk(const gemm_args g)
     }
 }
 
+/* Products with 16-byte aligned rows: operands by LDS DMA. Each thread
+ * loads 16-byte chunks of the A and B panels straight into LDS
+ * (buffer_load ... lds: no register staging, no transposing stores), 32
+ * k per slice, two slices in flight, one barrier per slice. Rows of the
+ * [row][k] panels (A, and B given N x K) hold their eight chunks in the
+ * order chunk ^ (row / 2 % 8), so that the 32 rows an MFMA operand reads
+ * spread over the banks; a K x N panel of B swaps the two halves of every
+ * odd k row for the same reason. The MFMA steps take k in the order
+ * 4 g + 2 h + j (lane half h, step j of group g) for both operands, so a
+ * lane reads its two k of a group with one 8-byte load. */
+template <int BM, int BN, int WM, int WN, int MODE>
+__global__ void __launch_bounds__(64 * WM * WN) gemm_dma(const gemm_args g)
+{
+    constexpr int NT = 64 * WM * WN, BK = 32;
+    constexpr int TM = BM / WM / 32, TN = BN / WN / 32;
+    constexpr int ASZ = BM * BK, BSZ = BN * BK; /* floats per slice */
+    constexpr int AL = ASZ / 4 / NT, BL = BSZ / 4 / NT; /* chunks per thread */
+    static_assert(AL >= 1 && BL >= 1 && ASZ % (4 * NT) == 0 && BSZ % (4 * NT) == 0 &&
+                      BN >= 64,
+                  "tile shape");
+    __shared__ __align__(16) float lds[2 * (ASZ + BSZ)];
+    float *const A0 = lds, *const B0 = lds + ASZ, *const A1 = lds + ASZ + BSZ,
+                 *const B1 = lds + 2 * ASZ + BSZ;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN, h = lane >> 5, r32 = lane & 31;
+    const int tiles_n = (g.N + BN - 1) / BN;
+    const int tiles = tiles_n * ((g.M + BM - 1) / BM);
+    const int tile = xcd_tile(blockIdx.x, tiles);
+    const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+    const long long bt = blockIdx.y, b0 = bt / g.nb1, b1 = bt % g.nb1;
+    const float *A = g.A + b0 * g.sa0 + b1 * g.sa1;
+    const float *B = g.B + b0 * g.sb0 + b1 * g.sb1;
+    const int M = g.M, N = g.N, K = g.K;
+    const long long lda = g.lda, ldb = g.ldb;
+    /* Windows over whole operands (their byte offsets fit in 31 bits). */
+    const long long abytes = ((long long)(M - 1) * lda + K) * 4;
+    const long long bbytes = MODE == GEMM_B_NK ? ((long long)(N - 1) * ldb + K) * 4
+                                               : ((long long)(K - 1) * ldb + N) * 4;
+    int arow[AL], ak[AL], brow[BL], bk[BL];
+    floatx16 acc[TM][TN];
+
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                acc[i][j][r] = 0.0f;
+    /* Chunk slot s of this thread (LDS floats 4 s .. 4 s + 3): A (and B
+     * given N x K) row s / 8, its chunk (s % 8) ^ (row / 2 % 8); B given
+     * K x N: k row s / (BN / 4), columns 4 ((s % (BN / 4)) ^ 8 (k & 1)). */
+#pragma unroll
+    for (int q = 0; q < AL; q++) {
+        const int sl = tid + NT * q, row = sl / 8;
+
+        arow[q] = row;
+        ak[q] = 4 * ((sl % 8) ^ ((row >> 1) & 7));
+    }
+#pragma unroll
+    for (int q = 0; q < BL; q++) {
+        const int sl = tid + NT * q;
+
+        if (MODE == GEMM_B_NK) {
+            const int row = sl / 8;
+
+            brow[q] = row;
+            bk[q] = 4 * ((sl % 8) ^ ((row >> 1) & 7));
+        }
+        else {
+            const int kr = sl / (BN / 4);
+
+            brow[q] = kr;
+            bk[q] = 4 * ((sl % (BN / 4)) ^ ((kr & 1) ? 8 : 0));
+        }
+    }
+
+    auto load = [&](int k0, float *__restrict__ As, float *__restrict__ Bs) {
+        const __amdgpu_buffer_rsrc_t ra = gemm_rsrc(A, abytes);
+        const __amdgpu_buffer_rsrc_t rb = gemm_rsrc(B, bbytes);
+
+#pragma unroll
+        for (int q = 0; q < AL; q++) {
+            const int gm = m0 + arow[q], gk = k0 + ak[q];
+            const unsigned off = gm < M && gk < K ? (unsigned)((gm * lda + gk) * 4) : GEMM_OOB;
+
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void *)(As + 4 * (NT * q + 64 * wave)), 16,
+                (int)off, 0, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < BL; q++) {
+            unsigned off;
+
+            if (MODE == GEMM_B_NK) {
+                const int gn = n0 + brow[q], gk = k0 + bk[q];
+
+                off = gn < N && gk < K ? (unsigned)((gn * ldb + gk) * 4) : GEMM_OOB;
+            }
+            else {
+                const int gk = k0 + brow[q], gn = n0 + bk[q];
+
+                off = gk < K && gn < N ? (unsigned)((gk * ldb + gn) * 4) : GEMM_OOB;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (__attribute__((address_space(3))) void *)(Bs + 4 * (NT * q + 64 * wave)), 16,
+                (int)off, 0, 0, 0);
+        }
+    };
+    auto compute = [&](const float *__restrict__ As, const float *__restrict__ Bs) {
+#pragma unroll
+        for (int gq = 0; gq < BK / 4; gq++) {
+            float2 a[TM], b[TN];
+
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int row = wm * (BM / WM) + i * 32 + r32;
+
+                a[i] = *(const float2 *)(As + row * BK + 4 * (gq ^ ((row >> 1) & 7)) + 2 * h);
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = wn * (BN / WN) + j * 32 + r32;
+
+                if (MODE == GEMM_B_NK) {
+                    b[j] = *(const float2 *)(Bs + n * BK + 4 * (gq ^ ((n >> 1) & 7)) + 2 * h);
+                }
+                else {
+                    const int k = 4 * gq + 2 * h;
+
+                    b[j].x = Bs[k * BN + n];
+                    b[j].y = Bs[(k + 1) * BN + (((n >> 2) ^ 8) << 2) + (n & 3)];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] =
+                        __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] =
+                        __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
+        }
+    };
+
+    const int nk = (K + BK - 1) / BK;
+    /* Slice kt from (Ac, Bc) while slice kt + 1 loads into (An, Bn); the
+     * loads have landed (LDS DMA counts in vmcnt) and everyone's reads of
+     * (Ac, Bc) are done at the barrier. */
+    auto step = [&](int kt, const float *__restrict__ Ac, const float *__restrict__ Bc,
+                    float *__restrict__ An, float *__restrict__ Bn) {
+        if (kt + 1 < nk)
+            load((kt + 1) * BK, An, Bn);
+        compute(Ac, Bc);
+        __builtin_amdgcn_s_waitcnt(GEMM_WAIT_VM0);
+        __syncthreads();
+    };
+
+    load(0, A0, B0);
+    __builtin_amdgcn_s_waitcnt(GEMM_WAIT_VM0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+        step(kt, A0, B0, A1, B1);
+        if (kt + 1 < nk)
+            step(kt + 1, A1, B1, A0, B0);
+    }
+    gemm_epilogue<TM, TN>(g, acc, b0, b1, m0 + wm * (BM / WM), n0 + wn * (BN / WN), lane);
+}
+
 template <int BM, int BN, int BK, int WGM, int WGN, int MODE>
 static void launch_mode(const gemm_args &g, int nb, bool va, bool vb,
                         hipStream_t s)
@@ -623,6 +807,30 @@ void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
                 hipLaunchKernelGGL(gemm_smallk<GEMM_B_NK>, grid, dim3(512), 0, s, g);
             else
                 hipLaunchKernelGGL(gemm_smallk<GEMM_B_KN>, grid, dim3(512), 0, s, g);
+            return;
+        }
+    }
+    /* The LDS-DMA kernel: in the ELoFTR and RoMa pipelines it is faster
+     * only for products with few output rows (M <= 256, B given K x N,
+     * K >= 256: the MLP's second layer); on larger grids the main
+     * kernel's smaller LDS footprint (more blocks per CU) wins, and on
+     * K <= 128 its shorter slices do. It addresses whole operands with
+     * 31-bit byte offsets. */
+    if (bmode == GEMM_B_KN && va && vb && g.M <= 256 && g.K >= 256 && g.ksplit == 0) {
+        const long long lim = 1LL << 31;
+        const long long ab = ((long long)(g.M - 1) * g.lda + g.K) * 4;
+        const long long bb = bmode == GEMM_B_NK
+                                 ? ((long long)(g.N - 1) * g.ldb + g.K) * 4
+                                 : ((long long)(g.K - 1) * g.ldb + g.N) * 4;
+
+        if (ab < lim && bb < lim) {
+            const int tiles = ((g.M + 63) / 64) * ((g.N + 63) / 64);
+            const dim3 grid(tiles, nb);
+
+            if (bmode == GEMM_B_NK)
+                hipLaunchKernelGGL((gemm_dma<64, 64, 2, 2, GEMM_B_NK>), grid, dim3(256), 0, s, g);
+            else
+                hipLaunchKernelGGL((gemm_dma<64, 64, 2, 2, GEMM_B_KN>), grid, dim3(256), 0, s, g);
             return;
         }
     }

@@ -19,7 +19,7 @@ GEMM_SHAPES = [
     # (M, N, K, transb, nb, act, residual, biasrow): aggregated-attention
     # projections (400 and 800 tokens, K = 256) and o_proj (B transposed,
     # two images), ragged tiles, K = 16 and 48, both bias layouts; the
-    # last two have K = 272 and N % 4 != 0 (main kernel).
+    # next two have K = 272 and N % 4 != 0 (main kernel).
     (400, 256, 256, 1, 1, 0, 0, 0),
     (800, 512, 256, 1, 1, 0, 0, 1),
     (256, 400, 256, 1, 2, 0, 0, 0),
@@ -28,6 +28,10 @@ GEMM_SHAPES = [
     (96, 100, 256, 0, 2, 3, 0, 1),
     (64, 64, 272, 0, 1, 1, 0, 0),
     (50, 30, 64, 0, 1, 1, 1, 0),
+    # LDS-DMA kernel (B given K x N, M <= 256, K >= 256): the MLP's second
+    # layer, ragged rows and columns, K not a multiple of 32.
+    (256, 1600, 512, 0, 2, 0, 1, 1),
+    (200, 300, 292, 0, 1, 3, 0, 0),
 ]
 
 
