@@ -336,13 +336,14 @@ def main():
     cells = np.stack(np.meshgrid(np.arange(w), np.arange(h)), -1).reshape(-1, 2)
     cells = np.ascontiguousarray(np.concatenate([cells, cells], 1).astype(np.int32))
     bc, bo = dev.upload(cells), dev.zeros(4 * n)
-    f0m, f1m = ic.lib().icoreg_eloftr_buffer(net.m, b"fine0"), ic.lib().icoreg_eloftr_buffer(net.m, b"fine1")
-    dev.api.eloftr_fine(dev.po, f0m, f1m, H, W, bc.mem, n, 10.0, bo.mem)
+    # The matcher's own form: windows sampled from the half-resolution maps.
+    f0m, f1m = ic.lib().icoreg_eloftr_buffer(net.m, b"fineh0"), ic.lib().icoreg_eloftr_buffer(net.m, b"fineh1")
+    dev.api.eloftr_fine_half(dev.po, f0m, f1m, H, W, bc.mem, n, 10.0, bo.mem)
     dev.finish()
     dev.reset_events()
     ea = dev.event()
     for _ in range(5):
-        dev.api.eloftr_fine(dev.po, f0m, f1m, H, W, bc.mem, n, 10.0, bo.mem)
+        dev.api.eloftr_fine_half(dev.po, f0m, f1m, H, W, bc.mem, n, 10.0, bo.mem)
     eb = dev.event()
     fine_nmax_ms = dev.elapsed_ms(ea, eb) / 5
 

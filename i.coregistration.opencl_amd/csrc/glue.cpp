@@ -56,6 +56,8 @@ extern "C" cl_mem icoreg_eloftr_buffer(struct eloftr_model *m, const char *name)
         {"x1", offsetof(struct eloftr_model, x[1])},
         {"fine0", offsetof(struct eloftr_model, fine[0])},
         {"fine1", offsetof(struct eloftr_model, fine[1])},
+        {"fineh0", offsetof(struct eloftr_model, fine_h[0])},
+        {"fineh1", offsetof(struct eloftr_model, fine_h[1])},
         {"f1_0", offsetof(struct eloftr_model, f1[0])},
         {"f1_1", offsetof(struct eloftr_model, f1[1])},
         {"f2_0", offsetof(struct eloftr_model, f2[0])},
@@ -66,7 +68,7 @@ extern "C" cl_mem icoreg_eloftr_buffer(struct eloftr_model *m, const char *name)
     };
 
     /* The full-resolution fine maps are written on request only. */
-    if (strncmp(name, "fine", 4) == 0 && m->fu_c && m->finep)
+    if ((strcmp(name, "fine0") == 0 || strcmp(name, "fine1") == 0) && m->fu_c && m->finep)
         eloftr_fine_maps(m);
     for (size_t i = 0; i < sizeof(tab) / sizeof(tab[0]); i++)
         if (strcmp(tab[i].name, name) == 0)

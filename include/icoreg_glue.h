@@ -35,8 +35,8 @@ void icoreg_eloftr_set_pos_scale(struct eloftr_model *m, float s);
 
 /* A named device buffer of the model: "x0", "x1" (1/8 features, 256 x
  * n), "fine0", "fine1" (64 x H x W, written from the last match's
- * half-resolution maps by this request), "f1_0", "f2_0", ... Returns NULL
- * for an unknown name. */
+ * half-resolution maps by this request), "fineh0", "fineh1" (those maps,
+ * 64 x H/2 x W/2), "f1_0", "f2_0", ... Returns NULL for an unknown name. */
 cl_mem icoreg_eloftr_buffer(struct eloftr_model *m, const char *name);
 
 struct roma_model *icoreg_roma_new(void);
