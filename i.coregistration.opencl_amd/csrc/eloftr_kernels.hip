@@ -617,12 +617,16 @@ __global__ void __launch_bounds__(64 * LNR_NW)
     const int nc = max(0, min(cw, C - c0));
     const long long base = (long long)blockIdx.y * C * n;
     const bool on = j < n;
-    float v[CPW];
+    float v[CPW], xv[CPW];
     float s = 0.0f, mean, r;
 
+    /* The residual's values load with the MLP output's: one round trip. */
 #pragma unroll
     for (int k = 0; k < CPW; k++) {
-        v[k] = on && k < nc ? Mm[base + (long long)(c0 + k) * n + j] : 0.0f;
+        const bool in = on && k < nc;
+
+        v[k] = in ? Mm[base + (long long)(c0 + k) * n + j] : 0.0f;
+        xv[k] = in ? X[base + (long long)(c0 + k) * n + j] : 0.0f;
         s += v[k];
     }
     part[0][wave][lane] = s;
@@ -656,7 +660,7 @@ __global__ void __launch_bounds__(64 * LNR_NW)
             float u = (v[k] - mean) * r;
 
             u = u * g[c] + bt[c];
-            X[base + (long long)c * n + j] += u;
+            X[base + (long long)c * n + j] = xv[k] + u;
         }
     }
 }
@@ -688,9 +692,12 @@ void eloftr_ln_residual(struct ops *o, cl_mem M, int nb, int C, int n,
  * then each row LayerNorm over the channels (gain g, bias bt), written
  * token-major: eloftr.c:411-423 (depthwise 4 x 4 aggregation, 4 x 4 max
  * pooling, transposes to tokens, LayerNorm) in one launch. A block takes
- * AGG_T consecutive tokens; thread c reads its channel's 4 x 4 windows as
- * 16-byte rows (consecutive tokens of a row share cache lines), the
- * values go to LDS token-major, and wave t normalises token t of both
+ * AGG_T = 4 consecutive tokens and all 256 channels: (channel, token)
+ * pair p of the block is c = p / 4, token p % 4, so the four lanes of a
+ * channel read one 64-byte run of each window row (when the four tokens
+ * share an aggregated row) and a wave instruction touches 16 runs, not
+ * 64 scattered 16-byte pieces. The filters are staged in LDS,
+ * the values go to LDS token-major, and wave t normalises token t of both
  * outputs. */
 #define AGG_D 256
 #define AGG_T 4
@@ -703,38 +710,62 @@ __global__ void __launch_bounds__(AGG_D)
 {
     static_assert(AGG_D / 64 == AGG_T, "one wave per token");
     __shared__ float sv[2][AGG_T][AGG_D];
-    const int c = threadIdx.x, b = blockIdx.y, na = (h / 4) * aw;
+    __shared__ __align__(16) float ws[AGG_D * 16];
+    const int tid = threadIdx.x, b = blockIdx.y, na = (h / 4) * aw;
     const int p0 = blockIdx.x * AGG_T;
-    float4 wr[4];
+    constexpr int PP = AGG_D * AGG_T / AGG_D; /* pairs per thread */
+    float q[PP], kv[PP];
 
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        wr[i] = *(const float4 *)(wq + c * 16 + i * 4);
-#pragma unroll
-    for (int t = 0; t < AGG_T; t++) {
-        const int p = min(p0 + t, na - 1), ay = p / aw, ax = p - ay * aw;
-        const long long base = (long long)b * img + (long long)c * h * w +
-                               (long long)(4 * ay) * w + 4 * ax;
-        float q = 0.0f, kv = -INFINITY;
+        *(float4 *)&ws[(tid + AGG_D * i) * 4] = *(const float4 *)(wq + (tid + AGG_D * i) * 4);
+    {
+        float4 xr[PP][4], yr[PP][4];
 
-        /* Rows of a window are 16-byte aligned (w % 4 == 0). */
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 xr = *(const float4 *)(X + base + i * w);
-            const float4 yr = *(const float4 *)(Y + base + i * w);
+        for (int r = 0; r < PP; r++) {
+            const int pr = tid + AGG_D * r, c = pr / AGG_T, t = pr % AGG_T;
+            const int p = min(p0 + t, na - 1), ay = p / aw, ax = p - ay * aw;
+            const long long base = (long long)b * img + (long long)c * h * w +
+                                   (long long)(4 * ay) * w + 4 * ax;
 
-            q = fmaf(wr[i].x, xr.x, q);
-            q = fmaf(wr[i].y, xr.y, q);
-            q = fmaf(wr[i].z, xr.z, q);
-            q = fmaf(wr[i].w, xr.w, q);
-            kv = fmaxf(kv, fmaxf(fmaxf(yr.x, yr.y), fmaxf(yr.z, yr.w)));
+            /* Rows of a window are 16-byte aligned (w % 4 == 0). */
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                xr[r][i] = *(const float4 *)(X + base + i * w);
+                yr[r][i] = *(const float4 *)(Y + base + i * w);
+            }
         }
-        sv[0][t][c] = q;
-        sv[1][t][c] = kv;
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < PP; r++) {
+            const int pr = tid + AGG_D * r, c = pr / AGG_T;
+
+            q[r] = 0.0f;
+            kv[r] = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 wr = *(const float4 *)&ws[c * 16 + i * 4];
+
+                q[r] = fmaf(wr.x, xr[r][i].x, q[r]);
+                q[r] = fmaf(wr.y, xr[r][i].y, q[r]);
+                q[r] = fmaf(wr.z, xr[r][i].z, q[r]);
+                q[r] = fmaf(wr.w, xr[r][i].w, q[r]);
+                kv[r] = fmaxf(kv[r], fmaxf(fmaxf(yr[r][i].x, yr[r][i].y),
+                                           fmaxf(yr[r][i].z, yr[r][i].w)));
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < PP; r++) {
+        const int pr = tid + AGG_D * r, c = pr / AGG_T, t = pr % AGG_T;
+
+        sv[0][t][c] = q[r];
+        sv[1][t][c] = kv[r];
     }
     __syncthreads();
-    if (p0 + (c >> 6) < na) {
-        const int lane = c & 63, t = c >> 6;
+    if (p0 + (tid >> 6) < na) {
+        const int lane = tid & 63, t = tid >> 6;
         const long long row = (long long)b * na + p0 + t;
 
 #pragma unroll
