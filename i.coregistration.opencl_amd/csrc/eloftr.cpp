@@ -539,6 +539,8 @@ static void coarse_match(struct eloftr_model *m)
     const int D = ELOFTR_DIM, n = m->h * m->w, R = m->blk_rows;
     const float alpha = 1.0f / (D * COARSE_T);
     const bool one_block = R >= n;
+    /* Both passes read each block of S once (rows and columns together). */
+    const bool tiles = eloftr_tiles_ok(m->s_blk, n);
 
     ops_transpose(o, m->x[0], m->t_tok, 1, D, n);
     ops_transpose(o, m->x[1], m->t_h1, 1, D, n);
@@ -554,9 +556,16 @@ static void coarse_match(struct eloftr_model *m)
                 ops_gemm(o, rows, n, D, ops_mat(m->t_tok, (long)r0 * D, D),
                          ops_mat(m->t_h1, 0, D), 1, ops_mat(m->s_blk, 0, n), 1,
                          1, NULL, 0, NULL, 0, alpha, ACT_NONE, 0);
-            if (pass == 0) {
+            if (pass == 0 && tiles) {
+                eloftr_lse_tiles(o, m->s_blk, rows, n, r0, m->row_lse, m->col_m, m->col_s);
+            }
+            else if (pass == 0) {
                 eloftr_row_lse(o, m->s_blk, rows, n, r0, m->row_lse);
                 eloftr_col_lse(o, m->s_blk, rows, n, m->col_m, m->col_s);
+            }
+            else if (tiles) {
+                eloftr_conf_tiles(o, m->s_blk, rows, n, r0, m->row_lse, m->col_m, m->col_s,
+                                  m->row_max, m->row_arg, m->col_max, m->col_arg);
             }
             else {
                 eloftr_conf_row(o, m->s_blk, rows, n, r0, m->row_lse, m->col_m,

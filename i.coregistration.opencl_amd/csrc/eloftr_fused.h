@@ -28,4 +28,16 @@ void eloftr_aggregate(struct ops *o, cl_mem X, cl_mem Y, int nb, int C, int h,
                       int w, cl_mem wq, cl_mem g, cl_mem b, float eps,
                       cl_mem Q, cl_mem KV);
 
+/* The coarse dual softmax of a block of R rows of S (rows r0.., N
+ * columns) in one read of S per pass: eloftr_row_lse and eloftr_col_lse
+ * together (eloftr_lse_tiles), then eloftr_conf_row and eloftr_conf_col
+ * together (eloftr_conf_tiles); same arguments and running states as
+ * those four (eloftr_kernels.cl:9-144 of i.coregistration.opencl).
+ * eloftr_tiles_ok: N % 4 == 0 and S 16-byte aligned, which both need. */
+bool eloftr_tiles_ok(cl_mem S, int N);
+void eloftr_lse_tiles(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse, cl_mem cm,
+                      cl_mem cs);
+void eloftr_conf_tiles(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse, cl_mem cm,
+                       cl_mem cs, cl_mem rmax, cl_mem rarg, cl_mem cmax, cl_mem carg);
+
 #endif /* ICOREG_ELOFTR_FUSED_H */

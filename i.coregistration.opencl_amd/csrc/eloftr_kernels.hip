@@ -25,6 +25,7 @@
 
 #include "bilinear.h"
 #include "common.h"
+#include "eloftr_fused.h"
 #include "icoreg_kernels.h"
 #include "reduce.h"
 
@@ -350,6 +351,280 @@ extern "C" void eloftr_conf_col(struct ops *o, cl_mem S, int R, int N, int r0,
                        fptr(cmax), (int *)carg->ptr);
     launch_check(op);
     ICOREG_API_END
+}
+
+/* ---- the two passes, each in one read of S ---------------------------------- */
+
+/* The driver's form of the four passes above: a block of R rows of S is
+ * read once for both row and column log-sum-exps, and once more for both
+ * confidence maxima. Tile: 64 rows (one column chunk, 16 per wave) x 256
+ * columns (one band, 4 per lane, 16-byte loads). Rows are reduced across
+ * the wave into one partial per (row, band), columns within the lane and
+ * then across the block's waves in row order into one partial per
+ * (chunk, column); the column partials are merged by the kernels above,
+ * the row partials band by band in increasing order. N % 4 == 0. */
+#define TB_RPW 16 /* rows per wave */
+
+/* The passes are bound by the exponentials (two per element), so they
+ * use the hardware exp2 (__expf: relative error about 1e-6, far inside
+ * the confidence tolerance; the argmax rules are unchanged). */
+__device__ __forceinline__ float dual_conf_fast(float s, float lr, float lc)
+{
+    return __expf(s - lr) * __expf(s - lc);
+}
+
+__global__ void __launch_bounds__(256)
+    lse_tile_kernel(const float *__restrict__ S, int R, int N, int nbands,
+                    float2 *__restrict__ rpart, float2 *__restrict__ cpart)
+{
+    __shared__ float2 cp[4][256];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int b = blockIdx.x, c = blockIdx.y, j0 = b * 256 + 4 * lane;
+    const int rb = c * COL_CHUNK + TB_RPW * w;
+    float4 v[TB_RPW];
+
+#pragma unroll
+    for (int i = 0; i < TB_RPW; i++)
+        v[i] = rb + i < R && j0 < N ? *(const float4 *)(S + (long long)(rb + i) * N + j0)
+                                     : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+#pragma unroll
+    for (int i = 0; i < TB_RPW; i++) {
+        const float m = wave_max(fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+        float e = 0.0f;
+
+        if (m != -INFINITY)
+            e = __expf(v[i].x - m) + __expf(v[i].y - m) + __expf(v[i].z - m) + __expf(v[i].w - m);
+        e = wave_sum(e);
+        if (lane == 0 && rb + i < R)
+            rpart[(long long)(rb + i) * nbands + b] = make_float2(m, e);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        float m = -INFINITY, e = 0.0f;
+
+#pragma unroll
+        for (int i = 0; i < TB_RPW; i++)
+            m = fmaxf(m, ((const float *)&v[i])[k]);
+        if (m != -INFINITY)
+#pragma unroll
+            for (int i = 0; i < TB_RPW; i++)
+                e += __expf(((const float *)&v[i])[k] - m);
+        cp[w][4 * lane + k] = make_float2(m, e);
+    }
+    __syncthreads();
+    {
+        const int j = b * 256 + tid;
+        float m = -INFINITY, e = 0.0f;
+
+        if (j >= N)
+            return;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            m = fmaxf(m, cp[q][tid].x);
+        if (m != -INFINITY)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                e += cp[q][tid].x == -INFINITY ? 0.0f : cp[q][tid].y * __expf(cp[q][tid].x - m);
+        cpart[(long long)c * N + j] = make_float2(m, e);
+    }
+}
+
+/* lse[r0 + r] from the band partials of row r. */
+__global__ void __launch_bounds__(256)
+    lse_row_merge_kernel(const float2 *__restrict__ rpart, int R, int nbands, int r0,
+                         float *__restrict__ lse)
+{
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    const float2 *p;
+    float m = -INFINITY, e = 0.0f;
+
+    if (r >= R)
+        return;
+    p = rpart + (long long)r * nbands;
+    for (int q = 0; q < nbands; q++)
+        m = fmaxf(m, p[q].x);
+    if (m != -INFINITY)
+        for (int q = 0; q < nbands; q++)
+            e += p[q].x == -INFINITY ? 0.0f : p[q].y * __expf(p[q].x - m);
+    lse[r0 + r] = m + logf(e);
+}
+
+/* Confidence maxima of the tile: per (row, band) and per (chunk, column),
+ * first index on ties as in the sequential scans. */
+__global__ void __launch_bounds__(256)
+    conf_tile_kernel(const float *__restrict__ S, int R, int N, int r0, int nbands,
+                     const float *__restrict__ lse, const float *__restrict__ lc,
+                     float *__restrict__ rpv, int *__restrict__ rpi,
+                     float *__restrict__ cpv, int *__restrict__ cpi)
+{
+    __shared__ float cv[4][256];
+    __shared__ int ci[4][256];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int b = blockIdx.x, c = blockIdx.y, j0 = b * 256 + 4 * lane;
+    const int rb = c * COL_CHUNK + TB_RPW * w;
+    const bool jon = j0 < N;
+    float4 v[TB_RPW];
+    float4 l4 = jon ? *(const float4 *)(lc + j0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float cb[4] = {-1.0f, -1.0f, -1.0f, -1.0f};
+    int cbi[4] = {-1, -1, -1, -1};
+
+#pragma unroll
+    for (int i = 0; i < TB_RPW; i++)
+        v[i] = rb + i < R && jon ? *(const float4 *)(S + (long long)(rb + i) * N + j0)
+                                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int i = 0; i < TB_RPW; i++) {
+        const int r = rb + i;
+        const float lr = r < R ? lse[r0 + r] : 0.0f;
+        float best = -1.0f;
+        int bi = 0;
+
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float x = dual_conf_fast(((const float *)&v[i])[k], lr, ((const float *)&l4)[k]);
+
+            if (jon && r < R) {
+                if (x > best) {
+                    best = x;
+                    bi = j0 + k;
+                }
+                if (x > cb[k]) {
+                    cb[k] = x;
+                    cbi[k] = r0 + r;
+                }
+            }
+        }
+        wave_argmax(best, bi);
+        if (lane == 0 && r < R) {
+            rpv[(long long)r * nbands + b] = best;
+            rpi[(long long)r * nbands + b] = bi;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        cv[w][4 * lane + k] = cb[k];
+        ci[w][4 * lane + k] = cbi[k];
+    }
+    __syncthreads();
+    {
+        const int j = b * 256 + tid;
+        float best = -1.0f;
+        int bi = -1;
+
+        if (j >= N)
+            return;
+        /* Waves in row order, strict comparison: the first row wins. */
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (cv[q][tid] > best) {
+                best = cv[q][tid];
+                bi = ci[q][tid];
+            }
+        cpv[(long long)c * N + j] = best;
+        cpi[(long long)c * N + j] = bi;
+    }
+}
+
+/* rmax / rarg from the band partials in increasing band order. */
+__global__ void __launch_bounds__(256)
+    conf_row_merge_kernel(const float *__restrict__ rpv, const int *__restrict__ rpi, int R,
+                          int nbands, int r0, float *__restrict__ rmax, int *__restrict__ rarg)
+{
+    const int r = blockIdx.x * 256 + threadIdx.x;
+    float best = -1.0f;
+    int bi = 0;
+
+    if (r >= R)
+        return;
+    for (int q = 0; q < nbands; q++) {
+        const float x = rpv[(long long)r * nbands + q];
+
+        if (x > best) {
+            best = x;
+            bi = rpi[(long long)r * nbands + q];
+        }
+    }
+    rmax[r0 + r] = best;
+    rarg[r0 + r] = bi;
+}
+
+bool eloftr_tiles_ok(cl_mem S, int N)
+{
+    return N % 4 == 0 && ((uintptr_t)S->ptr & 15) == 0;
+}
+
+void eloftr_lse_tiles(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse, cl_mem cm,
+                      cl_mem cs)
+{
+    const char *op = "eloftr_lse_tiles";
+    const int nch = (R + COL_CHUNK - 1) / COL_CHUNK, nbands = (N + 255) / 256;
+    size_t rb;
+    cl_mem sc;
+
+    check_block(S, R, N, op);
+    if (R == 0)
+        return;
+    if (!eloftr_tiles_ok(S, N))
+        icoreg_fatal("%s: N %% 4 and 16-byte alignment required", op);
+    need_floats(lse, r0, R, op, "lse");
+    need_floats(cm, 0, N, op, "cm");
+    need_floats(cs, 0, N, op, "cs");
+    rb = ((size_t)R * nbands * sizeof(float2) + 255) & ~(size_t)255;
+    sc = scratch_get(o, rb + (size_t)nch * N * sizeof(float2));
+    prof_scope ps(o->ocl, op);
+    hipLaunchKernelGGL(lse_tile_kernel, dim3(nbands, nch), dim3(256), 0, stream_of(o->ocl),
+                       cfptr(S), R, N, nbands, (float2 *)sc->ptr,
+                       (float2 *)((char *)sc->ptr + rb));
+    hipLaunchKernelGGL(lse_row_merge_kernel, dim3((R + 255) / 256), dim3(256), 0,
+                       stream_of(o->ocl), (const float2 *)sc->ptr, R, nbands, r0, fptr(lse));
+    hipLaunchKernelGGL(col_lse_merge_kernel, dim3((N + 255) / 256), dim3(256), 0,
+                       stream_of(o->ocl), (const float2 *)((char *)sc->ptr + rb), nch, N,
+                       fptr(cm), fptr(cs));
+    launch_check(op);
+}
+
+void eloftr_conf_tiles(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse, cl_mem cm,
+                       cl_mem cs, cl_mem rmax, cl_mem rarg, cl_mem cmax, cl_mem carg)
+{
+    const char *op = "eloftr_conf_tiles";
+    const int nch = (R + COL_CHUNK - 1) / COL_CHUNK, nbands = (N + 255) / 256;
+    size_t lcb, rpb, cpb;
+    cl_mem sc;
+    char *base;
+
+    check_block(S, R, N, op);
+    if (R == 0)
+        return;
+    if (!eloftr_tiles_ok(S, N))
+        icoreg_fatal("%s: N %% 4 and 16-byte alignment required", op);
+    need_floats(lse, r0, R, op, "lse");
+    need_floats(cm, 0, N, op, "cm");
+    need_floats(cs, 0, N, op, "cs");
+    need_floats(rmax, r0, R, op, "rmax");
+    need_bytes(rarg, 4LL * r0, 4LL * R, op, "rarg");
+    need_floats(cmax, 0, N, op, "cmax");
+    need_bytes(carg, 0, 4LL * N, op, "carg");
+    lcb = ((size_t)N * 4 + 255) & ~(size_t)255;
+    rpb = ((size_t)R * nbands * 4 + 255) & ~(size_t)255;
+    cpb = ((size_t)nch * N * 4 + 255) & ~(size_t)255;
+    sc = scratch_get(o, lcb + 2 * rpb + 2 * cpb);
+    base = (char *)sc->ptr;
+    prof_scope ps(o->ocl, op);
+    hipLaunchKernelGGL(col_logz_kernel, dim3((N + 255) / 256), dim3(256), 0,
+                       stream_of(o->ocl), cfptr(cm), cfptr(cs), N, (float *)base);
+    hipLaunchKernelGGL(conf_tile_kernel, dim3(nbands, nch), dim3(256), 0, stream_of(o->ocl),
+                       cfptr(S), R, N, r0, nbands, cfptr(lse), (const float *)base,
+                       (float *)(base + lcb), (int *)(base + lcb + rpb),
+                       (float *)(base + lcb + 2 * rpb), (int *)(base + lcb + 2 * rpb + cpb));
+    hipLaunchKernelGGL(conf_row_merge_kernel, dim3((R + 255) / 256), dim3(256), 0,
+                       stream_of(o->ocl), (const float *)(base + lcb),
+                       (const int *)(base + lcb + rpb), R, nbands, r0, fptr(rmax),
+                       (int *)rarg->ptr);
+    hipLaunchKernelGGL(conf_col_merge_kernel, dim3((N + 255) / 256), dim3(256), 0,
+                       stream_of(o->ocl), (const float *)(base + lcb + 2 * rpb),
+                       (const int *)(base + lcb + 2 * rpb + cpb), nch, N, fptr(cmax),
+                       (int *)carg->ptr);
+    launch_check(op);
 }
 
 /* ---- fine matching ------------------------------------------------------------ */

@@ -253,7 +253,7 @@ void ops_gemm_up2res(struct ops *o, int M, int N, int K, struct opnd A,
     need_floats(R, 0, (long long)(nb - 1) * rstride + (long long)M * (H / 2) * (W / 2), op,
                 "R");
     if (C.ld != N)
-        icoreg_fatal("%s: C rows must be whole planes (ld %ld, N %d)", op, C.ld, N);
+        icoreg_fatal("%s: C rows must be whole planes (ld %lld, N %d)", op, (long long)C.ld, N);
     count32((long long)M * N, "gemm output");
 
     memset(&g, 0, sizeof(g));
