@@ -389,12 +389,12 @@ __global__ void __launch_bounds__(256)
                                      : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
 #pragma unroll
     for (int i = 0; i < TB_RPW; i++) {
-        const float m = wave_max(fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+        const float m = wave_max_full(fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
         float e = 0.0f;
 
         if (m != -INFINITY)
             e = __expf(v[i].x - m) + __expf(v[i].y - m) + __expf(v[i].z - m) + __expf(v[i].w - m);
-        e = wave_sum(e);
+        e = wave_sum_full(e);
         if (lane == 0 && rb + i < R)
             rpart[(long long)(rb + i) * nbands + b] = make_float2(m, e);
     }
@@ -494,7 +494,7 @@ __global__ void __launch_bounds__(256)
                 }
             }
         }
-        wave_argmax(best, bi);
+        wave_argmax_full(best, bi);
         if (lane == 0 && r < R) {
             rpv[(long long)r * nbands + b] = best;
             rpi[(long long)r * nbands + b] = bi;
