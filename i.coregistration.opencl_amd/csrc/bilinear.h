@@ -39,16 +39,23 @@ static __device__ __forceinline__ float bl_mix(const float *r0, const float *r1,
     return fmaf(fy, bot, (1.0f - fy) * top);
 }
 
-/* Value at output (y, x) of the 2x resize (pixel centres, scale 1 / 2) of
- * plane p (h x w). */
-static __device__ __forceinline__ float bl_up2(const float *p, int h, int w, int y, int x)
+/* Value at output (y, x) of a resize with pixel centres and source step
+ * s (1 / scale) of plane p (h x w). */
+static __device__ __forceinline__ float bl_up(const float *p, int h, int w, float s, int y,
+                                              int x)
 {
     int y0, y1, x0, x1;
     float fy, fx;
 
-    bl_taps(y, 2 * h, h, 0, 0.5f, y0, y1, fy);
-    bl_taps(x, 2 * w, w, 0, 0.5f, x0, x1, fx);
+    bl_taps(y, 0, h, 0, s, y0, y1, fy);
+    bl_taps(x, 0, w, 0, s, x0, x1, fx);
     return bl_mix(p + (long long)y0 * w, p + (long long)y1 * w, x0, x1, fx, fy);
+}
+
+/* The 2x resize (scale 2, source step 1 / 2). */
+static __device__ __forceinline__ float bl_up2(const float *p, int h, int w, int y, int x)
+{
+    return bl_up(p, h, w, 0.5f, y, x);
 }
 
 #endif /* ICOREG_BILINEAR_H */

@@ -22,9 +22,13 @@
  *    same sums per output value, in another memory layout;
  *  - k_proj and v_proj run as one product with their weights stacked;
  *  - an attention block's aggregation, pooling, transposes to tokens and
- *    both LayerNorms are one kernel, o_proj writes the message
- *    channel-major directly, and fc1 reads [x; message] as two row
- *    blocks instead of a copied concatenation;
+ *    both LayerNorms are one kernel;
+ *  - fc1 [x; up4(o_proj O^T)] runs as fc1[:, :256] x + up4(Wm O^T) with
+ *    Wm = fc1[:, 256:] o_proj multiplied at load: the 4x upsampling is
+ *    linear within each channel plane, so it commutes with the channel
+ *    products, and the message half of fc1 runs on the 400 aggregated
+ *    tokens instead of the 6400 upsampled ones (sampled in the product's
+ *    epilogue, with the resize's arithmetic);
  *  - the fusion's "1 x 1 convolution + upsampled coarser level" sums are
  *    the 1 x 1 products' residual inputs instead of separate adds;
  *  - the same-size 3 x 3 convolutions run as Winograd F(2 x 2, 3 x 3)
@@ -189,7 +193,6 @@ static void load_attn(struct eloftr_model *m, struct pth_file *pf, int layer,
     LD(norm_g, "aggregation.norm.weight", 1, v1);
     LD(norm_b, "aggregation.norm.bias", 1, v1);
     LD(wq, "attention.q_proj.weight", 2, sq);
-    LD(wo, "attention.o_proj.weight", 2, sq);
     LD(fc1, "mlp.fc1.weight", 2, s1);
     LD(fc2, "mlp.fc2.weight", 2, s2);
     LD(mlp_g, "mlp.layer_norm.weight", 1, v1);
@@ -213,6 +216,43 @@ static void load_attn(struct eloftr_model *m, struct pth_file *pf, int layer,
         free(w);
         a->wkv = upload(m, kv, 2 * dd, "attention.kv_proj");
         free(kv);
+    }
+    {
+        /* The message reaches the MLP only as fc1[:, D:2D] up4(o_proj O^T)
+         * (O the attention output, up4 the 4x bilinear upsampling). The
+         * upsampling mixes pixels of one channel plane and the products
+         * mix channels of one pixel, so this equals
+         * up4((fc1[:, D:2D] o_proj) O^T): the two weights are multiplied
+         * here once, in double, and fc1's message half then runs on the
+         * na aggregated tokens instead of the n upsampled ones. */
+        const int D = ELOFTR_DIM;
+        float *wo, *f1, *wm = (float *)malloc((size_t)MLP * D * sizeof(float));
+        double *acc = (double *)malloc((size_t)D * sizeof(double));
+
+        if (!wm || !acc)
+            icoreg_fatal("ELoFTR: out of host memory");
+        snprintf(name, sizeof(name), "%s.attention.o_proj.weight", pre);
+        wo = read_host(pf, name, 2, sq);
+        snprintf(name, sizeof(name), "%s.mlp.fc1.weight", pre);
+        f1 = read_host(pf, name, 2, s1);
+        for (int i = 0; i < MLP; i++) {
+            for (int j = 0; j < D; j++)
+                acc[j] = 0.0;
+            for (int c = 0; c < D; c++) {
+                const double f = f1[(size_t)i * 2 * D + D + c];
+                const float *wr = wo + (size_t)c * D;
+
+                for (int j = 0; j < D; j++)
+                    acc[j] += f * wr[j];
+            }
+            for (int j = 0; j < D; j++)
+                wm[(size_t)i * D + j] = (float)acc[j];
+        }
+        a->wmsg = upload(m, wm, (size_t)MLP * D, "attention.message");
+        free(wo);
+        free(f1);
+        free(wm);
+        free(acc);
     }
 }
 
@@ -367,8 +407,7 @@ extern "C" void eloftr_alloc(struct eloftr_model *m, int H, int W)
     m->t_Q = walloc(m, 2 * ELOFTR_DIM * na, "queries");
     m->t_KV = walloc(m, 4 * ELOFTR_DIM * na, "keys and values");
     m->t_O = walloc(m, 2 * ELOFTR_DIM * na, "attention");
-    m->t_O2 = walloc(m, 2 * ELOFTR_DIM * na, "attention");
-    m->t_cat = walloc(m, 2 * ELOFTR_DIM * n, "messages");
+    m->t_O2 = walloc(m, 2 * MLP * na, "attention");
     m->t_tok = walloc(m, ELOFTR_DIM * n, "tokens");
     m->t_h1 = walloc(m, 2 * MLP * n, "mlp");
     m->t_h2 = walloc(m, 2 * ELOFTR_DIM * n, "mlp");
@@ -464,10 +503,11 @@ static void backbone(struct eloftr_model *m)
  *
  * The reference's sequence, with its layout changes folded away: the
  * aggregation, pooling, transposes to tokens and LayerNorms are one
- * kernel; o_proj writes the message channel-major (a product with the
- * token-major output as the transposed operand) for the 4x upsampling;
- * the MLP runs on channel-major maps, fc1 reading [x; message] as two row
- * blocks of one operand, and the MLP LayerNorm is fused with the residual
+ * kernel; o_proj and fc1's message half are one product (their weights
+ * multiplied at load) on the aggregated tokens, written channel-major (the
+ * token-major attention output as the transposed operand); its 4x
+ * upsampling is added inside fc1's product with x; the MLP runs on
+ * channel-major maps, and the MLP LayerNorm is fused with the residual
  * add. */
 static void agg_attn(struct eloftr_model *m, const struct eloftr_attn *a,
                      cl_mem X, cl_mem Y, int nimg, int use_rope)
@@ -489,28 +529,26 @@ static void agg_attn(struct eloftr_model *m, const struct eloftr_attn *a,
         ops_rope(o, m->t_Q, 0, D, rows, 1, D, na, m->rope, 1);
         ops_rope(o, m->t_KV, 0, 2 * D, rows, 1, D, na, m->rope, 1);
     }
-    for (int i = 0; i < nimg; i++) {
-        const long off = (long)i * na * D, kv = 2 * off;
-
-        ops_attention(o, ops_mat(m->t_Q, off, D), ops_mat(m->t_KV, kv, 2 * D),
-                      ops_mat(m->t_KV, kv + D, 2 * D),
-                      ops_mat(m->t_O, off, D), na, na, HEADS, hd,
-                      1.0f / sqrtf((float)hd), NULL);
-    }
-    /* message (D x na per image) = o_proj (D x D) * O^T, O token-major. */
-    ops_gemm(o, D, na, D, ops_mat(a->wo, 0, D),
+    /* Image i's queries attend to image i's keys: one launch for all. */
+    ops_attention_batch(o, nimg, ops_mat(m->t_Q, 0, D), (long)na * D,
+                        ops_mat(m->t_KV, 0, 2 * D), 2L * na * D,
+                        ops_mat(m->t_KV, D, 2 * D), 2L * na * D,
+                        ops_mat(m->t_O, 0, D), (long)na * D, na, na, HEADS, hd,
+                        1.0f / sqrtf((float)hd), NULL);
+    /* P (MLP x na per image) = (fc1[:, D:2D] o_proj) (MLP x D) * O^T, O
+     * token-major: fc1's message half on the aggregated tokens. */
+    ops_gemm(o, MLP, na, D, ops_mat(a->wmsg, 0, D),
              ops_bmat(m->t_O, 0, D, (long)na * D, 0), 1,
-             ops_bmat(m->t_O2, 0, na, (long)D * na, 0), nimg, 1, NULL, 0,
+             ops_bmat(m->t_O2, 0, na, (long)MLP * na, 0), nimg, 1, NULL, 0,
              NULL, 0, 1.0f, ACT_NONE, 0);
-    /* Upsampled messages of all images, (nimg D, h, w). */
-    ops_resize(o, m->t_O2, nimg * D, m->ah, m->aw, m->t_cat, m->h, m->w, 0, 0,
-               4.0f);
-    /* h1 (MLP x n) = leaky(fc1 (MLP x 2D) * [x; message] (2D x n)). */
-    ops_gemm_cat(o, MLP, n, 2 * D, ops_mat(a->fc1, 0, 2 * D),
-                 ops_bmat(X, 0, n, (long)D * n, 0),
-                 ops_bmat(m->t_cat, 0, n, (long)D * n, 0), D,
-                 ops_bmat(m->t_h1, 0, n, (long)MLP * n, 0), nimg, ACT_LEAKY,
-                 LEAKY);
+    /* h1 (MLP x n) = leaky(fc1[:, 0:D] (MLP x D) * x (D x n) + up4(P)):
+     * fc1 (MLP x 2D) * [x; up4(message)], the 4x upsampling (ops_resize,
+     * scale 4) sampled in the product's epilogue. */
+    ops_gemm_upres(o, MLP, n, D, ops_mat(a->fc1, 0, 2 * D),
+                   ops_bmat(X, 0, n, (long)D * n, 0),
+                   ops_bmat(m->t_h1, 0, n, (long)MLP * n, 0), nimg, m->t_O2,
+                   (long)MLP * na, m->ah, m->aw, m->h, m->w, 4, 1, ACT_LEAKY,
+                   LEAKY);
     /* h2 (D x n) = fc2 (D x MLP) * h1. */
     ops_gemm(o, D, n, MLP, ops_mat(a->fc2, 0, MLP),
              ops_bmat(m->t_h1, 0, n, (long)MLP * n, 0), 0,
@@ -616,16 +654,16 @@ static void conv1x1_up2_pair(struct eloftr_model *m, cl_mem X, int C, int H, int
 {
     const long HW = (long)H * W;
 
-    ops_gemm_up2res(m->ops, K, (int)HW, C, ops_mat(Wt, 0, C),
-                    ops_bmat(X, 0, HW, (long)C * HW, 0), ops_bmat(Y, 0, HW, (long)K * HW, 0),
-                    2, Rlow, (long)K * (HW / 4), H, W);
+    ops_gemm_upres(m->ops, K, (int)HW, C, ops_mat(Wt, 0, C),
+                   ops_bmat(X, 0, HW, (long)C * HW, 0), ops_bmat(Y, 0, HW, (long)K * HW, 0),
+                   2, Rlow, (long)K * (HW / 4), H / 2, W / 2, H, W, 2, 0, ACT_NONE, 0);
 }
 
 /* FPN fusion of both images (eloftr.c:573-604), every layer one launch for
  * the pair (the pair's channels are contiguous). The reference's three 2x
  * resizes are sampled on the fly by their consumers, with the resize's
  * arithmetic: the residuals of the two 1 x 1 convolutions
- * (ops_gemm_up2res) and fine matching (eloftr_fine_half). The result is
+ * (ops_gemm_upres) and fine matching (eloftr_fine_half). The result is
  * fu_c, the fine maps at half resolution (64, H / 2, W / 2) per image. */
 static void fusion(struct eloftr_model *m)
 {
@@ -756,8 +794,7 @@ extern "C" void eloftr_free(struct eloftr_model *m)
         &m->img,     &m->s_a,
         &m->s_b,     &m->f1p,     &m->f2p,     &m->xp,    &m->finep,
         &m->t_qn,    &m->t_kvn,   &m->t_Q,     &m->t_KV,  &m->t_O,
-        &m->t_O2,
-        &m->t_cat,   &m->t_tok,   &m->t_h1,    &m->t_h2,  &m->rope,
+        &m->t_O2,    &m->t_tok,   &m->t_h1,    &m->t_h2,  &m->rope,
         &m->s_blk,   &m->row_lse, &m->col_m,   &m->col_s, &m->row_max,
         &m->row_arg, &m->col_max, &m->col_arg, &m->fu_a,  &m->fu_b,
         &m->fu_c,    &m->m_idx,   &m->m_out,   &m->f_out};
@@ -777,7 +814,7 @@ extern "C" void eloftr_free(struct eloftr_model *m)
         for (int j = 0; j < 2; j++) {
             cl_mem *f[] = {&a[j]->q_agg, &a[j]->norm_g, &a[j]->norm_b,
                            &a[j]->wq,    &a[j]->wkv,
-                           &a[j]->wo,    &a[j]->fc1,    &a[j]->fc2,
+                           &a[j]->wmsg,  &a[j]->fc1,    &a[j]->fc2,
                            &a[j]->mlp_g, &a[j]->mlp_b};
 
             for (size_t i = 0; i < sizeof(f) / sizeof(f[0]); i++)

@@ -39,11 +39,13 @@ struct gemm_args {
      * the concatenation [B; B2] without being materialised. */
     const float *B2;
     int ksplit;
-    /* rup = 2: R is not in C's layout but (nb0 batches rs0 floats apart)
-     * M rows of rh x rw planes, and C's column n = y * rwo + x (rwo =
-     * 2 rw) receives R's 2x bilinear resize at (y, x) (ops_resize, pixel
-     * centres), sampled on the fly. */
-    int rup, rh, rw, rwo;
+    /* rup = 2 or 4: R is not in C's layout but (nb0 batches rs0 floats
+     * apart) M rows of rh x rw planes, and C's column n = y * rwo + x
+     * receives R's rup x bilinear resize at (y, x) (ops_resize with scale
+     * rup, pixel centres: source step rsc = 1 / rup), sampled on the fly.
+     * rpre: R is added before the activation instead of after it. */
+    int rup, rh, rw, rwo, rpre;
+    float rsc;
     long long rs0;
 };
 
@@ -65,13 +67,15 @@ void ops_gemm_cat(struct ops *o, int M, int N, int K, struct opnd A,
                   struct opnd B1, struct opnd B2, int ksplit, struct opnd C,
                   int nb, int act, float slope);
 
-/* C (M x N, nb batches C.s0 apart) = A (M x K) B (K x N, not transposed)
- * + the 2x bilinear resize of R, R holding nb batches (M, H / 2, W / 2)
- * rstride floats apart and N = H W: a product whose residual is an
- * upsampled map (ops_resize, then ops_gemm with residual), without
- * writing the upsampled map. */
-void ops_gemm_up2res(struct ops *o, int M, int N, int K, struct opnd A,
-                     struct opnd B, struct opnd C, int nb, cl_mem R,
-                     long rstride, int H, int W);
+/* C (M x N, nb batches C.s0 apart) = act(A (M x K) B (K x N, not
+ * transposed)) + the up x bilinear resize (ops_resize with scale up) of R
+ * to H x W = N, R holding nb batches (M, rh, rw) rstride floats apart;
+ * pre: the resize is added before the activation. A product whose
+ * residual or addend is an upsampled map (ops_resize, then ops_gemm with
+ * the map), without writing the upsampled map. */
+void ops_gemm_upres(struct ops *o, int M, int N, int K, struct opnd A,
+                    struct opnd B, struct opnd C, int nb, cl_mem R,
+                    long rstride, int rh, int rw, int H, int W, int up, int pre,
+                    int act, float slope);
 
 #endif /* ICOREG_GEMM_H */

@@ -132,9 +132,12 @@ __device__ __forceinline__ void gemm_epilogue(const gemm_args &g, const floatx16
                 v = g.alpha * acc[i][j][r];
                 if (g.bias)
                     v += g.bias[g.biasrow ? row : col];
+                if (R && g.rpre)
+                    v += bl_up(R + (long long)row * g.rh * g.rw, g.rh, g.rw, g.rsc, ry, rx);
                 v = icoreg_act(v, g.act, g.slope);
-                if (R)
-                    v += g.rup ? bl_up2(R + (long long)row * g.rh * g.rw, g.rh, g.rw, ry, rx)
+                if (R && !g.rpre)
+                    v += g.rup ? bl_up(R + (long long)row * g.rh * g.rw, g.rh, g.rw, g.rsc, ry,
+                                       rx)
                                : R[(long long)row * g.ldc + col];
                 C[(long long)row * g.ldc + col] = v;
             }

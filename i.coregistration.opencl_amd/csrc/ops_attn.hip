@@ -134,7 +134,8 @@ __global__ void __launch_bounds__(64 * ATT_NW)
                      float *__restrict__ O, int ldo, int Nq, int Nk, int d,
                      float scale, const unsigned char *__restrict__ kmask,
                      int tiles_per_split, float *__restrict__ part_o,
-                     float2 *__restrict__ part_ml)
+                     float2 *__restrict__ part_ml, int nh, long long bq,
+                     long long bk, long long bv, long long bo)
 {
     constexpr int DP = 32 * ND;     /* padded head dimension */
     constexpr int KP = DP + 1;      /* K tile row pitch (odd: no conflicts) */
@@ -146,7 +147,8 @@ __global__ void __launch_bounds__(64 * ATT_NW)
     __shared__ __align__(16) float Vs[2][ATT_KT * VP];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int h = blockIdx.y, half = lane >> 5, col = lane & 31;
+    const int h = blockIdx.y % nh, bi = blockIdx.y / nh;
+    const int half = lane >> 5, col = lane & 31;
     const int qi = (blockIdx.x * ATT_NW + wave) * 32 + col;
     const int ntiles = (Nk + ATT_KT - 1) / ATT_KT;
     const int t0 = blockIdx.z * tiles_per_split;
@@ -161,9 +163,9 @@ __global__ void __launch_bounds__(64 * ATT_NW)
      * one v_exp_f32. */
     const float qscale = scale * 1.4426950408889634f;
 
-    Q += (long long)h * d;
-    K += (long long)h * d;
-    V += (long long)h * d;
+    Q += bi * bq + (long long)h * d;
+    K += bi * bk + (long long)h * d;
+    V += bi * bv + (long long)h * d;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
         const int dd = 2 * s + half;
@@ -339,7 +341,7 @@ __global__ void __launch_bounds__(64 * ATT_NW)
         return;
     if (!part_o) {
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-        float *out = O + (long long)qi * ldo + (long long)h * d;
+        float *out = O + bi * bo + (long long)qi * ldo + (long long)h * d;
 
 #pragma unroll
         for (int tt = 0; tt < ND; tt++)
@@ -353,7 +355,7 @@ __global__ void __launch_bounds__(64 * ATT_NW)
     }
     else {
         const long long row =
-            ((long long)blockIdx.z * gridDim.y + h) * Nq + qi;
+            ((long long)blockIdx.z * gridDim.y + blockIdx.y) * Nq + qi;
         float *out = part_o + row * DP;
 
 #pragma unroll
@@ -366,30 +368,33 @@ __global__ void __launch_bounds__(64 * ATT_NW)
     }
 }
 
-/* Combine nsplit partial results per (query, head): weights
+/* Combine nsplit partial results per (image, query, head): weights
  * 2^(m_s - max m) (the maxima are in the base-2 domain), O = sum_s w_s O_s
  * / sum_s w_s l_s (zeros when no key was kept). One thread per output
  * value. */
 __global__ void __launch_bounds__(256)
     attn_merge_kernel(const float *__restrict__ part_o,
-                      const float2 *__restrict__ part_ml, int nsplit, int nh,
-                      int Nq, int d, int DP, float *__restrict__ O, int ldo)
+                      const float2 *__restrict__ part_ml, int nsplit, int nb,
+                      int nh, int Nq, int d, int DP, float *__restrict__ O,
+                      int ldo, long long bo)
 {
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-    const long long total = (long long)Nq * nh * d;
+    const long long total = (long long)nb * Nq * nh * d;
 
     if (idx >= total)
         return;
     const int dd = (int)(idx % d);
     const int h = (int)((idx / d) % nh);
-    const int qi = (int)(idx / ((long long)d * nh));
+    const long long bq = idx / ((long long)d * nh);
+    const int qi = (int)(bq % Nq), bi = (int)(bq / Nq);
+    const int y = bi * nh + h, ny = nb * nh;
     float mx = -INFINITY, L = 0.0f, acc = 0.0f;
 
     for (int s = 0; s < nsplit; s++)
-        mx = fmaxf(mx, part_ml[((long long)s * nh + h) * Nq + qi].x);
+        mx = fmaxf(mx, part_ml[((long long)s * ny + y) * Nq + qi].x);
     if (mx != -INFINITY)
         for (int s = 0; s < nsplit; s++) {
-            const long long row = ((long long)s * nh + h) * Nq + qi;
+            const long long row = ((long long)s * ny + y) * Nq + qi;
             const float2 ml = part_ml[row];
             const float w =
                 ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - mx);
@@ -397,14 +402,16 @@ __global__ void __launch_bounds__(256)
             L += w * ml.y;
             acc += w * part_o[row * DP + dd];
         }
-    O[(long long)qi * ldo + (long long)h * d + dd] = L > 0.0f ? acc / L : 0.0f;
+    O[bi * bo + (long long)qi * ldo + (long long)h * d + dd] =
+        L > 0.0f ? acc / L : 0.0f;
 }
 
 template <int ND, bool VEC, bool MASK>
-static void launch_nd(struct ops *ops, hipStream_t st, int nh, const float *Q,
-                      int ldq, const float *K, int ldk, const float *V, int ldv,
-                      float *O, int ldo, int Nq, int Nk, int d, float scale,
-                      const unsigned char *kmask)
+static void launch_nd(struct ops *ops, hipStream_t st, int nb, int nh,
+                      const float *Q, int ldq, long long bq, const float *K,
+                      int ldk, long long bk, const float *V, int ldv,
+                      long long bv, float *O, int ldo, long long bo, int Nq,
+                      int Nk, int d, float scale, const unsigned char *kmask)
 {
     const int qb = (Nq + 32 * ATT_NW - 1) / (32 * ATT_NW);
     const int ntiles = (Nk + ATT_KT - 1) / ATT_KT;
@@ -412,7 +419,7 @@ static void launch_nd(struct ops *ops, hipStream_t st, int nh, const float *Q,
      * least 2 key tiles (measured: more splits cost more in the merge
      * than they gain in occupancy). */
     const long long want = 8LL * (ops->ocl->cu_count > 0 ? ops->ocl->cu_count : 256);
-    const long long base = (long long)qb * ATT_NW * nh;
+    const long long base = (long long)qb * ATT_NW * nh * nb;
     int nsplit = (int)((want + base - 1) / base);
     int tps;
 
@@ -421,72 +428,79 @@ static void launch_nd(struct ops *ops, hipStream_t st, int nh, const float *Q,
     nsplit = tps > 0 ? (ntiles + tps - 1) / tps : 1;
     if (nsplit == 1) {
         hipLaunchKernelGGL((attention_kernel<ND, VEC, MASK>),
-                           dim3((unsigned)qb, (unsigned)nh, 1),
+                           dim3((unsigned)qb, (unsigned)(nh * nb), 1),
                            dim3(64 * ATT_NW), 0, st, Q, ldq, K, ldk, V, ldv,
                            O, ldo, Nq, Nk, d, scale, kmask, tps, nullptr,
-                           nullptr);
+                           nullptr, nh, bq, bk, bv, bo);
         return;
     }
     {
-        const size_t rows = (size_t)nsplit * nh * Nq;
+        const size_t rows = (size_t)nsplit * nb * nh * Nq;
         const size_t ob = rows * 32 * ND * sizeof(float);
         cl_mem sc = scratch_get(ops, ob + rows * sizeof(float2));
         float *po = (float *)sc->ptr;
         float2 *pml = (float2 *)((char *)sc->ptr + ob);
-        const long long total = (long long)Nq * nh * d;
+        const long long total = (long long)nb * Nq * nh * d;
 
         hipLaunchKernelGGL((attention_kernel<ND, VEC, MASK>),
-                           dim3((unsigned)qb, (unsigned)nh, (unsigned)nsplit),
+                           dim3((unsigned)qb, (unsigned)(nh * nb),
+                                (unsigned)nsplit),
                            dim3(64 * ATT_NW), 0, st, Q, ldq, K, ldk, V, ldv,
-                           O, ldo, Nq, Nk, d, scale, kmask, tps, po, pml);
+                           O, ldo, Nq, Nk, d, scale, kmask, tps, po, pml, nh,
+                           bq, bk, bv, bo);
         hipLaunchKernelGGL(attn_merge_kernel,
                            dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                           st, po, pml, nsplit, nh, Nq, d, 32 * ND, O, ldo);
+                           st, po, pml, nsplit, nb, nh, Nq, d, 32 * ND, O, ldo,
+                           bo);
     }
 }
 
-static void need_rows(const struct opnd &x, int rows, int cols,
-                      const char *operand)
+static void need_rows(const struct opnd &x, int nb, long long bs, int rows,
+                      int cols, const char *op, const char *operand)
 {
-    if (x.off < 0 || x.ld < 0)
-        icoreg_fatal("ops_attention: %s has a negative offset or ld", operand);
-    need_floats(x.buf, x.off, (long long)(rows - 1) * x.ld + cols,
-                "ops_attention", operand);
+    if (x.off < 0 || x.ld < 0 || bs < 0)
+        icoreg_fatal("%s: %s has a negative offset, ld or batch stride", op,
+                     operand);
+    need_floats(x.buf, x.off + (nb - 1) * bs,
+                (long long)(rows - 1) * x.ld + cols, op, operand);
 }
 
-extern "C" void ops_attention(struct ops *o, struct opnd Q, struct opnd K,
-                              struct opnd V, struct opnd O, int Nq, int Nk,
-                              int nh, int d, float scale, cl_mem kmask)
+/* nb independent problems at batch strides bq .. bo floats (the key mask,
+ * when given, is shared by all of them). */
+static void attention_impl(struct ops *o, const char *op, int nb,
+                           struct opnd Q, long long bq, struct opnd K,
+                           long long bk, struct opnd V, long long bv,
+                           struct opnd O, long long bo, int Nq, int Nk, int nh,
+                           int d, float scale, cl_mem kmask)
 {
-    ICOREG_API_BEGIN
     hipStream_t st = stream_of(o->ocl);
 
     if (d < 1 || d > OPS_MAX_HEAD_DIM)
         icoreg_fatal("HIP: attention head dimension %d not in 1..%d", d,
                      OPS_MAX_HEAD_DIM);
-    if (Nq < 0 || Nk < 0 || nh < 1 || nh > 65535)
-        icoreg_fatal("ops_attention: invalid sizes Nq=%d Nk=%d nh=%d", Nq, Nk,
-                     nh);
+    if (Nq < 0 || Nk < 0 || nh < 1 || nb < 1 || (long long)nh * nb > 65535)
+        icoreg_fatal("%s: invalid sizes Nq=%d Nk=%d nh=%d nb=%d", op, Nq, Nk,
+                     nh, nb);
     if (Nq == 0)
         return;
-    need_rows(Q, Nq, nh * d, "Q");
-    need_rows(O, Nq, nh * d, "O");
+    need_rows(Q, nb, bq, Nq, nh * d, op, "Q");
+    need_rows(O, nb, bo, Nq, nh * d, op, "O");
     if (Nk > 0) {
-        need_rows(K, Nk, nh * d, "K");
-        need_rows(V, Nk, nh * d, "V");
+        need_rows(K, nb, bk, Nk, nh * d, op, "K");
+        need_rows(V, nb, bv, Nk, nh * d, op, "V");
     }
     if (kmask)
-        need_bytes(kmask, 0, Nk, "ops_attention", "kmask");
+        need_bytes(kmask, 0, Nk, op, "kmask");
     prof_scope ps(o->ocl, "attention");
 #define ARGS                                                                   \
-    o, st, nh, cfptr(Q.buf) + Q.off, Q.ld, cfptr(K.buf) + K.off, K.ld,         \
-        cfptr(V.buf) + V.off, V.ld, fptr(O.buf) + O.off, O.ld, Nq, Nk, d,     \
-        scale, kmask ? (const unsigned char *)kmask->ptr : nullptr
+    o, st, nb, nh, cfptr(Q.buf) + Q.off, Q.ld, bq, cfptr(K.buf) + K.off, K.ld, \
+        bk, cfptr(V.buf) + V.off, V.ld, bv, fptr(O.buf) + O.off, O.ld, bo, Nq, \
+        Nk, d, scale, kmask ? (const unsigned char *)kmask->ptr : nullptr
     {
         /* 16-byte K / V loads when every row and head start is aligned. */
         const bool vec = d % 4 == 0 && K.ld % 4 == 0 && V.ld % 4 == 0 &&
-                         K.off % 4 == 0 && V.off % 4 == 0 &&
-                         ((uintptr_t)K.buf->ptr & 15) == 0 &&
+                         K.off % 4 == 0 && V.off % 4 == 0 && bk % 4 == 0 &&
+                         bv % 4 == 0 && ((uintptr_t)K.buf->ptr & 15) == 0 &&
                          ((uintptr_t)V.buf->ptr & 15) == 0;
 
 #define DISPATCH(ND)                                                           \
@@ -512,5 +526,26 @@ extern "C" void ops_attention(struct ops *o, struct opnd Q, struct opnd K,
     }
 #undef ARGS
     launch_check("attention");
+}
+
+extern "C" void ops_attention(struct ops *o, struct opnd Q, struct opnd K,
+                              struct opnd V, struct opnd O, int Nq, int Nk,
+                              int nh, int d, float scale, cl_mem kmask)
+{
+    ICOREG_API_BEGIN
+    attention_impl(o, "ops_attention", 1, Q, 0, K, 0, V, 0, O, 0, Nq, Nk, nh,
+                   d, scale, kmask);
+    ICOREG_API_END
+}
+
+extern "C" void ops_attention_batch(struct ops *o, int nb, struct opnd Q,
+                                    long bq, struct opnd K, long bk,
+                                    struct opnd V, long bv, struct opnd O,
+                                    long bo, int Nq, int Nk, int nh, int d,
+                                    float scale, cl_mem kmask)
+{
+    ICOREG_API_BEGIN
+    attention_impl(o, "ops_attention_batch", nb, Q, bq, K, bk, V, bv, O, bo,
+                   Nq, Nk, nh, d, scale, kmask);
     ICOREG_API_END
 }

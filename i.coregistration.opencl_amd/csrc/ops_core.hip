@@ -236,22 +236,23 @@ void ops_gemm_cat(struct ops *o, int M, int N, int K, struct opnd A,
     }
 }
 
-void ops_gemm_up2res(struct ops *o, int M, int N, int K, struct opnd A,
-                     struct opnd B, struct opnd C, int nb, cl_mem R,
-                     long rstride, int H, int W)
+void ops_gemm_upres(struct ops *o, int M, int N, int K, struct opnd A,
+                    struct opnd B, struct opnd C, int nb, cl_mem R,
+                    long rstride, int rh, int rw, int H, int W, int up, int pre,
+                    int act, float slope)
 {
-    const char *op = "ops_gemm_up2res";
+    const char *op = "ops_gemm_upres";
     gemm_args g;
 
-    if (M < 1 || N < 1 || K < 1 || nb < 1 || nb > 65535 || H < 2 || W < 2 ||
-        H % 2 || W % 2 || (long long)H * W != N || rstride < (long long)M * (H / 2) * (W / 2))
-        icoreg_fatal("%s: invalid sizes M=%d N=%d K=%d H=%d W=%d nb=%d", op, M, N, K, H,
-                     W, nb);
+    if (M < 1 || N < 1 || K < 1 || nb < 1 || nb > 65535 || rh < 1 || rw < 1 ||
+        H < 1 || W < 1 || (up != 2 && up != 4) || (long long)H * W != N ||
+        rstride < (long long)M * rh * rw)
+        icoreg_fatal("%s: invalid sizes M=%d N=%d K=%d rh=%d rw=%d H=%d W=%d up=%d nb=%d",
+                     op, M, N, K, rh, rw, H, W, up, nb);
     need_matrix(A.buf, A.off, A.ld, A.s0, A.s1, M, K, nb, 1, op, "A");
     need_matrix(B.buf, B.off, B.ld, B.s0, B.s1, K, N, nb, 1, op, "B");
     need_matrix(C.buf, C.off, C.ld, C.s0, C.s1, M, N, nb, 1, op, "C");
-    need_floats(R, 0, (long long)(nb - 1) * rstride + (long long)M * (H / 2) * (W / 2), op,
-                "R");
+    need_floats(R, 0, (long long)(nb - 1) * rstride + (long long)M * rh * rw, op, "R");
     if (C.ld != N)
         icoreg_fatal("%s: C rows must be whole planes (ld %lld, N %d)", op, (long long)C.ld, N);
     count32((long long)M * N, "gemm output");
@@ -271,11 +272,14 @@ void ops_gemm_up2res(struct ops *o, int M, int N, int K, struct opnd A,
     g.sc0 = C.s0;
     g.nb1 = 1;
     g.alpha = 1.0f;
-    g.act = ACT_NONE;
+    g.act = act;
+    g.slope = slope;
     g.R = cfptr(R);
-    g.rup = 2;
-    g.rh = H / 2;
-    g.rw = W / 2;
+    g.rup = up;
+    g.rpre = pre != 0;
+    g.rsc = 1.0f / (float)up;
+    g.rh = rh;
+    g.rw = rw;
     g.rwo = W;
     g.rs0 = rstride;
     if (!gemm_shape_ok(g, GEMM_B_KN))

@@ -332,6 +332,84 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+static inline bool aligned16(cl_mem m)
+{
+    return ((uintptr_t)m->ptr & 15) == 0;
+}
+
+/* The same for C % 4 == 0 and 16-byte aligned rows: lane l holds the
+ * float4 groups l + 64 t (t < NV), all of them loaded before the first
+ * reduction; DPP wave sums. */
+template <int NV>
+__global__ void __launch_bounds__(256)
+    layernorm4_kernel(const float4 *X, float4 *Y, const float4 *__restrict__ g,
+                      const float4 *__restrict__ bt, int C, long long rows,
+                      float eps, int act, float slope)
+{
+    const int lane = threadIdx.x & 63, C4 = C >> 2;
+    const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const float4 *x;
+    float4 *y, v[NV];
+    float s = 0.0f, mean, r;
+
+    if (row >= rows)
+        return;
+    x = X + row * C4;
+    y = Y + row * C4;
+#pragma unroll
+    for (int t = 0; t < NV; t++) {
+        const int c = lane + 64 * t;
+
+        v[t] = c < C4 ? x[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll
+    for (int t = 0; t < NV; t++)
+        s += (v[t].x + v[t].y) + (v[t].z + v[t].w);
+    mean = wave_sum_full(s) / C;
+    s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NV; t++)
+        if (lane + 64 * t < C4) {
+            const float d0 = v[t].x - mean, d1 = v[t].y - mean;
+            const float d2 = v[t].z - mean, d3 = v[t].w - mean;
+
+            s = fmaf(d0, d0, s);
+            s = fmaf(d1, d1, s);
+            s = fmaf(d2, d2, s);
+            s = fmaf(d3, d3, s);
+        }
+    r = 1.0f / sqrtf(wave_sum_full(s) / C + eps);
+#pragma unroll
+    for (int t = 0; t < NV; t++) {
+        const int c = lane + 64 * t;
+        float u[4] = {(v[t].x - mean) * r, (v[t].y - mean) * r,
+                      (v[t].z - mean) * r, (v[t].w - mean) * r};
+
+        if (c >= C4)
+            continue;
+        if (g) {
+            const float4 gv = g[c];
+
+            u[0] *= gv.x;
+            u[1] *= gv.y;
+            u[2] *= gv.z;
+            u[3] *= gv.w;
+        }
+        if (bt) {
+            const float4 bv = bt[c];
+
+            u[0] += bv.x;
+            u[1] += bv.y;
+            u[2] += bv.z;
+            u[3] += bv.w;
+        }
+        y[c] = make_float4(icoreg_act(u[0], act, slope),
+                           icoreg_act(u[1], act, slope),
+                           icoreg_act(u[2], act, slope),
+                           icoreg_act(u[3], act, slope));
+    }
+}
+
 extern "C" void ops_layernorm(struct ops *o, long rows, int C, cl_mem X,
                               cl_mem Y, cl_mem g, cl_mem b, float eps, int act,
                               float slope)
@@ -358,7 +436,24 @@ extern "C" void ops_layernorm(struct ops *o, long rows, int C, cl_mem X,
     hipLaunchKernelGGL(layernorm_kernel<V>, grid, block, 0, stream_of(o->ocl), \
                        cfptr(X), fptr(Y), cfptr(g), cfptr(b), C,               \
                        (long long)rows, eps, act, slope)
-    if (C <= 256)
+#define LN4(V)                                                                 \
+    hipLaunchKernelGGL(layernorm4_kernel<V>, grid, block, 0,                   \
+                       stream_of(o->ocl), (const float4 *)cfptr(X),            \
+                       (float4 *)fptr(Y), (const float4 *)cfptr(g),            \
+                       (const float4 *)cfptr(b), C, (long long)rows, eps, act, \
+                       slope)
+    const bool v4 = C % 4 == 0 && C <= 2048 && aligned16(X) && aligned16(Y) &&
+                    (!g || aligned16(g)) && (!b || aligned16(b));
+
+    if (v4 && C <= 256)
+        LN4(1);
+    else if (v4 && C <= 512)
+        LN4(2);
+    else if (v4 && C <= 1024)
+        LN4(4);
+    else if (v4)
+        LN4(8);
+    else if (C <= 256)
         LN(4);
     else if (C <= 512)
         LN(8);
@@ -369,6 +464,7 @@ extern "C" void ops_layernorm(struct ops *o, long rows, int C, cl_mem X,
     else
         LN(0);
 #undef LN
+#undef LN4
     launch_check("layernorm");
     ICOREG_API_END
 }

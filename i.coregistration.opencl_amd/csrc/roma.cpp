@@ -655,15 +655,12 @@ static void block(struct roma_model *m, const struct roma_block *b, int nimg,
     ops_layernorm(o, R, D, m->t_x, m->t_n, b->n1g, b->n1b, eps, ACT_NONE, 0);
     ops_linear(o, (int)R, D, 3 * D, m->t_n, 0, b->qkv_w, b->qkv_b, m->t_qkv, 0,
                ACT_NONE, 0, 0);
-    for (int k = 0; k < nimg; k++) {
-        const long q0 = (long)k * N * 3 * D;
-
-        ops_attention(o, ops_mat(m->t_qkv, q0, 3 * D),
-                      ops_mat(m->t_qkv, q0 + D, 3 * D),
-                      ops_mat(m->t_qkv, q0 + 2 * D, 3 * D),
-                      ops_mat(m->t_o, (long)k * N * D, D), N, N, heads, hd,
-                      1.0f / sqrtf((float)hd), NULL);
-    }
+    /* Each image's tokens attend within the image: one launch for all. */
+    ops_attention_batch(o, nimg, ops_mat(m->t_qkv, 0, 3 * D), 3L * N * D,
+                        ops_mat(m->t_qkv, D, 3 * D), 3L * N * D,
+                        ops_mat(m->t_qkv, 2 * D, 3 * D), 3L * N * D,
+                        ops_mat(m->t_o, 0, D), (long)N * D, N, N, heads, hd,
+                        1.0f / sqrtf((float)hd), NULL);
     ops_linear(o, (int)R, D, D, m->t_o, 0, b->proj_w, b->proj_b, m->t_x, 0,
                ACT_NONE, 0, 1);
     ops_layernorm(o, R, D, m->t_x, m->t_n, b->n2g, b->n2b, eps, ACT_NONE, 0);

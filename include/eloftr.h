@@ -31,7 +31,9 @@ extern "C" {
 struct eloftr_attn {
     cl_mem q_agg;          /* Depthwise 4 x 4 (256, 1, 4, 4). */
     cl_mem norm_g, norm_b; /* LayerNorm of the aggregated tokens. */
-    cl_mem wq, wo;         /* (256, 256), no bias. */
+    cl_mem wq;             /* (256, 256), no bias. */
+    /* fc1[:, 256:512] o_proj (512, 256): the message's route into fc1. */
+    cl_mem wmsg;
     cl_mem wkv;            /* k_proj over v_proj: (512, 256), no bias. */
     cl_mem fc1, fc2;       /* (512, 512), (256, 512), no bias. */
     cl_mem mlp_g, mlp_b;   /* LayerNorm after the MLP. */
@@ -63,7 +65,7 @@ struct eloftr_model {
      * reads the half-resolution maps fine_h[k] (views of fu_c). */
     cl_mem img, s_a, s_b, f1p, f2p, xp, finep;
     cl_mem f1[2], f2[2], x[2], fine[2], fine_h[2];
-    cl_mem t_qn, t_kvn, t_Q, t_KV, t_O, t_O2, t_cat, t_tok, t_h1, t_h2,
+    cl_mem t_qn, t_kvn, t_Q, t_KV, t_O, t_O2, t_tok, t_h1, t_h2,
         rope;
     cl_mem s_blk, row_lse, col_m, col_s, row_max, row_arg, col_max, col_arg;
     cl_mem fu_a, fu_b, fu_c, m_idx, m_out;

@@ -148,6 +148,16 @@ void ops_attention(struct ops *o, struct opnd Q, struct opnd K, struct opnd V,
                    struct opnd O, int Nq, int Nk, int nh, int d, float scale,
                    cl_mem kmask);
 
+/* ops_attention on nb independent problems in one launch, problem i's Q,
+ * K, V and O starting bq, bk, bv, bo floats after problem i - 1's (kmask
+ * shared). No counterpart in the reference, which loops over the images
+ * of a pair with one attention launch each (eloftr.c:405-449,
+ * roma.c:692-713). */
+void ops_attention_batch(struct ops *o, int nb, struct opnd Q, long bq,
+                         struct opnd K, long bk, struct opnd V, long bv,
+                         struct opnd O, long bo, int Nq, int Nk, int nh, int d,
+                         float scale, cl_mem kmask);
+
 /* Rotary encoding in place on rows x (nh heads of d) of X (row stride
  * ld, offset off), row r at table row r % npos of cs (npos x d / 2
  * (cos, sin) pairs). interleaved: pairs (2f, 2f + 1), else (f, f + d/2).

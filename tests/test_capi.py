@@ -100,6 +100,9 @@ def test_bounds_checks_reject_out_of_range_views(ic):
         api.ops_act(C.byref(ops), buf, buf, 1 << 31, 0, 0.0)
     with pytest.raises(ic.IcoregError, match="head dimension 129"):
         api.ops_attention(C.byref(ops), m, m, m, m, 1, 1, 1, 129, 1.0, None)
+    with pytest.raises(ic.IcoregError, match="ops_attention_batch: Q"):
+        api.ops_attention_batch(C.byref(ops), 2, m, 4, m, 0, m, 0, m, 0, 1, 1, 1, 1,
+                                1.0, None)
     g = ic.geom(3, 3, 1, 1, 1, 1, 1, 1, 2)
     with pytest.raises(ic.IcoregError, match="3 -> 4 channels in 2 groups"):
         api.ops_conv2d(C.byref(ops), buf, 3, 4, 4, buf, None, 4, C.byref(g), None,

@@ -76,6 +76,35 @@ def test_attention_shapes(shape, dev, ic, orc):
     assert err <= 1e-5, f"{shape}: {err:.2e}"
 
 
+@pytest.mark.parametrize("shape", [(400, 400, 8, 32, 2), (161, 97, 4, 64, 3)],
+                         ids=["eloftr", "ragged"])
+def test_attention_batch(shape, dev, ic, orc):
+    """ops_attention_batch against the oracle problem by problem, the
+    problems laid out with a gap between them."""
+    from oracle_lib import fp
+    Nq, Nk, nh, d, nb = shape
+    print(f"[attention_batch] {shape}", flush=True)
+    rng = np.random.default_rng(99 + nb)
+    E = nh * d
+    bq, bk, bo = Nq * E + 12, Nk * 2 * E + 8, Nq * E + 4
+    q = rng.uniform(-2, 2, nb * bq).astype(np.float32)
+    kv = rng.uniform(-2, 2, nb * bk).astype(np.float32)
+    Q, KV, O = dev.upload(q), dev.upload(kv), dev.zeros(nb * bo)
+    scale = float(1.0 / np.sqrt(d))
+    dev.api.ops_attention_batch(dev.po, nb, ic.mat(Q, 0, E), bq, ic.mat(KV, 0, 2 * E), bk,
+                                ic.mat(KV, E, 2 * E), bk, ic.mat(O, 0, E), bo, Nq, Nk, nh,
+                                d, scale, None)
+    got = dev.read(O, nb * bo)
+    for i in range(nb):
+        ref = np.zeros(Nq * E, np.float32)
+        qi, ki = q[i * bq:], kv[i * bk:]
+        orc.orc_attention(fp(qi), 0, E, fp(ki), 0, 2 * E, fp(ki), E, 2 * E, fp(ref), 0, E,
+                          Nq, Nk, nh, d, scale, None)
+        err = opcases.rel_err(got[i * bo:i * bo + Nq * E], ref)
+        assert err <= 1e-5, f"{shape} problem {i}: {err:.2e}"
+        assert not got[i * bo + Nq * E:(i + 1) * bo].any(), "gap written"
+
+
 CONV_SHAPES = [
     # (nb, C, H, W, K, k, s, p, norm, act): ELoFTR backbone / fusion, VGG,
     # DISK (5 x 5 with normalisation), stride 2, ragged sizes.
@@ -130,5 +159,37 @@ def test_conv_shapes(shape, dev, ic, orc):
                              C.byref(g), *[ic.mem(v) for v in mb], act, 0.1, Y.mem,
                              K * Ho * Wo)
     got = dev.read(Y, nb * K * Ho * Wo)
+    err = opcases.rel_err(got, ref)
+    assert err <= 1e-5, f"{shape}: {err:.2e}"
+
+
+LN_SHAPES = [
+    # (rows, C, affine): the RoMa ViT rows (1024) and the float4 variants'
+    # lane tails (C / 4 not a multiple of 64), the scalar form (C % 4 != 0).
+    (3202, 1024, 1),
+    (7, 2048, 1),
+    (33, 260, 0),
+    (10, 4, 1),
+    (5, 2050, 1),
+]
+
+
+@pytest.mark.parametrize("shape", LN_SHAPES, ids=[str(s) for s in LN_SHAPES])
+def test_layernorm_shapes(shape, dev, ic, orc):
+    from oracle_lib import fp
+    rows, Cc, affine = shape
+    print(f"[layernorm] {shape}", flush=True)
+    rng = np.random.default_rng(500 + Cc)
+    x = rng.uniform(-3, 3, rows * Cc).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, Cc).astype(np.float32) if affine else None
+    b = rng.uniform(-1, 1, Cc).astype(np.float32) if affine else None
+    ref = np.zeros(rows * Cc, np.float32)
+    orc.orc_layernorm(rows, Cc, fp(x), fp(ref), fp(g), fp(b), 1e-6, opcases.ACT_GELU, 0.0)
+    X, Y = dev.upload(x), dev.zeros(rows * Cc)
+    G = dev.upload(g) if affine else None
+    B = dev.upload(b) if affine else None
+    dev.api.ops_layernorm(dev.po, rows, Cc, X.mem, Y.mem, ic.mem(G), ic.mem(B), 1e-6,
+                          opcases.ACT_GELU, 0.0)
+    got = dev.read(Y, rows * Cc)
     err = opcases.rel_err(got, ref)
     assert err <= 1e-5, f"{shape}: {err:.2e}"
