@@ -47,9 +47,26 @@ bool conv_wino_supported(int kh, int kw, int sy, int sx, int py, int px,
 size_t conv_wino_weight_floats(int K, int C, bool norm);
 /* U from w (K, C, 3, 3), in the order conv_wino_weight_floats names. */
 void conv_wino_weights(const float *w, int K, int C, bool norm, float *U, hipStream_t s);
+/* Work split of the row-split Winograd kernel. A unit is one block's
+ * output: 32 channels (nkb channel blocks) x 32 tiles (ntb tile blocks) of
+ * one image. Units 0..nfull-1 run whole; each later unit is cut into
+ * split pieces over its input channels, which write partial sums to part
+ * (split x 4096 floats per unit), added up by a second kernel. */
+struct wino_split {
+    int nkb, ntb, nfull, split;
+    float *part;
+};
+
+/* The split for nb images on cus CUs: the units left over after an equal
+ * whole number per CU are cut so that every CU gets about one piece. */
+wino_split conv_wino_plan(const conv_args &a, int nb, int cus);
+/* Floats of part that the plan needs (0 without split). */
+size_t conv_wino_part_floats(const conv_args &a, int nb, const wino_split &sp);
+
 /* The convolution of a (a.w unused) with filters U from conv_wino_weights
- * with norm = (a.mean != NULL), nb images. */
-void conv_wino_launch(const conv_args &a, const float *U, int nb,
+ * with norm = (a.mean != NULL), nb images, split sp (conv_wino_plan, part
+ * set). */
+void conv_wino_launch(const conv_args &a, const float *U, int nb, const wino_split &sp,
                       hipStream_t s);
 
 /* Filters of a 3 x 3 convolution without input normalisation transformed

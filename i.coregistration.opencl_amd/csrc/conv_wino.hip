@@ -37,6 +37,7 @@
  *    xi are combined through LDS, and bias and activation are applied on
  *    the 2 x 2 outputs. */
 
+#include <algorithm>
 #include <hip/hip_runtime.h>
 
 #include "act.h"
@@ -437,12 +438,40 @@ __global__ void __launch_bounds__(256)
 }
 
 /* gfx9 s_waitcnt immediates: vmcnt(0) alone; vmcnt(0) and lgkmcnt(0). */
+/* Most pieces per split unit. */
+#define WR_MAX_SPLIT 8
+
+/* Output channel kg of a 2 x 2 output tile at (oy, ox): y = (y(oy, ox),
+ * y(oy + 1, ox), y(oy, ox + 1), y(oy + 1, ox + 1)) plus bias, activated,
+ * clipped to the output. */
+static __device__ __forceinline__ void wr_store(const conv_args &a, float *out, int kg, int oy,
+                                                int ox, float4 y)
+{
+    const float yy[2][2] = {{y.x, y.y}, {y.z, y.w}};
+    float bias;
+
+    if (kg >= a.K)
+        return;
+    bias = a.bias ? a.bias[kg] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        if (ox + j >= a.Wo)
+            continue;
+        if (oy < a.Ho)
+            out[((long long)kg * a.Ho + oy) * a.Wo + ox + j] =
+                icoreg_act(yy[j][0] + bias, a.act, a.slope);
+        if (oy + 1 < a.Ho)
+            out[((long long)kg * a.Ho + oy + 1) * a.Wo + ox + j] =
+                icoreg_act(yy[j][1] + bias, a.act, a.slope);
+    }
+}
+
 #define WR_WAIT_VM0 0x0F70
 #define WR_WAIT_VM0_LGKM0 0x0070
 
 template <bool X4>
 __global__ void __launch_bounds__(256, 4)
-    conv_wino_rows_kernel(const conv_args a, const float *__restrict__ Uf)
+    conv_wino_rows_kernel(const conv_args a, const float *__restrict__ Uf, const wino_split sp)
 {
     constexpr int TR = 4, TC = 8, BK = 32;
     /* Per-slice patch buffer (floats) and pitches of the two layouts. */
@@ -457,16 +486,30 @@ __global__ void __launch_bounds__(256, 4)
     const int half = lane >> 5, col = lane & 31;
     const int tr = col >> 3, tc = col & 7;
     const int C = a.C, H = a.H, W = a.W, K = a.K;
+    const int nk = (C + WR_CC - 1) / WR_CC;
+    /* Unit u = (image bz, tile block by, channel block bx), channel blocks
+     * fastest (they share the input tiles in L2); units from nfull on are
+     * cut into split pieces over the input-channel slices. */
+    int u = blockIdx.x, piece = -1, kt0 = 0, kt1 = nk;
+
+    if (u >= sp.nfull) {
+        const int p = u - sp.nfull;
+
+        piece = p % sp.split;
+        u = sp.nfull + p / sp.split;
+        kt0 = piece * nk / sp.split;
+        kt1 = (piece + 1) * nk / sp.split;
+    }
+    const int bx = u % sp.nkb, by = (u / sp.nkb) % sp.ntb, bz = u / (sp.nkb * sp.ntb);
     const int tiles_w = (W + 1) / 2, bw = (tiles_w + TC - 1) / TC;
-    const int ty0 = (blockIdx.y / bw) * TR, tx0 = (blockIdx.y % bw) * TC;
-    const int k0 = blockIdx.x * BK;
+    const int ty0 = (by / bw) * TR, tx0 = (by % bw) * TC;
+    const int k0 = bx * BK;
     const int iy0 = 2 * ty0 - 1, ix0 = 2 * tx0 - 1;
     const long long HW = (long long)H * W;
-    const float *in = a.in + (long long)blockIdx.z * a.in_stride;
+    const float *in = a.in + (long long)bz * a.in_stride;
     const unsigned long long ibytes = (unsigned long long)C * HW * 4;
-    const int nk = (C + WR_CC - 1) / WR_CC;
     /* This wave's filter fragments: 16 floats a lane, 4096 a slice. */
-    const float *uf = Uf + ((long long)blockIdx.x * nk * 16 + wave * 4) * 256 + lane * 4;
+    const float *uf = Uf + ((long long)bx * nk * 16 + wave * 4) * 256 + lane * 4;
     /* Rows of the tile that row xi of B^T combines: u = d[ra] + be d[rb]
      * (row 2 negated in the filters). */
     const int ra = wave == 0 ? 0 : 1, rb = wave == 3 ? 3 : 2;
@@ -557,7 +600,7 @@ __global__ void __launch_bounds__(256, 4)
      * (to Pn) and filters (to rn) are loaded meanwhile. */
     auto step = [&](int kt, const float *__restrict__ Pc, float *__restrict__ Pn, float *ru,
                     float *rn) {
-        const bool more = kt + 1 < nk;
+        const bool more = kt + 1 < kt1;
         float bv[4][4];
 
         /* ru arrived before the last barrier. Redefining it here (an empty
@@ -616,13 +659,13 @@ __global__ void __launch_bounds__(256, 4)
         __syncthreads();
     };
 
-    load_patch(0, P0);
-    load_u(0, ruA);
+    load_patch(kt0 * WR_CC, P0);
+    load_u(kt0, ruA);
     __builtin_amdgcn_s_waitcnt(WR_WAIT_VM0);
     __syncthreads();
-    for (int kt = 0; kt < nk; kt += 2) {
+    for (int kt = kt0; kt < kt1; kt += 2) {
         step(kt, P0, P1, ruA, ruB);
-        if (kt + 1 < nk)
+        if (kt + 1 < kt1)
             step(kt + 1, P1, P0, ruB, ruA);
     }
 
@@ -630,7 +673,13 @@ __global__ void __launch_bounds__(256, 4)
      * registers, Y = A^T Z over xi through LDS. */
     {
         float *Zs = lds; /* [xi][j][k][t32] */
-        float *out = a.out + (long long)blockIdx.z * a.out_stride;
+        float *out = a.out + (long long)bz * a.out_stride;
+        const int ts = tid & 31, otr = ts / TC, otc = ts % TC;
+        const int oy = 2 * (ty0 + otr), ox = 2 * (tx0 + otc);
+        /* (y0, y1) of output columns ox, ox + 1 (rows oy, oy + 1) for
+         * channel (tid / 32) + 8 i of the block, before bias and
+         * activation. */
+        float4 yv[BK / 8];
 
 #pragma unroll
         for (int r = 0; r < 16; r++) {
@@ -642,37 +691,74 @@ __global__ void __launch_bounds__(256, 4)
             Zs[((wave * 2 + 1) * BK + k) * 32 + col] = z1;
         }
         __syncthreads();
-        {
-            const int ts = tid & 31, otr = ts / TC, otc = ts % TC;
-            const int oy = 2 * (ty0 + otr), ox = 2 * (tx0 + otc);
+#pragma unroll
+        for (int i = 0; i < BK / 8; i++) {
+            const int k = (tid >> 5) + 8 * i;
+            float y[2][2];
 
 #pragma unroll
-            for (int i = 0; i < BK / 8; i++) {
-                const int k = (tid >> 5) + 8 * i, kg = k0 + k;
-                const float bias = a.bias && kg < K ? a.bias[kg] : 0.0f;
+            for (int j = 0; j < 2; j++) {
+                const float z0 = Zs[((0 * 2 + j) * BK + k) * 32 + ts];
+                const float z1 = Zs[((1 * 2 + j) * BK + k) * 32 + ts];
+                const float z2 = Zs[((2 * 2 + j) * BK + k) * 32 + ts];
+                const float z3 = Zs[((3 * 2 + j) * BK + k) * 32 + ts];
 
-                if (kg >= K)
-                    continue;
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const float z0 = Zs[((0 * 2 + j) * BK + k) * 32 + ts];
-                    const float z1 = Zs[((1 * 2 + j) * BK + k) * 32 + ts];
-                    const float z2 = Zs[((2 * 2 + j) * BK + k) * 32 + ts];
-                    const float z3 = Zs[((3 * 2 + j) * BK + k) * 32 + ts];
-                    const float y0 = z0 + z1 + z2, y1 = z1 - z2 - z3;
-
-                    if (ox + j >= a.Wo)
-                        continue;
-                    if (oy < a.Ho)
-                        out[((long long)kg * a.Ho + oy) * a.Wo + ox + j] =
-                            icoreg_act(y0 + bias, a.act, a.slope);
-                    if (oy + 1 < a.Ho)
-                        out[((long long)kg * a.Ho + oy + 1) * a.Wo + ox + j] =
-                            icoreg_act(y1 + bias, a.act, a.slope);
-                }
+                y[j][0] = z0 + z1 + z2;
+                y[j][1] = z1 - z2 - z3;
             }
+            yv[i] = make_float4(y[0][0], y[0][1], y[1][0], y[1][1]);
         }
+        if (piece >= 0) {
+            /* A piece of a split unit: partial sums to the unit's slot,
+             * added up by wino_pieces_kernel. */
+            float4 *pp = (float4 *)sp.part +
+                         ((long long)(u - sp.nfull) * sp.split + piece) * (BK * 32);
+
+#pragma unroll
+            for (int i = 0; i < BK / 8; i++)
+                pp[((tid >> 5) + 8 * i) * 32 + ts] = yv[i];
+            return;
+        }
+#pragma unroll
+        for (int i = 0; i < BK / 8; i++)
+            wr_store(a, out, k0 + (tid >> 5) + 8 * i, oy, ox, yv[i]);
     }
+}
+
+/* The split units: one thread per (unit, channel, 2 x 2 tile) adds the
+ * pieces' partial sums in piece order (all loads issued first) and
+ * stores the output as conv_wino_rows_kernel does. */
+__global__ void __launch_bounds__(256)
+    wino_pieces_kernel(const conv_args a, const wino_split sp, int tail)
+{
+    constexpr int TR = 4, TC = 8, BK = 32;
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int t = (int)(e / (BK * 32)), w = (int)(e % (BK * 32));
+    const int k = w / 32, ts = w % 32;
+
+    if (t >= tail)
+        return;
+    const int u = sp.nfull + t;
+    const int bx = u % sp.nkb, by = (u / sp.nkb) % sp.ntb, bz = u / (sp.nkb * sp.ntb);
+    const int bw = ((a.W + 1) / 2 + TC - 1) / TC;
+    const int oy = 2 * ((by / bw) * TR + ts / TC), ox = 2 * ((by % bw) * TC + ts % TC);
+    const float4 *q = (const float4 *)sp.part + (long long)t * sp.split * (BK * 32) + w;
+    float4 p[WR_MAX_SPLIT], v;
+
+#pragma unroll
+    for (int pc = 0; pc < WR_MAX_SPLIT; pc++)
+        if (pc < sp.split)
+            p[pc] = q[(long long)pc * (BK * 32)];
+    v = p[0];
+#pragma unroll
+    for (int pc = 1; pc < WR_MAX_SPLIT; pc++)
+        if (pc < sp.split) {
+            v.x += p[pc].x;
+            v.y += p[pc].y;
+            v.z += p[pc].z;
+            v.w += p[pc].w;
+        }
+    wr_store(a, a.out + (long long)bz * a.out_stride, bx * BK + k, oy, ox, v);
 }
 
 /* Blocks of 8 x 16 output pixels (the larger block's 16 x 16 on a
@@ -733,20 +819,66 @@ static void wino_launch(const conv_args &a, const float *U, int nb,
                            dim3(256), 0, s, a, U);
 }
 
-void conv_wino_launch(const conv_args &a, const float *U, int nb,
+wino_split conv_wino_plan(const conv_args &a, int nb, int cus)
+{
+    wino_split sp;
+    const int nk = (a.C + WR_CC - 1) / WR_CC;
+    long long units, rem;
+
+    sp.nkb = (a.K + 31) / 32;
+    sp.ntb = (int)wino_blocks(a.Ho, a.Wo, 4);
+    sp.part = nullptr;
+    units = (long long)sp.nkb * sp.ntb * nb;
+    sp.nfull = (int)units;
+    sp.split = 1;
+    if (!wino_rows(a.C, a.mean != nullptr) || cus < 1 || nk < 4)
+        return sp;
+    rem = units % cus;
+    /* Only when the leftover is a large share of the work: a CU holds
+     * up to 4 blocks, and with fewer than 4 units per CU the CUs that get
+     * one more unit than the others set the time. */
+    if (rem == 0 || units >= 4LL * cus)
+        return sp;
+    /* rem leftover units over cus CUs: about one piece per CU, at least
+     * two slices per piece. */
+    sp.split = (int)std::min<long long>(std::min<long long>(cus / rem, nk / 2), WR_MAX_SPLIT);
+    if (sp.split < 2) {
+        sp.split = 1;
+        return sp;
+    }
+    sp.nfull = (int)(units - rem);
+    return sp;
+}
+
+size_t conv_wino_part_floats(const conv_args &a, int nb, const wino_split &sp)
+{
+    const long long units = (long long)sp.nkb * sp.ntb * nb;
+
+    (void)a;
+    return sp.split > 1 ? (size_t)(units - sp.nfull) * sp.split * 4096 : 0;
+}
+
+void conv_wino_launch(const conv_args &a, const float *U, int nb, const wino_split &sp,
                       hipStream_t s)
 {
     if (wino_rows(a.C, a.mean != nullptr)) {
         /* Row-split kernel; 16-byte patch loads when every image row
          * starts 16-byte aligned. */
-        const dim3 grid((a.K + 31) / 32, (unsigned)wino_blocks(a.Ho, a.Wo, 4), nb);
+        const long long units = (long long)sp.nkb * sp.ntb * nb;
+        const dim3 grid((unsigned)(sp.nfull + (units - sp.nfull) * sp.split));
         const bool x4 = a.W % 4 == 0 && a.in_stride % 4 == 0 &&
                         ((unsigned long long)(size_t)a.in) % 16 == 0;
 
         if (x4)
-            hipLaunchKernelGGL(conv_wino_rows_kernel<true>, grid, dim3(256), 0, s, a, U);
+            hipLaunchKernelGGL(conv_wino_rows_kernel<true>, grid, dim3(256), 0, s, a, U, sp);
         else
-            hipLaunchKernelGGL(conv_wino_rows_kernel<false>, grid, dim3(256), 0, s, a, U);
+            hipLaunchKernelGGL(conv_wino_rows_kernel<false>, grid, dim3(256), 0, s, a, U, sp);
+        if (sp.split > 1) {
+            const long long tail = units - sp.nfull;
+
+            hipLaunchKernelGGL(wino_pieces_kernel, dim3((unsigned)((tail * 1024 + 255) / 256)),
+                               dim3(256), 0, s, a, sp, (int)tail);
+        }
         return;
     }
     /* 32 tiles x 32 channels per block, 8 input channels per slice,

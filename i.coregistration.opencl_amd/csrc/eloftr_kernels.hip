@@ -19,6 +19,7 @@
  * (v_mfma_f32_32x32x2f32, 8 output tiles over 4 waves), the softmax
  * statistics, argmax and the 3 x 3 second stage read from LDS. */
 
+#include <climits>
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -34,6 +35,10 @@ using namespace icoreg;
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 #define COL_CHUNK 64
+/* Column merges: MERGE_C columns per block, MERGE_G thread groups per
+ * column splitting the chunks. */
+#define MERGE_C 16
+#define MERGE_G 16
 
 /* ---- rows ----------------------------------------------------------------- */
 
@@ -146,30 +151,41 @@ __global__ void __launch_bounds__(256)
     part[(long long)c * N + j] = make_float2(m, s);
 }
 
-/* Chunks merged into the block's (max, sum) in two passes (the maximum
- * of the chunk maxima, then the rescaled sums: independent loads, no
- * serial chain), then into the running (cm, cs) as eloftr_col_lse does
- * (eloftr_kernels.cl:62-65). */
+/* Chunks merged into the block's (max, sum): group g of a column's
+ * threads takes chunks g, g + MERGE_G, ... in two passes (the maximum of
+ * the chunk maxima, then the rescaled sums: independent loads, no serial
+ * chain), the groups are combined in order, and the result goes into the
+ * running (cm, cs) as eloftr_col_lse does (eloftr_kernels.cl:62-65). */
 __global__ void __launch_bounds__(256)
     col_lse_merge_kernel(const float2 *__restrict__ part, int nchunks, int N,
                          float *__restrict__ cm, float *__restrict__ cs)
 {
-    const int j = blockIdx.x * 256 + threadIdx.x;
+    __shared__ float2 red[MERGE_G][MERGE_C];
+    const int cl = threadIdx.x % MERGE_C, g = threadIdx.x / MERGE_C;
+    const int j = blockIdx.x * MERGE_C + cl;
     float m = -INFINITY, s = 0.0f, mo, mn;
 
-    if (j >= N)
-        return;
-#pragma unroll 8
-    for (int c = 0; c < nchunks; c++)
-        m = fmaxf(m, part[(long long)c * N + j].x);
-    if (m != -INFINITY) {
-#pragma unroll 8
-        for (int c = 0; c < nchunks; c++) {
-            const float2 p = part[(long long)c * N + j];
+    if (j < N) {
+        for (int c = g; c < nchunks; c += MERGE_G)
+            m = fmaxf(m, part[(long long)c * N + j].x);
+        if (m != -INFINITY)
+            for (int c = g; c < nchunks; c += MERGE_G) {
+                const float2 p = part[(long long)c * N + j];
 
-            s += p.x == -INFINITY ? 0.0f : p.y * expf(p.x - m);
-        }
+                s += p.x == -INFINITY ? 0.0f : p.y * expf(p.x - m);
+            }
     }
+    red[g][cl] = make_float2(m, s);
+    __syncthreads();
+    if (g != 0 || j >= N)
+        return;
+    m = -INFINITY;
+    s = 0.0f;
+    for (int q = 0; q < MERGE_G; q++)
+        m = fmaxf(m, red[q][cl].x);
+    if (m != -INFINITY)
+        for (int q = 0; q < MERGE_G; q++)
+            s += red[q][cl].x == -INFINITY ? 0.0f : red[q][cl].y * expf(red[q][cl].x - m);
     mo = cm[j];
     mn = fmaxf(mo, m);
     if (mn == -INFINITY)
@@ -206,29 +222,46 @@ __global__ void __launch_bounds__(256)
     pi[(long long)c * N + j] = bi;
 }
 
-/* Chunks merged in increasing row order with a strict comparison, from
- * the running state (cmax, carg): the first row reaching the maximum
- * wins, as in the sequential scan of eloftr_conf_col. */
+/* Chunks merged from the running state (cmax, carg): group g of a
+ * column's threads scans chunks g, g + MERGE_G, ... in increasing order
+ * with a strict comparison, and the groups' results are merged with ties
+ * to the lowest row. Rows of the running state precede the block's, so
+ * the first row reaching the maximum wins, as in the sequential scan of
+ * eloftr_conf_col. */
 __global__ void __launch_bounds__(256)
     conf_col_merge_kernel(const float *__restrict__ pv,
                           const int *__restrict__ pi, int nchunks, int N,
                           float *__restrict__ cmax, int *__restrict__ carg)
 {
-    const int j = blockIdx.x * 256 + threadIdx.x;
-    float best;
-    int bi;
+    __shared__ float rv[MERGE_G][MERGE_C];
+    __shared__ int ri[MERGE_G][MERGE_C];
+    const int cl = threadIdx.x % MERGE_C, g = threadIdx.x / MERGE_C;
+    const int j = blockIdx.x * MERGE_C + cl;
+    float best = -INFINITY;
+    int bi = INT_MAX;
 
-    if (j >= N)
+    if (j < N)
+        for (int c = g; c < nchunks; c += MERGE_G) {
+            const float v = pv[(long long)c * N + j];
+
+            if (v > best) {
+                best = v;
+                bi = pi[(long long)c * N + j];
+            }
+        }
+    rv[g][cl] = best;
+    ri[g][cl] = bi;
+    __syncthreads();
+    if (g != 0 || j >= N)
         return;
     best = cmax[j];
     bi = carg[j];
-#pragma unroll 8
-    for (int c = 0; c < nchunks; c++) {
-        const float v = pv[(long long)c * N + j];
+    for (int q = 0; q < MERGE_G; q++) {
+        const float v = rv[q][cl];
 
-        if (v > best) {
+        if (v > best || (v == best && ri[q][cl] < bi && v != -INFINITY)) {
             best = v;
-            bi = pi[(long long)c * N + j];
+            bi = ri[q][cl];
         }
     }
     cmax[j] = best;
@@ -279,7 +312,7 @@ extern "C" void eloftr_col_lse(struct ops *o, cl_mem S, int R, int N,
     hipLaunchKernelGGL(col_lse_part_kernel, dim3((N + 255) / 256, nch),
                        dim3(256), 0, stream_of(o->ocl), cfptr(S), R, N,
                        (float2 *)part->ptr);
-    hipLaunchKernelGGL(col_lse_merge_kernel, dim3((N + 255) / 256), dim3(256),
+    hipLaunchKernelGGL(col_lse_merge_kernel, dim3((N + MERGE_C - 1) / MERGE_C), dim3(256),
                        0, stream_of(o->ocl), (const float2 *)part->ptr, nch, N,
                        fptr(cm), fptr(cs));
     launch_check(op);
@@ -345,7 +378,7 @@ extern "C" void eloftr_conf_col(struct ops *o, cl_mem S, int R, int N, int r0,
                        cfptr(lse), (const float *)base,
                        (float *)(base + lc_bytes),
                        (int *)(base + lc_bytes + pv_bytes));
-    hipLaunchKernelGGL(conf_col_merge_kernel, dim3((N + 255) / 256), dim3(256),
+    hipLaunchKernelGGL(conf_col_merge_kernel, dim3((N + MERGE_C - 1) / MERGE_C), dim3(256),
                        0, stream_of(o->ocl), (const float *)(base + lc_bytes),
                        (const int *)(base + lc_bytes + pv_bytes), nch, N,
                        fptr(cmax), (int *)carg->ptr);
@@ -429,24 +462,31 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-/* lse[r0 + r] from the band partials of row r. */
+/* lse[r0 + r] from the band partials of row r: MERGE_C lanes per row
+ * split the bands, combined with lane exchanges in a fixed order. */
 __global__ void __launch_bounds__(256)
     lse_row_merge_kernel(const float2 *__restrict__ rpart, int R, int nbands, int r0,
                          float *__restrict__ lse)
 {
-    const int r = blockIdx.x * 256 + threadIdx.x;
-    const float2 *p;
-    float m = -INFINITY, e = 0.0f;
+    const int r = blockIdx.x * (256 / MERGE_C) + threadIdx.x / MERGE_C;
+    const int q0 = threadIdx.x % MERGE_C;
+    const float2 *p = rpart + (long long)min(r, R - 1) * nbands;
+    float m = -INFINITY, e = 0.0f, mt;
 
-    if (r >= R)
-        return;
-    p = rpart + (long long)r * nbands;
-    for (int q = 0; q < nbands; q++)
+    for (int q = q0; q < nbands; q += MERGE_C)
         m = fmaxf(m, p[q].x);
-    if (m != -INFINITY)
-        for (int q = 0; q < nbands; q++)
-            e += p[q].x == -INFINITY ? 0.0f : p[q].y * __expf(p[q].x - m);
-    lse[r0 + r] = m + logf(e);
+    mt = m;
+#pragma unroll
+    for (int o = MERGE_C / 2; o > 0; o >>= 1)
+        mt = fmaxf(mt, __shfl_xor(mt, o, MERGE_C));
+    if (mt != -INFINITY)
+        for (int q = q0; q < nbands; q += MERGE_C)
+            e += p[q].x == -INFINITY ? 0.0f : p[q].y * __expf(p[q].x - mt);
+#pragma unroll
+    for (int o = MERGE_C / 2; o > 0; o >>= 1)
+        e += __shfl_xor(e, o, MERGE_C);
+    if (r < R && q0 == 0)
+        lse[r0 + r] = mt + logf(e);
 }
 
 /* Confidence maxima of the tile: per (row, band) and per (chunk, column),
@@ -575,9 +615,9 @@ void eloftr_lse_tiles(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse,
     hipLaunchKernelGGL(lse_tile_kernel, dim3(nbands, nch), dim3(256), 0, stream_of(o->ocl),
                        cfptr(S), R, N, nbands, (float2 *)sc->ptr,
                        (float2 *)((char *)sc->ptr + rb));
-    hipLaunchKernelGGL(lse_row_merge_kernel, dim3((R + 255) / 256), dim3(256), 0,
+    hipLaunchKernelGGL(lse_row_merge_kernel, dim3((R + 256 / MERGE_C - 1) / (256 / MERGE_C)), dim3(256), 0,
                        stream_of(o->ocl), (const float2 *)sc->ptr, R, nbands, r0, fptr(lse));
-    hipLaunchKernelGGL(col_lse_merge_kernel, dim3((N + 255) / 256), dim3(256), 0,
+    hipLaunchKernelGGL(col_lse_merge_kernel, dim3((N + MERGE_C - 1) / MERGE_C), dim3(256), 0,
                        stream_of(o->ocl), (const float2 *)((char *)sc->ptr + rb), nch, N,
                        fptr(cm), fptr(cs));
     launch_check(op);
@@ -620,7 +660,7 @@ void eloftr_conf_tiles(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse
                        stream_of(o->ocl), (const float *)(base + lcb),
                        (const int *)(base + lcb + rpb), R, nbands, r0, fptr(rmax),
                        (int *)rarg->ptr);
-    hipLaunchKernelGGL(conf_col_merge_kernel, dim3((N + 255) / 256), dim3(256), 0,
+    hipLaunchKernelGGL(conf_col_merge_kernel, dim3((N + MERGE_C - 1) / MERGE_C), dim3(256), 0,
                        stream_of(o->ocl), (const float *)(base + lcb + 2 * rpb),
                        (const int *)(base + lcb + 2 * rpb + cpb), nch, N, fptr(cmax),
                        (int *)carg->ptr);

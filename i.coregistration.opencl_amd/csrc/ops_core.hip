@@ -444,15 +444,26 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
         a.gate = mean ? cfptr(alpha) : nullptr;
         a.act = act;
         a.slope = slope;
+        wino_split sp = conv_wino_plan(a, nb, o->ocl->cu_count);
+        const size_t pb = conv_wino_part_floats(a, nb, sp) * sizeof(float);
+        const float *Uf;
+
         if (!U) {
-            U = scratch_get(o, conv_wino_weight_floats(K, C, mean != nullptr) *
-                                   sizeof(float));
+            /* Filters, then the split pieces' partial sums, in scratch. */
+            const size_t ub = (conv_wino_weight_floats(K, C, mean != nullptr) *
+                                   sizeof(float) + 255) & ~(size_t)255;
+            cl_mem sc = scratch_get(o, ub + pb);
+
+            Uf = cfptr(sc);
+            sp.part = pb ? (float *)((char *)sc->ptr + ub) : nullptr;
             prof_scope ps(o->ocl, "conv_wino_weights");
-            conv_wino_weights(cfptr(w), K, C, mean != nullptr, fptr(U),
+            conv_wino_weights(cfptr(w), K, C, mean != nullptr, fptr(sc),
                               stream_of(o->ocl));
             launch_check("conv_wino_weights");
         }
         else {
+            Uf = cfptr(U);
+            sp.part = pb ? fptr(scratch_get(o, pb)) : nullptr;
             /* Prepared filters are in the order of a convolution without
              * input normalisation. */
             if (mean)
@@ -462,7 +473,7 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
                         op, "Winograd filters");
         }
         prof_scope ps(o->ocl, "conv_wino");
-        conv_wino_launch(a, cfptr(U), nb, stream_of(o->ocl));
+        conv_wino_launch(a, Uf, nb, sp, stream_of(o->ocl));
         launch_check("conv_wino");
         return;
     }

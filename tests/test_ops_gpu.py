@@ -129,6 +129,11 @@ CONV_SHAPES = [
     # an odd number of 8-channel slices, a partial block of output channels.
     (2, 40, 23, 37, 40, 3, 1, 1, 0, 2),
     (1, 72, 18, 28, 36, 3, 1, 1, 0, 1),
+    # Row-split Winograd with whole and split units on 256 CUs: 300 units
+    # (256 whole, 44 in 4 pieces), and 336 units (256 whole, 80 in 3
+    # pieces, the partial channel block among the split ones).
+    (1, 64, 80, 80, 192, 3, 1, 1, 0, 2),
+    (2, 48, 30, 90, 200, 3, 1, 1, 0, 1),
 ]
 
 
