@@ -11,6 +11,15 @@
 
 #include "ops.h"
 
+/* Rotary rotation of the pair (a, b) by (cos, sin) = rot, the order of
+ * operations fixed so that every kernel that applies it rounds alike. */
+__device__ __forceinline__ void icoreg_rope_pair(float a, float b, float2 rot, float &x0,
+                                                 float &x1)
+{
+    x0 = fmaf(a, rot.x, -(b * rot.y));
+    x1 = fmaf(a, rot.y, b * rot.x);
+}
+
 __device__ __forceinline__ float icoreg_act(float v, int act, float slope)
 {
     switch (act) {

@@ -518,17 +518,12 @@ static void agg_attn(struct eloftr_model *m, const struct eloftr_attn *a,
 
     eloftr_aggregate(o, X, Y, nimg, D, m->h, m->w, a->q_agg, a->norm_g,
                      a->norm_b, EPS_LN, m->t_qn, m->t_kvn);
-    ops_linear(o, rows, D, D, m->t_qn, 0, a->wq, NULL, m->t_Q, 0, ACT_NONE, 0,
-               0);
-    /* Keys (columns 0..D-1) and values (D..2D-1) of t_KV in one
-     * product. */
-    ops_linear(o, rows, D, 2 * D, m->t_kvn, 0, a->wkv, NULL, m->t_KV, 0,
-               ACT_NONE, 0, 0);
-    if (use_rope) {
-        /* Row r takes table row r % na: the same positions per image. */
-        ops_rope(o, m->t_Q, 0, D, rows, 1, D, na, m->rope, 1);
-        ops_rope(o, m->t_KV, 0, 2 * D, rows, 1, D, na, m->rope, 1);
-    }
+    /* Queries, and keys (columns 0..D-1) with values (D..2D-1) of t_KV,
+     * in one launch, the rotary encoding of the queries and keys in its
+     * epilogue; row r takes table row r % na: the same positions per
+     * image. */
+    ops_linear2_rope(o, rows, D, m->t_qn, a->wq, m->t_Q, D, use_rope ? D : 0, m->t_kvn, a->wkv,
+                     m->t_KV, 2 * D, use_rope ? D : 0, m->rope, D, na);
     /* Image i's queries attend to image i's keys: one launch for all. */
     ops_attention_batch(o, nimg, ops_mat(m->t_Q, 0, D), (long)na * D,
                         ops_mat(m->t_KV, 0, 2 * D), 2L * na * D,

@@ -47,6 +47,11 @@ struct gemm_args {
     int rup, rh, rw, rwo, rpre;
     float rsc;
     long long rs0;
+    /* Small-product kernel only: rotary encoding of output columns
+     * 0..rcols-1 (ops_rope with one head of rd columns, interleaved pairs,
+     * table row r % rnpos of rope for output row r). */
+    const float2 *rope;
+    int rcols, rd, rnpos;
 };
 
 /* True if the kernel takes these leading dimensions: each at least its
@@ -58,7 +63,23 @@ bool gemm_shape_ok(const gemm_args &g, int bmode);
 void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
                  int cus, hipStream_t s);
 
+/* True if gemm_launch would run g on the small-product kernel. */
+bool gemm_smallk_ok(const gemm_args &g, int bmode, int nb, bool va, bool vb, int cus);
+
+/* Two products that both pass gemm_smallk_ok with B given N x K and one
+ * batch, in one launch of the small-product kernel. */
+void gemm_launch_smallk2(const gemm_args &g1, const gemm_args &g2, hipStream_t s);
+
 #include "ops.h"
+
+/* Y1 (rows x n1) = X1 (rows x in) W1^T and Y2 (rows x n2) = X2 W2^T, both
+ * token-major with no bias (two ops_linear calls), followed by the rotary
+ * encoding ops_rope(Y, 0, n, rows, 1, rd, npos, cs, 1) of the first rc1 /
+ * rc2 columns (0: none): one launch when both products are small,
+ * otherwise the separate calls. */
+void ops_linear2_rope(struct ops *o, int rows, int in, cl_mem X1, cl_mem W1, cl_mem Y1, int n1,
+                      int rc1, cl_mem X2, cl_mem W2, cl_mem Y2, int n2, int rc2, cl_mem cs,
+                      int rd, int npos);
 
 /* ops_gemm with B (K x N, not transposed) given as two row blocks: rows
  * 0..ksplit-1 in B1, the rest in B2 (same ld and batch stride s0; ksplit a

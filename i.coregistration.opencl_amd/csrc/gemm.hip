@@ -422,7 +422,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
 #define GEMM_SK_MAXK 256
 
 template <int MODE>
-__global__ void __launch_bounds__(512) gemm_smallk(const gemm_args g)
+__global__ void __launch_bounds__(512)
+    gemm_smallk(const gemm_args g1, const gemm_args g2, int nblk1)
 {
     constexpr int NTH = 512, T = 32;
     /* Row-major panels as loaded (no transposing stores): A [m][k] and B
@@ -432,9 +433,13 @@ __global__ void __launch_bounds__(512) gemm_smallk(const gemm_args g)
     constexpr int P = GEMM_SK_MAXK + 2;
     __shared__ __align__(16) float As[T * P], Bs[T * P];
 
+    /* Blocks nblk1.. run the second product. */
+    const bool second = (int)blockIdx.x >= nblk1;
+    const gemm_args &g = second ? g2 : g1;
+    const int bx = second ? (int)blockIdx.x - nblk1 : (int)blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tiles_n = (g.N + T - 1) / T;
-    const int m0 = (blockIdx.x / tiles_n) * T, n0 = (blockIdx.x % tiles_n) * T;
+    const int m0 = (bx / tiles_n) * T, n0 = (bx % tiles_n) * T;
     const long long bt = blockIdx.y, b0 = bt / g.nb1, b1 = bt % g.nb1;
     const float *A = g.A + b0 * g.sa0 + b1 * g.sa1;
     const float *B = g.B + b0 * g.sb0 + b1 * g.sb1;
@@ -527,13 +532,12 @@ __global__ void __launch_bounds__(512) gemm_smallk(const gemm_args g)
     {
         float *C = g.C + b0 * g.sc0 + b1 * g.sc1;
         const float *R = g.R ? g.R + b0 * g.sc0 + b1 * g.sc1 : nullptr;
-
-        for (int e = tid; e < T * T; e += NTH) {
-            const int row = e / T, col = e % T, gr = m0 + row, gc = n0 + col;
+        /* Output (row, col) of the tile: the 8 partials in order, then
+         * alpha, bias, activation, residual. */
+        auto value = [&](int row, int col) {
+            const int gr = m0 + row, gc = n0 + col;
             float v = 0.0f;
 
-            if (gr >= M || gc >= N)
-                continue;
 #pragma unroll
             for (int w = 0; w < 8; w++)
                 v += As[(w * T + row) * T + col];
@@ -543,6 +547,33 @@ __global__ void __launch_bounds__(512) gemm_smallk(const gemm_args g)
             v = icoreg_act(v, g.act, g.slope);
             if (R)
                 v += R[(long long)gr * g.ldc + gc];
+            return v;
+        };
+
+        for (int e = tid; e < T * T; e += NTH) {
+            const int row = e / T, col = e % T, gr = m0 + row, gc = n0 + col;
+            float v;
+
+            if (gr >= M || gc >= N)
+                continue;
+            v = value(row, col);
+            if (g.rope && gc < g.rcols) {
+                /* The pair (gc & ~1, gc | 1) lies in the tile (n0 is a
+                 * multiple of 32, rcols even and at most N). */
+                const float vp = value(row, col ^ 1);
+                const float2 rot =
+                    g.rope[(long long)(gr % g.rnpos) * (g.rd / 2) + (gc % g.rd) / 2];
+                float x0, x1;
+
+                if (col & 1) {
+                    icoreg_rope_pair(vp, v, rot, x0, x1);
+                    v = x1;
+                }
+                else {
+                    icoreg_rope_pair(v, vp, rot, x0, x1);
+                    v = x0;
+                }
+            }
             C[(long long)gr * g.ldc + gc] = v;
         }
     }
@@ -781,6 +812,26 @@ bool gemm_shape_ok(const gemm_args &g, int bmode)
     return true;
 }
 
+bool gemm_smallk_ok(const gemm_args &g, int bmode, int nb, bool va, bool vb, int cus)
+{
+    /* Small products that would fill under half of the CUs with 64 x 64
+     * tiles: the one-shot small-K kernel. */
+    const long long tiles64 = (long long)((g.M + 63) / 64) * ((g.N + 63) / 64) * nb;
+
+    va = va && g.K % 4 == 0;
+    vb = vb && (bmode == GEMM_B_KN ? g.N % 4 == 0 : g.K % 4 == 0);
+    return bmode != GEMM_B_CONV && va && vb && g.K <= GEMM_SK_MAXK && g.K % 16 == 0 &&
+           g.ksplit == 0 && g.rup == 0 && 2 * tiles64 <= cus;
+}
+
+void gemm_launch_smallk2(const gemm_args &g1, const gemm_args &g2, hipStream_t s)
+{
+    const int n1 = ((g1.M + 31) / 32) * ((g1.N + 31) / 32);
+    const int n2 = ((g2.M + 31) / 32) * ((g2.N + 31) / 32);
+
+    hipLaunchKernelGGL(gemm_smallk<GEMM_B_NK>, dim3(n1 + n2, 1), dim3(512), 0, s, g1, g2, n1);
+}
+
 void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
                  int cus, hipStream_t s)
 {
@@ -796,22 +847,15 @@ void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
      * ELoFTR pipelines (operands fresh from the previous kernel) they
      * were 5-70 % slower on the same shapes, so the kernel's WGM x WGN
      * generality is not used here. */
-    {
-        /* Small products that would fill under half of the CUs with 64 x
-         * 64 tiles: the one-shot small-K kernel. */
-        const long long tiles64 =
-            (long long)((g.M + 63) / 64) * ((g.N + 63) / 64) * nb;
+    if (gemm_smallk_ok(g, bmode, nb, va, vb, cus)) {
+        const int nblk = ((g.M + 31) / 32) * ((g.N + 31) / 32);
+        const dim3 grid(nblk, nb);
 
-        if (bmode != GEMM_B_CONV && va && vb && g.K <= GEMM_SK_MAXK && g.K % 16 == 0 &&
-            g.ksplit == 0 && g.rup == 0 && 2 * tiles64 <= cus) {
-            const dim3 grid(((g.M + 31) / 32) * ((g.N + 31) / 32), nb);
-
-            if (bmode == GEMM_B_NK)
-                hipLaunchKernelGGL(gemm_smallk<GEMM_B_NK>, grid, dim3(512), 0, s, g);
-            else
-                hipLaunchKernelGGL(gemm_smallk<GEMM_B_KN>, grid, dim3(512), 0, s, g);
-            return;
-        }
+        if (bmode == GEMM_B_NK)
+            hipLaunchKernelGGL(gemm_smallk<GEMM_B_NK>, grid, dim3(512), 0, s, g, g, nblk);
+        else
+            hipLaunchKernelGGL(gemm_smallk<GEMM_B_KN>, grid, dim3(512), 0, s, g, g, nblk);
+        return;
     }
     /* The LDS-DMA kernel: in the ELoFTR and RoMa pipelines it is faster
      * only for products with few output rows (M <= 256, B given K x N,

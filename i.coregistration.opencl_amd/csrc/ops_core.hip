@@ -119,22 +119,13 @@ static bool vec_ok(const struct opnd &x)
            x.s0 % 4 == 0 && x.s1 % 4 == 0;
 }
 
-extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
-                         struct opnd B, int transb, struct opnd C, int nb,
-                         int nb1, cl_mem bias, int biasrow, cl_mem R, long roff,
-                         float alpha, int act, float slope)
+/* ops_gemm's checks and kernel arguments (M, N > 0). */
+static gemm_args gemm_make(const char *op, int M, int N, int K, struct opnd A, struct opnd B,
+                           int transb, struct opnd C, int nb, int nb1, cl_mem bias,
+                           int biasrow, cl_mem R, long roff, float alpha, int act, float slope)
 {
-    ICOREG_API_BEGIN
-    const char *op = "ops_gemm";
     gemm_args g;
 
-    if (M < 0 || N < 0 || K < 0 || nb < 1 || nb1 < 1 || nb > 65535)
-        icoreg_fatal("%s: invalid sizes M=%d N=%d K=%d nb=%d nb1=%d", op, M, N,
-                     K, nb, nb1);
-    if (act < ACT_NONE || act > ACT_GELU_TANH)
-        icoreg_fatal("%s: unknown activation %d", op, act);
-    if (M == 0 || N == 0)
-        return;
     need_matrix(A.buf, A.off, A.ld, A.s0, A.s1, M, K, nb, nb1, op, "A");
     if (transb)
         need_matrix(B.buf, B.off, B.ld, B.s0, B.s1, N, K, nb, nb1, op, "B");
@@ -174,7 +165,27 @@ extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
         icoreg_fatal("%s: leading dimensions lda=%d ldb=%d not supported "
                      "(each at least its row length, below 4 Mi floats)",
                      op, A.ld, B.ld);
+    return g;
+}
+
+extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
+                         struct opnd B, int transb, struct opnd C, int nb,
+                         int nb1, cl_mem bias, int biasrow, cl_mem R, long roff,
+                         float alpha, int act, float slope)
+{
+    ICOREG_API_BEGIN
+    const char *op = "ops_gemm";
+
+    if (M < 0 || N < 0 || K < 0 || nb < 1 || nb1 < 1 || nb > 65535)
+        icoreg_fatal("%s: invalid sizes M=%d N=%d K=%d nb=%d nb1=%d", op, M, N,
+                     K, nb, nb1);
+    if (act < ACT_NONE || act > ACT_GELU_TANH)
+        icoreg_fatal("%s: unknown activation %d", op, act);
+    if (M == 0 || N == 0)
+        return;
     {
+        const gemm_args g = gemm_make(op, M, N, K, A, B, transb, C, nb, nb1, bias, biasrow,
+                                      R, roff, alpha, act, slope);
         prof_scope ps(o->ocl, "gemm");
 
         gemm_launch(g, transb ? GEMM_B_NK : GEMM_B_KN, nb, vec_ok(A),
@@ -182,6 +193,49 @@ extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
         launch_check("gemm");
     }
     ICOREG_API_END
+}
+
+void ops_linear2_rope(struct ops *o, int rows, int in, cl_mem X1, cl_mem W1, cl_mem Y1, int n1,
+                      int rc1, cl_mem X2, cl_mem W2, cl_mem Y2, int n2, int rc2, cl_mem cs,
+                      int rd, int npos)
+{
+    const char *op = "ops_linear2_rope";
+    const int cus = o->ocl->cu_count;
+
+    if (rows < 1 || in < 1 || n1 < 1 || n2 < 1 || rd < 2 || rd % 2 || npos < 1 || rc1 < 0 ||
+        rc2 < 0 || rc1 % rd || rc2 % rd || rc1 > n1 || rc2 > n2)
+        icoreg_fatal("%s: invalid sizes rows=%d in=%d n1=%d n2=%d rc1=%d rc2=%d rd=%d", op, rows,
+                     in, n1, n2, rc1, rc2, rd);
+    if (rc1 || rc2)
+        need_floats(cs, 0, (long long)(rows < npos ? rows : npos) * rd, op, "cs");
+    {
+        const struct opnd x1 = ops_mat(X1, 0, in), w1 = ops_mat(W1, 0, in);
+        const struct opnd x2 = ops_mat(X2, 0, in), w2 = ops_mat(W2, 0, in);
+        gemm_args g1 = gemm_make(op, rows, n1, in, x1, w1, 1, ops_mat(Y1, 0, n1), 1, 1, NULL, 0,
+                                 NULL, 0, 1.0f, ACT_NONE, 0.0f);
+        gemm_args g2 = gemm_make(op, rows, n2, in, x2, w2, 1, ops_mat(Y2, 0, n2), 1, 1, NULL, 0,
+                                 NULL, 0, 1.0f, ACT_NONE, 0.0f);
+
+        if (gemm_smallk_ok(g1, GEMM_B_NK, 1, vec_ok(x1), vec_ok(w1), cus) &&
+            gemm_smallk_ok(g2, GEMM_B_NK, 1, vec_ok(x2), vec_ok(w2), cus)) {
+            g1.rope = rc1 ? (const float2 *)cfptr(cs) : nullptr;
+            g1.rcols = rc1;
+            g2.rope = rc2 ? (const float2 *)cfptr(cs) : nullptr;
+            g2.rcols = rc2;
+            g1.rd = g2.rd = rd;
+            g1.rnpos = g2.rnpos = npos;
+            prof_scope ps(o->ocl, "gemm");
+            gemm_launch_smallk2(g1, g2, stream_of(o->ocl));
+            launch_check("gemm");
+            return;
+        }
+    }
+    ops_linear(o, rows, in, n1, X1, 0, W1, NULL, Y1, 0, ACT_NONE, 0.0f, 0);
+    ops_linear(o, rows, in, n2, X2, 0, W2, NULL, Y2, 0, ACT_NONE, 0.0f, 0);
+    if (rc1)
+        ops_rope(o, Y1, 0, n1, rows, rc1 / rd, rd, npos, cs, 1);
+    if (rc2)
+        ops_rope(o, Y2, 0, n2, rows, rc2 / rd, rd, npos, cs, 1);
 }
 
 void ops_gemm_cat(struct ops *o, int M, int N, int K, struct opnd A,

@@ -538,8 +538,7 @@ __global__ void __launch_bounds__(256)
     i1 = interleaved ? 2 * f + 1 : f + nf;
     a = x[i0];
     b = x[i1];
-    x[i0] = a * rot.x - b * rot.y;
-    x[i1] = a * rot.y + b * rot.x;
+    icoreg_rope_pair(a, b, rot, x[i0], x[i1]);
 }
 
 extern "C" void ops_rope(struct ops *o, cl_mem X, long off, int ld, long rows,
