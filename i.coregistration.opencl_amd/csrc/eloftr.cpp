@@ -510,7 +510,7 @@ static void backbone(struct eloftr_model *m)
  * channel-major maps, and the MLP LayerNorm is fused with the residual
  * add. */
 static void agg_attn(struct eloftr_model *m, const struct eloftr_attn *a,
-                     cl_mem X, cl_mem Y, int nimg, int use_rope)
+                     cl_mem X, cl_mem Y, int nimg, int use_rope, cl_mem T = NULL)
 {
     struct ops *o = m->ops;
     const int D = ELOFTR_DIM, n = m->h * m->w, na = m->ah * m->aw;
@@ -549,7 +549,7 @@ static void agg_attn(struct eloftr_model *m, const struct eloftr_attn *a,
              ops_bmat(m->t_h1, 0, n, (long)MLP * n, 0), 0,
              ops_bmat(m->t_h2, 0, n, (long)D * n, 0), nimg, 1, NULL, 1, NULL,
              0, 1.0f, ACT_NONE, 0);
-    eloftr_ln_residual(o, m->t_h2, nimg, D, n, a->mlp_g, a->mlp_b, EPS_LN, X);
+    eloftr_ln_residual(o, m->t_h2, nimg, D, n, a->mlp_g, a->mlp_b, EPS_LN, X, T);
 }
 
 /* eloftr.c:451-463: image 1's cross attention sees image 0's features
@@ -558,9 +558,13 @@ static void agg_attn(struct eloftr_model *m, const struct eloftr_attn *a,
 static void transformer(struct eloftr_model *m)
 {
     for (int l = 0; l < ELOFTR_LAYERS; l++) {
+        const bool last = l == ELOFTR_LAYERS - 1;
+
         agg_attn(m, &m->self_attn[l], m->xp, m->xp, 2, 1);
-        agg_attn(m, &m->cross_attn[l], m->x[0], m->x[1], 1, 0);
-        agg_attn(m, &m->cross_attn[l], m->x[1], m->x[0], 1, 0);
+        /* The last layer also writes the features token-major for the
+         * coarse matching (t_tok, t_h1 once its MLP is done). */
+        agg_attn(m, &m->cross_attn[l], m->x[0], m->x[1], 1, 0, last ? m->t_tok : NULL);
+        agg_attn(m, &m->cross_attn[l], m->x[1], m->x[0], 1, 0, last ? m->t_h1 : NULL);
     }
 }
 
@@ -575,12 +579,14 @@ static void coarse_match(struct eloftr_model *m)
     /* Both passes read each block of S once (rows and columns together). */
     const bool tiles = eloftr_tiles_ok(m->s_blk, n);
 
-    ops_transpose(o, m->x[0], m->t_tok, 1, D, n);
-    ops_transpose(o, m->x[1], m->t_h1, 1, D, n);
-    ocl_fill(m->ocl, m->col_m, 0, n, -INFINITY);
-    ocl_fill(m->ocl, m->col_s, 0, n, 0.0f);
-    ocl_fill(m->ocl, m->col_max, 0, n, -1.0f);
-    ocl_fill_u32(m->ocl, m->col_arg, 0, n, 0xffffffffu);
+    /* The features arrive token-major in t_tok and t_h1 (transformer). The
+     * tile passes start the column statistics from their first block. */
+    if (!tiles) {
+        ocl_fill(m->ocl, m->col_m, 0, n, -INFINITY);
+        ocl_fill(m->ocl, m->col_s, 0, n, 0.0f);
+        ocl_fill(m->ocl, m->col_max, 0, n, -1.0f);
+        ocl_fill_u32(m->ocl, m->col_arg, 0, n, 0xffffffffu);
+    }
     for (int pass = 0; pass < 2; pass++)
         for (int r0 = 0; r0 < n; r0 += R) {
             const int rows = n - r0 < R ? n - r0 : R;

@@ -13,9 +13,12 @@
  * of M (nb, C, n), gain g and bias b (C each), epsilon eps: the
  * LayerNorm of the MLP output and the residual add that end an
  * aggregated-attention block (eloftr.c:445-448 of i.coregistration.opencl:
- * ops_layernorm on token-major rows, transpose back, ops_axpby). */
+ * ops_layernorm on token-major rows, transpose back, ops_axpby). T (or
+ * NULL; C % 64 == 0, 16-byte aligned) also receives the result
+ * token-major, (nb, n, C): the transpose that precedes the coarse
+ * matching (eloftr.c:471-480). */
 void eloftr_ln_residual(struct ops *o, cl_mem M, int nb, int C, int n,
-                        cl_mem g, cl_mem b, float eps, cl_mem X);
+                        cl_mem g, cl_mem b, float eps, cl_mem X, cl_mem T);
 
 /* Tokens of an aggregated-attention block for nb images of C = 256
  * channels (h x w maps, multiples of 4; image k of X and Y C h w floats

@@ -155,10 +155,11 @@ __global__ void __launch_bounds__(256)
  * threads takes chunks g, g + MERGE_G, ... in two passes (the maximum of
  * the chunk maxima, then the rescaled sums: independent loads, no serial
  * chain), the groups are combined in order, and the result goes into the
- * running (cm, cs) as eloftr_col_lse does (eloftr_kernels.cl:62-65). */
+ * running (cm, cs) as eloftr_col_lse does (eloftr_kernels.cl:62-65);
+ * first: there is no running state yet (the first row block). */
 __global__ void __launch_bounds__(256)
     col_lse_merge_kernel(const float2 *__restrict__ part, int nchunks, int N,
-                         float *__restrict__ cm, float *__restrict__ cs)
+                         float *__restrict__ cm, float *__restrict__ cs, int first)
 {
     __shared__ float2 red[MERGE_G][MERGE_C];
     const int cl = threadIdx.x % MERGE_C, g = threadIdx.x / MERGE_C;
@@ -186,6 +187,11 @@ __global__ void __launch_bounds__(256)
     if (m != -INFINITY)
         for (int q = 0; q < MERGE_G; q++)
             s += red[q][cl].x == -INFINITY ? 0.0f : red[q][cl].y * expf(red[q][cl].x - m);
+    if (first) {
+        cm[j] = m;
+        cs[j] = m == -INFINITY ? 0.0f : s;
+        return;
+    }
     mo = cm[j];
     mn = fmaxf(mo, m);
     if (mn == -INFINITY)
@@ -227,11 +233,11 @@ __global__ void __launch_bounds__(256)
  * with a strict comparison, and the groups' results are merged with ties
  * to the lowest row. Rows of the running state precede the block's, so
  * the first row reaching the maximum wins, as in the sequential scan of
- * eloftr_conf_col. */
+ * eloftr_conf_col. first: no running state yet, start from (-1, -1). */
 __global__ void __launch_bounds__(256)
     conf_col_merge_kernel(const float *__restrict__ pv,
                           const int *__restrict__ pi, int nchunks, int N,
-                          float *__restrict__ cmax, int *__restrict__ carg)
+                          float *__restrict__ cmax, int *__restrict__ carg, int first)
 {
     __shared__ float rv[MERGE_G][MERGE_C];
     __shared__ int ri[MERGE_G][MERGE_C];
@@ -254,8 +260,8 @@ __global__ void __launch_bounds__(256)
     __syncthreads();
     if (g != 0 || j >= N)
         return;
-    best = cmax[j];
-    bi = carg[j];
+    best = first ? -1.0f : cmax[j];
+    bi = first ? -1 : carg[j];
     for (int q = 0; q < MERGE_G; q++) {
         const float v = rv[q][cl];
 
@@ -314,7 +320,7 @@ extern "C" void eloftr_col_lse(struct ops *o, cl_mem S, int R, int N,
                        (float2 *)part->ptr);
     hipLaunchKernelGGL(col_lse_merge_kernel, dim3((N + MERGE_C - 1) / MERGE_C), dim3(256),
                        0, stream_of(o->ocl), (const float2 *)part->ptr, nch, N,
-                       fptr(cm), fptr(cs));
+                       fptr(cm), fptr(cs), 0);
     launch_check(op);
     ICOREG_API_END
 }
@@ -381,7 +387,7 @@ extern "C" void eloftr_conf_col(struct ops *o, cl_mem S, int R, int N, int r0,
     hipLaunchKernelGGL(conf_col_merge_kernel, dim3((N + MERGE_C - 1) / MERGE_C), dim3(256),
                        0, stream_of(o->ocl), (const float *)(base + lc_bytes),
                        (const int *)(base + lc_bytes + pv_bytes), nch, N,
-                       fptr(cmax), (int *)carg->ptr);
+                       fptr(cmax), (int *)carg->ptr, 0);
     launch_check(op);
     ICOREG_API_END
 }
@@ -619,7 +625,7 @@ void eloftr_lse_tiles(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse,
                        stream_of(o->ocl), (const float2 *)sc->ptr, R, nbands, r0, fptr(lse));
     hipLaunchKernelGGL(col_lse_merge_kernel, dim3((N + MERGE_C - 1) / MERGE_C), dim3(256), 0,
                        stream_of(o->ocl), (const float2 *)((char *)sc->ptr + rb), nch, N,
-                       fptr(cm), fptr(cs));
+                       fptr(cm), fptr(cs), r0 == 0);
     launch_check(op);
 }
 
@@ -663,7 +669,7 @@ void eloftr_conf_tiles(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse
     hipLaunchKernelGGL(conf_col_merge_kernel, dim3((N + MERGE_C - 1) / MERGE_C), dim3(256), 0,
                        stream_of(o->ocl), (const float *)(base + lcb + 2 * rpb),
                        (const int *)(base + lcb + 2 * rpb + cpb), nch, N, fptr(cmax),
-                       (int *)carg->ptr);
+                       (int *)carg->ptr, r0 == 0);
     launch_check(op);
 }
 
@@ -916,13 +922,15 @@ extern "C" void eloftr_fine_half(struct ops *o, cl_mem f0, cl_mem f1, int H, int
  * its LNR_NW waves split the C <= 256 channels, each lane holding its
  * token's share in registers, so M is read once; the per-token sums are
  * combined across the waves in LDS. Reads of one channel row are 256
- * contiguous bytes per wave. */
+ * contiguous bytes per wave. T (or NULL) also receives the result
+ * token-major, T[b][j][c]. */
 #define LNR_MAXC 256
 #define LNR_NW 16
 __global__ void __launch_bounds__(64 * LNR_NW)
     chan_ln_add_kernel(const float *__restrict__ Mm, float *__restrict__ X,
                        const float *__restrict__ g,
-                       const float *__restrict__ bt, int C, int n, float eps)
+                       const float *__restrict__ bt, int C, int n, float eps,
+                       float *__restrict__ T)
 {
     constexpr int CPW = LNR_MAXC / LNR_NW;
     __shared__ float part[2][LNR_NW][64];
@@ -975,13 +983,23 @@ __global__ void __launch_bounds__(64 * LNR_NW)
             float u = (v[k] - mean) * r;
 
             u = u * g[c] + bt[c];
-            X[base + (long long)c * n + j] = xv[k] + u;
+            xv[k] += u;
+            X[base + (long long)c * n + j] = xv[k];
         }
+    }
+    if (T) {
+        /* C % 64 == 0: every wave's channel share is whole float4s. */
+        float4 *t = (float4 *)(T + base + (long long)j * C + c0);
+
+#pragma unroll
+        for (int q = 0; q < CPW / 4; q++)
+            if (4 * q < nc)
+                t[q] = make_float4(xv[4 * q], xv[4 * q + 1], xv[4 * q + 2], xv[4 * q + 3]);
     }
 }
 
 void eloftr_ln_residual(struct ops *o, cl_mem M, int nb, int C, int n,
-                        cl_mem g, cl_mem b, float eps, cl_mem X)
+                        cl_mem g, cl_mem b, float eps, cl_mem X, cl_mem T)
 {
     const char *op = "eloftr_ln_residual";
 
@@ -992,10 +1010,15 @@ void eloftr_ln_residual(struct ops *o, cl_mem M, int nb, int C, int n,
     need_floats(X, 0, (long long)nb * C * n, op, "X");
     need_floats(g, 0, C, op, "g");
     need_floats(b, 0, C, op, "b");
+    if (T) {
+        need_floats(T, 0, (long long)nb * C * n, op, "T");
+        if (C % 64 || ((uintptr_t)T->ptr & 15))
+            icoreg_fatal("%s: token-major copy needs C %% 64 == 0 and 16-byte alignment", op);
+    }
     prof_scope ps(o->ocl, "ln_residual");
     hipLaunchKernelGGL(chan_ln_add_kernel, dim3((n + 63) / 64, nb),
                        dim3(64 * LNR_NW), 0, stream_of(o->ocl), cfptr(M), fptr(X),
-                       cfptr(g), cfptr(b), C, n, eps);
+                       cfptr(g), cfptr(b), C, n, eps, T ? fptr(T) : nullptr);
     launch_check(op);
 }
 
