@@ -273,6 +273,59 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
     }
 }
 
+/* One input channel (ELoFTR's grey first layer): one thread per output
+ * pixel holds its KS x KS taps in registers and runs over the K output
+ * channels, the filters and bias staged in LDS (K KS^2 <= C1_MAXW, K <=
+ * C1_MAXK); each channel's store is one contiguous run per wave. No MFMA:
+ * K C KS^2 products per pixel are few, and the layer is bound by its
+ * output writes. */
+#define C1_MAXW 4096
+#define C1_MAXK 256
+template <int KS, int ST>
+__global__ void __launch_bounds__(256) conv_c1_kernel(const conv_args a)
+{
+    __shared__ float ws[C1_MAXW], bs[C1_MAXK];
+    const int HWo = a.Ho * a.Wo;
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    const float *in = a.in + (long long)blockIdx.z * a.in_stride;
+    float *out = a.out + (long long)blockIdx.z * a.out_stride;
+    float t[KS * KS];
+
+    for (int i = threadIdx.x; i < a.K * KS * KS; i += 256)
+        ws[i] = a.w[i];
+    for (int i = threadIdx.x; i < a.K; i += 256)
+        bs[i] = a.bias ? a.bias[i] : 0.0f;
+    {
+        const int pc = min(p, HWo - 1);
+        const int oy = pc / a.Wo, ox = pc - oy * a.Wo;
+        const int iy0 = oy * ST - a.pad, ix0 = ox * ST - a.pad;
+
+#pragma unroll
+        for (int i = 0; i < KS; i++)
+#pragma unroll
+            for (int j = 0; j < KS; j++) {
+                const int iy = iy0 + i, ix = ix0 + j;
+
+                t[i * KS + j] = iy >= 0 && iy < a.H && ix >= 0 && ix < a.W
+                                    ? in[(long long)iy * a.W + ix]
+                                    : 0.0f;
+            }
+    }
+    __syncthreads();
+    if (p >= HWo)
+        return;
+#pragma unroll 8
+    for (int k = 0; k < a.K; k++) {
+        const float *wk = ws + k * KS * KS;
+        float v = 0.0f;
+
+#pragma unroll
+        for (int q = 0; q < KS * KS; q++)
+            v = fmaf(wk[q], t[q], v);
+        out[(long long)k * HWo + p] = icoreg_act(v + bs[k], a.act, a.slope);
+    }
+}
+
 bool conv_direct_supported(int kh, int kw, int sy, int sx, int dy, int dx,
                            int groups)
 {
@@ -343,6 +396,19 @@ static void launch_ks(const conv_args &a, int nb, int cus, hipStream_t s)
 void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,
                         int cus, hipStream_t s)
 {
+    if (a.C == 1 && !a.mean && a.K <= C1_MAXK && a.K * ks * ks <= C1_MAXW) {
+        const dim3 grid((unsigned)(((long long)a.Ho * a.Wo + 255) / 256), 1, nb);
+
+        if (ks == 3 && stride == 1)
+            hipLaunchKernelGGL((conv_c1_kernel<3, 1>), grid, dim3(256), 0, s, a);
+        else if (ks == 3)
+            hipLaunchKernelGGL((conv_c1_kernel<3, 2>), grid, dim3(256), 0, s, a);
+        else if (stride == 1)
+            hipLaunchKernelGGL((conv_c1_kernel<5, 1>), grid, dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL((conv_c1_kernel<5, 2>), grid, dim3(256), 0, s, a);
+        return;
+    }
     if (ks == 3 && stride == 1)
         launch_ks<3, 1>(a, nb, cus, s);
     else if (ks == 3)

@@ -134,6 +134,9 @@ CONV_SHAPES = [
     # pieces, the partial channel block among the split ones).
     (1, 64, 80, 80, 192, 3, 1, 1, 0, 2),
     (2, 48, 30, 90, 200, 3, 1, 1, 0, 1),
+    # One input channel (the per-pixel kernel): 5 x 5 and 3 x 3, stride 1.
+    (1, 1, 37, 45, 20, 5, 1, 2, 0, 1),
+    (2, 1, 30, 31, 16, 3, 1, 1, 0, 0),
 ]
 
 
