@@ -52,6 +52,11 @@ struct gemm_args {
      * table row r % rnpos of rope for output row r). */
     const float2 *rope;
     int rcols, rd, rnpos;
+    /* Main kernel, one batch: tiles nfull.. are cut into split pieces
+     * over K whose partial sums go to part (4096 floats a piece) and are
+     * added by a second kernel (gemm_split_floats; split <= 1: none). */
+    int nfull, split;
+    float *part;
 };
 
 /* True if the kernel takes these leading dimensions: each at least its
@@ -62,6 +67,10 @@ bool gemm_shape_ok(const gemm_args &g, int bmode);
  * 16-byte vector loads allowed for A / B (every row start aligned). */
 void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
                  int cus, hipStream_t s);
+
+/* Floats of part that gemm_launch's main kernel needs for g (0: it
+ * runs without pieces). */
+size_t gemm_split_floats(const gemm_args &g, int bmode, int nb, bool va, bool vb, int cus);
 
 /* True if gemm_launch would run g on the small-product kernel. */
 bool gemm_smallk_ok(const gemm_args &g, int bmode, int nb, bool va, bool vb, int cus);

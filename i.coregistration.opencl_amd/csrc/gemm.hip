@@ -30,6 +30,7 @@
  *  - output tiles are assigned so that each of the 8 XCDs (one L2 each)
  *    works on a contiguous band of tiles, which share A rows in its L2. */
 
+#include <algorithm>
 #include <hip/hip_runtime.h>
 
 #include "act.h"
@@ -90,6 +91,9 @@ __device__ __forceinline__ float4 mask4(float4 v, int lo, int hi)
     v.w = lo + 3 < hi ? v.w : 0.0f;
     return v;
 }
+
+/* Most pieces a cut GEMM tile is split into. */
+#define GEMM_MAX_SPLIT 8
 
 /* Output tile of linear block id L among T tiles: blocks are dealt to
  * the 8 XCDs round-robin (L % 8), so give XCD x the x-th contiguous
@@ -169,7 +173,20 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
     const int wm = wave / WGN, wn = wave % WGN;
     const int tiles_n = (g.N + BN - 1) / BN;
     const int tiles = tiles_n * ((g.M + BM - 1) / BM);
-    const int tile = xcd_tile(blockIdx.x, tiles);
+    const int nk = (g.K + BK - 1) / BK;
+    /* Unit (tile) L; units from nfull on are cut into pieces over the
+     * k slices. */
+    int L = blockIdx.x, piece = -1, kt0 = 0, kt1 = nk;
+
+    if (g.split > 1 && L >= g.nfull) {
+        const int p = L - g.nfull;
+
+        piece = p % g.split;
+        L = g.nfull + p / g.split;
+        kt0 = piece * nk / g.split;
+        kt1 = (piece + 1) * nk / g.split;
+    }
+    const int tile = xcd_tile(L, tiles);
     const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
     const long long bt = blockIdx.y, b0 = bt / g.nb1, b1 = bt % g.nb1;
     const float *A = g.A + b0 * g.sa0 + b1 * g.sa1;
@@ -354,17 +371,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
         }
     };
 
-    const int nk = (K + BK - 1) / BK;
-
-    if (nk > 0) {
-        fetch(0);
+    if (kt0 < kt1) {
+        fetch(kt0 * BK);
         stash(0);
     }
     __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
+    for (int kt = kt0; kt < kt1; kt++) {
+        const int cur = (kt - kt0) & 1;
 
-        if (kt + 1 < nk)
+        if (kt + 1 < kt1)
             fetch((kt + 1) * BK);
         {
             const float *as = As[cur] + wm * (BM / WGM) + (lane & 31);
@@ -401,7 +416,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
                     for (int j = 0; j < TN; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
                             a[ks % NB][i], b[ks % NB][j], acc[i][j], 0, 0, 0);
-                if (ks == NS - 2 && kt + 1 < nk)
+                if (ks == NS - 2 && kt + 1 < kt1)
                     stash(cur ^ 1);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -409,8 +424,66 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
         __syncthreads();
     }
 
+    if (piece >= 0) {
+        /* Raw partial sums of the piece, [row][col] of the BM x BN tile. */
+        float *pp = g.part + ((long long)(L - g.nfull) * g.split + piece) * (BM * BN);
+
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int row = wm * (BM / WGM) + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 +
+                                    (r & 3);
+                    const int col = wn * (BN / WGN) + j * 32 + (lane & 31);
+
+                    pp[row * BN + col] = acc[i][j][r];
+                }
+        return;
+    }
     gemm_epilogue<TM, TN>(g, acc, b0, b1, m0 + wm * (BM / WGM), n0 + wn * (BN / WGN), lane);
 }
+
+/* The cut tiles of gemm_mfma<64, 64, ...> (one batch): one thread per
+ * output adds the pieces' partial sums in piece order (all loads issued
+ * first), then alpha, bias, activation and residual as gemm_epilogue. */
+__global__ void __launch_bounds__(256) gemm_pieces_kernel(const gemm_args g, int tail)
+{
+    constexpr int BM = 64, BN = 64;
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int t = (int)(e / (BM * BN)), w = (int)(e % (BM * BN));
+
+    if (t >= tail)
+        return;
+    const int tiles_n = (g.N + BN - 1) / BN;
+    const int tiles = tiles_n * ((g.M + BM - 1) / BM);
+    const int tile = xcd_tile(g.nfull + t, tiles);
+    const int row = (tile / tiles_n) * BM + w / BN, col = (tile % tiles_n) * BN + w % BN;
+    const float *q = g.part + (long long)t * g.split * (BM * BN) + w;
+    float p[GEMM_MAX_SPLIT], v;
+
+    if (row >= g.M || col >= g.N)
+        return;
+#pragma unroll
+    for (int pc = 0; pc < GEMM_MAX_SPLIT; pc++)
+        if (pc < g.split)
+            p[pc] = q[(long long)pc * (BM * BN)];
+    v = p[0];
+#pragma unroll
+    for (int pc = 1; pc < GEMM_MAX_SPLIT; pc++)
+        if (pc < g.split)
+            v += p[pc];
+    v *= g.alpha;
+    if (g.bias)
+        v += g.bias[g.biasrow ? row : col];
+    v = icoreg_act(v, g.act, g.slope);
+    if (g.R)
+        v += g.R[(long long)row * g.ldc + col];
+    g.C[(long long)row * g.ldc + col] = v;
+}
+
+
 
 /* Small products (few output tiles, K <= 256): one 32 x 32 output tile per
  * block of 8 waves. Both operand panels (32 x K of A, K x 32 of B) are
@@ -755,10 +828,10 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_dma(const gemm_args g)
 
 template <int BM, int BN, int BK, int WGM, int WGN, int MODE>
 static void launch_mode(const gemm_args &g, int nb, bool va, bool vb,
-                        hipStream_t s)
+                        hipStream_t s, int blocks)
 {
     const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-    dim3 grid(tiles, nb), block(64 * WGM * WGN);
+    dim3 grid(blocks > 0 ? blocks : tiles, nb), block(64 * WGM * WGN);
 
 #define GEMM_LAUNCH(VA_, VB_)                                                  \
     hipLaunchKernelGGL((gemm_mfma<BM, BN, BK, MODE, VA_, VB_, WGM, WGN>),      \
@@ -782,17 +855,17 @@ static void launch_mode(const gemm_args &g, int nb, bool va, bool vb,
 
 template <int BM, int BN, int BK, int WGM, int WGN>
 static void launch_cfg(const gemm_args &g, int bmode, int nb, bool va,
-                       bool vb, hipStream_t s)
+                       bool vb, hipStream_t s, int blocks)
 {
     switch (bmode) {
     case GEMM_B_KN:
-        launch_mode<BM, BN, BK, WGM, WGN, GEMM_B_KN>(g, nb, va, vb, s);
+        launch_mode<BM, BN, BK, WGM, WGN, GEMM_B_KN>(g, nb, va, vb, s, blocks);
         break;
     case GEMM_B_NK:
-        launch_mode<BM, BN, BK, WGM, WGN, GEMM_B_NK>(g, nb, va, vb, s);
+        launch_mode<BM, BN, BK, WGM, WGN, GEMM_B_NK>(g, nb, va, vb, s, blocks);
         break;
     default:
-        launch_mode<BM, BN, BK, WGM, WGN, GEMM_B_CONV>(g, nb, va, vb, s);
+        launch_mode<BM, BN, BK, WGM, WGN, GEMM_B_CONV>(g, nb, va, vb, s, blocks);
         break;
     }
 }
@@ -832,6 +905,61 @@ void gemm_launch_smallk2(const gemm_args &g1, const gemm_args &g2, hipStream_t s
     hipLaunchKernelGGL(gemm_smallk<GEMM_B_NK>, dim3(n1 + n2, 1), dim3(512), 0, s, g1, g2, n1);
 }
 
+/* The LDS-DMA kernel: in the ELoFTR and RoMa pipelines it is faster only
+ * for products with few output rows (M <= 256, B given K x N, K >= 256:
+ * the MLP's second layer); on larger grids the main kernel's smaller LDS
+ * footprint (more blocks per CU) wins, and on K <= 128 its shorter
+ * slices do. It addresses whole operands with 31-bit byte offsets. va,
+ * vb as adjusted by gemm_launch. */
+static bool gemm_dma_ok(const gemm_args &g, int bmode, bool va, bool vb)
+{
+    const long long lim = 1LL << 31;
+
+    if (!(bmode == GEMM_B_KN && va && vb && g.M <= 256 && g.K >= 256 && g.ksplit == 0))
+        return false;
+    return ((long long)(g.M - 1) * g.lda + g.K) * 4 < lim &&
+           ((long long)(g.K - 1) * g.ldb + g.N) * 4 < lim;
+}
+
+/* Main-kernel work split over cus CUs: with under 4 tiles per CU, the
+ * tiles left over after an equal whole number per CU (at most half the
+ * CUs' worth) are cut over K so that each CU gets about one piece of at
+ * least 4 k slices; one batch, plain epilogues only. */
+static bool gemm_plan(const gemm_args &g, int bmode, int nb, int cus, int &nfull, int &split)
+{
+    const int tiles = ((g.M + 63) / 64) * ((g.N + 63) / 64);
+    const int nk = (g.K + 15) / 16;
+    int rem;
+
+    nfull = tiles;
+    split = 1;
+    if (nb != 1 || g.nb1 != 1 || bmode == GEMM_B_CONV || g.rup || g.ksplit || cus < 1 ||
+        tiles >= 4 * cus)
+        return false;
+    rem = tiles % cus;
+    if (rem == 0 || 2 * rem > cus)
+        return false;
+    split = std::min(std::min(cus / rem, nk / 4), GEMM_MAX_SPLIT);
+    if (split < 2) {
+        split = 1;
+        return false;
+    }
+    nfull = tiles - rem;
+    return true;
+}
+
+size_t gemm_split_floats(const gemm_args &g, int bmode, int nb, bool va, bool vb, int cus)
+{
+    int nfull, split;
+
+    va = va && g.K % 4 == 0;
+    vb = vb && (bmode == GEMM_B_KN ? g.N % 4 == 0 : g.K % 4 == 0);
+    if (gemm_smallk_ok(g, bmode, nb, va, vb, cus) || gemm_dma_ok(g, bmode, va, vb) ||
+        !gemm_plan(g, bmode, nb, cus, nfull, split))
+        return 0;
+    return (size_t)(((g.M + 63) / 64) * ((g.N + 63) / 64) - nfull) * split * 4096;
+}
+
 void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
                  int cus, hipStream_t s)
 {
@@ -863,23 +991,31 @@ void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
      * kernel's smaller LDS footprint (more blocks per CU) wins, and on
      * K <= 128 its shorter slices do. It addresses whole operands with
      * 31-bit byte offsets. */
-    if (bmode == GEMM_B_KN && va && vb && g.M <= 256 && g.K >= 256 && g.ksplit == 0) {
-        const long long lim = 1LL << 31;
-        const long long ab = ((long long)(g.M - 1) * g.lda + g.K) * 4;
-        const long long bb = bmode == GEMM_B_NK
-                                 ? ((long long)(g.N - 1) * g.ldb + g.K) * 4
-                                 : ((long long)(g.K - 1) * g.ldb + g.N) * 4;
+    if (gemm_dma_ok(g, bmode, va, vb)) {
+        const int tiles = ((g.M + 63) / 64) * ((g.N + 63) / 64);
+        const dim3 grid(tiles, nb);
 
-        if (ab < lim && bb < lim) {
+        if (bmode == GEMM_B_NK)
+            hipLaunchKernelGGL((gemm_dma<64, 64, 2, 2, GEMM_B_NK>), grid, dim3(256), 0, s, g);
+        else
+            hipLaunchKernelGGL((gemm_dma<64, 64, 2, 2, GEMM_B_KN>), grid, dim3(256), 0, s, g);
+        return;
+    }
+    {
+        int nfull, split;
+
+        if (g.part && gemm_plan(g, bmode, nb, cus, nfull, split)) {
+            gemm_args gs = g;
             const int tiles = ((g.M + 63) / 64) * ((g.N + 63) / 64);
-            const dim3 grid(tiles, nb);
+            const long long tail = tiles - nfull;
 
-            if (bmode == GEMM_B_NK)
-                hipLaunchKernelGGL((gemm_dma<64, 64, 2, 2, GEMM_B_NK>), grid, dim3(256), 0, s, g);
-            else
-                hipLaunchKernelGGL((gemm_dma<64, 64, 2, 2, GEMM_B_KN>), grid, dim3(256), 0, s, g);
+            gs.nfull = nfull;
+            gs.split = split;
+            launch_cfg<64, 64, 16, 2, 2>(gs, bmode, nb, va, vb, s, nfull + (int)tail * split);
+            hipLaunchKernelGGL(gemm_pieces_kernel, dim3((unsigned)((tail * 4096 + 255) / 256)),
+                               dim3(256), 0, s, gs, (int)tail);
             return;
         }
     }
-    launch_cfg<64, 64, 16, 2, 2>(g, bmode, nb, va, vb, s);
+    launch_cfg<64, 64, 16, 2, 2>(g, bmode, nb, va, vb, s, 0);
 }

@@ -184,12 +184,16 @@ extern "C" void ops_gemm(struct ops *o, int M, int N, int K, struct opnd A,
     if (M == 0 || N == 0)
         return;
     {
-        const gemm_args g = gemm_make(op, M, N, K, A, B, transb, C, nb, nb1, bias, biasrow,
-                                      R, roff, alpha, act, slope);
-        prof_scope ps(o->ocl, "gemm");
+        const int bmode = transb ? GEMM_B_NK : GEMM_B_KN;
+        gemm_args g = gemm_make(op, M, N, K, A, B, transb, C, nb, nb1, bias, biasrow, R, roff,
+                                alpha, act, slope);
+        /* Partial sums of cut tiles, when the grid leaves CUs uneven. */
+        const size_t pf = gemm_split_floats(g, bmode, nb, vec_ok(A), vec_ok(B), o->ocl->cu_count);
 
-        gemm_launch(g, transb ? GEMM_B_NK : GEMM_B_KN, nb, vec_ok(A),
-                    vec_ok(B), o->ocl->cu_count, stream_of(o->ocl));
+        if (pf)
+            g.part = fptr(scratch_get(o, pf * sizeof(float)));
+        prof_scope ps(o->ocl, "gemm");
+        gemm_launch(g, bmode, nb, vec_ok(A), vec_ok(B), o->ocl->cu_count, stream_of(o->ocl));
         launch_check("gemm");
     }
     ICOREG_API_END

@@ -32,6 +32,12 @@ GEMM_SHAPES = [
     # layer, ragged rows and columns, K not a multiple of 32.
     (256, 1600, 512, 0, 2, 0, 1, 1),
     (200, 300, 292, 0, 1, 3, 0, 0),
+    # Main kernel with tiles cut over K on 256 CUs (one batch, under 4
+    # tiles per CU): 288 tiles (256 whole, 32 in 8 pieces) with in-place
+    # residual and bias; 64 tiles in 4 pieces each, ragged edges, K not a
+    # multiple of 16.
+    (1100, 1024, 512, 1, 1, 4, 1, 0),
+    (500, 500, 520, 1, 1, 1, 0, 1),
 ]
 
 
