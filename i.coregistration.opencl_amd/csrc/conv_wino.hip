@@ -485,7 +485,7 @@ __global__ void __launch_bounds__(256, 4)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int half = lane >> 5, col = lane & 31;
     const int tr = col >> 3, tc = col & 7;
-    const int C = a.C, H = a.H, W = a.W, K = a.K;
+    const int C = a.C, H = a.H, W = a.W;
     const int nk = (C + WR_CC - 1) / WR_CC;
     /* Unit u = (image bz, tile block by, channel block bx), channel blocks
      * fastest (they share the input tiles in L2); units from nfull on are

@@ -34,11 +34,6 @@ struct gemm_args {
      * input normalisation and PReLU gate per input channel. */
     int cc, ch, cw, kh, kw, sy, sx, py, px, dy, dx, wo;
     const float *mean, *rstd, *gate;
-    /* GEMM_B_KN with ksplit > 0 (a multiple of 16): rows k >= ksplit of
-     * B are rows k - ksplit of B2 (same ldb and batch strides), i.e. B is
-     * the concatenation [B; B2] without being materialised. */
-    const float *B2;
-    int ksplit;
     /* rup = 2 or 4: R is not in C's layout but (nb0 batches rs0 floats
      * apart) M rows of rh x rw planes, and C's column n = y * rwo + x
      * receives R's rup x bilinear resize at (y, x) (ops_resize with scale
@@ -89,13 +84,6 @@ void gemm_launch_smallk2(const gemm_args &g1, const gemm_args &g2, hipStream_t s
 void ops_linear2_rope(struct ops *o, int rows, int in, cl_mem X1, cl_mem W1, cl_mem Y1, int n1,
                       int rc1, cl_mem X2, cl_mem W2, cl_mem Y2, int n2, int rc2, cl_mem cs,
                       int rd, int npos);
-
-/* ops_gemm with B (K x N, not transposed) given as two row blocks: rows
- * 0..ksplit-1 in B1, the rest in B2 (same ld and batch stride s0; ksplit a
- * multiple of 16); nb batches over s0, no bias or residual. */
-void ops_gemm_cat(struct ops *o, int M, int N, int K, struct opnd A,
-                  struct opnd B1, struct opnd B2, int ksplit, struct opnd C,
-                  int nb, int act, float slope);
 
 /* C (M x N, nb batches C.s0 apart) = act(A (M x K) B (K x N, not
  * transposed)) + the up x bilinear resize (ops_resize with scale up) of R

@@ -191,7 +191,6 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
     const long long bt = blockIdx.y, b0 = bt / g.nb1, b1 = bt % g.nb1;
     const float *A = g.A + b0 * g.sa0 + b1 * g.sa1;
     const float *B = g.B + b0 * g.sb0 + b1 * g.sb1;
-    const float *B2 = g.B2 ? g.B2 + b0 * g.sb0 + b1 * g.sb1 : nullptr;
     const int M = g.M, N = g.N, K = g.K;
     const long long lda = g.lda, ldb = g.ldb;
     /* Rows of A and columns of B inside the matrix for this tile. */
@@ -264,13 +263,8 @@ __global__ void __launch_bounds__(64 * WGM * WGN) gemm_mfma(const gemm_args g)
                 rb[e] = gemm_load4<VB>(wb, boff[e]);
         }
         else if (MODE == GEMM_B_KN) {
-            /* Rows of a slice come from B or, past ksplit, from B2 (BK
-             * divides ksplit, so a slice never straddles the two). */
-            const bool second = g.ksplit > 0 && k0 >= g.ksplit;
-            const float *Bk = second ? B2 + (long long)(k0 - g.ksplit) * ldb
-                                     : B + (long long)k0 * ldb;
-            const int kend = g.ksplit > 0 && !second ? g.ksplit : K;
-            const int kv = min(BK, kend - k0);
+            const float *Bk = B + (long long)k0 * ldb;
+            const int kv = min(BK, K - k0);
             const __amdgpu_buffer_rsrc_t wb =
                 gemm_rsrc(Bk + n0, ((kv - 1) * ldb + cols_b) * 4);
 
@@ -494,7 +488,7 @@ __global__ void __launch_bounds__(256) gemm_pieces_kernel(const gemm_args g, int
  * here every block has one load round trip and K / 16 MFMA steps. */
 #define GEMM_SK_MAXK 256
 
-template <int MODE>
+template <int MODE, bool DIRECT>
 __global__ void __launch_bounds__(512)
     gemm_smallk(const gemm_args g1, const gemm_args g2, int nblk1)
 {
@@ -502,9 +496,12 @@ __global__ void __launch_bounds__(512)
     /* Row-major panels as loaded (no transposing stores): A [m][k] and B
      * given N x K as [n][k], K + 2 floats a row, so the 32 lanes of an
      * MFMA operand (32 rows, one k) fall in 32 different even banks and
-     * lanes 32-63 (k + 1) in the odd ones; B given K x N as [k][n]. */
+     * lanes 32-63 (k + 1) in the odd ones; B given K x N as [k][n].
+     * DIRECT (K % 64 == 0): no panels; LDS holds only the 8 partial
+     * tiles. */
     constexpr int P = GEMM_SK_MAXK + 2;
-    __shared__ __align__(16) float As[T * P], Bs[T * P];
+    __shared__ __align__(16) float lds[DIRECT ? 8 * T * T : 2 * T * P];
+    float *const As = lds, *const Bs = lds + (DIRECT ? 0 : T * P);
 
     /* Blocks nblk1.. run the second product. */
     const bool second = (int)blockIdx.x >= nblk1;
@@ -521,74 +518,128 @@ __global__ void __launch_bounds__(512)
     const long long lda = g.lda, ldb = g.ldb;
     floatx16 acc;
 
-    /* Panels: 16-byte loads through windows ending at the last row inside
-     * the matrix (rows past it read 0), all issued before the first LDS
-     * store. At most 32 x 256 / 4 / 512 = 4 per thread and operand. */
-    {
-        constexpr int NL = GEMM_SK_MAXK * T / 4 / NTH;
+    for (int r = 0; r < 16; r++)
+        acc[r] = 0.0f;
+    if constexpr (DIRECT) {
+        /* Wave w takes k in [w kw, (w + 1) kw), kw = K / 8, lane half h
+         * the half [w kw + h kw / 2, + kw / 2): MFMA step s pairs k =
+         * w kw + s (lanes 0-31) with w kw + kw / 2 + s (lanes 32-63) for
+         * both operands. Each lane reads its row's kw / 2 floats straight
+         * into registers through windows ending at the last row inside
+         * the matrix (rows past it read 0). */
+        constexpr int KH = GEMM_SK_MAXK / 16; /* most k per lane */
+        const int kh = K / 16, c = lane & 31;
+        const int kb = wave * (K / 8) + (lane >> 5) * kh;
         const __amdgpu_buffer_rsrc_t wa =
             gemm_rsrc(A + m0 * lda, ((rows_a - 1) * lda + K) * 4);
         const __amdgpu_buffer_rsrc_t wb =
             MODE == GEMM_B_NK ? gemm_rsrc(B + n0 * ldb, ((cols_b - 1) * ldb + K) * 4)
                               : gemm_rsrc(B + n0, ((K - 1) * ldb + cols_b) * 4);
-        const int nq4 = T * KQ; /* float4 groups per panel */
-        float4 va[NL], vb[NL];
+        float av[KH], bv[KH];
 
 #pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const int q = tid + i * NTH, row = q / KQ, kq = (q % KQ) * 4;
+        for (int q = 0; q < KH / 4; q++)
+            if (4 * q < kh) {
+                const float4 t = gemm_load4<true>(wa, (unsigned)((c * lda + kb + 4 * q) * 4));
 
-            va[i] = q < nq4 ? gemm_load4<true>(wa, (unsigned)((row * lda + kq) * 4))
-                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (MODE == GEMM_B_NK) {
-                vb[i] = q < nq4 ? gemm_load4<true>(wb, (unsigned)((row * ldb + kq) * 4))
-                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            }
-            else {
-                const int kk = q / (T / 4), nq = (q % (T / 4)) * 4;
+                av[4 * q] = t.x;
+                av[4 * q + 1] = t.y;
+                av[4 * q + 2] = t.z;
+                av[4 * q + 3] = t.w;
+                if (MODE == GEMM_B_NK) {
+                    const float4 u = gemm_load4<true>(wb, (unsigned)((c * ldb + kb + 4 * q) * 4));
 
-                /* Columns past N of rows before the window's last read
-                 * the next row. */
-                vb[i] = q < nq4 ? mask4(gemm_load4<true>(wb, (unsigned)((kk * ldb + nq) * 4)),
-                                        nq, cols_b)
-                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            }
-        }
+                    bv[4 * q] = u.x;
+                    bv[4 * q + 1] = u.y;
+                    bv[4 * q + 2] = u.z;
+                    bv[4 * q + 3] = u.w;
+                }
+                else {
+                    /* Columns past N of rows before the window's last
+                     * read the next row: zeroed. */
 #pragma unroll
-        for (int i = 0; i < NL; i++) {
-            const int q = tid + i * NTH, row = q / KQ, kq = (q % KQ) * 4;
+                    for (int e = 0; e < 4; e++) {
+                        const float v = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(
+                                       wb, (int)(((kb + 4 * q + e) * ldb + c) * 4), 0, 0));
 
-            if (q >= nq4)
-                continue;
-            *(float2 *)&As[row * pk + kq] = make_float2(va[i].x, va[i].y);
-            *(float2 *)&As[row * pk + kq + 2] = make_float2(va[i].z, va[i].w);
-            if (MODE == GEMM_B_NK) {
-                *(float2 *)&Bs[row * pk + kq] = make_float2(vb[i].x, vb[i].y);
-                *(float2 *)&Bs[row * pk + kq + 2] = make_float2(vb[i].z, vb[i].w);
+                        bv[4 * q + e] = c < cols_b ? v : 0.0f;
+                    }
+                }
             }
-            else {
-                const int kk = q / (T / 4), nq = (q % (T / 4)) * 4;
+#pragma unroll
+        for (int q = 0; q < KH; q++)
+            if (q < kh)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[q], bv[q], acc, 0, 0, 0);
+    }
+    else {
+        /* Panels: 16-byte loads through windows ending at the last row inside
+         * the matrix (rows past it read 0), all issued before the first LDS
+         * store. At most 32 x 256 / 4 / 512 = 4 per thread and operand. */
+        {
+            constexpr int NL = GEMM_SK_MAXK * T / 4 / NTH;
+            const __amdgpu_buffer_rsrc_t wa =
+                gemm_rsrc(A + m0 * lda, ((rows_a - 1) * lda + K) * 4);
+            const __amdgpu_buffer_rsrc_t wb =
+                MODE == GEMM_B_NK ? gemm_rsrc(B + n0 * ldb, ((cols_b - 1) * ldb + K) * 4)
+                                  : gemm_rsrc(B + n0, ((K - 1) * ldb + cols_b) * 4);
+            const int nq4 = T * KQ; /* float4 groups per panel */
+            float4 va[NL], vb[NL];
 
-                *(float4 *)&Bs[kk * T + nq] = vb[i];
+#pragma unroll
+            for (int i = 0; i < NL; i++) {
+                const int q = tid + i * NTH, row = q / KQ, kq = (q % KQ) * 4;
+
+                va[i] = q < nq4 ? gemm_load4<true>(wa, (unsigned)((row * lda + kq) * 4))
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (MODE == GEMM_B_NK) {
+                    vb[i] = q < nq4 ? gemm_load4<true>(wb, (unsigned)((row * ldb + kq) * 4))
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+                else {
+                    const int kk = q / (T / 4), nq = (q % (T / 4)) * 4;
+
+                    /* Columns past N of rows before the window's last read
+                     * the next row. */
+                    vb[i] = q < nq4 ? mask4(gemm_load4<true>(wb, (unsigned)((kk * ldb + nq) * 4)),
+                                            nq, cols_b)
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NL; i++) {
+                const int q = tid + i * NTH, row = q / KQ, kq = (q % KQ) * 4;
+
+                if (q >= nq4)
+                    continue;
+                *(float2 *)&As[row * pk + kq] = make_float2(va[i].x, va[i].y);
+                *(float2 *)&As[row * pk + kq + 2] = make_float2(va[i].z, va[i].w);
+                if (MODE == GEMM_B_NK) {
+                    *(float2 *)&Bs[row * pk + kq] = make_float2(vb[i].x, vb[i].y);
+                    *(float2 *)&Bs[row * pk + kq + 2] = make_float2(vb[i].z, vb[i].w);
+                }
+                else {
+                    const int kk = q / (T / 4), nq = (q % (T / 4)) * 4;
+
+                    *(float4 *)&Bs[kk * T + nq] = vb[i];
+                }
             }
         }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    /* Wave w: k in [w K / 8, (w + 1) K / 8). */
-    for (int r = 0; r < 16; r++)
-        acc[r] = 0.0f;
-    {
-        const int kw = K / 8, kb = wave * kw, kh = lane >> 5, c = lane & 31;
+        /* Wave w: k in [w K / 8, (w + 1) K / 8). */
+        {
+            const int kw = K / 8, kb = wave * kw, kh = lane >> 5, c = lane & 31;
 
-        for (int ks = 0; ks < kw; ks += 2) {
-            const int kr = kb + ks + kh;
-            const float bvl = MODE == GEMM_B_NK ? Bs[c * pk + kr] : Bs[kr * T + c];
+            for (int ks = 0; ks < kw; ks += 2) {
+                const int kr = kb + ks + kh;
+                const float bvl = MODE == GEMM_B_NK ? Bs[c * pk + kr] : Bs[kr * T + c];
 
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[c * pk + kr], bvl, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(As[c * pk + kr], bvl, acc, 0, 0, 0);
+            }
         }
+        __syncthreads();
     }
-    __syncthreads();
     /* Partial tiles [w][row][col] over the A panel, then the sum of the 8
      * per output in the fixed order w = 0..7. */
     {
@@ -894,7 +945,7 @@ bool gemm_smallk_ok(const gemm_args &g, int bmode, int nb, bool va, bool vb, int
     va = va && g.K % 4 == 0;
     vb = vb && (bmode == GEMM_B_KN ? g.N % 4 == 0 : g.K % 4 == 0);
     return bmode != GEMM_B_CONV && va && vb && g.K <= GEMM_SK_MAXK && g.K % 16 == 0 &&
-           g.ksplit == 0 && g.rup == 0 && 2 * tiles64 <= cus;
+           g.rup == 0 && 2 * tiles64 <= cus;
 }
 
 void gemm_launch_smallk2(const gemm_args &g1, const gemm_args &g2, hipStream_t s)
@@ -902,7 +953,12 @@ void gemm_launch_smallk2(const gemm_args &g1, const gemm_args &g2, hipStream_t s
     const int n1 = ((g1.M + 31) / 32) * ((g1.N + 31) / 32);
     const int n2 = ((g2.M + 31) / 32) * ((g2.N + 31) / 32);
 
-    hipLaunchKernelGGL(gemm_smallk<GEMM_B_NK>, dim3(n1 + n2, 1), dim3(512), 0, s, g1, g2, n1);
+    if (g1.K % 64 == 0 && g2.K % 64 == 0)
+        hipLaunchKernelGGL((gemm_smallk<GEMM_B_NK, true>), dim3(n1 + n2, 1), dim3(512), 0, s, g1,
+                           g2, n1);
+    else
+        hipLaunchKernelGGL((gemm_smallk<GEMM_B_NK, false>), dim3(n1 + n2, 1), dim3(512), 0, s,
+                           g1, g2, n1);
 }
 
 /* The LDS-DMA kernel: in the ELoFTR and RoMa pipelines it is faster only
@@ -915,7 +971,7 @@ static bool gemm_dma_ok(const gemm_args &g, int bmode, bool va, bool vb)
 {
     const long long lim = 1LL << 31;
 
-    if (!(bmode == GEMM_B_KN && va && vb && g.M <= 256 && g.K >= 256 && g.ksplit == 0))
+    if (!(bmode == GEMM_B_KN && va && vb && g.M <= 256 && g.K >= 256))
         return false;
     return ((long long)(g.M - 1) * g.lda + g.K) * 4 < lim &&
            ((long long)(g.K - 1) * g.ldb + g.N) * 4 < lim;
@@ -933,7 +989,7 @@ static bool gemm_plan(const gemm_args &g, int bmode, int nb, int cus, int &nfull
 
     nfull = tiles;
     split = 1;
-    if (nb != 1 || g.nb1 != 1 || bmode == GEMM_B_CONV || g.rup || g.ksplit || cus < 1 ||
+    if (nb != 1 || g.nb1 != 1 || bmode == GEMM_B_CONV || g.rup || cus < 1 ||
         tiles >= 4 * cus)
         return false;
     rem = tiles % cus;
@@ -979,10 +1035,16 @@ void gemm_launch(const gemm_args &g, int bmode, int nb, bool va, bool vb,
         const int nblk = ((g.M + 31) / 32) * ((g.N + 31) / 32);
         const dim3 grid(nblk, nb);
 
-        if (bmode == GEMM_B_NK)
-            hipLaunchKernelGGL(gemm_smallk<GEMM_B_NK>, grid, dim3(512), 0, s, g, g, nblk);
+        const bool direct = g.K % 64 == 0;
+
+        if (bmode == GEMM_B_NK && direct)
+            hipLaunchKernelGGL((gemm_smallk<GEMM_B_NK, true>), grid, dim3(512), 0, s, g, g, nblk);
+        else if (bmode == GEMM_B_NK)
+            hipLaunchKernelGGL((gemm_smallk<GEMM_B_NK, false>), grid, dim3(512), 0, s, g, g, nblk);
+        else if (direct)
+            hipLaunchKernelGGL((gemm_smallk<GEMM_B_KN, true>), grid, dim3(512), 0, s, g, g, nblk);
         else
-            hipLaunchKernelGGL(gemm_smallk<GEMM_B_KN>, grid, dim3(512), 0, s, g, g, nblk);
+            hipLaunchKernelGGL((gemm_smallk<GEMM_B_KN, false>), grid, dim3(512), 0, s, g, g, nblk);
         return;
     }
     /* The LDS-DMA kernel: in the ELoFTR and RoMa pipelines it is faster

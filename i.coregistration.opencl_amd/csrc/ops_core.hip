@@ -242,58 +242,6 @@ void ops_linear2_rope(struct ops *o, int rows, int in, cl_mem X1, cl_mem W1, cl_
         ops_rope(o, Y2, 0, n2, rows, rc2 / rd, rd, npos, cs, 1);
 }
 
-void ops_gemm_cat(struct ops *o, int M, int N, int K, struct opnd A,
-                  struct opnd B1, struct opnd B2, int ksplit, struct opnd C,
-                  int nb, int act, float slope)
-{
-    const char *op = "ops_gemm_cat";
-    gemm_args g;
-
-    if (M < 1 || N < 1 || K < 1 || nb < 1 || nb > 65535 || ksplit < 16 ||
-        ksplit >= K || ksplit % 16)
-        icoreg_fatal("%s: invalid sizes M=%d N=%d K=%d ksplit=%d nb=%d", op, M,
-                     N, K, ksplit, nb);
-    if (B1.ld != B2.ld || B1.s0 != B2.s0)
-        icoreg_fatal("%s: B1 and B2 must share ld and batch stride", op);
-    if (act < ACT_NONE || act > ACT_GELU_TANH)
-        icoreg_fatal("%s: unknown activation %d", op, act);
-    need_matrix(A.buf, A.off, A.ld, A.s0, A.s1, M, K, nb, 1, op, "A");
-    need_matrix(B1.buf, B1.off, B1.ld, B1.s0, 0, ksplit, N, nb, 1, op, "B1");
-    need_matrix(B2.buf, B2.off, B2.ld, B2.s0, 0, K - ksplit, N, nb, 1, op,
-                "B2");
-    need_matrix(C.buf, C.off, C.ld, C.s0, C.s1, M, N, nb, 1, op, "C");
-    count32((long long)M * N, "gemm output");
-
-    memset(&g, 0, sizeof(g));
-    g.M = M;
-    g.N = N;
-    g.K = K;
-    g.A = cfptr(A.buf) + A.off;
-    g.lda = A.ld;
-    g.sa0 = A.s0;
-    g.B = cfptr(B1.buf) + B1.off;
-    g.B2 = cfptr(B2.buf) + B2.off;
-    g.ksplit = ksplit;
-    g.ldb = B1.ld;
-    g.sb0 = B1.s0;
-    g.C = fptr(C.buf) + C.off;
-    g.ldc = C.ld;
-    g.sc0 = C.s0;
-    g.nb1 = 1;
-    g.alpha = 1.0f;
-    g.act = act;
-    g.slope = slope;
-    if (!gemm_shape_ok(g, GEMM_B_KN))
-        icoreg_fatal("%s: leading dimensions not supported", op);
-    {
-        prof_scope ps(o->ocl, "gemm");
-
-        gemm_launch(g, GEMM_B_KN, nb, vec_ok(A), vec_ok(B1) && vec_ok(B2),
-                    o->ocl->cu_count, stream_of(o->ocl));
-        launch_check("gemm");
-    }
-}
-
 void ops_gemm_upres(struct ops *o, int M, int N, int K, struct opnd A,
                     struct opnd B, struct opnd C, int nb, cl_mem R,
                     long rstride, int rh, int rw, int H, int W, int up, int pre,
