@@ -406,6 +406,50 @@ __global__ void __launch_bounds__(256)
         L > 0.0f ? acc / L : 0.0f;
 }
 
+/* attn_merge_kernel with four consecutive values of a row per thread
+ * (d % 4 == 0, 16-byte aligned output rows): 16-byte loads and stores,
+ * the (max, sum) pairs read once per four values. */
+__global__ void __launch_bounds__(256)
+    attn_merge4_kernel(const float4 *__restrict__ part_o,
+                       const float2 *__restrict__ part_ml, int nsplit, int nb,
+                       int nh, int Nq, int d, int DP, float *__restrict__ O,
+                       int ldo, long long bo)
+{
+    const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int d4 = d / 4;
+    const long long total = (long long)nb * Nq * nh * d4;
+
+    if (idx >= total)
+        return;
+    const int dq = (int)(idx % d4);
+    const int h = (int)((idx / d4) % nh);
+    const long long bq = idx / ((long long)d4 * nh);
+    const int qi = (int)(bq % Nq), bi = (int)(bq / Nq);
+    const int y = bi * nh + h, ny = nb * nh;
+    float mx = -INFINITY, L = 0.0f;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+
+    for (int s = 0; s < nsplit; s++)
+        mx = fmaxf(mx, part_ml[((long long)s * ny + y) * Nq + qi].x);
+    if (mx != -INFINITY)
+        for (int s = 0; s < nsplit; s++) {
+            const long long row = ((long long)s * ny + y) * Nq + qi;
+            const float2 ml = part_ml[row];
+            const float w =
+                ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - mx);
+            const float4 p = part_o[row * (DP / 4) + dq];
+
+            L += w * ml.y;
+            acc.x += w * p.x;
+            acc.y += w * p.y;
+            acc.z += w * p.z;
+            acc.w += w * p.w;
+        }
+    *(float4 *)(O + bi * bo + (long long)qi * ldo + (long long)h * d + 4 * dq) =
+        L > 0.0f ? make_float4(acc.x / L, acc.y / L, acc.z / L, acc.w / L)
+                 : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
+
 template <int ND, bool VEC, bool MASK>
 static void launch_nd(struct ops *ops, hipStream_t st, int nb, int nh,
                       const float *Q, int ldq, long long bq, const float *K,
@@ -466,10 +510,16 @@ static void launch_nd(struct ops *ops, hipStream_t st, int nb, int nh,
                            dim3(64 * ATT_NW), 0, st, Q, ldq, K, ldk, V, ldv,
                            O, ldo, Nq, Nk, d, scale, kmask, tps, po, pml, nh,
                            bq, bk, bv, bo);
-        hipLaunchKernelGGL(attn_merge_kernel,
-                           dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                           st, po, pml, nsplit, nb, nh, Nq, d, 32 * ND, O, ldo,
-                           bo);
+        if (d % 4 == 0 && ldo % 4 == 0 && bo % 4 == 0 && ((uintptr_t)O & 15) == 0)
+            hipLaunchKernelGGL(attn_merge4_kernel,
+                               dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0,
+                               st, (const float4 *)po, pml, nsplit, nb, nh, Nq, d, 32 * ND,
+                               O, ldo, bo);
+        else
+            hipLaunchKernelGGL(attn_merge_kernel,
+                               dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                               st, po, pml, nsplit, nb, nh, Nq, d, 32 * ND, O, ldo,
+                               bo);
     }
 }
 
