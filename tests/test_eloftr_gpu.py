@@ -200,3 +200,24 @@ def test_network_640_properties(dev, ic, weights_file):
             assert np.isfinite(r["kp"]).all()
     finally:
         net.close()
+
+
+def test_network_wide_vs_oracle(dev, ic, weights, weights_file):
+    """A wide 64 x 512 pair (1/8 maps of 8 x 64, aggregated 2 x 16):
+    coarse features and scores against the oracle."""
+    print("[eloftr] network 64x512", flush=True)
+    H, W = 64, 512
+    g0, g1, _ = synth.eloftr_pair(H, W)
+    o = eloftr_forward(weights, g0, g1, backbone=True, coarse=True, fine=False)
+    net = ic.Eloftr(dev, weights_file, H, W)
+    try:
+        r = net.match(g0, g1)
+        n = (H // 8) * (W // 8)
+        for k in range(2):
+            x = net.buffer(f"x{k}", 256 * n)
+            assert rel(x, o["coarse"][k]) <= TOL
+        assert rel(r["row_max"], o["row_max"]) <= TOL
+        sure = o["row_margin"] / np.maximum(o["row_max"], 1e-30) > MARGIN
+        assert np.array_equal(r["row_arg"][sure], o["row_arg"][sure])
+    finally:
+        net.close()
