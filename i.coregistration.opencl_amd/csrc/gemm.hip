@@ -977,31 +977,46 @@ static bool gemm_dma_ok(const gemm_args &g, int bmode, bool va, bool vb)
            ((long long)(g.K - 1) * g.ldb + g.N) * 4 < lim;
 }
 
-/* Main-kernel work split over cus CUs: with under 4 tiles per CU, the
- * tiles left over after an equal whole number per CU (at most half the
- * CUs' worth) are cut over K so that each CU gets about one piece of at
- * least 4 k slices; one batch, plain epilogues only. */
+/* Main-kernel work split over cus CUs, for one-batch grids of under 4
+ * tiles per CU with plain epilogues: the tiles from nfull on are cut over
+ * K into split pieces of at least 4 k slices. Either the tiles left over
+ * after an equal whole number per CU are cut (about one piece per CU), or
+ * all of them; the choice with the smallest per-CU load (in tiles) is
+ * taken when it is at least 10 % below the uncut grid's, which pays for
+ * the second launch. */
 static bool gemm_plan(const gemm_args &g, int bmode, int nb, int cus, int &nfull, int &split)
 {
     const int tiles = ((g.M + 63) / 64) * ((g.N + 63) / 64);
     const int nk = (g.K + 15) / 16;
-    int rem;
+    const int smax = std::min(nk / 4, GEMM_MAX_SPLIT);
+    const int rem = cus > 0 ? tiles % cus : 0;
+    double best;
 
     nfull = tiles;
     split = 1;
     if (nb != 1 || g.nb1 != 1 || bmode == GEMM_B_CONV || g.rup || cus < 1 ||
-        tiles >= 4 * cus)
+        tiles >= 4 * cus || smax < 2)
         return false;
-    rem = tiles % cus;
-    if (rem == 0 || 2 * rem > cus)
-        return false;
-    split = std::min(std::min(cus / rem, nk / 4), GEMM_MAX_SPLIT);
-    if (split < 2) {
-        split = 1;
-        return false;
+    best = 0.9 * (double)((tiles + cus - 1) / cus);
+    for (int s = 2; s <= smax; s++) {
+        /* All tiles cut. */
+        const double all = (double)(((long long)tiles * s + cus - 1) / cus) / s;
+        /* Only the leftover tiles cut. */
+        const double left =
+            rem ? (double)(tiles - rem) / cus + (double)((rem * s + cus - 1) / cus) / s : 1e30;
+
+        if (left < best) {
+            best = left;
+            nfull = tiles - rem;
+            split = s;
+        }
+        if (all < best) {
+            best = all;
+            nfull = 0;
+            split = s;
+        }
     }
-    nfull = tiles - rem;
-    return true;
+    return split > 1;
 }
 
 size_t gemm_split_floats(const gemm_args &g, int bmode, int nb, bool va, bool vb, int cus)
