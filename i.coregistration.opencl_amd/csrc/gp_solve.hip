@@ -179,16 +179,21 @@ __global__ void __launch_bounds__(256)
     for (int j = 0; j < nb; j++) {
         if (tid < 64) {
             const double d = s[j][j];
-            const double sq = sqrt(d);
+            /* 1 / sqrt(d) from the hardware estimate and two Newton
+             * steps (each doubles the correct bits), then sqrt(d) = d r:
+             * no division or square-root sequence on the column chain. */
+            double r = __builtin_amdgcn_rsq(d);
 
+            r = r * fma(-0.5 * d * r, r, 1.5);
+            r = r * fma(-0.5 * d * r, r, 1.5);
             if (tid == 0 && !(d > 0.0) && *info == 0)
                 *info = k + j + 1;
             if (tid == j) {
-                s[j][j] = sq;
-                dinv[j] = 1.0 / sq;
+                s[j][j] = d * r;
+                dinv[j] = r;
             }
             else if (tid < nb)
-                s[tid][j] /= sq;
+                s[tid][j] *= r;
         }
         __syncthreads();
         {
