@@ -1039,7 +1039,8 @@ void eloftr_ln_residual(struct ops *o, cl_mem M, int nb, int C, int n,
  * outputs. */
 #define AGG_D 256
 #define AGG_T 4
-__global__ void __launch_bounds__(AGG_D)
+#define AGG_NT 1024 /* threads: one (channel, token) pair each */
+__global__ void __launch_bounds__(AGG_NT)
     aggregate_kernel(const float *__restrict__ X, const float *__restrict__ Y,
                      long long img, const float *__restrict__ wq,
                      const float *__restrict__ g, const float *__restrict__ bt,
@@ -1051,18 +1052,16 @@ __global__ void __launch_bounds__(AGG_D)
     __shared__ __align__(16) float ws[AGG_D * 16];
     const int tid = threadIdx.x, b = blockIdx.y, na = (h / 4) * aw;
     const int p0 = blockIdx.x * AGG_T;
-    constexpr int PP = AGG_D * AGG_T / AGG_D; /* pairs per thread */
+    constexpr int PP = AGG_D * AGG_T / AGG_NT; /* pairs per thread */
     float q[PP], kv[PP];
 
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-        *(float4 *)&ws[(tid + AGG_D * i) * 4] = *(const float4 *)(wq + (tid + AGG_D * i) * 4);
+    *(float4 *)&ws[tid * 4] = *(const float4 *)(wq + tid * 4);
     {
         float4 xr[PP][4], yr[PP][4];
 
 #pragma unroll
         for (int r = 0; r < PP; r++) {
-            const int pr = tid + AGG_D * r, c = pr / AGG_T, t = pr % AGG_T;
+            const int pr = tid + AGG_NT * r, c = pr / AGG_T, t = pr % AGG_T;
             const int p = min(p0 + t, na - 1), ay = p / aw, ax = p - ay * aw;
             const long long base = (long long)b * img + (long long)c * h * w +
                                    (long long)(4 * ay) * w + 4 * ax;
@@ -1077,7 +1076,7 @@ __global__ void __launch_bounds__(AGG_D)
         __syncthreads();
 #pragma unroll
         for (int r = 0; r < PP; r++) {
-            const int pr = tid + AGG_D * r, c = pr / AGG_T;
+            const int pr = tid + AGG_NT * r, c = pr / AGG_T;
 
             q[r] = 0.0f;
             kv[r] = -INFINITY;
@@ -1096,13 +1095,13 @@ __global__ void __launch_bounds__(AGG_D)
     }
 #pragma unroll
     for (int r = 0; r < PP; r++) {
-        const int pr = tid + AGG_D * r, c = pr / AGG_T, t = pr % AGG_T;
+        const int pr = tid + AGG_NT * r, c = pr / AGG_T, t = pr % AGG_T;
 
         sv[0][t][c] = q[r];
         sv[1][t][c] = kv[r];
     }
     __syncthreads();
-    if (p0 + (tid >> 6) < na) {
+    if (tid < 64 * AGG_T && p0 + (tid >> 6) < na) {
         const int lane = tid & 63, t = tid >> 6;
         const long long row = (long long)b * na + p0 + t;
 
@@ -1155,7 +1154,7 @@ void eloftr_aggregate(struct ops *o, cl_mem X, cl_mem Y, int nb, int C, int h,
     need_floats(KV, 0, (long long)nb * ah * aw * C, op, "KV");
     prof_scope ps(o->ocl, "aggregate");
     hipLaunchKernelGGL(aggregate_kernel, dim3((ah * aw + AGG_T - 1) / AGG_T, nb),
-                       dim3(AGG_D), 0,
+                       dim3(AGG_NT), 0,
                        stream_of(o->ocl), cfptr(X), cfptr(Y), img, cfptr(wq),
                        cfptr(g), cfptr(b), h, w, aw, eps, fptr(Q), fptr(KV));
     launch_check(op);
