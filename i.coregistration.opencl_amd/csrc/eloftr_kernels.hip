@@ -404,13 +404,9 @@ extern "C" void eloftr_conf_col(struct ops *o, cl_mem S, int R, int N, int r0,
  * the row partials band by band in increasing order. N % 4 == 0. */
 #define TB_RPW 16 /* rows per wave */
 
-/* The passes are bound by the exponentials (two per element), so they
- * use the hardware exp2 (__expf: relative error about 1e-6, far inside
- * the confidence tolerance; the argmax rules are unchanged). */
-__device__ __forceinline__ float dual_conf_fast(float s, float lr, float lc)
-{
-    return __expf(s - lr) * __expf(s - lc);
-}
+/* The exponentials are the full-precision expf of the reference's
+ * dual_conf (eloftr_kernels.cl:68-72): these passes decide the row and
+ * column argmaxes and the 0.2 threshold, so no fast exp2 form is used. */
 
 __global__ void __launch_bounds__(256)
     lse_tile_kernel(const float *__restrict__ S, int R, int N, int nbands,
@@ -432,7 +428,7 @@ __global__ void __launch_bounds__(256)
         float e = 0.0f;
 
         if (m != -INFINITY)
-            e = __expf(v[i].x - m) + __expf(v[i].y - m) + __expf(v[i].z - m) + __expf(v[i].w - m);
+            e = expf(v[i].x - m) + expf(v[i].y - m) + expf(v[i].z - m) + expf(v[i].w - m);
         e = wave_sum_full(e);
         if (lane == 0 && rb + i < R)
             rpart[(long long)(rb + i) * nbands + b] = make_float2(m, e);
@@ -447,7 +443,7 @@ __global__ void __launch_bounds__(256)
         if (m != -INFINITY)
 #pragma unroll
             for (int i = 0; i < TB_RPW; i++)
-                e += __expf(((const float *)&v[i])[k] - m);
+                e += expf(((const float *)&v[i])[k] - m);
         cp[w][4 * lane + k] = make_float2(m, e);
     }
     __syncthreads();
@@ -463,7 +459,7 @@ __global__ void __launch_bounds__(256)
         if (m != -INFINITY)
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                e += cp[q][tid].x == -INFINITY ? 0.0f : cp[q][tid].y * __expf(cp[q][tid].x - m);
+                e += cp[q][tid].x == -INFINITY ? 0.0f : cp[q][tid].y * expf(cp[q][tid].x - m);
         cpart[(long long)c * N + j] = make_float2(m, e);
     }
 }
@@ -487,7 +483,7 @@ __global__ void __launch_bounds__(256)
         mt = fmaxf(mt, __shfl_xor(mt, o, MERGE_C));
     if (mt != -INFINITY)
         for (int q = q0; q < nbands; q += MERGE_C)
-            e += p[q].x == -INFINITY ? 0.0f : p[q].y * __expf(p[q].x - mt);
+            e += p[q].x == -INFINITY ? 0.0f : p[q].y * expf(p[q].x - mt);
 #pragma unroll
     for (int o = MERGE_C / 2; o > 0; o >>= 1)
         e += __shfl_xor(e, o, MERGE_C);
@@ -527,7 +523,7 @@ __global__ void __launch_bounds__(256)
 
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const float x = dual_conf_fast(((const float *)&v[i])[k], lr, ((const float *)&l4)[k]);
+            const float x = dual_conf(((const float *)&v[i])[k], lr, ((const float *)&l4)[k]);
 
             if (jon && r < R) {
                 if (x > best) {

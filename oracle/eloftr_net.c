@@ -384,7 +384,7 @@ int orc_eloftr_forward(const struct orc_named *weights, int nweights,
     orc_transpose(x[1], tok1, 1, D, n);
     orc_eloftr_coarse(tok0, tok1, n, D, 1.0f / (D * 0.1f), n, out->row_max,
                       out->row_arg, out->col_arg, out->row_margin,
-                      out->col_margin);
+                      out->col_margin, out->col_max);
     free(tok0);
     free(tok1);
     nm = orc_eloftr_select(out->row_max, out->row_arg, out->col_arg, h, w,

@@ -558,7 +558,8 @@ void orc_fold_bn(float *w, float *b, int K, long per, const float *gamma,
 
 void orc_eloftr_coarse(const float *F0, const float *F1, int n, int D,
                        float alpha, int blk, float *row_max, int *row_arg,
-                       int *col_arg, float *row_margin, float *col_margin)
+                       int *col_arg, float *row_margin, float *col_margin,
+                       float *col_max)
 {
     float *S = malloc((size_t)n * n * sizeof(float));
     float *lse = malloc((size_t)n * sizeof(float));
@@ -660,6 +661,8 @@ void orc_eloftr_coarse(const float *F0, const float *F1, int n, int D,
         c2[i] = second;
         if (col_margin)
             col_margin[i] = best - second;
+        if (col_max)
+            col_max[i] = best;
     }
     free(S);
     free(lse);

@@ -102,11 +102,13 @@ void orc_fold_bn(float *w, float *b, int K, long per, const float *gamma,
 /* Coarse dual-softmax statistics and argmaxes of the n x n score matrix
  * S = alpha F0 F1^T (F0, F1 token-major n x D), eloftr_kernels.cl:10-144
  * as scheduled by eloftr.c:498-548 (row blocks of blk rows): row_max,
- * row_arg, col_arg (n each). Also returns the row margin (top-1 minus
- * top-2 confidence) when margin is not NULL. */
+ * row_arg, col_arg (n each). Also returns the row and column margins
+ * (top-1 minus top-2 confidence) and the column maximum confidence when
+ * those pointers are not NULL. */
 void orc_eloftr_coarse(const float *F0, const float *F1, int n, int D,
                        float alpha, int blk, float *row_max, int *row_arg,
-                       int *col_arg, float *row_margin, float *col_margin);
+                       int *col_arg, float *row_margin, float *col_margin,
+                       float *col_max);
 
 /* Host mutual / threshold / border selection, eloftr.c:552-566. Returns
  * the match count; mi, mj, mconf sized n. */
@@ -159,6 +161,7 @@ struct orc_eloftr_out {
     int *mi, *mj;
     float *mconf, *kp, *fine_margin;
     float *fine[2]; /* 64 x H x W each */
+    float *col_max;
 };
 
 /* The whole Efficient LoFTR pass of eloftr.c:654-681 on grey H x W

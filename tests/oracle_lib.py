@@ -38,7 +38,7 @@ SIGS = {
     "orc_transpose": (None, [_FP, _FP, _I, _I, _I]),
     "orc_axpby": (None, [_FP, _FP, _F, _FP, _F, _L, _L]),
     "orc_fold_bn": (None, [_FP, _FP, _I, _L, _FP, _FP, _FP, _FP, _F]),
-    "orc_eloftr_coarse": (None, [_FP, _FP, _I, _I, _F, _I, _FP, _IP, _IP, _FP, _FP]),
+    "orc_eloftr_coarse": (None, [_FP, _FP, _I, _I, _F, _I, _FP, _IP, _IP, _FP, _FP, _FP]),
     "orc_eloftr_select": (_I, [_FP, _IP, _IP, _I, _I, _F, _I, _IP, _IP, _FP]),
     "orc_eloftr_fine": (None, [_FP, _FP, _I, _I, _IP, _I, _F, _FP, _FP]),
     "orc_roma_row_norm": (None, [_FP, _I, _I, _FP]),
@@ -63,7 +63,7 @@ class EloftrOut(C.Structure):
         ("row_arg", _IP), ("col_arg", _IP),
         ("nm", C.c_int), ("mi", _IP), ("mj", _IP),
         ("mconf", _FP), ("kp", _FP), ("fine_margin", _FP),
-        ("fine", _FP * 2),
+        ("fine", _FP * 2), ("col_max", _FP),
     ]
 
 
@@ -113,13 +113,14 @@ def eloftr_forward(weights, g0, g1, pos_scale=1.0, backbone=False, coarse=False,
     H, W = g0.shape
     n = (H // 8) * (W // 8)
     arr, keep = named_array(weights)
-    out = {k: np.zeros(n, np.float32) for k in ("row_max", "row_margin", "col_margin", "mconf")}
+    out = {k: np.zeros(n, np.float32)
+           for k in ("row_max", "row_margin", "col_margin", "col_max", "mconf")}
     for k in ("row_arg", "col_arg", "mi", "mj"):
         out[k] = np.zeros(n, np.int32)
     out["kp"] = np.zeros(4 * n, np.float32)
     out["fine_margin"] = np.zeros(n, np.float32)
     st = EloftrOut()
-    for k in ("row_max", "row_margin", "col_margin", "mconf", "kp", "fine_margin"):
+    for k in ("row_max", "row_margin", "col_margin", "col_max", "mconf", "kp", "fine_margin"):
         setattr(st, k, fp(out[k]))
     for k in ("row_arg", "col_arg", "mi", "mj"):
         setattr(st, k, ip(out[k]))

@@ -32,7 +32,7 @@ def oracle_coarse(orc, F0, F1, alpha, blk):
     rarg, carg = np.zeros(n, np.int32), np.zeros(n, np.int32)
     rmar, cmar = np.zeros(n, np.float32), np.zeros(n, np.float32)
     orc.orc_eloftr_coarse(fp(F0), fp(F1), n, D, alpha, blk, fp(rmax), ip(rarg),
-                          ip(carg), fp(rmar), fp(cmar))
+                          ip(carg), fp(rmar), fp(cmar), None)
     return rmax, rarg, carg, rmar, cmar
 
 
