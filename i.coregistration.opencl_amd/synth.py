@@ -190,6 +190,20 @@ def save_safetensors(tensors, path):
     return path
 
 
+def save_torch(tensors, path, legacy=False, wrap=None, prefix=""):
+    """Write tensors with torch.save, as the published checkpoints are:
+    the zip archive (or the legacy pickle stream with legacy=True), names
+    prefixed by prefix, the dict optionally wrapped as {wrap: dict, ...}
+    the way training checkpoints hold it."""
+    import torch
+    path = Path(path)
+    path.parent.mkdir(parents=True, exist_ok=True)
+    sd = {prefix + k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in tensors.items()}
+    obj = {wrap: sd, "epoch": 7} if wrap else sd
+    torch.save(obj, str(path), _use_new_zipfile_serialization=not legacy)
+    return path
+
+
 def eloftr_weights_file(path, seed=BASE_SEED + CONFIG_ELOFTR):
     """Write (once) and return the ELoFTR weights file."""
     path = Path(path)

@@ -1,12 +1,13 @@
 /* SPDX-License-Identifier: Unlicense */
 
 /* Checkpoint reader of the model drivers: the API of the reference's
- * pth_loader.h (pth_loader.h:9-61 of i.coregistration.opencl), over
- * safetensors files (F32, F16, BF16 tensors; other dtypes are indexed
- * as PTH_OTHER and skipped by the drivers). The torch zip and legacy
- * pickle formats the reference also reads are not part of this build:
- * weights reach the HIP path as safetensors with the reference's tensor
- * names. Every format or lookup problem is a fatal error. */
+ * pth_loader.h (pth_loader.h:9-61 of i.coregistration.opencl) over the
+ * three formats its pth_loader.c reads: torch.save zip archives (stored
+ * entries, Zip64 included), legacy torch.save pickle streams and
+ * safetensors files. float32, float16 and bfloat16 tensors are indexed
+ * (read back as float32); integer and boolean tensors are left out.
+ * Pickles are interpreted without executing anything. Every format or
+ * lookup problem is a fatal error. */
 
 #ifndef ICOREG_PTH_LOADER_H
 #define ICOREG_PTH_LOADER_H
@@ -26,11 +27,11 @@ struct pth_tensor {
     char *name;
     int ndim;
     long shape[PTH_MAX_DIMS];
-    long stride[PTH_MAX_DIMS]; /* Contiguous, in elements. */
-    long storage_offset;       /* In elements (always 0 here). */
+    long stride[PTH_MAX_DIMS]; /* In elements. */
+    long storage_offset;       /* In elements. */
     enum pth_dtype dtype;
-    long data_offset;     /* Byte offset of the data in the file. */
-    size_t storage_bytes; /* Byte size of the data. */
+    long data_offset;     /* Byte offset of the storage in the file. */
+    size_t storage_bytes; /* Byte size of the storage. */
 };
 
 struct pth_file {
@@ -40,7 +41,7 @@ struct pth_file {
     struct pth_tensor *tensors;
 };
 
-/* Open and index a safetensors file (pth_loader.h:36-38). */
+/* Open and index a checkpoint (pth_loader.h:36-38). */
 void pth_open(struct pth_file *pf, const char *path);
 
 /* The tensor called name, or NULL (pth_loader.h:40-41). */

@@ -158,3 +158,24 @@ def test_detect_512_properties(dev, ic, weights):
     assert np.array_equal(g["score"], heat[xy[:, 1], xy[:, 0]])
     assert np.abs(np.linalg.norm(g["desc"], axis=1) - 1).max() < 1e-5
     assert rel(g["desc"], R.gather(out, xy)) < 1e-5
+
+
+def test_detect_from_torch_checkpoint(dev, ic, weights, tmp_path):
+    """The same weights in a torch.save zip archive, held under
+    "extractor" as DISK's published checkpoint holds them, give the same
+    keypoints, scores and descriptors bit for bit as the safetensors load."""
+    print("[disk] detect from a torch.save checkpoint", flush=True)
+    fpath, wd = weights
+    pth = synth.save_torch(wd, tmp_path / "disk-save.pth", wrap="extractor")
+    img = synth.disk_image(128, 128)
+    out = []
+    for p in (fpath, pth):
+        net = ic.Disk(dev, p, 128, 128, nmax=512)
+        try:
+            out.append(net.detect(img, n=512, thresh=0.0))
+        finally:
+            net.close()
+    a, b = out
+    assert a["n"] == b["n"] > 0
+    for k in ("xy", "score", "desc"):
+        assert np.array_equal(a[k], b[k]), k

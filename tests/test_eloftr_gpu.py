@@ -320,3 +320,23 @@ def check_coarse_indices(r, o, min_sure=0.8):
     sure_c = o["col_margin"] / np.maximum(o["col_max"], 1e-30) > MARGIN
     assert sure_c.mean() > min_sure
     assert np.array_equal(r["col_arg"][sure_c], o["col_arg"][sure_c])
+
+
+def test_network_from_torch_checkpoint(dev, ic, weights, weights_file, tmp_path):
+    """The ELoFTR weights in a torch.save zip archive (under "state_dict")
+    give the same coarse statistics and matches bit for bit."""
+    H, W = 128, 160
+    print(f"[eloftr] network {H}x{W} from a torch.save checkpoint", flush=True)
+    pth = synth.save_torch(weights, tmp_path / "eloftr.pth", wrap="state_dict")
+    g0, g1 = synth.eloftr_noise_pair(H, W, shift=(8, 16))
+    out = []
+    for p in (weights_file, pth):
+        net = ic.Eloftr(dev, p, H, W)
+        try:
+            out.append(net.match(g0, g1))
+        finally:
+            net.close()
+    a, b = out
+    assert a["nm"] == b["nm"] > 0
+    for k in ("row_max", "row_arg", "col_arg", "mi", "mj", "mconf", "kp"):
+        assert np.array_equal(a[k], b[k]), k

@@ -166,3 +166,24 @@ def test_roma_coarse_560_properties(dev, ic, weights, tmp_path):
         assert np.abs(cls_full - flow).max() < 1e-5
     finally:
         net.close()
+
+
+def test_roma_match_from_torch_checkpoints(dev, ic, weights, tmp_path):
+    """RoMa from torch.save files the way the published ones are laid out
+    (the matcher's tensors under "matcher.model.", DINOv2 in the legacy
+    pickle stream here) gives the same warp and certainty bit for bit as
+    the safetensors load."""
+    print(f"[roma] match from torch.save checkpoints coarse={COARSE} tile={TILE}", flush=True)
+    (fm, fd, _), (wm, wd, _) = weights
+    pm = synth.save_torch(wm, tmp_path / "roma_outdoor.pth", prefix="matcher.model.")
+    pd = synth.save_torch(wd, tmp_path / "dinov2_vitl14_pretrain.pth", legacy=True)
+    a, b, _ = synth.roma_pair(TILE, TILE)
+    out = []
+    for m, d in ((fm, fd), (pm, pd)):
+        net = ic.Roma(dev, m, d, TILE, TILE, coarse=COARSE)
+        try:
+            out.append(net.match(a, b))
+        finally:
+            net.close()
+    for k in ("flow", "cert"):
+        assert np.array_equal(out[0][k], out[1][k]), k
