@@ -223,6 +223,222 @@ def bench_roma(ic, dev, synth, wdir, steps, warmup, profile_steps):
     }
 
 
+VGG_BLOCKS = ((2, 64), (2, 128), (4, 256), (4, 512))
+# RoMa's v1 refiners at scales 8, 4, 2, 1: features, embedding, radius
+# (roma.c:60-64); input channels 2 f + e + (2 r + 1)^2.
+REFINE_V1 = ((8, 512, 64, 3), (4, 256, 32, 2), (2, 64, 16, 0), (1, 9, 6, 0))
+PROJ_V1 = {8: (512, 512), 4: (256, 256), 2: (128, 64), 1: (64, 9)}
+
+
+def vgg_flops(H, W, nblk=4, proj=PROJ_V1):
+    """One image through VGG19-BN's first nblk blocks plus the 1 x 1
+    projections to the refiner features (roma.c:740-768)."""
+    f, cin, h, w = 0.0, 3, H, W
+    for b, (n, c) in enumerate(VGG_BLOCKS[:nblk]):
+        for _ in range(n):
+            f += 2.0 * c * cin * 9 * h * w
+            cin = c
+        pi, po = proj[1 << b]
+        f += 2.0 * po * pi * h * w
+        h, w = h // 2, w // 2
+    return f
+
+
+def refiner_flops(H, W, table=REFINE_V1):
+    """The v1 refiners on an H x W pass: per scale the displacement
+    embedding, local correlation ((2 r + 2)^2 whole-cell dot products per
+    cell), 9 depthwise 5 x 5 + 1 x 1 blocks and the output convolution."""
+    f = 0.0
+    for s, feat, emb, r in table:
+        n = (H // s) * (W // s)
+        cin = 2 * feat + emb + ((2 * r + 1) ** 2 if r else 0)
+        f += 2.0 * emb * 2 * n
+        if r:
+            f += 2.0 * feat * (2 * r + 2) ** 2 * n
+        f += 9 * (2.0 * cin * 25 * n + 2.0 * cin * cin * n)
+        f += 2.0 * 3 * cin * n
+    return f
+
+
+def disk_flops(H=512, W=512):
+    """DISK's nine 5 x 5 convolutions on one H x W image (disk.c:28-30)."""
+    cin = (3, 16, 32, 64, 64, 128, 128, 96, 80)
+    cout = (16, 32, 64, 64, 64, 64, 64, 64, 129)
+    lvl = (0, 1, 2, 3, 4, 3, 2, 1, 0)
+    return sum(2.0 * co * ci * 25 * (H >> l) * (W >> l) for ci, co, l in zip(cin, cout, lvl))
+
+
+def hbm_kernel_bytes(kind, C, n, r=0):
+    """Compulsory HBM bytes of a refiner sampling kernel on n cells:
+    warp sample reads the C x n map and the warp, writes C x n; local
+    correlation reads both C x n maps and the warp, writes (2 r + 1)^2 x n."""
+    if kind == "warp_sample":
+        return 4 * C * n + 8 * n + 4 * C * n
+    return 2 * 4 * C * n + 8 * n + 4 * (2 * r + 1) ** 2 * n
+
+
+def time_launches(dev, fn, reps=20):
+    """Mean ms of fn() over reps launches after one warm-up, HIP events on
+    the library's stream."""
+    fn()
+    dev.finish()
+    dev.reset_events()
+    e0 = dev.event()
+    for _ in range(reps):
+        fn()
+    e1 = dev.event()
+    dev.finish()
+    return dev.elapsed_ms(e0, e1) / reps
+
+
+def bench_hbm_kernels(ic, dev, H=864, W=864):
+    """The refiner sampling kernels alone at the refiner config's shapes
+    (864 x 864: s8, s4, s2, s1): warp sample and local correlation on
+    seeded features and a smooth warp, each timed over 20 launches;
+    achieved GB/s = compulsory bytes / mean launch time."""
+    out = []
+    rng = np.random.default_rng(7)
+    for s, feat, emb, r in REFINE_V1:
+        h, w = H // s, W // s
+        n = h * w
+        f1 = dev.upload(rng.standard_normal((feat, n), np.float32))
+        f2 = dev.upload(rng.standard_normal((feat, n), np.float32))
+        gx = (2 * (np.arange(w) + 0.5) / w - 1)[None, :] + 0 * np.arange(h)[:, None]
+        gy = (2 * (np.arange(h) + 0.5) / h - 1)[:, None] + 0 * np.arange(w)[None, :]
+        fl = np.stack([gx + 0.03 * np.sin(gy * 3), gy + 0.03 * np.cos(gx * 2)]).astype(np.float32)
+        flow = dev.upload(fl)
+        side = 2 * r + 1
+        d = dev.zeros((feat + side * side) * n)
+        api, po = dev.api, dev.po
+        ms = time_launches(dev, lambda: api.roma_warp_sample(po, f2.mem, feat, h, w, flow.mem,
+                                                             d.mem, 0))
+        b = hbm_kernel_bytes("warp_sample", feat, n)
+        out.append({"kernel": "warp_sample", "scale": s, "C": feat, "cells": n,
+                    "ms": round(ms, 5), "bytes": b, "GBps": round(b / ms / 1e6, 1),
+                    "frac_hbm": round(b / ms / 1e6 / PEAK_HBM, 4)})
+        if r:
+            ms = time_launches(dev, lambda: api.roma_local_corr(po, f1.mem, f2.mem, feat, h, w, r,
+                                                                flow.mem, d.mem, 0))
+            b = hbm_kernel_bytes("local_corr", feat, n, r)
+            out.append({"kernel": "local_corr", "scale": s, "C": feat, "r": r, "cells": n,
+                        "ms": round(ms, 5), "bytes": b, "GBps": round(b / ms / 1e6, 1),
+                        "frac_hbm": round(b / ms / 1e6 / PEAK_HBM, 4)})
+        for x in (f1, f2, flow, d):
+            x.release()
+    return out
+
+
+def _kernel_table(table, steps):
+    return {k: {"ms_per_step": round(v[0] / steps, 4), "launches_per_step": v[1] / steps}
+            for k, v in sorted(table.items(), key=lambda kv: -kv[1][0])}
+
+
+def bench_refiners(ic, dev, synth, wdir, steps, warmup, profile_steps, H=864):
+    """The refiner config (roma_refine_device): VGG19-BN on both 864 x 864
+    images, then RoMa's refiners at 1/8 .. 1/1 from the synthetic initial
+    warp, on a pair already in HBM."""
+    fm, fd, _ = synth.roma_weights_files(wdir)
+    a, b, flow8, cert8 = synth.roma_refine_inputs(H, H)
+    net = ic.Roma(dev, fm, fd, H, H)
+    pair = dev.upload(np.stack([synth.imagenet_norm(a), synth.imagenet_norm(b)]))
+    f8, c8 = dev.upload(flow8), dev.upload(cert8)
+    run = lambda: net.refine_device(pair, f8, c8)
+    for _ in range(warmup):
+        run()
+    dev.finish()
+    dev.reset_events()
+    t0 = time.perf_counter()
+    e0 = dev.event()
+    for _ in range(steps):
+        run()
+    e1 = dev.event()
+    dev.finish()
+    ms = max(dev.elapsed_ms(e0, e1), (time.perf_counter() - t0) * 1e3) / steps
+    dev.profile_reset()
+    dev.set_profile(2)
+    for _ in range(profile_steps):
+        run()
+    dev.finish()
+    table = dev.profile_table()
+    dev.set_profile(0)
+    net.close()
+    fl = 2 * vgg_flops(H, H) + refiner_flops(H, H)
+    kern = _kernel_table(table, profile_steps)
+    print("[bench] refiners per-kernel ms per pair: " + json.dumps(kern), file=sys.stderr,
+          flush=True)
+    return {"workload": f"RoMa refiner stack, {H}x{H} RGB pair in HBM: VGG19-BN x 2, v1 "
+                        "refiners at 1/8, 1/4, 1/2, 1/1 (local correlation r = 3, 2) from the "
+                        "synthetic initial warp (roma_refine_device)",
+            "pairs_per_s": round(1000.0 / ms, 3), "ms_per_pair": round(ms, 4),
+            "gflop_per_pair": round(fl / 1e9, 1),
+            "pipeline_tflops": round(fl / (ms * 1e-3) / 1e12, 2), "kernels": kern}
+
+
+def bench_v2ref(ic, dev, synth, wdir, steps, warmup, H=1024):
+    """roma_v2ref end to end on a 1024 x 1024 pair: host images in (PIL
+    bicubic resampling, upload), RoMa coarse at 560 with both VGG19-BN
+    stacks, v2 refiners at 1/4, 1/2, 1/1 of the coarse and of the tile
+    pass, host epilogue out (roma_match)."""
+    fm, fd, f2 = synth.roma_weights_files(wdir)
+    a, b, _ = synth.roma_pair(H, H, seed=synth.BASE_SEED + synth.CONFIG_V2REF)
+    net = ic.Roma(dev, fm, fd, H, H, v2_path=f2)
+    for _ in range(warmup):
+        net.match(a, b)
+    dev.finish()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        net.match(a, b)
+    dev.finish()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    dev.profile_reset()
+    dev.set_profile(2)
+    net.match(a, b)
+    dev.finish()
+    table = dev.profile_table()
+    dev.set_profile(0)
+    net.close()
+    kern = _kernel_table(table, 1)
+    dev_ms = sum(v["ms_per_step"] for v in kern.values())
+    print("[bench] v2ref per-kernel ms per pair: " + json.dumps(kern), file=sys.stderr,
+          flush=True)
+    return {"workload": f"roma_v2ref end to end on a {H}x{H} RGB pair (host images in, "
+                        "roma_match: coarse 560 + v2 refiners, host epilogue out)",
+            "pairs_per_s": round(1000.0 / ms, 3), "ms_per_pair": round(ms, 3),
+            "device_kernel_ms_per_pair": round(dev_ms, 3), "kernels": kern}
+
+
+def bench_disk(ic, dev, synth, wdir, steps, warmup, H=512, n=2048):
+    """DISK on one 512 x 512 RGB image, host image in and keypoints out
+    (disk_detect: U-Net, NMS, top-n, descriptors)."""
+    fpath = synth.disk_weights_file(wdir / "disk_random.safetensors")
+    img = synth.disk_image(H, H)
+    net = ic.Disk(dev, fpath, H, H, nmax=n)
+    for _ in range(warmup):
+        r = net.detect(img, n=n, thresh=0.0)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        r = net.detect(img, n=n, thresh=0.0)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    dev.profile_reset()
+    dev.set_profile(2)
+    net.detect(img, n=n, thresh=0.0)
+    dev.finish()
+    table = dev.profile_table()
+    dev.set_profile(0)
+    net.close()
+    kern = _kernel_table(table, 1)
+    fl = disk_flops(H, H)
+    conv_ms = sum(v["ms_per_step"] for k, v in kern.items() if k.startswith("conv"))
+    print("[bench] DISK per-kernel ms per image: " + json.dumps(kern), file=sys.stderr,
+          flush=True)
+    return {"workload": f"DISK {H}x{H} RGB image, n = {n} (host image in, keypoints and "
+                        "descriptors out)",
+            "images_per_s": round(1000.0 / ms, 3), "ms_per_image": round(ms, 4),
+            "keypoints": int(r["n"]), "gflop_per_image": round(fl / 1e9, 1),
+            "conv_tflops": round(fl / (conv_ms * 1e-3) / 1e12, 2) if conv_ms else None,
+            "kernels": kern}
+
+
 def cpu_baseline(weights, size=256):
     """The oracle (C port of the reference kernels and schedule, OpenMP)
     on one size x size pair, scaled to a 640 x 640 pair by algorithmic
@@ -255,6 +471,8 @@ def main():
     ap.add_argument("--roma-only", action="store_true",
                     help="run only the RoMa leg and print its JSON object (for profiling)")
     ap.add_argument("--roma-steps", type=int, default=10)
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the refiner, roma_v2ref, DISK and HBM-kernel legs")
     ap.add_argument("--copy-calib", type=int, default=0,
                     help="MiB: one device-to-device copy of this size, the known-size "
                          "reference for HBM byte counters under rocprofv3 --pmc")
@@ -377,6 +595,13 @@ def main():
     if not args.no_roma:
         roma = bench_roma(ic, dev, synth, wdir, args.roma_steps, 2, args.profile_steps)
 
+    extra = {}
+    if not args.no_extra:
+        extra["refiners864"] = bench_refiners(ic, dev, synth, wdir, 10, 2, 2)
+        extra["hbm_kernels"] = bench_hbm_kernels(ic, dev)
+        extra["roma_v2ref1024"] = bench_v2ref(ic, dev, synth, wdir, 3, 1)
+        extra["disk512"] = bench_disk(ic, dev, synth, wdir, 20, 3)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(synth.eloftr_weights_calibrated())
@@ -416,6 +641,7 @@ def main():
         "eloftr_with_matches": with_matches,
         "cpu_baseline": cpu,
         "roma560": roma,
+        **extra,
     }
     print(json.dumps(line), flush=True)
     dev.close()

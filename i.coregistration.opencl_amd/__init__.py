@@ -181,6 +181,7 @@ SIGNATURES = {
     "roma_alloc": (None, [_P, _I, _I]),
     "roma_match": (None, [_P, _P, _P, _S, _I]),
     "roma_coarse_device": (None, [_P, Mem]),
+    "roma_refine_device": (None, [_P, Mem, Mem, Mem]),
     "roma_free": (None, [_P]),
     # binding glue (include/icoreg_glue.h)
     "icoreg_pth_new": (_P, []),
@@ -199,6 +200,7 @@ SIGNATURES = {
                                 C.POINTER(C.POINTER(C.c_float))]),
     "icoreg_roma_buffer": (Mem, [_P, _S]),
     "icoreg_roma_gp_info": (_I, [_P]),
+    "icoreg_roma_last": (_I, [_P]),
     "icoreg_roma_set_imagenet": (None, [_P, _I]),
 }
 
@@ -211,7 +213,8 @@ _NO_CHECK = {"icoreg_set_fatal_mode", "icoreg_last_error", "icoreg_clear_error",
              "icoreg_eloftr_result", "icoreg_eloftr_coarse_stats",
              "icoreg_eloftr_set_pos_scale", "icoreg_eloftr_buffer", "roma_gp_work_bytes",
              "icoreg_roma_new", "icoreg_roma_result", "icoreg_roma_buffer",
-             "icoreg_roma_set_imagenet", "icoreg_disk_new", "icoreg_disk_buffer"}
+             "icoreg_roma_set_imagenet", "icoreg_disk_new", "icoreg_disk_buffer",
+             "icoreg_roma_last"}
 
 _lib = None
 
@@ -471,6 +474,13 @@ class Roma:
 
     def coarse_device(self, pair):
         self.dev.api.roma_coarse_device(self.m, pair.mem)
+
+    def refine_device(self, pair, flow8, cert8):
+        """roma_refine_device; returns the names of the buffers holding
+        the full-size warp and certainty logit."""
+        self.dev.api.roma_refine_device(self.m, pair.mem, flow8.mem, cert8.mem)
+        k = lib().icoreg_roma_last(self.m)
+        return f"fl{k}", f"ce{k}"
 
     def result(self):
         f, c, s = (C.POINTER(C.c_float)(), C.POINTER(C.c_float)(), C.POINTER(C.c_float)())

@@ -770,7 +770,7 @@ static void gp_check(struct roma_model *m)
  * (pw[r], pb[r]: pin -> pout channels, r = the scale index of block b)
  * into the pair buffer dst[r] (image B at dstride[r]). roma.c:740-768,
  * 997-1027. */
-static void vgg_pair(struct roma_model *m, int nblk, const cl_mem *w,
+static void vgg_pair(struct roma_model *m, cl_mem src, int nblk, const cl_mem *w,
                      const cl_mem *b, const int *cin, const int *cout,
                      const int *scale_of_block, const cl_mem *pw,
                      const cl_mem *pb, const int *pin, const int *pout,
@@ -778,7 +778,7 @@ static void vgg_pair(struct roma_model *m, int nblk, const cl_mem *w,
 {
     struct ops *o = m->ops;
     struct conv_geom g = ops_geom(3, 1, 1);
-    cl_mem in = m->img, out;
+    cl_mem in = src, out;
     int l = 0, h = H, wd = W;
 
     for (int blk = 0; blk < nblk; blk++) {
@@ -806,11 +806,11 @@ static void vgg_pair(struct roma_model *m, int nblk, const cl_mem *w,
     }
 }
 
-static void vgg(struct roma_model *m, int H, int W)
+static void vgg(struct roma_model *m, int H, int W, cl_mem src)
 {
     static const int sob[4] = {4, 3, 2, 1};
 
-    vgg_pair(m, 4, m->vgg_w, m->vgg_b, m->vgg_cin, m->vgg_cout, sob,
+    vgg_pair(m, src, 4, m->vgg_w, m->vgg_b, m->vgg_cin, m->vgg_cout, sob,
              m->proj_w, m->proj_b, m->proj_in, m->proj_out, m->P, m->pstride,
              H, W);
 }
@@ -822,7 +822,7 @@ static void vgg2(struct roma_model *m, int H, int W)
 
     for (int j = 0; j < ROMA2_SCALES; j++)
         pout[j] = m->ref2[j].feat;
-    vgg_pair(m, 3, m->vgg2_w, m->vgg2_b, m->vgg2_cin, m->vgg2_cout, sob,
+    vgg_pair(m, m->img, 3, m->vgg2_w, m->vgg2_b, m->vgg2_cin, m->vgg2_cout, sob,
              m->proj2_w, m->proj2_b, m->proj2_in, pout, m->P2, m->p2stride, H,
              W);
 }
@@ -1166,6 +1166,30 @@ extern "C" void roma_coarse_device(struct roma_model *m, cl_mem pair)
     ICOREG_API_END
 }
 
+extern "C" void roma_refine_device(struct roma_model *m, cl_mem pair,
+                                   cl_mem flow8, cl_mem cert8)
+{
+    ICOREG_API_BEGIN
+    const char *op = "roma_refine_device";
+    const int h8 = side(m, m->H, 1), w8 = side(m, m->W, 1);
+    const float sf = sqrtf((float)m->H * m->W) / m->coarse;
+    int cur = 0;
+
+    if (!m->H)
+        icoreg_fatal("%s before roma_alloc", op);
+    if (m->v2)
+        icoreg_fatal("%s: RoMa's own (v1) refiners only", op);
+    need_floats(pair, 0, 2L * 3 * m->H * m->W, op, "pair");
+    need_floats(flow8, 0, 2L * h8 * w8, op, "flow8");
+    need_floats(cert8, 0, (long)h8 * w8, op, "cert8");
+    vgg(m, m->H, m->W, pair);
+    ocl_copy(m->ocl, flow8, 0, m->fl[0], 0, 2 * (size_t)h8 * w8 * 4);
+    ocl_copy(m->ocl, cert8, 0, m->ce[0], 0, (size_t)h8 * w8 * 4);
+    refiners(m, 1, 1, ROMA_SCALES, m->H, m->W, sf, &cur, NULL, 0);
+    m->last = cur;
+    ICOREG_API_END
+}
+
 extern "C" void roma_match(struct roma_model *m, const float *imgA,
                            const float *imgB, const char *dump, int tile)
 {
@@ -1179,7 +1203,7 @@ extern "C" void roma_match(struct roma_model *m, const float *imgA,
         icoreg_fatal("roma_match before roma_alloc");
     /* Coarse pass. */
     upload_pair(m, imgA, imgB, m->coarse, m->coarse, m->in_c);
-    vgg(m, m->coarse, m->coarse);
+    vgg(m, m->coarse, m->coarse, m->img);
     if (m->v2)
         vgg2(m, m->coarse, m->coarse);
     dino_pair(m, m->img);
@@ -1209,7 +1233,7 @@ extern "C" void roma_match(struct roma_model *m, const float *imgA,
         dump_host(dump, tile, "in_f_0", m->in_f, 3 * hw);
         dump_host(dump, tile, "in_f_1", m->in_f + 3 * hw, 3 * hw);
     }
-    vgg(m, m->H, m->W);
+    vgg(m, m->H, m->W, m->img);
     ops_resize(m->ops, m->fl[cur], 2, m->coarse, m->coarse, m->fl[!cur],
                side(m, m->H, 1), side(m, m->W, 1), 0, 0, 0.0f);
     ops_resize(m->ops, m->ce[cur], 1, m->coarse, m->coarse, m->ce[!cur],

@@ -246,6 +246,38 @@ def roma_pair(H=560, W=560, seed=BASE_SEED + CONFIG_ROMA):
     return a, np.clip(b, 0.0, 1.0).astype(np.float32), d
 
 
+CONFIG_REFINE = 3
+CONFIG_V2REF = 4
+
+
+def imagenet_norm(img):
+    """(3, H, W) in 0..1 normalised with the ImageNet mean and deviation,
+    as RoMa's inputs are (roma.c:1170-1186)."""
+    mean = np.array([0.485, 0.456, 0.406], np.float32)[:, None, None]
+    std = np.array([0.229, 0.224, 0.225], np.float32)[:, None, None]
+    return ((img - mean) / std).astype(np.float32)
+
+
+def roma_refine_inputs(H=864, W=864, seed=BASE_SEED + CONFIG_REFINE, noise_px=2.0):
+    """The refiner config's inputs: the RoMa pair at H x W (A blurred
+    noise, B = A under a TPS warp) and the initial 1/8-scale warp of A
+    onto B, the TPS ground truth at the cell centres perturbed by
+    N(0, noise_px) px, normalised to -1..1 with align_corners = 0
+    (roma_kernels.cl:1-7), with a zero certainty logit. B(p) = A(p + d(p)),
+    so a point q of A lies near q - d(q) in B (first order)."""
+    a, b, d = roma_pair(H, W, seed)
+    rng = np.random.default_rng(seed + 500)
+    h, w = H // 8, W // 8
+    ys = (np.arange(h) * 8 + 3.5)[:, None]
+    xs = (np.arange(w) * 8 + 3.5)[None, :]
+    yi = np.clip(np.rint(ys).astype(int), 0, H - 1)
+    xi = np.clip(np.rint(xs).astype(int), 0, W - 1)
+    qx = xs - d[0][yi, xi] + rng.normal(0.0, noise_px, (h, w))
+    qy = ys - d[1][yi, xi] + rng.normal(0.0, noise_px, (h, w))
+    flow = np.stack([(2 * qx + 1) / W - 1, (2 * qy + 1) / H - 1]).astype(np.float32)
+    return a, b, flow, np.zeros((h, w), np.float32)
+
+
 def _rn(rng, shape, std):
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
 

@@ -59,6 +59,9 @@ cl_mem icoreg_roma_buffer(const struct roma_model *m, const char *name);
 /* 1 + the first failing GP pivot of the last solve, 0 if it succeeded
  * (waits for the stream). */
 int icoreg_roma_gp_info(struct roma_model *m);
+/* Index (0 or 1) of the fl / ce buffers holding roma_refine_device's
+ * result. */
+int icoreg_roma_last(const struct roma_model *m);
 
 void icoreg_roma_set_imagenet(struct roma_model *m, int on);
 

@@ -104,6 +104,7 @@ struct roma_model {
      * predicted standard deviation sd (H, W) in cells. */
     float *flow, *cert, *sd;
     float *in_c, *in_f; /* normalised inputs of both passes (pairs) */
+    int last;           /* fl / ce index holding roma_refine_device's result */
 };
 
 /* Read the weights: RoMa's RegressionMatcher state dict (names as
@@ -138,6 +139,17 @@ void roma_match(struct roma_model *m, const float *imgA, const float *imgB,
  * leaving the 1/14 warp and certainty logit in fl[0], ce[0]. The timed
  * unit of the benchmark. */
 void roma_coarse_device(struct roma_model *m, cl_mem pair);
+
+/* Extension: the fine pass of roma_match (roma.c:1404-1412) on a pair
+ * already on the device — two normalised (3, H, W) images back to back
+ * in pair, H x W the allocated tile — from a warp flow8 (2, H / 8, W / 8)
+ * and certainty logit cert8 (H / 8 x W / 8): VGG19-BN on both images,
+ * then the refiners at 1/8, 1/4, 1/2 and 1/1 with their resizes. The
+ * warp and certainty logit at full size are left in fl[last], ce[last].
+ * RoMa's own refiners only (no roma_load_v2). The timed unit of the
+ * refiner benchmark. */
+void roma_refine_device(struct roma_model *m, cl_mem pair, cl_mem flow8,
+                        cl_mem cert8);
 
 void roma_free(struct roma_model *m);
 

@@ -187,3 +187,88 @@ def test_roma_match_from_torch_checkpoints(dev, ic, weights, tmp_path):
             net.close()
     for k in ("flow", "cert"):
         assert np.array_equal(out[0][k], out[1][k]), k
+
+
+def _refine_from_dumps(dev, ic, net, folder, H, W, coarse):
+    """roma_refine_device on roma_match's own fine-pass inputs read back
+    from its dumps: the normalised pair and the coarse pass's final warp
+    and certainty, resized to 1/8 as roma_match resizes them."""
+    pair = np.concatenate([_read_dump(folder, "in_f_0"), _read_dump(folder, "in_f_1")])
+    f0 = dev.upload(_read_dump(folder, "p0_s1_flow"))
+    c0 = dev.upload(_read_dump(folder, "p0_s1_cert"))
+    h8, w8 = H // 8, W // 8
+    f8, c8 = dev.zeros(2 * h8 * w8), dev.zeros(h8 * w8)
+    dev.api.ops_resize(dev.po, f0.mem, 2, coarse, coarse, f8.mem, h8, w8, 0, 0, 0.0)
+    dev.api.ops_resize(dev.po, c0.mem, 1, coarse, coarse, c8.mem, h8, w8, 0, 0, 0.0)
+    fl, ce = net.refine_device(dev.upload(pair), f8, c8)
+    return net.buffer(fl, 2 * H * W), net.buffer(ce, H * W)
+
+
+def test_refine_device_is_the_fine_pass(dev, ic, weights, tmp_path):
+    """roma_refine_device (the refiner benchmark's unit) reproduces the
+    fine pass of roma_match bit for bit from the same inputs."""
+    print(f"[roma] refine_device vs match coarse={COARSE} tile={TILE}", flush=True)
+    (fm, fd, _), _ = weights
+    a, b, _ = synth.roma_pair(TILE, TILE)
+    net = ic.Roma(dev, fm, fd, TILE, TILE, coarse=COARSE)
+    try:
+        net.match(a, b, dump=str(tmp_path), tile=1)
+        flow, cert = _refine_from_dumps(dev, ic, net, tmp_path, TILE, TILE, COARSE)
+    finally:
+        net.close()
+    assert np.array_equal(flow, _read_dump(tmp_path, "p1_s1_flow"))
+    assert np.array_equal(cert, _read_dump(tmp_path, "p1_s1_cert"))
+
+
+def test_refiners_864_properties(dev, ic, weights, tmp_path):
+    """The refiner config at full size (864 x 864: VGG19-BN on both
+    images, refiners at 1/8 .. 1/1 with C = 512, 256, 64, 9 and local
+    correlation radii 3 and 2): from the synthetic initial warp the
+    outputs are finite and stay near it, and roma_match's own fine pass
+    at 864 x 864 is reproduced bit for bit by roma_refine_device."""
+    H = W = 864
+    print(f"[roma] refiners {H}x{W}", flush=True)
+    (fm, fd, _), _ = weights
+    a, b, flow8, cert8 = synth.roma_refine_inputs(H, W)
+    net = ic.Roma(dev, fm, fd, H, W)
+    try:
+        pair = dev.upload(np.stack([synth.imagenet_norm(a), synth.imagenet_norm(b)]))
+        fl, ce = net.refine_device(pair, dev.upload(flow8), dev.upload(cert8))
+        flow = net.buffer(fl, 2 * H * W).reshape(2, H, W)
+        cert = net.buffer(ce, H * W)
+        assert np.isfinite(flow).all() and np.isfinite(cert).all()
+        # The refiners move the warp by bounded steps: the result stays
+        # within a few cells of the initial warp (resized to full size).
+        up = np.repeat(np.repeat(flow8, 8, 1), 8, 2)
+        assert np.median(np.abs(flow - up)) < 0.1
+        got = net.match(a, b, dump=str(tmp_path), tile=1)
+        assert np.isfinite(got["flow"]).all()
+        assert ((got["cert"] >= 0) & (got["cert"] <= 1)).all()
+        flow2, cert2 = _refine_from_dumps(dev, ic, net, tmp_path, H, W, 560)
+    finally:
+        net.close()
+    assert np.array_equal(flow2, _read_dump(tmp_path, "p1_s1_flow"))
+    assert np.array_equal(cert2, _read_dump(tmp_path, "p1_s1_cert"))
+
+
+def test_roma_v2ref_1024_properties(dev, ic, weights):
+    """The full roma_v2ref config at 1024 x 1024 (RoMa coarse at 560 with
+    both VGG19-BN stacks, v2 refiners at 1/4, 1/2, 1/1, host epilogue):
+    finite warp in -1..1, certainty in 0..1, a finite positive standard
+    deviation wherever the precision is positive definite (almost
+    everywhere)."""
+    H = W = 1024
+    print(f"[roma] v2ref {H}x{W}", flush=True)
+    (fm, fd, f2), _ = weights
+    a, b, _ = synth.roma_pair(H, W, seed=synth.BASE_SEED + synth.CONFIG_V2REF)
+    net = ic.Roma(dev, fm, fd, H, W, v2_path=f2)
+    try:
+        got = net.match(a, b)
+        assert net.gp_info() == 0
+    finally:
+        net.close()
+    flow, cert, sd = got["flow"], got["cert"], got["sd"]
+    assert np.isfinite(flow).all() and np.abs(flow).max() <= 1.0
+    assert np.isfinite(cert).all() and ((cert >= 0) & (cert <= 1)).all()
+    ok = np.isfinite(sd)
+    assert ok.mean() > 0.99 and (sd[ok] > 0).all()
