@@ -128,14 +128,25 @@ __device__ __forceinline__ float bilinear_zero(const float *__restrict__ p,
            fy * ((1.0f - fx) * v10 + fx * v11);
 }
 
+/* One thread per (point, group of GS_CG channels): the point's taps
+ * and weights are computed once for its group, the group's planes read
+ * at the same offsets with all loads in flight together, and each
+ * channel's stores are 256 consecutive points. The grid's y dimension
+ * runs over the groups, so that a few thousand points still fill the
+ * GPU. */
+#define GS_CG 8
+
 __global__ void __launch_bounds__(256)
     grid_sample_kernel(const float *__restrict__ in, int C, int H, int W,
                        const float2 *__restrict__ grid, int n, int align,
                        float *__restrict__ out)
 {
-    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int i = blockIdx.x * 256 + threadIdx.x, c0 = blockIdx.y * GS_CG;
+    const long long plane = (long long)H * W;
     float2 g;
-    float ix, iy;
+    float ix, iy, fx = 0.0f, fy = 0.0f, v[GS_CG][4];
+    int x0 = 0, y0 = 0, o[4] = {0, 0, 0, 0};
+    bool ok, in4[4];
 
     if (i >= n)
         return;
@@ -148,12 +159,38 @@ __global__ void __launch_bounds__(256)
         ix = ((g.x + 1.0f) * W - 1.0f) * 0.5f;
         iy = ((g.y + 1.0f) * H - 1.0f) * 0.5f;
     }
-    /* One point per thread for every channel: the point's weights and
-     * taps are computed once, the channel planes read at the same
-     * offsets. */
-    for (int c = 0; c < C; c++)
-        out[(long long)c * n + i] =
-            bilinear_zero(in + (long long)c * H * W, H, W, ix, iy);
+    /* bilinear_zero's arithmetic, taps shared by the group. */
+    ok = isfinite(ix) && isfinite(iy);
+    if (ok) {
+        ix = fminf(fmaxf(ix, -2.0f), (float)W + 1.0f);
+        iy = fminf(fmaxf(iy, -2.0f), (float)H + 1.0f);
+        x0 = (int)floorf(ix);
+        y0 = (int)floorf(iy);
+        fx = ix - x0;
+        fy = iy - y0;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int xx = x0 + (q & 1), yy = y0 + (q >> 1);
+
+        in4[q] = ok && xx >= 0 && xx < W && yy >= 0 && yy < H;
+        o[q] = in4[q] ? yy * W + xx : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < GS_CG; k++) {
+        const float *p = in + (long long)min(c0 + k, C - 1) * plane;
+
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            v[k][q] = in4[q] ? p[o[q]] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < GS_CG; k++)
+        if (c0 + k < C)
+            out[(long long)(c0 + k) * n + i] =
+                ok ? (1.0f - fy) * ((1.0f - fx) * v[k][0] + fx * v[k][1]) +
+                         fy * ((1.0f - fx) * v[k][2] + fx * v[k][3])
+                   : 0.0f;
 }
 
 extern "C" void ops_grid_sample(struct ops *o, cl_mem in, int C, int H, int W,
@@ -173,7 +210,8 @@ extern "C" void ops_grid_sample(struct ops *o, cl_mem in, int C, int H, int W,
     need_floats(grid, 0, 2LL * n, op, "grid");
     need_floats(out, 0, (long long)C * n, op, "out");
     prof_scope ps(o->ocl, "grid_sample");
-    hipLaunchKernelGGL(grid_sample_kernel, dim3((unsigned)((n + 255) / 256)),
+    hipLaunchKernelGGL(grid_sample_kernel,
+                       dim3((unsigned)((n + 255) / 256), (unsigned)((C + GS_CG - 1) / GS_CG)),
                        dim3(256), 0, stream_of(o->ocl), cfptr(in), C, H, W,
                        (const float2 *)cfptr(grid), n, align_corners,
                        fptr(out));

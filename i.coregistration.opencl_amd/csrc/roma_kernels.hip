@@ -24,6 +24,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <limits.h>
 #include <math.h>
 
 #include "common.h"
@@ -149,15 +150,26 @@ __device__ __forceinline__ bil bilinear_setup(float x, float y, int H, int W,
     return b;
 }
 
+/* One thread per (cell, group of channels): the cell's taps and weights
+ * are computed once for its group, the group's channel planes read at
+ * the same offsets (all loads of the group in flight together), and the
+ * stores of a channel are 256 consecutive cells. The grid's y dimension
+ * runs over the channel groups, so that a few thousand cells still fill
+ * the GPU (11 664 cells x 512 channels at 1/8 of 864 x 864: 2944 blocks
+ * instead of 46). */
+#define WS_CG 8 /* channels per thread */
+
 __global__ void __launch_bounds__(256)
     warp_sample_kernel(const float *__restrict__ in, int C, int H, int W,
                        const float *__restrict__ flow, float *__restrict__ out,
                        int coff)
 {
     const int i = blockIdx.x * 256 + threadIdx.x, n = H * W;
+    const int c0 = blockIdx.y * WS_CG;
     bil b;
     bool in00, in01, in10, in11;
     int o00, o01, o10, o11;
+    float v[WS_CG][4];
 
     if (i >= n)
         return;
@@ -167,25 +179,77 @@ __global__ void __launch_bounds__(256)
     in10 = b.ok && b.x0 >= 0 && b.x0 < W && b.y0 + 1 >= 0 && b.y0 + 1 < H;
     in11 = b.ok && b.x0 + 1 >= 0 && b.x0 + 1 < W && b.y0 + 1 >= 0 &&
            b.y0 + 1 < H;
-    o00 = b.y0 * W + b.x0;
-    o01 = o00 + 1;
-    o10 = o00 + W;
-    o11 = o10 + 1;
-    for (int c = 0; c < C; c++) {
-        const float *p = in + (long long)c * n;
-        const float v00 = in00 ? p[o00] : 0.0f, v01 = in01 ? p[o01] : 0.0f;
-        const float v10 = in10 ? p[o10] : 0.0f, v11 = in11 ? p[o11] : 0.0f;
+    o00 = in00 ? b.y0 * W + b.x0 : 0;
+    o01 = in01 ? b.y0 * W + b.x0 + 1 : 0;
+    o10 = in10 ? (b.y0 + 1) * W + b.x0 : 0;
+    o11 = in11 ? (b.y0 + 1) * W + b.x0 + 1 : 0;
+#pragma unroll
+    for (int k = 0; k < WS_CG; k++) {
+        const float *p = in + (long long)min(c0 + k, C - 1) * n;
 
-        out[(long long)(coff + c) * n + i] =
-            b.ok ? (1.0f - b.fy) * ((1.0f - b.fx) * v00 + b.fx * v01) +
-                       b.fy * ((1.0f - b.fx) * v10 + b.fx * v11)
-                 : 0.0f;
+        v[k][0] = in00 ? p[o00] : 0.0f;
+        v[k][1] = in01 ? p[o01] : 0.0f;
+        v[k][2] = in10 ? p[o10] : 0.0f;
+        v[k][3] = in11 ? p[o11] : 0.0f;
     }
+#pragma unroll
+    for (int k = 0; k < WS_CG; k++)
+        if (c0 + k < C)
+            out[(long long)(coff + c0 + k) * n + i] =
+                b.ok ? (1.0f - b.fy) * ((1.0f - b.fx) * v[k][0] + b.fx * v[k][1]) +
+                           b.fy * ((1.0f - b.fx) * v[k][2] + b.fx * v[k][3])
+                     : 0.0f;
 }
 
 /* ---- local correlation ------------------------------------------------------------- */
 
-#define CORR_MAXC 1024
+/* out[k, i] for the (2 r + 1)^2 offsets k of cell i is the bilinear
+ * combination (at the warp's fractional position) of whole-cell dot
+ * products S[e] = sum_c f1[c, i] / sqrt(C) * f2[c, e] over the cells e of
+ * the (2 r + 2)^2 window at the warp's integer position (zero outside
+ * the image), roma_kernels.cl:143-192.
+ *
+ * A block takes a 4 x 4 patch of cells. Neighbouring cells of a smooth
+ * warp have overlapping windows, so the union of the patch's windows
+ * (clipped to the image) is a box of about (4 + 2 r + 1)^2 cells instead
+ * of 16 (2 r + 2)^2 reads. When the box holds at most LC_NB cells, the
+ * block brings, for 16 channels at a time, the patch's f1 columns and
+ * the box's f2 columns into LDS by LDS DMA (buffer_load ... lds: no
+ * register staging; box slots past the box and channels past C load as
+ * zeros from outside the buffer window), the next chunk in flight while
+ * the current one is used, one barrier per chunk, and forms every
+ * patch-cell x box-cell product on the matrix cores
+ * (v_mfma_f32_16x16x4f32: 16 cells x 16 box cells x 4 channels, box
+ * tiles shared out over the 4 waves). Each cell then reads its window's
+ * products from the box. Patches whose windows scatter (far-off or
+ * broken warps) take the per-cell path instead: one wave per cell, lanes
+ * over the window cells, channels in order. Patches go to the XCDs in
+ * contiguous bands, so that neighbouring patches share their f2 rows in
+ * one L2. */
+#define CORR_MAXC 1024 /* channels accepted (the reference's kernel: 512) */
+#define LC_T 16        /* cells of a patch (4 x 4) */
+#define LC_NB 256      /* box cells on the matrix-core path */
+#define LC_KC 16       /* channels per LDS chunk */
+#define LC_PMAX 272    /* largest LDS row pitch of a box chunk */
+#define LC_GS 260      /* LDS row pitch of the products */
+#define LC_OOB 0x80000000u
+#define LC_WAIT_VM0 0x0F70 /* s_waitcnt vmcnt(0) */
+
+typedef float lc_f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t lc_window(const float *p, unsigned bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)bytes, 0x00020000);
+}
+
+/* Block L of T to a tile: the 8 XCDs (blocks L, L + 8, ... on XCD L % 8)
+ * each get a contiguous band of tiles. */
+__device__ __forceinline__ int lc_xcd_tile(int L, int T)
+{
+    const int q = T >> 3, rem = T & 7, x = L & 7, idx = L >> 3;
+
+    return (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + idx;
+}
 
 __global__ void __launch_bounds__(256)
     local_corr_kernel(const float *__restrict__ f1,
@@ -193,65 +257,189 @@ __global__ void __launch_bounds__(256)
                       const float *__restrict__ flow, float *__restrict__ out,
                       int coff)
 {
-    __shared__ float a1[4][CORR_MAXC];
-    __shared__ float S[4][256];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int i = blockIdx.x * 4 + w, n = H * W;
-    const int side = 2 * r + 1, ps = 2 * r + 2, np = ps * ps;
+    __shared__ float G[LC_T * LC_GS]; /* products of the patch's cells */
+    __shared__ int cid[LC_T], ox[LC_T], oy[LC_T], okc[LC_T];
+    __shared__ float cfx[LC_T], cfy[LC_T];
+    __shared__ int box[4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tiles_x = (W + 3) >> 2, ntiles = tiles_x * ((H + 3) >> 2);
+    const int tile_id = lc_xcd_tile(blockIdx.x, ntiles);
+    const int px0 = (tile_id % tiles_x) * 4, py0 = (tile_id / tiles_x) * 4;
+    const int n = H * W, ps = 2 * r + 2, side = 2 * r + 1;
     const float rc = 1.0f / sqrtf((float)C);
-    const bool active = i < n;
-    bil b;
 
-    if (active) {
-        for (int c = lane; c < C; c += 64)
-            a1[w][c] = f1[(long long)c * n + i] * rc;
-        b = bilinear_setup(flow[i], flow[n + i], H, W, r);
+    /* The patch's cells: window origins and the box of their windows. */
+    if (tid < 64) {
+        const int x = px0 + (tid & 3), y = py0 + ((tid >> 2) & 3);
+        int lo_x = INT_MAX, lo_y = INT_MAX, hi_x = INT_MIN, hi_y = INT_MIN;
+
+        if (tid < LC_T) {
+            bil b = bilinear_setup(0.0f, 0.0f, H, W);
+            int ci = -1;
+
+            if (x < W && y < H) {
+                ci = y * W + x;
+                b = bilinear_setup(flow[ci], flow[n + ci], H, W, r);
+            }
+            cid[tid] = ci;
+            okc[tid] = ci >= 0 && b.ok;
+            ox[tid] = b.x0 - r;
+            oy[tid] = b.y0 - r;
+            cfx[tid] = b.fx;
+            cfy[tid] = b.fy;
+            if (ci >= 0 && b.ok) {
+                lo_x = b.x0 - r;
+                lo_y = b.y0 - r;
+                hi_x = b.x0 - r + ps - 1;
+                hi_y = b.y0 - r + ps - 1;
+            }
+        }
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) {
+            lo_x = min(lo_x, __shfl_xor(lo_x, o, 16));
+            lo_y = min(lo_y, __shfl_xor(lo_y, o, 16));
+            hi_x = max(hi_x, __shfl_xor(hi_x, o, 16));
+            hi_y = max(hi_y, __shfl_xor(hi_y, o, 16));
+        }
+        if (tid == 0) {
+            lo_x = max(lo_x, 0);
+            lo_y = max(lo_y, 0);
+            hi_x = min(hi_x, W - 1);
+            hi_y = min(hi_y, H - 1);
+            box[0] = lo_x;
+            box[1] = lo_y;
+            box[2] = hi_x >= lo_x ? hi_x - lo_x + 1 : 0;
+            box[3] = hi_y >= lo_y ? hi_y - lo_y + 1 : 0;
+        }
     }
-    else
-        b = bilinear_setup(0.0f, 0.0f, H, W);
     __syncthreads();
-    /* Whole-cell dot products of the (2 r + 2)^2 window, lanes over the
-     * window cells (up to 4 per lane at r = 7). */
-    if (active) {
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        int off[4];
-        bool ok[4];
+    const int bx0 = box[0], by0 = box[1], bw = box[2], bh = box[3];
+    const int nb = bw * bh;
+    const bool tiled = nb <= LC_NB;
+
+    if (tiled && nb > 0) {
+        /* Each wave streams its box tiles' operands straight from memory
+         * into registers (no LDS, no barriers): per step of 4 channels,
+         * lane l reads f1 of patch cell l % 16 and f2 of box cell
+         * 16 t + l % 16 of each of its tiles t, channel l / 16 of the step. */
+        const int nt = (nb + 15) >> 4;
+        const int acell = cid[lane & 15], kq = lane >> 4;
+        unsigned boff[4];
+        bool bon[4];
+        lc_f4 acc[4];
 
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int e = lane + 64 * q;
-            const int yy = b.y0 - r + e / ps, xx = b.x0 - r + e % ps;
+        for (int t = 0; t < 4; t++) {
+            const int j = (wv + 4 * t) * 16 + (lane & 15);
 
-            ok[q] = e < np && b.ok && xx >= 0 && xx < W && yy >= 0 && yy < H;
-            off[q] = ok[q] ? yy * W + xx : 0;
+            bon[t] = j < nb;
+            boff[t] = bon[t] ? (unsigned)((by0 + j / bw) * W + bx0 + j % bw) : 0u;
+            acc[t] = (lc_f4){0.0f, 0.0f, 0.0f, 0.0f};
         }
-        for (int c = 0; c < C; c++) {
-            const float a = a1[w][c];
-            const float *p = f2 + (long long)c * n;
+        const bool aon = acell >= 0;
+        const unsigned aoff = aon ? (unsigned)acell : 0u;
+        const int ntw = nt > wv ? (nt - wv + 3) >> 2 : 0; /* tiles of this wave */
+        const int cmain = C & ~31;
 
+        auto step = [&](int c, bool tail) {
+            const bool cok = !tail || c < C;
+            const long long base = (long long)c * n;
+            const float a = aon && cok ? f1[base + aoff] * rc : 0.0f;
+            float b[4];
+
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                b[t] = t < ntw && bon[t] && cok ? f2[base + boff[t]] : 0.0f;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                if (t < ntw)
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b[t], acc[t], 0, 0, 0);
+        };
+        for (int c0 = 0; c0 < cmain; c0 += 32) {
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                step(c0 + 4 * s + kq, false);
+        }
+        for (int c0 = cmain; c0 < C; c0 += 4)
+            step(c0 + kq, true);
+        /* Products to LDS: lane l holds rows 4 (l / 16) + v of the tile's
+         * 16 x 16 block, column l % 16. */
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int tile = wv + 4 * t;
+
+            if (tile < nt)
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    G[(4 * (lane >> 4) + v) * LC_GS + tile * 16 + (lane & 15)] = acc[t][v];
+        }
+    }
+    else if (!tiled) {
+        /* Per-cell path: wave wv takes cells wv, wv + 4, ...; S of cell m
+         * over its own window goes to row m of G. */
+        for (int m = wv; m < LC_T; m += 4) {
+            const int i = cid[m];
+            float a4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            int off[4];
+            bool ok[4];
+
+            if (i < 0 || !okc[m])
+                continue;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int e = lane + 64 * q;
+                const int yy = oy[m] + e / ps, xx = ox[m] + e % ps;
+
+                ok[q] = e < ps * ps && xx >= 0 && xx < W && yy >= 0 && yy < H;
+                off[q] = ok[q] ? yy * W + xx : 0;
+            }
+            for (int c = 0; c < C; c++) {
+                const float a = f1[(long long)c * n + i] * rc;
+                const float *p = f2 + (long long)c * n;
+
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (ok[q])
+                        a4[q] = fmaf(a, p[off[q]], a4[q]);
+            }
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                if (ok[q])
-                    acc[q] = fmaf(a, p[off[q]], acc[q]);
-        }
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int e = lane + 64 * q;
-
-            if (e < np)
-                S[w][e] = acc[q];
+                if (lane + 64 * q < ps * ps)
+                    G[m * LC_GS + lane + 64 * q] = a4[q];
         }
     }
     __syncthreads();
-    if (!active)
-        return;
-    for (int k = lane; k < side * side; k += 64) {
-        const int e0 = (k / side) * ps + k % side, e1 = e0 + ps;
-        const float *s = S[w];
+    /* Outputs: consecutive threads take consecutive cells of one offset. */
+    for (int idx = tid; idx < LC_T * side * side; idx += 256) {
+        const int m = idx & 15, k = idx >> 4;
+        const int i = cid[m];
 
-        out[(long long)(coff + k) * n + i] =
-            (1.0f - b.fy) * ((1.0f - b.fx) * s[e0] + b.fx * s[e0 + 1]) +
-            b.fy * ((1.0f - b.fx) * s[e1] + b.fx * s[e1 + 1]);
+        if (i < 0)
+            continue;
+        float v = 0.0f;
+
+        if (okc[m]) {
+            const int ky = k / side, kx = k - ky * side;
+            const int yy = oy[m] + ky, xx = ox[m] + kx;
+            const float fx = cfx[m], fy = cfy[m];
+            float s[4];
+
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int y = yy + (q >> 1), x = xx + (q & 1);
+
+                if (tiled)
+                    s[q] = x >= bx0 && x < bx0 + bw && y >= by0 && y < by0 + bh
+                               ? G[m * LC_GS + (y - by0) * bw + (x - bx0)]
+                               : 0.0f;
+                else
+                    s[q] = G[m * LC_GS + (ky + (q >> 1)) * ps + kx + (q & 1)];
+            }
+            v = (1.0f - fy) * ((1.0f - fx) * s[0] + fx * s[1]) +
+                fy * ((1.0f - fx) * s[2] + fx * s[3]);
+        }
+        out[(long long)(coff + k) * n + i] = v;
     }
 }
 
@@ -430,8 +618,8 @@ extern "C" void roma_warp_sample(struct ops *o, cl_mem in, int C, int H, int W,
     need_floats(flow, 0, 2 * n, op, "flow");
     need_floats(out, (long long)coff * n, (long long)C * n, op, "out");
     prof_scope ps(o->ocl, op);
-    hipLaunchKernelGGL(warp_sample_kernel, dim3(nblk(n, 256)), dim3(256), 0,
-                       stream_of(o->ocl), cfptr(in), C, H, W, cfptr(flow),
+    hipLaunchKernelGGL(warp_sample_kernel, dim3(nblk(n, 256), nblk(C, WS_CG)), dim3(256),
+                       0, stream_of(o->ocl), cfptr(in), C, H, W, cfptr(flow),
                        fptr(out), coff);
     launch_check(op);
     ICOREG_API_END
@@ -450,13 +638,17 @@ extern "C" void roma_local_corr(struct ops *o, cl_mem f1, cl_mem f2, int C,
         icoreg_fatal("%s: invalid sizes C=%d r=%d (C <= %d, r <= 7)", op, C, r,
                      CORR_MAXC);
     count32((long long)(coff + (2 * r + 1) * (2 * r + 1)) * n, op);
+    /* Byte offsets inside a 16-channel chunk stay below 2^31. */
+    if (n >= (1LL << 25))
+        icoreg_fatal("%s: %lld cells (at most 2^25)", op, n);
     need_floats(f1, 0, (long long)C * n, op, "f1");
     need_floats(f2, 0, (long long)C * n, op, "f2");
     need_floats(flow, 0, 2 * n, op, "flow");
     need_floats(out, (long long)coff * n, (long long)(2 * r + 1) * (2 * r + 1) * n,
                 op, "out");
     prof_scope ps(o->ocl, op);
-    hipLaunchKernelGGL(local_corr_kernel, dim3(nblk(n, 4)), dim3(256), 0,
+    hipLaunchKernelGGL(local_corr_kernel,
+                       dim3((unsigned)(((W + 3) / 4) * ((H + 3) / 4))), dim3(256), 0,
                        stream_of(o->ocl), cfptr(f1), cfptr(f2), C, H, W, r,
                        cfptr(flow), fptr(out), coff);
     launch_check(op);

@@ -201,3 +201,33 @@ def test_layernorm_shapes(shape, dev, ic, orc):
     got = dev.read(Y, rows * Cc)
     err = opcases.rel_err(got, ref)
     assert err <= 1e-5, f"{shape}: {err:.2e}"
+
+
+GS_SHAPES = [
+    (13, 20, 25, 777, 0),   # channel groups of 8 with a tail
+    (64, 48, 40, 3000, 1),
+    (512, 108, 108, 11664, 0),  # a refiner-sized map
+]
+
+
+@pytest.mark.parametrize("shape", GS_SHAPES, ids=[str(s) for s in GS_SHAPES])
+def test_grid_sample_shapes(shape, dev, ic, orc):
+    """grid_sample over many channels (the (point, channel-group) grid)
+    against the oracle, with points outside, on the border and
+    non-finite, both align_corners conventions."""
+    from oracle_lib import fp
+    Cc, H, W, n, align = shape
+    print(f"[grid_sample] {shape}", flush=True)
+    rng = np.random.default_rng(700 + Cc)
+    x = rng.standard_normal((Cc, H, W)).astype(np.float32)
+    g = rng.uniform(-1.2, 1.2, (n, 2)).astype(np.float32)
+    g[:4] = [[-1, -1], [1, 1], [np.nan, 0], [0, np.inf]]
+    g[4:8] = [[1e6, 0], [-3e9, 2], [1, -1], [-1, 1]]
+    ref = np.zeros(Cc * n, np.float32)
+    orc.orc_grid_sample(fp(x), Cc, H, W, fp(g), n, align, fp(ref))
+    X, Gd, Y = dev.upload(x), dev.upload(g), dev.zeros(Cc * n)
+    dev.api.ops_grid_sample(dev.po, X.mem, Cc, H, W, Gd.mem, n, align, Y.mem)
+    got = dev.read(Y, Cc * n)
+    assert np.isfinite(got).all()
+    err = opcases.rel_err(got, ref)
+    assert err <= 1e-5, f"{shape}: {err:.2e}"

@@ -40,6 +40,29 @@ def warps(rng, H, W):
     return np.ascontiguousarray(f.astype(np.float32))
 
 
+def smooth_warps(rng, H, W, outliers=True):
+    """A smooth warp (the identity plus a displacement of a few cells
+    varying slowly over the grid), as the refiners see, with a sprinkle
+    of broken cells (far off, non-finite) so that some 4 x 4 patches
+    scatter."""
+    gy = -1 + (2 * np.arange(H) + 1) / H
+    gx = -1 + (2 * np.arange(W) + 1) / W
+    gy, gx = np.meshgrid(gy, gx, indexing="ij")
+    ph = rng.uniform(0, 2 * np.pi, 4)
+    dx = 3.0 / W * (np.sin(2.1 * gy + ph[0]) + np.cos(1.7 * gx + ph[1]))
+    dy = 3.0 / H * (np.sin(1.3 * gx + ph[2]) + np.cos(2.5 * gy + ph[3]))
+    f = np.stack([gx + dx, gy + dy]) + 0.1 / max(H, W) * rng.standard_normal((2, H, W))
+    if outliers:
+        flat = f.reshape(2, -1)
+        k = rng.choice(H * W, 12, replace=False)
+        flat[:, k[:4]] *= 3.0
+        flat[0, k[4]] = 1e6
+        flat[1, k[5]] = np.nan
+        flat[0, k[6]] = -np.inf
+        flat[:, k[7:12]] = rng.uniform(-1, 1, (2, 5))
+    return np.ascontiguousarray(f.astype(np.float32))
+
+
 def test_row_norm_cos_exp(dev, ic, orc):
     print("[roma] row_norm / cos_exp", flush=True)
     rng = np.random.default_rng(31)
@@ -81,12 +104,14 @@ def test_cls_to_flow(dev, ic, orc, res, n):
     assert np.array_equal(dev.read(bc), cert)
 
 
-@pytest.mark.parametrize("C,H,W", [(3, 37, 45), (64, 70, 70)])
-def test_warp_sample(dev, ic, orc, C, H, W):
+@pytest.mark.parametrize("C,H,W,smooth", [(3, 37, 45, False), (64, 70, 70, False),
+                                          (13, 31, 17, True), (512, 108, 108, True),
+                                          (9, 432, 432, True)])
+def test_warp_sample(dev, ic, orc, C, H, W, smooth):
     print(f"[roma] warp_sample C={C} {H}x{W}", flush=True)
     rng = np.random.default_rng(C)
     x = rng.standard_normal((C, H, W)).astype(np.float32)
-    f = warps(rng, H, W)
+    f = smooth_warps(rng, H, W) if smooth else warps(rng, H, W)
     n = H * W
     ref = np.zeros((C + 1, n), np.float32)
     orc.orc_roma_warp_sample(fp(x), C, H, W, fp(f), fp(ref), 1)
@@ -95,17 +120,28 @@ def test_warp_sample(dev, ic, orc, C, H, W):
     dev.api.roma_warp_sample(dev.po, bx.mem, C, H, W, bf.mem, out.mem, 1)
     got = dev.read(out).reshape(C + 1, n)
     assert np.all(got[0] == 7.0)
-    assert rel(got[1:], ref[1:]) < TOL
+    # The element-wise bar (1e-4): the pixel coordinate ((x + 1) W - 1) / 2
+    # is rounded differently where the compiler fuses its multiply-add
+    # (the oracle's x86 build does not), about 1 ulp of a coordinate of
+    # up to 432, which moves a sample by its gradient times that.
+    assert rel(got[1:], ref[1:]) < 1e-4
 
 
-@pytest.mark.parametrize("C,H,W,r", [(512, 35, 35, 7), (1024, 20, 27, 3),
-                                     (256, 70, 70, 2), (24, 9, 13, 7)])
-def test_local_corr(dev, ic, orc, C, H, W, r):
-    print(f"[roma] local_corr C={C} {H}x{W} r={r}", flush=True)
+@pytest.mark.parametrize("C,H,W,r,smooth", [(512, 35, 35, 7, False), (1024, 20, 27, 3, False),
+                                            (256, 70, 70, 2, False), (24, 9, 13, 7, False),
+                                            (512, 35, 37, 3, True), (100, 23, 30, 2, True),
+                                            (7, 13, 9, 1, True), (64, 21, 19, 7, True),
+                                            (512, 108, 108, 3, True), (256, 216, 216, 2, True)])
+def test_local_corr(dev, ic, orc, C, H, W, r, smooth):
+    """Random warps (most 4 x 4 patches scatter: the per-cell path) and
+    smooth ones (the matrix-core path over the patch's window box, with a
+    few broken cells), up to the refiner config's 1/8 and 1/4 shapes at
+    864 x 864."""
+    print(f"[roma] local_corr C={C} {H}x{W} r={r} smooth={smooth}", flush=True)
     rng = np.random.default_rng(C + r)
     f0 = rng.standard_normal((C, H, W)).astype(np.float32)
     f1 = rng.standard_normal((C, H, W)).astype(np.float32)
-    f = warps(rng, H, W)
+    f = smooth_warps(rng, H, W) if smooth else warps(rng, H, W)
     n, K = H * W, (2 * r + 1) ** 2
     ref = np.zeros((K + 2, n), np.float32)
     orc.orc_roma_local_corr(fp(f0), fp(f1), C, H, W, r, fp(f), fp(ref), 2)
