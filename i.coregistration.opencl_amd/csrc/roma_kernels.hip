@@ -213,34 +213,27 @@ __global__ void __launch_bounds__(256)
  * warp have overlapping windows, so the union of the patch's windows
  * (clipped to the image) is a box of about (4 + 2 r + 1)^2 cells instead
  * of 16 (2 r + 2)^2 reads. When the box holds at most LC_NB cells, the
- * block brings, for 16 channels at a time, the patch's f1 columns and
- * the box's f2 columns into LDS by LDS DMA (buffer_load ... lds: no
- * register staging; box slots past the box and channels past C load as
- * zeros from outside the buffer window), the next chunk in flight while
- * the current one is used, one barrier per chunk, and forms every
- * patch-cell x box-cell product on the matrix cores
+ * block forms every patch-cell x box-cell product on the matrix cores
  * (v_mfma_f32_16x16x4f32: 16 cells x 16 box cells x 4 channels, box
- * tiles shared out over the 4 waves). Each cell then reads its window's
- * products from the box. Patches whose windows scatter (far-off or
- * broken warps) take the per-cell path instead: one wave per cell, lanes
- * over the window cells, channels in order. Patches go to the XCDs in
- * contiguous bands, so that neighbouring patches share their f2 rows in
- * one L2. */
+ * tiles shared out over the 4 waves), each wave streaming its operands
+ * from memory straight into registers with no LDS staging and no
+ * barriers (32 channels of loads in flight per wave). Each cell then
+ * reads its window's products from the box. Patches whose windows
+ * scatter (far-off or broken warps) take the per-cell path instead: one
+ * wave per cell, lanes over the window cells, channels in order.
+ * Patches go to the XCDs in contiguous bands, so that neighbouring
+ * patches share their f2 rows in one L2.
+ *
+ * Measured at 864 x 864 (1/8: C = 512, r = 3; 1/4: C = 256, r = 2) the
+ * kernel is bound by L1 misses (each 4 x 4 patch touches its box rows
+ * channel by channel, 16-44 bytes of every 128-byte line), not by HBM or
+ * the matrix cores. */
 #define CORR_MAXC 1024 /* channels accepted (the reference's kernel: 512) */
 #define LC_T 16        /* cells of a patch (4 x 4) */
 #define LC_NB 256      /* box cells on the matrix-core path */
-#define LC_KC 16       /* channels per LDS chunk */
-#define LC_PMAX 272    /* largest LDS row pitch of a box chunk */
 #define LC_GS 260      /* LDS row pitch of the products */
-#define LC_OOB 0x80000000u
-#define LC_WAIT_VM0 0x0F70 /* s_waitcnt vmcnt(0) */
 
 typedef float lc_f4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t lc_window(const float *p, unsigned bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)bytes, 0x00020000);
-}
 
 /* Block L of T to a tile: the 8 XCDs (blocks L, L + 8, ... on XCD L % 8)
  * each get a contiguous band of tiles. */
