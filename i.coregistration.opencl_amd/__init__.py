@@ -123,6 +123,7 @@ SIGNATURES = {
     "ops_layernorm": (None, [_O, _L, _I, Mem, Mem, Mem, Mem, _F, _I, _F]),
     "ops_softmax_rows": (None, [_O, Mem, _L, _I, _F]),
     "ops_attention": (None, [_O, Opnd, Opnd, Opnd, Opnd, _I, _I, _I, _I, _F, Mem]),
+    "ops_attention_noalloc": (None, [_O, Opnd, Opnd, Opnd, Opnd, _I, _I, _I, _I, _F, Mem]),
     "ops_attention_batch": (None, [_O, _I, Opnd, _L, Opnd, _L, Opnd, _L, Opnd, _L, _I,
                                    _I, _I, _I, _F, Mem]),
     "ops_rope": (None, [_O, Mem, _L, _I, _L, _I, _I, _I, Mem, _I]),

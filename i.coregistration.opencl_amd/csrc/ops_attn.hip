@@ -32,6 +32,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include <math.h>
 
 #include "common.h"
@@ -450,12 +452,16 @@ __global__ void __launch_bounds__(256)
                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
+/* Partials of the key splits: the ops work buffer (grown on demand), or,
+ * for ops_attention_noalloc, the fixed device array `fixed` of
+ * fixed_bytes bytes (too small a one is a fatal error). */
 template <int ND, bool VEC, bool MASK>
 static void launch_nd(struct ops *ops, hipStream_t st, int nb, int nh,
                       const float *Q, int ldq, long long bq, const float *K,
                       int ldk, long long bk, const float *V, int ldv,
                       long long bv, float *O, int ldo, long long bo, int Nq,
-                      int Nk, int d, float scale, const unsigned char *kmask)
+                      int Nk, int d, float scale, const unsigned char *kmask,
+                      float *fixed, size_t fixed_bytes)
 {
     const int qb = (Nq + 32 * ATT_NW - 1) / (32 * ATT_NW);
     const int ntiles = (Nk + ATT_KT - 1) / ATT_KT;
@@ -499,9 +505,18 @@ static void launch_nd(struct ops *ops, hipStream_t st, int nb, int nh,
     {
         const size_t rows = (size_t)nsplit * nb * nh * Nq;
         const size_t ob = rows * 32 * ND * sizeof(float);
-        cl_mem sc = scratch_get(ops, ob + rows * sizeof(float2));
-        float *po = (float *)sc->ptr;
-        float2 *pml = (float2 *)((char *)sc->ptr + ob);
+        float *po;
+
+        if (fixed) {
+            if (ob + rows * sizeof(float2) > fixed_bytes)
+                icoreg_fatal("ops_attention_noalloc: the key-split partials (%zu bytes) "
+                             "exceed the %zu-byte scratch array",
+                             ob + rows * sizeof(float2), fixed_bytes);
+            po = fixed;
+        }
+        else
+            po = (float *)scratch_get(ops, ob + rows * sizeof(float2))->ptr;
+        float2 *pml = (float2 *)((char *)po + ob);
         const long long total = (long long)nb * Nq * nh * d;
 
         hipLaunchKernelGGL((attention_kernel<ND, VEC, MASK>),
@@ -539,7 +554,8 @@ static void attention_impl(struct ops *o, const char *op, int nb,
                            struct opnd Q, long long bq, struct opnd K,
                            long long bk, struct opnd V, long long bv,
                            struct opnd O, long long bo, int Nq, int Nk, int nh,
-                           int d, float scale, cl_mem kmask)
+                           int d, float scale, cl_mem kmask, float *fixed = nullptr,
+                           size_t fixed_bytes = 0)
 {
     hipStream_t st = stream_of(o->ocl);
 
@@ -563,7 +579,8 @@ static void attention_impl(struct ops *o, const char *op, int nb,
 #define ARGS                                                                   \
     o, st, nb, nh, cfptr(Q.buf) + Q.off, Q.ld, bq, cfptr(K.buf) + K.off, K.ld, \
         bk, cfptr(V.buf) + V.off, V.ld, bv, fptr(O.buf) + O.off, O.ld, bo, Nq, \
-        Nk, d, scale, kmask ? (const unsigned char *)kmask->ptr : nullptr
+        Nk, d, scale, kmask ? (const unsigned char *)kmask->ptr : nullptr, fixed,   \
+        fixed_bytes
     {
         /* 16-byte K / V loads when every row and head start is aligned. */
         const bool vec = d % 4 == 0 && K.ld % 4 == 0 && V.ld % 4 == 0 &&
@@ -603,6 +620,51 @@ extern "C" void ops_attention(struct ops *o, struct opnd Q, struct opnd K,
     ICOREG_API_BEGIN
     attention_impl(o, "ops_attention", 1, Q, 0, K, 0, V, 0, O, 0, Nq, Nk, nh,
                    d, scale, kmask);
+    ICOREG_API_END
+}
+
+/* ---- ops_attention without allocation ------------------------------------------ */
+
+/* The key-split partials of ops_attention_noalloc: a fixed array per
+ * GPU, held until the process ends, shared by every call on that GPU. */
+#define ATT_NOALLOC_BYTES ((size_t)64 << 20)
+static __device__ __align__(256) float scratch[ATT_NOALLOC_BYTES / sizeof(float)];
+
+/* scratch's device address on each GPU (hipGetSymbolAddress once per
+ * device, with that device current); the host symbol is only a
+ * stand-in and is never handed to a kernel or a copy. */
+static float *scratch_dev[64];
+static std::mutex scratch_mu;
+
+static float *noalloc_scratch(void)
+{
+    int dev = -1;
+    float *p;
+
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= 64)
+        icoreg_fatal("ops_attention_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(scratch_mu);
+    if (!scratch_dev[dev]) {
+        p = nullptr;
+        hip_check(hipGetSymbolAddress((void **)&p, HIP_SYMBOL(scratch)),
+                  "hipGetSymbolAddress(scratch)");
+        if (!p)
+            icoreg_fatal("ops_attention_noalloc: no device address for the scratch array");
+        scratch_dev[dev] = p;
+    }
+    return scratch_dev[dev];
+}
+
+extern "C" void ops_attention_noalloc(struct ops *o, struct opnd Q, struct opnd K,
+                                      struct opnd V, struct opnd O, int Nq, int Nk,
+                                      int nh, int d, float scale, cl_mem kmask)
+{
+    ICOREG_API_BEGIN
+    float *p = noalloc_scratch();
+
+    attention_impl(o, "ops_attention_noalloc", 1, Q, 0, K, 0, V, 0, O, 0, Nq, Nk, nh,
+                   d, scale, kmask, p, ATT_NOALLOC_BYTES);
     ICOREG_API_END
 }
 

@@ -148,6 +148,18 @@ void ops_attention(struct ops *o, struct opnd Q, struct opnd K, struct opnd V,
                    struct opnd O, int Nq, int Nk, int nh, int d, float scale,
                    cl_mem kmask);
 
+/* ops_attention that allocates nothing: the key-split partials go to a
+ * fixed 64 MiB device array (one per GPU, held until the process ends)
+ * instead of the ops work buffer, which ops_attention grows with
+ * hipMalloc. No counterpart in the reference; for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops). Same results as ops_attention. A problem whose partials
+ * exceed 64 MiB is a fatal error. Every call on one GPU shares the
+ * array: calls that overlap on one GPU (other streams or threads) race. */
+void ops_attention_noalloc(struct ops *o, struct opnd Q, struct opnd K,
+                           struct opnd V, struct opnd O, int Nq, int Nk, int nh,
+                           int d, float scale, cl_mem kmask);
+
 /* ops_attention on nb independent problems in one launch, problem i's Q,
  * K, V and O starting bq, bk, bv, bo floats after problem i - 1's (kmask
  * shared). No counterpart in the reference, which loops over the images
