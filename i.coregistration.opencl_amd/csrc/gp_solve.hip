@@ -8,17 +8,20 @@
  * a host Cholesky of n = 1600 and a write per tile pair; here the same
  * arithmetic stays on the GPU.
  *
- * Blocked right-looking Cholesky with 64-column panels:
- *  - chol_diag: the 64 x 64 diagonal block factored in LDS by one
- *    work-group, and its triangular inverse Linv formed there too;
- *  - the panel below it, L21 = A21 Linv^T, and the trailing update
- *    A22 -= L21 L21^T (lower tiles only) are both fp64 GEMMs;
- *  - the two triangular solves run block by block the same way: a block
- *    of rows times Linv (or Linv^T), then a GEMM update of the rows still
- *    to solve.
+ * Blocked right-looking Cholesky with 64-column panels, the forward solve
+ * carried along as extra columns:
+ *  - chol_diag: the 64 x 64 diagonal block factored and its factor
+ *    inverted in LDS by one work-group, one barrier per column;
+ *  - one launch per panel for both L21 = A21 Linv^T and Y_b = Linv_b Z_b,
+ *    one for both the trailing update A22 -= L21 L21^T (lower tiles) and
+ *    Z_rest -= L21 Y_b (fp64 GEMM tiles, two problems per launch);
+ *  - the backward solve L^T X = Y from the last block: each launch
+ *    updates the rows above block b (Y[0:k] -= L[k:k+64, 0:k]^T X_b) and,
+ *    in the epilogue of the tiles of block b - 1, finishes that block
+ *    (X_{b-1} = Linv_{b-1}^T Y_{b-1}).
  * Working matrices: A (n x n, the trailing updates), L (n x n, the
- * factor), Linv per panel, Z and Y (n x d). Every GEMM reads one matrix
- * and writes another, so no launch reads what it writes. */
+ * factor), Linv per panel, Z and Y (n x d). No launch reads what it
+ * writes. About 4 launches per panel (n = 1600: 102). */
 
 #include <hip/hip_runtime.h>
 
@@ -35,7 +38,10 @@ using namespace icoreg;
 
 /* C = alpha A B + beta C with A(i, q) = A[i a_ri + q a_rk], B(q, j) =
  * B[q b_rk + j b_rj], C(i, j) = C[i c_ri + j]; lower: skip output tiles
- * strictly above the diagonal. */
+ * strictly above the diagonal. With linv set (the backward solve's
+ * epilogue), the output tiles of tile row epi_row are also multiplied by
+ * linv^T (GP_NB x GP_NB, row-major) and the product stored at X (row
+ * stride x_ri, same rows and columns as C). */
 struct dg_args {
     int M, N, K;
     const double *A;
@@ -46,31 +52,60 @@ struct dg_args {
     long long c_ri;
     double alpha;
     int beta, lower;
+    const double *linv;
+    int epi_row;
+    double *X;
+    long long x_ri;
 };
 
-__global__ void __launch_bounds__(256) dgemm_kernel(dg_args a)
+/* Up to two independent problems per launch: blockIdx.z picks one. */
+struct dg_pair {
+    dg_args p[2];
+};
+
+__global__ void __launch_bounds__(256) dgemm_kernel(dg_pair pr)
 {
-    __shared__ double As[DG_K][DG_T + 1], Bs[DG_K][DG_T + 1];
+    /* The two operand chunks; the backward-solve epilogue reuses both as
+     * one 64 x 65 tile. */
+    __shared__ double sm[2][DG_K][DG_T + 1];
+    __shared__ double lvs[GP_NB * GP_NB]; /* the epilogue's linv */
+    double(*As)[DG_T + 1] = sm[0], (*Bs)[DG_T + 1] = sm[1];
+    const dg_args &a = pr.p[blockIdx.z];
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     const int i0 = blockIdx.y * DG_T, j0 = blockIdx.x * DG_T;
-    double acc[4][4];
+    const bool epi = a.linv && (int)blockIdx.y == a.epi_row;
+    double acc[4][4], cprev[4][4];
 
-    if (a.lower && j0 > i0 + DG_T - 1)
+    if (i0 >= a.M || j0 >= a.N || (a.lower && j0 > i0 + DG_T - 1))
         return;
+    /* The accumulated C and the epilogue's linv are read at the start, so
+     * that their latency overlaps the products. */
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int i = min(i0 + ty + 16 * p, a.M - 1), j = min(j0 + tx + 16 * r, a.N - 1);
+
+            cprev[p][r] = a.beta ? a.C[(long long)i * a.c_ri + j] : 0.0;
+        }
+    if (epi)
+        for (int e = tid; e < GP_NB * GP_NB; e += 256)
+            lvs[e] = a.linv[e];
 #pragma unroll
     for (int p = 0; p < 4; p++)
 #pragma unroll
         for (int q = 0; q < 4; q++)
             acc[p][q] = 0.0;
-    for (int k0 = 0; k0 < a.K; k0 += DG_K) {
-        /* 32 x 64 of A and of B, 8 values per thread, the unit-stride
-         * index fastest across threads. Every load reads a valid address
-         * (indices clamped to the last row / column) and the value is
-         * selected afterwards, so that the 16 loads are all in flight
-         * together instead of one per guarded branch. */
-        double va[8], vb[8];
-        bool oka[8], okb[8];
+    /* 32 x 64 of A and of B per chunk, 8 values per thread, the
+     * unit-stride index fastest across threads. Every load reads a valid
+     * address (indices clamped to the last row / column) and the value is
+     * selected afterwards, so that the 16 loads are all in flight together;
+     * the next chunk's loads are issued before the current chunk's
+     * products. */
+    double va[8], vb[8];
+    bool oka[8], okb[8];
 
+    auto fetch = [&](int k0) {
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const int e = tid + 256 * t;
@@ -86,6 +121,9 @@ __global__ void __launch_bounds__(256) dgemm_kernel(dg_args a)
             vb[t] = a.B[(long long)min(k0 + qb, a.K - 1) * a.b_rk +
                         (long long)min(j0 + j, a.N - 1) * a.b_rj];
         }
+    };
+    fetch(0);
+    for (int k0 = 0; k0 < a.K; k0 += DG_K) {
 #pragma unroll
         for (int t = 0; t < 8; t++) {
             const int e = tid + 256 * t;
@@ -98,6 +136,8 @@ __global__ void __launch_bounds__(256) dgemm_kernel(dg_args a)
             Bs[qb][j] = okb[t] ? vb[t] : 0.0;
         }
         __syncthreads();
+        if (k0 + DG_K < a.K)
+            fetch(k0 + DG_K);
 #pragma unroll 8
         for (int q = 0; q < DG_K; q++) {
             double av[4], bv[4];
@@ -126,12 +166,72 @@ __global__ void __launch_bounds__(256) dgemm_kernel(dg_args a)
             const int j = j0 + tx + 16 * r;
 
             if (j < a.N) {
-                double *c = a.C + (long long)i * a.c_ri + j;
+                const double v = a.alpha * acc[p][r] + cprev[p][r];
 
-                *c = a.alpha * acc[p][r] + (a.beta ? *c : 0.0);
+                a.C[(long long)i * a.c_ri + j] = v;
+                acc[p][r] = v;
             }
         }
     }
+    /* Backward-solve epilogue: X = linv^T T for this tile T (a full
+     * 64-row block: the rows of the block being finished). */
+    if (epi) {
+        double(*T)[DG_T + 1] = sm[0]; /* rows 0..63 run on through sm[1] */
+
+#pragma unroll
+        for (int p = 0; p < 4; p++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                T[ty + 16 * p][tx + 16 * r] = acc[p][r];
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < 4; p++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                acc[p][r] = 0.0;
+        /* X[i][j] = sum_{q >= i} linv[q][i] T[q][j]. */
+#pragma unroll 8
+        for (int q = 0; q < GP_NB; q++) {
+            double lv[4], tv[4];
+
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const int i = ty + 16 * p;
+
+                lv[p] = q >= i ? lvs[q * GP_NB + i] : 0.0;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                tv[r] = T[q][tx + 16 * r];
+#pragma unroll
+            for (int p = 0; p < 4; p++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    acc[p][r] = fma(lv[p], tv[r], acc[p][r]);
+        }
+#pragma unroll
+        for (int p = 0; p < 4; p++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int j = j0 + tx + 16 * r;
+
+                if (j < a.N)
+                    a.X[(long long)(i0 + ty + 16 * p) * a.x_ri + j] = acc[p][r];
+            }
+    }
+}
+
+/* ---- the diagonal block ------------------------------------------------------------ */
+
+/* 1 / sqrt(x) from the hardware estimate and two Newton steps (each
+ * doubles the correct bits). */
+__device__ __forceinline__ double rsqrt_nr(double x)
+{
+    double r = __builtin_amdgcn_rsq(x);
+
+    r = r * fma(-0.5 * x * r, r, 1.5);
+    r = r * fma(-0.5 * x * r, r, 1.5);
+    return r;
 }
 
 /* Cholesky factor of the nb x nb diagonal block at (k, k) of A (n x n)
@@ -140,101 +240,128 @@ __global__ void __launch_bounds__(256) dgemm_kernel(dg_args a)
  * first column whose pivot is not positive (the factor then holds NaN
  * from there on).
  *
- * LDS holds the block: its lower triangle becomes L, its strictly upper
- * triangle holds the inverse transposed (Linv[r][c] at s[c][r], c < r,
- * starting as the identity's zeros), the inverse's diagonal is dinv.
- * Column j: one wave takes the pivot's square root and divides column j
- * below it (L) and above it (row j of the inverse, in transposed
- * storage) by it; then every thread updates the cells it owns (rows
- * ty + 16 a, columns tx + 16 b): the trailing lower triangle of A
+ * LDS holds the block: its lower triangle the trailing matrix, its
+ * strictly upper triangle the inverse transposed (Linv[r][c] at s[c][r],
+ * c < r, starting as the identity's zeros). Column j is used unscaled:
+ * every thread reads the pivot, forms r = 1 / sqrt(pivot) itself and
+ * scales the column values it reads (L[x][j] = r s[x][j] below the
+ * pivot, Linv[j][x] = r s[x][j] above it), so no pass writes column j
+ * back and one barrier per column separates the steps. The threads that
+ * own column j's cells put the finished column into f (same layout,
+ * another array; written to L and Linv at the end, so that no global
+ * store sits before a barrier). 1024 threads, 4 cells each (rows
+ * ty + 32 a, columns tx + 32 b), so that every SIMD holds 4 waves to hide
+ * the latency of the short per-column chain; each thread updates its
+ * cells branch-free and writes all of them back (a cell of column j is
+ * written back unchanged by its only owner): the trailing lower triangle
  * (A[r][c] -= L[r][j] L[c][j], c > j) and the inverse's rows below j
- * (B[r][c] -= L[r][j] Linv[j][c], c <= j), branch-free so that all its
- * LDS reads issue together. */
-__global__ void __launch_bounds__(256)
+ * (Linv[c][r] -= L[c][j] Linv[j][r], r <= j < c). */
+__global__ void __launch_bounds__(1024)
     chol_diag_kernel(const double *__restrict__ A, double *__restrict__ L,
                      double *__restrict__ Linv, int n, int k, int nb,
                      int *__restrict__ info)
 {
-    __shared__ double s[GP_NB][GP_NB + 1];
+    __shared__ double s[GP_NB][GP_NB + 1], f[GP_NB][GP_NB + 1];
     __shared__ double dinv[GP_NB];
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int tid = threadIdx.x, tx = tid & 31, ty = tid >> 5;
 
     {
-        double v[16];
+        double v[4];
 
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int e = tid + 256 * i, r = e >> 6, c = e & 63;
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 1024 * i, r = e >> 6, c = e & 63;
 
             v[i] = A[(long long)(k + min(r, nb - 1)) * n + k + min(c, nb - 1)];
         }
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int e = tid + 256 * i, r = e >> 6, c = e & 63;
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 1024 * i, r = e >> 6, c = e & 63;
 
             s[r][c] = r < nb && c <= r ? v[i] : 0.0;
         }
     }
     __syncthreads();
-    for (int j = 0; j < nb; j++) {
-        if (tid < 64) {
-            const double d = s[j][j];
-            /* 1 / sqrt(d) from the hardware estimate and two Newton
-             * steps (each doubles the correct bits), then sqrt(d) = d r:
-             * no division or square-root sequence on the column chain. */
-            double r = __builtin_amdgcn_rsq(d);
+    /* Two columns per step (j and j1 = j + 1, one barrier): every thread
+     * forms both pivots' roots itself (the second from the first's
+     * update of s[j1][j1]) and the two columns' values it needs, then
+     * applies both rank-one updates to its cells at once. */
+    for (int j = 0; j < nb; j += 2) {
+        const int j1 = j + 1;
+        const bool two = j1 < nb;
+        const double piv0 = s[j][j];
+        const double r0 = rsqrt_nr(piv0);
+        const double l10 = two ? s[j1][j] * r0 : 0.0;
+        const double piv1 = two ? fma(-l10, l10, s[j1][j1]) : 1.0;
+        const double r1 = two ? rsqrt_nr(piv1) : 0.0;
+        /* u, w: column j and j1 values at index x: L below the pivot,
+         * the inverse's rows j and j1 above it. */
+        auto uw = [&](int x, double &u, double &w) {
+            const double sj = s[x][j], sj1 = two ? s[x][j1] : 0.0;
 
-            r = r * fma(-0.5 * d * r, r, 1.5);
-            r = r * fma(-0.5 * d * r, r, 1.5);
-            if (tid == 0 && !(d > 0.0) && *info == 0)
-                *info = k + j + 1;
-            if (tid == j) {
-                s[j][j] = d * r;
-                dinv[j] = r;
-            }
-            else if (tid < nb)
-                s[tid][j] *= r;
+            u = x == j ? piv0 * r0 : sj * r0;
+            w = !two ? 0.0 : x == j1 ? piv1 * r1 : x == j ? -l10 * r0 * r1 : (sj1 - u * l10) * r1;
+        };
+        double ur[2], wr[2], uc[2], wc[2], v[2][2];
+
+        if (tid == 0 && *info == 0 && (!(piv0 > 0.0) || (two && !(piv1 > 0.0))))
+            *info = k + (piv0 > 0.0 ? j1 : j) + 1;
+#pragma unroll
+        for (int a2 = 0; a2 < 2; a2++) {
+            uw(ty + 32 * a2, ur[a2], wr[a2]);
+            uw(tx + 32 * a2, uc[a2], wc[a2]);
         }
-        __syncthreads();
-        {
-            const double dj = dinv[j];
-            double lr[4], lc[4], v[4][4];
-
 #pragma unroll
-            for (int a4 = 0; a4 < 4; a4++) {
-                lr[a4] = s[ty + 16 * a4][j];
-                lc[a4] = s[tx + 16 * a4][j];
-            }
+        for (int a2 = 0; a2 < 2; a2++)
 #pragma unroll
-            for (int a4 = 0; a4 < 4; a4++)
+            for (int b2 = 0; b2 < 2; b2++)
+                v[a2][b2] = s[ty + 32 * a2][tx + 32 * b2];
+        /* The finished columns (f holds L and the inverse transposed, the
+         * same layout as s). */
+        if (tx == (j & 31)) {
 #pragma unroll
-                for (int b4 = 0; b4 < 4; b4++)
-                    v[a4][b4] = s[ty + 16 * a4][tx + 16 * b4];
-#pragma unroll
-            for (int a4 = 0; a4 < 4; a4++)
-#pragma unroll
-                for (int b4 = 0; b4 < 4; b4++) {
-                    const int r = ty + 16 * a4, c = tx + 16 * b4;
-                    /* lower: factor update; upper (r < c): inverse cell
-                     * (c, r), updated for r <= j < c. */
-                    const bool low = r < nb && c > j && c <= r;
-                    const bool inv = c < nb && r <= j && j < c;
-                    const double f = r == j ? dj : lr[a4];
-
-                    s[r][c] = low ? fma(-lr[a4], lc[b4], v[a4][b4])
-                              : inv ? fma(-lc[b4], f, v[a4][b4])
-                                    : v[a4][b4];
-                }
+            for (int a2 = 0; a2 < 2; a2++)
+                f[ty + 32 * a2][j] = ur[a2];
+            if (ty == 0)
+                dinv[j] = r0;
         }
+        if (two && tx == (j1 & 31)) {
+#pragma unroll
+            for (int a2 = 0; a2 < 2; a2++)
+                f[ty + 32 * a2][j1] = wr[a2];
+            if (ty == 0)
+                dinv[j1] = r1;
+        }
+        const int jl = two ? j1 : j; /* the last column of the step */
+#pragma unroll
+        for (int a2 = 0; a2 < 2; a2++)
+#pragma unroll
+            for (int b2 = 0; b2 < 2; b2++) {
+                const int r = ty + 32 * a2, c = tx + 32 * b2;
+                /* lower: factor update by both columns; upper (r < c):
+                 * inverse cell (c, r) for r <= jl < c, by the inverse's
+                 * rows j (p, zero at r = j1) and j1 (q). */
+                const bool low = r < nb && c > jl && c <= r;
+                const bool inv = c < nb && r <= jl && jl < c;
+                const double p = r == j ? r0 : r < j ? ur[a2] : 0.0;
+                const double q = r == j1 ? r1 : wr[a2];
+                double x = v[a2][b2];
+
+                if (low)
+                    x = fma(-ur[a2], uc[b2], fma(-wr[a2], wc[b2], x));
+                else if (inv)
+                    x = fma(-uc[b2], p, fma(-wc[b2], q, x));
+                s[r][c] = x;
+            }
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const int e = tid + 256 * i, r = e >> 6, c = e & 63;
+    for (int i = 0; i < 4; i++) {
+        const int e = tid + 1024 * i, r = e >> 6, c = e & 63;
 
         if (r < nb && c < nb) {
-            L[(long long)(k + r) * n + k + c] = c <= r ? s[r][c] : 0.0;
-            Linv[r * GP_NB + c] = r == c ? dinv[c] : r > c ? s[c][r] : 0.0;
+            L[(long long)(k + r) * n + k + c] = c <= r ? f[r][c] : 0.0;
+            Linv[r * GP_NB + c] = r == c ? dinv[c] : r > c ? f[c][r] : 0.0;
         }
     }
 }
@@ -269,14 +396,33 @@ __global__ void __launch_bounds__(256)
         F[idx] = (float)X[idx];
 }
 
-static void dgemm(const dg_args &a, hipStream_t s)
+static dg_args dg(int M, int N, int K, const double *A, long long a_ri, long long a_rk,
+                  const double *B, long long b_rk, long long b_rj, double *C,
+                  long long c_ri, double alpha, int beta, int lower)
 {
-    if (a.M <= 0 || a.N <= 0)
+    dg_args a = {M, N, K, A, a_ri, a_rk, B, b_rk, b_rj, C, c_ri, alpha, beta, lower,
+                 nullptr, -1, nullptr, 0};
+
+    return a;
+}
+
+/* One launch for p0 and, when np = 2, p1 (problems with no output are
+ * skipped). */
+static void dgemm(hipStream_t s, const dg_args &p0, const dg_args *p1 = nullptr)
+{
+    dg_pair pr;
+    int np = 0, tx = 0, ty = 0;
+
+    for (const dg_args *a : {&p0, p1})
+        if (a && a->M > 0 && a->N > 0) {
+            pr.p[np++] = *a;
+            tx = max(tx, (a->N + DG_T - 1) / DG_T);
+            ty = max(ty, (a->M + DG_T - 1) / DG_T);
+        }
+    if (np == 0)
         return;
-    hipLaunchKernelGGL(dgemm_kernel,
-                       dim3((unsigned)((a.N + DG_T - 1) / DG_T),
-                            (unsigned)((a.M + DG_T - 1) / DG_T)),
-                       dim3(256), 0, s, a);
+    hipLaunchKernelGGL(dgemm_kernel, dim3((unsigned)tx, (unsigned)ty, (unsigned)np),
+                       dim3(256), 0, s, pr);
 }
 
 extern "C" size_t roma_gp_work_bytes(int n, int d)
@@ -319,60 +465,49 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
         hipLaunchKernelGGL(gp_init_kernel, dim3((unsigned)((tot + 255) / 256)),
                            dim3(256), 0, s, cfptr(K), n, (double)noise, A,
                            cfptr(F), nd, Z, (int *)info->ptr);
+        /* Factor panel by panel; Y = L^-1 Z alongside. */
         for (int b = 0; b < nblk; b++) {
             const int k = b * GP_NB, nb = n - k < GP_NB ? n - k : GP_NB;
             const int rest = n - k - nb;
             double *Lk = Li + (long long)b * GP_NB * GP_NB;
-            dg_args g;
+            double *L21 = L + (long long)(k + nb) * n + k;
 
-            hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(256), 0, s, A,
-                               L, Lk, n, k, nb, (int *)info->ptr);
+            hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(1024), 0, s, A, L, Lk, n, k,
+                               nb, (int *)info->ptr);
+            /* L21 = A21 Linv^T and Y_b = Linv_b Z_b. */
+            const dg_args panel = dg(rest, nb, nb, A + (long long)(k + nb) * n + k, n, 1,
+                                     Lk, 1, GP_NB, L21, n, 1.0, 0, 0);
+            const dg_args yb = dg(nb, d, nb, Lk, GP_NB, 1, Z + (long long)k * d, d, 1,
+                                  Y + (long long)k * d, d, 1.0, 0, 0);
+            dgemm(s, yb, &panel);
             if (rest == 0)
                 continue;
-            /* L21 = A21 Linv^T. */
-            g = dg_args{rest, nb, nb, A + (long long)(k + nb) * n + k, n, 1,
-                        Lk, 1, GP_NB, L + (long long)(k + nb) * n + k, n,
-                        1.0, 0, 0};
-            dgemm(g, s);
-            /* A22 -= L21 L21^T, lower tiles. */
-            g = dg_args{rest, rest, nb, L + (long long)(k + nb) * n + k, n, 1,
-                        L + (long long)(k + nb) * n + k, 1, n,
-                        A + (long long)(k + nb) * n + k + nb, n, -1.0, 1, 1};
-            dgemm(g, s);
+            /* A22 -= L21 L21^T (lower tiles) and Z_rest -= L21 Y_b. */
+            const dg_args trail = dg(rest, rest, nb, L21, n, 1, L21, 1, n,
+                                     A + (long long)(k + nb) * n + k + nb, n, -1.0, 1, 1);
+            const dg_args zr = dg(rest, d, nb, L21, n, 1, Y + (long long)k * d, d, 1,
+                                  Z + (long long)(k + nb) * d, d, -1.0, 1, 0);
+            dgemm(s, trail, &zr);
         }
-        /* L Y = Z, block by block. */
-        for (int b = 0; b < nblk; b++) {
-            const int k = b * GP_NB, nb = n - k < GP_NB ? n - k : GP_NB;
-            const int rest = n - k - nb;
-            dg_args g;
+        /* L^T X = Y from the last block; X goes to Z. The last block
+         * alone, then per block b: Y[0:k] -= L[k:k+nb, 0:k]^T X_b with
+         * block b - 1 finished in the epilogue. */
+        {
+            const int b = nblk - 1, k = b * GP_NB, nb = n - k;
 
-            g = dg_args{nb, d, nb, Li + (long long)b * GP_NB * GP_NB, GP_NB,
-                        1, Z + (long long)k * d, d, 1, Y + (long long)k * d,
-                        d, 1.0, 0, 0};
-            dgemm(g, s);
-            if (rest == 0)
-                continue;
-            g = dg_args{rest, d, nb, L + (long long)(k + nb) * n + k, n, 1,
-                        Y + (long long)k * d, d, 1,
-                        Z + (long long)(k + nb) * d, d, -1.0, 1, 0};
-            dgemm(g, s);
+            dgemm(s, dg(nb, d, nb, Li + (long long)b * GP_NB * GP_NB, 1, GP_NB,
+                        Y + (long long)k * d, d, 1, Z + (long long)k * d, d, 1.0, 0, 0));
         }
-        /* L^T X = Y, from the last block; X goes to Z (consumed). */
-        for (int b = nblk - 1; b >= 0; b--) {
+        for (int b = nblk - 1; b > 0; b--) {
             const int k = b * GP_NB, nb = n - k < GP_NB ? n - k : GP_NB;
-            dg_args g;
+            dg_args g = dg(k, d, nb, L + (long long)k * n, 1, n, Z + (long long)k * d, d, 1,
+                           Y, d, -1.0, 1, 0);
 
-            /* X_k = Linv^T Y_k: A(i, q) = Linv[q][i]. */
-            g = dg_args{nb, d, nb, Li + (long long)b * GP_NB * GP_NB, 1,
-                        GP_NB, Y + (long long)k * d, d, 1,
-                        Z + (long long)k * d, d, 1.0, 0, 0};
-            dgemm(g, s);
-            if (k == 0)
-                continue;
-            /* Y[0:k] -= L[k:k+nb, 0:k]^T X_k: A(i, q) = L[k + q][i]. */
-            g = dg_args{k, d, nb, L + (long long)k * n, 1, n,
-                        Z + (long long)k * d, d, 1, Y, d, -1.0, 1, 0};
-            dgemm(g, s);
+            g.linv = Li + (long long)(b - 1) * GP_NB * GP_NB;
+            g.epi_row = b - 1;
+            g.X = Z;
+            g.x_ri = d;
+            dgemm(s, g);
         }
         hipLaunchKernelGGL(gp_store_kernel, dim3((unsigned)((nd + 255) / 256)),
                            dim3(256), 0, s, Z, nd, fptr(F));

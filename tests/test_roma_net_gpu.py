@@ -41,7 +41,8 @@ def cos_kernel(rng, n, d=64):
     return np.exp((x @ x.T - 1) / 0.2).astype(np.float32)
 
 
-@pytest.mark.parametrize("n,d", [(1600, 512), (100, 512), (65, 7)])
+@pytest.mark.parametrize("n,d", [(1600, 512), (100, 512), (65, 7), (1, 3), (31, 5),
+                                 (32, 64), (33, 65), (64, 130), (127, 9), (200, 512)])
 def test_gp_solve(dev, ic, n, d):
     print(f"[roma] gp_solve n={n} d={d}", flush=True)
     rng = np.random.default_rng(n)
