@@ -1,13 +1,15 @@
 /* SPDX-License-Identifier: Unlicense */
 
 /* DISK driver on the HIP path: the U-Net of kornia.feature.DISK, heatmap
- * NMS, the host top-n selection and the descriptor gather, with the
- * layer plan, constants and order of operations of the reference
- * (disk.c:23-273 of i.coregistration.opencl), because the keypoints must
- * be the same. Every convolution is a 5 x 5, stride 1, pad 2 one-group
- * convolution, which ops_conv2d runs as the direct MFMA kernel with the
- * InstanceNorm + PReLU of the block applied to its input as it is
- * loaded. */
+ * NMS, top-n selection and descriptor gather, with the layer plan,
+ * constants and order of operations of the reference (disk.c:23-273 of
+ * i.coregistration.opencl), because the keypoints must be the same.
+ * Every convolution is a 5 x 5, stride 1, pad 2 one-group convolution,
+ * which ops_conv2d runs as the direct MFMA kernel with the InstanceNorm +
+ * PReLU of the block applied to its input as it is loaded. Unlike the
+ * reference, the down path writes its skip outputs straight into the up
+ * path's concatenation buffers, and the top-n selection runs on the
+ * device (disk_topn), so a detection syncs once, to read the keypoints. */
 
 #include <math.h>
 #include <stdlib.h>
@@ -86,24 +88,30 @@ extern "C" void disk_alloc(struct disk_model *m, int H, int W, int nmax)
     m->W = W;
     m->nmax = nmax;
     m->input = ocl_alloc(m->ocl, 3 * px * sizeof(float), "input");
-    for (int k = 0; k < 5; k++)
-        m->f[k] = ocl_alloc(m->ocl,
-                            layer_cout[k] * (px >> (2 * k)) * sizeof(float),
-                            "down features");
+    for (int l = 0; l < 4; l++) {
+        const size_t plane = px >> (2 * l);
+
+        m->cat[l] = ocl_alloc(m->ocl, (64 + layer_cout[l]) * plane * sizeof(float),
+                              "concatenation");
+        m->f[l] = ocl_wrap((float *)m->cat[l]->ptr + 64 * plane,
+                           layer_cout[l] * plane * sizeof(float));
+    }
+    m->f[4] = ocl_alloc(m->ocl, layer_cout[4] * (px >> 8) * sizeof(float), "down features");
     for (int k = 0; k < 3; k++)
         m->u[k] = ocl_alloc(m->ocl, 64 * (px >> (2 * (3 - k))) * sizeof(float),
                             "up features");
-    m->tmp = ocl_alloc(m->ocl, 16 * (px >> 2) * sizeof(float), "pooled");
-    m->cat = ocl_alloc(m->ocl, 80 * px * sizeof(float), "concatenation");
+    m->tmp = ocl_alloc(m->ocl, 64 * (px >> 8) * sizeof(float), "pooled");
     m->out = ocl_alloc(m->ocl, (DISK_DESC + 1) * px * sizeof(float), "output");
     m->mean = ocl_alloc(m->ocl, 128 * sizeof(float), "mean");
     m->rstd = ocl_alloc(m->ocl, 128 * sizeof(float), "rstd");
     m->mask = ocl_alloc(m->ocl, px, "nms mask");
+    m->valid = ocl_alloc(m->ocl, px, "valid mask");
     m->xy = ocl_alloc(m->ocl, 2 * (size_t)nmax * sizeof(int), "keypoints");
+    m->score = ocl_alloc(m->ocl, (size_t)nmax * sizeof(float), "scores");
+    m->count = ocl_alloc(m->ocl, sizeof(int), "keypoint count");
     m->desc = ocl_alloc(m->ocl, (size_t)nmax * DISK_DESC * sizeof(float),
                         "descriptors");
-    m->heat = (float *)malloc(px * sizeof(float));
-    m->maskh = (unsigned char *)malloc(px);
+    m->topn_work = ocl_alloc(m->ocl, disk_topn_work_bytes(H, W), "top-n");
     ICOREG_API_END
 }
 
@@ -122,13 +130,6 @@ static void conv(struct disk_model *m, int l, cl_mem in, int H, int W,
                    &g, NULL, NULL, NULL, ACT_NONE, 0, out);
 }
 
-static int cmp_desc_float(const void *a, const void *b)
-{
-    const float x = *(const float *)a, y = *(const float *)b;
-
-    return (x < y) - (x > y);
-}
-
 extern "C" int disk_detect(struct disk_model *m, const float *img, int H,
                            int W, int h, int w, int n, float thresh,
                            const unsigned char *valid, int *xy, float *score,
@@ -137,8 +138,7 @@ extern "C" int disk_detect(struct disk_model *m, const float *img, int H,
     ICOREG_API_BEGIN
     const size_t px = (size_t)H * W;
     const long off = (long)DISK_DESC * (long)px;
-    int ncand = 0, nk = 0;
-    float *cand, cut = -INFINITY;
+    int nk = 0;
 
     if (H > m->H || W > m->W || px > (size_t)m->H * m->W || H % DISK_MULTIPLE ||
         W % DISK_MULTIPLE)
@@ -147,13 +147,20 @@ extern "C" int disk_detect(struct disk_model *m, const float *img, int H,
         icoreg_fatal("DISK crop %d x %d outside the %d x %d tile", h, w, H, W);
     if (n > m->nmax)
         n = m->nmax;
+    if (n < 0)
+        n = 0;
     ocl_write(m->ocl, m->input, 0, img, 3 * px * sizeof(float));
+    if (valid && (size_t)h * w > 0)
+        ocl_write(m->ocl, m->valid, 0, valid, (size_t)h * w);
 
-    /* Down path (disk.c:186-200). */
+    /* Down path (disk.c:186-200): block lev average-pools block lev - 1's
+     * output (into its own level's concatenation buffer, whose first 64
+     * channels the up path fills only later) and writes its output into
+     * the skip part of that buffer. */
     conv(m, 0, m->input, H, W, m->f[0]);
     for (int lev = 1; lev < 5; lev++) {
         const int c = layer_cout[lev - 1], hh = H >> lev, ww = W >> lev;
-        cl_mem t = lev == 1 ? m->tmp : m->cat;
+        cl_mem t = lev < 4 ? m->cat[lev] : m->tmp;
 
         ops_avgpool2(m->ops, m->f[lev - 1], c, H >> (lev - 1), W >> (lev - 1),
                      t);
@@ -161,53 +168,31 @@ extern "C" int disk_detect(struct disk_model *m, const float *img, int H,
         conv(m, lev, t, hh, ww, m->f[lev]);
     }
     /* Up path (disk.c:202-218): bottom input upsampled into the first 64
-     * channels of the concatenation, the skip connection after it. */
+     * channels of the concatenation, the skip connection already after
+     * it. */
     for (int j = 0; j < 4; j++) {
         const int l = 5 + j, lvl = 3 - j, hh = H >> lvl, ww = W >> lvl;
         cl_mem bot = j == 0 ? m->f[4] : m->u[j - 1];
         const int cb = 64, ch = layer_cout[lvl];
         const size_t plane = (size_t)hh * ww;
 
-        ops_resize(m->ops, bot, cb, hh / 2, ww / 2, m->cat, hh, ww, 0, 0,
+        ops_resize(m->ops, bot, cb, hh / 2, ww / 2, m->cat[lvl], hh, ww, 0, 0,
                    2.0f);
-        ocl_copy(m->ocl, m->f[lvl], 0, m->cat, cb * plane * sizeof(float),
-                 ch * plane * sizeof(float));
-        ops_chan_stats(m->ops, m->cat, cb + ch, (int)plane, 1e-5f, m->mean,
+        ops_chan_stats(m->ops, m->cat[lvl], cb + ch, (int)plane, 1e-5f, m->mean,
                        m->rstd);
-        conv(m, l, m->cat, hh, ww, j < 3 ? m->u[j] : m->out);
+        conv(m, l, m->cat[lvl], hh, ww, j < 3 ? m->u[j] : m->out);
     }
-    /* Heatmap NMS on the h x w crop, then the host top-n (disk.c:220-253). */
+    /* Heatmap NMS on the h x w crop, top-n (disk.c:220-253), descriptors;
+     * then the keypoints come back. */
     disk_nms5x5(m->ops, m->out, off, W, h, w, thresh, m->mask);
-    ocl_read(m->ocl, m->mask, 0, m->maskh, (size_t)h * w);
-    ocl_read(m->ocl, m->out, off * sizeof(float), m->heat,
-             (size_t)h * W * sizeof(float));
-    cand = (float *)malloc(((size_t)h * w + 1) * sizeof(float));
-    for (int y = 0; y < h; y++)
-        for (int x = 0; x < w; x++)
-            if (m->maskh[(size_t)y * w + x] &&
-                (!valid || valid[(size_t)y * w + x]))
-                cand[ncand++] = m->heat[(size_t)y * W + x];
-    if (ncand > 0) {
-        qsort(cand, ncand, sizeof(float), cmp_desc_float);
-        cut = cand[ncand > n ? n : ncand - 1];
-    }
-    free(cand);
-    for (int y = 0; y < h && nk < n; y++)
-        for (int x = 0; x < w && nk < n; x++) {
-            const size_t i = (size_t)y * w + x;
-            const float v = m->heat[(size_t)y * W + x];
-
-            if (!m->maskh[i] || (valid && !valid[i]) || !(v > cut))
-                continue;
-            xy[2 * nk] = x;
-            xy[2 * nk + 1] = y;
-            score[nk++] = v;
-        }
+    disk_topn(m->ops, m->out, off, W, h, w, m->mask, valid ? m->valid : NULL, n, m->xy,
+              m->score, m->count, m->topn_work);
+    disk_gather_desc_count(m->ops, m->out, H, W, DISK_DESC, m->xy, m->count, n, m->desc);
+    ocl_read(m->ocl, m->count, 0, &nk, sizeof(int));
     if (nk > 0) {
-        ocl_write(m->ocl, m->xy, 0, xy, 2 * (size_t)nk * sizeof(int));
-        disk_gather_desc(m->ops, m->out, H, W, DISK_DESC, m->xy, nk, m->desc);
-        ocl_read(m->ocl, m->desc, 0, desc,
-                 (size_t)nk * DISK_DESC * sizeof(float));
+        ocl_read(m->ocl, m->xy, 0, xy, 2 * (size_t)nk * sizeof(int));
+        ocl_read(m->ocl, m->score, 0, score, (size_t)nk * sizeof(float));
+        ocl_read(m->ocl, m->desc, 0, desc, (size_t)nk * DISK_DESC * sizeof(float));
     }
     return nk;
     ICOREG_API_END_RET(0)
@@ -225,17 +210,20 @@ extern "C" void disk_free(struct disk_model *m)
     ocl_release(&m->input);
     for (int k = 0; k < 5; k++)
         ocl_release(&m->f[k]);
+    for (int k = 0; k < 4; k++)
+        ocl_release(&m->cat[k]);
     for (int k = 0; k < 3; k++)
         ocl_release(&m->u[k]);
     ocl_release(&m->tmp);
-    ocl_release(&m->cat);
     ocl_release(&m->out);
     ocl_release(&m->mean);
     ocl_release(&m->rstd);
     ocl_release(&m->mask);
+    ocl_release(&m->valid);
     ocl_release(&m->xy);
+    ocl_release(&m->score);
+    ocl_release(&m->count);
     ocl_release(&m->desc);
-    free(m->heat);
-    free(m->maskh);
+    ocl_release(&m->topn_work);
     memset(m, 0, sizeof(*m));
 }

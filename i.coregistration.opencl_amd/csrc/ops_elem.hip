@@ -29,29 +29,85 @@ static unsigned blocks_for(long long n, int per_block, long long cap = 1 << 20)
 
 /* ---- instance statistics -------------------------------------------- */
 
+/* Per-channel mean and 1 / sqrt(biased variance + eps), two passes as
+ * the reference's chan_stats (ops.cl:453-492): the mean first, then the
+ * squared deviations from it. Each channel is cut into segments of whole
+ * 1024-float chunks so that a handful of channels still fill the GPU
+ * (DISK's last level: 80 channels of 512 x 512); each pass writes one
+ * partial per (channel, segment), and every block that needs a channel's
+ * mean or variance adds that channel's partials itself, in segment
+ * order, so the result does not depend on the schedule. Float4 loads
+ * when HW % 4 == 0. */
+#define CS_MAXSEG 64
+
+__device__ __forceinline__ float cs_seg_sum(const float *__restrict__ p, int HW, int s0,
+                                            int s1, float m, bool dev, bool v4)
+{
+    float acc = 0.0f;
+
+    if (v4) {
+        const float4 *q = (const float4 *)p;
+
+        for (int i = s0 / 4 + threadIdx.x; i < s1 / 4; i += 256) {
+            const float4 v = q[i];
+
+            if (dev) {
+                acc = fmaf(v.x - m, v.x - m, acc);
+                acc = fmaf(v.y - m, v.y - m, acc);
+                acc = fmaf(v.z - m, v.z - m, acc);
+                acc = fmaf(v.w - m, v.w - m, acc);
+            }
+            else
+                acc += (v.x + v.y) + (v.z + v.w);
+        }
+    }
+    else
+        for (int i = s0 + threadIdx.x; i < s1; i += 256) {
+            const float v = p[i];
+
+            acc = dev ? fmaf(v - m, v - m, acc) : acc + v;
+        }
+    return acc;
+}
+
+__device__ __forceinline__ float cs_total(const float *__restrict__ part, int nseg)
+{
+    float t = 0.0f;
+
+    for (int k = 0; k < nseg; k++)
+        t += part[k];
+    return t;
+}
+
+/* Pass 1 (dev = 0): part_s = sum of the segment. Pass 2 (dev = 1): part_d
+ * = sum of squared deviations from the channel's mean. */
 __global__ void __launch_bounds__(256)
-    chan_stats_kernel(const float *__restrict__ x, int HW, float eps,
-                      float *__restrict__ mean, float *__restrict__ rstd)
+    chan_stats_part_kernel(const float *__restrict__ x, int HW, int seg, int nseg,
+                           const float *__restrict__ part_s, float *__restrict__ out,
+                           int dev)
 {
     __shared__ float red[4];
-    const int c = blockIdx.x, l = threadIdx.x;
-    const float *p = x + (long long)c * HW;
-    float s = 0.0f, m;
+    const int c = blockIdx.y, k = blockIdx.x;
+    const int s0 = k * seg, s1 = min(HW, s0 + seg);
+    const float m = dev ? cs_total(part_s + (long long)c * nseg, nseg) / HW : 0.0f;
+    float acc = cs_seg_sum(x + (long long)c * HW, HW, s0, s1, m, dev != 0, (HW & 3) == 0);
 
-    for (int i = l; i < HW; i += 256)
-        s += p[i];
-    m = block_sum<4>(s, red) / HW;
-    s = 0.0f;
-    for (int i = l; i < HW; i += 256) {
-        const float d = p[i] - m;
+    acc = block_sum<4>(acc, red);
+    if (threadIdx.x == 0)
+        out[(long long)c * nseg + k] = acc;
+}
 
-        s = fmaf(d, d, s);
-    }
-    s = block_sum<4>(s, red);
-    if (l == 0) {
-        mean[c] = m;
-        rstd[c] = 1.0f / sqrtf(s / HW + eps);
-    }
+__global__ void __launch_bounds__(256)
+    chan_stats_final_kernel(const float *__restrict__ part_s,
+                            const float *__restrict__ part_d, int C, int HW, int nseg,
+                            float eps, float *__restrict__ mean, float *__restrict__ rstd)
+{
+    const int c = blockIdx.x * 256 + threadIdx.x;
+
+    if (c >= C)
+        return;
+    mean[c] = cs_total(part_s + (long long)c * nseg, nseg) / HW;
+    rstd[c] = 1.0f / sqrtf(cs_total(part_d + (long long)c * nseg, nseg) / HW + eps);
 }
 
 extern "C" void ops_chan_stats(struct ops *o, cl_mem x, int C, int HW,
@@ -66,10 +122,29 @@ extern "C" void ops_chan_stats(struct ops *o, cl_mem x, int C, int HW,
     need_floats(x, 0, (long long)C * HW, op, "x");
     need_floats(mean, 0, C, op, "mean");
     need_floats(rstd, 0, C, op, "rstd");
-    prof_scope ps(o->ocl, "chan_stats");
-    hipLaunchKernelGGL(chan_stats_kernel, dim3(C), dim3(256), 0,
-                       stream_of(o->ocl), cfptr(x), HW, eps, fptr(mean),
-                       fptr(rstd));
+    {
+        /* Segments of whole 1024-float chunks: about 2048 blocks in all. */
+        const long long chunks = (HW + 1023) / 1024;
+        long long want = (2048 + C - 1) / C;
+        int nseg, seg;
+
+        want = want < 1 ? 1 : want > CS_MAXSEG ? CS_MAXSEG : want;
+        want = want > chunks ? chunks : want;
+        seg = (int)((chunks + want - 1) / want) * 1024;
+        nseg = (int)((HW + seg - 1) / seg);
+        cl_mem sc = scratch_get(o, 2 * (size_t)C * nseg * sizeof(float));
+        float *ps = (float *)sc->ptr, *pd = ps + (size_t)C * nseg;
+        hipStream_t st = stream_of(o->ocl);
+
+        prof_scope pr(o->ocl, "chan_stats");
+        hipLaunchKernelGGL(chan_stats_part_kernel, dim3(nseg, C), dim3(256), 0, st,
+                           cfptr(x), HW, seg, nseg, (const float *)ps, ps, 0);
+        hipLaunchKernelGGL(chan_stats_part_kernel, dim3(nseg, C), dim3(256), 0, st,
+                           cfptr(x), HW, seg, nseg, (const float *)ps, pd, 1);
+        hipLaunchKernelGGL(chan_stats_final_kernel, dim3((C + 255) / 256), dim3(256), 0, st,
+                           (const float *)ps, (const float *)pd, C, HW, nseg, eps, fptr(mean),
+                           fptr(rstd));
+    }
     launch_check("chan_stats");
     ICOREG_API_END
 }

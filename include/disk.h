@@ -8,8 +8,9 @@
  * down 16-32-64-64-64, up 64-64-64-129, InstanceNorm + PReLU on each
  * block's input) runs on this build's direct 5 x 5 convolution on the
  * matrix cores with the normalisation fused into its input loads; the
- * heatmap NMS and descriptor gather are HIP kernels (icoreg_kernels.h);
- * the top-n selection stays on the host, as in the reference. */
+ * heatmap NMS, the top-n selection (on the host in the reference) and
+ * the descriptor gather are HIP kernels (icoreg_kernels.h); the host
+ * reads back only the keypoints. */
 
 #ifndef ICOREG_DISK_H
 #define ICOREG_DISK_H
@@ -31,11 +32,13 @@ struct disk_model {
     struct ops *ops;
     int cin[DISK_LAYERS], cout[DISK_LAYERS];
     cl_mem w[DISK_LAYERS], b[DISK_LAYERS], alpha[DISK_LAYERS];
-    /* Work buffers for tiles of up to H x W cells. */
+    /* Work buffers for tiles of up to H x W cells. cat[l] is the up
+     * path's concatenation at level l (64 upsampled channels, then the
+     * skip connection); f[l] (l < 4) is a view of its skip part, where
+     * the down path writes, so no copy joins them. */
     int H, W, nmax;
-    cl_mem input, f[5], u[3], tmp, cat, out, mean, rstd, mask, xy, desc;
-    float *heat;
-    unsigned char *maskh;
+    cl_mem input, f[5], u[3], cat[4], tmp, out, mean, rstd, mask, valid;
+    cl_mem xy, score, count, desc, topn_work;
 };
 
 /* Read the DISK weights ("unet.path_down.*", "unet.path_up.*" of the

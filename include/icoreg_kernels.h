@@ -128,6 +128,26 @@ void disk_nms5x5(struct ops *o, cl_mem heat, long off, int W, int h, int w,
 void disk_gather_desc(struct ops *o, cl_mem feat, int H, int W, int D,
                       cl_mem xy, int n, cl_mem desc);
 
+/* The top-n selection of disk_detect on the device (the reference does
+ * it on the host, disk.c:228-253): among the cells of mask (h x w bytes,
+ * 1 = NMS maximum) that valid (h x w bytes, or NULL) allows, the cut is
+ * the (n+1)-th highest heat value, or the lowest when there are no more
+ * than n; the cells strictly above it are kept in raster order: xy (x, y
+ * int pairs, capacity n) and score, their number into count (one int on
+ * the device). heat as for disk_nms5x5. work holds
+ * disk_topn_work_bytes(h, w) bytes. No counterpart among the reference's
+ * kernels. */
+size_t disk_topn_work_bytes(int h, int w);
+void disk_topn(struct ops *o, cl_mem heat, long off, int W, int h, int w,
+               cl_mem mask, cl_mem valid, int n, cl_mem xy, cl_mem score,
+               cl_mem count, cl_mem work);
+
+/* disk_gather_desc for the keypoints disk_topn left on the device: their
+ * number in count (one int, at most nmax), xy within h x w by
+ * construction. No counterpart among the reference's kernels. */
+void disk_gather_desc_count(struct ops *o, cl_mem feat, int H, int W, int D,
+                            cl_mem xy, cl_mem count, int nmax, cl_mem desc);
+
 /* Extension with no counterpart among the reference's kernels: the
  * Gaussian-process solve that roma.c:770-836 runs on the host in double
  * precision, on the device in double precision. F (n x d floats) is

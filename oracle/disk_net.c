@@ -86,6 +86,38 @@ static int cmp_desc(const void *a, const void *b)
     return (x < y) - (x > y);
 }
 
+/* disk.c:228-253: cut = the (n+1)-th highest candidate (the lowest with
+ * no more than n), keep the candidates above it in raster order. */
+int orc_disk_topn(const float *heat, int W, int h, int w,
+                  const unsigned char *mask, const unsigned char *valid, int n,
+                  int *xy, float *score)
+{
+    float *cand = malloc(((size_t)h * w + 1) * sizeof(float)), cut = -INFINITY;
+    int x, y, ncand = 0, nk = 0;
+
+    for (y = 0; y < h; y++)
+        for (x = 0; x < w; x++)
+            if (mask[(long)y * w + x] && (!valid || valid[(long)y * w + x]))
+                cand[ncand++] = heat[(long)y * W + x];
+    if (ncand > 0) {
+        qsort(cand, ncand, sizeof(float), cmp_desc);
+        cut = cand[ncand > n ? n : ncand - 1];
+    }
+    free(cand);
+    for (y = 0; y < h && nk < n; y++)
+        for (x = 0; x < w && nk < n; x++) {
+            const long i = (long)y * w + x;
+            const float v = heat[(long)y * W + x];
+
+            if (!mask[i] || (valid && !valid[i]) || !(v > cut))
+                continue;
+            xy[2 * nk] = x;
+            xy[2 * nk + 1] = y;
+            score[nk++] = v;
+        }
+    return nk;
+}
+
 int orc_disk_detect(const struct orc_named *weights, int nweights,
                     const float *img, int H, int W, int h, int w, int n,
                     float thresh, const unsigned char *valid, int *xy,
@@ -93,10 +125,9 @@ int orc_disk_detect(const struct orc_named *weights, int nweights,
 {
     const long px = (long)H * W;
     const float *wt[LAYERS], *bs[LAYERS], *al[LAYERS];
-    float *f[5], *u[3], *tmp, *cat, *out, mean[128], rstd[128], *cand;
+    float *f[5], *u[3], *tmp, *cat, *out, mean[128], rstd[128];
     unsigned char *mask;
-    float cut = -INFINITY;
-    int l, k, lev, j, x, y, ncand = 0, nk = 0;
+    int l, k, lev, j, nk = 0;
     char name[128];
 
     for (l = 0; l < LAYERS; l++) {
@@ -156,27 +187,7 @@ int orc_disk_detect(const struct orc_named *weights, int nweights,
         const float *heat = out + (long)DESC * px;
 
         orc_disk_nms5x5(heat, W, h, w, thresh, mask);
-        cand = malloc(((size_t)h * w + 1) * sizeof(float));
-        for (y = 0; y < h; y++)
-            for (x = 0; x < w; x++)
-                if (mask[(long)y * w + x] && (!valid || valid[(long)y * w + x]))
-                    cand[ncand++] = heat[(long)y * W + x];
-        if (ncand > 0) {
-            qsort(cand, ncand, sizeof(float), cmp_desc);
-            cut = cand[ncand > n ? n : ncand - 1];
-        }
-        free(cand);
-        for (y = 0; y < h && nk < n; y++)
-            for (x = 0; x < w && nk < n; x++) {
-                const long i = (long)y * w + x;
-                const float v = heat[(long)y * W + x];
-
-                if (!mask[i] || (valid && !valid[i]) || !(v > cut))
-                    continue;
-                xy[2 * nk] = x;
-                xy[2 * nk + 1] = y;
-                score[nk++] = v;
-            }
+        nk = orc_disk_topn(heat, W, h, w, mask, valid, n, xy, score);
     }
     if (nk > 0)
         orc_disk_gather_desc(out, H, W, DESC, xy, nk, desc);

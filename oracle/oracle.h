@@ -179,6 +179,11 @@ void orc_disk_nms5x5(const float *heat, int W, int h, int w, float thresh,
 /* disk_kernels.cl:37-60. */
 void orc_disk_gather_desc(const float *feat, int H, int W, int D,
                           const int *xy, int n, float *desc);
+/* The host top-n of disk.c:228-253 on the NMS mask (h x w) and valid
+ * (or NULL): returns the count, xy / score in raster order. */
+int orc_disk_topn(const float *heat, int W, int h, int w,
+                  const unsigned char *mask, const unsigned char *valid, int n,
+                  int *xy, float *score);
 /* disk_detect (disk.c:164-273) on a (3, H, W) image: returns the keypoint
  * count; out_full (129 x H x W, or NULL) gets the U-Net output. */
 int orc_disk_detect(const struct orc_named *weights, int nweights,

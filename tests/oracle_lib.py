@@ -84,6 +84,7 @@ SIGS["orc_roma_forward"] = (_I, [C.POINTER(Named), _I, C.POINTER(Named), _I,
                                  C.POINTER(RomaOut)])
 _UP = C.POINTER(C.c_ubyte)
 SIGS["orc_disk_nms5x5"] = (None, [_FP, _I, _I, _I, _F, _UP])
+SIGS["orc_disk_topn"] = (_I, [_FP, _I, _I, _I, _UP, _UP, _I, _IP, _FP])
 SIGS["orc_disk_gather_desc"] = (None, [_FP, _I, _I, _I, _IP, _I, _FP])
 SIGS["orc_disk_detect"] = (_I, [C.POINTER(Named), _I, _FP, _I, _I, _I, _I, _I, _F, _UP,
                                 _IP, _FP, _FP, _FP])

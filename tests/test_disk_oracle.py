@@ -5,6 +5,7 @@ F.conv2d / F.instance_norm / F.prelu / F.avg_pool2d / F.interpolate, the
 strict 5 x 5 NMS through F.unfold, the top-n through torch.topk and the
 descriptors through F.normalize."""
 
+import ctypes as C
 import sys
 from pathlib import Path
 
@@ -76,3 +77,45 @@ def test_detect(weights, H, W, h, w, n, valid):
     assert np.array_equal(o["xy"], xy)
     assert np.array_equal(o["score"], heat[xy[:, 1], xy[:, 0]])
     assert rel(o["desc"], R.gather(o["out"], xy)) < 1e-5
+
+
+def _bruteforce_topn(heat, mask, valid, n):
+    """The kept cells by counting, not sorting: with more than n
+    candidates a candidate v is kept iff at most n candidates are >= v
+    (it is then above the (n+1)-th highest); with n or fewer, iff it is
+    above the lowest candidate. Raster order, at most n."""
+    m = mask.astype(bool) & (valid.astype(bool) if valid is not None else True)
+    ys, xs = np.nonzero(m)
+    v = heat[ys, xs].astype(np.float64)
+    if len(v) == 0 or n == 0:
+        return np.zeros((0, 2), np.int32)
+    if len(v) > n:
+        keep = np.array([(v >= x).sum() <= n for x in v])
+    else:
+        keep = v > v.min()
+    return np.stack([xs[keep], ys[keep]], 1).astype(np.int32)[:n]
+
+
+@pytest.mark.parametrize("seed,n,levels,use_valid", [(1, 50, 0, False), (2, 50, 7, False),
+                                                     (3, 3, 4, True), (4, 1000, 5, False),
+                                                     (5, 0, 0, False), (6, 1, 2, True)])
+def test_topn_matches_counting_rule(orc, seed, n, levels, use_valid):
+    """orc_disk_topn (disk.c:228-253, qsort and cut) against the counting
+    statement of the same rule, with ties at the cut (heat values
+    quantised to a few levels), fewer candidates than n, n = 0, a valid
+    mask."""
+    rng = np.random.default_rng(seed)
+    h, w, W = 37, 45, 48
+    heat = rng.standard_normal((h, W)).astype(np.float32)
+    if levels:
+        heat = np.round(heat * levels / 3).astype(np.float32)
+    mask = (rng.uniform(size=(h, w)) < 0.15).astype(np.uint8)
+    valid = (rng.uniform(size=(h, w)) < 0.7).astype(np.uint8) if use_valid else None
+    xy = np.zeros((max(n, 1), 2), np.int32)
+    sc = np.zeros(max(n, 1), np.float32)
+    up = lambda a: a.ctypes.data_as(C.POINTER(C.c_ubyte)) if a is not None else None
+    nk = orc.orc_disk_topn(fp(heat), W, h, w, up(mask), up(valid), n, ip(xy), fp(sc))
+    want = _bruteforce_topn(heat[:, :w], mask, valid, n)
+    assert nk == len(want)
+    assert np.array_equal(xy[:nk], want)
+    assert np.array_equal(sc[:nk], heat[want[:, 1], want[:, 0]])
