@@ -439,24 +439,71 @@ def bench_disk(ic, dev, synth, wdir, steps, warmup, H=512, n=2048):
             "kernels": kern}
 
 
-def cpu_baseline(weights, size=256):
-    """The oracle (C port of the reference kernels and schedule, OpenMP)
-    on one size x size pair, scaled to a 640 x 640 pair by algorithmic
-    FLOPs."""
+def _cpu_threads():
+    """(CPUs this process may run on, OpenMP threads the baseline pins):
+    the box's CPU share per GPU is 16 threads."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return n, min(n, 16)
+
+
+def cpu_baseline(weights, H=640, W=640):
+    """The oracle (C port of the reference kernels and eloftr.c schedule,
+    OpenMP) timed on one whole H x W pair of the config: no scaling."""
     sys.path.insert(0, str(ROOT / "tests"))
     sys.path.insert(0, str(PKG_DIR))
     import synth
-    from oracle_lib import eloftr_forward
-    g0, g1, _ = synth.eloftr_pair(size, size)
+    from oracle_lib import eloftr_forward, oracle
+    orc = oracle()
+    nproc, thr = _cpu_threads()
+    orc.orc_set_threads(thr)
+    g0, g1, _ = synth.eloftr_pair(H, W)
     t0 = time.perf_counter()
     eloftr_forward(weights, g0, g1)
     dt = time.perf_counter() - t0
-    ratio = eloftr_flops(640, 640)["total"] / eloftr_flops(size, size)["total"]
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": 1.0 / (dt * ratio), "unit": "tile-pairs/s", "cores": cores, "kind": "port",
+    return {"value": 1.0 / dt, "unit": "tile-pairs/s", "cores": int(orc.orc_threads()),
+            "kind": "port",
             "sample": f"oracle/ (C port of the reference kernels + eloftr.c schedule, OpenMP) "
-                      f"full ELoFTR pass on one {size}x{size} pair in {dt:.1f} s, scaled to a "
-                      f"640x640 pair by algorithmic FLOPs (x{ratio:.2f})"}
+                      f"full ELoFTR pass on one {H}x{W} pair (the config itself, no scaling) "
+                      f"in {dt:.1f} s; {thr} OpenMP threads set by omp_set_num_threads, "
+                      f"{nproc} CPUs visible to the process"}
+
+
+def cpu_baseline_roma(coarse=560, blocks=2):
+    """The oracle's DINOv2 ViT-L block (roma.c:675-713, the block() the
+    oracle's RoMa forward runs) timed on `blocks` whole blocks at the
+    config's token count; the pair's 48 blocks plus the rest of the
+    coarse pass are priced at the blocks' rate by algorithmic FLOPs."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_lib import oracle, vit_block
+    orc = oracle()
+    nproc, thr = _cpu_threads()
+    orc.orc_set_threads(thr)
+    D = 1024
+    nt = (coarse // 14) ** 2 + 1
+    rng = np.random.default_rng(0)
+    s = 1.0 / np.sqrt(D)
+    shapes = [(D,), (D,), (3 * D, D), (3 * D,), (D, D), (D,), (D,), (D,), (4 * D, D),
+              (4 * D,), (D, 4 * D), (D,)]
+    w = [(s * rng.standard_normal(sh)).astype(np.float32) for sh in shapes]
+    X = rng.standard_normal((nt, D)).astype(np.float32)
+    vit_block(w, X[:64])  # first touch of the weights and the thread pool
+    t0 = time.perf_counter()
+    for _ in range(blocks):
+        X = vit_block(w, X)
+    dt = (time.perf_counter() - t0) / blocks
+    blk = 2.0 * nt * D * 12 * D + 4.0 * 16 * nt * nt * 64
+    fl = roma_coarse_flops(coarse)
+    pair_s = dt * fl["total"] / blk
+    return {"value": 1.0 / pair_s, "unit": "tile-pairs/s", "cores": int(orc.orc_threads()),
+            "kind": "port",
+            "sample": f"oracle/ DINOv2 ViT-L/14 block (C port, OpenMP) timed on {blocks} whole "
+                      f"blocks at {nt} tokens ({dt:.2f} s per block, {blk / 1e9:.1f} GFLOP); "
+                      f"the coarse pair ({fl['total'] / 1e9:.0f} GFLOP: 48 such blocks, "
+                      f"patch embedding, GP, decoder) priced at that rate "
+                      f"(x{fl['total'] / blk:.1f}); {thr} OpenMP threads, {nproc} CPUs visible"}
 
 
 def main():
@@ -604,7 +651,13 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(synth.eloftr_weights_calibrated())
+        print("[bench] CPU baseline: oracle ELoFTR pass at the config size", file=sys.stderr,
+              flush=True)
+        cpu = cpu_baseline(synth.eloftr_weights_calibrated(), H, W)
+        if roma is not None:
+            print("[bench] CPU baseline: oracle ViT-L blocks at 1601 tokens", file=sys.stderr,
+                  flush=True)
+            roma["cpu_baseline"] = cpu_baseline_roma()
 
     line = {
         "metric": "tile-pairs/sec (1 GPU) ELoFTR 640² & RoMa 560², fp32; % MFMA/HBM peak",

@@ -7,6 +7,7 @@
  * convolution sums in k order with fused multiply-adds, as mad). */
 
 #include <math.h>
+#include <omp.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -809,4 +810,14 @@ void orc_eloftr_fine(const float *f0, const float *f1, int H, int W,
             out[4 * k + 3] = cy1 * FW + qi - (FW / 2 - 0.5f) + ey;
         }
     }
+}
+
+/* OpenMP threads the oracle's parallel loops use, and how to set them
+ * (timing of the CPU baseline states and pins the count). */
+int orc_threads(void) { return omp_get_max_threads(); }
+
+void orc_set_threads(int n)
+{
+    if (n > 0)
+        omp_set_num_threads(n);
 }

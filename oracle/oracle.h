@@ -191,6 +191,16 @@ int orc_disk_detect(const struct orc_named *weights, int nweights,
                     float thresh, const unsigned char *valid, int *xy,
                     float *score, float *desc, float *out_full);
 
+/* One pre-norm ViT block (DINOv2's, roma.c:675-713) on X (N x 1024) in
+ * place; w[12] = norm1 g, b; qkv W, b; proj W, b; norm2 g, b; fc1 W, b;
+ * fc2 W, b, layer scale folded into proj and fc2. */
+void orc_vit_block(const float *const w[12], float *X, int N, int heads,
+                   float eps);
+
+/* OpenMP threads of the oracle's parallel loops. */
+int orc_threads(void);
+void orc_set_threads(int n);
+
 /* ---- RoMa network (roma.c) ------------------------------------------------ */
 
 /* Host input preparation, roma.c:1106-1186: (3, H, W) resampled to (3, h,

@@ -490,6 +490,37 @@ static void block(const struct blk *b, float *X, int N, int heads, float eps)
     free(h);
 }
 
+/* One pre-norm ViT block of width DV on X (N x DV) in place, weights w[12]
+ * = norm1 g, b; qkv W, b (b may be NULL); proj W, b; norm2 g, b; fc1 W, b;
+ * fc2 W, b, with layer scale already folded into proj and fc2 (the form
+ * load_block keeps). The same block() DINOv2 runs (roma.c:675-713). */
+void orc_vit_block(const float *const w[12], float *X, int N, int heads,
+                   float eps)
+{
+    float *own[4];
+    struct blk b;
+    int i;
+
+    for (i = 0; i < 4; i++) {
+        const long n = i == 0 ? (long)DV * DV : i == 2 ? 4L * DV * DV : DV;
+        own[i] = dup(w[4 + i + (i >= 2 ? 4 : 0)], n);
+    }
+    b.n1g = w[0];
+    b.n1b = w[1];
+    b.qkv_w = w[2];
+    b.qkv_b = w[3];
+    b.proj_w = own[0];
+    b.proj_b = own[1];
+    b.n2g = w[6];
+    b.n2b = w[7];
+    b.fc1_w = w[8];
+    b.fc1_b = w[9];
+    b.fc2_w = own[2];
+    b.fc2_b = own[3];
+    block(&b, X, N, heads, eps);
+    free_block(&b);
+}
+
 /* DINOv2 on img (3, c, c): normed patch tokens (DV, n16) into feat and the
  * 1/16 projection (512, n16) into P0. roma.c:715-738. */
 static void dino(const struct net *m, const float *img, float *feat, float *P0)

@@ -89,8 +89,22 @@ SIGS["orc_disk_gather_desc"] = (None, [_FP, _I, _I, _I, _IP, _I, _FP])
 SIGS["orc_disk_detect"] = (_I, [C.POINTER(Named), _I, _FP, _I, _I, _I, _I, _I, _F, _UP,
                                 _IP, _FP, _FP, _FP])
 SIGS["orc_roma_prepare"] = (None, [_FP, _I, _I, _FP, _I, _I, _I])
+SIGS["orc_vit_block"] = (None, [_FP * 12, _FP, _I, _I, _F])
+SIGS["orc_threads"] = (_I, [])
+SIGS["orc_set_threads"] = (None, [_I])
 
 _lib = None
+
+
+def vit_block(w, X, heads=16, eps=1e-6):
+    """orc_vit_block on a copy of X (N x 1024); w: the 12 float32 arrays in
+    the order norm1 g, b; qkv W, b; proj W, b; norm2 g, b; fc1 W, b; fc2 W, b."""
+    import numpy as np
+    X = np.ascontiguousarray(X, np.float32).copy()
+    ws = [np.ascontiguousarray(a, np.float32) for a in w]
+    arr = (_FP * 12)(*[fp(a) for a in ws])
+    oracle().orc_vit_block(arr, fp(X), X.shape[0], heads, eps)
+    return X
 
 
 def named_array(weights):

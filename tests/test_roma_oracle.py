@@ -202,3 +202,44 @@ def test_roma_forward_matches_float64_restatement(roma_weights, v2):
         both = np.isfinite(o["sd"]) & np.isfinite(r["sd"])
         assert both.mean() > 0.99
         assert rel(o["sd"][both], r["sd"][both]) < 1e-3
+
+
+def test_vit_block_vs_torch(orc):
+    """orc_vit_block (the DINOv2 block the oracle runs, roma.c:675-713, and
+    the CPU baseline times) against torch float64: pre-norm attention with
+    16 heads, exact-erf GELU MLP, both residuals. A swapped q / k slice, a
+    missing residual or a tanh GELU fails the bound."""
+    from oracle_lib import vit_block
+    rng = np.random.default_rng(7)
+    N, D = 19, 1024
+    s = 1.0 / np.sqrt(D)
+    w = [1 + 0.1 * rng.standard_normal(D), 0.1 * rng.standard_normal(D),
+         s * rng.standard_normal((3 * D, D)), 0.1 * rng.standard_normal(3 * D),
+         s * rng.standard_normal((D, D)), 0.1 * rng.standard_normal(D),
+         1 + 0.1 * rng.standard_normal(D), 0.1 * rng.standard_normal(D),
+         s * rng.standard_normal((4 * D, D)), 0.1 * rng.standard_normal(4 * D),
+         0.5 * s * rng.standard_normal((D, 4 * D)), 0.1 * rng.standard_normal(D)]
+    w = [a.astype(np.float32) for a in w]
+    X = rng.standard_normal((N, D)).astype(np.float32)
+    got = vit_block(w, X)
+    t = [R.t64(a) for a in w]
+    x = R.t64(X)
+    ln = torch.nn.functional.layer_norm
+    h = ln(x, (D,), t[0], t[1], 1e-6)
+    qkv = (h @ t[2].T + t[3]).reshape(N, 3, 16, 64).permute(1, 2, 0, 3)
+    a = torch.softmax(qkv[0] @ qkv[1].transpose(1, 2) / 8.0, -1) @ qkv[2]
+    x = x + a.permute(1, 0, 2).reshape(N, D) @ t[4].T + t[5]
+    h = ln(x, (D,), t[6], t[7], 1e-6)
+    x = x + torch.nn.functional.gelu(h @ t[8].T + t[9]) @ t[10].T + t[11]
+    assert rel(got, x.numpy()) < 1e-5
+
+
+def test_oracle_threads(orc):
+    """The thread count the CPU baseline pins is the one the oracle's loops
+    use afterwards."""
+    n0 = orc.orc_threads()
+    orc.orc_set_threads(3)
+    try:
+        assert orc.orc_threads() == 3
+    finally:
+        orc.orc_set_threads(n0)
