@@ -328,6 +328,50 @@ def bench_hbm_kernels(ic, dev, H=864, W=864):
     return out
 
 
+def bench_adalam(ic, dev, n=2048, dim=128):
+    """AdaLAM's nearest-neighbour search (adalam_nearest) on two sets of n
+    unit descriptors, the DISK config's keypoint count: distance tiles on
+    the matrix cores, top-2 per row and argmin per column fused, timed
+    over 20 launches. Algorithmic work 2 n^2 dim flop."""
+    rng = np.random.default_rng(9)
+    d = rng.standard_normal((2, n, dim))
+    d = (d / np.linalg.norm(d, axis=2, keepdims=True)).astype(np.float32)
+    b1, b2 = dev.upload(d[0]), dev.upload(d[1])
+    nn12, sc, nn21 = dev.zeros(n), dev.zeros(n), dev.zeros(n)
+    work = dev.alloc(int(dev.api.adalam_nearest_work_bytes(n, n)))
+    api, po = dev.api, dev.po
+    ms = time_launches(dev, lambda: api.adalam_nearest(po, b1.mem, n, b2.mem, n, dim, nn12.mem,
+                                                       sc.mem, nn21.mem, work.mem))
+    fl = 2.0 * n * n * dim
+    for x in (b1, b2, nn12, sc, nn21, work):
+        x.release()
+    return {"workload": f"AdaLAM nearest neighbours, {n} x {n} unit descriptors of {dim} "
+                        "(nn12, Lowe ratio, nn21)",
+            "ms": round(ms, 5), "gflop": round(fl / 1e9, 3),
+            "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
+
+
+def cpu_adalam(n=2048, dim=128):
+    """The oracle's restatement of the host loop (adalam.c:38-116, OpenMP
+    over rows as there) on the same sizes, timed once."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from oracle_lib import fp, ip, oracle
+    orc = oracle()
+    nproc, thr = _cpu_threads()
+    orc.orc_set_threads(thr)
+    rng = np.random.default_rng(9)
+    d = rng.standard_normal((2, n, dim))
+    d = np.ascontiguousarray((d / np.linalg.norm(d, axis=2, keepdims=True)).astype(np.float32))
+    nn12, sc, nn21 = np.zeros(n, np.int32), np.zeros(n, np.float32), np.zeros(n, np.int32)
+    d1, d2 = np.ascontiguousarray(d[0]), np.ascontiguousarray(d[1])
+    t0 = time.perf_counter()
+    orc.orc_adalam_nearest(fp(d1), n, fp(d2), n, dim, ip(nn12), fp(sc), ip(nn21))
+    dt = time.perf_counter() - t0
+    return {"value": round(dt * 1e3, 3), "unit": "ms", "cores": int(orc.orc_threads()),
+            "kind": "port", "sample": f"oracle/ orc_adalam_nearest on the same {n} x {n} x {dim} "
+                                      f"sets, one run, {thr} OpenMP threads"}
+
+
 def _kernel_table(table, steps):
     return {k: {"ms_per_step": round(v[0] / steps, 4), "launches_per_step": v[1] / steps}
             for k, v in sorted(table.items(), key=lambda kv: -kv[1][0])}
@@ -648,6 +692,7 @@ def main():
         extra["hbm_kernels"] = bench_hbm_kernels(ic, dev)
         extra["roma_v2ref1024"] = bench_v2ref(ic, dev, synth, wdir, 3, 1)
         extra["disk512"] = bench_disk(ic, dev, synth, wdir, 20, 3)
+        extra["adalam_nn2048"] = bench_adalam(ic, dev)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -658,6 +703,8 @@ def main():
             print("[bench] CPU baseline: oracle ViT-L blocks at 1601 tokens", file=sys.stderr,
                   flush=True)
             roma["cpu_baseline"] = cpu_baseline_roma()
+        if "adalam_nn2048" in extra:
+            extra["adalam_nn2048"]["cpu_baseline"] = cpu_adalam()
 
     line = {
         "metric": "tile-pairs/sec (1 GPU) ELoFTR 640² & RoMa 560², fp32; % MFMA/HBM peak",

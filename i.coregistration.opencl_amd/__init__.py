@@ -173,6 +173,10 @@ SIGNATURES = {
     "disk_topn_work_bytes": (C.c_size_t, [_I, _I]),
     "disk_topn": (None, [_O, Mem, _L, _I, _I, _I, Mem, Mem, _I, Mem, Mem, Mem, Mem]),
     "disk_gather_desc_count": (None, [_O, Mem, _I, _I, _I, Mem, Mem, _I, Mem]),
+    # AdaLAM's nearest-neighbour search (include/adalam_nn.h)
+    "adalam_nearest_work_bytes": (C.c_size_t, [_I, _I]),
+    "adalam_nearest": (None, [_O, Mem, _I, Mem, _I, _I, Mem, Mem, Mem, Mem]),
+    "adalam_nearest_host": (None, [_O, _P, _I, _P, _I, _I, _P, _P, _P]),
     # DISK model (include/disk.h)
     "disk_load": (None, [_P, _O, _P]),
     "disk_alloc": (None, [_P, _I, _I, _I]),
@@ -218,7 +222,7 @@ _NO_CHECK = {"icoreg_set_fatal_mode", "icoreg_last_error", "icoreg_clear_error",
              "icoreg_eloftr_set_pos_scale", "icoreg_eloftr_buffer", "roma_gp_work_bytes",
              "icoreg_roma_new", "icoreg_roma_result", "icoreg_roma_buffer",
              "icoreg_roma_set_imagenet", "icoreg_disk_new", "icoreg_disk_buffer",
-             "icoreg_roma_last", "disk_topn_work_bytes"}
+             "icoreg_roma_last", "disk_topn_work_bytes", "adalam_nearest_work_bytes"}
 
 _lib = None
 

@@ -191,6 +191,15 @@ int orc_disk_detect(const struct orc_named *weights, int nweights,
                     float thresh, const unsigned char *valid, int *xy,
                     float *score, float *desc, float *out_full);
 
+/* ---- AdaLAM's nearest-neighbour search (adalam.c:38-116) --------------- */
+
+/* Per row of d1 (n1 x dim): the first index of the nearest row of d2
+ * (n2 x dim) by squared distance, and the ratio of the two smallest
+ * distances (second clamped to 1e-3); per row of d2, when nn21 is not
+ * NULL, the first index of the nearest row of d1. */
+void orc_adalam_nearest(const float *d1, int n1, const float *d2, int n2,
+                        int dim, int *nn12, float *score, int *nn21);
+
 /* One pre-norm ViT block (DINOv2's, roma.c:675-713) on X (N x 1024) in
  * place; w[12] = norm1 g, b; qkv W, b; proj W, b; norm2 g, b; fc1 W, b;
  * fc2 W, b, layer scale folded into proj and fc2. */

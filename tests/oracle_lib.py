@@ -89,6 +89,7 @@ SIGS["orc_disk_gather_desc"] = (None, [_FP, _I, _I, _I, _IP, _I, _FP])
 SIGS["orc_disk_detect"] = (_I, [C.POINTER(Named), _I, _FP, _I, _I, _I, _I, _I, _F, _UP,
                                 _IP, _FP, _FP, _FP])
 SIGS["orc_roma_prepare"] = (None, [_FP, _I, _I, _FP, _I, _I, _I])
+SIGS["orc_adalam_nearest"] = (None, [_FP, _I, _FP, _I, _I, _IP, _FP, _IP])
 SIGS["orc_vit_block"] = (None, [_FP * 12, _FP, _I, _I, _F])
 SIGS["orc_threads"] = (_I, [])
 SIGS["orc_set_threads"] = (None, [_I])
