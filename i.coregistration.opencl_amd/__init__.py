@@ -168,6 +168,9 @@ SIGNATURES = {
     "roma_dwconv5": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem]),
     "roma_gp_work_bytes": (C.c_size_t, [_I, _I]),
     "roma_gp_solve": (None, [_O, Mem, _I, _F, Mem, _I, Mem, Mem]),
+    "roma_prepare": (None, [_O, Mem, _I, _I, _I, Mem, _I, _I, _I]),
+    "roma_epilogue": (None, [_O, Mem, Mem, Mem, _L]),
+    "roma_sd": (None, [_O, Mem, _L, Mem, _L]),
     "disk_nms5x5": (None, [_O, Mem, _L, _I, _I, _I, _F, Mem]),
     "disk_gather_desc": (None, [_O, Mem, _I, _I, _I, Mem, _I, Mem]),
     "disk_topn_work_bytes": (C.c_size_t, [_I, _I]),

@@ -18,7 +18,12 @@
  *  - the Gaussian-process solve stays on the device in double precision
  *    (roma_gp_solve) instead of a host Cholesky;
  *  - the position embedding and the GP basis are made at alloc for the
- *    coarse side in use (560 by default, settable for tests). */
+ *    coarse side in use (560 by default, settable for tests);
+ *  - the input pair is uploaded once per match as given and resampled
+ *    (antialiased bicubic, ImageNet normalisation) on the device for
+ *    each pass (roma_prepare), and the certainty sigmoid, the bounds
+ *    test and v2's standard deviation run on the device before the
+ *    results are read (roma_epilogue, roma_sd). */
 
 #include <math.h>
 #include <stdio.h>
@@ -64,9 +69,6 @@ static const int ref2_radius[ROMA2_SCALES] = {3, 1, 0};
 /* VGG19-BN features: convolutions per block and their widths. */
 static const int vgg_blocks[4] = {2, 2, 4, 4};
 static const int vgg_width[4] = {64, 128, 256, 512};
-
-static const float im_mean[3] = {0.485f, 0.456f, 0.406f};
-static const float im_std[3] = {0.229f, 0.224f, 0.225f};
 
 /* ---- loading --------------------------------------------------------- */
 
@@ -635,9 +637,7 @@ extern "C" void roma_alloc(struct roma_model *m, int H, int W)
     m->flow = (float *)malloc(2 * (size_t)H * W * sizeof(float));
     m->cert = (float *)malloc((size_t)H * W * sizeof(float));
     m->sd = m->v2 ? (float *)malloc((size_t)H * W * sizeof(float)) : NULL;
-    m->in_c = (float *)malloc(2 * 3 * (size_t)m->coarse * m->coarse *
-                              sizeof(float));
-    m->in_f = (float *)malloc(2 * 3 * (size_t)H * W * sizeof(float));
+    m->raw = walloc(m, 2 * 3 * (size_t)H * W, "input pair");
     ICOREG_API_END
 }
 
@@ -875,87 +875,6 @@ static void refine2(struct roma_model *m, int j, int hs, int ws, int Hp, int Wp,
     roma2_update(m->ops, fl, cf, m->d_c, hs * ws, (float)ws, (float)hs);
 }
 
-/* ---- host stages ------------------------------------------------------ */
-
-/* Pillow's antialiased bicubic filter (a = -0.5): support 2 scaled by
- * the reduction, taps normalised per output (roma.c:1106-1167 resamples
- * with it to reproduce RoMa's PIL resize). */
-static double pil_cubic(double x)
-{
-    const double a = -0.5;
-
-    x = fabs(x);
-    if (x < 1)
-        return ((a + 2) * x - (a + 3)) * x * x + 1;
-    if (x < 2)
-        return (((x - 5) * x + 8) * x - 4) * a;
-    return 0;
-}
-
-/* Resample count lines of n_in samples (stride in_stride, lines in_step
- * apart) to n_out samples. */
-static void resample_axis(const float *in, int n_in, long in_stride,
-                          float *out, int n_out, long out_stride, int count,
-                          long in_step, long out_step)
-{
-    const double scale = (double)n_in / n_out, fs = scale > 1 ? scale : 1;
-    const double support = 2 * fs;
-
-    for (int o = 0; o < n_out; o++) {
-        const double center = (o + 0.5) * scale;
-        double k[64], ww = 0;
-        int lo = (int)(center - support + 0.5), hi, nt;
-
-        if (lo < 0)
-            lo = 0;
-        hi = (int)(center + support + 0.5);
-        if (hi > n_in)
-            hi = n_in;
-        nt = hi - lo;
-        if (nt > 64)
-            icoreg_fatal("RoMa: resampling ratio too large");
-        for (int x = 0; x < nt; x++) {
-            k[x] = pil_cubic((x + lo - center + 0.5) / fs);
-            ww += k[x];
-        }
-        for (int x = 0; x < nt; x++)
-            k[x] = ww != 0 ? k[x] / ww : 0;
-        for (int c = 0; c < count; c++) {
-            const float *src = in + c * in_step + (long)lo * in_stride;
-            double s = 0;
-
-            for (int x = 0; x < nt; x++)
-                s += k[x] * src[x * in_stride];
-            out[c * out_step + o * out_stride] = (float)s;
-        }
-    }
-}
-
-/* (3, H, W) in 0..1 to (3, h, w), ImageNet-normalised when imagenet is
- * set. roma.c:1169-1186. */
-static void prepare(const float *in, int H, int W, float *out, int h, int w,
-                    int imagenet)
-{
-    const size_t p = (size_t)h * w;
-
-    if (H == h && W == w)
-        memcpy(out, in, 3 * p * sizeof(float));
-    else {
-        float *tmp = (float *)malloc((size_t)H * w * sizeof(float));
-
-        for (int c = 0; c < 3; c++) {
-            resample_axis(in + (size_t)c * H * W, W, 1, tmp, w, 1, H, W, w);
-            resample_axis(tmp, H, w, out + c * p, h, w, w, 1, 1);
-        }
-        free(tmp);
-    }
-    if (!imagenet)
-        return;
-    for (int c = 0; c < 3; c++)
-        for (size_t i = 0; i < p; i++)
-            out[c * p + i] = (out[c * p + i] - im_mean[c]) / im_std[c];
-}
-
 /* ---- dumps (the reference's names, roma.c:1188-1227) --------------------- */
 
 static void dump_host(const char *dir, int tile, const char *what,
@@ -1083,69 +1002,44 @@ static void refiners2(struct roma_model *m, int p, int Hp, int Wp, int *h,
     }
 }
 
-/* Inputs of a pass: both images prepared at h x w into the host pair
- * staging and uploaded into m->img. */
-static void upload_pair(struct roma_model *m, const float *imgA,
-                        const float *imgB, int h, int w, float *stage)
+/* Both images (3, H, W) in 0..1 into m->raw, once per match. */
+static void upload_raw(struct roma_model *m, const float *imgA, const float *imgB)
 {
-    const size_t p = 3 * (size_t)h * w;
+    const size_t p = 3 * (size_t)m->H * m->W * sizeof(float);
 
-    prepare(imgA, m->H, m->W, stage, h, w, m->imagenet);
-    prepare(imgB, m->H, m->W, stage + p, h, w, m->imagenet);
-    ocl_write(m->ocl, m->img, 0, stage, 2 * p * sizeof(float));
+    ocl_write(m->ocl, m->raw, 0, imgA, p);
+    ocl_write(m->ocl, m->raw, p, imgB, p);
 }
 
-/* Host epilogue: sigmoid certainty (attenuated by the coarse one in v1),
- * zero where the warp leaves image B, warp clamped. roma.c:1328-1349,
- * 1413-1429. */
-static void epilogue(struct roma_model *m, const float *low)
+/* Inputs of a pass: both images resampled to h x w (and normalised) on
+ * the device into m->img. */
+static void prepare_pair(struct roma_model *m, int h, int w)
 {
-    const size_t hw = (size_t)m->H * m->W;
-
-    for (size_t i = 0; i < hw; i++) {
-        float c = m->cert[i] - (low && low[i] < 0 ? 0.5f * low[i] : 0.0f);
-        float *fx = m->flow + i, *fy = m->flow + hw + i;
-
-        c = 1.0f / (1.0f + expf(-c));
-        if (fabsf(*fx) > 1 || fabsf(*fy) > 1)
-            c = 0;
-        *fx = *fx < -1 ? -1 : *fx > 1 ? 1 : *fx;
-        *fy = *fy < -1 ? -1 : *fy > 1 ? 1 : *fy;
-        m->cert[i] = c;
-    }
+    roma_prepare(m->ops, m->raw, 2, m->H, m->W, m->img, h, w, m->imagenet);
 }
 
-static void match_v2(struct roma_model *m, int cur, const float *imgA,
-                     const float *imgB, const char *dump, int tile)
+static void match_v2(struct roma_model *m, int cur, const char *dump, int tile)
 {
     const size_t hw = (size_t)m->H * m->W;
     int h = side(m, m->coarse, 1), w = side(m, m->coarse, 1);
     const size_t n = (size_t)h * w;
-    float *prec;
 
     ocl_fill(m->ocl, m->cf[cur], 0, 4 * n, 0.0f);
     ocl_copy(m->ocl, m->ce[cur], 0, m->cf[cur], 0, n * 4);
     refiners2(m, 0, m->coarse, m->coarse, &h, &w, &cur, 0, dump, tile);
-    upload_pair(m, imgA, imgB, m->H, m->W, m->in_f);
+    prepare_pair(m, m->H, m->W);
     if (dump) {
-        dump_host(dump, tile, "in_f_0", m->in_f, 3 * hw);
-        dump_host(dump, tile, "in_f_1", m->in_f + 3 * hw, 3 * hw);
+        dump_dev(m, dump, tile, "in_f_0", m->img, 0, 3 * hw);
+        dump_dev(m, dump, tile, "in_f_1", m->img, 3 * hw, 3 * hw);
     }
     vgg2(m, m->H, m->W);
     refiners2(m, 1, m->H, m->W, &h, &w, &cur, 1, dump, tile);
+    /* cf[cur]: the certainty logit, then the three precision entries. */
+    roma_sd(m->ops, m->cf[cur], (long)hw, m->lowres, (long)hw);
+    roma_epilogue(m->ops, m->fl[cur], m->cf[cur], NULL, (long)hw);
     ocl_read(m->ocl, m->fl[cur], 0, m->flow, 2 * hw * sizeof(float));
     ocl_read(m->ocl, m->cf[cur], 0, m->cert, hw * sizeof(float));
-    prec = (float *)malloc(3 * hw * sizeof(float));
-    ocl_read(m->ocl, m->cf[cur], hw * sizeof(float), prec,
-             3 * hw * sizeof(float));
-    for (size_t i = 0; i < hw; i++) {
-        const double det = (double)prec[i] * prec[2 * hw + i] -
-                           (double)prec[hw + i] * prec[hw + i];
-
-        m->sd[i] = det > 0 ? (float)pow(det, -0.25) : NAN;
-    }
-    free(prec);
-    epilogue(m, NULL);
+    ocl_read(m->ocl, m->lowres, 0, m->sd, hw * sizeof(float));
     if (dump) {
         dump_host(dump, tile, "flow", m->flow, 2 * hw);
         dump_host(dump, tile, "cert", m->cert, hw);
@@ -1202,14 +1096,15 @@ extern "C" void roma_match(struct roma_model *m, const float *imgA,
     if (!m->H)
         icoreg_fatal("roma_match before roma_alloc");
     /* Coarse pass. */
-    upload_pair(m, imgA, imgB, m->coarse, m->coarse, m->in_c);
+    upload_raw(m, imgA, imgB);
+    prepare_pair(m, m->coarse, m->coarse);
     vgg(m, m->coarse, m->coarse, m->img);
     if (m->v2)
         vgg2(m, m->coarse, m->coarse);
     dino_pair(m, m->img);
     if (dump) {
-        dump_host(dump, tile, "in_c_0", m->in_c, pc);
-        dump_host(dump, tile, "in_c_1", m->in_c + pc, pc);
+        dump_dev(m, dump, tile, "in_c_0", m->img, 0, pc);
+        dump_dev(m, dump, tile, "in_c_1", m->img, pc, pc);
         dump_dino(m, dump, tile);
     }
     gp(m);
@@ -1224,14 +1119,14 @@ extern "C" void roma_match(struct roma_model *m, const float *imgA,
     refiners(m, 0, 0, m->v2 ? 2 : ROMA_SCALES, m->coarse, m->coarse, 1.0f,
              &cur, dump, tile);
     if (m->v2) {
-        match_v2(m, cur, imgA, imgB, dump, tile);
+        match_v2(m, cur, dump, tile);
         goto done;
     }
     /* Fine pass at the tile's size from the coarse pass's finest warp. */
-    upload_pair(m, imgA, imgB, m->H, m->W, m->in_f);
+    prepare_pair(m, m->H, m->W);
     if (dump) {
-        dump_host(dump, tile, "in_f_0", m->in_f, 3 * hw);
-        dump_host(dump, tile, "in_f_1", m->in_f + 3 * hw, 3 * hw);
+        dump_dev(m, dump, tile, "in_f_0", m->img, 0, 3 * hw);
+        dump_dev(m, dump, tile, "in_f_1", m->img, 3 * hw, 3 * hw);
     }
     vgg(m, m->H, m->W, m->img);
     ops_resize(m->ops, m->fl[cur], 2, m->coarse, m->coarse, m->fl[!cur],
@@ -1242,15 +1137,9 @@ extern "C" void roma_match(struct roma_model *m, const float *imgA,
     refiners(m, 1, 1, ROMA_SCALES, m->H, m->W, sf, &cur, dump, tile);
     ops_resize(m->ops, m->cert16, 1, m->c16, m->c16, m->lowres, m->H, m->W, 0,
                0, 0.0f);
+    roma_epilogue(m->ops, m->fl[cur], m->ce[cur], m->lowres, (long)hw);
     ocl_read(m->ocl, m->fl[cur], 0, m->flow, 2 * hw * sizeof(float));
     ocl_read(m->ocl, m->ce[cur], 0, m->cert, hw * sizeof(float));
-    {
-        float *low = (float *)malloc(hw * sizeof(float));
-
-        ocl_read(m->ocl, m->lowres, 0, low, hw * sizeof(float));
-        epilogue(m, low);
-        free(low);
-    }
     if (dump) {
         dump_host(dump, tile, "flow", m->flow, 2 * hw);
         dump_host(dump, tile, "cert", m->cert, hw);
@@ -1296,7 +1185,7 @@ extern "C" void roma_free(struct roma_model *m)
                      &m->gp_work, &m->gp_info,  &m->d_a,     &m->d_b,
                      &m->d_c,     &m->fl[0],    &m->fl[1],   &m->ce[0],
                      &m->ce[1],   &m->cf[0],    &m->cf[1],   &m->cert16,
-                     &m->lowres};
+                     &m->lowres,  &m->raw};
 
     if (m->ocl && m->ocl->stream)
         ocl_finish(m->ocl);
@@ -1336,7 +1225,5 @@ extern "C" void roma_free(struct roma_model *m)
     free(m->flow);
     free(m->cert);
     free(m->sd);
-    free(m->in_c);
-    free(m->in_f);
     memset(m, 0, sizeof(*m));
 }

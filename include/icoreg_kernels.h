@@ -63,6 +63,25 @@ void eloftr_fine_half(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
  * Warps are channel-major (2, n): x then y, normalised to -1..1 with
  * align_corners = 0 (cell centres at -1 + (2 i + 1) / size). */
 
+/* nimg images (3, H, W) in 0..1, consecutive in `in`, resampled to
+ * (3, h, w) into `out` with Pillow's antialiased bicubic filter (Keys'
+ * cubic, a = -0.5, support scaled by the reduction; width pass first,
+ * sums in double) and ImageNet-normalised when imagenet is set: the
+ * host's prepare of roma.c:1106-1186. Reductions up to 15.5x per axis.
+ * Uses the ops work buffer. */
+void roma_prepare(struct ops *o, cl_mem in, int nimg, int H, int W, cl_mem out,
+                  int h, int w, int imagenet);
+
+/* The host epilogue of roma.c:1328-1349,1413-1429 on hw cells in place:
+ * certainty c -= 0.5 low where low < 0 (low may be NULL: v2),
+ * sigmoid, 0 where the warp leaves [-1, 1]^2; warp (2, hw) clamped. */
+void roma_epilogue(struct ops *o, cl_mem flow, cl_mem cert, cl_mem low, long hw);
+
+/* RoMa v2's standard deviation (roma.c:1330-1339): det = p0 p2 - p1^2 of
+ * the precision planes (3, hw) at float offset poff of prec, in double;
+ * det^-0.25, or NaN where det <= 0. */
+void roma_sd(struct ops *o, cl_mem prec, long poff, cl_mem sd, long hw);
+
 /* Euclidean norm of each row of X (rows x C). roma_kernels.cl:9-23. */
 void roma_row_norm(struct ops *o, cl_mem X, int rows, int C, cl_mem out);
 

@@ -103,7 +103,7 @@ struct roma_model {
      * -1..1 in image B, certainty (H, W) in 0..1, and with v2 the
      * predicted standard deviation sd (H, W) in cells. */
     float *flow, *cert, *sd;
-    float *in_c, *in_f; /* normalised inputs of both passes (pairs) */
+    cl_mem raw; /* 2 x 3 x H x W: the pair as given, resampled on the device */
     int last;           /* fl / ce index holding roma_refine_device's result */
 };
 

@@ -197,3 +197,72 @@ def test_dwconv5(dev, ic, orc, C, H, W):
     bx, bw, bb, bo = dev.upload(x), dev.upload(w), dev.upload(b), dev.zeros(C * H * W)
     dev.api.roma_dwconv5(dev.po, bx.mem, C, H, W, bw.mem, bb.mem, bo.mem)
     assert rel(dev.read(bo), ref) < TOL
+
+
+@pytest.mark.parametrize("H,W,h,w,nimg,imagenet", [
+    (1024, 1024, 560, 560, 2, 1), (864, 864, 560, 560, 2, 1), (640, 480, 560, 560, 1, 0),
+    (64, 64, 112, 112, 2, 1), (100, 70, 56, 84, 1, 1), (2048, 1000, 140, 112, 1, 0),
+    (64, 96, 64, 96, 2, 1), (37, 45, 37, 45, 1, 0)])
+def test_prepare_vs_oracle(dev, ic, orc, H, W, h, w, nimg, imagenet):
+    """roma_prepare (the host prepare of roma.c:1106-1186 on the device)
+    against orc_roma_prepare image by image: the filter weights and sums
+    are the same double arithmetic, so the results agree to float32
+    rounding at most (bar 1e-6 of the largest magnitude, the north
+    star's 1e-4 for elementwise work); reductions, enlargements, mixed
+    axes, 15x, same size (normalisation only), ImageNet on and off."""
+    print(f"[roma] prepare {H}x{W} -> {h}x{w} nimg={nimg} imagenet={imagenet}", flush=True)
+    rng = np.random.default_rng(H + W + h)
+    img = rng.uniform(0, 1, (nimg, 3, H, W)).astype(np.float32)
+    img[:, :, H // 3:H // 3 + 5, :] = 1.0  # a sharp edge: negative lobes, overshoot
+    ref = np.zeros((nimg, 3, h, w), np.float32)
+    for k in range(nimg):
+        orc.orc_roma_prepare(fp(np.ascontiguousarray(img[k])), H, W, fp(ref[k]), h, w, imagenet)
+    bi, bo = dev.upload(img), dev.zeros(nimg * 3 * h * w)
+    dev.api.roma_prepare(dev.po, bi.mem, nimg, H, W, bo.mem, h, w, imagenet)
+    got = dev.read(bo).reshape(nimg, 3, h, w)
+    assert rel(got, ref) < 1e-6
+    assert (got == ref).mean() > 0.999
+
+
+def test_prepare_rejects_large_reductions(dev, ic):
+    bi, bo = dev.zeros(3 * 1600 * 16), dev.zeros(3 * 100)
+    with pytest.raises(ic.IcoregError, match="15.5"):
+        dev.api.roma_prepare(dev.po, bi.mem, 1, 1600, 16, bo.mem, 100, 1, 0)
+
+
+def test_epilogue_and_sd(dev, ic):
+    """roma_epilogue and roma_sd against float64 statements of the host
+    loops (roma.c:1330-1349, 1415-1428): attenuation by the negative
+    coarse certainty (v1) or none (v2), sigmoid, zero outside [-1, 1]^2,
+    clamped warp with NaN kept, det^-0.25 or NaN."""
+    rng = np.random.default_rng(2)
+    hw = 70001
+    flow = rng.uniform(-1.3, 1.3, (2, hw)).astype(np.float32)
+    flow[0, :7] = [np.nan, 1.0, -1.0, 1.0000001, np.inf, -np.inf, 0.5]
+    cert = rng.normal(0, 4, hw).astype(np.float32)
+    low = rng.normal(0, 2, hw).astype(np.float32)
+    for use_low in (True, False):
+        bf, bc, bl = dev.upload(flow), dev.upload(cert), dev.upload(low)
+        dev.api.roma_epilogue(dev.po, bf.mem, bc.mem, bl.mem if use_low else None, hw)
+        gf, gc = dev.read(bf).reshape(2, hw), dev.read(bc)
+        c = cert.astype(np.float64) - (np.where(low < 0, 0.5 * low, 0) if use_low else 0)
+        c = 1 / (1 + np.exp(-c))
+        with np.errstate(invalid="ignore"):
+            out = (np.abs(flow[0]) > 1) | (np.abs(flow[1]) > 1)
+        c[out] = 0
+        assert np.abs(gc - c).max() < 1e-6
+        assert np.array_equal(np.isnan(gf), np.isnan(flow))
+        ok = ~np.isnan(flow)
+        assert np.array_equal(gf[ok], np.clip(flow, -1, 1)[ok])
+    prec = rng.normal(0, 1, (3, hw)).astype(np.float32)
+    prec[0] = np.abs(prec[0]) + 0.1
+    prec[2] = np.abs(prec[2]) + 0.1
+    bp, bs = dev.upload(np.concatenate([np.zeros(hw, np.float32), prec.ravel()])), dev.zeros(hw)
+    dev.api.roma_sd(dev.po, bp.mem, hw, bs.mem, hw)
+    gs = dev.read(bs)
+    p = prec.astype(np.float64)
+    det = p[0] * p[2] - p[1] * p[1]
+    assert (det <= 0).any() and (det > 0).any()
+    assert np.array_equal(np.isnan(gs), det <= 0)
+    pos = det > 0
+    assert np.abs(gs[pos] / det[pos] ** -0.25 - 1).max() < 1e-6
