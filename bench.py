@@ -292,9 +292,10 @@ def time_launches(dev, fn, reps=20):
 
 
 def bench_hbm_kernels(ic, dev, H=864, W=864):
-    """The refiner sampling kernels alone at the refiner config's shapes
-    (864 x 864: s8, s4, s2, s1): warp sample and local correlation on
-    seeded features and a smooth warp, each timed over 20 launches;
+    """The memory-bound kernels alone at their config shapes: the refiner
+    stack's (864 x 864: s8, s4, s2, s1) warp sample, local correlation
+    and depthwise 5 x 5, grid_sample at s8, on seeded features and a
+    smooth warp; DISK's NMS at 512 x 512. Each timed over 20 launches;
     achieved GB/s = compulsory bytes / mean launch time."""
     out = []
     rng = np.random.default_rng(7)
@@ -323,8 +324,46 @@ def bench_hbm_kernels(ic, dev, H=864, W=864):
             out.append({"kernel": "local_corr", "scale": s, "C": feat, "r": r, "cells": n,
                         "ms": round(ms, 5), "bytes": b, "GBps": round(b / ms / 1e6, 1),
                         "frac_hbm": round(b / ms / 1e6 / PEAK_HBM, 4)})
-        for x in (f1, f2, flow, d):
-            x.release()
+        # The refiner's depthwise 5 x 5 on its input width at this scale
+        # (2 feat + emb + (2 r + 1)^2 channels): reads and writes it once.
+        cin = 2 * feat + emb + (2 * r + 1) ** 2 * (r > 0)
+        x = dev.upload(rng.standard_normal((cin, n), np.float32))
+        y = dev.zeros(cin * n)
+        wdw, bdw = dev.upload(rng.standard_normal((cin, 25), np.float32)), dev.zeros(cin)
+        ms = time_launches(dev, lambda: api.roma_dwconv5(po, x.mem, cin, h, w, wdw.mem, bdw.mem,
+                                                         y.mem))
+        b = 2 * 4 * cin * n + 26 * 4 * cin
+        out.append({"kernel": "dwconv5", "scale": s, "C": cin, "cells": n,
+                    "ms": round(ms, 5), "bytes": b, "GBps": round(b / ms / 1e6, 1),
+                    "frac_hbm": round(b / ms / 1e6 / PEAK_HBM, 4)})
+        for t in (f1, f2, flow, d, x, y, wdw, bdw):
+            t.release()
+    # grid_sample (ops.cl's contract) at the s8 shape on a smooth warp.
+    C8, h8 = 512, H // 8
+    n8 = h8 * h8
+    gx = (2 * (np.arange(h8) + 0.5) / h8 - 1)[None, :] + 0 * np.arange(h8)[:, None]
+    gy = (2 * (np.arange(h8) + 0.5) / h8 - 1)[:, None] + 0 * np.arange(h8)[None, :]
+    g = np.stack([gx + 0.03 * np.sin(gy * 3), gy + 0.03 * np.cos(gx * 2)], -1)
+    src, grid = dev.upload(rng.standard_normal((C8, n8), np.float32)), \
+        dev.upload(np.ascontiguousarray(g.reshape(n8, 2), np.float32))
+    dst = dev.zeros(C8 * n8)
+    ms = time_launches(dev, lambda: api.ops_grid_sample(po, src.mem, C8, h8, h8, grid.mem, n8, 0,
+                                                        dst.mem))
+    b = 8 * C8 * n8 + 8 * n8
+    out.append({"kernel": "grid_sample", "scale": 8, "C": C8, "cells": n8, "ms": round(ms, 5),
+                "bytes": b, "GBps": round(b / ms / 1e6, 1),
+                "frac_hbm": round(b / ms / 1e6 / PEAK_HBM, 4)})
+    # DISK's NMS on the 512 x 512 heatmap: reads it, writes the byte mask.
+    heat = dev.upload(rng.standard_normal(512 * 512).astype(np.float32))
+    mask = dev.zeros(512 * 512 // 4)
+    ms = time_launches(dev, lambda: api.disk_nms5x5(po, heat.mem, 0, 512, 512, 512, 0.0,
+                                                    mask.mem))
+    b = 5 * 512 * 512
+    out.append({"kernel": "nms5x5", "C": 1, "cells": 512 * 512, "ms": round(ms, 5),
+                "bytes": b, "GBps": round(b / ms / 1e6, 1),
+                "frac_hbm": round(b / ms / 1e6 / PEAK_HBM, 4)})
+    for t in (src, grid, dst, heat, mask):
+        t.release()
     return out
 
 
@@ -370,6 +409,137 @@ def cpu_adalam(n=2048, dim=128):
     return {"value": round(dt * 1e3, 3), "unit": "ms", "cores": int(orc.orc_threads()),
             "kind": "port", "sample": f"oracle/ orc_adalam_nearest on the same {n} x {n} x {dim} "
                                       f"sets, one run, {thr} OpenMP threads"}
+
+
+REF_DIR = ROOT / "oracle" / "_ref"
+REF_CASES = ["vitblock:1601", "gemm:1601:3072:1024:1", "gemm:1601:4096:1024:1",
+             "gemm:1601:1024:4096:1", "attention:400:400:8:32",
+             "localcorr:512:108:108:3", "localcorr:256:216:216:2",
+             "warpsample:512:108:108", "warpsample:256:216:216", "warpsample:64:432:432",
+             "warpsample:9:864:864", "gridsample:512:108:108:11664"]
+
+
+def _ours_case(ic, dev, case):
+    """This library's kernels on a reference case's shapes: the mean ms of
+    one launch (one block schedule for vitblock), HIP events."""
+    kind, *a = case.split(":")
+    a = [int(x) for x in a]
+    rng = np.random.default_rng(1)
+    api, po = dev.api, dev.po
+    keep = []
+
+    def up(*shape, s=1.0):
+        b = dev.upload((s * rng.uniform(-1, 1, shape)).astype(np.float32))
+        keep.append(b)
+        return b
+
+    def zeros(n):
+        b = dev.zeros(n)
+        keep.append(b)
+        return b
+
+    if kind == "gemm":
+        M, N, K, tb = a
+        A, B, Cb = up(M, K), up(N, K) if tb else up(K, N), zeros(M * N)
+        fn = lambda: api.ops_gemm(po, M, N, K, ic.mat(A, 0, K), ic.mat(B, 0, K if tb else N), tb,
+                                  ic.mat(Cb, 0, N), 1, 1, None, 0, None, 0, 1.0, 0, 0.0)
+    elif kind == "vitblock":
+        N, D = a[0], 1024
+        x, t, qkv = up(N, D), zeros(N * D), zeros(N * 3 * D)
+        o, h = zeros(N * D), zeros(N * 4 * D)
+        wq, wp, w1, w2 = up(3 * D, D, s=0.03), up(D, D, s=0.03), up(4 * D, D, s=0.03), \
+            up(D, 4 * D, s=0.03)
+        bb, gg = up(4 * D, s=0.1), up(D)
+
+        def fn():
+            api.ops_layernorm(po, N, D, x.mem, t.mem, gg.mem, bb.mem, 1e-6, 0, 0.0)
+            api.ops_linear(po, N, D, 3 * D, t.mem, 0, wq.mem, bb.mem, qkv.mem, 0, 0, 0.0, 0)
+            api.ops_attention(po, ic.mat(qkv, 0, 3 * D), ic.mat(qkv, D, 3 * D),
+                              ic.mat(qkv, 2 * D, 3 * D), ic.mat(o, 0, D), N, N, 16, 64,
+                              0.125, None)
+            api.ops_linear(po, N, D, D, o.mem, 0, wp.mem, bb.mem, x.mem, 0, 0, 0.0, 1)
+            api.ops_layernorm(po, N, D, x.mem, t.mem, gg.mem, bb.mem, 1e-6, 0, 0.0)
+            api.ops_linear(po, N, D, 4 * D, t.mem, 0, w1.mem, bb.mem, h.mem, 0, 1, 0.0, 0)
+            api.ops_linear(po, N, 4 * D, D, h.mem, 0, w2.mem, bb.mem, x.mem, 0, 0, 0.0, 1)
+    elif kind == "attention":
+        Nq, Nk, nh, d = a
+        Q, K, V, O = up(Nq, nh * d), up(Nk, nh * d), up(Nk, nh * d), zeros(Nq * nh * d)
+        fn = lambda: api.ops_attention(po, ic.mat(Q, 0, nh * d), ic.mat(K, 0, nh * d),
+                                       ic.mat(V, 0, nh * d), ic.mat(O, 0, nh * d), Nq, Nk, nh,
+                                       d, 1.0 / np.sqrt(d), None)
+    elif kind in ("localcorr", "warpsample"):
+        Cc, hh, ww = a[:3]
+        n = hh * ww
+        gx = (2 * (np.arange(ww) + 0.5) / ww - 1)[None, :] + 0 * np.arange(hh)[:, None]
+        gy = (2 * (np.arange(hh) + 0.5) / hh - 1)[:, None] + 0 * np.arange(ww)[None, :]
+        fl = dev.upload(np.stack([gx + 0.03 * np.sin(gy * 3),
+                                  gy + 0.03 * np.cos(gx * 2)]).astype(np.float32))
+        keep.append(fl)
+        f1, f2 = up(Cc, n), up(Cc, n)
+        if kind == "localcorr":
+            r = a[3]
+            out = zeros((2 * r + 1) ** 2 * n)
+            fn = lambda: api.roma_local_corr(po, f1.mem, f2.mem, Cc, hh, ww, r, fl.mem,
+                                             out.mem, 0)
+        else:
+            out = zeros(Cc * n)
+            fn = lambda: api.roma_warp_sample(po, f2.mem, Cc, hh, ww, fl.mem, out.mem, 0)
+    elif kind == "gridsample":
+        Cc, H, W, n = a
+        src, out = up(Cc, H * W), zeros(Cc * n)
+        if n == H * W:  # a smooth warp of the same grid, as the reference case
+            gx = (2 * (np.arange(W) + 0.5) / W - 1)[None, :] + 0 * np.arange(H)[:, None]
+            gy = (2 * (np.arange(H) + 0.5) / H - 1)[:, None] + 0 * np.arange(W)[None, :]
+            g = np.stack([gx + 0.03 * np.sin(gy * 3), gy + 0.03 * np.cos(gx * 2)], -1)
+            grid = dev.upload(np.ascontiguousarray(g.reshape(n, 2), np.float32))
+            keep.append(grid)
+        else:
+            grid = up(n, 2, s=1.05)
+        fn = lambda: api.ops_grid_sample(po, src.mem, Cc, H, W, grid.mem, n, 0, out.mem)
+    else:
+        raise ValueError(case)
+    ms = time_launches(dev, fn, reps=10)
+    for b in keep:
+        b.release()
+    return ms
+
+
+def reference_same_gpu(ic, dev):
+    """The reference's own OpenCL kernels (ops.cl, roma_kernels.cl, built
+    by oracle/Makefile's `ref` target from the reference sources) on this
+    GPU through the ROCm OpenCL runtime, at the headline shapes, beside
+    this library's kernels on the same shapes. None when the reference
+    build is absent."""
+    exe = REF_DIR / "ref_ocl"
+    if not exe.exists():
+        return None
+    import subprocess
+    p = subprocess.run([str(exe), str(REF_DIR)] + REF_CASES, capture_output=True, text=True,
+                       timeout=300)
+    if p.returncode != 0:
+        return {"error": p.stderr.strip()[-500:]}
+    rows = []
+    for line in p.stdout.splitlines():
+        r = json.loads(line)
+        ours = _ours_case(ic, dev, r["case"])
+        row = {"case": r["case"], "reference_kernel": r["kernel"],
+               "reference_ms": round(r["ms"], 5), "ours_ms": round(ours, 5),
+               "speedup": round(r["ms"] / ours, 2), "reference_check_rel": r["check_rel"]}
+        if "gflop" in r:
+            row["reference_tflops"] = round(r["gflop"] / r["ms"], 2)
+            row["ours_tflops"] = round(r["gflop"] / ours, 2)
+        if "bytes" in r:
+            row["reference_GBps"] = round(r["bytes"] / r["ms"] / 1e6, 1)
+            row["ours_GBps"] = round(r["bytes"] / ours / 1e6, 1)
+        if "parts_ms" in r:
+            row["reference_parts_ms"] = r["parts_ms"]
+        rows.append(row)
+    return {"what": "the reference's ops.cl / roma_kernels.cl compiled for gfx950 and run "
+                    "through the ROCm OpenCL runtime on the same MI355X, argument conventions "
+                    "of its ops.c / roma.c dispatch, outputs checked in double; ours on the "
+                    "same shapes (vitblock: the reference's DINOv2 block schedule on one "
+                    "1601-token image against this library's)",
+            "cases": rows}
 
 
 def _kernel_table(table, steps):
@@ -550,6 +720,20 @@ def cpu_baseline_roma(coarse=560, blocks=2):
                       f"(x{fl['total'] / blk:.1f}); {thr} OpenMP threads, {nproc} CPUs visible"}
 
 
+def copy_calibration(dev, mib):
+    """One device-to-device copy of mib MiB: the known-size reference that
+    scales the HBM byte counters of a rocprofv3 --pmc run."""
+    nb = mib << 20
+    src, dst = dev.alloc(nb, "calibration"), dev.alloc(nb, "calibration")
+    dev.api.ocl_fill(dev.pb, src.mem, 0, nb // 4, 1.0)
+    dev.finish()
+    dev.api.ocl_copy(dev.pb, src.mem, 0, dst.mem, 0, nb)
+    dev.finish()
+    print(f"[bench] calibration copy of {mib} MiB done", file=sys.stderr, flush=True)
+    src.release()
+    dst.release()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -562,6 +746,11 @@ def main():
     ap.add_argument("--roma-only", action="store_true",
                     help="run only the RoMa leg and print its JSON object (for profiling)")
     ap.add_argument("--roma-steps", type=int, default=10)
+    ap.add_argument("--leg", choices=["refiners864", "v2ref1024", "disk512", "adalam_nn2048"],
+                    help="run only this extra leg and print its JSON (for profiling)")
+    ap.add_argument("--hbm-only", action="store_true",
+                    help="run only the memory-bound kernels' leg (and --copy-calib) and "
+                         "print its JSON (for counter profiles)")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the refiner, roma_v2ref, DISK and HBM-kernel legs")
     ap.add_argument("--copy-calib", type=int, default=0,
@@ -582,6 +771,21 @@ def main():
     dev = ic.Device("auto")
     print(f"[bench] {dev.name} ({dev.arch}), {dev.ocl.cu_count} CUs", file=sys.stderr, flush=True)
     wdir = Path(tempfile.gettempdir()) / "icoreg_bench"
+    if args.leg:
+        wd = Path(tempfile.gettempdir()) / "icoreg_bench"
+        fn = {"refiners864": lambda: bench_refiners(ic, dev, synth, wd, 10, 2, 2),
+              "v2ref1024": lambda: bench_v2ref(ic, dev, synth, wd, 3, 1),
+              "disk512": lambda: bench_disk(ic, dev, synth, wd, 20, 3),
+              "adalam_nn2048": lambda: bench_adalam(ic, dev)}[args.leg]
+        print(json.dumps({args.leg: fn()}), flush=True)
+        dev.close()
+        return
+    if args.hbm_only:
+        if args.copy_calib:
+            copy_calibration(dev, args.copy_calib)
+        print(json.dumps({"hbm_kernels": bench_hbm_kernels(ic, dev)}), flush=True)
+        dev.close()
+        return
     if args.roma_only:
         print(json.dumps(bench_roma(ic, dev, synth, wdir, args.roma_steps, 2,
                                     args.profile_steps)), flush=True)
@@ -609,15 +813,7 @@ def main():
     nm = int(res["nm"])
 
     if args.copy_calib:
-        nb = args.copy_calib << 20
-        src, dst = dev.alloc(nb, "calibration"), dev.alloc(nb, "calibration")
-        dev.api.ocl_fill(dev.pb, src.mem, 0, nb // 4, 1.0)
-        dev.finish()
-        dev.api.ocl_copy(dev.pb, src.mem, 0, dst.mem, 0, nb)
-        dev.finish()
-        print(f"[bench] calibration copy of {args.copy_calib} MiB done", file=sys.stderr, flush=True)
-        src.release()
-        dst.release()
+        copy_calibration(dev, args.copy_calib)
 
     # Per-kernel times over a few more steps (event pairs, no sync).
     dev.profile_reset()
@@ -705,6 +901,9 @@ def main():
             roma["cpu_baseline"] = cpu_baseline_roma()
         if "adalam_nn2048" in extra:
             extra["adalam_nn2048"]["cpu_baseline"] = cpu_adalam()
+        print("[bench] baseline: the reference's OpenCL kernels on this GPU", file=sys.stderr,
+              flush=True)
+        extra["reference_opencl_same_gpu"] = reference_same_gpu(ic, dev)
 
     line = {
         "metric": "tile-pairs/sec (1 GPU) ELoFTR 640² & RoMa 560², fp32; % MFMA/HBM peak",

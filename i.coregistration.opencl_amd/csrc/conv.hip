@@ -326,6 +326,97 @@ __global__ void __launch_bounds__(256) conv_c1_kernel(const conv_args a)
     }
 }
 
+/* The last few output channels (at most FK_MAXK) of a layer whose
+ * channel count would leave a nearly empty MFMA block (DISK's last layer:
+ * 129 = 128 + 1 channels, where a second 128-channel block would repeat
+ * the whole layer's matrix work for one channel): one thread per output
+ * pixel of a 16 x 16 tile, FK_CC input channels' patches staged in LDS
+ * per step (normalised and gated exactly as conv_mfma loads them), the
+ * next step's patch values loaded into registers while this one is
+ * used, the nk filters in LDS. */
+#define FK_MAXK 8
+#define FK_MAXW 8192
+#define FK_CC 4
+template <int KS, int ST>
+__global__ void __launch_bounds__(256) conv_fewk_kernel(const conv_args a, int k0, int nk)
+{
+    constexpr int T = 16, P = (T - 1) * ST + KS, KK = KS * KS;
+    constexpr int PN = FK_CC * P * P, NP = (PN + 255) / 256;
+    __shared__ float ws[FK_MAXW];
+    __shared__ float patch[FK_CC][P][P + 1];
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    const int ox0 = blockIdx.x * T, oy0 = blockIdx.y * T;
+    const int iy0 = oy0 * ST - a.pad, ix0 = ox0 * ST - a.pad;
+    const long long HW = (long long)a.H * a.W;
+    const float *in = a.in + (long long)blockIdx.z * a.in_stride;
+    float acc[FK_MAXK], rp[NP];
+
+#pragma unroll
+    for (int k = 0; k < FK_MAXK; k++)
+        acc[k] = 0.0f;
+    for (int i = threadIdx.x; i < nk * a.C * KK; i += 256)
+        ws[i] = a.w[(long long)k0 * a.C * KK + i];
+    auto fetch = [&](int c0) {
+#pragma unroll
+        for (int q = 0; q < NP; q++) {
+            const int e = threadIdx.x + 256 * q, cc = e / (P * P), rem = e - cc * (P * P);
+            const int py = rem / P, px = rem - py * P, iy = iy0 + py, ix = ix0 + px;
+            const int c = c0 + cc;
+            float v = 0.0f;
+
+            if (e < PN && c < a.C && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W) {
+                v = in[c * HW + (long long)iy * a.W + ix];
+                if (a.mean) {
+                    v = (v - a.mean[c]) * a.rstd[c];
+                    if (a.gate)
+                        v = v >= 0.0f ? v : a.gate[c] * v;
+                }
+            }
+            rp[q] = v;
+        }
+    };
+    fetch(0);
+    for (int c0 = 0; c0 < a.C; c0 += FK_CC) {
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < NP; q++) {
+            const int e = threadIdx.x + 256 * q, cc = e / (P * P), rem = e - cc * (P * P);
+
+            if (e < PN)
+                patch[cc][rem / P][rem % P] = rp[q];
+        }
+        __syncthreads();
+        if (c0 + FK_CC < a.C)
+            fetch(c0 + FK_CC);
+        for (int cc = 0; cc < FK_CC && c0 + cc < a.C; cc++)
+#pragma unroll
+            for (int i = 0; i < KS; i++)
+#pragma unroll
+                for (int j = 0; j < KS; j++) {
+                    const float x = patch[cc][ty * ST + i][tx * ST + j];
+
+#pragma unroll
+                    for (int k = 0; k < FK_MAXK; k++)
+                        if (k < nk)
+                            acc[k] = fmaf(ws[(k * a.C + c0 + cc) * KK + i * KS + j], x, acc[k]);
+                }
+    }
+    {
+        const int ox = ox0 + tx, oy = oy0 + ty;
+        float *out = a.out + (long long)blockIdx.z * a.out_stride;
+
+        if (ox >= a.Wo || oy >= a.Ho)
+            return;
+#pragma unroll
+        for (int k = 0; k < FK_MAXK; k++)
+            if (k < nk) {
+                const float v = acc[k] + (a.bias ? a.bias[k0 + k] : 0.0f);
+
+                out[((long long)(k0 + k) * a.Ho + oy) * a.Wo + ox] = icoreg_act(v, a.act, a.slope);
+            }
+    }
+}
+
 bool conv_direct_supported(int kh, int kw, int sy, int sx, int dy, int dx,
                            int groups)
 {
@@ -354,7 +445,21 @@ static void launch_cfg(const conv_args &a, int nb, hipStream_t s)
     constexpr int CC = BM == 128 ? 2 : 4;
     constexpr int TH = 64 * NJ / TW;
     const int tiles = ((a.Wo + TW - 1) / TW) * ((a.Ho + TH - 1) / TH);
+    const int rem = a.K % BM;
 
+    /* A last block of at most FK_MAXK channels goes to the side kernel. */
+    if (a.K > BM && rem <= FK_MAXK && (long long)rem * a.C * KS * KS <= FK_MAXW) {
+        conv_args m = a;
+
+        m.K = a.K - rem;
+        hipLaunchKernelGGL((conv_mfma<KS, ST, BM, TW, CC, NJ>),
+                           dim3(tiles, m.K / BM, nb), dim3(256), 0, s, m);
+        if (rem)
+            hipLaunchKernelGGL((conv_fewk_kernel<KS, ST>),
+                               dim3((a.Wo + 15) / 16, (a.Ho + 15) / 16, nb), dim3(256), 0,
+                               s, a, m.K, rem);
+        return;
+    }
     hipLaunchKernelGGL((conv_mfma<KS, ST, BM, TW, CC, NJ>),
                        dim3(tiles, (a.K + BM - 1) / BM, nb), dim3(256), 0, s,
                        a);

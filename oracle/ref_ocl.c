@@ -1,0 +1,669 @@
+/* SPDX-License-Identifier: Unlicense */
+
+/* ORACLE — measurement infrastructure only (bench.py's baseline leg):
+ * the reference's own OpenCL kernels on the MI355X. oracle/Makefile
+ * compiles ops.cl and roma_kernels.cl of i.coregistration.opencl, where
+ * they lie, to gfx950 code objects in oracle/_ref/ (clang, the options of
+ * ocl_backend.c:166-187); this program loads them through the ROCm
+ * OpenCL runtime, launches kernels with the argument conventions and
+ * work sizes of the reference's host dispatch (ops.c, roma.c), times
+ * each case with OpenCL profiling events, checks a sample of outputs
+ * against a double-precision recomputation (so that a mis-set argument
+ * cannot pass as a timing), and prints one JSON line per case.
+ *
+ *   ref_ocl DIR CASE...
+ *   CASE: gemm:M:N:K:transb      ops_gemm (ops.c:148-188), one product
+ *         vitblock:N             roma.c:675-713: DINOv2's block schedule
+ *                                (1024 wide, 16 heads) on one image
+ *         attention:Nq:Nk:nh:d   ops_attention (ops.c:443-474)
+ *         localcorr:C:h:w:r      roma_local_corr as roma.c:956-968
+ *         warpsample:C:h:w       roma_warp_sample as roma.c:936-945
+ *         gridsample:C:H:W:n     ops_grid_sample (ops.c:520-534); with
+ *                                n = H W the points of a smooth warp */
+
+#define CL_TARGET_OPENCL_VERSION 120
+#include <CL/cl.h>
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+static cl_context ctx;
+static cl_command_queue q;
+static cl_device_id devid;
+static cl_program prog_ops, prog_roma;
+
+static void die(const char *what, cl_int e)
+{
+    fprintf(stderr, "ref_ocl: %s failed (%d)\n", what, (int)e);
+    exit(2);
+}
+
+#define CK(call)                                                               \
+    do {                                                                       \
+        cl_int e_ = (call);                                                    \
+        if (e_ != CL_SUCCESS)                                                  \
+            die(#call, e_);                                                    \
+    } while (0)
+
+static cl_program load_program(const char *path)
+{
+    FILE *fp = fopen(path, "rb");
+    unsigned char *bin;
+    size_t n;
+    cl_int e, st;
+    cl_program p;
+
+    if (!fp) {
+        fprintf(stderr, "ref_ocl: cannot open %s\n", path);
+        exit(2);
+    }
+    fseek(fp, 0, SEEK_END);
+    n = (size_t)ftell(fp);
+    fseek(fp, 0, SEEK_SET);
+    bin = malloc(n);
+    if (fread(bin, 1, n, fp) != n)
+        die("fread", -1);
+    fclose(fp);
+    p = clCreateProgramWithBinary(ctx, 1, &devid, &n, (const unsigned char **)&bin, &st, &e);
+    if (e != CL_SUCCESS || st != CL_SUCCESS) {
+        fprintf(stderr, "ref_ocl: clCreateProgramWithBinary(%s): %d / %d\n", path, (int)e,
+                (int)st);
+        exit(2);
+    }
+    e = clBuildProgram(p, 1, &devid, "", NULL, NULL);
+    if (e != CL_SUCCESS) {
+        char log[8192] = "";
+
+        clGetProgramBuildInfo(p, devid, CL_PROGRAM_BUILD_LOG, sizeof(log) - 1, log, NULL);
+        fprintf(stderr, "ref_ocl: clBuildProgram(%s): %d\n%s\n", path, (int)e, log);
+        exit(2);
+    }
+    free(bin);
+    return p;
+}
+
+static cl_kernel kern(cl_program p, const char *name)
+{
+    cl_int e;
+    cl_kernel k = clCreateKernel(p, name, &e);
+
+    if (e != CL_SUCCESS)
+        die(name, e);
+    return k;
+}
+
+static cl_mem buf(size_t bytes, const void *host)
+{
+    cl_int e;
+    cl_mem m = clCreateBuffer(ctx, CL_MEM_READ_WRITE, bytes ? bytes : 4, NULL, &e);
+
+    if (e != CL_SUCCESS)
+        die("clCreateBuffer", e);
+    if (host)
+        CK(clEnqueueWriteBuffer(q, m, CL_TRUE, 0, bytes, host, 0, NULL, NULL));
+    return m;
+}
+
+static void readb(cl_mem m, size_t bytes, void *host)
+{
+    CK(clEnqueueReadBuffer(q, m, CL_TRUE, 0, bytes, host, 0, NULL, NULL));
+}
+
+/* Deterministic uniform values in [-s, s). */
+static unsigned long long rng_state = 88172645463325252ULL;
+
+static float urand(float s)
+{
+    rng_state ^= rng_state << 13;
+    rng_state ^= rng_state >> 7;
+    rng_state ^= rng_state << 17;
+    return s * (2.0f * (float)((rng_state >> 40) * (1.0 / 16777216.0)) - 1.0f);
+}
+
+static float *rand_host(size_t n, float s)
+{
+    float *h = malloc(n * sizeof(float) + 4);
+
+    for (size_t i = 0; i < n; i++)
+        h[i] = urand(s);
+    return h;
+}
+
+#define SET(k, i, v)                                                           \
+    do {                                                                       \
+        __typeof__(v) v_ = (v);                                                \
+        CK(clSetKernelArg(k, i, sizeof(v_), &v_));                             \
+    } while (0)
+
+/* Launch and return the kernel's duration in ms (profiling event). */
+static double launch(cl_kernel k, cl_uint dims, const size_t *g, const size_t *l)
+{
+    cl_event ev;
+    cl_ulong t0, t1;
+
+    CK(clEnqueueNDRangeKernel(q, k, dims, NULL, g, l, 0, NULL, &ev));
+    CK(clWaitForEvents(1, &ev));
+    CK(clGetEventProfilingInfo(ev, CL_PROFILING_COMMAND_START, sizeof(t0), &t0, NULL));
+    CK(clGetEventProfilingInfo(ev, CL_PROFILING_COMMAND_END, sizeof(t1), &t1, NULL));
+    clReleaseEvent(ev);
+    return (t1 - t0) * 1e-6;
+}
+
+/* ---- ops_gemm, ops.c:148-188 ------------------------------------------- */
+
+struct opnd {
+    cl_mem buf;
+    cl_long off;
+    cl_int ld;
+    cl_long s0, s1;
+};
+
+static cl_kernel k_gemm, k_gemm_big, k_softmax, k_layernorm, k_attention, k_grid;
+static cl_kernel k_corr, k_warp;
+static const char *last_gemm = "gemm";
+
+static double gemm(int M, int N, int K, struct opnd A, struct opnd B, int transb,
+                   struct opnd C, int nb, int nb1, cl_mem bias, int biasrow, cl_mem R,
+                   long roff, float alpha, int act)
+{
+    const int big = M >= 128 && N >= 64 && K % 4 == 0 && A.ld % 4 == 0 && A.off % 4 == 0 &&
+                    A.s0 % 4 == 0 && A.s1 % 4 == 0 && B.ld % 4 == 0 && B.off % 4 == 0 &&
+                    B.s0 % 4 == 0 && B.s1 % 4 == 0;
+    const int tile = big ? 128 : 64;
+    cl_kernel k = big ? k_gemm_big : k_gemm;
+    size_t g[3], l[3] = {16, 16, 1};
+
+    last_gemm = big ? "gemm_big" : "gemm";
+
+    SET(k, 0, (cl_int)M);
+    SET(k, 1, (cl_int)N);
+    SET(k, 2, (cl_int)K);
+    SET(k, 3, A.buf);
+    SET(k, 4, A.off);
+    SET(k, 5, A.ld);
+    SET(k, 6, A.s0);
+    SET(k, 7, A.s1);
+    SET(k, 8, B.buf);
+    SET(k, 9, B.off);
+    SET(k, 10, B.ld);
+    SET(k, 11, B.s0);
+    SET(k, 12, B.s1);
+    SET(k, 13, (cl_int)transb);
+    SET(k, 14, C.buf);
+    SET(k, 15, C.off);
+    SET(k, 16, C.ld);
+    SET(k, 17, C.s0);
+    SET(k, 18, C.s1);
+    SET(k, 19, (cl_int)nb1);
+    SET(k, 20, bias);
+    SET(k, 21, (cl_int)biasrow);
+    SET(k, 22, R);
+    SET(k, 23, (cl_long)roff);
+    SET(k, 24, (cl_float)alpha);
+    SET(k, 25, (cl_int)act);
+    SET(k, 26, (cl_float)0.0f);
+    g[0] = (size_t)((N + tile - 1) / tile) * 16;
+    g[1] = (size_t)((M + tile - 1) / tile) * 16;
+    g[2] = (size_t)nb;
+    return launch(k, 3, g, l);
+}
+
+static struct opnd mat(cl_mem b, long off, int ld, long s0)
+{
+    struct opnd o = {b, off, ld, s0, 0};
+
+    return o;
+}
+
+/* ops.c:397-410: a power of two from 32 up to 256, at least L. */
+static size_t row_group(int L)
+{
+    size_t l = 32;
+
+    while (l < 256 && (int)l < L)
+        l *= 2;
+    return l;
+}
+
+static double layernorm(long rows, int C, cl_mem X, cl_mem Y, cl_mem g, cl_mem b)
+{
+    size_t ls = row_group(C), gs = rows * ls;
+
+    SET(k_layernorm, 0, X);
+    SET(k_layernorm, 1, Y);
+    SET(k_layernorm, 2, g);
+    SET(k_layernorm, 3, b);
+    SET(k_layernorm, 4, (cl_int)C);
+    SET(k_layernorm, 5, (cl_float)1e-6f);
+    SET(k_layernorm, 6, (cl_int)0);
+    SET(k_layernorm, 7, (cl_float)0.0f);
+    return launch(k_layernorm, 1, &gs, &ls);
+}
+
+static double softmax(cl_mem S, long rows, int L)
+{
+    size_t ls = row_group(L), gs = rows * ls;
+
+    SET(k_softmax, 0, S);
+    SET(k_softmax, 1, (cl_int)L);
+    SET(k_softmax, 2, (cl_float)1.0f);
+    return launch(k_softmax, 1, &gs, &ls);
+}
+
+static int reps = 10;
+
+static void case_gemm(const char *spec, int M, int N, int K, int transb)
+{
+    const size_t na = (size_t)M * K, nbb = (size_t)K * N, nc = (size_t)M * N;
+    float *A = rand_host(na, 1.0f), *B = rand_host(nbb, 1.0f), *Ch = malloc(nc * 4);
+    cl_mem a = buf(na * 4, A), b = buf(nbb * 4, B), c = buf(nc * 4, NULL);
+    double ms = 0, err = 0, ref = 0;
+
+    gemm(M, N, K, mat(a, 0, K, 0), mat(b, 0, transb ? K : N, 0), transb, mat(c, 0, N, 0), 1,
+         1, NULL, 0, NULL, 0, 1.0f, 0);
+    for (int r = 0; r < reps; r++)
+        ms += gemm(M, N, K, mat(a, 0, K, 0), mat(b, 0, transb ? K : N, 0), transb,
+                   mat(c, 0, N, 0), 1, 1, NULL, 0, NULL, 0, 1.0f, 0);
+    readb(c, nc * 4, Ch);
+    for (int s = 0; s < 64; s++) {
+        const size_t i = (size_t)(s * 7919) % M, j = (size_t)(s * 104729) % N;
+        double d = 0;
+
+        for (int kk = 0; kk < K; kk++)
+            d += (double)A[i * K + kk] * (transb ? B[j * K + kk] : B[(size_t)kk * N + j]);
+        err = fmax(err, fabs(d - Ch[i * N + j]));
+        ref = fmax(ref, fabs(d));
+    }
+    printf("{\"case\": \"%s\", \"kernel\": \"%s\", \"ms\": %.5f, \"gflop\": %.3f, "
+           "\"check_rel\": %.3g}\n",
+           spec, last_gemm, ms / reps, 2.0 * M * N * K / 1e9, err / fmax(ref, 1e-30));
+    clReleaseMemObject(a);
+    clReleaseMemObject(b);
+    clReleaseMemObject(c);
+    free(A);
+    free(B);
+    free(Ch);
+}
+
+/* roma.c:675-713 on one image of N tokens: LayerNorm, qkv, scores,
+ * softmax, values, proj + residual, LayerNorm, fc1 + GELU, fc2 +
+ * residual; ops_linear maps to ops_gemm with B the [out, in] weight. */
+static void case_vitblock(const char *spec, int N)
+{
+    const int D = 1024, H = 16, hd = 64;
+    const long nn = (long)N * N;
+    float *hx = rand_host((size_t)N * D, 1.0f), *w = rand_host((size_t)4 * D * D, 0.03f);
+    float *bvec = rand_host((size_t)4 * D, 0.1f), *g = rand_host(D, 1.0f);
+    cl_mem x = buf((size_t)N * D * 4, hx), t = buf((size_t)N * D * 4, NULL);
+    cl_mem qkv = buf((size_t)N * 3 * D * 4, NULL), s = buf((size_t)H * nn * 4, NULL);
+    cl_mem o = buf((size_t)N * D * 4, NULL), h = buf((size_t)N * 4 * D * 4, NULL);
+    cl_mem wq = buf((size_t)3 * D * D * 4, w), wp = buf((size_t)D * D * 4, w);
+    cl_mem w1 = buf((size_t)4 * D * D * 4, w), w2 = buf((size_t)4 * D * D * 4, w);
+    cl_mem bb = buf((size_t)4 * D * 4, bvec), gg = buf((size_t)D * 4, g);
+    double tot[9] = {0};
+    const char *names[9] = {"layernorm", "qkv", "scores", "softmax", "values", "proj",
+                            "layernorm2", "fc1", "fc2"};
+    float *hs = malloc((size_t)N * 4);
+
+    for (int r = -1; r < reps; r++) {
+        double e[9];
+
+        clEnqueueWriteBuffer(q, x, CL_TRUE, 0, (size_t)N * D * 4, hx, 0, NULL, NULL);
+        e[0] = layernorm(N, D, x, t, gg, bb);
+        e[1] = gemm(N, 3 * D, D, mat(t, 0, D, 0), mat(wq, 0, D, 0), 1, mat(qkv, 0, 3 * D, 0),
+                    1, 1, bb, 0, NULL, 0, 1.0f, 0);
+        e[2] = gemm(N, N, hd, mat(qkv, 0, 3 * D, hd), mat(qkv, D, 3 * D, hd), 1,
+                    mat(s, 0, N, nn), H, 1, NULL, 0, NULL, 0, 1.0f / sqrtf((float)hd), 0);
+        e[3] = softmax(s, (long)H * N, N);
+        e[4] = gemm(N, hd, N, mat(s, 0, N, nn), mat(qkv, 2 * D, 3 * D, hd), 0,
+                    mat(o, 0, D, hd), H, 1, NULL, 0, NULL, 0, 1.0f, 0);
+        e[5] = gemm(N, D, D, mat(o, 0, D, 0), mat(wp, 0, D, 0), 1, mat(x, 0, D, 0), 1, 1, bb,
+                    0, x, 0, 1.0f, 0);
+        e[6] = layernorm(N, D, x, t, gg, bb);
+        e[7] = gemm(N, 4 * D, D, mat(t, 0, D, 0), mat(w1, 0, D, 0), 1, mat(h, 0, 4 * D, 0), 1,
+                    1, bb, 0, NULL, 0, 1.0f, 1);
+        e[8] = gemm(N, D, 4 * D, mat(h, 0, 4 * D, 0), mat(w2, 0, 4 * D, 0), 1,
+                    mat(x, 0, D, 0), 1, 1, bb, 0, x, 0, 1.0f, 0);
+        if (r >= 0)
+            for (int i = 0; i < 9; i++)
+                tot[i] += e[i];
+    }
+    /* Check: the softmax rows of head 0, query 0 sum to one. */
+    readb(s, (size_t)N * 4, hs);
+    {
+        double sum = 0, all = 0;
+
+        for (int j = 0; j < N; j++)
+            sum += hs[j];
+        printf("{\"case\": \"%s\", \"kernel\": \"vit_block\", \"ms\": ", spec);
+        for (int i = 0; i < 9; i++)
+            all += tot[i] / reps;
+        printf("%.5f, \"parts_ms\": {", all);
+        for (int i = 0; i < 9; i++)
+            printf("%s\"%s\": %.5f", i ? ", " : "", names[i], tot[i] / reps);
+        printf("}, \"gflop\": %.3f, \"check_rel\": %.3g}\n",
+               (2.0 * N * D * 12 * D + 4.0 * H * (double)N * N * hd) / 1e9, fabs(sum - 1));
+    }
+    clReleaseMemObject(x);
+    clReleaseMemObject(t);
+    clReleaseMemObject(qkv);
+    clReleaseMemObject(s);
+    clReleaseMemObject(o);
+    clReleaseMemObject(h);
+    clReleaseMemObject(wq);
+    clReleaseMemObject(wp);
+    clReleaseMemObject(w1);
+    clReleaseMemObject(w2);
+    clReleaseMemObject(bb);
+    clReleaseMemObject(gg);
+    free(hx);
+    free(w);
+    free(bvec);
+    free(g);
+    free(hs);
+}
+
+static void case_attention(const char *spec, int Nq, int Nk, int nh, int d)
+{
+    const int ld = nh * d;
+    float *Q = rand_host((size_t)Nq * ld, 1.0f), *K = rand_host((size_t)Nk * ld, 1.0f);
+    float *V = rand_host((size_t)Nk * ld, 1.0f), *O = malloc((size_t)Nq * ld * 4);
+    cl_mem bq = buf((size_t)Nq * ld * 4, Q), bk = buf((size_t)Nk * ld * 4, K);
+    cl_mem bv = buf((size_t)Nk * ld * 4, V), bo = buf((size_t)Nq * ld * 4, NULL);
+    const float scale = 1.0f / sqrtf((float)d);
+    size_t gs[3] = {16, (size_t)(Nq + 15) / 16 * 16, (size_t)nh}, ls[3] = {16, 16, 1};
+    double ms = 0, err = 0, ref = 0;
+    const cl_long zero = 0;
+    const cl_mem none = NULL;
+
+    SET(k_attention, 0, bq);
+    SET(k_attention, 1, zero);
+    SET(k_attention, 2, (cl_int)ld);
+    SET(k_attention, 3, bk);
+    SET(k_attention, 4, zero);
+    SET(k_attention, 5, (cl_int)ld);
+    SET(k_attention, 6, bv);
+    SET(k_attention, 7, zero);
+    SET(k_attention, 8, (cl_int)ld);
+    SET(k_attention, 9, bo);
+    SET(k_attention, 10, zero);
+    SET(k_attention, 11, (cl_int)ld);
+    SET(k_attention, 12, (cl_int)Nq);
+    SET(k_attention, 13, (cl_int)Nk);
+    SET(k_attention, 14, (cl_int)d);
+    SET(k_attention, 15, (cl_float)scale);
+    SET(k_attention, 16, none);
+    launch(k_attention, 3, gs, ls);
+    for (int r = 0; r < reps; r++)
+        ms += launch(k_attention, 3, gs, ls);
+    readb(bo, (size_t)Nq * ld * 4, O);
+    for (int s = 0; s < 8; s++) {
+        const int i = (s * 7919) % Nq, h = s % nh;
+        double m = -1e300, sum = 0, *p = malloc((size_t)Nk * sizeof(double));
+
+        for (int j = 0; j < Nk; j++) {
+            double dot = 0;
+
+            for (int c = 0; c < d; c++)
+                dot += (double)Q[(size_t)i * ld + h * d + c] * K[(size_t)j * ld + h * d + c];
+            p[j] = dot * scale;
+            m = fmax(m, p[j]);
+        }
+        for (int j = 0; j < Nk; j++)
+            sum += p[j] = exp(p[j] - m);
+        for (int c = 0; c < d; c++) {
+            double v = 0;
+
+            for (int j = 0; j < Nk; j++)
+                v += p[j] * V[(size_t)j * ld + h * d + c];
+            v /= sum;
+            err = fmax(err, fabs(v - O[(size_t)i * ld + h * d + c]));
+            ref = fmax(ref, fabs(v));
+        }
+        free(p);
+    }
+    printf("{\"case\": \"%s\", \"kernel\": \"attention\", \"ms\": %.5f, \"gflop\": %.3f, "
+           "\"check_rel\": %.3g}\n",
+           spec, ms / reps, 4.0 * nh * (double)Nq * Nk * d / 1e9, err / fmax(ref, 1e-30));
+    clReleaseMemObject(bq);
+    clReleaseMemObject(bk);
+    clReleaseMemObject(bv);
+    clReleaseMemObject(bo);
+    free(Q);
+    free(K);
+    free(V);
+    free(O);
+}
+
+/* A smooth warp on the h x w grid (normalised coordinates). */
+static float *smooth_flow(int h, int w)
+{
+    float *f = malloc((size_t)2 * h * w * 4);
+
+    for (int y = 0; y < h; y++)
+        for (int x = 0; x < w; x++) {
+            const float gx = 2 * (x + 0.5f) / w - 1, gy = 2 * (y + 0.5f) / h - 1;
+
+            f[(size_t)y * w + x] = gx + 0.03f * sinf(gy * 3);
+            f[(size_t)h * w + (size_t)y * w + x] = gy + 0.03f * cosf(gx * 2);
+        }
+    return f;
+}
+
+static double bilin(const float *p, int H, int W, double x, double y)
+{
+    const double ix = ((x + 1) * W - 1) * 0.5, iy = ((y + 1) * H - 1) * 0.5;
+    const int x0 = (int)floor(ix), y0 = (int)floor(iy);
+    const double fx = ix - x0, fy = iy - y0;
+#define AT(yy, xx) ((xx) >= 0 && (xx) < W && (yy) >= 0 && (yy) < H ? p[(size_t)(yy) * W + (xx)] : 0.0)
+    return (1 - fy) * ((1 - fx) * AT(y0, x0) + fx * AT(y0, x0 + 1)) +
+           fy * ((1 - fx) * AT(y0 + 1, x0) + fx * AT(y0 + 1, x0 + 1));
+#undef AT
+}
+
+static void case_localcorr(const char *spec, int C, int h, int w, int r)
+{
+    const size_t n = (size_t)h * w;
+    const int side = 2 * r + 1;
+    float *f1 = rand_host(C * n, 1.0f), *f2 = rand_host(C * n, 1.0f), *fl = smooth_flow(h, w);
+    float *out = malloc((size_t)side * side * n * 4);
+    cl_mem b1 = buf(C * n * 4, f1), b2 = buf(C * n * 4, f2), bf = buf(2 * n * 4, fl);
+    cl_mem bo = buf((size_t)side * side * n * 4, NULL);
+    size_t gc = n * 64, lc = 64;
+    double ms = 0, err = 0, ref = 0;
+
+    if (C > 512 || r > 7) {
+        fprintf(stderr, "ref_ocl: localcorr needs C <= 512, r <= 7\n");
+        exit(2);
+    }
+    SET(k_corr, 0, b1);
+    SET(k_corr, 1, b2);
+    SET(k_corr, 2, (cl_int)C);
+    SET(k_corr, 3, (cl_int)h);
+    SET(k_corr, 4, (cl_int)w);
+    SET(k_corr, 5, (cl_int)r);
+    SET(k_corr, 6, bf);
+    SET(k_corr, 7, bo);
+    SET(k_corr, 8, (cl_int)0);
+    launch(k_corr, 1, &gc, &lc);
+    for (int t = 0; t < reps; t++)
+        ms += launch(k_corr, 1, &gc, &lc);
+    readb(bo, (size_t)side * side * n * 4, out);
+    for (int s = 0; s < 32; s++) {
+        const size_t i = (size_t)(s * 7919) % n;
+        /* Window offset k = (a, b), a the row: the warp moved by (b - r,
+         * a - r) cells, a cell being 2 / w by 2 / h in normalised units. */
+        for (int k = 0; k < side * side; k++) {
+            const double x = fl[i] + (k % side - r) * (2.0 / w);
+            const double y = fl[n + i] + (k / side - r) * (2.0 / h);
+            double v = 0;
+
+            for (int c = 0; c < C; c++)
+                v += (double)f1[c * n + i] * bilin(f2 + c * n, h, w, x, y);
+            v /= sqrt((double)C);
+            err = fmax(err, fabs(v - out[(size_t)k * n + i]));
+            ref = fmax(ref, fabs(v));
+        }
+    }
+    printf("{\"case\": \"%s\", \"kernel\": \"roma_local_corr\", \"ms\": %.5f, "
+           "\"bytes\": %.0f, \"check_rel\": %.3g}\n",
+           spec, ms / reps, 8.0 * C * n + 8.0 * n + 4.0 * side * side * n,
+           err / fmax(ref, 1e-30));
+    clReleaseMemObject(b1);
+    clReleaseMemObject(b2);
+    clReleaseMemObject(bf);
+    clReleaseMemObject(bo);
+    free(f1);
+    free(f2);
+    free(fl);
+    free(out);
+}
+
+static void case_warpsample(const char *spec, int C, int h, int w)
+{
+    const size_t n = (size_t)h * w;
+    float *in = rand_host(C * n, 1.0f), *fl = smooth_flow(h, w), *out = malloc(C * n * 4);
+    cl_mem bi = buf(C * n * 4, in), bf = buf(2 * n * 4, fl), bo = buf(C * n * 4, NULL);
+    size_t g2[2] = {n, (size_t)C};
+    double ms = 0, err = 0, ref = 0;
+
+    SET(k_warp, 0, bi);
+    SET(k_warp, 1, (cl_int)C);
+    SET(k_warp, 2, (cl_int)h);
+    SET(k_warp, 3, (cl_int)w);
+    SET(k_warp, 4, bf);
+    SET(k_warp, 5, bo);
+    SET(k_warp, 6, (cl_int)0);
+    launch(k_warp, 2, g2, NULL);
+    for (int t = 0; t < reps; t++)
+        ms += launch(k_warp, 2, g2, NULL);
+    readb(bo, C * n * 4, out);
+    for (int s = 0; s < 256; s++) {
+        const size_t i = (size_t)(s * 7919) % n, c = (size_t)(s * 31) % C;
+        const double v = bilin(in + c * n, h, w, fl[i], fl[n + i]);
+
+        err = fmax(err, fabs(v - out[c * n + i]));
+        ref = fmax(ref, fabs(v));
+    }
+    printf("{\"case\": \"%s\", \"kernel\": \"roma_warp_sample\", \"ms\": %.5f, "
+           "\"bytes\": %.0f, \"check_rel\": %.3g}\n",
+           spec, ms / reps, 8.0 * C * n + 8.0 * n, err / fmax(ref, 1e-30));
+    clReleaseMemObject(bi);
+    clReleaseMemObject(bf);
+    clReleaseMemObject(bo);
+    free(in);
+    free(fl);
+    free(out);
+}
+
+static void case_gridsample(const char *spec, int C, int H, int W, int n)
+{
+    float *in = rand_host((size_t)C * H * W, 1.0f), *grid = rand_host(2 * (size_t)n, 1.05f);
+
+    /* n = H W: the points of a smooth warp of the same grid (the
+     * refiners' access pattern), else uniform points. */
+    if ((size_t)n == (size_t)H * W) {
+        float *f = smooth_flow(H, W);
+
+        for (int i = 0; i < n; i++) {
+            grid[2 * i] = f[i];
+            grid[2 * i + 1] = f[(size_t)n + i];
+        }
+        free(f);
+    }
+    float *out = malloc((size_t)C * n * 4);
+    cl_mem bi = buf((size_t)C * H * W * 4, in), bg = buf(2 * (size_t)n * 4, grid);
+    cl_mem bo = buf((size_t)C * n * 4, NULL);
+    size_t g[2] = {(size_t)(n + 63) / 64 * 64, (size_t)C}, l[2] = {64, 1};
+    double ms = 0, err = 0, ref = 0;
+
+    SET(k_grid, 0, bi);
+    SET(k_grid, 1, (cl_int)C);
+    SET(k_grid, 2, (cl_int)H);
+    SET(k_grid, 3, (cl_int)W);
+    SET(k_grid, 4, bg);
+    SET(k_grid, 5, (cl_int)n);
+    SET(k_grid, 6, (cl_int)0);
+    SET(k_grid, 7, bo);
+    launch(k_grid, 2, g, l);
+    for (int t = 0; t < reps; t++)
+        ms += launch(k_grid, 2, g, l);
+    readb(bo, (size_t)C * n * 4, out);
+    for (int s = 0; s < 256; s++) {
+        const size_t i = (size_t)(s * 7919) % n, c = (size_t)(s * 31) % C;
+        const double v = bilin(in + c * H * W, H, W, grid[2 * i], grid[2 * i + 1]);
+
+        err = fmax(err, fabs(v - out[c * n + i]));
+        ref = fmax(ref, fabs(v));
+    }
+    printf("{\"case\": \"%s\", \"kernel\": \"grid_sample\", \"ms\": %.5f, \"bytes\": %.0f, "
+           "\"check_rel\": %.3g}\n",
+           spec, ms / reps, 4.0 * C * H * W + 8.0 * n + 4.0 * C * n, err / fmax(ref, 1e-30));
+    clReleaseMemObject(bi);
+    clReleaseMemObject(bg);
+    clReleaseMemObject(bo);
+    free(in);
+    free(grid);
+    free(out);
+}
+
+int main(int argc, char **argv)
+{
+    cl_platform_id plat;
+    cl_uint np = 0;
+    cl_int e;
+    char path[4096], name[256] = "";
+
+    if (argc < 3) {
+        fprintf(stderr, "usage: ref_ocl DIR CASE...\n");
+        return 2;
+    }
+    CK(clGetPlatformIDs(1, &plat, &np));
+    CK(clGetDeviceIDs(plat, CL_DEVICE_TYPE_GPU, 1, &devid, NULL));
+    clGetDeviceInfo(devid, CL_DEVICE_NAME, sizeof(name), name, NULL);
+    ctx = clCreateContext(NULL, 1, &devid, NULL, NULL, &e);
+    if (e != CL_SUCCESS)
+        die("clCreateContext", e);
+    q = clCreateCommandQueue(ctx, devid, CL_QUEUE_PROFILING_ENABLE, &e);
+    if (e != CL_SUCCESS)
+        die("clCreateCommandQueue", e);
+    snprintf(path, sizeof(path), "%s/ops.co", argv[1]);
+    prog_ops = load_program(path);
+    snprintf(path, sizeof(path), "%s/roma_kernels.co", argv[1]);
+    prog_roma = load_program(path);
+    k_gemm = kern(prog_ops, "gemm");
+    k_gemm_big = kern(prog_ops, "gemm_big");
+    k_softmax = kern(prog_ops, "softmax_rows");
+    k_layernorm = kern(prog_ops, "layernorm");
+    k_attention = kern(prog_ops, "attention");
+    k_grid = kern(prog_ops, "grid_sample");
+    k_corr = kern(prog_roma, "roma_local_corr");
+    k_warp = kern(prog_roma, "roma_warp_sample");
+    fprintf(stderr, "ref_ocl: device %s\n", name);
+    for (int i = 2; i < argc; i++) {
+        int a = 0, b = 0, c = 0, d = 0;
+
+        if (sscanf(argv[i], "gemm:%d:%d:%d:%d", &a, &b, &c, &d) == 4)
+            case_gemm(argv[i], a, b, c, d);
+        else if (sscanf(argv[i], "vitblock:%d", &a) == 1)
+            case_vitblock(argv[i], a);
+        else if (sscanf(argv[i], "attention:%d:%d:%d:%d", &a, &b, &c, &d) == 4)
+            case_attention(argv[i], a, b, c, d);
+        else if (sscanf(argv[i], "localcorr:%d:%d:%d:%d", &a, &b, &c, &d) == 4)
+            case_localcorr(argv[i], a, b, c, d);
+        else if (sscanf(argv[i], "warpsample:%d:%d:%d", &a, &b, &c) == 3)
+            case_warpsample(argv[i], a, b, c);
+        else if (sscanf(argv[i], "gridsample:%d:%d:%d:%d", &a, &b, &c, &d) == 4)
+            case_gridsample(argv[i], a, b, c, d);
+        else {
+            fprintf(stderr, "ref_ocl: unknown case %s\n", argv[i]);
+            return 2;
+        }
+        fflush(stdout);
+    }
+    clReleaseCommandQueue(q);
+    clReleaseContext(ctx);
+    return 0;
+}

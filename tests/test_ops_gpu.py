@@ -134,6 +134,13 @@ CONV_SHAPES = [
     # pieces, the partial channel block among the split ones).
     (1, 64, 80, 80, 192, 3, 1, 1, 0, 2),
     (2, 48, 30, 90, 200, 3, 1, 1, 0, 1),
+    # A last block of 1-8 output channels on the few-channel side kernel:
+    # DISK's last layer (129 = 128 + 1) at a size that takes 128-channel
+    # blocks, 64-channel blocks with 2, 3 and 6 left, strides 1 and 2.
+    (1, 80, 256, 200, 129, 5, 1, 2, 1, 0),
+    (2, 16, 41, 39, 66, 5, 2, 2, 1, 2),
+    (1, 24, 30, 34, 70, 3, 1, 1, 1, 1),
+    (1, 20, 25, 27, 67, 3, 2, 1, 0, 2),
     # One input channel (the per-pixel kernel): 5 x 5 and 3 x 3, stride 1.
     (1, 1, 37, 45, 20, 5, 1, 2, 0, 1),
     (2, 1, 30, 31, 16, 3, 1, 1, 0, 0),
