@@ -329,92 +329,146 @@ __global__ void __launch_bounds__(256) conv_c1_kernel(const conv_args a)
 /* The last few output channels (at most FK_MAXK) of a layer whose
  * channel count would leave a nearly empty MFMA block (DISK's last layer:
  * 129 = 128 + 1 channels, where a second 128-channel block would repeat
- * the whole layer's matrix work for one channel): one thread per output
- * pixel of a 16 x 16 tile, FK_CC input channels' patches staged in LDS
- * per step (normalised and gated exactly as conv_mfma loads them), the
- * next step's patch values loaded into registers while this one is
- * used, the nk filters in LDS. */
+ * the whole layer's matrix work for one channel). A block takes a 16 x 32
+ * output tile, each thread two vertically adjacent pixels (their windows
+ * share KS - 1 rows). The patches of 4 input channels (2 at stride 2)
+ * are staged in LDS per step, normalised and gated exactly as conv_mfma loads them, the
+ * next step's values loaded into registers while this one is used; a
+ * channel's NK filters are read from LDS once and used for both pixels. */
 #define FK_MAXK 8
 #define FK_MAXW 8192
-#define FK_CC 4
-template <int KS, int ST>
-__global__ void __launch_bounds__(256) conv_fewk_kernel(const conv_args a, int k0, int nk)
+#define FK_MAXC 1024
+template <int KS, int ST, int NK>
+__global__ void __launch_bounds__(256) conv_fewk_kernel(const conv_args a, int k0)
 {
-    constexpr int T = 16, P = (T - 1) * ST + KS, KK = KS * KS;
-    constexpr int PN = FK_CC * P * P, NP = (PN + 255) / 256;
+    constexpr int TW = 16, TH = 32, KK = KS * KS, FK_CC = ST == 1 ? 4 : 2;
+    constexpr int PW = (TW - 1) * ST + KS, PH = (TH - 1) * ST + KS;
+    constexpr int PN = FK_CC * PH * PW, NP = (PN + 255) / 256;
+    static_assert(NP <= 32, "validity mask");
     __shared__ float ws[FK_MAXW];
-    __shared__ float patch[FK_CC][P][P + 1];
+    __shared__ float nm[3][FK_MAXC]; /* mean, rstd, gate per input channel */
+    __shared__ float patch[FK_CC][PH][PW + 1];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    const int ox0 = blockIdx.x * T, oy0 = blockIdx.y * T;
+    const int ox0 = blockIdx.x * TW, oy0 = blockIdx.y * TH;
     const int iy0 = oy0 * ST - a.pad, ix0 = ox0 * ST - a.pad;
     const long long HW = (long long)a.H * a.W;
     const float *in = a.in + (long long)blockIdx.z * a.in_stride;
-    float acc[FK_MAXK], rp[NP];
+    float acc[2][NK], rp[NP];
+    unsigned valid = 0;
 
 #pragma unroll
-    for (int k = 0; k < FK_MAXK; k++)
-        acc[k] = 0.0f;
-    for (int i = threadIdx.x; i < nk * a.C * KK; i += 256)
+    for (int k = 0; k < NK; k++)
+        acc[0][k] = acc[1][k] = 0.0f;
+    for (int i = threadIdx.x; i < NK * a.C * KK; i += 256)
         ws[i] = a.w[(long long)k0 * a.C * KK + i];
+    if (a.mean)
+        for (int c = threadIdx.x; c < a.C; c += 256) {
+            nm[0][c] = a.mean[c];
+            nm[1][c] = a.rstd[c];
+            nm[2][c] = a.gate ? a.gate[c] : 1.0f;
+        }
+    /* Loads only, every one issued before any is used: out-of-range
+     * values read the channel's first element and are masked later. */
     auto fetch = [&](int c0) {
+        valid = 0;
 #pragma unroll
         for (int q = 0; q < NP; q++) {
-            const int e = threadIdx.x + 256 * q, cc = e / (P * P), rem = e - cc * (P * P);
-            const int py = rem / P, px = rem - py * P, iy = iy0 + py, ix = ix0 + px;
-            const int c = c0 + cc;
-            float v = 0.0f;
+            const int e = threadIdx.x + 256 * q, cc = e / (PH * PW), rem = e - cc * (PH * PW);
+            const int py = rem / PW, px = rem - py * PW, iy = iy0 + py, ix = ix0 + px;
+            const int c = min(c0 + cc, a.C - 1);
+            const bool ok = e < PN && c0 + cc < a.C && iy >= 0 && iy < a.H && ix >= 0 &&
+                            ix < a.W;
 
-            if (e < PN && c < a.C && iy >= 0 && iy < a.H && ix >= 0 && ix < a.W) {
-                v = in[c * HW + (long long)iy * a.W + ix];
-                if (a.mean) {
-                    v = (v - a.mean[c]) * a.rstd[c];
-                    if (a.gate)
-                        v = v >= 0.0f ? v : a.gate[c] * v;
-                }
-            }
-            rp[q] = v;
+            rp[q] = in[c * HW + (ok ? (long long)iy * a.W + ix : 0)];
+            valid |= ok ? 1u << q : 0u;
         }
     };
     fetch(0);
+    __syncthreads();
     for (int c0 = 0; c0 < a.C; c0 += FK_CC) {
-        __syncthreads();
 #pragma unroll
         for (int q = 0; q < NP; q++) {
-            const int e = threadIdx.x + 256 * q, cc = e / (P * P), rem = e - cc * (P * P);
+            const int e = threadIdx.x + 256 * q, cc = e / (PH * PW), rem = e - cc * (PH * PW);
+            const int c = min(c0 + cc, a.C - 1);
+            float v = rp[q];
 
+            if (a.mean) {
+                v = (v - nm[0][c]) * nm[1][c];
+                if (a.gate)
+                    v = v >= 0.0f ? v : nm[2][c] * v;
+            }
             if (e < PN)
-                patch[cc][rem / P][rem % P] = rp[q];
+                patch[cc][rem / PW][rem % PW] = valid >> q & 1u ? v : 0.0f;
         }
         __syncthreads();
         if (c0 + FK_CC < a.C)
             fetch(c0 + FK_CC);
-        for (int cc = 0; cc < FK_CC && c0 + cc < a.C; cc++)
+        for (int cc = 0; cc < FK_CC && c0 + cc < a.C; cc++) {
+            float wk[NK][KK];
+
 #pragma unroll
-            for (int i = 0; i < KS; i++)
+            for (int k = 0; k < NK; k++)
+#pragma unroll
+                for (int t = 0; t < KK; t++)
+                    wk[k][t] = ws[(k * a.C + c0 + cc) * KK + t];
+#pragma unroll
+            for (int i = 0; i < KS + ST; i++)
 #pragma unroll
                 for (int j = 0; j < KS; j++) {
-                    const float x = patch[cc][ty * ST + i][tx * ST + j];
+                    const float x = patch[cc][2 * ty * ST + i][tx * ST + j];
 
 #pragma unroll
-                    for (int k = 0; k < FK_MAXK; k++)
-                        if (k < nk)
-                            acc[k] = fmaf(ws[(k * a.C + c0 + cc) * KK + i * KS + j], x, acc[k]);
+                    for (int k = 0; k < NK; k++) {
+                        if (i < KS)
+                            acc[0][k] = fmaf(wk[k][i * KS + j], x, acc[0][k]);
+                        if (i >= ST)
+                            acc[1][k] = fmaf(wk[k][(i - ST) * KS + j], x, acc[1][k]);
+                    }
                 }
+        }
+        __syncthreads();
     }
     {
-        const int ox = ox0 + tx, oy = oy0 + ty;
+        const int ox = ox0 + tx;
         float *out = a.out + (long long)blockIdx.z * a.out_stride;
 
-        if (ox >= a.Wo || oy >= a.Ho)
-            return;
 #pragma unroll
-        for (int k = 0; k < FK_MAXK; k++)
-            if (k < nk) {
-                const float v = acc[k] + (a.bias ? a.bias[k0 + k] : 0.0f);
+        for (int r = 0; r < 2; r++) {
+            const int oy = oy0 + 2 * ty + r;
 
-                out[((long long)(k0 + k) * a.Ho + oy) * a.Wo + ox] = icoreg_act(v, a.act, a.slope);
+            if (ox >= a.Wo || oy >= a.Ho)
+                continue;
+#pragma unroll
+            for (int k = 0; k < NK; k++) {
+                const float v = acc[r][k] + (a.bias ? a.bias[k0 + k] : 0.0f);
+
+                out[((long long)(k0 + k) * a.Ho + oy) * a.Wo + ox] =
+                    icoreg_act(v, a.act, a.slope);
             }
+        }
     }
+}
+
+template <int KS, int ST>
+static void launch_fewk(const conv_args &a, int k0, int nk, int nb, hipStream_t s)
+{
+    const dim3 grid((a.Wo + 15) / 16, (a.Ho + 31) / 32, nb);
+
+#define FK_CASE(N)                                                             \
+    case N:                                                                    \
+        hipLaunchKernelGGL((conv_fewk_kernel<KS, ST, N>), grid, dim3(256), 0, s, a, k0); \
+        break;
+    switch (nk) {
+        FK_CASE(1)
+        FK_CASE(2)
+        FK_CASE(3)
+        FK_CASE(4)
+        FK_CASE(5)
+        FK_CASE(6)
+        FK_CASE(7)
+        FK_CASE(8)
+    }
+#undef FK_CASE
 }
 
 bool conv_direct_supported(int kh, int kw, int sy, int sx, int dy, int dx,
@@ -448,16 +502,15 @@ static void launch_cfg(const conv_args &a, int nb, hipStream_t s)
     const int rem = a.K % BM;
 
     /* A last block of at most FK_MAXK channels goes to the side kernel. */
-    if (a.K > BM && rem <= FK_MAXK && (long long)rem * a.C * KS * KS <= FK_MAXW) {
+    if (a.K > BM && rem <= FK_MAXK && a.C <= FK_MAXC &&
+        (long long)rem * a.C * KS * KS <= FK_MAXW) {
         conv_args m = a;
 
         m.K = a.K - rem;
         hipLaunchKernelGGL((conv_mfma<KS, ST, BM, TW, CC, NJ>),
                            dim3(tiles, m.K / BM, nb), dim3(256), 0, s, m);
         if (rem)
-            hipLaunchKernelGGL((conv_fewk_kernel<KS, ST>),
-                               dim3((a.Wo + 15) / 16, (a.Ho + 15) / 16, nb), dim3(256), 0,
-                               s, a, m.K, rem);
+            launch_fewk<KS, ST>(a, m.K, rem, nb, s);
         return;
     }
     hipLaunchKernelGGL((conv_mfma<KS, ST, BM, TW, CC, NJ>),
