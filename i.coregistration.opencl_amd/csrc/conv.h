@@ -22,6 +22,11 @@ struct conv_args {
     const float *mean, *rstd, *gate; /* optional input normalisation */
     int act;
     float slope;
+    /* Direct kernel only: split > 1 cuts the input channels into split
+     * pieces (grid z = piece + split * image) whose partial sums go to
+     * part (split x nb x K x Ho x Wo floats), added by a second pass. */
+    int split;
+    float *part;
 };
 
 /* True if the direct kernel handles this geometry. */
@@ -31,6 +36,10 @@ bool conv_direct_supported(int kh, int kw, int sy, int sx, int dy, int dx,
 /* True if the tensors are small enough for the kernel's 32-bit buffer
  * offsets (per-image input and the weights below 2 GiB). */
 bool conv_direct_fits(long long in_floats, long long w_floats);
+
+/* Bytes of the partial sums conv_direct_launch needs for a (0: none);
+ * the caller passes that much memory as a.part. */
+size_t conv_direct_part_bytes(const conv_args &a, int ks, int stride, int nb, int cus);
 
 void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,
                         int cus, hipStream_t s);

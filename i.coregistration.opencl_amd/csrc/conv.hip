@@ -89,7 +89,8 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
     const int iy0 = oy0 * ST - a.pad, ix0 = ox0 * ST - a.pad;
     const int C = a.C, H = a.H, W = a.W, K = a.K;
     const long long HW = (long long)H * W;
-    const float *in = a.in + (long long)blockIdx.z * a.in_stride;
+    const int piece = blockIdx.z % a.split, img = blockIdx.z / a.split;
+    const float *in = a.in + (long long)img * a.in_stride;
     const long long wrow = (long long)C * KK;
     unsigned woff[NA], poff[NP];
     int lda_[NA], ldp[NP];
@@ -174,16 +175,19 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
             Ps[buf][ldp[q]] = rp[q];
     };
 
-    const int nk = (C + CC - 1) / CC;
+    /* Slices [kt0, kt1) of CC channels: all of them, or this piece's
+     * share (the host makes every piece non-empty). */
+    const int nk_all = (C + CC - 1) / CC, per = (nk_all + a.split - 1) / a.split;
+    const int kt0 = piece * per, nk = min(nk_all, kt0 + per);
     /* This lane's first pixel: row r of the tile, column x. */
     const int pr = (wn * 32 * NJ + col) / TW, px0 = col % TW;
     const int pbase = pr * ST * PWP + px0;
 
-    fetch(0);
+    fetch(kt0 * CC);
     stash(0);
     __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
+    for (int kt = kt0; kt < nk; kt++) {
+        const int cur = (kt - kt0) & 1;
 
         if (kt + 1 < nk)
             fetch((kt + 1) * CC);
@@ -245,7 +249,12 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
     }
 
     {
-        float *out = a.out + (long long)blockIdx.z * a.out_stride;
+        /* Whole: bias, activation, the output. Piece: raw partial sums
+         * into part[piece][img]. */
+        const bool whole = a.split == 1;
+        float *out = whole ? a.out + (long long)img * a.out_stride
+                           : a.part + ((long long)piece * (gridDim.z / a.split) + img) *
+                                          K * a.Ho * a.Wo;
 
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
@@ -264,13 +273,33 @@ __global__ void __launch_bounds__(256) conv_mfma(const conv_args a)
                     if (m >= K)
                         continue;
                     v = acc[i][j][r];
-                    if (a.bias)
-                        v += a.bias[m];
-                    out[((long long)m * a.Ho + oy) * a.Wo + ox] =
-                        icoreg_act(v, a.act, a.slope);
+                    if (whole) {
+                        if (a.bias)
+                            v += a.bias[m];
+                        v = icoreg_act(v, a.act, a.slope);
+                    }
+                    out[((long long)m * a.Ho + oy) * a.Wo + ox] = v;
                 }
         }
     }
+}
+
+/* Sum of the split pieces' partials in piece order, bias, activation. */
+__global__ void __launch_bounds__(256) conv_pieces_kernel(const conv_args a, int nb)
+{
+    const long long plane = (long long)a.K * a.Ho * a.Wo;
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int img = blockIdx.y;
+
+    if (e >= plane)
+        return;
+    float v = a.part[(long long)img * plane + e];
+
+    for (int p = 1; p < a.split; p++)
+        v += a.part[((long long)p * nb + img) * plane + e];
+    if (a.bias)
+        v += a.bias[e / ((long long)a.Ho * a.Wo)];
+    a.out[(long long)img * a.out_stride + e] = icoreg_act(v, a.act, a.slope);
 }
 
 /* One input channel (ELoFTR's grey first layer): one thread per output
@@ -491,64 +520,109 @@ static long long tiled_area(int Ho, int Wo, int th, int tw)
     return (long long)((Ho + th - 1) / th) * th * ((Wo + tw - 1) / tw) * tw;
 }
 
-template <int KS, int ST, int BM, int TW, int NJ>
-static void launch_cfg(const conv_args &a, int nb, hipStream_t s)
-{
-    /* K = 100 (5 x 5) or 36 (3 x 3) per slice at 64 channels per block,
-     * 50 at 128. */
-    constexpr int CC = BM == 128 ? 2 : 4;
-    constexpr int TH = 64 * NJ / TW;
-    const int tiles = ((a.Wo + TW - 1) / TW) * ((a.Ho + TH - 1) / TH);
-    const int rem = a.K % BM;
-
-    /* A last block of at most FK_MAXK channels goes to the side kernel. */
-    if (a.K > BM && rem <= FK_MAXK && a.C <= FK_MAXC &&
-        (long long)rem * a.C * KS * KS <= FK_MAXW) {
-        conv_args m = a;
-
-        m.K = a.K - rem;
-        hipLaunchKernelGGL((conv_mfma<KS, ST, BM, TW, CC, NJ>),
-                           dim3(tiles, m.K / BM, nb), dim3(256), 0, s, m);
-        if (rem)
-            launch_fewk<KS, ST>(a, m.K, rem, nb, s);
-        return;
-    }
-    hipLaunchKernelGGL((conv_mfma<KS, ST, BM, TW, CC, NJ>),
-                       dim3(tiles, (a.K + BM - 1) / BM, nb), dim3(256), 0, s,
-                       a);
-}
+/* The direct kernel's configuration for a: channels per block (bm),
+ * tile width (tw), the channels the MFMA kernel takes (kmain; the last
+ * K - kmain go to the few-channel kernel) and the input-channel pieces. */
+struct direct_plan {
+    int bm, tw, kmain, split;
+};
 
 /* 3 x 3: blocks of 64 channels x 64 pixels, the fastest of the 64 / 128
  * channel x 64 / 128 pixel blocks at every ELoFTR layer measured (the
  * small block keeps the most waves per CU in flight). 5 x 5: 128 pixels,
  * and 128 channels unless that grid would leave CUs with fewer than two
  * blocks each. The tile is 2 x 32 / 4 x 32 or 4 x 16 / 8 x 16 pixels,
- * whichever pads the image less. */
+ * whichever pads the image less. A last block of at most FK_MAXK
+ * channels goes to the few-channel kernel. Grids of fewer blocks than
+ * CUs (DISK's 64 x 64 and 32 x 32 layers: 8-32 blocks) are cut over the
+ * input channels into up to 16 pieces, so that about two blocks per CU
+ * run, each piece at least one channel slice. */
+static direct_plan plan_direct(const conv_args &a, int ks, int nb, int cus)
+{
+    const int nj = ks == 3 ? 1 : 2, px = 64 * nj;
+    const bool narrow = tiled_area(a.Ho, a.Wo, px / 16, 16) < tiled_area(a.Ho, a.Wo, px / 32, 32);
+    const int tw = narrow ? 16 : 32, th = px / tw;
+    const long long tiles = (long long)((a.Wo + tw - 1) / tw) * ((a.Ho + th - 1) / th);
+    direct_plan p;
+
+    p.tw = tw;
+    p.bm = ks == 5 && a.K > 64 && tiles * ((a.K + 127) / 128) * nb >= 2LL * cus ? 128 : 64;
+    {
+        const int rem = a.K % p.bm;
+
+        p.kmain = a.K > p.bm && rem <= FK_MAXK && a.C <= FK_MAXC &&
+                          (long long)rem * a.C * ks * ks <= FK_MAXW
+                      ? a.K - rem
+                      : a.K;
+    }
+    {
+        const int cc = p.bm == 128 ? 2 : 4, nk = (a.C + cc - 1) / cc;
+        const long long blocks = tiles * ((p.kmain + p.bm - 1) / p.bm) * nb;
+        int split = blocks < cus ? (int)((2LL * cus + blocks - 1) / blocks) : 1;
+
+        split = split < 16 ? split : 16;
+        split = split < nk ? split : nk;
+        /* Every piece non-empty: pieces of ceil(nk / split) slices. */
+        if (split > 1) {
+            const int per = (nk + split - 1) / split;
+
+            split = (nk + per - 1) / per;
+        }
+        if (nb * (long long)split > 65535)
+            split = 1;
+        p.split = split;
+    }
+    return p;
+}
+
+size_t conv_direct_part_bytes(const conv_args &a, int ks, int stride, int nb, int cus)
+{
+    if (a.C == 1 && !a.mean && a.K <= C1_MAXK && a.K * ks * ks <= C1_MAXW)
+        return 0;
+    const direct_plan p = plan_direct(a, ks, nb, cus);
+
+    return p.split > 1 ? (size_t)p.split * nb * p.kmain * a.Ho * a.Wo * sizeof(float) : 0;
+}
+
+template <int KS, int ST, int BM, int TW, int NJ>
+static void launch_cfg(const conv_args &a, const direct_plan &p, int nb, hipStream_t s)
+{
+    /* K = 100 (5 x 5) or 36 (3 x 3) per slice at 64 channels per block,
+     * 50 at 128. */
+    constexpr int CC = BM == 128 ? 2 : 4;
+    constexpr int TH = 64 * NJ / TW;
+    const int tiles = ((a.Wo + TW - 1) / TW) * ((a.Ho + TH - 1) / TH);
+    conv_args m = a;
+
+    m.K = p.kmain;
+    m.split = p.split;
+    hipLaunchKernelGGL((conv_mfma<KS, ST, BM, TW, CC, NJ>),
+                       dim3(tiles, (m.K + BM - 1) / BM, nb * p.split), dim3(256), 0, s, m);
+    if (p.split > 1)
+        hipLaunchKernelGGL(conv_pieces_kernel,
+                           dim3((unsigned)(((long long)m.K * a.Ho * a.Wo + 255) / 256), nb),
+                           dim3(256), 0, s, m, nb);
+    if (p.kmain < a.K)
+        launch_fewk<KS, ST>(a, p.kmain, a.K - p.kmain, nb, s);
+}
+
 template <int KS, int ST>
 static void launch_ks(const conv_args &a, int nb, int cus, hipStream_t s)
 {
     constexpr int NJ = KS == 3 ? 1 : 2;
-    constexpr int P = 64 * NJ;
-    const bool narrow = tiled_area(a.Ho, a.Wo, P / 16, 16) <
-                        tiled_area(a.Ho, a.Wo, P / 32, 32);
+    const direct_plan p = plan_direct(a, KS, nb, cus);
 
-    if constexpr (KS == 5) {
-        const long long tiles =
-            narrow ? (long long)((a.Wo + 15) / 16) * ((a.Ho + 7) / 8)
-                   : (long long)((a.Wo + 31) / 32) * ((a.Ho + 3) / 4);
-
-        if (a.K > 64 && tiles * ((a.K + 127) / 128) * nb >= 2LL * cus) {
-            if (narrow)
-                launch_cfg<KS, ST, 128, 16, NJ>(a, nb, s);
-            else
-                launch_cfg<KS, ST, 128, 32, NJ>(a, nb, s);
-            return;
-        }
+    if (p.bm == 128) {
+        if (p.tw == 16)
+            launch_cfg<KS, ST, 128, 16, NJ>(a, p, nb, s);
+        else
+            launch_cfg<KS, ST, 128, 32, NJ>(a, p, nb, s);
+        return;
     }
-    if (narrow)
-        launch_cfg<KS, ST, 64, 16, NJ>(a, nb, s);
+    if (p.tw == 16)
+        launch_cfg<KS, ST, 64, 16, NJ>(a, p, nb, s);
     else
-        launch_cfg<KS, ST, 64, 32, NJ>(a, nb, s);
+        launch_cfg<KS, ST, 64, 32, NJ>(a, p, nb, s);
 }
 
 void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,

@@ -450,6 +450,8 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
         a.gate = mean ? cfptr(alpha) : nullptr;
         a.act = act;
         a.slope = slope;
+        a.split = 1;
+        a.part = nullptr;
         wino_split sp = conv_wino_plan(a, nb, o->ocl->cu_count);
         const size_t pb = conv_wino_part_floats(a, nb, sp) * sizeof(float);
         const float *Uf;
@@ -508,6 +510,14 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
         a.gate = mean ? cfptr(alpha) : nullptr;
         a.act = act;
         a.slope = slope;
+        a.split = 1;
+        a.part = nullptr;
+        {
+            const size_t pb = conv_direct_part_bytes(a, g->kh, g->sy, nb, o->ocl->cu_count);
+
+            if (pb)
+                a.part = fptr(scratch_get(o, pb));
+        }
         prof_scope ps(o->ocl, "conv_direct");
         conv_direct_launch(a, g->kh, g->sy, nb, o->ocl->cu_count,
                            stream_of(o->ocl));

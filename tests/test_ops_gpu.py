@@ -141,6 +141,13 @@ CONV_SHAPES = [
     (2, 16, 41, 39, 66, 5, 2, 2, 1, 2),
     (1, 24, 30, 34, 70, 3, 1, 1, 1, 1),
     (1, 20, 25, 27, 67, 3, 2, 1, 0, 2),
+    # Grids smaller than the CU count, cut over the input channels into
+    # pieces (DISK's 64 x 64 and 32 x 32 layers, ragged channel slices,
+    # pieces together with the few-channel kernel).
+    (1, 64, 64, 64, 64, 5, 1, 2, 1, 0),
+    (1, 128, 32, 32, 64, 5, 1, 2, 1, 2),
+    (2, 37, 24, 20, 48, 3, 1, 1, 1, 1),
+    (1, 80, 40, 40, 129, 5, 1, 2, 1, 0),
     # One input channel (the per-pixel kernel): 5 x 5 and 3 x 3, stride 1.
     (1, 1, 37, 45, 20, 5, 1, 2, 0, 1),
     (2, 1, 30, 31, 16, 3, 1, 1, 0, 0),
