@@ -63,6 +63,11 @@ void conv_wino_weights(const float *w, int K, int C, bool norm, float *U, hipStr
  * (split x 4096 floats per unit), added up by a second kernel. */
 struct wino_split {
     int nkb, ntb, nfull, split;
+    /* Units are ordered (channel group, image, tile block, channel block
+     * of the group); whole units go to the XCDs in contiguous bands of
+     * that order, so an XCD holds the filters of kgroups-th of the
+     * channel blocks and the inputs of its own tiles. */
+    int kgroups, nb;
     float *part;
 };
 

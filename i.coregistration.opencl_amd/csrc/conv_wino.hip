@@ -438,6 +438,28 @@ __global__ void __launch_bounds__(256)
 }
 
 /* gfx9 s_waitcnt immediates: vmcnt(0) alone; vmcnt(0) and lgkmcnt(0). */
+/* Block L of T to a position in the unit order: the 8 XCDs (blocks L,
+ * L + 8, ... run on XCD L % 8) each get a contiguous band. */
+__device__ __forceinline__ int wino_xcd_band(int L, int T)
+{
+    const int q = T >> 3, rem = T & 7, x = L & 7, idx = L >> 3;
+
+    return (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + idx;
+}
+
+/* Unit v of the order (channel group, image, tile block, channel block of
+ * the group). */
+__device__ __forceinline__ void wino_unit(const wino_split &sp, int v, int &bx, int &by,
+                                          int &bz)
+{
+    const int cbg = sp.nkb / sp.kgroups, per = sp.ntb * sp.nb * cbg;
+    const int g = v / per, r = v - g * per, t = r / cbg;
+
+    bx = g * cbg + (r - t * cbg);
+    by = t % sp.ntb;
+    bz = t / sp.ntb;
+}
+
 /* Most pieces per split unit. */
 #define WR_MAX_SPLIT 8
 
@@ -487,10 +509,11 @@ __global__ void __launch_bounds__(256, 4)
     const int tr = col >> 3, tc = col & 7;
     const int C = a.C, H = a.H, W = a.W;
     const int nk = (C + WR_CC - 1) / WR_CC;
-    /* Unit u = (image bz, tile block by, channel block bx), channel blocks
-     * fastest (they share the input tiles in L2); units from nfull on are
-     * cut into split pieces over the input-channel slices. */
-    int u = blockIdx.x, piece = -1, kt0 = 0, kt1 = nk;
+    /* Unit (image bz, tile block by, channel block bx) in wino_unit's
+     * order, channel blocks of a group fastest (they share the input
+     * tiles in L2); whole units in XCD bands, units from nfull on cut into
+     * split pieces over the input-channel slices. */
+    int u = blockIdx.x, piece = -1, kt0 = 0, kt1 = nk, bx, by, bz;
 
     if (u >= sp.nfull) {
         const int p = u - sp.nfull;
@@ -500,7 +523,9 @@ __global__ void __launch_bounds__(256, 4)
         kt0 = piece * nk / sp.split;
         kt1 = (piece + 1) * nk / sp.split;
     }
-    const int bx = u % sp.nkb, by = (u / sp.nkb) % sp.ntb, bz = u / (sp.nkb * sp.ntb);
+    else
+        u = wino_xcd_band(u, sp.nfull);
+    wino_unit(sp, u, bx, by, bz);
     const int tiles_w = (W + 1) / 2, bw = (tiles_w + TC - 1) / TC;
     const int ty0 = (by / bw) * TR, tx0 = (by % bw) * TC;
     const int k0 = bx * BK;
@@ -738,8 +763,9 @@ __global__ void __launch_bounds__(256)
 
     if (t >= tail)
         return;
-    const int u = sp.nfull + t;
-    const int bx = u % sp.nkb, by = (u / sp.nkb) % sp.ntb, bz = u / (sp.nkb * sp.ntb);
+    int bx, by, bz;
+
+    wino_unit(sp, sp.nfull + t, bx, by, bz);
     const int bw = ((a.W + 1) / 2 + TC - 1) / TC;
     const int oy = 2 * ((by / bw) * TR + ts / TC), ox = 2 * ((by % bw) * TC + ts % TC);
     const float4 *q = (const float4 *)sp.part + (long long)t * sp.split * (BK * 32) + w;
@@ -828,6 +854,11 @@ wino_split conv_wino_plan(const conv_args &a, int nb, int cus)
     sp.nkb = (a.K + 31) / 32;
     sp.ntb = (int)wino_blocks(a.Ho, a.Wo, 4);
     sp.part = nullptr;
+    sp.nb = nb;
+    /* Two channel groups from 8 channel blocks (256 channels) up: an XCD
+     * then reads half the filters (2 MB of U at C = K = 256) and a
+     * quarter of the inputs, instead of every input tile. */
+    sp.kgroups = sp.nkb >= 8 && sp.nkb % 2 == 0 ? 2 : 1;
     units = (long long)sp.nkb * sp.ntb * nb;
     sp.nfull = (int)units;
     sp.split = 1;

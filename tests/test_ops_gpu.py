@@ -134,6 +134,10 @@ CONV_SHAPES = [
     # pieces, the partial channel block among the split ones).
     (1, 64, 80, 80, 192, 3, 1, 1, 0, 2),
     (2, 48, 30, 90, 200, 3, 1, 1, 0, 1),
+    # Two channel groups (256 output channels) in XCD bands, with and
+    # without split units (320 units: 256 whole, 64 in pieces).
+    (1, 64, 40, 128, 256, 3, 1, 1, 0, 2),
+    (2, 256, 20, 24, 256, 3, 1, 1, 0, 1),
     # A last block of 1-8 output channels on the few-channel side kernel:
     # DISK's last layer (129 = 128 + 1) at a size that takes 128-channel
     # blocks, 64-channel blocks with 2, 3 and 6 left, strides 1 and 2.
