@@ -812,6 +812,35 @@ def main():
     res = net.result()
     nm = int(res["nm"])
 
+    # The same pair from a HIP graph: the whole device stage recorded once
+    # (eloftr_match_enqueue) and replayed, the matches read after the
+    # last replay.
+    graph = None
+    try:
+        dev.api.ocl_graph_begin(dev.pb)
+        dev.api.eloftr_match_enqueue(net.m, b0.mem, b1.mem)
+        graph = dev.api.ocl_graph_end(dev.pb)
+        for _ in range(args.warmup):
+            dev.api.ocl_graph_launch(dev.pb, graph)
+        dev.finish()
+        dev.reset_events()
+        t0 = time.perf_counter()
+        e0 = dev.event()
+        for _ in range(args.steps):
+            dev.api.ocl_graph_launch(dev.pb, graph)
+        e1 = dev.event()
+        dev.finish()
+        wall = time.perf_counter() - t0
+        ms_g = max(dev.elapsed_ms(e0, e1), wall * 1e3) / args.steps
+        dev.api.eloftr_match_collect(net.m)
+        graph_leg = {"workload": f"the headline pair, its device stage replayed from one HIP "
+                                 f"graph ({args.steps} replays)",
+                     "pairs_per_s": round(1000.0 / ms_g, 3), "ms_per_pair": round(ms_g, 4),
+                     "coarse_matches": int(net.result()["nm"])}
+    finally:
+        if graph:
+            ic.lib().ocl_graph_free(graph)
+
     if args.copy_calib:
         copy_calibration(dev, args.copy_calib)
 
@@ -938,6 +967,7 @@ def main():
         "pipeline_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
         "fine_ms_at_max_matches": round(fine_nmax_ms, 4),
         "eloftr_with_matches": with_matches,
+        "eloftr_graph": graph_leg,
         "cpu_baseline": cpu,
         "roma560": roma,
         **extra,

@@ -91,6 +91,10 @@ SIGNATURES = {
     "ocl_copy": (None, [_B, Mem, C.c_size_t, Mem, C.c_size_t, C.c_size_t]),
     "ocl_copy_rect": (None, [_B, Mem, C.c_size_t, C.c_size_t, Mem, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t]),
     "ocl_fill": (None, [_B, Mem, C.c_size_t, C.c_size_t, _F]),
+    "ocl_graph_begin": (None, [_B]),
+    "ocl_graph_end": (_P, [_B]),
+    "ocl_graph_launch": (None, [_B, _P]),
+    "ocl_graph_free": (None, [_P]),
     "ocl_finish": (None, [_B]),
     "ocl_wrap": (Mem, [_P, C.c_size_t]),
     "ocl_event_record": (_I, [_B]),
@@ -150,6 +154,8 @@ SIGNATURES = {
     "eloftr_alloc": (None, [_P, _I, _I]),
     "eloftr_match": (None, [_P, _P, _P, _S, _I]),
     "eloftr_match_device": (None, [_P, Mem, Mem]),
+    "eloftr_match_enqueue": (None, [_P, Mem, Mem]),
+    "eloftr_match_collect": (None, [_P]),
     "eloftr_free": (None, [_P]),
     "eloftr_row_lse": (None, [_O, Mem, _I, _I, _I, Mem]),
     "eloftr_col_lse": (None, [_O, Mem, _I, _I, Mem, Mem]),
@@ -157,6 +163,8 @@ SIGNATURES = {
     "eloftr_conf_col": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
     "eloftr_fine": (None, [_O, Mem, Mem, _I, _I, Mem, _I, _F, Mem]),
     "eloftr_fine_half": (None, [_O, Mem, Mem, _I, _I, Mem, _I, _F, Mem]),
+    "eloftr_fine_half_count": (None, [_O, Mem, Mem, _I, _I, Mem, Mem, _I, _F, Mem]),
+    "eloftr_mutual": (None, [_O, Mem, Mem, Mem, _I, _I, _I, _F, Mem, Mem, Mem, Mem, Mem]),
     "roma_row_norm": (None, [_O, Mem, _I, _I, Mem]),
     "roma_cos_exp": (None, [_O, Mem, Mem, Mem, _I, _I, _F, _F]),
     "roma_cls_to_flow": (None, [_O, Mem, _I, _I, _I, _I, Mem, Mem]),
@@ -216,7 +224,7 @@ SIGNATURES = {
 }
 
 # Entry points that never raise through the fatal path (no error check).
-_NO_CHECK = {"icoreg_set_fatal_mode", "icoreg_last_error", "icoreg_clear_error",
+_NO_CHECK = {"ocl_graph_free", "icoreg_set_fatal_mode", "icoreg_last_error", "icoreg_clear_error",
              "ocl_errstr", "ops_mat", "ops_bmat", "ops_geom", "ops_conv_out",
              "ocl_wrap", "icoreg_prof_entry", "icoreg_prof_reset", "icoreg_prof_flush", "ops_report",
              "pth_find", "pth_numel", "pth_bytes", "pth_strip_prefix",

@@ -433,6 +433,10 @@ extern "C" void eloftr_alloc(struct eloftr_model *m, int H, int W)
     m->nmax = (int)n;
     m->m_idx = ocl_alloc(m->ocl, n * 4 * sizeof(int), "match cells");
     m->m_out = walloc(m, n * 4, "fine matches");
+    m->d_mi = ocl_alloc(m->ocl, n * sizeof(int), "matches");
+    m->d_mj = ocl_alloc(m->ocl, n * sizeof(int), "matches");
+    m->d_mconf = walloc(m, n, "match confidences");
+    m->m_count = ocl_alloc(m->ocl, 2 * sizeof(int), "match count");
     m->mi = (int *)malloc(n * sizeof(int));
     m->mj = (int *)malloc(n * sizeof(int));
     m->mconf = (float *)malloc(n * sizeof(float));
@@ -613,26 +617,10 @@ static void coarse_match(struct eloftr_model *m)
                                 m->col_s, m->col_max, m->col_arg);
             }
         }
-    ocl_read(m->ocl, m->row_max, 0, m->h_rmax, n * sizeof(float));
-    ocl_read(m->ocl, m->row_arg, 0, m->h_rarg, n * sizeof(int));
-    ocl_read(m->ocl, m->col_arg, 0, m->h_carg, n * sizeof(int));
-    m->nm = 0;
-    for (int i = 0; i < n; i++) {
-        const int j = m->h_rarg[i];
-        const int xi = i % m->w, yi = i / m->w, xj = j % m->w, yj = j / m->w;
-
-        if (j < 0 || j >= n)
-            icoreg_fatal("ELoFTR: row argmax %d out of range", j);
-        if (!(m->h_rmax[i] > COARSE_THR) || m->h_carg[j] != i)
-            continue;
-        if (xi < BORDER || yi < BORDER || xi >= m->w - BORDER ||
-            yi >= m->h - BORDER || xj < BORDER || yj < BORDER ||
-            xj >= m->w - BORDER || yj >= m->h - BORDER)
-            continue;
-        m->mi[m->nm] = i;
-        m->mj[m->nm] = j;
-        m->mconf[m->nm++] = m->h_rmax[i];
-    }
+    /* Mutual selection on the device (eloftr.c:606-636): the matches
+     * stay in HBM for fine matching and come back with its results. */
+    eloftr_mutual(o, m->row_max, m->row_arg, m->col_arg, m->h, m->w, BORDER, COARSE_THR,
+                  m->d_mi, m->d_mj, m->d_mconf, m->m_idx, m->m_count);
 }
 
 /* 1 x 1 convolution of both images: W (K, C) times X (C, HW) per image,
@@ -695,24 +683,29 @@ extern "C" void eloftr_fine_maps(struct eloftr_model *m)
                m->W, 0, 0, 2.0f);
 }
 
+/* Fine matching of the device's matches, their count read there. */
 static void fine_match(struct eloftr_model *m)
 {
-    int *cells;
+    eloftr_fine_half_count(m->ops, m->fine_h[0], m->fine_h[1], m->H, m->W, m->m_idx,
+                           m->m_count, m->nmax, FINE_T, m->m_out);
+}
 
-    if (m->nm == 0)
-        return;
-    cells = (int *)malloc((size_t)m->nm * 4 * sizeof(int));
-    for (int i = 0; i < m->nm; i++) {
-        cells[4 * i] = m->mi[i] % m->w;
-        cells[4 * i + 1] = m->mi[i] / m->w;
-        cells[4 * i + 2] = m->mj[i] % m->w;
-        cells[4 * i + 3] = m->mj[i] / m->w;
+/* The one read-back of a pair: the count, the matches and their refined
+ * positions. */
+static void collect_matches(struct eloftr_model *m)
+{
+    int cnt[2];
+
+    ocl_read(m->ocl, m->m_count, 0, cnt, sizeof(cnt));
+    if (cnt[1])
+        icoreg_fatal("ELoFTR: a row argmax is out of range");
+    m->nm = cnt[0];
+    if (m->nm > 0) {
+        ocl_read(m->ocl, m->d_mi, 0, m->mi, (size_t)m->nm * sizeof(int));
+        ocl_read(m->ocl, m->d_mj, 0, m->mj, (size_t)m->nm * sizeof(int));
+        ocl_read(m->ocl, m->d_mconf, 0, m->mconf, (size_t)m->nm * sizeof(float));
+        ocl_read(m->ocl, m->m_out, 0, m->kp, (size_t)m->nm * 4 * sizeof(float));
     }
-    ocl_write(m->ocl, m->m_idx, 0, cells, (size_t)m->nm * 4 * sizeof(int));
-    free(cells);
-    eloftr_fine_half(m->ops, m->fine_h[0], m->fine_h[1], m->H, m->W, m->m_idx, m->nm,
-                     FINE_T, m->m_out);
-    ocl_read(m->ocl, m->m_out, 0, m->kp, (size_t)m->nm * 4 * sizeof(float));
 }
 
 static void dump_dev(struct eloftr_model *m, const char *dir, int tile,
@@ -736,7 +729,7 @@ static void dump_dev(struct eloftr_model *m, const char *dir, int tile,
 }
 
 static void match_stages(struct eloftr_model *m, cl_mem dev0, cl_mem dev1,
-                         const char *dump, int tile)
+                         const char *dump, int tile, bool collect)
 {
     const size_t n = (size_t)m->h * m->w, hw = (size_t)m->H * m->W;
 
@@ -763,13 +756,29 @@ static void match_stages(struct eloftr_model *m, cl_mem dev0, cl_mem dev1,
         dump_dev(m, dump, tile, "fine_1", m->fine[1], ELOFTR_FINE_DIM * hw);
     }
     fine_match(m);
+    if (collect)
+        collect_matches(m);
 }
 
 extern "C" void eloftr_match_device(struct eloftr_model *m, cl_mem dev0,
                                     cl_mem dev1)
 {
     ICOREG_API_BEGIN
-    match_stages(m, dev0, dev1, NULL, 0);
+    match_stages(m, dev0, dev1, NULL, 0, true);
+    ICOREG_API_END
+}
+
+extern "C" void eloftr_match_enqueue(struct eloftr_model *m, cl_mem dev0, cl_mem dev1)
+{
+    ICOREG_API_BEGIN
+    match_stages(m, dev0, dev1, NULL, 0, false);
+    ICOREG_API_END
+}
+
+extern "C" void eloftr_match_collect(struct eloftr_model *m)
+{
+    ICOREG_API_BEGIN
+    collect_matches(m);
     ICOREG_API_END
 }
 
@@ -783,7 +792,7 @@ extern "C" void eloftr_match(struct eloftr_model *m, const float *grey0,
      * fusion, on its way to the pair's input buffer. */
     ocl_write(m->ocl, m->img, 0, grey0, hw * sizeof(float));
     ocl_write(m->ocl, m->fu_a, 0, grey1, hw * sizeof(float));
-    match_stages(m, m->img, m->fu_a, dump, tile);
+    match_stages(m, m->img, m->fu_a, dump, tile, true);
     ICOREG_API_END
 }
 
@@ -798,7 +807,8 @@ extern "C" void eloftr_free(struct eloftr_model *m)
         &m->t_O2,    &m->t_tok,   &m->t_h1,    &m->t_h2,  &m->rope,
         &m->s_blk,   &m->row_lse, &m->col_m,   &m->col_s, &m->row_max,
         &m->row_arg, &m->col_max, &m->col_arg, &m->fu_a,  &m->fu_b,
-        &m->fu_c,    &m->m_idx,   &m->m_out,   &m->f_out};
+        &m->fu_c,    &m->m_idx,   &m->m_out,   &m->f_out, &m->d_mi,
+        &m->d_mj,    &m->d_mconf, &m->m_count};
 
     if (m->ocl && m->ocl->stream)
         ocl_finish(m->ocl);

@@ -687,7 +687,7 @@ template <bool UP2>
 __global__ void __launch_bounds__(256)
     fine_kernel(const float *__restrict__ f0, const float *__restrict__ f1,
                 int H, int W, const int4 *__restrict__ cells, int M, float T,
-                float4 *__restrict__ out)
+                float4 *__restrict__ out, const int *__restrict__ mcount)
 {
     __shared__ float A[NP * WP];
     __shared__ float B[NQ * WP];
@@ -700,6 +700,8 @@ __global__ void __launch_bounds__(256)
     const long long plane = UP2 ? (long long)(H / 2) * (W / 2) : (long long)H * W;
     int4 cl;
 
+    if (mcount)
+        M = min(M, *mcount);
     if (k >= M)
         return;
     cl = cells[k];
@@ -880,7 +882,7 @@ extern "C" void eloftr_fine(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
     prof_scope ps(o->ocl, op);
     hipLaunchKernelGGL(fine_kernel<false>, dim3(M), dim3(256), 0, stream_of(o->ocl),
                        cfptr(f0), cfptr(f1), H, W, (const int4 *)cells->ptr, M,
-                       T, (float4 *)out->ptr);
+                       T, (float4 *)out->ptr, nullptr);
     launch_check(op);
     ICOREG_API_END
 }
@@ -904,7 +906,151 @@ extern "C" void eloftr_fine_half(struct ops *o, cl_mem f0, cl_mem f1, int H, int
     prof_scope ps(o->ocl, op);
     hipLaunchKernelGGL(fine_kernel<true>, dim3(M), dim3(256), 0, stream_of(o->ocl),
                        cfptr(f0), cfptr(f1), H, W, (const int4 *)cells->ptr, M, T,
-                       (float4 *)out->ptr);
+                       (float4 *)out->ptr, nullptr);
+    launch_check(op);
+    ICOREG_API_END
+}
+
+extern "C" void eloftr_fine_half_count(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
+                                       cl_mem cells, cl_mem count, int nmax, float T,
+                                       cl_mem out)
+{
+    ICOREG_API_BEGIN
+    const char *op = "eloftr_fine_half_count";
+
+    if (nmax < 0 || H < 2 || W < 2 || H % 2 || W % 2)
+        icoreg_fatal("%s: invalid sizes nmax=%d H=%d W=%d", op, nmax, H, W);
+    if (nmax == 0)
+        return;
+    need_floats(f0, 0, (long long)FC * (H / 2) * (W / 2), op, "f0");
+    need_floats(f1, 0, (long long)FC * (H / 2) * (W / 2), op, "f1");
+    need_bytes(cells, 0, 16LL * nmax, op, "cells");
+    need_bytes(count, 0, 4, op, "count");
+    need_floats(out, 0, 4LL * nmax, op, "out");
+    if (((uintptr_t)cells->ptr & 15) || ((uintptr_t)out->ptr & 15))
+        icoreg_fatal("%s: cells and out must be 16-byte aligned", op);
+    prof_scope ps(o->ocl, "eloftr_fine_half");
+    hipLaunchKernelGGL(fine_kernel<true>, dim3(nmax), dim3(256), 0, stream_of(o->ocl),
+                       cfptr(f0), cfptr(f1), H, W, (const int4 *)cells->ptr, nmax, T,
+                       (float4 *)out->ptr, (const int *)count->ptr);
+    launch_check(op);
+    ICOREG_API_END
+}
+
+/* ---- mutual nearest-neighbour selection of the coarse matches ---------- */
+
+/* The host loop of eloftr.c:606-636 on the device: cell i of image 0 is
+ * kept with j = its row argmax when its best confidence exceeds thr, j's
+ * column argmax is i, and both cells are at least border cells from the
+ * edges. One block of 1024 threads: each thread takes a contiguous run
+ * of cells, counts, the counts are scanned, and the kept matches are
+ * written in raster order (i, j, confidence, and the cells' (x, y) for
+ * fine matching). count[0] = the number kept; count[1] = 1 if a row
+ * argmax was out of range (the host raises the error). */
+#define MU_T 1024
+__global__ void __launch_bounds__(MU_T)
+    mutual_kernel(const float *__restrict__ rmax, const int *__restrict__ rarg,
+                  const int *__restrict__ carg, int h, int w, int border, float thr,
+                  int *__restrict__ mi, int *__restrict__ mj, float *__restrict__ mconf,
+                  int4 *__restrict__ cells, int *__restrict__ count)
+{
+    __shared__ int wsum[MU_T / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n = h * w, per = (n + MU_T - 1) / MU_T;
+    const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
+    int cnt = 0, bad = 0, off;
+
+    auto keep = [&](int i, int &j) {
+        j = rarg[i];
+        if (j < 0 || j >= n) {
+            bad = 1;
+            return false;
+        }
+        const int xi = i % w, yi = i / w, xj = j % w, yj = j / w;
+
+        return rmax[i] > thr && carg[j] == i && xi >= border && yi >= border &&
+               xi < w - border && yi < h - border && xj >= border && yj >= border &&
+               xj < w - border && yj < h - border;
+    };
+    for (int i = i0; i < i1; i++) {
+        int j;
+
+        cnt += keep(i, j) ? 1 : 0;
+    }
+    /* Exclusive scan of the counts over the block. */
+    {
+        int x = cnt;
+
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int y = __shfl_up(x, d);
+
+            if (lane >= d)
+                x += y;
+        }
+        if (lane == 63)
+            wsum[wv] = x;
+        __syncthreads();
+        if (wv == 0) {
+            int t = lane < MU_T / 64 ? wsum[lane] : 0;
+
+#pragma unroll
+            for (int d = 1; d < MU_T / 64; d <<= 1) {
+                const int y = __shfl_up(t, d);
+
+                if (lane >= d)
+                    t += y;
+            }
+            if (lane < MU_T / 64)
+                wsum[lane] = t;
+        }
+        __syncthreads();
+        off = x - cnt + (wv > 0 ? wsum[wv - 1] : 0);
+        if (tid == MU_T - 1)
+            count[0] = wsum[MU_T / 64 - 1];
+    }
+    for (int i = i0; i < i1; i++) {
+        int j;
+
+        if (keep(i, j)) {
+            mi[off] = i;
+            mj[off] = j;
+            mconf[off] = rmax[i];
+            cells[off] = make_int4(i % w, i / w, j % w, j / w);
+            off++;
+        }
+    }
+    bad = __syncthreads_or(bad);
+    if (tid == 0)
+        count[1] = bad;
+}
+
+extern "C" void eloftr_mutual(struct ops *o, cl_mem row_max, cl_mem row_arg, cl_mem col_arg,
+                              int h, int w, int border, float thr, cl_mem mi, cl_mem mj,
+                              cl_mem mconf, cl_mem cells, cl_mem count)
+{
+    ICOREG_API_BEGIN
+    const char *op = "eloftr_mutual";
+    const long long n = (long long)h * w;
+
+    if (h < 1 || w < 1)
+        icoreg_fatal("%s: invalid sizes h=%d w=%d", op, h, w);
+    count32(n, op);
+    need_floats(row_max, 0, n, op, "row_max");
+    need_bytes(row_arg, 0, 4 * n, op, "row_arg");
+    need_bytes(col_arg, 0, 4 * n, op, "col_arg");
+    need_bytes(mi, 0, 4 * n, op, "mi");
+    need_bytes(mj, 0, 4 * n, op, "mj");
+    need_floats(mconf, 0, n, op, "mconf");
+    need_bytes(cells, 0, 16 * n, op, "cells");
+    need_bytes(count, 0, 8, op, "count");
+    if ((uintptr_t)cells->ptr & 15)
+        icoreg_fatal("%s: cells must be 16-byte aligned", op);
+    prof_scope ps(o->ocl, op);
+    hipLaunchKernelGGL(mutual_kernel, dim3(1), dim3(MU_T), 0, stream_of(o->ocl),
+                       cfptr(row_max), (const int *)row_arg->ptr, (const int *)col_arg->ptr, h,
+                       w, border, thr, (int *)mi->ptr, (int *)mj->ptr, fptr(mconf),
+                       (int4 *)cells->ptr, (int *)count->ptr);
     launch_check(op);
     ICOREG_API_END
 }

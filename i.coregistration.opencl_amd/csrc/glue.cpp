@@ -30,15 +30,20 @@ extern "C" int icoreg_eloftr_result(const struct eloftr_model *m,
     return m->nm;
 }
 
-extern "C" int icoreg_eloftr_coarse_stats(const struct eloftr_model *m,
+extern "C" int icoreg_eloftr_coarse_stats(struct eloftr_model *m,
                                           const float **row_max,
                                           const int **row_arg,
                                           const int **col_arg)
 {
+    const size_t n = (size_t)m->h * m->w;
+
+    ocl_read(m->ocl, m->row_max, 0, m->h_rmax, n * sizeof(float));
+    ocl_read(m->ocl, m->row_arg, 0, m->h_rarg, n * sizeof(int));
+    ocl_read(m->ocl, m->col_arg, 0, m->h_carg, n * sizeof(int));
     *row_max = m->h_rmax;
     *row_arg = m->h_rarg;
     *col_arg = m->h_carg;
-    return m->h * m->w;
+    return (int)n;
 }
 
 extern "C" void icoreg_eloftr_set_pos_scale(struct eloftr_model *m, float s)

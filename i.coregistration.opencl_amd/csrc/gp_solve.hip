@@ -264,6 +264,9 @@ __global__ void __launch_bounds__(1024)
     __shared__ double s[GP_NB][GP_NB + 1], f[GP_NB][GP_NB + 1];
     __shared__ double dinv[GP_NB];
     const int tid = threadIdx.x, tx = tid & 31, ty = tid >> 5;
+    /* First failing column of this block (thread 0), reported at the end:
+     * no global access inside the column loop. */
+    int bad = 0;
 
     {
         double v[4];
@@ -304,8 +307,8 @@ __global__ void __launch_bounds__(1024)
         };
         double ur[2], wr[2], uc[2], wc[2], v[2][2];
 
-        if (tid == 0 && *info == 0 && (!(piv0 > 0.0) || (two && !(piv1 > 0.0))))
-            *info = k + (piv0 > 0.0 ? j1 : j) + 1;
+        if (tid == 0 && bad == 0 && (!(piv0 > 0.0) || (two && !(piv1 > 0.0))))
+            bad = k + (piv0 > 0.0 ? j1 : j) + 1;
 #pragma unroll
         for (int a2 = 0; a2 < 2; a2++) {
             uw(ty + 32 * a2, ur[a2], wr[a2]);
@@ -355,6 +358,8 @@ __global__ void __launch_bounds__(1024)
             }
         __syncthreads();
     }
+    if (tid == 0 && bad && *info == 0)
+        *info = bad;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int e = tid + 1024 * i, r = e >> 6, c = e & 63;

@@ -492,6 +492,49 @@ extern "C" void ocl_finish(struct ocl_backend *ocl)
     ICOREG_API_END
 }
 
+/* ---- graphs ----------------------------------------------------------- */
+
+extern "C" void ocl_graph_begin(struct ocl_backend *ocl)
+{
+    ICOREG_API_BEGIN
+    icoreg::hip_check(hipStreamBeginCapture(icoreg::stream_of(ocl),
+                                            hipStreamCaptureModeThreadLocal),
+                      "hipStreamBeginCapture");
+    ICOREG_API_END
+}
+
+extern "C" void *ocl_graph_end(struct ocl_backend *ocl)
+{
+    hipGraphExec_t exec = nullptr;
+    ICOREG_API_BEGIN
+    hipGraph_t g = nullptr;
+
+    icoreg::hip_check(hipStreamEndCapture(icoreg::stream_of(ocl), &g), "hipStreamEndCapture");
+    {
+        const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+
+        (void)hipGraphDestroy(g);
+        icoreg::hip_check(e, "hipGraphInstantiate");
+    }
+    ICOREG_API_END_RET((void *)exec)
+}
+
+extern "C" void ocl_graph_launch(struct ocl_backend *ocl, void *graph)
+{
+    ICOREG_API_BEGIN
+    if (!graph)
+        icoreg_fatal("ocl_graph_launch: no graph");
+    icoreg::hip_check(hipGraphLaunch((hipGraphExec_t)graph, icoreg::stream_of(ocl)),
+                      "hipGraphLaunch");
+    ICOREG_API_END
+}
+
+extern "C" void ocl_graph_free(void *graph)
+{
+    if (graph)
+        (void)hipGraphExecDestroy((hipGraphExec_t)graph);
+}
+
 /* ---- events ----------------------------------------------------------- */
 
 #define NEVENTS 1024

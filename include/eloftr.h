@@ -69,6 +69,7 @@ struct eloftr_model {
         rope;
     cl_mem s_blk, row_lse, col_m, col_s, row_max, row_arg, col_max, col_arg;
     cl_mem fu_a, fu_b, fu_c, m_idx, m_out;
+    cl_mem d_mi, d_mj, d_mconf, m_count; /* the matches on the device */
     int blk_rows;
     /* Last match: coarse matches (cell indices i, j and confidence) and
      * their refined positions (x0, y0, x1, y1 per match, pixel index -
@@ -77,7 +78,8 @@ struct eloftr_model {
     int *mi, *mj;
     float *mconf, *kp;
     /* Host copies of the coarse statistics of the last match (n each):
-     * row maximum, row argmax, column argmax. */
+     * row maximum, row argmax, column argmax (read on request by
+     * icoreg_eloftr_coarse_stats). */
     float *h_rmax;
     int *h_rarg, *h_carg;
 };
@@ -99,10 +101,18 @@ void eloftr_match(struct eloftr_model *m, const float *grey0,
                   const float *grey1, const char *dump, int tile);
 
 /* eloftr_match on a pair already in device memory (dev0, dev1: H x W
- * floats each): the same stages with no image upload; the only host
- * transfers are the coarse statistics read for the mutual selection,
- * the match cells written for the fine stage and its result. */
+ * floats each): the same stages with no image upload; the mutual
+ * selection and the fine stage run on the device, and the only host
+ * transfer is the final read of the matches. */
 void eloftr_match_device(struct eloftr_model *m, cl_mem dev0, cl_mem dev1);
+
+/* eloftr_match_device split in two (no counterpart in the reference):
+ * enqueue queues every stage on the library's stream with no host
+ * transfer or synchronisation (so it can be recorded as a HIP graph,
+ * ocl_graph_begin / ocl_graph_end); collect waits and reads the matches
+ * into nm, mi, mj, mconf, kp. */
+void eloftr_match_enqueue(struct eloftr_model *m, cl_mem dev0, cl_mem dev1);
+void eloftr_match_collect(struct eloftr_model *m);
 
 void eloftr_free(struct eloftr_model *m);
 /* Write finep (fine[0], fine[1]: 64 x H x W each), the 2x bilinear resize

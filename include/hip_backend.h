@@ -65,6 +65,18 @@ struct ocl_backend {
 void ocl_init(struct ocl_backend *ocl, const char *device_opt,
               const char *platform_opt);
 
+/* No counterpart in the reference (the reference has no graphs): the
+ * launches and device copies queued on the library's stream between
+ * ocl_graph_begin and ocl_graph_end are recorded, not run, into a HIP
+ * graph that ocl_graph_launch replays on the stream. Calls that allocate,
+ * read, write or synchronise are errors while recording (run the work
+ * once before recording, so that the ops work buffer has its size). The
+ * graph holds the buffer addresses of the recording. */
+void ocl_graph_begin(struct ocl_backend *ocl);
+void *ocl_graph_end(struct ocl_backend *ocl);
+void ocl_graph_launch(struct ocl_backend *ocl, void *graph);
+void ocl_graph_free(void *graph);
+
 /* Synchronize, destroy the stream, reset the struct. */
 void ocl_free(struct ocl_backend *ocl);
 

@@ -24,11 +24,12 @@ struct eloftr_model *icoreg_eloftr_new(void);
 void icoreg_struct_delete(void *p);
 
 /* Results of the last eloftr_match: match count, host arrays (owned by
- * the model), coarse statistics (n = (H / 8) (W / 8) each). */
+ * the model); coarse statistics (n = (H / 8) (W / 8) each), read from the
+ * device into the model's host copies on each call. */
 int icoreg_eloftr_result(const struct eloftr_model *m, const int **mi,
                          const int **mj, const float **mconf,
                          const float **kp);
-int icoreg_eloftr_coarse_stats(const struct eloftr_model *m,
+int icoreg_eloftr_coarse_stats(struct eloftr_model *m,
                                const float **row_max, const int **row_arg,
                                const int **col_arg);
 void icoreg_eloftr_set_pos_scale(struct eloftr_model *m, float s);

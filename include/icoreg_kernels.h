@@ -59,6 +59,22 @@ void eloftr_fine(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
 void eloftr_fine_half(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
                       cl_mem cells, int M, float T, cl_mem out);
 
+/* No counterpart in the reference: eloftr_fine_half for the first
+ * *count of at most nmax matches, the count read on the device (the
+ * driver's matches never come back to the host before fine matching). */
+void eloftr_fine_half_count(struct ops *o, cl_mem f0, cl_mem f1, int H, int W,
+                            cl_mem cells, cl_mem count, int nmax, float T, cl_mem out);
+
+/* The mutual nearest-neighbour selection of eloftr.c:606-636 on the
+ * device: cell i (of h x w) is kept with j = row_arg[i] when row_max[i] >
+ * thr, col_arg[j] == i and both cells lie at least border cells inside;
+ * kept matches in raster order into mi, mj, mconf (n each) and cells
+ * (int4 x0, y0, x1, y1); count[0] = their number, count[1] = 1 if a row
+ * argmax was out of range. */
+void eloftr_mutual(struct ops *o, cl_mem row_max, cl_mem row_arg, cl_mem col_arg, int h,
+                   int w, int border, float thr, cl_mem mi, cl_mem mj, cl_mem mconf,
+                   cl_mem cells, cl_mem count);
+
 /* ---- RoMa (roma_kernels.cl) ----------------------------------------------
  * Warps are channel-major (2, n): x then y, normalised to -1..1 with
  * align_corners = 0 (cell centres at -1 + (2 i + 1) / size). */

@@ -340,3 +340,83 @@ def test_network_from_torch_checkpoint(dev, ic, weights, weights_file, tmp_path)
     assert a["nm"] == b["nm"] > 0
     for k in ("row_max", "row_arg", "col_arg", "mi", "mj", "mconf", "kp"):
         assert np.array_equal(a[k], b[k]), k
+
+
+@pytest.mark.parametrize("h,w,seed", [(80, 80, 0), (13, 37, 1), (1, 1, 2), (100, 2, 3)])
+def test_mutual_kernel(dev, ic, h, w, seed):
+    """eloftr_mutual (the mutual selection of eloftr.c:606-636 on the
+    device) against the rule stated in numpy: kept in raster order when
+    the confidence exceeds 0.2 (NaN does not), the column argmax points
+    back, and both cells lie 2 cells inside; cells as (x0, y0, x1, y1)."""
+    rng = np.random.default_rng(seed)
+    n = h * w
+    rarg = rng.integers(0, n, n).astype(np.int32)
+    carg = rng.integers(0, n, n).astype(np.int32)
+    mutual = rng.uniform(size=n) < 0.5
+    carg[rarg[mutual]] = np.nonzero(mutual)[0]
+    rmax = rng.uniform(0, 0.5, n).astype(np.float32)
+    rmax[rng.uniform(size=n) < 0.05] = np.nan
+    rmax[rng.uniform(size=n) < 0.05] = 0.2
+    i = np.arange(n)
+    xi, yi, xj, yj = i % w, i // w, rarg % w, rarg // w
+    keep = ((rmax > 0.2) & (carg[rarg] == i) & (xi >= 2) & (yi >= 2) & (xi < w - 2)
+            & (yi < h - 2) & (xj >= 2) & (yj >= 2) & (xj < w - 2) & (yj < h - 2))
+    br, ba, bc = dev.upload(rmax), dev.upload(rarg), dev.upload(carg)
+    bi, bj, bm = dev.upload(np.full(n, -1, np.int32)), dev.upload(np.full(n, -1, np.int32)), \
+        dev.zeros(n)
+    cells = dev.upload(np.full(4 * n, -1, np.int32))
+    cnt = dev.upload(np.full(2, -1, np.int32))
+    dev.api.eloftr_mutual(dev.po, br.mem, ba.mem, bc.mem, h, w, 2, 0.2, bi.mem, bj.mem,
+                          bm.mem, cells.mem, cnt.mem)
+    c = dev.read(cnt, 2, np.int32)
+    k = np.nonzero(keep)[0]
+    assert c[1] == 0 and c[0] == len(k)
+    assert np.array_equal(dev.read(bi, n, np.int32)[:len(k)], k)
+    assert np.array_equal(dev.read(bj, n, np.int32)[:len(k)], rarg[k])
+    assert np.array_equal(dev.read(bm, n)[:len(k)], rmax[k])
+    got = dev.read(cells, 4 * n, np.int32).reshape(n, 4)[:len(k)]
+    assert np.array_equal(got, np.stack([xi[k], yi[k], xj[k], yj[k]], 1))
+    # An out-of-range row argmax is flagged for the host's error.
+    rarg[n // 2] = n
+    ba2 = dev.upload(rarg)
+    dev.api.eloftr_mutual(dev.po, br.mem, ba2.mem, bc.mem, h, w, 2, 0.2, bi.mem, bj.mem,
+                          bm.mem, cells.mem, cnt.mem)
+    assert dev.read(cnt, 2, np.int32)[1] == 1
+
+
+def test_graph_replays_match_eager(dev, ic, weights_file):
+    """The pair's whole device stage recorded once as a HIP graph
+    (eloftr_match_enqueue between ocl_graph_begin / ocl_graph_end) and
+    replayed three times, with eager matches of another pair and host
+    synchronisations between the replays: every replay gives the eager
+    matches, confidences and keypoints bit for bit."""
+    H, W = 128, 160
+    print(f"[eloftr] graph replays {H}x{W}", flush=True)
+    g0, g1 = synth.eloftr_noise_pair(H, W, shift=(8, 16))
+    h0, h1 = synth.eloftr_noise_pair(H, W, shift=(0, 8), seed=5)
+    net = ic.Eloftr(dev, weights_file, H, W)
+    api, lib = dev.api, ic.lib()
+    graph = None
+    try:
+        b0, b1, c0, c1 = dev.upload(g0), dev.upload(g1), dev.upload(h0), dev.upload(h1)
+        net.match_device(b0, b1)
+        ref = {k: np.array(v, copy=True) if hasattr(v, "__len__") else v
+               for k, v in net.result().items()}
+        assert ref["nm"] > 50
+        api.ocl_graph_begin(dev.pb)
+        api.eloftr_match_enqueue(net.m, b0.mem, b1.mem)
+        graph = api.ocl_graph_end(dev.pb)
+        for rep in range(3):
+            net.match_device(c0, c1)
+            other = net.result()["nm"]
+            dev.finish()
+            api.ocl_graph_launch(dev.pb, graph)
+            api.eloftr_match_collect(net.m)
+            got = net.result()
+            assert got["nm"] == ref["nm"], (rep, other)
+            for k in ("mi", "mj", "mconf", "kp"):
+                assert np.array_equal(np.asarray(got[k]), ref[k]), (rep, k)
+    finally:
+        if graph:
+            lib.ocl_graph_free(graph)
+        net.close()
