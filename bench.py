@@ -189,6 +189,26 @@ def bench_roma(ic, dev, synth, wdir, steps, warmup, profile_steps):
     ms = max(dev.elapsed_ms(e0, e1), wall * 1e3) / steps
     if net.gp_info() != 0:
         raise RuntimeError("RoMa GP kernel not positive definite")
+    # The same pass replayed from one HIP graph.
+    graph = None
+    try:
+        dev.api.ocl_graph_begin(dev.pb)
+        net.coarse_device(pair)
+        graph = dev.api.ocl_graph_end(dev.pb)
+        for _ in range(warmup):
+            dev.api.ocl_graph_launch(dev.pb, graph)
+        dev.finish()
+        dev.reset_events()
+        t0 = time.perf_counter()
+        e0 = dev.event()
+        for _ in range(steps):
+            dev.api.ocl_graph_launch(dev.pb, graph)
+        e1 = dev.event()
+        dev.finish()
+        ms_g = max(dev.elapsed_ms(e0, e1), (time.perf_counter() - t0) * 1e3) / steps
+    finally:
+        if graph:
+            ic.lib().ocl_graph_free(graph)
     dev.profile_reset()
     dev.set_profile(2)
     for _ in range(profile_steps):
@@ -211,6 +231,8 @@ def bench_roma(ic, dev, synth, wdir, steps, warmup, profile_steps):
         "workload": "RoMa coarse forward, 560x560 RGB pair: DINOv2 ViT-L/14 x 2 (1601 tokens), "
                     "GP on 1600 tokens (device fp64 solve), coordinate decoder, cls_to_flow",
         "pairs_per_s": round(1000.0 / ms, 3), "ms_per_pair": round(ms, 4),
+        "graph": {"pairs_per_s": round(1000.0 / ms_g, 3), "ms_per_pair": round(ms_g, 4),
+                  "workload": f"the same pass replayed from one HIP graph ({steps} replays)"},
         "gflop_per_pair": round(fl["total"] / 1e9, 1),
         "pipeline_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
         "roofline": {"kernel": "gemm_mfma (fp32 MFMA GEMM: qkv, proj, MLP, GP, to_out)",

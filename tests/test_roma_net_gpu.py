@@ -273,3 +273,39 @@ def test_roma_v2ref_1024_properties(dev, ic, weights):
     assert np.isfinite(cert).all() and ((cert >= 0) & (cert <= 1)).all()
     ok = np.isfinite(sd)
     assert ok.mean() > 0.99 and (sd[ok] > 0).all()
+
+
+def test_coarse_graph_replays_match_eager(dev, ic, weights):
+    """RoMa's coarse pass (DINOv2, GP solve, decoder: roma_coarse_device,
+    no host transfer inside) recorded once as a HIP graph and replayed
+    three times, with eager passes on another pair and synchronisations
+    between: every replay gives the eager warp, certainty and GP solution
+    bit for bit."""
+    print(f"[roma] coarse graph replays coarse={COARSE}", flush=True)
+    (fm, fd, _), _ = weights
+    a, b, _ = synth.roma_pair(COARSE, COARSE)
+    c, d, _ = synth.roma_pair(COARSE, COARSE, seed=11)
+    net = ic.Roma(dev, fm, fd, COARSE, COARSE, coarse=COARSE)
+    api, lib = dev.api, ic.lib()
+    n = (COARSE // 14) ** 2
+    graph = None
+    try:
+        p0, p1 = dev.upload(np.stack([a, b])), dev.upload(np.stack([c, d]))
+        read = lambda: [net.buffer("fl0", 2 * n), net.buffer("ce0", n),
+                        net.buffer("g_f", n * 512)]
+        net.coarse_device(p0)
+        ref = read()
+        api.ocl_graph_begin(dev.pb)
+        net.coarse_device(p0)
+        graph = api.ocl_graph_end(dev.pb)
+        for rep in range(3):
+            net.coarse_device(p1)
+            dev.finish()
+            api.ocl_graph_launch(dev.pb, graph)
+            dev.finish()
+            for k, (g, r) in enumerate(zip(read(), ref)):
+                assert np.array_equal(g, r), (rep, k)
+    finally:
+        if graph:
+            lib.ocl_graph_free(graph)
+        net.close()
