@@ -234,6 +234,16 @@ __global__ void __launch_bounds__(256)
 
 typedef float lc_f4 __attribute__((ext_vector_type(4)));
 
+/* Any patch counted by local_corr_scan_kernel (nc block counts). */
+__device__ __forceinline__ bool lc_any_scattered(const int *__restrict__ counts, int nc)
+{
+    int any = 0;
+
+    for (int i = 0; i < nc; i++)
+        any |= counts[i];
+    return any != 0;
+}
+
 /* Block L of T to a tile: the 8 XCDs (blocks L, L + 8, ... on XCD L % 8)
  * each get a contiguous band of tiles. */
 __device__ __forceinline__ int lc_xcd_tile(int L, int T)
@@ -243,11 +253,16 @@ __device__ __forceinline__ int lc_xcd_tile(int L, int T)
     return (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + idx;
 }
 
+/* f1, f2 channel-major (C x n). t1, t2 (or NULL): the same maps
+ * cell-major (n x C, C % 4 == 0), read by the per-cell path, whose window
+ * reads then run along each window cell's own channel row. */
 __global__ void __launch_bounds__(256)
     local_corr_kernel(const float *__restrict__ f1,
                       const float *__restrict__ f2, int C, int H, int W, int r,
                       const float *__restrict__ flow, float *__restrict__ out,
-                      int coff)
+                      int coff, const float *__restrict__ t1,
+                      const float *__restrict__ t2, const int *__restrict__ tcounts,
+                      int tnc)
 {
     __shared__ float G[LC_T * LC_GS]; /* products of the patch's cells */
     __shared__ int cid[LC_T], ox[LC_T], oy[LC_T], okc[LC_T];
@@ -386,15 +401,36 @@ __global__ void __launch_bounds__(256)
                 ok[q] = e < ps * ps && xx >= 0 && xx < W && yy >= 0 && yy < H;
                 off[q] = ok[q] ? yy * W + xx : 0;
             }
-            for (int c = 0; c < C; c++) {
-                const float a = f1[(long long)c * n + i] * rc;
-                const float *p = f2 + (long long)c * n;
+            if (t1 && lc_any_scattered(tcounts, tnc)) {
+                /* Lane by lane along each window cell's own channel row
+                 * (the copies exist: this patch was counted). */
+                const float *pa = t1 + (long long)i * C;
+
+                for (int c = 0; c < C; c += 4) {
+                    const lc_f4 a = *(const lc_f4 *)(pa + c) * rc;
 
 #pragma unroll
-                for (int q = 0; q < 4; q++)
-                    if (ok[q])
-                        a4[q] = fmaf(a, p[off[q]], a4[q]);
+                    for (int q = 0; q < 4; q++)
+                        if (ok[q]) {
+                            const lc_f4 b = *(const lc_f4 *)(t2 + (long long)off[q] * C + c);
+
+                            a4[q] = fmaf(a[0], b[0], a4[q]);
+                            a4[q] = fmaf(a[1], b[1], a4[q]);
+                            a4[q] = fmaf(a[2], b[2], a4[q]);
+                            a4[q] = fmaf(a[3], b[3], a4[q]);
+                        }
+                }
             }
+            else
+                for (int c = 0; c < C; c++) {
+                    const float a = f1[(long long)c * n + i] * rc;
+                    const float *p = f2 + (long long)c * n;
+
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        if (ok[q])
+                            a4[q] = fmaf(a, p[off[q]], a4[q]);
+                }
 #pragma unroll
             for (int q = 0; q < 4; q++)
                 if (lane + 64 * q < ps * ps)
@@ -652,6 +688,87 @@ extern "C" void roma_warp_sample(struct ops *o, cl_mem in, int C, int H, int W,
     ICOREG_API_END
 }
 
+/* Patches whose windows do not fit one LC_NB-cell box (the per-cell path
+ * of local_corr_kernel), counted per block of 256 patches into
+ * counts[blockIdx.x]: one thread per 4 x 4 patch, the box formed as the
+ * kernel forms it. */
+__global__ void __launch_bounds__(256)
+    local_corr_scan_kernel(const float *__restrict__ flow, int H, int W, int r,
+                           int *__restrict__ counts)
+{
+    const int tiles_x = (W + 3) >> 2, ntiles = tiles_x * ((H + 3) >> 2);
+    const int t = blockIdx.x * 256 + threadIdx.x, n = H * W, ps = 2 * r + 2;
+    const int px0 = (t % tiles_x) * 4, py0 = (t / tiles_x) * 4;
+    int lo_x = INT_MAX, lo_y = INT_MAX, hi_x = INT_MIN, hi_y = INT_MIN;
+
+    for (int c = 0; c < LC_T && t < ntiles; c++) {
+        const int x = px0 + (c & 3), y = py0 + (c >> 2);
+
+        if (x < W && y < H) {
+            const int ci = y * W + x;
+            const bil b = bilinear_setup(flow[ci], flow[n + ci], H, W, r);
+
+            if (b.ok) {
+                lo_x = min(lo_x, b.x0 - r);
+                lo_y = min(lo_y, b.y0 - r);
+                hi_x = max(hi_x, b.x0 - r + ps - 1);
+                hi_y = max(hi_y, b.y0 - r + ps - 1);
+            }
+        }
+    }
+    lo_x = max(lo_x, 0);
+    lo_y = max(lo_y, 0);
+    hi_x = min(hi_x, W - 1);
+    hi_y = min(hi_y, H - 1);
+    {
+        const int bw = hi_x >= lo_x ? hi_x - lo_x + 1 : 0, bh = hi_y >= lo_y ? hi_y - lo_y + 1 : 0;
+        const int nsc = __syncthreads_count(t < ntiles && bw * bh > LC_NB);
+
+        if (threadIdx.x == 0)
+            counts[blockIdx.x] = nsc;
+    }
+}
+
+
+/* (C x n) to (n x C) for both maps, 32 x 32 tiles through LDS, the grid
+ * striding over the tiles of both; nothing when no patch scatters (then
+ * the launch costs a few microseconds). */
+__global__ void __launch_bounds__(256)
+    lc_transpose_kernel(const float *__restrict__ f1, const float *__restrict__ f2,
+                        float *__restrict__ o1, float *__restrict__ o2, int C, int n,
+                        const int *__restrict__ counts, int nc)
+{
+    __shared__ float t[32][33];
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    const int tiles_i = (n + 31) / 32, tiles = tiles_i * ((C + 31) / 32);
+
+    if (!lc_any_scattered(counts, nc))
+        return;
+    for (int u = blockIdx.x; u < 2 * tiles; u += gridDim.x) {
+        const int z = u >= tiles, v = u - z * tiles;
+        const int i0 = (v % tiles_i) * 32, c0 = (v / tiles_i) * 32;
+        const float *in = z ? f2 : f1;
+        float *out = z ? o2 : o1;
+
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 32; k += 8) {
+            const int c = c0 + ty + k, i = i0 + tx;
+
+            if (c < C && i < n)
+                t[ty + k][tx] = in[(long long)c * n + i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 32; k += 8) {
+            const int i = i0 + ty + k, c = c0 + tx;
+
+            if (c < C && i < n)
+                out[(long long)i * C + c] = t[tx][ty + k];
+        }
+    }
+}
+
 extern "C" void roma_local_corr(struct ops *o, cl_mem f1, cl_mem f2, int C,
                                 int H, int W, int r, cl_mem flow, cl_mem out,
                                 int coff)
@@ -673,11 +790,36 @@ extern "C" void roma_local_corr(struct ops *o, cl_mem f1, cl_mem f2, int C,
     need_floats(flow, 0, 2 * n, op, "flow");
     need_floats(out, (long long)coff * n, (long long)(2 * r + 1) * (2 * r + 1) * n,
                 op, "out");
-    prof_scope ps(o->ocl, op);
-    hipLaunchKernelGGL(local_corr_kernel,
-                       dim3((unsigned)(((W + 3) / 4) * ((H + 3) / 4))), dim3(256), 0,
-                       stream_of(o->ocl), cfptr(f1), cfptr(f2), C, H, W, r,
-                       cfptr(flow), fptr(out), coff);
+    {
+        const int tiles = ((W + 3) / 4) * ((H + 3) / 4);
+        const dim3 grid((unsigned)tiles);
+        hipStream_t st = stream_of(o->ocl);
+
+        prof_scope ps(o->ocl, op);
+        if (C % 4 == 0) {
+            /* Cell-major copies for the per-cell path, made only when a
+             * patch scatters (counted first on the device). */
+            const size_t cn = (size_t)C * n;
+            const int nc = (tiles + 255) / 256;
+            cl_mem sc = scratch_get(o, 2 * cn * sizeof(float) + (size_t)nc * sizeof(int));
+            float *t1 = (float *)sc->ptr, *t2 = t1 + cn;
+            int *counts = (int *)(t2 + cn);
+            const long long ttiles = 2LL * ((n + 31) / 32) * ((C + 31) / 32);
+            const dim3 tg((unsigned)(ttiles < 2048 ? ttiles : 2048));
+
+            hipLaunchKernelGGL(local_corr_scan_kernel, dim3((unsigned)nc), dim3(256), 0, st,
+                               cfptr(flow), H, W, r, counts);
+            hipLaunchKernelGGL(lc_transpose_kernel, tg, dim3(256), 0, st, cfptr(f1), cfptr(f2),
+                               t1, t2, C, (int)n, (const int *)counts, nc);
+            hipLaunchKernelGGL(local_corr_kernel, grid, dim3(256), 0, st, cfptr(f1),
+                               cfptr(f2), C, H, W, r, cfptr(flow), fptr(out), coff,
+                               (const float *)t1, (const float *)t2, (const int *)counts, nc);
+        }
+        else
+            hipLaunchKernelGGL(local_corr_kernel, grid, dim3(256), 0, st, cfptr(f1),
+                               cfptr(f2), C, H, W, r, cfptr(flow), fptr(out), coff, nullptr,
+                               nullptr, nullptr, 0);
+    }
     launch_check(op);
     ICOREG_API_END
 }
