@@ -141,7 +141,13 @@ __global__ void __launch_bounds__(256)
                        const float2 *__restrict__ grid, int n, int align,
                        float *__restrict__ out)
 {
-    const int i = blockIdx.x * 256 + threadIdx.x, c0 = blockIdx.y * GS_CG;
+    /* Block L -> (point block, channel group), groups fastest, in
+     * contiguous bands per XCD (L % 8): neighbouring point blocks of a
+     * smooth grid share input rows, fetched once into that XCD's L2. */
+    const int ng = (C + GS_CG - 1) / GS_CG, total = gridDim.x;
+    const int q = total >> 3, rem = total & 7, xc = blockIdx.x & 7, idx = blockIdx.x >> 3;
+    const int ord = (xc < rem ? xc * (q + 1) : rem * (q + 1) + (xc - rem) * q) + idx;
+    const int i = (ord / ng) * 256 + threadIdx.x, c0 = (ord % ng) * GS_CG;
     const long long plane = (long long)H * W;
     float2 g;
     float ix, iy, fx = 0.0f, fy = 0.0f, v[GS_CG][4];
@@ -210,8 +216,10 @@ extern "C" void ops_grid_sample(struct ops *o, cl_mem in, int C, int H, int W,
     need_floats(grid, 0, 2LL * n, op, "grid");
     need_floats(out, 0, (long long)C * n, op, "out");
     prof_scope ps(o->ocl, "grid_sample");
+    if ((long long)((n + 255) / 256) * ((C + GS_CG - 1) / GS_CG) >= (1LL << 31))
+        icoreg_fatal("%s: grid too large", op);
     hipLaunchKernelGGL(grid_sample_kernel,
-                       dim3((unsigned)((n + 255) / 256), (unsigned)((C + GS_CG - 1) / GS_CG)),
+                       dim3((unsigned)((long long)((n + 255) / 256) * ((C + GS_CG - 1) / GS_CG))),
                        dim3(256), 0, stream_of(o->ocl), cfptr(in), C, H, W,
                        (const float2 *)cfptr(grid), n, align_corners,
                        fptr(out));

@@ -163,8 +163,14 @@ __global__ void __launch_bounds__(256)
                        const float *__restrict__ flow, float *__restrict__ out,
                        int coff)
 {
-    const int i = blockIdx.x * 256 + threadIdx.x, n = H * W;
-    const int c0 = blockIdx.y * WS_CG;
+    /* Block L -> (cell block, channel group), channel groups fastest; the
+     * XCDs (L % 8) get contiguous bands of that order, so that the input
+     * rows two neighbouring cell blocks share are fetched into one L2. */
+    const int ng = (C + WS_CG - 1) / WS_CG, total = gridDim.x;
+    const int q = total >> 3, rem = total & 7, x = blockIdx.x & 7, idx = blockIdx.x >> 3;
+    const int ord = (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + idx;
+    const int n = H * W, i = (ord / ng) * 256 + threadIdx.x;
+    const int c0 = (ord % ng) * WS_CG;
     bil b;
     bool in00, in01, in10, in11;
     int o00, o01, o10, o11;
@@ -681,7 +687,9 @@ extern "C" void roma_warp_sample(struct ops *o, cl_mem in, int C, int H, int W,
     need_floats(flow, 0, 2 * n, op, "flow");
     need_floats(out, (long long)coff * n, (long long)C * n, op, "out");
     prof_scope ps(o->ocl, op);
-    hipLaunchKernelGGL(warp_sample_kernel, dim3(nblk(n, 256), nblk(C, WS_CG)), dim3(256),
+    if ((long long)nblk(n, 256) * nblk(C, WS_CG) >= (1LL << 31))
+        icoreg_fatal("%s: grid too large", op);
+    hipLaunchKernelGGL(warp_sample_kernel, dim3(nblk(n, 256) * nblk(C, WS_CG)), dim3(256),
                        0, stream_of(o->ocl), cfptr(in), C, H, W, cfptr(flow),
                        fptr(out), coff);
     launch_check(op);
