@@ -219,36 +219,36 @@ __global__ void __launch_bounds__(256)
  * (clipped to the image) is a box of about (4 + 2 r + 1)^2 cells instead
  * of 16 (2 r + 2)^2 reads. When the box holds at most LC_NB cells, the
  * block forms every patch-cell x box-cell product on the matrix cores
- * (v_mfma_f32_16x16x4f32: 16 cells x 16 box cells x 4 channels, box
- * tiles shared out over the 4 waves), each wave streaming its operands
- * from memory straight into registers with no LDS staging and no
- * barriers (32 channels of loads in flight per wave). Each cell then
- * reads its window's products from the box. Patches whose windows
- * scatter (far-off or broken warps) take the per-cell path instead: one
- * wave per cell, lanes over the window cells, channels in order.
- * Patches go to the XCDs in contiguous bands, so that neighbouring
- * patches share their f2 rows in one L2.
+ * (v_mfma_f32_16x16x4f32: 16 cells x 16 box cells x 4 channels), each
+ * wave streaming its operands from memory straight into registers with
+ * no LDS staging and no barriers. Each cell then reads its window's
+ * products from the box. Patches whose windows scatter (far-off or
+ * broken warps) take a per-cell path instead. Patches go to the XCDs in
+ * contiguous bands, so that neighbouring patches share their f2 rows in
+ * one L2.
  *
- * Measured at 864 x 864 (1/8: C = 512, r = 3; 1/4: C = 256, r = 2) the
- * kernel is bound by L1 misses (each 4 x 4 patch touches its box rows
- * channel by channel, 16-44 bytes of every 128-byte line), not by HBM or
- * the matrix cores. */
+ * Two forms:
+ *  - cell-major (C % 4 == 0, local_corr_cm_kernel): both maps are first
+ *    transposed to (n x C), so that a box cell's channels are one
+ *    contiguous row: every operand load is 16 bytes of a lane's own
+ *    4 channels, and a 16-channel chunk of a cell is one 64-byte piece.
+ *    Each of the 4 waves takes all box tiles over a quarter of the
+ *    channels (so a patch or box row is loaded once per block), and the
+ *    quarters' products meet in LDS. The per-cell path puts 16
+ *    lanes on each window cell (4 window cells per load instruction,
+ *    256 contiguous bytes each) and sums the 16 lanes by DPP;
+ *  - channel-major (other C, local_corr_kernel): operands read straight
+ *    from the (C x n) maps, 4-byte loads of 4 channels x 16 cells per
+ *    instruction (16-44 bytes of every 128-byte line: bound by L1
+ *    misses), the box tiles shared out over the 4 waves; per-cell path:
+ *    one wave per cell, lanes over the window cells, channels in order. */
 #define CORR_MAXC 1024 /* channels accepted (the reference's kernel: 512) */
 #define LC_T 16        /* cells of a patch (4 x 4) */
 #define LC_NB 256      /* box cells on the matrix-core path */
 #define LC_GS 260      /* LDS row pitch of the products */
+#define LC_PG 148      /* LDS row pitch of a channel-quarter plane (<= 144 box cells) */
 
 typedef float lc_f4 __attribute__((ext_vector_type(4)));
-
-/* Any patch counted by local_corr_scan_kernel (nc block counts). */
-__device__ __forceinline__ bool lc_any_scattered(const int *__restrict__ counts, int nc)
-{
-    int any = 0;
-
-    for (int i = 0; i < nc; i++)
-        any |= counts[i];
-    return any != 0;
-}
 
 /* Block L of T to a tile: the 8 XCDs (blocks L, L + 8, ... on XCD L % 8)
  * each get a contiguous band of tiles. */
@@ -259,30 +259,22 @@ __device__ __forceinline__ int lc_xcd_tile(int L, int T)
     return (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + idx;
 }
 
-/* f1, f2 channel-major (C x n). t1, t2 (or NULL): the same maps
- * cell-major (n x C, C % 4 == 0), read by the per-cell path, whose window
- * reads then run along each window cell's own channel row. */
-__global__ void __launch_bounds__(256)
-    local_corr_kernel(const float *__restrict__ f1,
-                      const float *__restrict__ f2, int C, int H, int W, int r,
-                      const float *__restrict__ flow, float *__restrict__ out,
-                      int coff, const float *__restrict__ t1,
-                      const float *__restrict__ t2, const int *__restrict__ tcounts,
-                      int tnc)
-{
-    __shared__ float G[LC_T * LC_GS]; /* products of the patch's cells */
-    __shared__ int cid[LC_T], ox[LC_T], oy[LC_T], okc[LC_T];
-    __shared__ float cfx[LC_T], cfy[LC_T];
-    __shared__ int box[4];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int tiles_x = (W + 3) >> 2, ntiles = tiles_x * ((H + 3) >> 2);
-    const int tile_id = lc_xcd_tile(blockIdx.x, ntiles);
-    const int px0 = (tile_id % tiles_x) * 4, py0 = (tile_id / tiles_x) * 4;
-    const int n = H * W, ps = 2 * r + 2, side = 2 * r + 1;
-    const float rc = 1.0f / sqrtf((float)C);
+/* A patch's cells (index, or -1 outside the map; whether the warp is
+ * finite; window origin; bilinear fractions) and the box of their
+ * windows clipped to the map (x0, y0, width, height). */
+struct lc_patch {
+    int cid[LC_T], ox[LC_T], oy[LC_T], okc[LC_T];
+    float cfx[LC_T], cfy[LC_T];
+    int box[4];
+};
 
-    /* The patch's cells: window origins and the box of their windows. */
+/* Fills p for the 4 x 4 patch at (px0, py0) from threads 0..63; the
+ * caller's barrier follows. */
+__device__ __forceinline__ void lc_setup(lc_patch &p, const float *__restrict__ flow, int H,
+                                         int W, int r, int px0, int py0, int tid)
+{
+    const int n = H * W, ps = 2 * r + 2;
+
     if (tid < 64) {
         const int x = px0 + (tid & 3), y = py0 + ((tid >> 2) & 3);
         int lo_x = INT_MAX, lo_y = INT_MAX, hi_x = INT_MIN, hi_y = INT_MIN;
@@ -295,12 +287,12 @@ __global__ void __launch_bounds__(256)
                 ci = y * W + x;
                 b = bilinear_setup(flow[ci], flow[n + ci], H, W, r);
             }
-            cid[tid] = ci;
-            okc[tid] = ci >= 0 && b.ok;
-            ox[tid] = b.x0 - r;
-            oy[tid] = b.y0 - r;
-            cfx[tid] = b.fx;
-            cfy[tid] = b.fy;
+            p.cid[tid] = ci;
+            p.okc[tid] = ci >= 0 && b.ok;
+            p.ox[tid] = b.x0 - r;
+            p.oy[tid] = b.y0 - r;
+            p.cfx[tid] = b.fx;
+            p.cfy[tid] = b.fy;
             if (ci >= 0 && b.ok) {
                 lo_x = b.x0 - r;
                 lo_y = b.y0 - r;
@@ -320,13 +312,87 @@ __global__ void __launch_bounds__(256)
             lo_y = max(lo_y, 0);
             hi_x = min(hi_x, W - 1);
             hi_y = min(hi_y, H - 1);
-            box[0] = lo_x;
-            box[1] = lo_y;
-            box[2] = hi_x >= lo_x ? hi_x - lo_x + 1 : 0;
-            box[3] = hi_y >= lo_y ? hi_y - lo_y + 1 : 0;
+            p.box[0] = lo_x;
+            p.box[1] = lo_y;
+            p.box[2] = hi_x >= lo_x ? hi_x - lo_x + 1 : 0;
+            p.box[3] = hi_y >= lo_y ? hi_y - lo_y + 1 : 0;
         }
     }
+}
+
+/* The outputs of the patch: out[coff + k, i] for its cells i and the
+ * (2 r + 1)^2 offsets k, the bilinear combination of the cell's window
+ * products. Tiled: np partial planes G + j pstride (rows gs apart, row m
+ * x box cell) added in order j = 0 .. np - 1; else G row m (LC_GS
+ * apart) holds cell m's (2 r + 2)^2 window. Consecutive threads take
+ * consecutive cells of one offset. */
+__device__ __forceinline__ void lc_outputs(const lc_patch &p, const float *G, int np, int pstride,
+                                           int gs, bool tiled, int r, int n,
+                                           float *__restrict__ out, int coff, int tid)
+{
+    const int ps = 2 * r + 2, side = 2 * r + 1;
+    const int bx0 = p.box[0], by0 = p.box[1], bw = p.box[2], bh = p.box[3];
+
+    for (int idx = tid; idx < LC_T * side * side; idx += 256) {
+        const int m = idx & 15, k = idx >> 4;
+        const int i = p.cid[m];
+
+        if (i < 0)
+            continue;
+        float v = 0.0f;
+
+        if (p.okc[m]) {
+            const int ky = k / side, kx = k - ky * side;
+            const int yy = p.oy[m] + ky, xx = p.ox[m] + kx;
+            const float fx = p.cfx[m], fy = p.cfy[m];
+            float s[4];
+
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int y = yy + (q >> 1), x = xx + (q & 1);
+
+                if (tiled) {
+                    const int e = m * gs + (y - by0) * bw + (x - bx0);
+                    const bool in = x >= bx0 && x < bx0 + bw && y >= by0 && y < by0 + bh;
+                    float v2 = 0.0f;
+
+                    if (in) {
+                        v2 = G[e];
+                        for (int j = 1; j < np; j++)
+                            v2 += G[e + j * pstride];
+                    }
+                    s[q] = v2;
+                }
+                else
+                    s[q] = G[m * LC_GS + (ky + (q >> 1)) * ps + kx + (q & 1)];
+            }
+            v = (1.0f - fy) * ((1.0f - fx) * s[0] + fx * s[1]) +
+                fy * ((1.0f - fx) * s[2] + fx * s[3]);
+        }
+        out[(long long)(coff + k) * n + i] = v;
+    }
+}
+
+/* Channel-major form: f1, f2 (C x n). */
+__global__ void __launch_bounds__(256)
+    local_corr_kernel(const float *__restrict__ f1,
+                      const float *__restrict__ f2, int C, int H, int W, int r,
+                      const float *__restrict__ flow, float *__restrict__ out,
+                      int coff)
+{
+    __shared__ float G[LC_T * LC_GS]; /* products of the patch's cells */
+    __shared__ lc_patch pt;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tiles_x = (W + 3) >> 2, ntiles = tiles_x * ((H + 3) >> 2);
+    const int tile_id = lc_xcd_tile(blockIdx.x, ntiles);
+    const int n = H * W, ps = 2 * r + 2;
+    const float rc = 1.0f / sqrtf((float)C);
+    const int *cid = pt.cid, *okc = pt.okc, *ox = pt.ox, *oy = pt.oy;
+
+    lc_setup(pt, flow, H, W, r, (tile_id % tiles_x) * 4, (tile_id / tiles_x) * 4, tid);
     __syncthreads();
+    const int *box = pt.box;
     const int bx0 = box[0], by0 = box[1], bw = box[2], bh = box[3];
     const int nb = bw * bh;
     const bool tiled = nb <= LC_NB;
@@ -407,36 +473,15 @@ __global__ void __launch_bounds__(256)
                 ok[q] = e < ps * ps && xx >= 0 && xx < W && yy >= 0 && yy < H;
                 off[q] = ok[q] ? yy * W + xx : 0;
             }
-            if (t1 && lc_any_scattered(tcounts, tnc)) {
-                /* Lane by lane along each window cell's own channel row
-                 * (the copies exist: this patch was counted). */
-                const float *pa = t1 + (long long)i * C;
-
-                for (int c = 0; c < C; c += 4) {
-                    const lc_f4 a = *(const lc_f4 *)(pa + c) * rc;
+            for (int c = 0; c < C; c++) {
+                const float a = f1[(long long)c * n + i] * rc;
+                const float *p = f2 + (long long)c * n;
 
 #pragma unroll
-                    for (int q = 0; q < 4; q++)
-                        if (ok[q]) {
-                            const lc_f4 b = *(const lc_f4 *)(t2 + (long long)off[q] * C + c);
-
-                            a4[q] = fmaf(a[0], b[0], a4[q]);
-                            a4[q] = fmaf(a[1], b[1], a4[q]);
-                            a4[q] = fmaf(a[2], b[2], a4[q]);
-                            a4[q] = fmaf(a[3], b[3], a4[q]);
-                        }
-                }
+                for (int q = 0; q < 4; q++)
+                    if (ok[q])
+                        a4[q] = fmaf(a, p[off[q]], a4[q]);
             }
-            else
-                for (int c = 0; c < C; c++) {
-                    const float a = f1[(long long)c * n + i] * rc;
-                    const float *p = f2 + (long long)c * n;
-
-#pragma unroll
-                    for (int q = 0; q < 4; q++)
-                        if (ok[q])
-                            a4[q] = fmaf(a, p[off[q]], a4[q]);
-                }
 #pragma unroll
             for (int q = 0; q < 4; q++)
                 if (lane + 64 * q < ps * ps)
@@ -444,36 +489,255 @@ __global__ void __launch_bounds__(256)
         }
     }
     __syncthreads();
-    /* Outputs: consecutive threads take consecutive cells of one offset. */
-    for (int idx = tid; idx < LC_T * side * side; idx += 256) {
-        const int m = idx & 15, k = idx >> 4;
-        const int i = cid[m];
+    lc_outputs(pt, G, 1, 0, LC_GS, tiled, r, n, out, coff, tid);
+}
 
-        if (i < 0)
-            continue;
-        float v = 0.0f;
+/* Sum over the 16 lanes of each DPP row (every lane of the row gets it). */
+__device__ __forceinline__ float lc_row_sum(float v)
+{
+    v += dpp_f(v, 0xB1);
+    v += dpp_f(v, 0x4E);
+    v += dpp_f(v, 0x141);
+    v += dpp_f(v, 0x140);
+    return v;
+}
 
-        if (okc[m]) {
-            const int ky = k / side, kx = k - ky * side;
-            const int yy = oy[m] + ky, xx = ox[m] + kx;
-            const float fx = cfx[m], fy = cfy[m];
-            float s[4];
+/* Loads at or past this byte offset of a buffer window return zeros. */
+#define LC_OOB 0x80000000u
+
+/* Raw buffer window over bytes bytes from p (< 2^31). */
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t lc_rsrc(const float *p, unsigned bytes)
+{
+    /* Word 3: 32-bit data, the gfx9-family raw buffer format. */
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ lc_f4 lc_load4(__amdgpu_buffer_rsrc_t r, unsigned off)
+{
+    return __builtin_bit_cast(lc_f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+/* NQ box tiles of the cell-major tiled path for one wave: the 16-channel
+ * chunks kw, kw + 4, ... (nch chunks in all) into acc[t]. ra, rb: windows
+ * over the two cell-major maps; ao / bo[t]: byte offset of the lane's
+ * patch cell / box cell row of tile t (LC_OOB: none), plus 16 (4 kq)
+ * for its channels. A chunk past C or a missing cell loads zeros from
+ * past the window's end, so that the loop has no branches and two
+ * chunks load while two multiply. */
+template <int NQ>
+__device__ __forceinline__ void lc_cm_tiles(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                            unsigned ao, const unsigned (&bo)[9], int kw, int nch,
+                                            int C, int kq, float rc, lc_f4 (&acc)[9])
+{
+    auto load = [&](int q, lc_f4 &a, lc_f4 (&b)[NQ]) {
+        const int c = q * 16 + 4 * kq;
+        const bool cok = q < nch && c < C;
+        const unsigned cb = 64u * q;
+
+        a = lc_load4(ra, cok && ao != LC_OOB ? ao + cb : LC_OOB) * rc;
+#pragma unroll
+        for (int t = 0; t < NQ; t++)
+            b[t] = lc_load4(rb, cok && bo[t] != LC_OOB ? bo[t] + cb : LC_OOB);
+    };
+    auto mul = [&](const lc_f4 &a, const lc_f4 (&b)[NQ]) {
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int t = 0; t < NQ; t++)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[t][s], acc[t], 0, 0, 0);
+    };
+    lc_f4 a0, a1, b0[NQ], b1[NQ];
+
+    /* The scheduling barriers keep this order: the compiler would
+     * otherwise gather both chunks' loads at the end of the body and wait
+     * for all of them at its top. */
+    load(kw, a0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(kw + 4, a1, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    for (int q = kw; q < nch; q += 8) {
+        mul(a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(q + 8, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        mul(a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        load(q + 12, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+/* Cell-major form: t1, t2 are f1, f2 as (n x C) with rows ld floats
+ * apart (C % 4 == 0, ld % 4 == 0, the maps 16-byte aligned). */
+__global__ void __launch_bounds__(256)
+    local_corr_cm_kernel(const float *__restrict__ t1, const float *__restrict__ t2, int C,
+                         int ld, int H, int W, int r, const float *__restrict__ flow,
+                         float *__restrict__ out, int coff)
+{
+    /* Products of the patch's cells: four planes LC_T x LC_PG (tiled path,
+     * at most 144 box cells), two planes LC_T x LC_GS (tiled path, more),
+     * or LC_T rows LC_GS apart (per-cell path's windows). */
+    __shared__ float G[4 * LC_T * LC_PG];
+    __shared__ lc_patch pt;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tiles_x = (W + 3) >> 2, ntiles = tiles_x * ((H + 3) >> 2);
+    const int tile_id = lc_xcd_tile(blockIdx.x, ntiles);
+    const int n = H * W, ps = 2 * r + 2;
+    const float rc = 1.0f / sqrtf((float)C);
+    const int m = lane & 15, kq = lane >> 4;
+
+    lc_setup(pt, flow, H, W, r, (tile_id % tiles_x) * 4, (tile_id / tiles_x) * 4, tid);
+    __syncthreads();
+    const int bx0 = pt.box[0], by0 = pt.box[1], bw = pt.box[2], bh = pt.box[3];
+    const int nb = bw * bh;
+    const bool tiled = nb <= LC_NB;
+
+    if (tiled) {
+        /* Wave wv takes the 16-channel chunks wv, wv + 4, ... of all box
+         * tiles (up to nine at a time), so that each patch and box row is loaded
+         * once per block. Per chunk lane l reads channels 4 (l / 16) .. + 3
+         * of patch cell l % 16 and of box cell 16 t + l % 16 of each tile t
+         * as one 16-byte load; in MFMA step s the lane's k index (l / 16)
+         * stands for channel 4 (l / 16) + s of the chunk, the same channel
+         * in both operands. The four channel quarters' products meet in
+         * LDS in a fixed order: with at most 9 tiles each wave stores into
+         * its own plane (LC_PG pitch) and the outputs add the four planes;
+         * with more, per 8 tiles waves 2 and 3 store into two planes
+         * (LC_GS pitch), waves 0 and 1 add theirs after a barrier, and the
+         * outputs add the two planes. */
+        const int nt = (nb + 15) >> 4, nch = (C + 15) >> 4;
+        const int acell = pt.cid[m];
+        const unsigned bytes = (unsigned)n * (unsigned)ld * 4u;
+        const __amdgpu_buffer_rsrc_t ra = lc_rsrc(t1, bytes), rb = lc_rsrc(t2, bytes);
+        const unsigned ao = acell >= 0 ? ((unsigned)acell * ld + 4 * kq) * 4u : LC_OOB;
+        const bool four = nt <= 9;
+        const int gp = four ? LC_PG : LC_GS, gsz = four ? 9 : 8;
+        float *Gw = G + (four ? wv : (wv & 1)) * LC_T * gp;
+
+        for (int u0 = 0; u0 < nt; u0 += gsz) {
+            const int nq = nt - u0 < gsz ? nt - u0 : gsz;
+            unsigned bo[9];
+            lc_f4 acc[9];
 
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int y = yy + (q >> 1), x = xx + (q & 1);
+            for (int t = 0; t < 9; t++) {
+                const int j = (u0 + t) * 16 + m;
 
-                if (tiled)
-                    s[q] = x >= bx0 && x < bx0 + bw && y >= by0 && y < by0 + bh
-                               ? G[m * LC_GS + (y - by0) * bw + (x - bx0)]
-                               : 0.0f;
-                else
-                    s[q] = G[m * LC_GS + (ky + (q >> 1)) * ps + kx + (q & 1)];
+                bo[t] = t < nq && j < nb
+                            ? ((unsigned)((by0 + j / bw) * W + bx0 + j % bw) * ld + 4 * kq) * 4u
+                            : LC_OOB;
+                acc[t] = (lc_f4){0.0f, 0.0f, 0.0f, 0.0f};
             }
-            v = (1.0f - fy) * ((1.0f - fx) * s[0] + fx * s[1]) +
-                fy * ((1.0f - fx) * s[2] + fx * s[3]);
+            switch (nq) {
+            case 1:
+                lc_cm_tiles<1>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                break;
+            case 2:
+                lc_cm_tiles<2>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                break;
+            case 3:
+                lc_cm_tiles<3>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                break;
+            case 4:
+                lc_cm_tiles<4>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                break;
+            case 5:
+                lc_cm_tiles<5>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                break;
+            case 6:
+                lc_cm_tiles<6>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                break;
+            case 7:
+                lc_cm_tiles<7>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                break;
+            case 8:
+                lc_cm_tiles<8>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                break;
+            default:
+                lc_cm_tiles<9>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+            }
+            /* Lane l holds rows 4 (l / 16) + v of the tile's 16 x 16 block,
+             * column l % 16. */
+            if (four || wv >= 2)
+#pragma unroll
+                for (int t = 0; t < 9; t++)
+                    if (t < nq)
+#pragma unroll
+                        for (int v = 0; v < 4; v++)
+                            Gw[(4 * kq + v) * gp + (u0 + t) * 16 + m] = acc[t][v];
+            if (!four) {
+                __syncthreads();
+                if (wv < 2)
+#pragma unroll
+                    for (int t = 0; t < 9; t++)
+                        if (t < nq)
+#pragma unroll
+                            for (int v = 0; v < 4; v++)
+                                Gw[(4 * kq + v) * gp + (u0 + t) * 16 + m] += acc[t][v];
+            }
         }
-        out[(long long)(coff + k) * n + i] = v;
+    }
+    else {
+        /* Per-cell path: wave wv takes cells wv, wv + 4, ...; 16 window
+         * cells e = e0 + 4 u + (l / 16) at a time, lane l summing channels
+         * 4 (l % 16) .. + 3 of every 64 of its window cells, the 16 lanes
+         * of a row then added by DPP; S of cell mm over its window goes to
+         * row mm of G. */
+        const int np2 = ps * ps;
+        const unsigned bytes = (unsigned)n * (unsigned)ld * 4u;
+        const __amdgpu_buffer_rsrc_t ra = lc_rsrc(t1, bytes), rb = lc_rsrc(t2, bytes);
+
+        for (int mm = wv; mm < LC_T; mm += 4) {
+            const int i = pt.cid[mm];
+
+            if (i < 0 || !pt.okc[mm])
+                continue;
+            const unsigned ao = (unsigned)i * ld * 4u;
+
+            for (int e0 = 0; e0 < np2; e0 += 16) {
+                unsigned bo[4];
+                float sum[4];
+
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int e = e0 + 4 * u + kq;
+                    const int yy = pt.oy[mm] + e / ps, xx = pt.ox[mm] + e % ps;
+                    const bool ok = e < np2 && xx >= 0 && xx < W && yy >= 0 && yy < H;
+
+                    bo[u] = ok ? (unsigned)(yy * W + xx) * ld * 4u : LC_OOB;
+                    sum[u] = 0.0f;
+                }
+                for (int c = 4 * m; c < C; c += 64) {
+                    const lc_f4 a = lc_load4(ra, ao + 4u * c) * rc;
+
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        const lc_f4 b = lc_load4(rb, bo[u] == LC_OOB ? LC_OOB : bo[u] + 4u * c);
+
+                        sum[u] = fmaf(a[0], b[0], sum[u]);
+                        sum[u] = fmaf(a[1], b[1], sum[u]);
+                        sum[u] = fmaf(a[2], b[2], sum[u]);
+                        sum[u] = fmaf(a[3], b[3], sum[u]);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int e = e0 + 4 * u + kq;
+                    const float v = lc_row_sum(sum[u]);
+
+                    if (m == 0 && e < np2)
+                        G[mm * LC_GS + e] = v;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    {
+        const bool four = ((nb + 15) >> 4) <= 9;
+
+        lc_outputs(pt, G, four ? 4 : 2, LC_T * (four ? LC_PG : LC_GS), four ? LC_PG : LC_GS,
+                   tiled, r, n, out, coff, tid);
     }
 }
 
@@ -696,83 +960,66 @@ extern "C" void roma_warp_sample(struct ops *o, cl_mem in, int C, int H, int W,
     ICOREG_API_END
 }
 
-/* Patches whose windows do not fit one LC_NB-cell box (the per-cell path
- * of local_corr_kernel), counted per block of 256 patches into
- * counts[blockIdx.x]: one thread per 4 x 4 patch, the box formed as the
- * kernel forms it. */
-__global__ void __launch_bounds__(256)
-    local_corr_scan_kernel(const float *__restrict__ flow, int H, int W, int r,
-                           int *__restrict__ counts)
-{
-    const int tiles_x = (W + 3) >> 2, ntiles = tiles_x * ((H + 3) >> 2);
-    const int t = blockIdx.x * 256 + threadIdx.x, n = H * W, ps = 2 * r + 2;
-    const int px0 = (t % tiles_x) * 4, py0 = (t / tiles_x) * 4;
-    int lo_x = INT_MAX, lo_y = INT_MAX, hi_x = INT_MIN, hi_y = INT_MIN;
-
-    for (int c = 0; c < LC_T && t < ntiles; c++) {
-        const int x = px0 + (c & 3), y = py0 + (c >> 2);
-
-        if (x < W && y < H) {
-            const int ci = y * W + x;
-            const bil b = bilinear_setup(flow[ci], flow[n + ci], H, W, r);
-
-            if (b.ok) {
-                lo_x = min(lo_x, b.x0 - r);
-                lo_y = min(lo_y, b.y0 - r);
-                hi_x = max(hi_x, b.x0 - r + ps - 1);
-                hi_y = max(hi_y, b.y0 - r + ps - 1);
-            }
-        }
-    }
-    lo_x = max(lo_x, 0);
-    lo_y = max(lo_y, 0);
-    hi_x = min(hi_x, W - 1);
-    hi_y = min(hi_y, H - 1);
-    {
-        const int bw = hi_x >= lo_x ? hi_x - lo_x + 1 : 0, bh = hi_y >= lo_y ? hi_y - lo_y + 1 : 0;
-        const int nsc = __syncthreads_count(t < ntiles && bw * bh > LC_NB);
-
-        if (threadIdx.x == 0)
-            counts[blockIdx.x] = nsc;
-    }
-}
-
-
-/* (C x n) to (n x C) for both maps, 32 x 32 tiles through LDS, the grid
- * striding over the tiles of both; nothing when no patch scatters (then
- * the launch costs a few microseconds). */
+/* (C x n) to (n x C) for both maps, output rows ld floats apart: one
+ * 64-cell x 64-channel tile per block through LDS, blocks 0 .. T - 1 on
+ * f1, T .. 2 T - 1 on f2. VEC (n % 4 == 0, C % 4 == 0, ld % 4 == 0, both
+ * inputs 16-byte aligned): 16-byte loads along the cells and 16-byte
+ * stores along the channels. */
+template <bool VEC>
 __global__ void __launch_bounds__(256)
     lc_transpose_kernel(const float *__restrict__ f1, const float *__restrict__ f2,
-                        float *__restrict__ o1, float *__restrict__ o2, int C, int n,
-                        const int *__restrict__ counts, int nc)
+                        float *__restrict__ o1, float *__restrict__ o2, int C, int ld, int n)
 {
-    __shared__ float t[32][33];
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-    const int tiles_i = (n + 31) / 32, tiles = tiles_i * ((C + 31) / 32);
+    __shared__ float t[64][65];
+    const int tid = threadIdx.x;
+    const int tiles_i = (n + 63) / 64, tiles = tiles_i * ((C + 63) / 64);
+    const int z = (int)blockIdx.x >= tiles, v = blockIdx.x - z * tiles;
+    const int i0 = (v % tiles_i) * 64, c0 = (v / tiles_i) * 64;
+    const float *in = z ? f2 : f1;
+    float *out = z ? o2 : o1;
 
-    if (!lc_any_scattered(counts, nc))
-        return;
-    for (int u = blockIdx.x; u < 2 * tiles; u += gridDim.x) {
-        const int z = u >= tiles, v = u - z * tiles;
-        const int i0 = (v % tiles_i) * 32, c0 = (v / tiles_i) * 32;
-        const float *in = z ? f2 : f1;
-        float *out = z ? o2 : o1;
+    if (VEC) {
+        const int j4 = (tid & 15) * 4, row = tid >> 4;
+        lc_f4 x[4];
 
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int c = c0 + row + 16 * k, i = i0 + j4;
+
+            x[k] = c < C && i < n ? *(const lc_f4 *)(in + (long long)c * n + i)
+                                  : (lc_f4){0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                t[row + 16 * k][j4 + e] = x[k][e];
         __syncthreads();
 #pragma unroll
-        for (int k = 0; k < 32; k += 8) {
+        for (int k = 0; k < 4; k++) {
+            const int i = i0 + row + 16 * k, c = c0 + j4;
+
+            if (i < n && c < C)
+                *(lc_f4 *)(out + (long long)i * ld + c) =
+                    (lc_f4){t[j4][row + 16 * k], t[j4 + 1][row + 16 * k],
+                            t[j4 + 2][row + 16 * k], t[j4 + 3][row + 16 * k]};
+        }
+    }
+    else {
+        const int tx = tid & 63, ty = tid >> 6;
+
+        for (int k = 0; k < 64; k += 4) {
             const int c = c0 + ty + k, i = i0 + tx;
 
             if (c < C && i < n)
                 t[ty + k][tx] = in[(long long)c * n + i];
         }
         __syncthreads();
-#pragma unroll
-        for (int k = 0; k < 32; k += 8) {
+        for (int k = 0; k < 64; k += 4) {
             const int i = i0 + ty + k, c = c0 + tx;
 
             if (c < C && i < n)
-                out[(long long)i * C + c] = t[tx][ty + k];
+                out[(long long)i * ld + c] = t[tx][ty + k];
         }
     }
 }
@@ -804,29 +1051,45 @@ extern "C" void roma_local_corr(struct ops *o, cl_mem f1, cl_mem f2, int C,
         hipStream_t st = stream_of(o->ocl);
 
         prof_scope ps(o->ocl, op);
-        if (C % 4 == 0) {
-            /* Cell-major copies for the per-cell path, made only when a
-             * patch scatters (counted first on the device). */
-            const size_t cn = (size_t)C * n;
-            const int nc = (tiles + 255) / 256;
-            cl_mem sc = scratch_get(o, 2 * cn * sizeof(float) + (size_t)nc * sizeof(int));
-            float *t1 = (float *)sc->ptr, *t2 = t1 + cn;
-            int *counts = (int *)(t2 + cn);
-            const long long ttiles = 2LL * ((n + 31) / 32) * ((C + 31) / 32);
-            const dim3 tg((unsigned)(ttiles < 2048 ? ttiles : 2048));
+        /* Cell-major row pitch: whole 256-byte units, an odd number of
+         * them, so that the 16 rows one load instruction reads at the same
+         * channel offset fall into different memory channels (a pitch of
+         * 2^k bytes sends them all to one or two); rows under 256 bytes
+         * are left unpadded. */
+        long long ld = C;
 
-            hipLaunchKernelGGL(local_corr_scan_kernel, dim3((unsigned)nc), dim3(256), 0, st,
-                               cfptr(flow), H, W, r, counts);
-            hipLaunchKernelGGL(lc_transpose_kernel, tg, dim3(256), 0, st, cfptr(f1), cfptr(f2),
-                               t1, t2, C, (int)n, (const int *)counts, nc);
-            hipLaunchKernelGGL(local_corr_kernel, grid, dim3(256), 0, st, cfptr(f1),
-                               cfptr(f2), C, H, W, r, cfptr(flow), fptr(out), coff,
-                               (const float *)t1, (const float *)t2, (const int *)counts, nc);
+        if (C >= 64) {
+            ld = (C + 63) / 64 * 64;
+            if ((ld / 64) % 2 == 0)
+                ld += 64;
+        }
+        if (C % 4 == 0 && ld * n * 4 < (1LL << 31)) {
+            /* Both maps cell-major into the scratch buffer (its start is
+             * 256-byte aligned, and ld % 4 == 0 keeps every row 16-byte
+             * aligned), then the cell-major kernel (its buffer windows
+             * take byte offsets below 2^31). */
+            const size_t cn = (size_t)ld * n;
+            cl_mem sc = scratch_get(o, 2 * cn * sizeof(float));
+            float *t1 = (float *)sc->ptr, *t2 = t1 + cn;
+            const long long ttiles = 2LL * ((n + 63) / 64) * ((C + 63) / 64);
+            const bool vec = n % 4 == 0 && ((uintptr_t)cfptr(f1) & 15) == 0 &&
+                             ((uintptr_t)cfptr(f2) & 15) == 0;
+
+            if (ttiles >= (1LL << 31))
+                icoreg_fatal("%s: transpose grid too large", op);
+            if (vec)
+                hipLaunchKernelGGL(lc_transpose_kernel<true>, dim3((unsigned)ttiles), dim3(256),
+                                   0, st, cfptr(f1), cfptr(f2), t1, t2, C, (int)ld, (int)n);
+            else
+                hipLaunchKernelGGL(lc_transpose_kernel<false>, dim3((unsigned)ttiles), dim3(256),
+                                   0, st, cfptr(f1), cfptr(f2), t1, t2, C, (int)ld, (int)n);
+            hipLaunchKernelGGL(local_corr_cm_kernel, grid, dim3(256), 0, st, (const float *)t1,
+                               (const float *)t2, C, (int)ld, H, W, r, cfptr(flow), fptr(out),
+                               coff);
         }
         else
             hipLaunchKernelGGL(local_corr_kernel, grid, dim3(256), 0, st, cfptr(f1),
-                               cfptr(f2), C, H, W, r, cfptr(flow), fptr(out), coff, nullptr,
-                               nullptr, nullptr, 0);
+                               cfptr(f2), C, H, W, r, cfptr(flow), fptr(out), coff);
     }
     launch_check(op);
     ICOREG_API_END
