@@ -64,6 +64,11 @@ inline hipStream_t stream_of(struct ocl_backend *ocl)
     return (hipStream_t)ocl->stream;
 }
 
+/* Channels per thread of the bilinear sampling kernels (warp sampling,
+ * grid_sample): 8, or 4 when that leaves fewer idle slots in the last
+ * group of C channels. */
+inline int sample_cg(int C) { return (C + 3) / 4 * 4 - C < (C + 7) / 8 * 8 - C ? 4 : 8; }
+
 /* Check the launch just queued (launch-configuration errors). */
 void launch_check(const char *what);
 

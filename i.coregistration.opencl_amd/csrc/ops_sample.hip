@@ -98,59 +98,29 @@ extern "C" void ops_resize(struct ops *o, cl_mem in, int C, int h, int w,
 
 /* ---- grid_sample -------------------------------------------------------- */
 
-/* Bilinear value of plane p (H x W) at pixel coordinates (ix, iy), zero
- * outside; non-finite coordinates give 0. Coordinates far outside are
- * clamped first (all four taps stay outside, so the value is still 0),
- * which keeps the integer conversion defined. */
-__device__ __forceinline__ float bilinear_zero(const float *__restrict__ p,
-                                               int H, int W, float ix,
-                                               float iy)
-{
-    int x0, y0;
-    float fx, fy, v00, v01, v10, v11;
-
-    if (!isfinite(ix) || !isfinite(iy))
-        return 0.0f;
-    ix = fminf(fmaxf(ix, -2.0f), (float)W + 1.0f);
-    iy = fminf(fmaxf(iy, -2.0f), (float)H + 1.0f);
-    x0 = (int)floorf(ix);
-    y0 = (int)floorf(iy);
-    fx = ix - x0;
-    fy = iy - y0;
-#define AT(yy, xx)                                                             \
-    ((xx) >= 0 && (xx) < W && (yy) >= 0 && (yy) < H ? p[(yy) * W + (xx)] : 0.0f)
-    v00 = AT(y0, x0);
-    v01 = AT(y0, x0 + 1);
-    v10 = AT(y0 + 1, x0);
-    v11 = AT(y0 + 1, x0 + 1);
-#undef AT
-    return (1.0f - fy) * ((1.0f - fx) * v00 + fx * v01) +
-           fy * ((1.0f - fx) * v10 + fx * v11);
-}
-
-/* One thread per (point, group of GS_CG channels): the point's taps
- * and weights are computed once for its group, the group's planes read
- * at the same offsets with all loads in flight together, and each
- * channel's stores are 256 consecutive points. The grid's y dimension
- * runs over the groups, so that a few thousand points still fill the
- * GPU. */
-#define GS_CG 8
-
+/* One thread per (point, group of CG channels): the point's taps and
+ * weights are computed once for its group, the group's planes read at
+ * the same offsets with all loads in flight together, and each channel's
+ * stores are 256 consecutive points, non-temporal (written once, read by
+ * the next kernel). A block takes 256 points of one channel group, so
+ * that a few thousand points still fill the GPU; CG is 8, or 4 when that
+ * leaves fewer idle channel slots. */
+template <int CG>
 __global__ void __launch_bounds__(256)
     grid_sample_kernel(const float *__restrict__ in, int C, int H, int W,
                        const float2 *__restrict__ grid, int n, int align,
                        float *__restrict__ out)
 {
-    /* Block L -> (point block, channel group), groups fastest, in
+    /* Block L -> (channel group, point block), point blocks fastest, in
      * contiguous bands per XCD (L % 8): neighbouring point blocks of a
      * smooth grid share input rows, fetched once into that XCD's L2. */
-    const int ng = (C + GS_CG - 1) / GS_CG, total = gridDim.x;
+    const int npb = (n + 255) / 256, total = gridDim.x;
     const int q = total >> 3, rem = total & 7, xc = blockIdx.x & 7, idx = blockIdx.x >> 3;
     const int ord = (xc < rem ? xc * (q + 1) : rem * (q + 1) + (xc - rem) * q) + idx;
-    const int i = (ord / ng) * 256 + threadIdx.x, c0 = (ord % ng) * GS_CG;
+    const int i = (ord % npb) * 256 + threadIdx.x, c0 = (ord / npb) * CG;
     const long long plane = (long long)H * W;
     float2 g;
-    float ix, iy, fx = 0.0f, fy = 0.0f, v[GS_CG][4];
+    float ix, iy, fx = 0.0f, fy = 0.0f, v[CG][4];
     int x0 = 0, y0 = 0, o[4] = {0, 0, 0, 0};
     bool ok, in4[4];
 
@@ -165,7 +135,9 @@ __global__ void __launch_bounds__(256)
         ix = ((g.x + 1.0f) * W - 1.0f) * 0.5f;
         iy = ((g.y + 1.0f) * H - 1.0f) * 0.5f;
     }
-    /* bilinear_zero's arithmetic, taps shared by the group. */
+    /* Coordinates far outside are clamped first (all four taps stay
+     * outside, so the value is still 0), which keeps the integer
+     * conversion defined; non-finite ones give 0. */
     ok = isfinite(ix) && isfinite(iy);
     if (ok) {
         ix = fminf(fmaxf(ix, -2.0f), (float)W + 1.0f);
@@ -183,7 +155,7 @@ __global__ void __launch_bounds__(256)
         o[q] = in4[q] ? yy * W + xx : 0;
     }
 #pragma unroll
-    for (int k = 0; k < GS_CG; k++) {
+    for (int k = 0; k < CG; k++) {
         const float *p = in + (long long)min(c0 + k, C - 1) * plane;
 
 #pragma unroll
@@ -191,12 +163,13 @@ __global__ void __launch_bounds__(256)
             v[k][q] = in4[q] ? p[o[q]] : 0.0f;
     }
 #pragma unroll
-    for (int k = 0; k < GS_CG; k++)
+    for (int k = 0; k < CG; k++)
         if (c0 + k < C)
-            out[(long long)(c0 + k) * n + i] =
+            __builtin_nontemporal_store(
                 ok ? (1.0f - fy) * ((1.0f - fx) * v[k][0] + fx * v[k][1]) +
                          fy * ((1.0f - fx) * v[k][2] + fx * v[k][3])
-                   : 0.0f;
+                   : 0.0f,
+                &out[(long long)(c0 + k) * n + i]);
 }
 
 extern "C" void ops_grid_sample(struct ops *o, cl_mem in, int C, int H, int W,
@@ -216,13 +189,21 @@ extern "C" void ops_grid_sample(struct ops *o, cl_mem in, int C, int H, int W,
     need_floats(grid, 0, 2LL * n, op, "grid");
     need_floats(out, 0, (long long)C * n, op, "out");
     prof_scope ps(o->ocl, "grid_sample");
-    if ((long long)((n + 255) / 256) * ((C + GS_CG - 1) / GS_CG) >= (1LL << 31))
-        icoreg_fatal("%s: grid too large", op);
-    hipLaunchKernelGGL(grid_sample_kernel,
-                       dim3((unsigned)((long long)((n + 255) / 256) * ((C + GS_CG - 1) / GS_CG))),
-                       dim3(256), 0, stream_of(o->ocl), cfptr(in), C, H, W,
-                       (const float2 *)cfptr(grid), n, align_corners,
-                       fptr(out));
+    {
+        const int cg = sample_cg(C);
+        const long long blocks = (long long)((n + 255) / 256) * ((C + cg - 1) / cg);
+
+        if (blocks >= (1LL << 31))
+            icoreg_fatal("%s: grid too large", op);
+        if (cg == 4)
+            hipLaunchKernelGGL(grid_sample_kernel<4>, dim3((unsigned)blocks), dim3(256), 0,
+                               stream_of(o->ocl), cfptr(in), C, H, W,
+                               (const float2 *)cfptr(grid), n, align_corners, fptr(out));
+        else
+            hipLaunchKernelGGL(grid_sample_kernel<8>, dim3((unsigned)blocks), dim3(256), 0,
+                               stream_of(o->ocl), cfptr(in), C, H, W,
+                               (const float2 *)cfptr(grid), n, align_corners, fptr(out));
+    }
     launch_check("grid_sample");
     ICOREG_API_END
 }

@@ -9,9 +9,9 @@
  * Design points:
  *  - row norms and cls_to_flow: one wave64 per row, cross-lane
  *    reductions (the reference: work-groups of 256 with LDS trees);
- *  - warp sampling: one thread per (cell, group of 8 channels), the
+ *  - warp sampling: one thread per (cell, group of 4 or 8 channels), the
  *    bilinear taps and weights computed once per group (the reference
- *    recomputes them per (cell, channel)), grid y over the groups;
+ *    recomputes them per (cell, channel)), blocks over the groups;
  *  - local correlation: 4 x 4 cell patches; the products of the patch's
  *    cells with the union box of their windows on the matrix cores when
  *    the box is small (a per-cell path otherwise), then the bilinear
@@ -149,32 +149,33 @@ __device__ __forceinline__ bil bilinear_setup(float x, float y, int H, int W,
     return b;
 }
 
-/* One thread per (cell, group of channels): the cell's taps and weights
- * are computed once for its group, the group's channel planes read at
- * the same offsets (all loads of the group in flight together), and the
- * stores of a channel are 256 consecutive cells. The grid's y dimension
- * runs over the channel groups, so that a few thousand cells still fill
+/* One thread per (cell, group of CG channels): the cell's taps and
+ * weights are computed once for its group, the group's channel planes
+ * read at the same offsets (all loads of the group in flight together),
+ * and the stores of a channel are 256 consecutive cells, non-temporal
+ * (the map is written once and read by the next kernel). A block takes
+ * 256 cells of one channel group, so that a few thousand cells still fill
  * the GPU (11 664 cells x 512 channels at 1/8 of 864 x 864: 2944 blocks
- * instead of 46). */
-#define WS_CG 8 /* channels per thread */
-
+ * instead of 46). CG is 8, or 4 when that leaves fewer idle channel slots
+ * (9 channels: 3 of 12 instead of 7 of 16). */
+template <int CG>
 __global__ void __launch_bounds__(256)
     warp_sample_kernel(const float *__restrict__ in, int C, int H, int W,
                        const float *__restrict__ flow, float *__restrict__ out,
                        int coff)
 {
-    /* Block L -> (cell block, channel group), channel groups fastest; the
+    /* Block L -> (channel group, cell block), cell blocks fastest; the
      * XCDs (L % 8) get contiguous bands of that order, so that the input
      * rows two neighbouring cell blocks share are fetched into one L2. */
-    const int ng = (C + WS_CG - 1) / WS_CG, total = gridDim.x;
+    const int n = H * W, ncb = (n + 255) / 256, total = gridDim.x;
     const int q = total >> 3, rem = total & 7, x = blockIdx.x & 7, idx = blockIdx.x >> 3;
     const int ord = (x < rem ? x * (q + 1) : rem * (q + 1) + (x - rem) * q) + idx;
-    const int n = H * W, i = (ord / ng) * 256 + threadIdx.x;
-    const int c0 = (ord % ng) * WS_CG;
+    const int i = (ord % ncb) * 256 + threadIdx.x;
+    const int c0 = (ord / ncb) * CG;
     bil b;
     bool in00, in01, in10, in11;
     int o00, o01, o10, o11;
-    float v[WS_CG][4];
+    float v[CG][4];
 
     if (i >= n)
         return;
@@ -189,7 +190,7 @@ __global__ void __launch_bounds__(256)
     o10 = in10 ? (b.y0 + 1) * W + b.x0 : 0;
     o11 = in11 ? (b.y0 + 1) * W + b.x0 + 1 : 0;
 #pragma unroll
-    for (int k = 0; k < WS_CG; k++) {
+    for (int k = 0; k < CG; k++) {
         const float *p = in + (long long)min(c0 + k, C - 1) * n;
 
         v[k][0] = in00 ? p[o00] : 0.0f;
@@ -198,12 +199,13 @@ __global__ void __launch_bounds__(256)
         v[k][3] = in11 ? p[o11] : 0.0f;
     }
 #pragma unroll
-    for (int k = 0; k < WS_CG; k++)
+    for (int k = 0; k < CG; k++)
         if (c0 + k < C)
-            out[(long long)(coff + c0 + k) * n + i] =
+            __builtin_nontemporal_store(
                 b.ok ? (1.0f - b.fy) * ((1.0f - b.fx) * v[k][0] + b.fx * v[k][1]) +
                            b.fy * ((1.0f - b.fx) * v[k][2] + b.fx * v[k][3])
-                     : 0.0f;
+                     : 0.0f,
+                &out[(long long)(coff + c0 + k) * n + i]);
 }
 
 /* ---- local correlation ------------------------------------------------------------- */
@@ -951,11 +953,20 @@ extern "C" void roma_warp_sample(struct ops *o, cl_mem in, int C, int H, int W,
     need_floats(flow, 0, 2 * n, op, "flow");
     need_floats(out, (long long)coff * n, (long long)C * n, op, "out");
     prof_scope ps(o->ocl, op);
-    if ((long long)nblk(n, 256) * nblk(C, WS_CG) >= (1LL << 31))
-        icoreg_fatal("%s: grid too large", op);
-    hipLaunchKernelGGL(warp_sample_kernel, dim3(nblk(n, 256) * nblk(C, WS_CG)), dim3(256),
-                       0, stream_of(o->ocl), cfptr(in), C, H, W, cfptr(flow),
-                       fptr(out), coff);
+    {
+        const int cg = sample_cg(C);
+
+        if ((long long)nblk(n, 256) * nblk(C, cg) >= (1LL << 31))
+            icoreg_fatal("%s: grid too large", op);
+        if (cg == 4)
+            hipLaunchKernelGGL(warp_sample_kernel<4>, dim3(nblk(n, 256) * nblk(C, 4)), dim3(256),
+                               0, stream_of(o->ocl), cfptr(in), C, H, W, cfptr(flow), fptr(out),
+                               coff);
+        else
+            hipLaunchKernelGGL(warp_sample_kernel<8>, dim3(nblk(n, 256) * nblk(C, 8)), dim3(256),
+                               0, stream_of(o->ocl), cfptr(in), C, H, W, cfptr(flow), fptr(out),
+                               coff);
+    }
     launch_check(op);
     ICOREG_API_END
 }

@@ -221,26 +221,47 @@ def test_layernorm_shapes(shape, dev, ic, orc):
     assert err <= 1e-5, f"{shape}: {err:.2e}"
 
 
+# (C, H, W, points, align_corners, smooth): random points scatter; smooth
+# ones are an image-shaped grid in raster order (neighbouring points share
+# taps), with W % 4 == 0 and not.
 GS_SHAPES = [
-    (13, 20, 25, 777, 0),   # channel groups of 8 with a tail
-    (64, 48, 40, 3000, 1),
-    (512, 108, 108, 11664, 0),  # a refiner-sized map
+    (13, 20, 25, 777, 0, False),   # channel groups with a tail
+    (64, 48, 40, 3000, 1, False),
+    (512, 108, 108, 11664, 0, False),  # a refiner-sized map
+    (512, 108, 108, 11664, 0, True),
+    (21, 37, 45, 37 * 45, 1, True),
+    (9, 64, 96, 60 * 90, 0, True),
 ]
+
+
+def smooth_grid(n, H, W):
+    """n points of an image-shaped grid (rows of W) in raster order,
+    slightly bent, as normalised (x, y)."""
+    h = (n + W - 1) // W
+    gx = (2 * (np.arange(W) + 0.5) / W - 1)[None, :] + 0 * np.arange(h)[:, None]
+    gy = (2 * (np.arange(h) + 0.5) / h - 1)[:, None] + 0 * np.arange(W)[None, :]
+    g = np.stack([gx + 0.03 * np.sin(3 * gy), gy + 0.03 * np.cos(2 * gx)], -1)
+    return np.ascontiguousarray(g.reshape(-1, 2)[:n], np.float32)
 
 
 @pytest.mark.parametrize("shape", GS_SHAPES, ids=[str(s) for s in GS_SHAPES])
 def test_grid_sample_shapes(shape, dev, ic, orc):
-    """grid_sample over many channels (the (point, channel-group) grid)
-    against the oracle, with points outside, on the border and
-    non-finite, both align_corners conventions."""
+    """grid_sample over many channels against the oracle, with points
+    outside, on the border and non-finite, both align_corners
+    conventions, on scattered and smooth grids."""
     from oracle_lib import fp
-    Cc, H, W, n, align = shape
+    Cc, H, W, n, align, smooth = shape
     print(f"[grid_sample] {shape}", flush=True)
     rng = np.random.default_rng(700 + Cc)
     x = rng.standard_normal((Cc, H, W)).astype(np.float32)
-    g = rng.uniform(-1.2, 1.2, (n, 2)).astype(np.float32)
-    g[:4] = [[-1, -1], [1, 1], [np.nan, 0], [0, np.inf]]
-    g[4:8] = [[1e6, 0], [-3e9, 2], [1, -1], [-1, 1]]
+    if smooth:
+        g = smooth_grid(n, H, W)
+        g[5] = [np.nan, 0]
+        g[W + 3] = [1e6, 0]
+    else:
+        g = rng.uniform(-1.2, 1.2, (n, 2)).astype(np.float32)
+        g[:4] = [[-1, -1], [1, 1], [np.nan, 0], [0, np.inf]]
+        g[4:8] = [[1e6, 0], [-3e9, 2], [1, -1], [-1, 1]]
     ref = np.zeros(Cc * n, np.float32)
     orc.orc_grid_sample(fp(x), Cc, H, W, fp(g), n, align, fp(ref))
     X, Gd, Y = dev.upload(x), dev.upload(g), dev.zeros(Cc * n)
