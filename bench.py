@@ -301,15 +301,29 @@ def hbm_kernel_bytes(kind, C, n, r=0):
 
 def time_launches(dev, fn, reps=20):
     """Mean ms of fn() over reps launches after one warm-up, HIP events on
-    the library's stream."""
+    the library's stream around one replay of a HIP graph that holds the
+    reps calls: the launches run back to back on the device, without the
+    host's per-call time (a few microseconds of Python and ctypes, as long
+    as the smaller kernels themselves) between them."""
     fn()
     dev.finish()
-    dev.reset_events()
-    e0 = dev.event()
-    for _ in range(reps):
-        fn()
-    e1 = dev.event()
-    dev.finish()
+    api = dev.api
+    api.ocl_graph_begin(dev.pb)
+    try:
+        for _ in range(reps):
+            fn()
+    finally:
+        graph = api.ocl_graph_end(dev.pb)
+    try:
+        api.ocl_graph_launch(dev.pb, graph)
+        dev.finish()
+        dev.reset_events()
+        e0 = dev.event()
+        api.ocl_graph_launch(dev.pb, graph)
+        e1 = dev.event()
+        dev.finish()
+    finally:
+        api.ocl_graph_free(graph)
     return dev.elapsed_ms(e0, e1) / reps
 
 
@@ -318,7 +332,9 @@ def bench_hbm_kernels(ic, dev, H=864, W=864):
     stack's (864 x 864: s8, s4, s2, s1) warp sample, local correlation
     and depthwise 5 x 5, grid_sample at s8, on seeded features and a
     smooth warp; DISK's NMS at 512 x 512. Each timed over 20 launches;
-    achieved GB/s = compulsory bytes / mean launch time."""
+    achieved GB/s = compulsory bytes / mean launch time, reported with
+    the rate of a device-to-device copy moving the same bytes (copy_GBps,
+    the practical ceiling at that size) and the fraction of it."""
     out = []
     rng = np.random.default_rng(7)
     for s, feat, emb, r in REFINE_V1:
@@ -386,6 +402,20 @@ def bench_hbm_kernels(ic, dev, H=864, W=864):
                 "frac_hbm": round(b / ms / 1e6 / PEAK_HBM, 4)})
     for t in (src, grid, dst, heat, mask):
         t.release()
+    # The practical ceiling at each size: a device-to-device copy that
+    # reads half the kernel's compulsory bytes and writes the other half,
+    # timed the same way.
+    rates = {}
+    for e in out:
+        half = (e["bytes"] // 2 + 255) // 256 * 256
+        if half not in rates:
+            a, b = dev.alloc(half, "copy ceiling"), dev.alloc(half, "copy ceiling")
+            ms = time_launches(dev, lambda: api.ocl_copy(dev.pb, a.mem, 0, b.mem, 0, half))
+            rates[half] = 2 * half / ms / 1e6
+            a.release()
+            b.release()
+        e["copy_GBps"] = round(rates[half], 1)
+        e["frac_copy"] = round(e["GBps"] / rates[half], 4)
     return out
 
 

@@ -413,8 +413,9 @@ static inline bool aligned16(cl_mem m)
 }
 
 /* The same for C % 4 == 0 and 16-byte aligned rows: lane l holds the
- * float4 groups l + 64 t (t < NV), all of them loaded before the first
- * reduction; DPP wave sums. */
+ * float4 groups l + 64 t (t < NV), all of them (and the matching gamma
+ * and beta groups) loaded before the first reduction, so a row costs one
+ * memory round trip; DPP wave sums. */
 template <int NV>
 __global__ void __launch_bounds__(256)
     layernorm4_kernel(const float4 *X, float4 *Y, const float4 *__restrict__ g,
@@ -424,7 +425,7 @@ __global__ void __launch_bounds__(256)
     const int lane = threadIdx.x & 63, C4 = C >> 2;
     const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
     const float4 *x;
-    float4 *y, v[NV];
+    float4 *y, v[NV], gv[NV], bv[NV];
     float s = 0.0f, mean, r;
 
     if (row >= rows)
@@ -434,8 +435,12 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
     for (int t = 0; t < NV; t++) {
         const int c = lane + 64 * t;
+        const float4 one = make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 
-        v[t] = c < C4 ? x[c] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[t] = c < C4 ? x[c] : zero;
+        gv[t] = g && c < C4 ? g[c] : one;
+        bv[t] = bt && c < C4 ? bt[c] : zero;
     }
 #pragma unroll
     for (int t = 0; t < NV; t++)
@@ -463,20 +468,16 @@ __global__ void __launch_bounds__(256)
         if (c >= C4)
             continue;
         if (g) {
-            const float4 gv = g[c];
-
-            u[0] *= gv.x;
-            u[1] *= gv.y;
-            u[2] *= gv.z;
-            u[3] *= gv.w;
+            u[0] *= gv[t].x;
+            u[1] *= gv[t].y;
+            u[2] *= gv[t].z;
+            u[3] *= gv[t].w;
         }
         if (bt) {
-            const float4 bv = bt[c];
-
-            u[0] += bv.x;
-            u[1] += bv.y;
-            u[2] += bv.z;
-            u[3] += bv.w;
+            u[0] += bv[t].x;
+            u[1] += bv[t].y;
+            u[2] += bv[t].z;
+            u[3] += bv[t].w;
         }
         y[c] = make_float4(icoreg_act(u[0], act, slope),
                            icoreg_act(u[1], act, slope),

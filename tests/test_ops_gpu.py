@@ -270,3 +270,22 @@ def test_grid_sample_shapes(shape, dev, ic, orc):
     assert np.isfinite(got).all()
     err = opcases.rel_err(got, ref)
     assert err <= 1e-5, f"{shape}: {err:.2e}"
+
+
+@pytest.mark.parametrize("soff,doff,nbytes", [(0, 0, 1 << 20), (16, 48, 4096 + 16 * 7),
+                                              (4, 0, 4096), (0, 8, 1000), (3, 5, 77),
+                                              (0, 0, 16), (256, 1024, 25165824)])
+def test_ocl_copy(soff, doff, nbytes, dev, ic):
+    """ocl_copy byte for byte: 16-byte aligned ends and sizes (the copy
+    kernel), misaligned ones (the runtime's copy); bytes around the
+    destination range stay as they were."""
+    print(f"[ocl_copy] soff={soff} doff={doff} n={nbytes}", flush=True)
+    rng = np.random.default_rng(nbytes)
+    src = rng.integers(0, 256, soff + nbytes, dtype=np.uint8)
+    dst0 = rng.integers(0, 256, doff + nbytes + 64, dtype=np.uint8)
+    S, D = dev.upload(src), dev.upload(dst0)
+    dev.api.ocl_copy(dev.pb, S.mem, soff, D.mem, doff, nbytes)
+    got = dev.read(D, dst0.nbytes, np.uint8)
+    want = dst0.copy()
+    want[doff:doff + nbytes] = src[soff:soff + nbytes]
+    assert np.array_equal(got, want)
