@@ -46,6 +46,9 @@ class OclBackend(C.Structure):
         ("profile", C.c_int),
         ("cu_count", C.c_int),
         ("arch", C.c_char * 64),
+        ("aux_stream", C.c_void_p),
+        ("aux_events", C.c_void_p),
+        ("aux_nevents", C.c_int),
     ]
 
 
@@ -203,6 +206,8 @@ SIGNATURES = {
     "roma_refine_device": (None, [_P, Mem, Mem, Mem]),
     "roma_free": (None, [_P]),
     # binding glue (include/icoreg_glue.h)
+    "icoreg_sizeof_backend": (C.c_size_t, []),
+    "icoreg_sizeof_ops": (C.c_size_t, []),
     "icoreg_pth_new": (_P, []),
     "icoreg_eloftr_new": (_P, []),
     "icoreg_struct_delete": (None, [_P]),
@@ -229,6 +234,7 @@ _NO_CHECK = {"ocl_graph_free", "icoreg_set_fatal_mode", "icoreg_last_error", "ic
              "ocl_wrap", "icoreg_prof_entry", "icoreg_prof_reset", "icoreg_prof_flush", "ops_report",
              "pth_find", "pth_numel", "pth_bytes", "pth_strip_prefix",
              "icoreg_pth_new", "icoreg_eloftr_new", "icoreg_struct_delete",
+             "icoreg_sizeof_backend", "icoreg_sizeof_ops",
              "icoreg_eloftr_result", "icoreg_eloftr_coarse_stats",
              "icoreg_eloftr_set_pos_scale", "icoreg_eloftr_buffer", "roma_gp_work_bytes",
              "icoreg_roma_new", "icoreg_roma_result", "icoreg_roma_buffer",

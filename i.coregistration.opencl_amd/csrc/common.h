@@ -69,6 +69,11 @@ inline hipStream_t stream_of(struct ocl_backend *ocl)
  * group of C channels. */
 inline int sample_cg(int C) { return (C + 3) / 4 * 4 - C < (C + 7) / 8 * 8 - C ? 4 : 8; }
 
+/* The backend's second stream (made on first use) and event i of its
+ * pool (disable-timing events, made on first use, i < 4096). */
+hipStream_t aux_stream_of(struct ocl_backend *ocl);
+hipEvent_t aux_event(struct ocl_backend *ocl, int i);
+
 /* Check the launch just queued (launch-configuration errors). */
 void launch_check(const char *what);
 

@@ -7,6 +7,10 @@
 
 #include "icoreg_glue.h"
 
+extern "C" size_t icoreg_sizeof_backend(void) { return sizeof(struct ocl_backend); }
+
+extern "C" size_t icoreg_sizeof_ops(void) { return sizeof(struct ops); }
+
 extern "C" struct pth_file *icoreg_pth_new(void)
 {
     return (struct pth_file *)calloc(1, sizeof(struct pth_file));

@@ -9,23 +9,32 @@
  * arithmetic stays on the GPU.
  *
  * Blocked right-looking Cholesky with 64-column panels, the forward solve
- * carried along as extra columns:
+ * carried along as extra columns of the right-hand side [F | I]: the
+ * identity block makes the forward solve produce Minv = L^-1 beside
+ * Y = L^-1 F, so that the backward solve X = Minv^T Y is a sum over the
+ * panels of their block rows' products, added as each becomes final,
+ * instead of a chain of one launch per panel after the factorisation.
  *  - chol_diag: the 64 x 64 diagonal block factored and its factor
- *    inverted in LDS by one work-group, one barrier per column;
- *  - one launch per panel for both L21 = A21 Linv^T and Y_b = Linv_b Z_b,
- *    one for both the trailing update A22 -= L21 L21^T (lower tiles) and
- *    Z_rest -= L21 Y_b (fp64 GEMM tiles, two problems per launch);
- *  - the backward solve L^T X = Y from the last block: each launch
- *    updates the rows above block b (Y[0:k] -= L[k:k+64, 0:k]^T X_b) and,
- *    in the epilogue of the tiles of block b - 1, finishes that block
- *    (X_{b-1} = Linv_{b-1}^T Y_{b-1}).
+ *    inverted in LDS by one work-group, one barrier per two columns,
+ *    after applying the previous panel's update to the block itself
+ *    (look-ahead); these run back to back on the main stream while
+ *    everything else runs on a second stream, joined back at the end;
+ *  - on the second stream, one launch per panel for both L21 = A21
+ *    Linv^T and Y_b = Linv_b Z_b (Z_b over the right-hand-side columns
+ *    that are not yet zero: F and the identity blocks of this panel and
+ *    the ones before), one for the trailing update A22 -= L21 L21^T
+ *    (lower tiles but the next diagonal block), Z_rest -= L21 Y_b and
+ *    X[0 : k + nb] += Minv_b^T Y_F,b (fp64 GEMM tiles, up to three
+ *    problems per launch).
  * Working matrices: A (n x n, the trailing updates), L (n x n, the
- * factor), Linv per panel, Z and Y (n x d). No launch reads what it
- * writes. About 4 launches per panel (n = 1600: 102). */
+ * factor), Linv per panel, Z and Y (n x (d + n)), X (n x d). No launch
+ * reads what another running beside it writes. */
 
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+
+#include <initializer_list>
 
 #include "common.h"
 #include "icoreg_kernels.h"
@@ -38,10 +47,7 @@ using namespace icoreg;
 
 /* C = alpha A B + beta C with A(i, q) = A[i a_ri + q a_rk], B(q, j) =
  * B[q b_rk + j b_rj], C(i, j) = C[i c_ri + j]; lower: skip output tiles
- * strictly above the diagonal. With linv set (the backward solve's
- * epilogue), the output tiles of tile row epi_row are also multiplied by
- * linv^T (GP_NB x GP_NB, row-major) and the product stored at X (row
- * stride x_ri, same rows and columns as C). */
+ * strictly above the diagonal; skip00: leave output tile (0, 0) alone. */
 struct dg_args {
     int M, N, K;
     const double *A;
@@ -52,34 +58,28 @@ struct dg_args {
     long long c_ri;
     double alpha;
     int beta, lower;
-    const double *linv;
-    int epi_row;
-    double *X;
-    long long x_ri;
+    int skip00;
 };
 
-/* Up to two independent problems per launch: blockIdx.z picks one. */
-struct dg_pair {
-    dg_args p[2];
+/* Up to three independent problems per launch: blockIdx.z picks one. */
+#define DG_MAXP 3
+struct dg_set {
+    dg_args p[DG_MAXP];
 };
 
-__global__ void __launch_bounds__(256) dgemm_kernel(dg_pair pr)
+__global__ void __launch_bounds__(256) dgemm_kernel(dg_set pr)
 {
-    /* The two operand chunks; the backward-solve epilogue reuses both as
-     * one 64 x 65 tile. */
-    __shared__ double sm[2][DG_K][DG_T + 1];
-    __shared__ double lvs[GP_NB * GP_NB]; /* the epilogue's linv */
-    double(*As)[DG_T + 1] = sm[0], (*Bs)[DG_T + 1] = sm[1];
+    __shared__ double As[DG_K][DG_T + 1], Bs[DG_K][DG_T + 1];
     const dg_args &a = pr.p[blockIdx.z];
     const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
     const int i0 = blockIdx.y * DG_T, j0 = blockIdx.x * DG_T;
-    const bool epi = a.linv && (int)blockIdx.y == a.epi_row;
     double acc[4][4], cprev[4][4];
 
-    if (i0 >= a.M || j0 >= a.N || (a.lower && j0 > i0 + DG_T - 1))
+    if (i0 >= a.M || j0 >= a.N || (a.lower && j0 > i0 + DG_T - 1) ||
+        (a.skip00 && i0 == 0 && j0 == 0))
         return;
-    /* The accumulated C and the epilogue's linv are read at the start, so
-     * that their latency overlaps the products. */
+    /* The accumulated C is read at the start, so that its latency
+     * overlaps the products. */
 #pragma unroll
     for (int p = 0; p < 4; p++)
 #pragma unroll
@@ -88,9 +88,6 @@ __global__ void __launch_bounds__(256) dgemm_kernel(dg_pair pr)
 
             cprev[p][r] = a.beta ? a.C[(long long)i * a.c_ri + j] : 0.0;
         }
-    if (epi)
-        for (int e = tid; e < GP_NB * GP_NB; e += 256)
-            lvs[e] = a.linv[e];
 #pragma unroll
     for (int p = 0; p < 4; p++)
 #pragma unroll
@@ -165,59 +162,9 @@ __global__ void __launch_bounds__(256) dgemm_kernel(dg_pair pr)
         for (int r = 0; r < 4; r++) {
             const int j = j0 + tx + 16 * r;
 
-            if (j < a.N) {
-                const double v = a.alpha * acc[p][r] + cprev[p][r];
-
-                a.C[(long long)i * a.c_ri + j] = v;
-                acc[p][r] = v;
-            }
+            if (j < a.N)
+                a.C[(long long)i * a.c_ri + j] = a.alpha * acc[p][r] + cprev[p][r];
         }
-    }
-    /* Backward-solve epilogue: X = linv^T T for this tile T (a full
-     * 64-row block: the rows of the block being finished). */
-    if (epi) {
-        double(*T)[DG_T + 1] = sm[0]; /* rows 0..63 run on through sm[1] */
-
-#pragma unroll
-        for (int p = 0; p < 4; p++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                T[ty + 16 * p][tx + 16 * r] = acc[p][r];
-        __syncthreads();
-#pragma unroll
-        for (int p = 0; p < 4; p++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                acc[p][r] = 0.0;
-        /* X[i][j] = sum_{q >= i} linv[q][i] T[q][j]. */
-#pragma unroll 8
-        for (int q = 0; q < GP_NB; q++) {
-            double lv[4], tv[4];
-
-#pragma unroll
-            for (int p = 0; p < 4; p++) {
-                const int i = ty + 16 * p;
-
-                lv[p] = q >= i ? lvs[q * GP_NB + i] : 0.0;
-            }
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                tv[r] = T[q][tx + 16 * r];
-#pragma unroll
-            for (int p = 0; p < 4; p++)
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    acc[p][r] = fma(lv[p], tv[r], acc[p][r]);
-        }
-#pragma unroll
-        for (int p = 0; p < 4; p++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int j = j0 + tx + 16 * r;
-
-                if (j < a.N)
-                    a.X[(long long)(i0 + ty + 16 * p) * a.x_ri + j] = acc[p][r];
-            }
     }
 }
 
@@ -256,10 +203,18 @@ __device__ __forceinline__ double rsqrt_nr(double x)
  * written back unchanged by its only owner): the trailing lower triangle
  * (A[r][c] -= L[r][j] L[c][j], c > j) and the inverse's rows below j
  * (Linv[c][r] -= L[c][j] Linv[j][r], r <= j < c). */
+typedef double gp_d4 __attribute__((ext_vector_type(4)));
+
+/* Dynamic LDS the diagonal block's launch reserves and does not use: with
+ * it the block holds 133 KB, so no GEMM block of the second stream (33 KB)
+ * is placed on its CU beside it to compete for the LDS bandwidth its
+ * column steps are bound by. */
+#define GP_EXCL_BYTES (66 * 1024)
+
 __global__ void __launch_bounds__(1024)
     chol_diag_kernel(const double *__restrict__ A, double *__restrict__ L,
                      double *__restrict__ Linv, int n, int k, int nb,
-                     int *__restrict__ info)
+                     const double *__restrict__ lprev, int *__restrict__ info)
 {
     __shared__ double s[GP_NB][GP_NB + 1], f[GP_NB][GP_NB + 1];
     __shared__ double dinv[GP_NB];
@@ -285,6 +240,63 @@ __global__ void __launch_bounds__(1024)
         }
     }
     __syncthreads();
+    /* Look-ahead (lprev: the previous panel's Linv; its trailing update of
+     * this block is left to this kernel): P = A[k.., k - 64..] lprev^T, the
+     * block's row of that panel's L21, then s -= P P^T on the lower
+     * triangle, in 16 x 16 tiles on v_mfma_f64_16x16x4f64: lane l gives
+     * A(l % 16, l / 16) and B(l / 16, l % 16) and holds D(l / 16 + 4 v,
+     * l % 16) (measured; the fp32 16 x 16 x 4 form holds rows
+     * 4 (l / 16) + v instead). P goes through f, which the factorisation
+     * overwrites later. */
+    if (lprev) {
+        /* Phase 1, P: wave w (on SIMD w % 4, slot w / 4) takes tile
+         * (w / 4, (w % 4 + w / 4) % 4), so each SIMD gets one tile of each
+         * tile column; tile column tc needs k < 16 (tc + 1) only (lprev is
+         * lower triangular). Phase 2, P P^T: the 10 lower tiles on waves
+         * 0..9, at most 3 a SIMD. */
+        const int w = tid >> 6, l = tid & 63, kq = l >> 4;
+        const int tr = w >> 2, tc = ((w & 3) + (w >> 2)) & 3;
+        const int ri = 16 * tr + (l & 15), ci = 16 * tc + (l & 15);
+        const double *trow = A + (long long)(k + min(ri, nb - 1)) * n + k - GP_NB;
+        double ta[16], lb[16];
+        gp_d4 acc = {0.0, 0.0, 0.0, 0.0};
+
+#pragma unroll
+        for (int kk = 0; kk < 16; kk++)
+            if (kk < 4 * (tc + 1)) {
+                ta[kk] = trow[4 * kk + kq];
+                lb[kk] = lprev[ci * GP_NB + 4 * kk + kq];
+            }
+#pragma unroll
+        for (int kk = 0; kk < 16; kk++)
+            if (kk < 4 * (tc + 1))
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(ri < nb ? ta[kk] : 0.0, lb[kk], acc, 0,
+                                                          0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            f[16 * tr + kq + 4 * v][16 * tc + (l & 15)] = acc[v];
+        __syncthreads();
+        if (w < 10) {
+            /* Lower tile w: row tr2 = the largest t with t (t + 1) / 2 <= w. */
+            const int tr2 = w >= 6 ? 3 : w >= 3 ? 2 : w >= 1 ? 1 : 0;
+            const int tc2 = w - tr2 * (tr2 + 1) / 2;
+            const int r2 = 16 * tr2 + (l & 15), c2 = 16 * tc2 + (l & 15);
+
+            acc = (gp_d4){0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+            for (int kk = 0; kk < 16; kk++)
+                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(f[r2][4 * kk + kq], f[c2][4 * kk + kq],
+                                                          acc, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int r = 16 * tr2 + kq + 4 * v, c = 16 * tc2 + (l & 15);
+
+                if (r < nb && c <= r)
+                    s[r][c] -= acc[v];
+            }
+        }
+        __syncthreads();
+    }
     /* Two columns per step (j and j1 = j + 1, one barrier): every thread
      * forms both pivots' roots itself (the second from the first's
      * update of s[j1][j1]) and the two columns' values it needs, then
@@ -371,14 +383,15 @@ __global__ void __launch_bounds__(1024)
     }
 }
 
-/* A = K + noise I (double), Z = F (double), info cleared. */
+/* A = K + noise I (double), Z = [F | I] (double, rows d + n wide), X = 0
+ * (n x d), info cleared. */
 __global__ void __launch_bounds__(256)
     gp_init_kernel(const float *__restrict__ K, int n, double noise,
-                   double *__restrict__ A, const float *__restrict__ F,
-                   long long nf, double *__restrict__ Z, int *__restrict__ info)
+                   double *__restrict__ A, const float *__restrict__ F, int d,
+                   double *__restrict__ Z, double *__restrict__ X, int *__restrict__ info)
 {
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
-    const long long nn = (long long)n * n;
+    const long long nn = (long long)n * n, w = (long long)d + n, nz = n * w;
 
     if (idx == 0)
         *info = 0;
@@ -387,13 +400,17 @@ __global__ void __launch_bounds__(256)
 
         A[idx] = (double)K[idx] + (r == c ? noise : 0.0);
     }
-    if (idx < nf)
-        Z[idx] = (double)F[idx];
+    if (idx < nz) {
+        const long long r = idx / w, c = idx % w;
+
+        Z[idx] = c < d ? (double)F[r * d + c] : c - d == r ? 1.0 : 0.0;
+    }
+    if (idx < (long long)n * d)
+        X[idx] = 0.0;
 }
 
 __global__ void __launch_bounds__(256)
-    gp_store_kernel(const double *__restrict__ X, long long nf,
-                    float *__restrict__ F)
+    gp_store_kernel(const double *__restrict__ X, long long nf, float *__restrict__ F)
 {
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
 
@@ -405,21 +422,21 @@ static dg_args dg(int M, int N, int K, const double *A, long long a_ri, long lon
                   const double *B, long long b_rk, long long b_rj, double *C,
                   long long c_ri, double alpha, int beta, int lower)
 {
-    dg_args a = {M, N, K, A, a_ri, a_rk, B, b_rk, b_rj, C, c_ri, alpha, beta, lower,
-                 nullptr, -1, nullptr, 0};
+    dg_args a = {M, N, K, A, a_ri, a_rk, B, b_rk, b_rj, C, c_ri, alpha, beta, lower, 0};
 
     return a;
 }
 
-/* One launch for p0 and, when np = 2, p1 (problems with no output are
- * skipped). */
-static void dgemm(hipStream_t s, const dg_args &p0, const dg_args *p1 = nullptr)
+/* One launch for the problems given (those with no output are skipped). */
+static void dgemm(hipStream_t s, std::initializer_list<const dg_args *> ps)
 {
-    dg_pair pr;
+    dg_set pr;
     int np = 0, tx = 0, ty = 0;
 
-    for (const dg_args *a : {&p0, p1})
+    for (const dg_args *a : ps)
         if (a && a->M > 0 && a->N > 0) {
+            if (np == DG_MAXP)
+                icoreg_fatal("roma_gp_solve: more than %d products in one launch", DG_MAXP);
             pr.p[np++] = *a;
             tx = max(tx, (a->N + DG_T - 1) / DG_T);
             ty = max(ty, (a->M + DG_T - 1) / DG_T);
@@ -432,10 +449,10 @@ static void dgemm(hipStream_t s, const dg_args &p0, const dg_args *p1 = nullptr)
 
 extern "C" size_t roma_gp_work_bytes(int n, int d)
 {
-    const size_t nblk = (size_t)(n + GP_NB - 1) / GP_NB;
+    const size_t nblk = (size_t)(n + GP_NB - 1) / GP_NB, w = (size_t)d + n;
 
-    return sizeof(double) * (2 * (size_t)n * n + nblk * GP_NB * GP_NB +
-                             2 * (size_t)n * d);
+    return sizeof(double) * (2 * (size_t)n * n + nblk * GP_NB * GP_NB + 2 * (size_t)n * w +
+                             (size_t)n * d);
 }
 
 extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
@@ -444,14 +461,14 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
     ICOREG_API_BEGIN
     const char *op = "roma_gp_solve";
     hipStream_t s;
-    double *A, *L, *Li, *Z, *Y;
+    double *A, *L, *Li, *Z, *Y, *X;
     const int nblk = (n + GP_NB - 1) / GP_NB;
-    const long long nd = (long long)n * d;
+    const long long nd = (long long)n * d, w = (long long)d + n;
 
     if (n < 1 || d < 1 || n > 46340)
         icoreg_fatal("%s: invalid sizes n=%d d=%d", op, n, d);
     count32((long long)n * n, op);
-    count32(nd, op);
+    count32((long long)n * w, op);
     need_floats(K, 0, (long long)n * n, op, "K");
     need_floats(F, 0, nd, op, "F");
     need_bytes(work, 0, (long long)roma_gp_work_bytes(n, d), op, "work");
@@ -461,61 +478,70 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
     L = A + (long long)n * n;
     Li = L + (long long)n * n;
     Z = Li + (long long)nblk * GP_NB * GP_NB;
-    Y = Z + nd;
+    Y = Z + n * w;
+    X = Y + n * w;
     {
         prof_scope ps(o->ocl, op);
-        const long long nn = (long long)n * n;
-        const long long tot = nn > nd ? nn : nd;
+        const long long nn = (long long)n * n, nz = n * w;
+        const long long tot = nn > nz ? nn : nz;
 
-        hipLaunchKernelGGL(gp_init_kernel, dim3((unsigned)((tot + 255) / 256)),
-                           dim3(256), 0, s, cfptr(K), n, (double)noise, A,
-                           cfptr(F), nd, Z, (int *)info->ptr);
-        /* Factor panel by panel; Y = L^-1 Z alongside. */
+        hipLaunchKernelGGL(gp_init_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s,
+                           cfptr(K), n, (double)noise, A, cfptr(F), d, Z, X, (int *)info->ptr);
+        /* The diagonal blocks on the main stream s, everything else of a
+         * panel on the second stream s2: diagonal block b waits for the
+         * trailing update of panel b - 2 (which has the whole of block
+         * b - 1's factorisation to finish) and applies panel b - 1's
+         * update to its own block itself; panel b's products wait for
+         * block b. Y = L^-1 [F | I] alongside, over the columns that are
+         * not yet zero (F and the identity blocks up to this panel's). */
+        hipStream_t s2 = aux_stream_of(o->ocl);
+
+        hip_check(hipEventRecord(aux_event(o->ocl, 2 * nblk), s), "hipEventRecord");
+        hip_check(hipStreamWaitEvent(s2, aux_event(o->ocl, 2 * nblk), 0), "hipStreamWaitEvent");
         for (int b = 0; b < nblk; b++) {
             const int k = b * GP_NB, nb = n - k < GP_NB ? n - k : GP_NB;
-            const int rest = n - k - nb;
+            const int rest = n - k - nb, wb = d + k + nb;
             double *Lk = Li + (long long)b * GP_NB * GP_NB;
             double *L21 = L + (long long)(k + nb) * n + k;
 
-            hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(1024), 0, s, A, L, Lk, n, k,
-                               nb, (int *)info->ptr);
+            if (b >= 2)
+                hip_check(hipStreamWaitEvent(s, aux_event(o->ocl, 2 * (b - 2) + 1), 0),
+                          "hipStreamWaitEvent");
+            hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(1024), GP_EXCL_BYTES, s, A, L, Lk, n, k,
+                               nb, b ? (const double *)(Lk - GP_NB * GP_NB) : nullptr,
+                               (int *)info->ptr);
+            hip_check(hipEventRecord(aux_event(o->ocl, 2 * b), s), "hipEventRecord");
+            hip_check(hipStreamWaitEvent(s2, aux_event(o->ocl, 2 * b), 0), "hipStreamWaitEvent");
             /* L21 = A21 Linv^T and Y_b = Linv_b Z_b. */
             const dg_args panel = dg(rest, nb, nb, A + (long long)(k + nb) * n + k, n, 1,
                                      Lk, 1, GP_NB, L21, n, 1.0, 0, 0);
-            const dg_args yb = dg(nb, d, nb, Lk, GP_NB, 1, Z + (long long)k * d, d, 1,
-                                  Y + (long long)k * d, d, 1.0, 0, 0);
-            dgemm(s, yb, &panel);
-            if (rest == 0)
-                continue;
-            /* A22 -= L21 L21^T (lower tiles) and Z_rest -= L21 Y_b. */
-            const dg_args trail = dg(rest, rest, nb, L21, n, 1, L21, 1, n,
-                                     A + (long long)(k + nb) * n + k + nb, n, -1.0, 1, 1);
-            const dg_args zr = dg(rest, d, nb, L21, n, 1, Y + (long long)k * d, d, 1,
-                                  Z + (long long)(k + nb) * d, d, -1.0, 1, 0);
-            dgemm(s, trail, &zr);
-        }
-        /* L^T X = Y from the last block; X goes to Z. The last block
-         * alone, then per block b: Y[0:k] -= L[k:k+nb, 0:k]^T X_b with
-         * block b - 1 finished in the epilogue. */
-        {
-            const int b = nblk - 1, k = b * GP_NB, nb = n - k;
+            const dg_args yb = dg(nb, wb, nb, Lk, GP_NB, 1, Z + k * w, w, 1, Y + k * w, w,
+                                  1.0, 0, 0);
+            dgemm(s2, {&yb, &panel});
+            /* X[0 : k + nb] += Minv_b^T Y_F,b: this panel's block row of
+             * Minv = L^-1 (Y[k.., d..], zero right of its own identity
+             * block) is final once Y_b is. */
+            dg_args xacc = dg(k + nb, d, nb, Y + k * w + d, 1, w, Y + k * w, w, 1, X, d, 1.0, 1,
+                              0);
+            if (rest > 0) {
+                /* A22 -= L21 L21^T (lower tiles but the next diagonal block,
+                 * which its own kernel updates) and Z_rest -= L21 Y_b. */
+                dg_args trail = dg(rest, rest, nb, L21, n, 1, L21, 1, n,
+                                   A + (long long)(k + nb) * n + k + nb, n, -1.0, 1, 1);
+                const dg_args zr = dg(rest, wb, nb, L21, n, 1, Y + k * w, w, 1,
+                                      Z + (k + nb) * w, w, -1.0, 1, 0);
 
-            dgemm(s, dg(nb, d, nb, Li + (long long)b * GP_NB * GP_NB, 1, GP_NB,
-                        Y + (long long)k * d, d, 1, Z + (long long)k * d, d, 1.0, 0, 0));
+                trail.skip00 = 1;
+                dgemm(s2, {&trail, &zr, &xacc});
+            }
+            else
+                dgemm(s2, {&xacc});
+            hip_check(hipEventRecord(aux_event(o->ocl, 2 * b + 1), s2), "hipEventRecord");
         }
-        for (int b = nblk - 1; b > 0; b--) {
-            const int k = b * GP_NB, nb = n - k < GP_NB ? n - k : GP_NB;
-            dg_args g = dg(k, d, nb, L + (long long)k * n, 1, n, Z + (long long)k * d, d, 1,
-                           Y, d, -1.0, 1, 0);
-
-            g.linv = Li + (long long)(b - 1) * GP_NB * GP_NB;
-            g.epi_row = b - 1;
-            g.X = Z;
-            g.x_ri = d;
-            dgemm(s, g);
-        }
-        hipLaunchKernelGGL(gp_store_kernel, dim3((unsigned)((nd + 255) / 256)),
-                           dim3(256), 0, s, Z, nd, fptr(F));
+        hip_check(hipStreamWaitEvent(s, aux_event(o->ocl, 2 * (nblk - 1) + 1), 0),
+                  "hipStreamWaitEvent");
+        hipLaunchKernelGGL(gp_store_kernel, dim3((unsigned)((nd + 255) / 256)), dim3(256), 0, s,
+                           (const double *)X, nd, fptr(F));
     }
     launch_check(op);
     ICOREG_API_END

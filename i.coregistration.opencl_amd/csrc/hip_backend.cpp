@@ -295,12 +295,57 @@ extern "C" void ocl_init(struct ocl_backend *ocl, const char *device_opt,
 
 static void destroy_events(void);
 
+#define AUX_MAXEV 4096
+
+namespace icoreg {
+
+hipStream_t aux_stream_of(struct ocl_backend *ocl)
+{
+    if (!ocl->aux_stream) {
+        hipStream_t s;
+
+        hip_check(hipSetDevice(ocl->device), "hipSetDevice");
+        hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate (aux)");
+        ocl->aux_stream = (void *)s;
+    }
+    return (hipStream_t)ocl->aux_stream;
+}
+
+hipEvent_t aux_event(struct ocl_backend *ocl, int i)
+{
+    if (i < 0 || i >= AUX_MAXEV)
+        icoreg_fatal("aux_event: index %d (at most %d events)", i, AUX_MAXEV);
+    if (i >= ocl->aux_nevents) {
+        const int m = i + 1 > 2 * ocl->aux_nevents ? i + 1 : 2 * ocl->aux_nevents;
+        const int nn = m < AUX_MAXEV ? m : AUX_MAXEV;
+        hipEvent_t *ev = (hipEvent_t *)realloc(ocl->aux_events, nn * sizeof(hipEvent_t));
+
+        if (!ev)
+            icoreg_fatal("aux_event: out of host memory");
+        ocl->aux_events = ev;
+        for (int k = ocl->aux_nevents; k < nn; k++) {
+            hip_check(hipEventCreateWithFlags(&ev[k], hipEventDisableTiming), "hipEventCreate");
+            ocl->aux_nevents = k + 1;
+        }
+    }
+    return ((hipEvent_t *)ocl->aux_events)[i];
+}
+
+} // namespace icoreg
+
 extern "C" void ocl_free(struct ocl_backend *ocl)
 {
     ICOREG_API_BEGIN
     if (ocl->stream) {
         (void)hipStreamSynchronize((hipStream_t)ocl->stream);
+        if (ocl->aux_stream)
+            (void)hipStreamSynchronize((hipStream_t)ocl->aux_stream);
         destroy_events();
+        for (int k = 0; k < ocl->aux_nevents; k++)
+            (void)hipEventDestroy(((hipEvent_t *)ocl->aux_events)[k]);
+        free(ocl->aux_events);
+        if (ocl->aux_stream)
+            (void)hipStreamDestroy((hipStream_t)ocl->aux_stream);
         (void)hipStreamDestroy((hipStream_t)ocl->stream);
     }
     memset(ocl, 0, sizeof(*ocl));

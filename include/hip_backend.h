@@ -55,6 +55,13 @@ struct ocl_backend {
     int profile; /* Per-launch timing (I_COREGISTRATION_OPENCL_PROFILE). */
     int cu_count;
     char arch[64]; /* gcnArchName, e.g. "gfx950:sramecc+:xnack-". */
+    /* A second in-order stream (default priority) and a pool of events,
+     * made on first use by operations that run independent work beside
+     * the main stream and join it back before they return (the GP solve);
+     * released by ocl_free. */
+    void *aux_stream;
+    void *aux_events;
+    int aux_nevents;
 };
 
 /* Select the device and create the stream. device_opt: "auto", "gpu"

@@ -18,6 +18,11 @@
 extern "C" {
 #endif
 
+/* sizeof(struct ocl_backend) and sizeof(struct ops), so that a binding
+ * that mirrors their layouts can check them. */
+size_t icoreg_sizeof_backend(void);
+size_t icoreg_sizeof_ops(void);
+
 /* Zeroed structs on the heap, freed with free() after *_free / pth_close. */
 struct pth_file *icoreg_pth_new(void);
 struct eloftr_model *icoreg_eloftr_new(void);

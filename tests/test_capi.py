@@ -71,6 +71,14 @@ def test_binding_covers_exports(ic):
         assert hasattr(lib, name), name
 
 
+def test_binding_struct_layouts_match(ic):
+    """The ctypes mirrors of struct ocl_backend and struct ops have the C
+    sizes (a field added on one side only would shift every later one)."""
+    lib = ic.lib()
+    assert C.sizeof(ic.OclBackend) == lib.icoreg_sizeof_backend()
+    assert C.sizeof(ic.Ops) == lib.icoreg_sizeof_ops()
+
+
 def test_fatal_errors_are_recorded_not_fatal(ic):
     """With the record mode of the binding, a host-side error (here: an
     invalid device option, found before any device call) raises instead of
