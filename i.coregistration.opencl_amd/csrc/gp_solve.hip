@@ -26,10 +26,20 @@
  *    (lower tiles but the next diagonal block), Z_rest -= L21 Y_b and
  *    X[0 : k + nb] += Minv_b^T Y_F,b (fp64 GEMM tiles, up to three
  *    problems per launch).
+ * Synchronisation: the second stream waits for diagonal block b through
+ * the completion event of that kernel's own launch, and the diagonal
+ * kernel of block b waits, inside the kernel, for a flag that a one-wave
+ * kernel sets on the second stream after panel b - 2's trailing update.
+ * The main stream thus holds the diagonal kernels alone: a stream wait
+ * or an event record between them costs 5-7 us of command-processor time
+ * each, on the solve's critical path. Under stream capture (a graph has
+ * no order between branches that an in-kernel wait could rely on), the
+ * diagonal kernels wait through stream events instead.
  * Working matrices: A (n x n, the trailing updates), L (n x n, the
- * factor), Linv per panel, Z and Y (n x (d + n)), X (n x d). No launch
- * reads what another running beside it writes. */
+ * factor), Linv per panel, Z and Y (n x (d + n)), X (n x d), one flag per
+ * panel. No launch reads what another running beside it writes. */
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -205,23 +215,42 @@ __device__ __forceinline__ double rsqrt_nr(double x)
  * (Linv[c][r] -= L[c][j] Linv[j][r], r <= j < c). */
 typedef double gp_d4 __attribute__((ext_vector_type(4)));
 
-/* Dynamic LDS the diagonal block's launch reserves and does not use: with
- * it the block holds 133 KB, so no GEMM block of the second stream (33 KB)
- * is placed on its CU beside it to compete for the LDS bandwidth its
- * column steps are bound by. */
-#define GP_EXCL_BYTES (66 * 1024)
+/* Polls of a panel flag before the diagonal kernel gives up (with a
+ * 64-clock sleep each: about 0.1 s, far beyond any trailing update): the wait
+ * then ends with info = -1 instead of hanging. */
+#define GP_SPIN_MAX (1 << 22)
 
 __global__ void __launch_bounds__(1024)
     chol_diag_kernel(const double *__restrict__ A, double *__restrict__ L,
                      double *__restrict__ Linv, int n, int k, int nb,
-                     const double *__restrict__ lprev, int *__restrict__ info)
+                     const double *__restrict__ lprev, const int *ready,
+                     int *__restrict__ info)
 {
     __shared__ double s[GP_NB][GP_NB + 1], f[GP_NB][GP_NB + 1];
     __shared__ double dinv[GP_NB];
     const int tid = threadIdx.x, tx = tid & 31, ty = tid >> 5;
     /* First failing column of this block (thread 0), reported at the end:
-     * no global access inside the column loop. */
+     * no global access inside the column loop; -1 if the wait for ready
+     * gave up. */
     int bad = 0;
+
+    /* ready (when given): set once the trailing update this block needs
+     * has finished on the other stream. Polled with device-coherent
+     * loads, then this CU's and XCD's caches are invalidated (acquire),
+     * so the block's reads below see that update. */
+    if (ready) {
+        if (tid == 0) {
+            int it = 0;
+
+            while (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
+                   ++it < GP_SPIN_MAX)
+                __builtin_amdgcn_s_sleep(1);
+            if (it >= GP_SPIN_MAX)
+                bad = -1;
+        }
+        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
 
     {
         double v[4];
@@ -384,17 +413,20 @@ __global__ void __launch_bounds__(1024)
 }
 
 /* A = K + noise I (double), Z = [F | I] (double, rows d + n wide), X = 0
- * (n x d), info cleared. */
+ * (n x d), info and the nblk panel flags cleared. */
 __global__ void __launch_bounds__(256)
     gp_init_kernel(const float *__restrict__ K, int n, double noise,
                    double *__restrict__ A, const float *__restrict__ F, int d,
-                   double *__restrict__ Z, double *__restrict__ X, int *__restrict__ info)
+                   double *__restrict__ Z, double *__restrict__ X, int *__restrict__ info,
+                   int *__restrict__ flags, int nblk)
 {
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
     const long long nn = (long long)n * n, w = (long long)d + n, nz = n * w;
 
     if (idx == 0)
         *info = 0;
+    if (idx < nblk)
+        flags[idx] = 0;
     if (idx < nn) {
         const int r = (int)(idx / n), c = (int)(idx % n);
 
@@ -407,6 +439,14 @@ __global__ void __launch_bounds__(256)
     }
     if (idx < (long long)n * d)
         X[idx] = 0.0;
+}
+
+/* Panel flag: set by one lane after the launches before it on its stream
+ * (the panel's trailing update) have finished; device-coherent store. */
+__global__ void __launch_bounds__(64) gp_mark_kernel(int *flag)
+{
+    if (threadIdx.x == 0)
+        __hip_atomic_store(flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __global__ void __launch_bounds__(256)
@@ -452,7 +492,8 @@ extern "C" size_t roma_gp_work_bytes(int n, int d)
     const size_t nblk = (size_t)(n + GP_NB - 1) / GP_NB, w = (size_t)d + n;
 
     return sizeof(double) * (2 * (size_t)n * n + nblk * GP_NB * GP_NB + 2 * (size_t)n * w +
-                             (size_t)n * d);
+                             (size_t)n * d) +
+           sizeof(int) * nblk;
 }
 
 extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
@@ -462,6 +503,7 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
     const char *op = "roma_gp_solve";
     hipStream_t s;
     double *A, *L, *Li, *Z, *Y, *X;
+    int *flags;
     const int nblk = (n + GP_NB - 1) / GP_NB;
     const long long nd = (long long)n * d, w = (long long)d + n;
 
@@ -480,13 +522,19 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
     Z = Li + (long long)nblk * GP_NB * GP_NB;
     Y = Z + n * w;
     X = Y + n * w;
+    flags = (int *)(X + nd);
     {
         prof_scope ps(o->ocl, op);
         const long long nn = (long long)n * n, nz = n * w;
         const long long tot = nn > nz ? nn : nz;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+
+        hip_check(hipStreamIsCapturing(s, &cs), "hipStreamIsCapturing");
+        const bool capture = cs != hipStreamCaptureStatusNone;
 
         hipLaunchKernelGGL(gp_init_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s,
-                           cfptr(K), n, (double)noise, A, cfptr(F), d, Z, X, (int *)info->ptr);
+                           cfptr(K), n, (double)noise, A, cfptr(F), d, Z, X, (int *)info->ptr,
+                           flags, nblk);
         /* The diagonal blocks on the main stream s, everything else of a
          * panel on the second stream s2: diagonal block b waits for the
          * trailing update of panel b - 2 (which has the whole of block
@@ -503,15 +551,31 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
             const int rest = n - k - nb, wb = d + k + nb;
             double *Lk = Li + (long long)b * GP_NB * GP_NB;
             double *L21 = L + (long long)(k + nb) * n + k;
+            const double *lprev = b ? (const double *)(Lk - GP_NB * GP_NB) : nullptr;
+            int *info_p = (int *)info->ptr;
+            const hipEvent_t done_b = aux_event(o->ocl, 2 * b);
 
-            if (b >= 2)
-                hip_check(hipStreamWaitEvent(s, aux_event(o->ocl, 2 * (b - 2) + 1), 0),
-                          "hipStreamWaitEvent");
-            hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(1024), GP_EXCL_BYTES, s, A, L, Lk, n, k,
-                               nb, b ? (const double *)(Lk - GP_NB * GP_NB) : nullptr,
-                               (int *)info->ptr);
-            hip_check(hipEventRecord(aux_event(o->ocl, 2 * b), s), "hipEventRecord");
-            hip_check(hipStreamWaitEvent(s2, aux_event(o->ocl, 2 * b), 0), "hipStreamWaitEvent");
+            if (capture) {
+                if (b >= 2)
+                    hip_check(hipStreamWaitEvent(s, aux_event(o->ocl, 2 * (b - 2) + 1), 0),
+                              "hipStreamWaitEvent");
+                hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(1024), 0, s, A,
+                                   L, Lk, n, k, nb, lprev, (const int *)nullptr, info_p);
+                hip_check(hipEventRecord(done_b, s), "hipEventRecord");
+            }
+            else {
+                /* The launch's completion signals done_b itself: no
+                 * separate record on s. */
+                const int *ready = b >= 2 ? flags + b - 2 : nullptr;
+                void *args[] = {(void *)&A, (void *)&L,     (void *)&Lk,    (void *)&n,
+                                (void *)&k, (void *)&nb,    (void *)&lprev, (void *)&ready,
+                                (void *)&info_p};
+
+                hip_check(hipExtLaunchKernel((const void *)chol_diag_kernel, dim3(1), dim3(1024),
+                                             args, 0, s, nullptr, done_b, 0),
+                          "hipExtLaunchKernel");
+            }
+            hip_check(hipStreamWaitEvent(s2, done_b, 0), "hipStreamWaitEvent");
             /* L21 = A21 Linv^T and Y_b = Linv_b Z_b. */
             const dg_args panel = dg(rest, nb, nb, A + (long long)(k + nb) * n + k, n, 1,
                                      Lk, 1, GP_NB, L21, n, 1.0, 0, 0);
@@ -536,7 +600,10 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
             }
             else
                 dgemm(s2, {&xacc});
-            hip_check(hipEventRecord(aux_event(o->ocl, 2 * b + 1), s2), "hipEventRecord");
+            if (!capture)
+                hipLaunchKernelGGL(gp_mark_kernel, dim3(1), dim3(64), 0, s2, flags + b);
+            if (capture || b == nblk - 1)
+                hip_check(hipEventRecord(aux_event(o->ocl, 2 * b + 1), s2), "hipEventRecord");
         }
         hip_check(hipStreamWaitEvent(s, aux_event(o->ocl, 2 * (nblk - 1) + 1), 0),
                   "hipStreamWaitEvent");

@@ -759,6 +759,9 @@ static void gp_check(struct roma_model *m)
     int info = 0;
 
     ocl_read(m->ocl, m->gp_info, 0, &info, sizeof(info));
+    if (info < 0)
+        icoreg_fatal("RoMa: Gaussian process solve: a diagonal block's wait for "
+                     "its trailing update gave up");
     if (info)
         icoreg_fatal("RoMa: Gaussian process kernel not positive definite "
                      "(column %d)",

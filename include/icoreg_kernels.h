@@ -190,7 +190,10 @@ void disk_gather_desc_count(struct ops *o, cl_mem feat, int H, int W, int D,
  * triangle read). work holds roma_gp_work_bytes(n, d) bytes; info (one
  * int, cleared by the call) gets 1 + the first column whose pivot is
  * not positive, the reference's "not positive definite" failure, for
- * the caller to check once the stream has run. */
+ * the caller to check once the stream has run (-1: an internal wait
+ * between the solve's two streams gave up, which does not happen when the
+ * device runs the launches). The call runs on the library's stream and
+ * on its second stream (joined back before it returns to the stream). */
 size_t roma_gp_work_bytes(int n, int d);
 void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise, cl_mem F,
                    int d, cl_mem work, cl_mem info);
