@@ -27,6 +27,7 @@
  * into registers while the matrix cores work on the current one. Images
  * of a batch run on the grid's z dimension. */
 
+#include <algorithm>
 #include <hip/hip_runtime.h>
 
 #include "act.h"
@@ -363,38 +364,63 @@ __global__ void __launch_bounds__(256) conv_c1_kernel(const conv_args a)
  * share KS - 1 rows). The patches of 4 input channels (2 at stride 2)
  * are staged in LDS per step, normalised and gated exactly as conv_mfma loads them, the
  * next step's values loaded into registers while this one is used; a
- * channel's NK filters are read from LDS once and used for both pixels. */
+ * channel's NK filters are read from LDS once and used for both pixels.
+ * The input channels can be cut into a.split pieces (grid z = image + nb
+ * piece, whole steps each): a grid of a few hundred tiles then still
+ * fills the CUs, each piece's raw sums going to a.part for
+ * conv_fewk_sum_kernel. Filters and normalisation of the block's channels
+ * sit in dynamic LDS (fewk_lds_bytes). */
 #define FK_MAXK 8
 #define FK_MAXW 8192
 #define FK_MAXC 1024
+
+/* Dynamic LDS of a conv_fewk_kernel block: the filters of its input
+ * channels (nk cpp KK floats) and their mean, rstd and gate. */
+static size_t fewk_lds_bytes(int nk, int cpp, int kk)
+{
+    return ((size_t)nk * cpp * kk + 3 * (size_t)cpp) * sizeof(float);
+}
+
 template <int KS, int ST, int NK>
-__global__ void __launch_bounds__(256) conv_fewk_kernel(const conv_args a, int k0)
+__global__ void __launch_bounds__(256) conv_fewk_kernel(const conv_args a, int k0, int nb,
+                                                        int cpp)
 {
     constexpr int TW = 16, TH = 32, KK = KS * KS, FK_CC = ST == 1 ? 4 : 2;
     constexpr int PW = (TW - 1) * ST + KS, PH = (TH - 1) * ST + KS;
     constexpr int PN = FK_CC * PH * PW, NP = (PN + 255) / 256;
     static_assert(NP <= 32, "validity mask");
-    __shared__ float ws[FK_MAXW];
-    __shared__ float nm[3][FK_MAXC]; /* mean, rstd, gate per input channel */
-    __shared__ float patch[FK_CC][PH][PW + 1];
+    /* Row pitch: at stride 1 the two rows a half-wave reads (2 pitch
+     * apart) fall on disjoint banks when 2 pitch = 16 (mod 32). */
+    constexpr int PP = ST == 1 ? (PW + 8) / 16 * 16 + 8 : PW + 1;
+    extern __shared__ float fk_dyn[];
+    __shared__ float patch[FK_CC][PH][PP];
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     const int ox0 = blockIdx.x * TW, oy0 = blockIdx.y * TH;
     const int iy0 = oy0 * ST - a.pad, ix0 = ox0 * ST - a.pad;
+    const int img = blockIdx.z % nb, piece = blockIdx.z / nb;
+    /* This block's input channels [cb, ce): cpp (a multiple of FK_CC) a
+     * piece. */
+    const int cb = piece * cpp, ce = min(a.C, cb + cpp), cn = ce - cb;
+    float *const ws = fk_dyn;              /* [NK][cn][KK] */
+    float *const nm = fk_dyn + NK * cpp * KK; /* mean, rstd, gate: [3][cn] */
     const long long HW = (long long)a.H * a.W;
-    const float *in = a.in + (long long)blockIdx.z * a.in_stride;
+    const float *in = a.in + (long long)img * a.in_stride + cb * HW;
     float acc[2][NK], rp[NP];
     unsigned valid = 0;
 
 #pragma unroll
     for (int k = 0; k < NK; k++)
         acc[0][k] = acc[1][k] = 0.0f;
-    for (int i = threadIdx.x; i < NK * a.C * KK; i += 256)
-        ws[i] = a.w[(long long)k0 * a.C * KK + i];
+    for (int i = threadIdx.x; i < NK * cn * KK; i += 256) {
+        const int k = i / (cn * KK), r = i - k * cn * KK;
+
+        ws[i] = a.w[((long long)(k0 + k) * a.C + cb) * KK + r];
+    }
     if (a.mean)
-        for (int c = threadIdx.x; c < a.C; c += 256) {
-            nm[0][c] = a.mean[c];
-            nm[1][c] = a.rstd[c];
-            nm[2][c] = a.gate ? a.gate[c] : 1.0f;
+        for (int c = threadIdx.x; c < cn; c += 256) {
+            nm[c] = a.mean[cb + c];
+            nm[cn + c] = a.rstd[cb + c];
+            nm[2 * cn + c] = a.gate ? a.gate[cb + c] : 1.0f;
         }
     /* Loads only, every one issued before any is used: out-of-range
      * values read the channel's first element and are masked later. */
@@ -404,8 +430,8 @@ __global__ void __launch_bounds__(256) conv_fewk_kernel(const conv_args a, int k
         for (int q = 0; q < NP; q++) {
             const int e = threadIdx.x + 256 * q, cc = e / (PH * PW), rem = e - cc * (PH * PW);
             const int py = rem / PW, px = rem - py * PW, iy = iy0 + py, ix = ix0 + px;
-            const int c = min(c0 + cc, a.C - 1);
-            const bool ok = e < PN && c0 + cc < a.C && iy >= 0 && iy < a.H && ix >= 0 &&
+            const int c = min(c0 + cc, cn - 1);
+            const bool ok = e < PN && c0 + cc < cn && iy >= 0 && iy < a.H && ix >= 0 &&
                             ix < a.W;
 
             rp[q] = in[c * HW + (ok ? (long long)iy * a.W + ix : 0)];
@@ -414,32 +440,32 @@ __global__ void __launch_bounds__(256) conv_fewk_kernel(const conv_args a, int k
     };
     fetch(0);
     __syncthreads();
-    for (int c0 = 0; c0 < a.C; c0 += FK_CC) {
+    for (int c0 = 0; c0 < cn; c0 += FK_CC) {
 #pragma unroll
         for (int q = 0; q < NP; q++) {
             const int e = threadIdx.x + 256 * q, cc = e / (PH * PW), rem = e - cc * (PH * PW);
-            const int c = min(c0 + cc, a.C - 1);
+            const int c = min(c0 + cc, cn - 1);
             float v = rp[q];
 
             if (a.mean) {
-                v = (v - nm[0][c]) * nm[1][c];
+                v = (v - nm[c]) * nm[cn + c];
                 if (a.gate)
-                    v = v >= 0.0f ? v : nm[2][c] * v;
+                    v = v >= 0.0f ? v : nm[2 * cn + c] * v;
             }
             if (e < PN)
                 patch[cc][rem / PW][rem % PW] = valid >> q & 1u ? v : 0.0f;
         }
         __syncthreads();
-        if (c0 + FK_CC < a.C)
+        if (c0 + FK_CC < cn)
             fetch(c0 + FK_CC);
-        for (int cc = 0; cc < FK_CC && c0 + cc < a.C; cc++) {
+        for (int cc = 0; cc < FK_CC && c0 + cc < cn; cc++) {
             float wk[NK][KK];
 
 #pragma unroll
             for (int k = 0; k < NK; k++)
 #pragma unroll
                 for (int t = 0; t < KK; t++)
-                    wk[k][t] = ws[(k * a.C + c0 + cc) * KK + t];
+                    wk[k][t] = ws[(k * cn + c0 + cc) * KK + t];
 #pragma unroll
             for (int i = 0; i < KS + ST; i++)
 #pragma unroll
@@ -459,7 +485,9 @@ __global__ void __launch_bounds__(256) conv_fewk_kernel(const conv_args a, int k
     }
     {
         const int ox = ox0 + tx;
-        float *out = a.out + (long long)blockIdx.z * a.out_stride;
+        float *out = a.out + (long long)img * a.out_stride;
+        /* Pieces: raw sums, planes [piece][image][k]. */
+        float *pp = a.part + ((long long)piece * nb + img) * NK * a.Ho * a.Wo;
 
 #pragma unroll
         for (int r = 0; r < 2; r++) {
@@ -469,6 +497,10 @@ __global__ void __launch_bounds__(256) conv_fewk_kernel(const conv_args a, int k
                 continue;
 #pragma unroll
             for (int k = 0; k < NK; k++) {
+                if (a.split > 1) {
+                    pp[((long long)k * a.Ho + oy) * a.Wo + ox] = acc[r][k];
+                    continue;
+                }
                 const float v = acc[r][k] + (a.bias ? a.bias[k0 + k] : 0.0f);
 
                 out[((long long)(k0 + k) * a.Ho + oy) * a.Wo + ox] =
@@ -478,14 +510,62 @@ __global__ void __launch_bounds__(256) conv_fewk_kernel(const conv_args a, int k
     }
 }
 
-template <int KS, int ST>
-static void launch_fewk(const conv_args &a, int k0, int nk, int nb, hipStream_t s)
+/* The pieces of conv_fewk_kernel: one thread per (image, channel, output)
+ * adds them in piece order, then bias and activation. */
+__global__ void __launch_bounds__(256)
+    conv_fewk_sum_kernel(const conv_args a, int k0, int nk, int nb)
 {
-    const dim3 grid((a.Wo + 15) / 16, (a.Ho + 31) / 32, nb);
+    const long long plane = (long long)nk * a.Ho * a.Wo;
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    const int img = blockIdx.y;
+
+    if (e >= plane)
+        return;
+    float v = a.part[(long long)img * plane + e];
+
+    for (int p = 1; p < a.split; p++)
+        v += a.part[((long long)p * nb + img) * plane + e];
+    const int k = (int)(e / ((long long)a.Ho * a.Wo));
+
+    if (a.bias)
+        v += a.bias[k0 + k];
+    a.out[(long long)img * a.out_stride + (long long)k0 * a.Ho * a.Wo + e] =
+        icoreg_act(v, a.act, a.slope);
+}
+
+/* Pieces of the input channels for conv_fewk_kernel over nb images: about
+ * eight blocks a CU, whole steps of FK_CC channels each. cpp: channels a
+ * piece. */
+static int fewk_split(const conv_args &a, int st, int nb, int cus, int &cpp)
+{
+    const int cc = st == 1 ? 4 : 2, steps = (a.C + cc - 1) / cc;
+    const long long blocks = (long long)((a.Wo + 15) / 16) * ((a.Ho + 31) / 32) * nb;
+    int split = blocks < 8LL * cus ? (int)((8LL * cus + blocks - 1) / blocks) : 1;
+
+    split = std::min(std::min(split, 8), steps);
+    if (nb * (long long)split > 65535)
+        split = 1;
+    cpp = (steps + split - 1) / split * cc;
+    return (a.C + cpp - 1) / cpp;
+}
+
+template <int KS, int ST>
+static void launch_fewk(const conv_args &a, int k0, int nk, int nb, int cus, hipStream_t s)
+{
+    int cpp;
+    const int split = a.part ? fewk_split(a, ST, nb, cus, cpp) : 1;
+    conv_args f = a;
+
+    if (split == 1)
+        cpp = (a.C + (ST == 1 ? 4 : 2) - 1) / (ST == 1 ? 4 : 2) * (ST == 1 ? 4 : 2);
+    f.split = split;
+    const dim3 grid((a.Wo + 15) / 16, (a.Ho + 31) / 32, nb * split);
+    const size_t lds = fewk_lds_bytes(nk, cpp, KS * KS);
 
 #define FK_CASE(N)                                                             \
     case N:                                                                    \
-        hipLaunchKernelGGL((conv_fewk_kernel<KS, ST, N>), grid, dim3(256), 0, s, a, k0); \
+        hipLaunchKernelGGL((conv_fewk_kernel<KS, ST, N>), grid, dim3(256), lds, s, f, k0, nb, \
+                           cpp);                                               \
         break;
     switch (nk) {
         FK_CASE(1)
@@ -498,6 +578,10 @@ static void launch_fewk(const conv_args &a, int k0, int nk, int nb, hipStream_t 
         FK_CASE(8)
     }
 #undef FK_CASE
+    if (split > 1)
+        hipLaunchKernelGGL(conv_fewk_sum_kernel,
+                           dim3((unsigned)(((long long)nk * a.Ho * a.Wo + 255) / 256), nb),
+                           dim3(256), 0, s, f, k0, nk, nb);
 }
 
 bool conv_direct_supported(int kh, int kw, int sy, int sx, int dy, int dx,
@@ -580,12 +664,23 @@ size_t conv_direct_part_bytes(const conv_args &a, int ks, int stride, int nb, in
     if (a.C == 1 && !a.mean && a.K <= C1_MAXK && a.K * ks * ks <= C1_MAXW)
         return 0;
     const direct_plan p = plan_direct(a, ks, nb, cus);
+    const size_t main = p.split > 1 ? (size_t)p.split * nb * p.kmain * a.Ho * a.Wo : 0;
+    size_t fewk = 0;
 
-    return p.split > 1 ? (size_t)p.split * nb * p.kmain * a.Ho * a.Wo * sizeof(float) : 0;
+    if (p.kmain < a.K) {
+        /* The few-channel kernel runs after the main one's pieces are
+         * added, so the two share the buffer. */
+        int cpp;
+        const int split = fewk_split(a, stride, nb, cus, cpp);
+
+        if (split > 1)
+            fewk = (size_t)split * nb * (a.K - p.kmain) * a.Ho * a.Wo;
+    }
+    return std::max(main, fewk) * sizeof(float);
 }
 
 template <int KS, int ST, int BM, int TW, int NJ>
-static void launch_cfg(const conv_args &a, const direct_plan &p, int nb, hipStream_t s)
+static void launch_cfg(const conv_args &a, const direct_plan &p, int nb, int cus, hipStream_t s)
 {
     /* K = 100 (5 x 5) or 36 (3 x 3) per slice at 64 channels per block,
      * 50 at 128. */
@@ -603,7 +698,7 @@ static void launch_cfg(const conv_args &a, const direct_plan &p, int nb, hipStre
                            dim3((unsigned)(((long long)m.K * a.Ho * a.Wo + 255) / 256), nb),
                            dim3(256), 0, s, m, nb);
     if (p.kmain < a.K)
-        launch_fewk<KS, ST>(a, p.kmain, a.K - p.kmain, nb, s);
+        launch_fewk<KS, ST>(a, p.kmain, a.K - p.kmain, nb, cus, s);
 }
 
 template <int KS, int ST>
@@ -614,15 +709,15 @@ static void launch_ks(const conv_args &a, int nb, int cus, hipStream_t s)
 
     if (p.bm == 128) {
         if (p.tw == 16)
-            launch_cfg<KS, ST, 128, 16, NJ>(a, p, nb, s);
+            launch_cfg<KS, ST, 128, 16, NJ>(a, p, nb, cus, s);
         else
-            launch_cfg<KS, ST, 128, 32, NJ>(a, p, nb, s);
+            launch_cfg<KS, ST, 128, 32, NJ>(a, p, nb, cus, s);
         return;
     }
     if (p.tw == 16)
-        launch_cfg<KS, ST, 64, 16, NJ>(a, p, nb, s);
+        launch_cfg<KS, ST, 64, 16, NJ>(a, p, nb, cus, s);
     else
-        launch_cfg<KS, ST, 64, 32, NJ>(a, p, nb, s);
+        launch_cfg<KS, ST, 64, 32, NJ>(a, p, nb, cus, s);
 }
 
 void conv_direct_launch(const conv_args &a, int ks, int stride, int nb,
