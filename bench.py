@@ -146,6 +146,24 @@ def conv_traffic(profile=ROOT / "profiles" / "eloftr_640_wino_traffic.md"):
     return int(m.group(1)) if m else None
 
 
+def conv_counters(profile=ROOT / "profiles" / "eloftr_640_wino_sq_counters.md"):
+    """The Winograd kernel's matrix-pipe share of its CUs' busy cycles and
+    its CU-busy share of the dispatch, from the committed rocprofv3 SQ
+    counter summary, or None."""
+    import re
+    try:
+        t = profile.read_text()
+    except OSError:
+        return None
+    m1 = re.search(r"mfma_issue_share_of_busy_cycles:\s*([0-9.]+)", t)
+    m2 = re.search(r"cu_busy_share:\s*([0-9.]+)", t)
+    if not (m1 and m2):
+        return None
+    return {"mfma_issue_share_of_busy_cycles": float(m1.group(1)),
+            "cu_busy_share": float(m2.group(1)),
+            "source": "profiles/eloftr_640_wino_sq_counters.md"}
+
+
 def roma_coarse_flops(coarse=560):
     """Algorithmic FLOPs of RoMa's coarse forward on one pair (DINOv2 x 2,
     GP, decoder), by kernel family; the GP's double-precision Cholesky
@@ -1012,6 +1030,7 @@ def main():
                      "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_FP32_MFMA, 4),
                      "traffic": conv_traffic() if H == W == 640 else None,
+                     "sq_counters": conv_counters() if H == W == 640 else None,
                      "algorithmic_bytes_per_launch": round(eloftr_wino_bytes(H, W) / 22),
                      "launches_per_step": wino_calls,
                      "gflop_per_step": round(wino_fl / 1e9, 2),
