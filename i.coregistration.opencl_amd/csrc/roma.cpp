@@ -255,31 +255,61 @@ static void load_dino(struct roma_model *m, struct pth_file *pf)
     m->norm_b = load_dev(m, pf, "norm.bias", 1, v1);
 }
 
+/* rows x cols (row-major) into prow x pcol, zero padded; frees v. */
+static float *pad2(float *v, long rows, long cols, long prow, long pcol)
+{
+    float *o = (float *)calloc((size_t)prow * pcol, sizeof(float));
+
+    if (!o)
+        icoreg_fatal("RoMa: out of host memory");
+    for (long r = 0; r < rows; r++)
+        memcpy(o + (size_t)r * pcol, v + (size_t)r * cols, (size_t)cols * sizeof(float));
+    free(v);
+    return o;
+}
+
 /* ConvRefiner blocks (block1, hidden_blocks.*) of cin channels under pre:
- * depthwise conv + BatchNorm names dw / bn, pointwise name pw. */
+ * depthwise conv + BatchNorm names dw / bn, pointwise name pw; uploaded
+ * padded to r->cp channels (zero weights and biases). */
 static void load_refiner_blocks(struct roma_model *m, struct pth_file *pf,
                                 const char *pre, const char *dw,
                                 const char *bn, const char *pw,
                                 struct roma_refiner *r)
 {
-    char blk[128], conv[160], norm[160], name[200];
+    char blk[128], name[200];
+    const long c = r->cin, cp = r->cp;
 
     for (int b = 0; b <= ROMA_HIDDEN; b++) {
-        long sdw[4] = {r->cin, 1, 5, 5}, spw[4] = {r->cin, r->cin, 1, 1};
-        long sb[1] = {r->cin};
+        long sdw[4] = {c, 1, 5, 5}, spw[4] = {c, c, 1, 1}, sb[1] = {c};
+        float *w, *bias;
 
         if (b == 0)
             snprintf(blk, sizeof(blk), "%s.block1", pre);
         else
             snprintf(blk, sizeof(blk), "%s.hidden_blocks.%d", pre, b - 1);
-        snprintf(conv, sizeof(conv), "%s.%s", blk, dw);
-        snprintf(norm, sizeof(norm), "%s.%s", blk, bn);
-        load_conv_bn(m, pf, conv, norm, r->cin, 4, sdw, &r->dw_w[b],
-                     &r->dw_b[b]);
+        /* Depthwise 5 x 5 with its BatchNorm folded in (load_conv_bn). */
+        snprintf(name, sizeof(name), "%s.%s.weight", blk, dw);
+        w = read_host(pf, name, 4, sdw);
+        snprintf(name, sizeof(name), "%s.%s.bias", blk, dw);
+        bias = pth_find(pf, name) ? read_host(pf, name, 1, sb)
+                                  : (float *)calloc((size_t)c, sizeof(float));
+        snprintf(name, sizeof(name), "%s.%s", blk, bn);
+        fold(pf, name, (int)c, 25, w, bias);
+        w = pad2(w, c, 25, cp, 25);
+        bias = pad2(bias, 1, c, 1, cp);
+        snprintf(name, sizeof(name), "%s.%s", blk, dw);
+        r->dw_w[b] = upload(m, w, (size_t)cp * 25, name);
+        r->dw_b[b] = upload(m, bias, cp, name);
+        free(w);
+        free(bias);
         snprintf(name, sizeof(name), "%s.%s.weight", blk, pw);
-        r->pw_w[b] = load_dev(m, pf, name, 4, spw);
+        w = pad2(read_host(pf, name, 4, spw), c, c, cp, cp);
         snprintf(name, sizeof(name), "%s.%s.bias", blk, pw);
-        r->pw_b[b] = load_dev(m, pf, name, 1, sb);
+        bias = pad2(read_host(pf, name, 1, sb), 1, c, 1, cp);
+        r->pw_w[b] = upload(m, w, (size_t)cp * cp, name);
+        r->pw_b[b] = upload(m, bias, cp, name);
+        free(w);
+        free(bias);
     }
 }
 
@@ -296,6 +326,7 @@ static void load_refiner(struct roma_model *m, struct pth_file *pf, int s)
     r->radius = ref_radius[s];
     corr = r->radius ? (2 * r->radius + 1) * (2 * r->radius + 1) : 0;
     r->cin = 2 * r->feat + r->emb + corr;
+    r->cp = (r->cin + 3) / 4 * 4;
     r->nout = 3;
     snprintf(pre, sizeof(pre), "decoder.conv_refiner.%d", r->scale);
     load_refiner_blocks(m, pf, pre, "0", "1", "3", r);
@@ -304,7 +335,12 @@ static void load_refiner(struct roma_model *m, struct pth_file *pf, int s)
         long se[4] = {r->emb, 2, 1, 1}, seb[1] = {r->emb};
 
         snprintf(name, sizeof(name), "%s.out_conv.weight", pre);
-        r->out_w = load_dev(m, pf, name, 4, so);
+        {
+            float *w = pad2(read_host(pf, name, 4, so), 3, r->cin, 3, r->cp);
+
+            r->out_w = upload(m, w, 3 * (size_t)r->cp, name);
+            free(w);
+        }
         snprintf(name, sizeof(name), "%s.out_conv.bias", pre);
         r->out_b = load_dev(m, pf, name, 1, sob);
         snprintf(name, sizeof(name), "%s.disp_emb.weight", pre);
@@ -373,6 +409,7 @@ static void load_refiner2(struct roma_model *m, struct pth_file *pf, int j)
     r->radius = ref2_radius[j];
     corr = r->radius ? (2 * r->radius + 1) * (2 * r->radius + 1) : 0;
     r->cin = 2 * r->feat + r->emb + corr;
+    r->cp = (r->cin + 3) / 4 * 4;
     r->nout = 6;
     snprintf(pre, sizeof(pre), "refiners.%d", r->scale);
     snprintf(name, sizeof(name), "%s.proj.weight", pre);
@@ -411,7 +448,8 @@ static void load_refiner2(struct roma_model *m, struct pth_file *pf, int j)
         for (int k = 0; k < 4; k++)
             bias[2 + k] = part[k];
         free(part);
-        r->out_w = upload(m, w, 6 * (size_t)r->cin, "heads");
+        w = pad2(w, 6, r->cin, 6, r->cp);
+        r->out_w = upload(m, w, 6 * (size_t)r->cp, "heads");
         r->out_b = upload(m, bias, 6, "heads");
         free(w);
     }
@@ -599,7 +637,7 @@ extern "C" void roma_alloc(struct roma_model *m, int H, int W)
             const int ph = p ? H : m->coarse, pw = p ? W : m->coarse;
             const size_t n = (size_t)side(m, ph, s) * side(m, pw, s);
 
-            dmax = max_sz(dmax, (size_t)m->ref[s].cin * n);
+            dmax = max_sz(dmax, (size_t)m->ref[s].cp * n);
         }
     if (m->v2) {
         for (int p = 0; p < 2; p++)
@@ -608,7 +646,7 @@ extern "C" void roma_alloc(struct roma_model *m, int H, int W)
                 const size_t n =
                     (size_t)(ph / ref2_scale[s]) * (pw / ref2_scale[s]);
 
-                dmax = max_sz(dmax, (size_t)m->ref2[s].cin * n);
+                dmax = max_sz(dmax, (size_t)m->ref2[s].cp * n);
             }
         for (int s = 0; s < ROMA2_SCALES; s++) {
             const size_t cells = (size_t)(m->hm / ref2_scale[s]) *
@@ -848,12 +886,15 @@ static void refiner_body(struct roma_model *m, const struct roma_refiner *r,
     if (r->radius)
         roma_local_corr(o, fa, fb, r->feat, hs, ws, r->radius, fl, m->d_a,
                         2 * r->feat + r->emb);
+    /* The padding channels (cin .. cp) start at zero and stay zero. */
+    if (r->cp > r->cin)
+        ocl_fill(m->ocl, m->d_a, (size_t)r->cin * n, (size_t)(r->cp - r->cin) * n, 0.0f);
     for (int b = 0; b <= ROMA_HIDDEN; b++) {
-        roma_dwconv5(o, m->d_a, r->cin, hs, ws, r->dw_w[b], r->dw_b[b], m->d_b);
-        ops_conv1x1(o, m->d_b, 0, r->cin, n, r->pw_w[b], r->pw_b[b], r->cin,
+        roma_dwconv5(o, m->d_a, r->cp, hs, ws, r->dw_w[b], r->dw_b[b], m->d_b);
+        ops_conv1x1(o, m->d_b, 0, r->cp, n, r->pw_w[b], r->pw_b[b], r->cp,
                     m->d_a, 0, ACT_NONE, 0);
     }
-    ops_conv1x1(o, m->d_a, 0, r->cin, n, r->out_w, r->out_b, r->nout, m->d_c, 0,
+    ops_conv1x1(o, m->d_a, 0, r->cp, n, r->out_w, r->out_b, r->nout, m->d_c, 0,
                 ACT_NONE, 0);
 }
 

@@ -45,7 +45,10 @@ struct roma_block {
  * of depthwise 5 x 5 (BatchNorm folded) + ReLU + 1 x 1; out_conv to 3
  * outputs (v1) or 6 (v2: warp head and confidence head). */
 struct roma_refiner {
-    int scale, feat, emb, radius, cin, nout;
+    /* cp: cin rounded up to a multiple of 4; the blocks and the output
+     * convolution run on cp channels, the padding channels zero (zero
+     * weights and biases), so that every weight row is 16-byte aligned. */
+    int scale, feat, emb, radius, cin, nout, cp;
     cl_mem dw_w[ROMA_HIDDEN + 1], dw_b[ROMA_HIDDEN + 1];
     cl_mem pw_w[ROMA_HIDDEN + 1], pw_b[ROMA_HIDDEN + 1];
     cl_mem out_w, out_b, emb_w, emb_b;
