@@ -177,6 +177,7 @@ SIGNATURES = {
     "roma_update": (None, [_O, Mem, Mem, Mem, _I, _F, _F, _F]),
     "roma2_update": (None, [_O, Mem, Mem, Mem, _I, _F, _F]),
     "roma_dwconv5": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem]),
+    "roma_dwpw_small": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
     "roma_gp_work_bytes": (C.c_size_t, [_I, _I]),
     "roma_gp_solve": (None, [_O, Mem, _I, _F, Mem, _I, Mem, Mem]),
     "roma_prepare": (None, [_O, Mem, _I, _I, _I, Mem, _I, _I, _I]),

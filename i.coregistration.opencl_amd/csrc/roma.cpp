@@ -889,12 +889,28 @@ static void refiner_body(struct roma_model *m, const struct roma_refiner *r,
     /* The padding channels (cin .. cp) start at zero and stay zero. */
     if (r->cp > r->cin)
         ocl_fill(m->ocl, m->d_a, (size_t)r->cin * n, (size_t)(r->cp - r->cin) * n, 0.0f);
-    for (int b = 0; b <= ROMA_HIDDEN; b++) {
-        roma_dwconv5(o, m->d_a, r->cp, hs, ws, r->dw_w[b], r->dw_b[b], m->d_b);
-        ops_conv1x1(o, m->d_b, 0, r->cp, n, r->pw_w[b], r->pw_b[b], r->cp,
-                    m->d_a, 0, ACT_NONE, 0);
+    cl_mem src = m->d_a;
+
+    if (r->cp <= 32 && r->cp % 8 == 0) {
+        /* Few channels: each block in one pass, alternating buffers. */
+        cl_mem dst = m->d_b;
+
+        for (int b = 0; b <= ROMA_HIDDEN; b++) {
+            roma_dwpw_small(o, src, r->cp, hs, ws, r->dw_w[b], r->dw_b[b], r->pw_w[b],
+                            r->pw_b[b], dst);
+            cl_mem t = src;
+
+            src = dst;
+            dst = t;
+        }
     }
-    ops_conv1x1(o, m->d_a, 0, r->cp, n, r->out_w, r->out_b, r->nout, m->d_c, 0,
+    else
+        for (int b = 0; b <= ROMA_HIDDEN; b++) {
+            roma_dwconv5(o, m->d_a, r->cp, hs, ws, r->dw_w[b], r->dw_b[b], m->d_b);
+            ops_conv1x1(o, m->d_b, 0, r->cp, n, r->pw_w[b], r->pw_b[b], r->cp,
+                        m->d_a, 0, ACT_NONE, 0);
+        }
+    ops_conv1x1(o, src, 0, r->cp, n, r->out_w, r->out_b, r->nout, m->d_c, 0,
                 ACT_NONE, 0);
 }
 

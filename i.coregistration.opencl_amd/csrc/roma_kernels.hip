@@ -1166,6 +1166,146 @@ extern "C" void roma2_update(struct ops *o, cl_mem flow, cl_mem conf, cl_mem d,
     ICOREG_API_END
 }
 
+/* A refiner block on C <= 32 channels (C % 8 == 0) in one pass: the
+ * depthwise 5 x 5 + bias + ReLU of dwconv5_kernel (same tap order), then
+ * the 1 x 1 convolution (pw: C x C, row k for output channel k; pb) that
+ * follows it, the depthwise results kept in registers instead of a
+ * C x H x W map written and read back. A block takes 64 columns (one a
+ * lane) x 8 rows (two a thread); the input patch goes through LDS four
+ * channels at a time, the next four loaded into registers meanwhile; the
+ * weights are uniform across the block (scalar loads). */
+#define DP_TW 64
+#define DP_TH 8
+#define DP_CC 4
+template <int C>
+__global__ void __launch_bounds__(256)
+    dwpw_small_kernel(const float *__restrict__ in, int H, int W,
+                      const float *__restrict__ dw, const float *__restrict__ db,
+                      const float *__restrict__ pw, const float *__restrict__ pb,
+                      float *__restrict__ out)
+{
+    constexpr int TR = 2, PR = DP_TH + 4, PC = DP_TW + 4, PN = DP_CC * PR * PC;
+    constexpr int NP = (PN + 255) / 256;
+    static_assert(C % DP_CC == 0 && C <= 32, "channels");
+    __shared__ float patch[DP_CC][PR][PC + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int x0 = blockIdx.x * DP_TW, y0 = blockIdx.y * DP_TH, ry = wave * TR;
+    const long long HW = (long long)H * W;
+    float acc[TR][C], rp[NP];
+
+#pragma unroll
+    for (int p = 0; p < TR; p++)
+#pragma unroll
+        for (int k = 0; k < C; k++)
+            acc[p][k] = 0.0f;
+    /* The patch of channels c0 .. c0 + 3 into registers (zero outside the
+     * map). */
+    auto fetch = [&](int c0) {
+#pragma unroll
+        for (int q = 0; q < NP; q++) {
+            const int e = tid + 256 * q, cc = e / (PR * PC), rem = e - cc * (PR * PC);
+            const int r = rem / PC, col = rem - r * PC;
+            const int gy = y0 + r - 2, gx = x0 + col - 2;
+            const bool ok = e < PN && gy >= 0 && gy < H && gx >= 0 && gx < W;
+
+            rp[q] = ok ? in[(c0 + cc) * HW + (long long)gy * W + gx] : 0.0f;
+        }
+    };
+    fetch(0);
+    for (int c0 = 0; c0 < C; c0 += DP_CC) {
+#pragma unroll
+        for (int q = 0; q < NP; q++) {
+            const int e = tid + 256 * q, cc = e / (PR * PC), rem = e - cc * (PR * PC);
+
+            if (e < PN)
+                patch[cc][rem / PC][rem % PC] = rp[q];
+        }
+        __syncthreads();
+        if (c0 + DP_CC < C)
+            fetch(c0 + DP_CC);
+#pragma unroll
+        for (int cc = 0; cc < DP_CC; cc++) {
+            const int c = c0 + cc;
+            float win[TR + 4][5];
+
+#pragma unroll
+            for (int i = 0; i < TR + 4; i++)
+#pragma unroll
+                for (int j = 0; j < 5; j++)
+                    win[i][j] = patch[cc][ry + i][lane + j];
+#pragma unroll
+            for (int p = 0; p < TR; p++) {
+                float a = db[c];
+
+#pragma unroll
+                for (int i = 0; i < 5; i++)
+#pragma unroll
+                    for (int j = 0; j < 5; j++)
+                        a = fmaf(win[p + i][j], dw[c * 25 + i * 5 + j], a);
+                a = fmaxf(a, 0.0f);
+#pragma unroll
+                for (int k = 0; k < C; k++)
+                    acc[p][k] = fmaf(pw[k * C + c], a, acc[p][k]);
+            }
+        }
+        __syncthreads();
+    }
+    const int x = x0 + lane;
+
+#pragma unroll
+    for (int p = 0; p < TR; p++) {
+        const int yy = y0 + ry + p;
+
+        if (x < W && yy < H)
+#pragma unroll
+            for (int k = 0; k < C; k++)
+                out[k * HW + (long long)yy * W + x] = acc[p][k] + pb[k];
+    }
+}
+
+extern "C" void roma_dwpw_small(struct ops *o, cl_mem in, int C, int H, int W, cl_mem dw,
+                                cl_mem db, cl_mem pw, cl_mem pb, cl_mem out)
+{
+    ICOREG_API_BEGIN
+    const char *op = "roma_dwpw_small";
+
+    if (C < 8 || C > 32 || C % 8 != 0 || H < 1 || W < 1)
+        icoreg_fatal("%s: invalid sizes C=%d H=%d W=%d (C one of 8, 16, 24, 32)", op, C, H, W);
+    count32((long long)C * H * W, op);
+    need_floats(in, 0, (long long)C * H * W, op, "in");
+    need_floats(dw, 0, 25LL * C, op, "dw");
+    need_floats(db, 0, C, op, "db");
+    need_floats(pw, 0, (long long)C * C, op, "pw");
+    need_floats(pb, 0, C, op, "pb");
+    need_floats(out, 0, (long long)C * H * W, op, "out");
+    if (in == out || (in->ptr == out->ptr))
+        icoreg_fatal("%s: in and out must not overlap", op);
+    prof_scope ps(o->ocl, op);
+    const dim3 grid(nblk(W, DP_TW), nblk(H, DP_TH));
+    hipStream_t s = stream_of(o->ocl);
+
+    switch (C) {
+    case 8:
+        hipLaunchKernelGGL(dwpw_small_kernel<8>, grid, dim3(256), 0, s, cfptr(in), H, W,
+                           cfptr(dw), cfptr(db), cfptr(pw), cfptr(pb), fptr(out));
+        break;
+    case 16:
+        hipLaunchKernelGGL(dwpw_small_kernel<16>, grid, dim3(256), 0, s, cfptr(in), H, W,
+                           cfptr(dw), cfptr(db), cfptr(pw), cfptr(pb), fptr(out));
+        break;
+    case 24:
+        hipLaunchKernelGGL(dwpw_small_kernel<24>, grid, dim3(256), 0, s, cfptr(in), H, W,
+                           cfptr(dw), cfptr(db), cfptr(pw), cfptr(pb), fptr(out));
+        break;
+    default:
+        hipLaunchKernelGGL(dwpw_small_kernel<32>, grid, dim3(256), 0, s, cfptr(in), H, W,
+                           cfptr(dw), cfptr(db), cfptr(pw), cfptr(pb), fptr(out));
+        break;
+    }
+    launch_check(op);
+    ICOREG_API_END
+}
+
 extern "C" void roma_dwconv5(struct ops *o, cl_mem in, int C, int H, int W,
                              cl_mem w, cl_mem bias, cl_mem out)
 {

@@ -148,6 +148,14 @@ void roma2_update(struct ops *o, cl_mem flow, cl_mem conf, cl_mem d, int n,
 void roma_dwconv5(struct ops *o, cl_mem in, int C, int H, int W, cl_mem w,
                   cl_mem bias, cl_mem out);
 
+/* No counterpart among the reference's kernels: a refiner block on C = 8,
+ * 16, 24 or 32 channels in one pass, out = pw (C x C) relu(dw5(in) + db)
+ * + pb, the same result as roma_dwconv5 followed by ops_conv1x1 (to
+ * float32 rounding) without the intermediate map. in and out must not
+ * overlap. */
+void roma_dwpw_small(struct ops *o, cl_mem in, int C, int H, int W, cl_mem dw,
+                     cl_mem db, cl_mem pw, cl_mem pb, cl_mem out);
+
 /* ---- DISK (disk_kernels.cl) -------------------------------------------- */
 
 /* Keypoint candidates of the heatmap (float offset off of heat, row

@@ -201,6 +201,33 @@ def test_dwconv5(dev, ic, orc, C, H, W):
     assert rel(dev.read(bo), ref) < TOL
 
 
+@pytest.mark.parametrize("C,H,W", [(24, 108, 108), (32, 70, 97), (8, 9, 65), (16, 1, 3)])
+def test_dwpw_small(dev, ic, orc, C, H, W):
+    """The fused refiner block (roma_dwpw_small) against the oracle's
+    depthwise 5 x 5 followed by the 1 x 1 in float64 (numpy), and against
+    the library's own two-kernel path (roma_dwconv5, ops_conv1x1)."""
+    print(f"[roma] dwpw_small C={C} {H}x{W}", flush=True)
+    rng = np.random.default_rng(C * H + W)
+    x = rng.standard_normal((C, H, W)).astype(np.float32)
+    w = rng.standard_normal((C, 25)).astype(np.float32)
+    b = rng.standard_normal(C).astype(np.float32)
+    pw = (rng.standard_normal((C, C)) / np.sqrt(C)).astype(np.float32)
+    pb = rng.standard_normal(C).astype(np.float32)
+    z = np.zeros((C, H, W), np.float32)
+    orc.orc_roma_dwconv5(fp(x), C, H, W, fp(w), fp(b), fp(z))
+    ref = (pw.astype(np.float64) @ z.reshape(C, -1).astype(np.float64)
+           + pb.astype(np.float64)[:, None]).reshape(C, H, W)
+    bx, bw, bb = dev.upload(x), dev.upload(w), dev.upload(b)
+    bpw, bpb, bo = dev.upload(pw), dev.upload(pb), dev.zeros(C * H * W)
+    dev.api.roma_dwpw_small(dev.po, bx.mem, C, H, W, bw.mem, bb.mem, bpw.mem, bpb.mem, bo.mem)
+    got = dev.read(bo).reshape(C, H, W)
+    assert rel(got, ref) < TOL
+    bz, b2 = dev.zeros(C * H * W), dev.zeros(C * H * W)
+    dev.api.roma_dwconv5(dev.po, bx.mem, C, H, W, bw.mem, bb.mem, bz.mem)
+    dev.api.ops_conv1x1(dev.po, bz.mem, 0, C, H * W, bpw.mem, bpb.mem, C, b2.mem, 0, 0, 0.0)
+    assert rel(got, dev.read(b2).reshape(C, H, W)) < TOL
+
+
 @pytest.mark.parametrize("H,W,h,w,nimg,imagenet", [
     (1024, 1024, 560, 560, 2, 1), (864, 864, 560, 560, 2, 1), (640, 480, 560, 560, 1, 0),
     (64, 64, 112, 112, 2, 1), (100, 70, 56, 84, 1, 1), (2048, 1000, 140, 112, 1, 0),
