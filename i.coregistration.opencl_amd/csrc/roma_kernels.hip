@@ -1192,24 +1192,32 @@ __global__ void __launch_bounds__(256)
     const int x0 = blockIdx.x * DP_TW, y0 = blockIdx.y * DP_TH, ry = wave * TR;
     const long long HW = (long long)H * W;
     float acc[TR][C], rp[NP];
+    /* This thread's patch elements: offset from channel c0's plane (cc HW
+     * + pixel), -1 outside the map; the same for every chunk. */
+    int so[NP];
 
 #pragma unroll
     for (int p = 0; p < TR; p++)
 #pragma unroll
         for (int k = 0; k < C; k++)
             acc[p][k] = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+        const int e = tid + 256 * q, cc = e / (PR * PC), rem = e - cc * (PR * PC);
+        const int r = rem / PC, col = rem - r * PC;
+        const int gy = y0 + r - 2, gx = x0 + col - 2;
+        const bool ok = e < PN && gy >= 0 && gy < H && gx >= 0 && gx < W;
+
+        so[q] = ok ? (int)(cc * HW + (long long)gy * W + gx) : -1;
+    }
     /* The patch of channels c0 .. c0 + 3 into registers (zero outside the
      * map). */
     auto fetch = [&](int c0) {
-#pragma unroll
-        for (int q = 0; q < NP; q++) {
-            const int e = tid + 256 * q, cc = e / (PR * PC), rem = e - cc * (PR * PC);
-            const int r = rem / PC, col = rem - r * PC;
-            const int gy = y0 + r - 2, gx = x0 + col - 2;
-            const bool ok = e < PN && gy >= 0 && gy < H && gx >= 0 && gx < W;
+        const float *base = in + c0 * HW;
 
-            rp[q] = ok ? in[(c0 + cc) * HW + (long long)gy * W + gx] : 0.0f;
-        }
+#pragma unroll
+        for (int q = 0; q < NP; q++)
+            rp[q] = so[q] >= 0 ? base[so[q]] : 0.0f;
     };
     fetch(0);
     for (int c0 = 0; c0 < C; c0 += DP_CC) {
@@ -1280,6 +1288,8 @@ extern "C" void roma_dwpw_small(struct ops *o, cl_mem in, int C, int H, int W, c
     need_floats(out, 0, (long long)C * H * W, op, "out");
     if (in == out || (in->ptr == out->ptr))
         icoreg_fatal("%s: in and out must not overlap", op);
+    if ((long long)DP_CC * H * W >= (1LL << 31))
+        icoreg_fatal("%s: %d x %d map too large", op, H, W);
     prof_scope ps(o->ocl, op);
     const dim3 grid(nblk(W, DP_TW), nblk(H, DP_TH));
     hipStream_t s = stream_of(o->ocl);
