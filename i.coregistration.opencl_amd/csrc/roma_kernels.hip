@@ -801,58 +801,74 @@ __global__ void __launch_bounds__(256)
 
 /* ---- depthwise 5 x 5 + bias + ReLU ----------------------------------------------------- */
 
-/* Depthwise 5 x 5 (+ bias, ReLU) of one channel plane per block tile:
- * 64 columns x 32 rows, one column per lane and 8 rows per thread. The
- * (36 x 68) input patch (1.2 times the tile, against 1.7 for a 32 x 8
- * tile) is loaded with every load issued before any is used, staged in
- * LDS, and each thread keeps the 12 x 5 neighbourhood of its 8 outputs in
- * registers, so each patch value is read from LDS about 1.2 times. Sums
- * in tap order, as the reference. */
+/* Depthwise 5 x 5 (+ bias, ReLU) over a block tile of 64 columns x 32
+ * rows, one column per lane and 8 rows per thread, for DW_CPB consecutive
+ * channel planes in turn. The (36 x 68) input patch (1.2 times the tile,
+ * against 1.7 for a 32 x 8 tile) is staged in LDS, and each thread keeps
+ * the 12 x 5 neighbourhood of its 8 outputs in registers, so each patch
+ * value is read from LDS about 1.2 times. The next channel's patch is
+ * loaded into registers while the current one is computed (prefetching
+ * two channels ahead needs 164 registers a thread and measured slower).
+ * Sums in tap order, as the reference. */
 #define DW_TW 64
 #define DW_RPT 8
 #define DW_TH (256 / DW_TW * DW_RPT)
 #define DW_PW (DW_TW + 4)
 #define DW_PH (DW_TH + 4)
 #define DW_NL ((DW_PW * DW_PH + 255) / 256)
+#define DW_CPB 4
 
 __global__ void __launch_bounds__(256)
-    dwconv5_kernel(const float *__restrict__ in, int H, int W,
+    dwconv5_kernel(const float *__restrict__ in, int C, int H, int W,
                    const float *__restrict__ wt, const float *__restrict__ bias,
                    float *__restrict__ out)
 {
     __shared__ float t[DW_PH][DW_PW + 1];
     const int lx = threadIdx.x % DW_TW, g = threadIdx.x / DW_TW;
-    const int x0 = blockIdx.x * DW_TW, y0 = blockIdx.y * DW_TH, c = blockIdx.z;
-    const float *p = in + (long long)c * H * W;
-    const float *w = wt + c * 25;
-    float v[DW_NL], nb[DW_RPT + 4][5], wk[25];
+    const int x0 = blockIdx.x * DW_TW, y0 = blockIdx.y * DW_TH;
+    const int cb = blockIdx.z * DW_CPB, ce = min(C, cb + DW_CPB);
+    const long long HW = (long long)H * W;
+    const int x = x0 + lx;
+    float v[DW_NL], nb[DW_RPT + 4][5];
+    /* This thread's patch elements: offset in a channel plane, -1 outside
+     * the map. */
+    int so[DW_NL];
 
 #pragma unroll
     for (int q = 0; q < DW_NL; q++) {
         const int e = threadIdx.x + 256 * q, yy = y0 - 2 + e / DW_PW, xx = x0 - 2 + e % DW_PW;
         const bool ok = e < DW_PW * DW_PH && yy >= 0 && yy < H && xx >= 0 && xx < W;
 
-        v[q] = p[ok ? (long long)yy * W + xx : 0];
-        v[q] = ok ? v[q] : 0.0f;
+        so[q] = ok ? yy * W + xx : -1;
     }
-#pragma unroll
-    for (int k = 0; k < 25; k++)
-        wk[k] = w[k];
-#pragma unroll
-    for (int q = 0; q < DW_NL; q++) {
-        const int e = threadIdx.x + 256 * q;
+    auto fetch = [&](int c) {
+        const float *p = in + c * HW;
 
-        if (e < DW_PW * DW_PH)
-            t[e / DW_PW][e % DW_PW] = v[q];
-    }
-    __syncthreads();
 #pragma unroll
-    for (int r = 0; r < DW_RPT + 4; r++)
+        for (int q = 0; q < DW_NL; q++)
+            v[q] = so[q] >= 0 ? p[so[q]] : 0.0f;
+    };
+    fetch(cb);
+    for (int c = cb; c < ce; c++) {
+        if (c > cb)
+            __syncthreads();
 #pragma unroll
-        for (int j = 0; j < 5; j++)
-            nb[r][j] = t[g * DW_RPT + r][lx + j];
-    {
-        const int x = x0 + lx;
+        for (int q = 0; q < DW_NL; q++) {
+            const int e = threadIdx.x + 256 * q;
+
+            if (e < DW_PW * DW_PH)
+                t[e / DW_PW][e % DW_PW] = v[q];
+        }
+        __syncthreads();
+        if (c + 1 < ce)
+            fetch(c + 1);
+#pragma unroll
+        for (int r = 0; r < DW_RPT + 4; r++)
+#pragma unroll
+            for (int j = 0; j < 5; j++)
+                nb[r][j] = t[g * DW_RPT + r][lx + j];
+
+        const float *w = wt + c * 25;
         const float b = bias[c];
 
 #pragma unroll
@@ -864,9 +880,9 @@ __global__ void __launch_bounds__(256)
             for (int i = 0; i < 5; i++)
 #pragma unroll
                 for (int j = 0; j < 5; j++)
-                    acc = fmaf(nb[r + i][j], wk[i * 5 + j], acc);
+                    acc = fmaf(nb[r + i][j], w[i * 5 + j], acc);
             if (x < W && y < H)
-                out[((long long)c * H + y) * W + x] = fmaxf(acc, 0.0f);
+                out[c * HW + (long long)y * W + x] = fmaxf(acc, 0.0f);
         }
     }
 }
@@ -1331,8 +1347,8 @@ extern "C" void roma_dwconv5(struct ops *o, cl_mem in, int C, int H, int W,
     need_floats(out, 0, (long long)C * H * W, op, "out");
     prof_scope ps(o->ocl, op);
     hipLaunchKernelGGL(dwconv5_kernel,
-                       dim3(nblk(W, DW_TW), nblk(H, DW_TH), (unsigned)C),
-                       dim3(256), 0, stream_of(o->ocl), cfptr(in), H, W,
+                       dim3(nblk(W, DW_TW), nblk(H, DW_TH), nblk(C, DW_CPB)),
+                       dim3(256), 0, stream_of(o->ocl), cfptr(in), C, H, W,
                        cfptr(w), cfptr(bias), fptr(out));
     launch_check(op);
     ICOREG_API_END

@@ -187,7 +187,7 @@ def test_disp_updates(dev, ic, orc):
     assert rel(dev.read(bc2), rc2) < TOL
 
 
-@pytest.mark.parametrize("C,H,W", [(5, 37, 70), (64, 140, 140), (2, 3, 4)])
+@pytest.mark.parametrize("C,H,W", [(5, 37, 70), (64, 140, 140), (2, 3, 4), (9, 108, 108)])
 def test_dwconv5(dev, ic, orc, C, H, W):
     print(f"[roma] dwconv5 C={C} {H}x{W}", flush=True)
     rng = np.random.default_rng(C * H)
