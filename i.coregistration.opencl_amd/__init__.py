@@ -164,6 +164,8 @@ SIGNATURES = {
     "eloftr_col_lse": (None, [_O, Mem, _I, _I, Mem, Mem]),
     "eloftr_conf_row": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
     "eloftr_conf_col": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
+    "eloftr_lse_block": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem]),
+    "eloftr_conf_block": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem, Mem, Mem]),
     "eloftr_fine": (None, [_O, Mem, Mem, _I, _I, Mem, _I, _F, Mem]),
     "eloftr_fine_half": (None, [_O, Mem, Mem, _I, _I, Mem, _I, _F, Mem]),
     "eloftr_fine_half_count": (None, [_O, Mem, Mem, _I, _I, Mem, Mem, _I, _F, Mem]),
@@ -180,6 +182,7 @@ SIGNATURES = {
     "roma_dwpw_small": (None, [_O, Mem, _I, _I, _I, Mem, Mem, Mem, Mem, Mem]),
     "roma_gp_work_bytes": (C.c_size_t, [_I, _I]),
     "roma_gp_solve": (None, [_O, Mem, _I, _F, Mem, _I, Mem, Mem]),
+    "roma_gp_solve_events": (None, [_O, Mem, _I, _F, Mem, _I, Mem, Mem]),
     "roma_prepare": (None, [_O, Mem, _I, _I, _I, Mem, _I, _I, _I]),
     "roma_epilogue": (None, [_O, Mem, Mem, Mem, _L]),
     "roma_sd": (None, [_O, Mem, _L, Mem, _L]),
@@ -227,6 +230,8 @@ SIGNATURES = {
     "icoreg_roma_gp_info": (_I, [_P]),
     "icoreg_roma_last": (_I, [_P]),
     "icoreg_roma_set_imagenet": (None, [_P, _I]),
+    "icoreg_gp_test_wait": (None, [_I, _I]),
+    "icoreg_roma_gp_retries": (_I, [_P]),
 }
 
 # Entry points that never raise through the fatal path (no error check).
@@ -240,7 +245,8 @@ _NO_CHECK = {"ocl_graph_free", "icoreg_set_fatal_mode", "icoreg_last_error", "ic
              "icoreg_eloftr_set_pos_scale", "icoreg_eloftr_buffer", "roma_gp_work_bytes",
              "icoreg_roma_new", "icoreg_roma_result", "icoreg_roma_buffer",
              "icoreg_roma_set_imagenet", "icoreg_disk_new", "icoreg_disk_buffer",
-             "icoreg_roma_last", "disk_topn_work_bytes", "adalam_nearest_work_bytes"}
+             "icoreg_roma_last", "disk_topn_work_bytes", "adalam_nearest_work_bytes",
+             "icoreg_gp_test_wait", "icoreg_roma_gp_retries"}
 
 _lib = None
 
@@ -525,6 +531,11 @@ class Roma:
 
     def gp_info(self):
         return lib().icoreg_roma_gp_info(self.m)
+
+    def gp_retries(self):
+        """GP solves roma_match re-ran with event waits after the solve's
+        in-kernel wait gave up."""
+        return lib().icoreg_roma_gp_retries(self.m)
 
     def close(self):
         if self.m:

@@ -136,6 +136,8 @@ extern "C" cl_mem icoreg_roma_buffer(const struct roma_model *m,
 
 extern "C" int icoreg_roma_last(const struct roma_model *m) { return m->last; }
 
+extern "C" int icoreg_roma_gp_retries(const struct roma_model *m) { return m->gp_retries; }
+
 extern "C" int icoreg_roma_gp_info(struct roma_model *m)
 {
     int info = 0;

@@ -223,7 +223,7 @@ typedef double gp_d4 __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(1024)
     chol_diag_kernel(const double *__restrict__ A, double *__restrict__ L,
                      double *__restrict__ Linv, int n, int k, int nb,
-                     const double *__restrict__ lprev, const int *ready,
+                     const double *__restrict__ lprev, const int *ready, int spin_max,
                      int *__restrict__ info)
 {
     __shared__ double s[GP_NB][GP_NB + 1], f[GP_NB][GP_NB + 1];
@@ -243,9 +243,9 @@ __global__ void __launch_bounds__(1024)
             int it = 0;
 
             while (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
-                   ++it < GP_SPIN_MAX)
+                   ++it < spin_max)
                 __builtin_amdgcn_s_sleep(1);
-            if (it >= GP_SPIN_MAX)
+            if (it >= spin_max)
                 bad = -1;
         }
         __syncthreads();
@@ -496,11 +496,25 @@ extern "C" size_t roma_gp_work_bytes(int n, int d)
            sizeof(int) * nblk;
 }
 
-extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
-                              cl_mem F, int d, cl_mem work, cl_mem info)
+/* Test hooks (icoreg_gp_test_wait): the in-kernel wait's poll limit and
+ * whether the second stream sets the panel flags at all. With the flags
+ * never set and a short limit, every waiting diagonal kernel gives up at
+ * once (info = -1) and still exits, so the give-up path and the caller's
+ * recovery can be exercised without a stalled stream. */
+static int g_spin_max = GP_SPIN_MAX;
+static int g_set_flags = 1;
+
+extern "C" void icoreg_gp_test_wait(int spin_max, int set_flags)
 {
-    ICOREG_API_BEGIN
-    const char *op = "roma_gp_solve";
+    g_spin_max = spin_max > 0 ? spin_max : GP_SPIN_MAX;
+    g_set_flags = set_flags != 0;
+}
+
+/* events: the diagonal kernels wait through stream events (the form a
+ * capture needs, and the fallback when the in-kernel wait gave up). */
+static void gp_solve_run(struct ops *o, cl_mem K, int n, float noise, cl_mem F, int d,
+                         cl_mem work, cl_mem info, bool events, const char *op)
+{
     hipStream_t s;
     double *A, *L, *Li, *Z, *Y, *X;
     int *flags;
@@ -530,7 +544,8 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
 
         hip_check(hipStreamIsCapturing(s, &cs), "hipStreamIsCapturing");
-        const bool capture = cs != hipStreamCaptureStatusNone;
+        const bool capture = events || cs != hipStreamCaptureStatusNone;
+        const int spin_max = g_spin_max;
 
         hipLaunchKernelGGL(gp_init_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s,
                            cfptr(K), n, (double)noise, A, cfptr(F), d, Z, X, (int *)info->ptr,
@@ -560,15 +575,17 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
                     hip_check(hipStreamWaitEvent(s, aux_event(o->ocl, 2 * (b - 2) + 1), 0),
                               "hipStreamWaitEvent");
                 hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(1024), 0, s, A,
-                                   L, Lk, n, k, nb, lprev, (const int *)nullptr, info_p);
+                                   L, Lk, n, k, nb, lprev, (const int *)nullptr, spin_max,
+                                   info_p);
                 hip_check(hipEventRecord(done_b, s), "hipEventRecord");
             }
             else {
                 /* The launch's completion signals done_b itself: no
                  * separate record on s. */
                 const int *ready = b >= 2 ? flags + b - 2 : nullptr;
-                void *args[] = {(void *)&A, (void *)&L,     (void *)&Lk,    (void *)&n,
-                                (void *)&k, (void *)&nb,    (void *)&lprev, (void *)&ready,
+                void *args[] = {(void *)&A,  (void *)&L,     (void *)&Lk,
+                                (void *)&n,  (void *)&k,     (void *)&nb,
+                                (void *)&lprev, (void *)&ready, (void *)&spin_max,
                                 (void *)&info_p};
 
                 hip_check(hipExtLaunchKernel((const void *)chol_diag_kernel, dim3(1), dim3(1024),
@@ -600,7 +617,7 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
             }
             else
                 dgemm(s2, {&xacc});
-            if (!capture)
+            if (!capture && g_set_flags)
                 hipLaunchKernelGGL(gp_mark_kernel, dim3(1), dim3(64), 0, s2, flags + b);
             if (capture || b == nblk - 1)
                 hip_check(hipEventRecord(aux_event(o->ocl, 2 * b + 1), s2), "hipEventRecord");
@@ -611,5 +628,20 @@ extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
                            (const double *)X, nd, fptr(F));
     }
     launch_check(op);
+}
+
+extern "C" void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise,
+                              cl_mem F, int d, cl_mem work, cl_mem info)
+{
+    ICOREG_API_BEGIN
+    gp_solve_run(o, K, n, noise, F, d, work, info, false, "roma_gp_solve");
+    ICOREG_API_END
+}
+
+extern "C" void roma_gp_solve_events(struct ops *o, cl_mem K, int n, float noise,
+                                     cl_mem F, int d, cl_mem work, cl_mem info)
+{
+    ICOREG_API_BEGIN
+    gp_solve_run(o, K, n, noise, F, d, work, info, true, "roma_gp_solve_events");
     ICOREG_API_END
 }

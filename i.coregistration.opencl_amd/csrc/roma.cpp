@@ -747,6 +747,22 @@ static void dino_pair(struct roma_model *m, cl_mem pair)
  * kernels, F = (K_yy + 0.1 I)^-1 basis on the device, mu = K_xy F into
  * t_x columns 0..511 and A's tokens into columns 512..1023 (the
  * decoder's input). */
+/* The GP solve on the basis (K_yy, already formed) and the posterior
+ * mean mu = K_xy F into the decoder input's first GP_DIM columns; events:
+ * roma_gp_solve_events instead of roma_gp_solve. */
+static void gp_posterior(struct roma_model *m, bool events)
+{
+    struct ops *o = m->ops;
+    const int n16 = m->n16;
+
+    ocl_copy(m->ocl, m->gp_basis, 0, m->g_f, 0, (size_t)n16 * GP_DIM * 4);
+    (events ? roma_gp_solve_events : roma_gp_solve)(o, m->g_kyy, n16, GP_NOISE, m->g_f,
+                                                    GP_DIM, m->gp_work, m->gp_info);
+    ops_gemm(o, n16, GP_DIM, n16, ops_mat(m->g_kxy, 0, n16),
+             ops_mat(m->g_f, 0, GP_DIM), 0, ops_mat(m->t_x, 0, ROMA_DEC_DIM),
+             1, 1, NULL, 0, NULL, 0, 1.0f, ACT_NONE, 0);
+}
+
 static void gp(struct roma_model *m)
 {
     struct ops *o = m->ops;
@@ -768,12 +784,7 @@ static void gp(struct roma_model *m)
              ops_mat(m->g_y, gb, GP_DIM), 1, ops_mat(m->g_kxy, 0, n16), 1, 1,
              NULL, 0, NULL, 0, 1.0f, ACT_NONE, 0);
     roma_cos_exp(o, m->g_kxy, m->g_nx, m->g_ny, n16, n16, GP_T, COS_EPS);
-    ocl_copy(m->ocl, m->gp_basis, 0, m->g_f, 0, (size_t)gb * 4);
-    roma_gp_solve(o, m->g_kyy, n16, GP_NOISE, m->g_f, GP_DIM, m->gp_work,
-                  m->gp_info);
-    ops_gemm(o, n16, GP_DIM, n16, ops_mat(m->g_kxy, 0, n16),
-             ops_mat(m->g_f, 0, GP_DIM), 0, ops_mat(m->t_x, 0, ROMA_DEC_DIM),
-             1, 1, NULL, 0, NULL, 0, 1.0f, ACT_NONE, 0);
+    gp_posterior(m, false);
     ocl_copy_rect(m->ocl, m->g_y, 0, GP_DIM * 4, m->t_x, GP_DIM * 4,
                   ROMA_DEC_DIM * 4, GP_DIM * 4, n16);
 }
@@ -792,14 +803,22 @@ static void decoder(struct roma_model *m)
                      m->fl[0], m->ce[0]);
 }
 
+/* The GP status once the stream has run. If a diagonal block's
+ * in-kernel wait gave up (info = -1: the solve's second stream could not
+ * run beside it), the solve and the posterior are run again with stream
+ * event waits, which cannot give up. */
 static void gp_check(struct roma_model *m)
 {
     int info = 0;
 
     ocl_read(m->ocl, m->gp_info, 0, &info, sizeof(info));
-    if (info < 0)
-        icoreg_fatal("RoMa: Gaussian process solve: a diagonal block's wait for "
-                     "its trailing update gave up");
+    if (info < 0) {
+        m->gp_retries++;
+        gp_posterior(m, true);
+        ocl_read(m->ocl, m->gp_info, 0, &info, sizeof(info));
+        if (info < 0)
+            icoreg_fatal("RoMa: Gaussian process solve: internal wait failed");
+    }
     if (info)
         icoreg_fatal("RoMa: Gaussian process kernel not positive definite "
                      "(column %d)",

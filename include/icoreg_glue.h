@@ -71,6 +71,16 @@ int icoreg_roma_last(const struct roma_model *m);
 
 void icoreg_roma_set_imagenet(struct roma_model *m, int on);
 
+/* Test hooks of the GP solve's in-kernel wait (roma_gp_solve): its poll
+ * limit (0: the default, about 0.1 s) and whether the panel flags are set
+ * at all (0: never, so every waiting diagonal kernel gives up after
+ * spin_max polls and reports info = -1). Process-wide; for tests of the
+ * give-up path and of roma_match's recovery. */
+void icoreg_gp_test_wait(int spin_max, int set_flags);
+/* How many times roma_match has re-run a GP solve through
+ * roma_gp_solve_events after the in-kernel wait gave up. */
+int icoreg_roma_gp_retries(const struct roma_model *m);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,19 @@ void eloftr_conf_row(struct ops *o, cl_mem S, int rows, int N, int r0,
 void eloftr_conf_col(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse,
                      cl_mem cm, cl_mem cs, cl_mem cmax, cl_mem carg);
 
+/* The form eloftr_match runs (no counterpart among the reference's
+ * kernels, which launch the four above one after the other): the first
+ * pass of a block, eloftr_row_lse and eloftr_col_lse in one read of S,
+ * and the second, eloftr_conf_row and eloftr_conf_col in one read of S;
+ * same arguments, states and results. With r0 == 0 the column state
+ * (cm, cs; cmax, carg) is started by the call itself, with no prior fill.
+ * N % 4 == 0 and S 16-byte aligned. */
+void eloftr_lse_block(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse,
+                      cl_mem cm, cl_mem cs);
+void eloftr_conf_block(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse,
+                       cl_mem cm, cl_mem cs, cl_mem rmax, cl_mem rarg, cl_mem cmax,
+                       cl_mem carg);
+
 /* Two-stage fine matching of M coarse matches: f0, f1 (64, H, W) fine
  * features, cells (int4: x0, y0, x1, y1 per match), T the second-stage
  * temperature, out (float4: x0, y0, x1, y1 per match, the reference's
@@ -198,13 +211,26 @@ void disk_gather_desc_count(struct ops *o, cl_mem feat, int H, int W, int D,
  * triangle read). work holds roma_gp_work_bytes(n, d) bytes; info (one
  * int, cleared by the call) gets 1 + the first column whose pivot is
  * not positive, the reference's "not positive definite" failure, for
- * the caller to check once the stream has run (-1: an internal wait
- * between the solve's two streams gave up, which does not happen when the
- * device runs the launches). The call runs on the library's stream and
- * on its second stream (joined back before it returns to the stream). */
+ * the caller to check once the stream has run. The call runs on the
+ * library's stream and on its second stream (joined back before it
+ * returns to the stream). Each diagonal block waits inside its kernel for
+ * the other stream's trailing update; that wait is bounded (about 0.1 s),
+ * and info = -1 reports that it gave up, which can happen only if the
+ * other stream's work could not run meanwhile (both streams of two
+ * concurrent solves mapped onto shared hardware queues, or a GPU
+ * time-sliced away for that long). The result is then not valid: F has
+ * been overwritten, so the caller restores it and calls
+ * roma_gp_solve_events, as roma_match does. */
 size_t roma_gp_work_bytes(int n, int d);
 void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise, cl_mem F,
                    int d, cl_mem work, cl_mem info);
+/* The same solve with the diagonal blocks waiting through stream events
+ * (no in-kernel wait, so info is never -1): the form used under stream
+ * capture, and the fallback after info = -1. Same arithmetic and results;
+ * about 0.1 ms slower at n = 1600 (the command processor's event waits on
+ * the critical path). */
+void roma_gp_solve_events(struct ops *o, cl_mem K, int n, float noise,
+                          cl_mem F, int d, cl_mem work, cl_mem info);
 
 #ifdef __cplusplus
 }

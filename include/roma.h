@@ -108,6 +108,7 @@ struct roma_model {
     float *flow, *cert, *sd;
     cl_mem raw; /* 2 x 3 x H x W: the pair as given, resampled on the device */
     int last;           /* fl / ce index holding roma_refine_device's result */
+    int gp_retries;     /* GP solves re-run after the in-kernel wait gave up */
 };
 
 /* Read the weights: RoMa's RegressionMatcher state dict (names as

@@ -71,6 +71,41 @@ def test_gp_solve_reports_indefinite(dev, ic):
     assert dev.read(info, 1, np.int32)[0] == 1
 
 
+def test_gp_solve_wait_gives_up_and_events_form(dev, ic):
+    """The diagonal kernels' bounded in-kernel wait forced to give up from
+    the host (icoreg_gp_test_wait: the panel flags never set, 64 polls):
+    every launch still exits, info is -1; roma_gp_solve_events (stream
+    event waits) on the same inputs gives the solution, and with the
+    default hooks both forms give the same bits."""
+    print("[roma] gp_solve forced give-up, n=300 d=64", flush=True)
+    lib = ic.lib()
+    n, d = 300, 64  # 5 panels: diagonal blocks 2, 3, 4 wait
+    rng = np.random.default_rng(3)
+    K = cos_kernel(rng, n)
+    F = rng.standard_normal((n, d)).astype(np.float32)
+    ref = np.linalg.solve(K.astype(np.float64) + 0.1 * np.eye(n), F.astype(np.float64))
+    bK = dev.upload(K)
+    work = dev.alloc(int(dev.api.roma_gp_work_bytes(n, d)))
+    info = dev.zeros(1, np.int32)
+    lib.icoreg_gp_test_wait(64, 0)
+    try:
+        bF = dev.upload(F)
+        dev.api.roma_gp_solve(dev.po, bK.mem, n, 0.1, bF.mem, d, work.mem, info.mem)
+        dev.finish()
+        assert dev.read(info, 1, np.int32)[0] == -1
+        bF = dev.upload(F)
+        dev.api.roma_gp_solve_events(dev.po, bK.mem, n, 0.1, bF.mem, d, work.mem, info.mem)
+        ev = dev.read(bF).reshape(n, d)
+        assert dev.read(info, 1, np.int32)[0] == 0
+        assert rel(ev, ref) < 1e-5
+    finally:
+        lib.icoreg_gp_test_wait(0, 1)
+    bF = dev.upload(F)
+    dev.api.roma_gp_solve(dev.po, bK.mem, n, 0.1, bF.mem, d, work.mem, info.mem)
+    assert dev.read(info, 1, np.int32)[0] == 0
+    assert np.array_equal(dev.read(bF).reshape(n, d), ev)
+
+
 @pytest.fixture(scope="module")
 def weights(tmp_path_factory):
     d = tmp_path_factory.mktemp("roma_w")
@@ -273,6 +308,32 @@ def test_roma_v2ref_1024_properties(dev, ic, weights):
     assert np.isfinite(cert).all() and ((cert >= 0) & (cert <= 1)).all()
     ok = np.isfinite(sd)
     assert ok.mean() > 0.99 and (sd[ok] > 0).all()
+
+
+def test_roma_match_recovers_from_gp_give_up(dev, ic, weights):
+    """roma_match with the GP solve's in-kernel wait forced to give up
+    (coarse 168: 144 tokens, 3 panels, diagonal block 2 waits): it re-runs
+    the solve with stream event waits and returns the same warp and
+    certainty bit for bit as an undisturbed run."""
+    print("[roma] match with a forced GP give-up, coarse=168 tile=64", flush=True)
+    (fm, fd, _), _ = weights
+    a, b, _ = synth.roma_pair(TILE, TILE)
+    lib = ic.lib()
+    out = []
+    for forced in (False, True):
+        net = ic.Roma(dev, fm, fd, TILE, TILE, coarse=168)
+        try:
+            if forced:
+                lib.icoreg_gp_test_wait(64, 0)
+            out.append(net.match(a, b))
+            assert net.gp_retries() == int(forced)
+            assert net.gp_info() == 0
+        finally:
+            lib.icoreg_gp_test_wait(0, 1)
+            net.close()
+    for k in ("flow", "cert"):
+        assert np.isfinite(out[0][k]).all()
+        assert np.array_equal(out[0][k], out[1][k]), k
 
 
 def test_coarse_graph_replays_match_eager(dev, ic, weights):
