@@ -315,11 +315,13 @@ void open_safetensors(const file_ref &f, std::vector<struct pth_tensor> &ts)
                              "offsets",
                              path, name.c_str());
             const size_t esz = st_dtype(dtype, &t.dtype);
-            long n = 1;
+            long long n = 1, nb = 0;
+            bool wrap = false;
 
             for (int d = 0; d < t.ndim; d++)
-                n *= t.shape[d];
-            if ((size_t)n * esz != (size_t)(o1 - o0) || data0 + o1 > f.size)
+                wrap |= __builtin_mul_overflow(n, (long long)t.shape[d], &n);
+            wrap |= __builtin_mul_overflow(n, (long long)esz, &nb);
+            if (wrap || nb != o1 - o0 || data0 + o1 > f.size)
                 icoreg_fatal("Checkpoint <%s>: tensor <%s> size does not match "
                              "its shape",
                              path, name.c_str());
@@ -1065,7 +1067,12 @@ void index_tensors(const file_ref &f, const val &sd,
             icoreg_fatal("Checkpoint <%s>: storage <%s> of tensor <%s> is missing",
                          path, tv->storage->s.c_str(), key->s.c_str());
         struct pth_tensor t;
-        long long last = tv->offset;
+        long long last = tv->offset, numel = 1, ext, end;
+        /* Shape, strides and offset come from the file: every extent is
+         * computed with overflow checks, so that a crafted entry cannot
+         * wrap past the storage bound below and index outside it later
+         * (pth_read_f32's strided gather). */
+        bool wrap = false;
 
         memset(&t, 0, sizeof(t));
         t.ndim = (int)tv->shape.size();
@@ -1078,12 +1085,17 @@ void index_tensors(const file_ref &f, const val &sd,
                 icoreg_fatal("Checkpoint <%s>: empty or negatively strided tensor "
                              "<%s>",
                              path, key->s.c_str());
-            last += (long long)(t.shape[d] - 1) * t.stride[d];
+            wrap |= __builtin_mul_overflow((long long)t.shape[d] - 1, (long long)t.stride[d],
+                                           &ext);
+            wrap |= __builtin_add_overflow(last, ext, &last);
+            wrap |= __builtin_mul_overflow(numel, (long long)t.shape[d], &numel);
         }
         t.data_offset = (long)it->second.off;
         t.storage_bytes = (size_t)it->second.bytes;
-        if (tv->offset < 0 ||
-            (last + 1) * (long long)elem_bytes(t.dtype) > it->second.bytes)
+        wrap |= __builtin_add_overflow(last, 1LL, &end);
+        wrap |= __builtin_mul_overflow(end, (long long)elem_bytes(t.dtype), &end);
+        wrap |= __builtin_mul_overflow(numel, (long long)sizeof(float), &ext);
+        if (wrap || tv->offset < 0 || end > it->second.bytes)
             icoreg_fatal("Checkpoint <%s>: tensor <%s> exceeds its storage", path,
                          key->s.c_str());
         t.name = strdup(key->s.c_str());

@@ -190,6 +190,50 @@ def test_bad_files_are_fatal_with_a_reason(ic, tmp_path):
     _raises(ic, p, "no state_dict")
 
 
+def _craft_zip(path, size, stride, nfloats=8):
+    """A torch.save-style zip archive written by hand: data.pkl holds
+    {"w": _rebuild_tensor_v2(storage "0" of nfloats floats, offset 0,
+    size, stride)}; the shape and strides are whatever is given."""
+    import collections
+    import pickle
+
+    class Storage:
+        pass
+
+    class Tensor:
+        def __reduce__(self):
+            return (torch._utils._rebuild_tensor_v2,
+                    (Storage(), 0, tuple(size), tuple(stride), False,
+                     collections.OrderedDict()))
+
+    class Pickler(pickle.Pickler):
+        def persistent_id(self, obj):
+            if isinstance(obj, Storage):
+                return ("storage", torch.FloatStorage, "0", "cpu", nfloats)
+            return None
+
+    b = io.BytesIO()
+    Pickler(b, protocol=2).dump({"w": Tensor()})
+    with zipfile.ZipFile(path, "w", zipfile.ZIP_STORED) as z:
+        z.writestr("archive/data.pkl", b.getvalue())
+        z.writestr("archive/data/0", np.arange(nfloats, dtype=np.float32).tobytes())
+        z.writestr("archive/version", "3\n")
+    return path
+
+
+def test_overflowing_shape_and_stride_are_rejected(ic, tmp_path):
+    """Extents computed from a file's shape and strides are checked for
+    overflow: 4 x (2^62 + 1) wraps to 4 in 64-bit arithmetic, which would
+    pass the storage bound (5 floats of 8) and then index far outside it
+    in the strided gather. A well-formed hand-written archive reads."""
+    ok = _craft_zip(tmp_path / "ok.pth", (2, 4), (1, 2))
+    got, _ = load(ic, ok)
+    assert np.array_equal(got["w"], np.arange(8, dtype=np.float32).reshape(4, 2).T)
+    _raises(ic, _craft_zip(tmp_path / "wrap.pth", (5,), (2 ** 62 + 1,)), "exceeds its storage")
+    _raises(ic, _craft_zip(tmp_path / "numel.pth", (2 ** 32, 2 ** 32), (0, 0)),
+            "exceeds its storage")
+
+
 def test_require_checks_shapes(ic, tmp_path):
     api = ic.api()
     p = synth.save_torch({"w": np.zeros((4, 3, 5, 5), np.float32)}, tmp_path / "w.pth")
