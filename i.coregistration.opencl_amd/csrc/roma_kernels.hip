@@ -1302,8 +1302,15 @@ extern "C" void roma_dwpw_small(struct ops *o, cl_mem in, int C, int H, int W, c
     need_floats(pw, 0, (long long)C * C, op, "pw");
     need_floats(pb, 0, C, op, "pb");
     need_floats(out, 0, (long long)C * H * W, op, "out");
-    if (in == out || (in->ptr == out->ptr))
-        icoreg_fatal("%s: in and out must not overlap", op);
+    {
+        /* Blocks read their input patches while others write: the two
+         * maps' byte ranges must be disjoint (views of one buffer too). */
+        const char *a = (const char *)in->ptr, *b = (const char *)out->ptr;
+        const size_t nb = (size_t)C * H * W * sizeof(float);
+
+        if (a < b + nb && b < a + nb)
+            icoreg_fatal("%s: in and out must not overlap", op);
+    }
     if ((long long)DP_CC * H * W >= (1LL << 31))
         icoreg_fatal("%s: %d x %d map too large", op, H, W);
     prof_scope ps(o->ocl, op);

@@ -137,3 +137,17 @@ def test_roma_kernels_reject_bad_sizes(ic):
     with pytest.raises(ic.IcoregError, match="roma_cls_to_flow"):
         api.roma_cls_to_flow(C.byref(ops), buf, 64, 64, 8, 1, buf, buf)
     lib.ocl_release(C.byref(buf))
+    # The fused refiner block's input and output maps (8 x 4 x 4 floats =
+    # 512 bytes) may not overlap, also as views into one allocation at
+    # different offsets. The addresses are never dereferenced: the check
+    # runs before any launch.
+    base = 1 << 20
+    a = lib.ocl_wrap(C.c_void_p(base), 1 << 16)
+    for off in (0, 64, 508):
+        b = lib.ocl_wrap(C.c_void_p(base + off), 1 << 16)
+        with pytest.raises(ic.IcoregError, match="roma_dwpw_small: in and out must not overlap"):
+            api.roma_dwpw_small(C.byref(ops), a, 8, 4, 4, a, a, a, a, b)
+        with pytest.raises(ic.IcoregError, match="roma_dwpw_small: in and out must not overlap"):
+            api.roma_dwpw_small(C.byref(ops), b, 8, 4, 4, a, a, a, a, a)
+        lib.ocl_release(C.byref(b))
+    lib.ocl_release(C.byref(a))
