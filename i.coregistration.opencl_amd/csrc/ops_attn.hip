@@ -626,8 +626,12 @@ extern "C" void ops_attention(struct ops *o, struct opnd Q, struct opnd K,
 /* ---- ops_attention without allocation ------------------------------------------ */
 
 /* The key-split partials of ops_attention_noalloc: a fixed array per
- * GPU, held until the process ends, shared by every call on that GPU. */
-#define ATT_NOALLOC_BYTES ((size_t)64 << 20)
+ * GPU, held until the process ends, shared by every call on that GPU.
+ * Its device memory is reserved wherever the library's code object is
+ * loaded, whether or not the entry point is called, so it is sized to
+ * the largest caller on the path: RoMa's ViT attention (1601 tokens, 16
+ * heads of 64, 3 key splits) needs 20.3 MB. */
+#define ATT_NOALLOC_BYTES ((size_t)24 << 20)
 static __device__ __align__(256) float scratch[ATT_NOALLOC_BYTES / sizeof(float)];
 
 /* scratch's device address on each GPU (hipGetSymbolAddress once per

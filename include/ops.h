@@ -149,13 +149,16 @@ void ops_attention(struct ops *o, struct opnd Q, struct opnd K, struct opnd V,
                    cl_mem kmask);
 
 /* ops_attention that allocates nothing: the key-split partials go to a
- * fixed 64 MiB device array (one per GPU, held until the process ends)
+ * fixed 24 MiB device array (one per GPU, held until the process ends)
  * instead of the ops work buffer, which ops_attention grows with
  * hipMalloc. No counterpart in the reference; for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving
  * loops). Same results as ops_attention. A problem whose partials
- * exceed 64 MiB is a fatal error. Every call on one GPU shares the
- * array: calls that overlap on one GPU (other streams or threads) race. */
+ * exceed 24 MiB is a fatal error (RoMa's ViT attention, the largest on
+ * the path, needs 20.3 MB). The array costs 24 MiB of device memory per
+ * process on every GPU where the library is loaded, called or not.
+ * Every call on one GPU shares the array: calls that overlap on one GPU
+ * (other streams or threads) race. */
 void ops_attention_noalloc(struct ops *o, struct opnd Q, struct opnd K,
                            struct opnd V, struct opnd O, int Nq, int Nk, int nh,
                            int d, float scale, cl_mem kmask);

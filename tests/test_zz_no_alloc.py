@@ -47,13 +47,14 @@ def test_noalloc_matches_ops_attention(dev, ic, Nq, Nk, nh, d):
 
 def test_noalloc_rejects_partials_beyond_the_array(dev, ic):
     """10 heads of 128 over 2176 queries and 1024 keys take 6 key splits,
-    64.7 MiB of partials: rejected on the host before any launch."""
+    64.7 MiB of partials, more than the 24 MiB array: rejected on the
+    host before any launch."""
     print("[noalloc] oversize rejection", flush=True)
     Nq, Nk, nh, d = 2176, 1024, 10, 128
     Q, K, V = dev.zeros(Nq * nh * d), dev.zeros(Nk * nh * d), dev.zeros(Nk * nh * d)
     O = dev.zeros(Nq * nh * d)
     ld = nh * d
-    with pytest.raises(ic.IcoregError, match="exceed the 67108864-byte scratch array"):
+    with pytest.raises(ic.IcoregError, match="exceed the 25165824-byte scratch array"):
         dev.api.ops_attention_noalloc(dev.po, ic.mat(Q, 0, ld), ic.mat(K, 0, ld),
                                       ic.mat(V, 0, ld), ic.mat(O, 0, ld), Nq, Nk, nh, d,
                                       0.1, None)
