@@ -1301,3 +1301,20 @@ void eloftr_aggregate(struct ops *o, cl_mem X, cl_mem Y, int nb, int C, int h,
                        cfptr(g), cfptr(b), h, w, aw, eps, fptr(Q), fptr(KV));
     launch_check(op);
 }
+
+extern "C" void eloftr_lse_block(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse,
+                                 cl_mem cm, cl_mem cs)
+{
+    ICOREG_API_BEGIN
+    eloftr_lse_tiles(o, S, R, N, r0, lse, cm, cs);
+    ICOREG_API_END
+}
+
+extern "C" void eloftr_conf_block(struct ops *o, cl_mem S, int R, int N, int r0, cl_mem lse,
+                                  cl_mem cm, cl_mem cs, cl_mem rmax, cl_mem rarg, cl_mem cmax,
+                                  cl_mem carg)
+{
+    ICOREG_API_BEGIN
+    eloftr_conf_tiles(o, S, R, N, r0, lse, cm, cs, rmax, rarg, cmax, carg);
+    ICOREG_API_END
+}

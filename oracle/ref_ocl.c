@@ -19,7 +19,25 @@
  *         localcorr:C:h:w:r      roma_local_corr as roma.c:956-968
  *         warpsample:C:h:w       roma_warp_sample as roma.c:936-945
  *         gridsample:C:H:W:n     ops_grid_sample (ops.c:520-534); with
- *                                n = H W the points of a smooth warp */
+ *                                n = H W the points of a smooth warp
+ *
+ * Parity cases: the reference's kernels on inputs given as raw files
+ * (written by a test, which runs this library's kernels on the same
+ * inputs), outputs written as raw files:
+ *         coarse:n:blk:S:OUT     eloftr_row_lse / col_lse / conf_row /
+ *                                conf_col over row blocks of blk rows of
+ *                                the n x n scores S, the schedule of
+ *                                eloftr.c:485-548; OUT: row_max (n
+ *                                floats), row_arg, col_arg (n ints each),
+ *                                col_max (n floats)
+ *         nms:h:w:W:off:thresh:HEAT:OUT   nms5x5 as disk.c:209-222 on
+ *                                HEAT (off + h W floats); OUT: h w bytes
+ *         gather:H:W:D:n:FEAT:XY:OUT      gather_desc as disk.c:255-268;
+ *                                FEAT (D + 1) H W floats, XY 2 n ints;
+ *                                OUT: n D floats
+ *         cls:n:ld:C:res:L:OUT   roma_cls_to_flow as roma.c:898-919 on
+ *                                L (n ld floats); OUT: flow (2 n floats),
+ *                                cert (n floats) */
 
 #define CL_TARGET_OPENCL_VERSION 120
 #include <CL/cl.h>
@@ -32,7 +50,7 @@
 static cl_context ctx;
 static cl_command_queue q;
 static cl_device_id devid;
-static cl_program prog_ops, prog_roma;
+static cl_program prog_ops, prog_roma, prog_eloftr, prog_disk;
 
 static void die(const char *what, cl_int e)
 {
@@ -609,6 +627,238 @@ static void case_gridsample(const char *spec, int C, int H, int W, int n)
     free(out);
 }
 
+/* ---- parity cases: inputs and outputs as raw files ------------------- */
+
+static void *read_file(const char *path, size_t bytes)
+{
+    FILE *fp = fopen(path, "rb");
+    void *p = malloc(bytes ? bytes : 4);
+
+    if (!fp || fread(p, 1, bytes, fp) != bytes) {
+        fprintf(stderr, "ref_ocl: cannot read %zu bytes of %s\n", bytes, path);
+        exit(2);
+    }
+    fclose(fp);
+    return p;
+}
+
+static void write_file(const char *path, const void *p, size_t bytes)
+{
+    FILE *fp = fopen(path, "wb");
+
+    if (!fp || fwrite(p, 1, bytes, fp) != bytes) {
+        fprintf(stderr, "ref_ocl: cannot write %s\n", path);
+        exit(2);
+    }
+    fclose(fp);
+}
+
+static cl_program need_program(cl_program p, const char *what)
+{
+    if (!p) {
+        fprintf(stderr, "ref_ocl: %s.co was not built\n", what);
+        exit(2);
+    }
+    return p;
+}
+
+static void exec_coarse(const char *spec, int n, int blk, const char *sf, const char *of)
+{
+    cl_program pe = need_program(prog_eloftr, "eloftr_kernels");
+    cl_kernel k_rl = kern(pe, "eloftr_row_lse"), k_cl = kern(pe, "eloftr_col_lse");
+    cl_kernel k_cr = kern(pe, "eloftr_conf_row"), k_cc = kern(pe, "eloftr_conf_col");
+    const size_t nn = (size_t)n * n;
+    float *S = read_file(sf, nn * 4), *f = malloc((size_t)n * 4);
+    int *iv = malloc((size_t)n * 4);
+    cl_mem sb = buf((size_t)blk * n * 4, NULL), lse = buf((size_t)n * 4, NULL);
+    cl_mem cm, cs, cmax, carg, rmax = buf((size_t)n * 4, NULL), rarg = buf((size_t)n * 4, NULL);
+    unsigned char *out = malloc((size_t)n * 16);
+    double ms = 0.0;
+    int i, pass, r0;
+
+    /* Column state as eloftr.c:485-496 writes it. */
+    for (i = 0; i < n; i++)
+        f[i] = -INFINITY;
+    cm = buf((size_t)n * 4, f);
+    for (i = 0; i < n; i++)
+        f[i] = 0.0f;
+    cs = buf((size_t)n * 4, f);
+    for (i = 0; i < n; i++)
+        f[i] = -1.0f;
+    cmax = buf((size_t)n * 4, f);
+    for (i = 0; i < n; i++)
+        iv[i] = -1;
+    carg = buf((size_t)n * 4, iv);
+    for (pass = 0; pass < 2; pass++)
+        for (r0 = 0; r0 < n; r0 += blk) {
+            const int rows = n - r0 < blk ? n - r0 : blk;
+            size_t gr = (size_t)rows * 256, lr = 256;
+            size_t gc = (size_t)(n + 63) / 64 * 64, lc = 64;
+
+            CK(clEnqueueWriteBuffer(q, sb, CL_TRUE, 0, (size_t)rows * n * 4,
+                                    S + (size_t)r0 * n, 0, NULL, NULL));
+            if (pass == 0) {
+                SET(k_rl, 0, sb);
+                SET(k_rl, 1, (cl_int)n);
+                SET(k_rl, 2, (cl_int)r0);
+                SET(k_rl, 3, lse);
+                ms += launch(k_rl, 1, &gr, &lr);
+                SET(k_cl, 0, sb);
+                SET(k_cl, 1, (cl_int)rows);
+                SET(k_cl, 2, (cl_int)n);
+                SET(k_cl, 3, cm);
+                SET(k_cl, 4, cs);
+                ms += launch(k_cl, 1, &gc, &lc);
+            }
+            else {
+                SET(k_cr, 0, sb);
+                SET(k_cr, 1, (cl_int)n);
+                SET(k_cr, 2, (cl_int)r0);
+                SET(k_cr, 3, lse);
+                SET(k_cr, 4, cm);
+                SET(k_cr, 5, cs);
+                SET(k_cr, 6, rmax);
+                SET(k_cr, 7, rarg);
+                ms += launch(k_cr, 1, &gr, &lr);
+                SET(k_cc, 0, sb);
+                SET(k_cc, 1, (cl_int)rows);
+                SET(k_cc, 2, (cl_int)n);
+                SET(k_cc, 3, (cl_int)r0);
+                SET(k_cc, 4, lse);
+                SET(k_cc, 5, cm);
+                SET(k_cc, 6, cs);
+                SET(k_cc, 7, cmax);
+                SET(k_cc, 8, carg);
+                ms += launch(k_cc, 1, &gc, &lc);
+            }
+        }
+    readb(rmax, (size_t)n * 4, out);
+    readb(rarg, (size_t)n * 4, out + (size_t)n * 4);
+    readb(carg, (size_t)n * 4, out + (size_t)n * 8);
+    readb(cmax, (size_t)n * 4, out + (size_t)n * 12);
+    write_file(of, out, (size_t)n * 16);
+    printf("{\"case\": \"%s\", \"kernel\": \"eloftr coarse dual softmax\", \"ms\": %.5f}\n",
+           spec, ms);
+    {
+        cl_mem all[8] = {sb, lse, cm, cs, cmax, carg, rmax, rarg};
+
+        for (i = 0; i < 8; i++)
+            clReleaseMemObject(all[i]);
+    }
+    clReleaseKernel(k_rl);
+    clReleaseKernel(k_cl);
+    clReleaseKernel(k_cr);
+    clReleaseKernel(k_cc);
+    free(S);
+    free(f);
+    free(iv);
+    free(out);
+}
+static void exec_nms(const char *spec, int h, int w, int W, long off, float thresh,
+                     const char *hf, const char *of)
+{
+    cl_kernel k = kern(need_program(prog_disk, "disk_kernels"), "nms5x5");
+    const size_t nh = (size_t)off + (size_t)h * W;
+    float *heat = read_file(hf, nh * 4);
+    unsigned char *mask = malloc((size_t)h * w + 1);
+    cl_mem bh = buf(nh * 4, heat), bm = buf((size_t)h * w, NULL);
+    size_t g[2] = {(size_t)w, (size_t)h};
+    double ms;
+
+    SET(k, 0, bh);
+    SET(k, 1, (cl_ulong)off);
+    SET(k, 2, (cl_int)W);
+    SET(k, 3, (cl_int)h);
+    SET(k, 4, (cl_int)w);
+    SET(k, 5, (cl_float)thresh);
+    SET(k, 6, bm);
+    ms = launch(k, 2, g, NULL);
+    readb(bm, (size_t)h * w, mask);
+    write_file(of, mask, (size_t)h * w);
+    printf("{\"case\": \"%s\", \"kernel\": \"nms5x5\", \"ms\": %.5f}\n", spec, ms);
+    clReleaseMemObject(bh);
+    clReleaseMemObject(bm);
+    clReleaseKernel(k);
+    free(heat);
+    free(mask);
+}
+
+static void exec_gather(const char *spec, int H, int W, int D, int n, const char *ff,
+                        const char *xf, const char *of)
+{
+    cl_kernel k = kern(need_program(prog_disk, "disk_kernels"), "gather_desc");
+    const size_t nf = (size_t)(D + 1) * H * W;
+    float *feat = read_file(ff, nf * 4), *desc = malloc((size_t)n * D * 4 + 4);
+    int *xy = read_file(xf, (size_t)n * 8);
+    cl_mem bf = buf(nf * 4, feat), bx = buf((size_t)n * 8, xy), bd = buf((size_t)n * D * 4, NULL);
+    size_t g = (size_t)n;
+    double ms;
+
+    SET(k, 0, bf);
+    SET(k, 1, (cl_int)H);
+    SET(k, 2, (cl_int)W);
+    SET(k, 3, (cl_int)D);
+    SET(k, 4, bx);
+    SET(k, 5, (cl_int)n);
+    SET(k, 6, bd);
+    ms = launch(k, 1, &g, NULL);
+    readb(bd, (size_t)n * D * 4, desc);
+    write_file(of, desc, (size_t)n * D * 4);
+    printf("{\"case\": \"%s\", \"kernel\": \"gather_desc\", \"ms\": %.5f}\n", spec, ms);
+    clReleaseMemObject(bf);
+    clReleaseMemObject(bx);
+    clReleaseMemObject(bd);
+    clReleaseKernel(k);
+    free(feat);
+    free(xy);
+    free(desc);
+}
+
+static void exec_cls(const char *spec, int n, int ld, int C, int res, const char *lf,
+                     const char *of)
+{
+    cl_kernel k = kern(prog_roma, "roma_cls_to_flow");
+    float *L = read_file(lf, (size_t)n * ld * 4), *out = malloc((size_t)n * 12);
+    cl_mem bl = buf((size_t)n * ld * 4, L), bf = buf((size_t)n * 8, NULL),
+           bc = buf((size_t)n * 4, NULL);
+    size_t g = (size_t)n * 256, l = 256;
+    double ms;
+
+    SET(k, 0, bl);
+    SET(k, 1, (cl_int)ld);
+    SET(k, 2, (cl_int)C);
+    SET(k, 3, (cl_int)res);
+    SET(k, 4, (cl_int)n);
+    SET(k, 5, bf);
+    SET(k, 6, bc);
+    ms = launch(k, 1, &g, &l);
+    readb(bf, (size_t)n * 8, out);
+    readb(bc, (size_t)n * 4, out + 2 * (size_t)n);
+    write_file(of, out, (size_t)n * 12);
+    printf("{\"case\": \"%s\", \"kernel\": \"roma_cls_to_flow\", \"ms\": %.5f}\n", spec,
+           ms);
+    clReleaseMemObject(bl);
+    clReleaseMemObject(bf);
+    clReleaseMemObject(bc);
+    clReleaseKernel(k);
+    free(L);
+    free(out);
+}
+
+/* A code object of DIR when it was built, else NULL. */
+static cl_program load_optional(const char *dir, const char *name)
+{
+    char path[4096];
+    FILE *fp;
+
+    snprintf(path, sizeof(path), "%s/%s.co", dir, name);
+    fp = fopen(path, "rb");
+    if (!fp)
+        return NULL;
+    fclose(fp);
+    return load_program(path);
+}
+
 int main(int argc, char **argv)
 {
     cl_platform_id plat;
@@ -641,11 +891,26 @@ int main(int argc, char **argv)
     k_grid = kern(prog_ops, "grid_sample");
     k_corr = kern(prog_roma, "roma_local_corr");
     k_warp = kern(prog_roma, "roma_warp_sample");
+    prog_eloftr = load_optional(argv[1], "eloftr_kernels");
+    prog_disk = load_optional(argv[1], "disk_kernels");
     fprintf(stderr, "ref_ocl: device %s\n", name);
     for (int i = 2; i < argc; i++) {
         int a = 0, b = 0, c = 0, d = 0;
+        long lo = 0;
+        float fl = 0.0f;
+        char f1[1024], f2[1024], f3[1024];
 
-        if (sscanf(argv[i], "gemm:%d:%d:%d:%d", &a, &b, &c, &d) == 4)
+        if (sscanf(argv[i], "coarse:%d:%d:%1023[^:]:%1023s", &a, &b, f1, f2) == 4)
+            exec_coarse(argv[i], a, b, f1, f2);
+        else if (sscanf(argv[i], "nms:%d:%d:%d:%ld:%f:%1023[^:]:%1023s", &a, &b, &c, &lo, &fl,
+                        f1, f2) == 7)
+            exec_nms(argv[i], a, b, c, lo, fl, f1, f2);
+        else if (sscanf(argv[i], "gather:%d:%d:%d:%d:%1023[^:]:%1023[^:]:%1023s", &a, &b, &c,
+                        &d, f1, f2, f3) == 7)
+            exec_gather(argv[i], a, b, c, d, f1, f2, f3);
+        else if (sscanf(argv[i], "cls:%d:%d:%d:%d:%1023[^:]:%1023s", &a, &b, &c, &d, f1, f2) == 6)
+            exec_cls(argv[i], a, b, c, d, f1, f2);
+        else if (sscanf(argv[i], "gemm:%d:%d:%d:%d", &a, &b, &c, &d) == 4)
             case_gemm(argv[i], a, b, c, d);
         else if (sscanf(argv[i], "vitblock:%d", &a) == 1)
             case_vitblock(argv[i], a);
