@@ -224,6 +224,18 @@ def bench_roma(ic, dev, synth, wdir, steps, warmup, profile_steps):
         e1 = dev.event()
         dev.finish()
         ms_g = max(dev.elapsed_ms(e0, e1), (time.perf_counter() - t0) * 1e3) / steps
+        # The replays' GP solve (stream-event form) succeeded and their
+        # warp, certainty and GP solution are the eager pass's.
+        if net.gp_info() != 0:
+            raise RuntimeError("RoMa graph replay: GP solve failed")
+        n16 = (560 // 14) ** 2
+        outs = lambda: [net.buffer("fl0", 2 * n16), net.buffer("ce0", n16),
+                        net.buffer("g_f", n16 * 512)]
+        replayed = outs()
+        net.coarse_device(pair)
+        dev.finish()
+        if not all(np.array_equal(a, b) for a, b in zip(replayed, outs())):
+            raise RuntimeError("RoMa graph replay differs from the eager pass")
     finally:
         if graph:
             ic.lib().ocl_graph_free(graph)
@@ -243,6 +255,7 @@ def bench_roma(ic, dev, synth, wdir, steps, warmup, profile_steps):
                for k, v in sorted(table.items(), key=lambda kv: -kv[1][0])}
     print("[bench] RoMa per-kernel ms per pair: " + json.dumps(kernels), file=sys.stderr,
           flush=True)
+    gp_ms = table.get("roma_gp_solve", (0.0, 0))[0] / ps
     g_tf = fl["gemm"] / (gemm_ms * 1e-3) / 1e12 if gemm_ms > 0 else 0.0
     a_tf = fl["attention"] / (attn_ms * 1e-3) / 1e12 if attn_ms > 0 else 0.0
     return {
@@ -253,6 +266,8 @@ def bench_roma(ic, dev, synth, wdir, steps, warmup, profile_steps):
                   "workload": f"the same pass replayed from one HIP graph ({steps} replays)"},
         "gflop_per_pair": round(fl["total"] / 1e9, 1),
         "pipeline_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
+        "gp_solve_ms": round(gp_ms, 4),
+        "kernels": kernels,
         "roofline": {"kernel": "gemm_mfma (fp32 MFMA GEMM: qkv, proj, MLP, GP, to_out)",
                      "bound": "mfma", "achieved": round(g_tf, 2), "peak": PEAK_FP32_MFMA,
                      "unit": "TFLOP/s", "frac": round(g_tf / PEAK_FP32_MFMA, 4),
@@ -804,6 +819,79 @@ def copy_calibration(dev, mib):
     dst.release()
 
 
+DETAIL = ROOT / "gpurun_out" / "bench_detail.json"
+
+
+def write_detail(obj):
+    """The full records of a run (per-kernel tables, every memory-bound
+    kernel and reference case) as JSON under gpurun_out/, and on stderr."""
+    text = json.dumps(obj)
+    print("[bench] detail: " + text, file=sys.stderr, flush=True)
+    try:
+        DETAIL.parent.mkdir(exist_ok=True)
+        DETAIL.write_text(text + "\n")
+    except OSError as e:
+        print(f"[bench] could not write {DETAIL}: {e}", file=sys.stderr, flush=True)
+
+
+def _short_cpu(c):
+    if not c:
+        return c
+    return {"value": round(c["value"], 5), "unit": c["unit"], "cores": c["cores"],
+            "kind": c["kind"], "sample": c["sample"]}
+
+
+def _short_roma(r):
+    """RoMa 560 coarse: throughput, the GEMM roofline and the attention
+    share, the HIP-graph rate and the CPU baseline."""
+    if not r:
+        return r
+    out = {"pairs_per_s": r["pairs_per_s"], "ms_per_pair": r["ms_per_pair"],
+           "graph_pairs_per_s": r["graph"]["pairs_per_s"],
+           "gflop_per_pair": r["gflop_per_pair"], "pipeline_tflops": r["pipeline_tflops"],
+           "roofline": {k: r["roofline"][k] for k in ("bound", "achieved", "peak", "unit", "frac")},
+           "attention_frac": r["attention"]["frac"], "gp_solve_ms": r.get("gp_solve_ms")}
+    out["roofline"]["kernel"] = "gemm_mfma (fp32 MFMA GEMMs of the ViT, GP and decoder)"
+    if r.get("cpu_baseline"):
+        out["cpu_baseline"] = _short_cpu(r["cpu_baseline"])
+    return out
+
+
+def _short_extra(extra):
+    """One figure or two per extra leg; memory-bound kernels as
+    [kernel, scale, GB/s, fraction of HBM peak]; reference cases as
+    their speed-ups."""
+    out = {}
+    if "refiners864" in extra:
+        e = extra["refiners864"]
+        out["refiners864"] = {"pairs_per_s": e["pairs_per_s"],
+                              "pipeline_tflops": e["pipeline_tflops"]}
+    if "roma_v2ref1024" in extra:
+        e = extra["roma_v2ref1024"]
+        out["roma_v2ref1024"] = {"pairs_per_s": e["pairs_per_s"],
+                                 "device_kernel_ms_per_pair": e["device_kernel_ms_per_pair"]}
+    if "disk512" in extra:
+        e = extra["disk512"]
+        out["disk512"] = {"images_per_s": e["images_per_s"], "conv_tflops": e["conv_tflops"],
+                          "keypoints": e["keypoints"]}
+        if e.get("cpu_baseline"):
+            out["disk512"]["cpu_baseline"] = _short_cpu(e["cpu_baseline"])
+    if "adalam_nn2048" in extra:
+        e = extra["adalam_nn2048"]
+        out["adalam_nn2048"] = {"ms": e["ms"], "tflops": e["tflops"]}
+        if e.get("cpu_baseline"):
+            out["adalam_nn2048"]["cpu_ms"] = e["cpu_baseline"]["value"]
+    if "hbm_kernels" in extra:
+        out["hbm_kernels"] = [[e["kernel"], e.get("scale"), e["GBps"], e["frac_hbm"]]
+                              for e in extra["hbm_kernels"]]
+    ref = extra.get("reference_opencl_same_gpu")
+    if ref and "cases" in ref:
+        out["reference_opencl_speedup"] = {c["case"]: c["speedup"] for c in ref["cases"]}
+    elif ref:
+        out["reference_opencl_speedup"] = ref
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1004,6 +1092,23 @@ def main():
               flush=True)
         extra["reference_opencl_same_gpu"] = reference_same_gpu(ic, dev)
 
+    # The full records (per-kernel tables, every memory-bound kernel and
+    # reference case) go to a file and to stderr; the JSON line on stdout
+    # keeps the figures, so that the whole line fits a log's tail.
+    detail = {"eloftr640": {"kernels": kernels, "with_matches": with_matches,
+                            "graph": graph_leg, "fine_ms_at_max_matches": round(fine_nmax_ms, 4)},
+              "roma560": roma, "cpu_baseline": cpu, **extra}
+    write_detail(detail)
+    rf = {"kernel": "conv_wino (3x3 stride-1 conv, Winograd F(2x2,3x3) on fp32 MFMA)",
+          "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA,
+          "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
+          "traffic": conv_traffic() if H == W == 640 else None,
+          "algorithmic_bytes_per_launch": round(eloftr_wino_bytes(H, W) / 22),
+          "launches_per_step": wino_calls, "gflop_per_step": round(wino_fl / 1e9, 2),
+          "direct_equivalent_tflops": round(direct_eq, 2)}
+    cc = conv_counters() if H == W == 640 else None
+    if cc:
+        rf["sq_counters"] = {k: v for k, v in cc.items() if k != "source"}
     line = {
         "metric": "tile-pairs/sec (1 GPU) ELoFTR 640² & RoMa 560², fp32; % MFMA/HBM peak",
         "value": round(1000.0 / ms, 3),
@@ -1018,30 +1123,18 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded blurred-noise grey pair, B = random affine of A + noise; "
                 "seeded He-normal weights, data-calibrated BatchNorm statistics)",
-        "config": {"workload": f"ELoFTR {H}x{W} grey pair, full device stage (backbone, "
-                               "transformer, coarse match, fusion, fine match on the "
-                               "pair's coarse matches: coarse_matches below; see "
-                               "eloftr_with_matches for a pair with thousands)",
-                   "tile": [H, W], "coarse_matches": nm,
-                   "gflop_per_pair": round(fl["total"] / 1e9, 1)},
-        "roofline": {"kernel": "conv_wino (3x3 stride-1 convolution, Winograd F(2x2,3x3), "
-                               "fp32 MFMA on the 16 transform-domain products)",
-                     "bound": "mfma", "achieved": round(achieved, 2),
-                     "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_MFMA, 4),
-                     "traffic": conv_traffic() if H == W == 640 else None,
-                     "sq_counters": conv_counters() if H == W == 640 else None,
-                     "algorithmic_bytes_per_launch": round(eloftr_wino_bytes(H, W) / 22),
-                     "launches_per_step": wino_calls,
-                     "gflop_per_step": round(wino_fl / 1e9, 2),
-                     "direct_equivalent_tflops": round(direct_eq, 2)},
+        "config": {"workload": f"ELoFTR {H}x{W} grey pair, full device stage (coarse + fine)",
+                   "coarse_matches": nm, "gflop_per_pair": round(fl["total"] / 1e9, 1),
+                   "roma560_pairs_per_s": roma["pairs_per_s"] if roma else None},
+        "roofline": rf,
+        "cpu_baseline": _short_cpu(cpu),
+        "eloftr_with_matches": {"coarse_matches": nm_m, "pairs_per_s": with_matches["pairs_per_s"],
+                                "ms_per_pair": with_matches["ms_per_pair"]},
+        "eloftr_graph_pairs_per_s": graph_leg["pairs_per_s"],
         "pipeline_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
-        "fine_ms_at_max_matches": round(fine_nmax_ms, 4),
-        "eloftr_with_matches": with_matches,
-        "eloftr_graph": graph_leg,
-        "cpu_baseline": cpu,
-        "roma560": roma,
-        **extra,
+        "roma560": _short_roma(roma),
+        **_short_extra(extra),
+        "detail": str(DETAIL.relative_to(ROOT)),
     }
     print(json.dumps(line), flush=True)
     dev.close()
