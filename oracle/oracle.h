@@ -241,6 +241,26 @@ int orc_roma_forward(const struct orc_named *weights, int nweights,
                      const float *imgB, int H, int W, int coarse, int imagenet,
                      const float *cls_flow_in, struct orc_roma_out *out);
 
+/* RoMa's coarse forward alone (roma.c:715-919: DINOv2 on both images,
+ * GP, decoder, cls_to_flow) on (3, coarse, coarse) images already
+ * ImageNet-normalised: cls_flow (2 n16), cls_cert (n16). Returns the GP
+ * status (0, or 1 + the failing column). */
+int orc_roma_coarse(const struct orc_named *weights, int nweights,
+                    const struct orc_named *dino, int ndino, const float *pairA,
+                    const float *pairB, int coarse, float *cls_flow, float *cls_cert);
+
+/* The fine pass alone (roma.c:1404-1413, the v1 refiners of scales 8 .. 1)
+ * on (3, H, W) images already ImageNet-normalised, from the 1/8 warp flow8
+ * (2, H/8, W/8) and certainty logit cert8 (H/8, W/8); coarse sets the
+ * displacement scale sqrt(H W) / coarse. out->flow (2 H W) and out->cert
+ * (H W) get the last refiner's warp and logit (no epilogue),
+ * out->scale_flow[1][s] (s = 1 .. 4, when set) the warp after each scale.
+ * Returns 0. */
+int orc_roma_refine(const struct orc_named *weights, int nweights,
+                    const struct orc_named *dino, int ndino, const float *pairA,
+                    const float *pairB, int H, int W, int coarse, const float *flow8,
+                    const float *cert8, struct orc_roma_out *out);
+
 #ifdef __cplusplus
 }
 #endif

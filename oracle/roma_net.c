@@ -1043,3 +1043,141 @@ int orc_roma_forward(const struct orc_named *weights, int nweights,
     unload(&m);
     return info;
 }
+
+/* The fine pass of RoMa's match alone (roma.c:1404-1413 and the refiner
+ * loop it runs, :1229-1256): VGG19-BN on both (3, H, W) images already
+ * prepared (ImageNet-normalised at the tile's size), then the refiners of
+ * scales 8 .. 1 from the given 1/8 warp (2, H/8, W/8) and certainty logit
+ * (H/8, W/8), with the displacement scale of a coarse pass of side
+ * coarse. out->flow / out->cert get the last refiner's warp and
+ * certainty logit (no epilogue); out->scale_flow[1][s] the warp after
+ * each scale. Returns 0. */
+int orc_roma_refine(const struct orc_named *weights, int nweights,
+                    const struct orc_named *dino_w, int ndino, const float *pairA,
+                    const float *pairB, int H, int W, int coarse, const float *flow8,
+                    const float *cert8, struct orc_roma_out *out)
+{
+    struct wset ws = {weights, nweights}, dn = {dino_w, ndino};
+    struct net m;
+    struct pass ps;
+    const int sob[4] = {4, 3, 2, 1};
+    const size_t hw = (size_t)H * W;
+    const size_t n8 = (size_t)side(H, 1) * side(W, 1);
+    const float sf = sqrtf((float)H * W) / coarse;
+    size_t dmax = 0;
+    int k, s, cur = 0;
+
+    memset(&m, 0, sizeof(m));
+    memset(&ps, 0, sizeof(ps));
+    m.coarse = coarse;
+    m.c16 = coarse / 14;
+    m.n16 = m.c16 * m.c16;
+    m.ntok = m.n16 + 1;
+    m.imagenet = 1;
+    load(&m, &ws, &dn, NULL);
+    for (k = 0; k < 2; k++) {
+        float *P[SCALES] = {NULL};
+
+        for (s = 1; s < SCALES; s++)
+            ps.P[s][k] = P[s] = malloc((size_t)ref_feat[s] * side(H, s) * side(W, s) * 4);
+        ps.fl[k] = malloc(2 * hw * 4);
+        ps.ce[k] = malloc(hw * 4);
+        vgg(m.vgg_w, m.vgg_b, m.vgg_cin, m.vgg_cout, 4, sob,
+            (const float *const *)m.proj_w, (const float *const *)m.proj_b,
+            proj_in, ref_feat, k ? pairB : pairA, H, W, P);
+    }
+    for (s = 1; s < SCALES; s++) {
+        const size_t n = (size_t)side(H, s) * side(W, s);
+
+        if ((size_t)m.ref[s].cin * n > dmax)
+            dmax = (size_t)m.ref[s].cin * n;
+    }
+    ps.da = malloc(dmax * 4);
+    ps.db = malloc(dmax * 4);
+    ps.dc = malloc(6 * hw * 4);
+    memcpy(ps.fl[0], flow8, 2 * n8 * 4);
+    memcpy(ps.ce[0], cert8, n8 * 4);
+    refiners(&m, &ps, 1, 1, SCALES, H, W, sf, &cur, NULL, out);
+    memcpy(out->flow, ps.fl[cur], 2 * hw * 4);
+    memcpy(out->cert, ps.ce[cur], hw * 4);
+    for (k = 0; k < 2; k++) {
+        for (s = 0; s < SCALES; s++)
+            free(ps.P[s][k]);
+        free(ps.fl[k]);
+        free(ps.ce[k]);
+    }
+    free(ps.da);
+    free(ps.db);
+    free(ps.dc);
+    unload(&m);
+    return 0;
+}
+
+/* RoMa's coarse forward alone (the benchmark's unit, roma.c:715-919): on
+ * a pair of (3, coarse, coarse) images already ImageNet-normalised,
+ * DINOv2 on each, the GP posterior and the decoder, into the anchor warp
+ * cls_flow (2, n16) and certainty logit cls_cert (n16). Returns the GP
+ * status (0, or 1 + the failing column). */
+int orc_roma_coarse(const struct orc_named *weights, int nweights,
+                    const struct orc_named *dino_w, int ndino, const float *pairA,
+                    const float *pairB, int coarse, float *cls_flow, float *cls_cert)
+{
+    struct wset ws = {weights, nweights}, dn = {dino_w, ndino};
+    struct net m;
+    float *feat, *P0[2], *gy[2], *nx, *ny, *kyy, *kxy, *F, *x, *logits;
+    int k, i, info, n16;
+
+    memset(&m, 0, sizeof(m));
+    m.coarse = coarse;
+    m.c16 = coarse / 14;
+    m.n16 = n16 = m.c16 * m.c16;
+    m.ntok = n16 + 1;
+    m.imagenet = 1;
+    load(&m, &ws, &dn, NULL);
+    feat = malloc((size_t)DV * n16 * 4);
+    for (k = 0; k < 2; k++) {
+        P0[k] = malloc((size_t)GP_DIM * n16 * 4);
+        gy[k] = malloc((size_t)n16 * GP_DIM * 4);
+        dino(&m, k ? pairB : pairA, feat, P0[k]);
+        orc_transpose(P0[k], gy[k], 1, GP_DIM, n16);
+    }
+    nx = malloc(n16 * 4);
+    ny = malloc(n16 * 4);
+    kyy = malloc((size_t)n16 * n16 * 4);
+    kxy = malloc((size_t)n16 * n16 * 4);
+    F = malloc((size_t)n16 * GP_DIM * 4);
+    x = calloc((size_t)n16 * DV, 4);
+    orc_roma_row_norm(gy[0], n16, GP_DIM, nx);
+    orc_roma_row_norm(gy[1], n16, GP_DIM, ny);
+    orc_gemm(n16, n16, GP_DIM, gy[1], 0, GP_DIM, 0, 0, gy[1], 0, GP_DIM, 0, 0, 1,
+             kyy, 0, n16, 0, 0, 1, 1, NULL, 0, NULL, 0, 1.0f, ACT_NONE, 0.0f);
+    orc_roma_cos_exp(kyy, ny, ny, n16, n16, 0.2f, 1e-6f);
+    orc_gemm(n16, n16, GP_DIM, gy[0], 0, GP_DIM, 0, 0, gy[1], 0, GP_DIM, 0, 0, 1,
+             kxy, 0, n16, 0, 0, 1, 1, NULL, 0, NULL, 0, 1.0f, ACT_NONE, 0.0f);
+    orc_roma_cos_exp(kxy, nx, ny, n16, n16, 0.2f, 1e-6f);
+    memcpy(F, m.basis, (size_t)n16 * GP_DIM * 4);
+    info = gp_solve(kyy, n16, F, GP_DIM);
+    orc_gemm(n16, GP_DIM, n16, kxy, 0, n16, 0, 0, F, 0, GP_DIM, 0, 0, 0, x, 0,
+             DV, 0, 0, 1, 1, NULL, 0, NULL, 0, 1.0f, ACT_NONE, 0.0f);
+    for (i = 0; i < n16; i++)
+        memcpy(x + (size_t)i * DV + GP_DIM, gy[0] + (size_t)i * GP_DIM, GP_DIM * 4);
+    for (i = 0; i < DEC_DEPTH; i++)
+        block(&m.dec[i], x, n16, 8, 1e-5f);
+    logits = malloc((size_t)n16 * (NCLS + 1) * 4);
+    linear(x, n16, DV, NCLS + 1, m.to_out_w, m.to_out_b, logits, ACT_NONE, 0);
+    orc_roma_cls_to_flow(logits, NCLS + 1, NCLS, CLS_RES, n16, cls_flow, cls_cert);
+    for (k = 0; k < 2; k++) {
+        free(P0[k]);
+        free(gy[k]);
+    }
+    free(feat);
+    free(nx);
+    free(ny);
+    free(kyy);
+    free(kxy);
+    free(F);
+    free(x);
+    free(logits);
+    unload(&m);
+    return info;
+}

@@ -82,6 +82,10 @@ class RomaOut(C.Structure):
 SIGS["orc_roma_forward"] = (_I, [C.POINTER(Named), _I, C.POINTER(Named), _I,
                                  C.POINTER(Named), _I, _FP, _FP, _I, _I, _I, _I, _FP,
                                  C.POINTER(RomaOut)])
+SIGS["orc_roma_coarse"] = (_I, [C.POINTER(Named), _I, C.POINTER(Named), _I, _FP, _FP, _I, _FP,
+                                _FP])
+SIGS["orc_roma_refine"] = (_I, [C.POINTER(Named), _I, C.POINTER(Named), _I, _FP, _FP, _I, _I,
+                                _I, _FP, _FP, C.POINTER(RomaOut)])
 _UP = C.POINTER(C.c_ubyte)
 SIGS["orc_disk_nms5x5"] = (None, [_FP, _I, _I, _I, _F, _UP])
 SIGS["orc_disk_topn"] = (_I, [_FP, _I, _I, _I, _UP, _UP, _I, _IP, _FP])
@@ -199,6 +203,53 @@ def roma_forward(wmain, wdino, wv2, imgA, imgB, coarse, imagenet=1, cls_flow_in=
     out["info"] = l.orc_roma_forward(a1, len(wmain), a2, len(wdino), a3,
                                      len(wv2) if wv2 else 0, fp(A), fp(B), H, W, coarse,
                                      imagenet, fp(cf), C.byref(st))
+    return out
+
+
+def roma_coarse(wmain, wdino, pairA, pairB):
+    """Run the oracle's coarse forward alone (DINOv2 x 2, GP, decoder) on
+    ImageNet-normalised (3, c, c) images; (cls_flow (2, n16), cls_cert
+    (n16), GP status)."""
+    import numpy as np
+    l = oracle()
+    c = pairA.shape[1]
+    n16 = (c // 14) ** 2
+    a1, k1 = named_array(wmain)
+    a2, k2 = named_array(wdino)
+    flow, cert = np.zeros((2, n16), np.float32), np.zeros(n16, np.float32)
+    A = np.ascontiguousarray(pairA, np.float32)
+    B = np.ascontiguousarray(pairB, np.float32)
+    info = l.orc_roma_coarse(a1, len(wmain), a2, len(wdino), fp(A), fp(B), c, fp(flow),
+                             fp(cert))
+    return flow, cert, info
+
+
+def roma_refine(wmain, wdino, pairA, pairB, flow8, cert8, coarse=560):
+    """Run the oracle's fine pass alone (the refiner config's unit) on
+    ImageNet-normalised (3, H, W) images from the 1/8 warp and certainty
+    logit; dict: flow (2, H, W), cert (H, W) (the last refiner's, no
+    epilogue) and scale_flow[s] for s = 8, 4, 2, 1."""
+    import numpy as np
+    l = oracle()
+    _, H, W = pairA.shape
+    a1, k1 = named_array(wmain)
+    a2, k2 = named_array(wdino)
+    out = {"flow": np.zeros((2, H, W), np.float32), "cert": np.zeros((H, W), np.float32),
+           "scale_flow": {}}
+    st = RomaOut()
+    st.flow, st.cert = fp(out["flow"]), fp(out["cert"])
+    for si, s in enumerate(ROMA_SCALES):
+        if si == 0:
+            continue
+        buf = np.zeros((2, H // s, W // s), np.float32)
+        out["scale_flow"][s] = buf
+        st.scale_flow[1][si] = fp(buf)
+    A = np.ascontiguousarray(pairA, np.float32)
+    B = np.ascontiguousarray(pairB, np.float32)
+    f8 = np.ascontiguousarray(flow8, np.float32)
+    c8 = np.ascontiguousarray(cert8, np.float32)
+    l.orc_roma_refine(a1, len(wmain), a2, len(wdino), fp(A), fp(B), H, W, coarse, fp(f8),
+                      fp(c8), C.byref(st))
     return out
 
 

@@ -204,6 +204,47 @@ def test_roma_forward_matches_float64_restatement(roma_weights, v2):
         assert rel(o["sd"][both], r["sd"][both]) < 1e-3
 
 
+def test_roma_coarse_is_the_coarse_pass(orc, roma_weights):
+    """orc_roma_coarse (the coarse unit alone: DINOv2 x 2, GP, decoder,
+    cls_to_flow on prepared images) gives the coarse warp and certainty
+    of the oracle's whole match bit for bit."""
+    from oracle_lib import roma_coarse
+    wm, wd, _ = roma_weights
+    a, b, _ = synth.roma_pair(COARSE, COARSE)
+    o = roma_forward(wm, wd, None, a, b, COARSE)
+    pa, pb = (np.zeros((3, COARSE, COARSE), np.float32) for _ in range(2))
+    orc.orc_roma_prepare(fp(np.ascontiguousarray(a)), COARSE, COARSE, fp(pa), COARSE, COARSE, 1)
+    orc.orc_roma_prepare(fp(np.ascontiguousarray(b)), COARSE, COARSE, fp(pb), COARSE, COARSE, 1)
+    flow, cert, info = roma_coarse(wm, wd, pa, pb)
+    assert info == 0
+    assert np.array_equal(flow, o["cls_flow"])
+    assert np.array_equal(cert, o["cls_cert"])
+
+
+def test_roma_refine_is_the_fine_pass(orc, roma_weights):
+    """orc_roma_refine (the refiner config's unit: VGG19-BN and the v1
+    refiners of scales 8 .. 1 from a given 1/8 warp) reproduces the fine
+    pass of the oracle's whole match bit for bit when started from that
+    match's own inputs: the tile's prepared images and the coarse pass's
+    last warp resized to 1/8. The certainty logit only accumulates the
+    refiners' deltas, so the warps do not depend on the starting one."""
+    from oracle_lib import roma_refine
+    wm, wd, _ = roma_weights
+    a, b, _ = synth.roma_pair(TILE, TILE)
+    o = roma_forward(wm, wd, None, a, b, COARSE)
+    pa, pb = np.zeros((3, TILE, TILE), np.float32), np.zeros((3, TILE, TILE), np.float32)
+    orc.orc_roma_prepare(fp(np.ascontiguousarray(a)), TILE, TILE, fp(pa), TILE, TILE, 1)
+    orc.orc_roma_prepare(fp(np.ascontiguousarray(b)), TILE, TILE, fp(pb), TILE, TILE, 1)
+    f0 = np.ascontiguousarray(o["scale_flow"][(0, 1)])
+    h8 = TILE // 8
+    f8 = np.zeros((2, h8, h8), np.float32)
+    orc.orc_resize(fp(f0), 2, COARSE, COARSE, fp(f8), h8, h8, 0, 0, 0.0)
+    r = roma_refine(wm, wd, pa, pb, f8, np.zeros((h8, h8), np.float32), COARSE)
+    for s in (8, 4, 2, 1):
+        assert np.array_equal(r["scale_flow"][s], o["scale_flow"][(1, s)]), s
+    assert np.array_equal(r["flow"], r["scale_flow"][1])
+
+
 def test_vit_block_vs_torch(orc):
     """orc_vit_block (the DINOv2 block the oracle runs, roma.c:675-713, and
     the CPU baseline times) against torch float64: pre-norm attention with
