@@ -64,19 +64,23 @@ def eloftr_pair(H=640, W=640, seed=BASE_SEED + CONFIG_ELOFTR):
     return a, b.astype(np.float32), M
 
 
-def eloftr_noise_pair(H, W, shift=(8, 16), seed=BASE_SEED + CONFIG_ELOFTR + 100):
+def eloftr_noise_pair(H, W, shift=(8, 16), seed=BASE_SEED + CONFIG_ELOFTR + 100, noise=0.01):
     """Grey pair that yields coarse matches with random-init weights:
     A is unblurred uniform noise, B is A translated by shift = (dy, dx) px
-    (whole 8-px cells), zeros where B leaves A, plus N(0, 0.01). With the
+    (whole 8-px cells), zeros where B leaves A, plus N(0, noise). With the
     config pair (blurred noise) random-init features barely separate the
-    cells and the mutual selection keeps almost nothing."""
+    cells and the mutual selection keeps almost nothing; sub-cell shifts
+    keep almost no coarse match either. A larger noise (0.05) leaves fewer
+    coarse matches but makes the fine stage's argmax decisive: with 0.01
+    the 64 window positions of a whole-cell shift match almost equally
+    well."""
     rng = np.random.default_rng(seed)
     a = rng.uniform(0.0, 1.0, (H, W)).astype(np.float32)
     dy, dx = shift
     b = np.zeros_like(a)
     b[max(dy, 0):H + min(dy, 0), max(dx, 0):W + min(dx, 0)] = \
         a[max(-dy, 0):H - max(dy, 0), max(-dx, 0):W - max(dx, 0)]
-    b = b + rng.normal(0.0, 0.01, b.shape).astype(np.float32)
+    b = b + rng.normal(0.0, noise, b.shape).astype(np.float32)
     return a, b.astype(np.float32)
 
 
