@@ -805,6 +805,78 @@ def cpu_baseline_roma(coarse=560, blocks=2):
                       f"(x{fl['total'] / blk:.1f}); {thr} OpenMP threads, {nproc} CPUs visible"}
 
 
+def cpu_baseline_roma_full(coarse=560):
+    """The oracle's whole coarse forward (orc_roma_coarse: DINOv2 on both
+    images, GP, decoder) on the config's pair, timed once (about two
+    minutes on 16 threads: only with --cpu-full)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    sys.path.insert(0, str(PKG_DIR))
+    import synth
+    from oracle_lib import oracle, roma_coarse
+    orc = oracle()
+    nproc, thr = _cpu_threads()
+    orc.orc_set_threads(thr)
+    a, b, _ = synth.roma_pair(coarse, coarse)
+    wm, wd = synth.roma_weights(), synth.dino_weights()
+    t0 = time.perf_counter()
+    _, _, info = roma_coarse(wm, wd, synth.imagenet_norm(a), synth.imagenet_norm(b))
+    dt = time.perf_counter() - t0
+    return {"value": 1.0 / dt, "unit": "tile-pairs/s", "cores": int(orc.orc_threads()),
+            "kind": "port", "gp_info": int(info),
+            "sample": f"oracle/ orc_roma_coarse (C port, OpenMP): the whole coarse forward of "
+                      f"the {coarse}x{coarse} config pair once, {dt:.1f} s; {thr} OpenMP "
+                      f"threads, {nproc} CPUs visible"}
+
+
+def cpu_baseline_disk(side=256, H=512):
+    """The oracle's DISK detection (disk.c:164-273: U-Net, NMS, top-n,
+    descriptors) on a side x side crop of the config image, scaled to the
+    H x H image by pixels (every layer's work is per pixel)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    sys.path.insert(0, str(PKG_DIR))
+    import synth
+    from oracle_lib import disk_detect, oracle
+    orc = oracle()
+    nproc, thr = _cpu_threads()
+    orc.orc_set_threads(thr)
+    img = np.ascontiguousarray(synth.disk_image(H, H)[:, :side, :side])
+    w = synth.disk_weights()
+    t0 = time.perf_counter()
+    disk_detect(w, img, n=2048 * side * side // (H * H), thresh=0.0)
+    dt = time.perf_counter() - t0
+    scale = (H * H) / (side * side)
+    return {"value": 1.0 / (dt * scale), "unit": "images/s", "cores": int(orc.orc_threads()),
+            "kind": "port",
+            "sample": f"oracle/ DISK detect (C port, OpenMP) on the {side}x{side} crop of the "
+                      f"config image in {dt:.1f} s, scaled x{scale:.0f} by pixels to {H}x{H}; "
+                      f"{thr} OpenMP threads, {nproc} CPUs visible"}
+
+
+def cpu_baseline_refiners(side=288, H=864):
+    """The oracle's refiner config unit (orc_roma_refine: VGG19-BN on both
+    images, v1 refiners at 1/8 .. 1/1 from the synthetic initial warp) on
+    a side x side pair of the same recipe, scaled to H x H by pixels."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    sys.path.insert(0, str(PKG_DIR))
+    import synth
+    from oracle_lib import oracle, roma_refine
+    orc = oracle()
+    nproc, thr = _cpu_threads()
+    orc.orc_set_threads(thr)
+    a, b, f8, c8 = synth.roma_refine_inputs(side, side)
+    wm, wd = synth.roma_weights(), synth.dino_weights()
+    t0 = time.perf_counter()
+    roma_refine(wm, wd, synth.imagenet_norm(a), synth.imagenet_norm(b), f8, c8, 560)
+    dt = time.perf_counter() - t0
+    scale = (H * H) / (side * side)
+    return {"value": 1.0 / (dt * scale), "unit": "tile-pairs/s", "cores": int(orc.orc_threads()),
+            "kind": "port",
+            "sample": f"oracle/ orc_roma_refine (C port, OpenMP, its weight load included) on "
+                      f"a {side}x{side} pair of the refiner recipe in {dt:.1f} s, scaled "
+                      f"x{scale:.0f} by pixels to "
+                      f"{H}x{H}; {thr} OpenMP threads, {nproc} CPUs visible"}
+
+
 def copy_calibration(dev, mib):
     """One device-to-device copy of mib MiB: the known-size reference that
     scales the HBM byte counters of a rocprofv3 --pmc run."""
@@ -854,6 +926,8 @@ def _short_roma(r):
     out["roofline"]["kernel"] = "gemm_mfma (fp32 MFMA GEMMs of the ViT, GP and decoder)"
     if r.get("cpu_baseline"):
         out["cpu_baseline"] = _short_cpu(r["cpu_baseline"])
+    if r.get("cpu_baseline_full"):
+        out["cpu_baseline_full"] = _short_cpu(r["cpu_baseline_full"])
     return out
 
 
@@ -866,6 +940,8 @@ def _short_extra(extra):
         e = extra["refiners864"]
         out["refiners864"] = {"pairs_per_s": e["pairs_per_s"],
                               "pipeline_tflops": e["pipeline_tflops"]}
+        if e.get("cpu_baseline"):
+            out["refiners864"]["cpu_baseline"] = _short_cpu(e["cpu_baseline"])
     if "roma_v2ref1024" in extra:
         e = extra["roma_v2ref1024"]
         out["roma_v2ref1024"] = {"pairs_per_s": e["pairs_per_s"],
@@ -900,6 +976,8 @@ def main():
     ap.add_argument("--size", type=int, default=640)
     ap.add_argument("--profile-steps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="also time the oracle's whole RoMa coarse pass (about two minutes)")
     ap.add_argument("--no-roma", action="store_true")
     ap.add_argument("--roma-only", action="store_true",
                     help="run only the RoMa leg and print its JSON object (for profiling)")
@@ -1088,6 +1166,18 @@ def main():
             roma["cpu_baseline"] = cpu_baseline_roma()
         if "adalam_nn2048" in extra:
             extra["adalam_nn2048"]["cpu_baseline"] = cpu_adalam()
+        if "disk512" in extra:
+            print("[bench] CPU baseline: oracle DISK on a 256x256 crop", file=sys.stderr,
+                  flush=True)
+            extra["disk512"]["cpu_baseline"] = cpu_baseline_disk()
+        if "refiners864" in extra:
+            print("[bench] CPU baseline: oracle refiners on a 288x288 pair", file=sys.stderr,
+                  flush=True)
+            extra["refiners864"]["cpu_baseline"] = cpu_baseline_refiners()
+        if args.cpu_full and roma is not None:
+            print("[bench] CPU baseline: oracle's whole RoMa coarse pass", file=sys.stderr,
+                  flush=True)
+            roma["cpu_baseline_full"] = cpu_baseline_roma_full()
         print("[bench] baseline: the reference's OpenCL kernels on this GPU", file=sys.stderr,
               flush=True)
         extra["reference_opencl_same_gpu"] = reference_same_gpu(ic, dev)

@@ -31,6 +31,7 @@
 #include <string.h>
 
 #include "common.h"
+#include "conv.h"
 #include "icoreg_kernels.h"
 #include "roma.h"
 
@@ -213,7 +214,7 @@ static void load_block(struct roma_model *m, struct pth_file *pf,
  * BatchNorm, ReLU per layer, one index per pooling). roma.c:213-238. */
 static void load_vgg(struct roma_model *m, struct pth_file *pf,
                      const char *pre, int nblk, cl_mem *w, cl_mem *b,
-                     int *cin_out, int *cout_out)
+                     int *cin_out, int *cout_out, cl_mem *U)
 {
     int l = 0, idx = 0, cin = 3;
 
@@ -226,6 +227,11 @@ static void load_vgg(struct roma_model *m, struct pth_file *pf,
             snprintf(conv, sizeof(conv), "%s.%d", pre, idx);
             snprintf(bn, sizeof(bn), "%s.%d", pre, idx + 1);
             load_conv_bn(m, pf, conv, bn, co, 4, shape, &w[l], &b[l]);
+            /* Same-size 3 x 3 filters in Winograd form, once (the passes
+             * would otherwise transform them on every call). */
+            U[l] = conv_wino_supported(3, 3, 1, 1, 1, 1, 1, 1, 1, cin, co, 1, 1)
+                       ? conv_wino_prepare(m->ops, w[l], co, cin)
+                       : NULL;
             cin_out[l] = cin;
             cout_out[l] = co;
             cin = co;
@@ -364,7 +370,7 @@ extern "C" void roma_load(struct roma_model *m, struct ops *ops,
     m->coarse = ROMA_COARSE;
     pth_strip_prefix(pf, "matcher.model.");
     load_vgg(m, pf, "encoder.cnn.layers", 4, m->vgg_w, m->vgg_b, m->vgg_cin,
-             m->vgg_cout);
+             m->vgg_cout, m->vgg_U);
     load_dino(m, dino);
     for (int s = 0; s < ROMA_SCALES; s++) {
         long shape[4] = {ref_feat[s], proj_in_ch[s], 1, 1};
@@ -461,7 +467,7 @@ extern "C" void roma_load_v2(struct roma_model *m, struct pth_file *pf)
     if (m->H)
         icoreg_fatal("roma_load_v2 after roma_alloc");
     load_vgg(m, pf, "refiner_features.layers", 3, m->vgg2_w, m->vgg2_b,
-             m->vgg2_cin, m->vgg2_cout);
+             m->vgg2_cin, m->vgg2_cout, m->vgg2_U);
     for (int j = 0; j < ROMA2_SCALES; j++)
         load_refiner2(m, pf, j);
     m->v2 = 1;
@@ -831,7 +837,7 @@ static void gp_check(struct roma_model *m)
  * into the pair buffer dst[r] (image B at dstride[r]). roma.c:740-768,
  * 997-1027. */
 static void vgg_pair(struct roma_model *m, cl_mem src, int nblk, const cl_mem *w,
-                     const cl_mem *b, const int *cin, const int *cout,
+                     const cl_mem *U, const cl_mem *b, const int *cin, const int *cout,
                      const int *scale_of_block, const cl_mem *pw,
                      const cl_mem *pb, const int *pin, const int *pout,
                      const cl_mem *dst, const long *dstride, int H, int W)
@@ -847,9 +853,13 @@ static void vgg_pair(struct roma_model *m, cl_mem src, int nblk, const cl_mem *w
 
         for (int j = 0; j < vgg_blocks[blk]; j++, l++) {
             out = in == m->v_a ? m->v_b : m->v_a;
-            ops_conv2d_batch(o, 2, in, (long)cin[l] * hw, cin[l], h, wd, w[l],
-                             b[l], cout[l], &g, NULL, NULL, NULL, ACT_RELU, 0,
-                             out, (long)cout[l] * hw);
+            if (U[l])
+                conv3x3_wino_batch(o, 2, in, (long)cin[l] * hw, cin[l], h, wd, w[l], U[l],
+                                   b[l], cout[l], ACT_RELU, 0, out, (long)cout[l] * hw);
+            else
+                ops_conv2d_batch(o, 2, in, (long)cin[l] * hw, cin[l], h, wd, w[l],
+                                 b[l], cout[l], &g, NULL, NULL, NULL, ACT_RELU, 0,
+                                 out, (long)cout[l] * hw);
             in = out;
         }
         ops_gemm(o, pout[r], (int)hw, pin[r], ops_bmat(pw[r], 0, pin[r], 0, 0),
@@ -870,7 +880,7 @@ static void vgg(struct roma_model *m, int H, int W, cl_mem src)
 {
     static const int sob[4] = {4, 3, 2, 1};
 
-    vgg_pair(m, src, 4, m->vgg_w, m->vgg_b, m->vgg_cin, m->vgg_cout, sob,
+    vgg_pair(m, src, 4, m->vgg_w, m->vgg_U, m->vgg_b, m->vgg_cin, m->vgg_cout, sob,
              m->proj_w, m->proj_b, m->proj_in, m->proj_out, m->P, m->pstride,
              H, W);
 }
@@ -882,7 +892,7 @@ static void vgg2(struct roma_model *m, int H, int W)
 
     for (int j = 0; j < ROMA2_SCALES; j++)
         pout[j] = m->ref2[j].feat;
-    vgg_pair(m, m->img, 3, m->vgg2_w, m->vgg2_b, m->vgg2_cin, m->vgg2_cout, sob,
+    vgg_pair(m, m->img, 3, m->vgg2_w, m->vgg2_U, m->vgg2_b, m->vgg2_cin, m->vgg2_cout, sob,
              m->proj2_w, m->proj2_b, m->proj2_in, pout, m->P2, m->p2stride, H,
              W);
 }
@@ -1273,10 +1283,12 @@ extern "C" void roma_free(struct roma_model *m)
     for (int i = 0; i < 16; i++) {
         ocl_release(&m->vgg_w[i]);
         ocl_release(&m->vgg_b[i]);
+        ocl_release(&m->vgg_U[i]);
     }
     for (int i = 0; i < 8; i++) {
         ocl_release(&m->vgg2_w[i]);
         ocl_release(&m->vgg2_b[i]);
+        ocl_release(&m->vgg2_U[i]);
     }
     for (int i = 0; i < ROMA_VIT_DEPTH; i++)
         release_block(&m->vit[i]);

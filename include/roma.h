@@ -68,6 +68,7 @@ struct roma_model {
     /* Weights. VGG19-BN (16 convolutions, BatchNorm folded). */
     cl_mem vgg_w[16], vgg_b[16];
     int vgg_cin[16], vgg_cout[16];
+    cl_mem vgg_U[16]; /* the same filters in Winograd form (NULL: direct) */
     /* DINOv2: patch embedding, class token, final norm; the position
      * embedding is interpolated to the coarse grid at alloc. */
     cl_mem patch_w, patch_b, cls, norm_g, norm_b, pos;
@@ -84,6 +85,7 @@ struct roma_model {
     int v2;
     cl_mem vgg2_w[8], vgg2_b[8];
     int vgg2_cin[8], vgg2_cout[8];
+    cl_mem vgg2_U[8];
     cl_mem proj2_w[ROMA2_SCALES], proj2_b[ROMA2_SCALES];
     int proj2_in[ROMA2_SCALES];
     struct roma_refiner ref2[ROMA2_SCALES];
