@@ -15,8 +15,8 @@
  * panels of their block rows' products, added as each becomes final,
  * instead of a chain of one launch per panel after the factorisation.
  *  - chol_diag: the 64 x 64 diagonal block factored and its factor
- *    inverted in LDS by one work-group, one barrier per two columns,
- *    after applying the previous panel's update to the block itself
+ *    inverted by one work-group (one wave each, in registers), after
+ *    applying the previous panel's update to the block itself
  *    (look-ahead); these run back to back on the main stream while
  *    everything else runs on a second stream, joined back at the end;
  *  - on the second stream, one launch per panel for both L21 = A21
@@ -191,28 +191,6 @@ __device__ __forceinline__ double rsqrt_nr(double x)
     return r;
 }
 
-/* Cholesky factor of the nb x nb diagonal block at (k, k) of A (n x n)
- * into L, and the inverse of that factor into Linv (nb x nb, row-major,
- * GP_NB apart), both in one pass over the columns. info gets 1 + the
- * first column whose pivot is not positive (the factor then holds NaN
- * from there on).
- *
- * LDS holds the block: its lower triangle the trailing matrix, its
- * strictly upper triangle the inverse transposed (Linv[r][c] at s[c][r],
- * c < r, starting as the identity's zeros). Column j is used unscaled:
- * every thread reads the pivot, forms r = 1 / sqrt(pivot) itself and
- * scales the column values it reads (L[x][j] = r s[x][j] below the
- * pivot, Linv[j][x] = r s[x][j] above it), so no pass writes column j
- * back and one barrier per column separates the steps. The threads that
- * own column j's cells put the finished column into f (same layout,
- * another array; written to L and Linv at the end, so that no global
- * store sits before a barrier). 1024 threads, 4 cells each (rows
- * ty + 32 a, columns tx + 32 b), so that every SIMD holds 4 waves to hide
- * the latency of the short per-column chain; each thread updates its
- * cells branch-free and writes all of them back (a cell of column j is
- * written back unchanged by its only owner): the trailing lower triangle
- * (A[r][c] -= L[r][j] L[c][j], c > j) and the inverse's rows below j
- * (Linv[c][r] -= L[c][j] Linv[j][r], r <= j < c). */
 typedef double gp_d4 __attribute__((ext_vector_type(4)));
 
 /* Polls of a panel flag before the diagonal kernel gives up (with a
@@ -220,24 +198,56 @@ typedef double gp_d4 __attribute__((ext_vector_type(4)));
  * then ends with info = -1 instead of hanging. */
 #define GP_SPIN_MAX (1 << 22)
 
-__global__ void __launch_bounds__(1024)
+/* Cholesky factor of the nb x nb diagonal block at (k, k) of A (n x n)
+ * into L, and the inverse of that factor into Linv (nb x nb, row-major,
+ * GP_NB apart). info gets 1 + the first column whose pivot is not
+ * positive (the factor then holds NaN from there on), or -1 if the wait
+ * for ready gave up. 256 threads.
+ *  - ready (when given): set once the trailing update this block needs
+ *    has finished on the other stream; polled with device-coherent loads,
+ *    then an acquire, so the block's reads see that update.
+ *  - Look-ahead (lprev: the previous panel's Linv; its trailing update of
+ *    this block is left to this kernel): P = A[k.., k - 64..] lprev^T,
+ *    the block's row of that panel's L21, then s -= P P^T on the lower
+ *    triangle, in 16 x 16 tiles on v_mfma_f64_16x16x4f64 (lane l gives
+ *    A(l % 16, l / 16) and B(l / 16, l % 16) and holds D(l / 16 + 4 v,
+ *    l % 16); the fp32 16 x 16 x 4 form holds rows 4 (l / 16) + v
+ *    instead). The 16 P tiles and the 10 lower P P^T tiles are dealt to
+ *    the 4 waves in turn; P goes through f.
+ *  - Wave 0 then sweeps the columns: lane r holds row r of the block
+ *    (a[c], c <= r; its upper part is never read). At step j every lane
+ *    forms the pivot's reciprocal root from lane j's a[j] (a cross-lane
+ *    read) and L[r][j] = a[j] / sqrt(pivot) on and below the pivot, 0
+ *    above; the column goes to LDS (lc) and each lane applies
+ *        a[c] -= L[r][j] L[c][j]      (the trailing block, c > j).
+ *  - Wave 1, beside it and a step behind, runs the forward substitution
+ *    of L X = I column by column: lane k holds column k of T (the
+ *    identity at first),
+ *        T[j][k] /= L[j][j],  T[c][k] -= L[c][j] T[j][k]   (c > j),
+ *    taking column j from lc once wave 0 has counted it (an LDS counter,
+ *    released at the start of wave 0's next step). Each wave holds 64
+ *    values a lane, so a step's column reads (16-byte loads, every lane
+ *    the same address) are issued together before its updates.
+ *  - All threads store the factor from lc in rows; the inverse is stored
+ *    from wave 1's registers (lane k: column k, so each store
+ *    instruction writes one row of it).
+ * Against the earlier form (1024 threads holding the block in LDS, one
+ * barrier per two columns): 59.7 -> 41 us a block at n = 1600. */
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
     chol_diag_kernel(const double *__restrict__ A, double *__restrict__ L,
-                     double *__restrict__ Linv, int n, int k, int nb,
-                     const double *__restrict__ lprev, const int *ready, int spin_max,
-                     int *__restrict__ info)
+                      double *__restrict__ Linv, int n, int k, int nb,
+                      const double *__restrict__ lprev, const int *ready, int spin_max,
+                      int *__restrict__ info)
 {
     __shared__ double s[GP_NB][GP_NB + 1], f[GP_NB][GP_NB + 1];
+    /* lc[j][r] = L[r][j]: each column contiguous, read with wide LDS
+     * loads (every lane the same address). */
+    __shared__ __align__(16) double lc[GP_NB][GP_NB];
     __shared__ double dinv[GP_NB];
-    const int tid = threadIdx.x, tx = tid & 31, ty = tid >> 5;
-    /* First failing column of this block (thread 0), reported at the end:
-     * no global access inside the column loop; -1 if the wait for ready
-     * gave up. */
+    __shared__ int prog;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     int bad = 0;
 
-    /* ready (when given): set once the trailing update this block needs
-     * has finished on the other stream. Polled with device-coherent
-     * loads, then this CU's and XCD's caches are invalidated (acquire),
-     * so the block's reads below see that update. */
     if (ready) {
         if (tid == 0) {
             int it = 0;
@@ -251,74 +261,57 @@ __global__ void __launch_bounds__(1024)
         __syncthreads();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
-
-    {
-        double v[4];
-
+    /* The block's lower triangle; rows and columns past nb are zero with
+     * a unit diagonal (their pivots stay 1 and they touch no real row). */
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = tid + 1024 * i, r = e >> 6, c = e & 63;
+    for (int i = 0; i < 16; i++) {
+        const int e = tid + 256 * i, r = e >> 6, c = e & 63;
+        const double v = A[(long long)(k + min(r, nb - 1)) * n + k + min(c, nb - 1)];
 
-            v[i] = A[(long long)(k + min(r, nb - 1)) * n + k + min(c, nb - 1)];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = tid + 1024 * i, r = e >> 6, c = e & 63;
-
-            s[r][c] = r < nb && c <= r ? v[i] : 0.0;
-        }
+        s[r][c] = r < nb && c <= r ? v : r == c ? 1.0 : 0.0;
     }
+    if (tid == 0)
+        prog = 0;
     __syncthreads();
-    /* Look-ahead (lprev: the previous panel's Linv; its trailing update of
-     * this block is left to this kernel): P = A[k.., k - 64..] lprev^T, the
-     * block's row of that panel's L21, then s -= P P^T on the lower
-     * triangle, in 16 x 16 tiles on v_mfma_f64_16x16x4f64: lane l gives
-     * A(l % 16, l / 16) and B(l / 16, l % 16) and holds D(l / 16 + 4 v,
-     * l % 16) (measured; the fp32 16 x 16 x 4 form holds rows
-     * 4 (l / 16) + v instead). P goes through f, which the factorisation
-     * overwrites later. */
     if (lprev) {
-        /* Phase 1, P: wave w (on SIMD w % 4, slot w / 4) takes tile
-         * (w / 4, (w % 4 + w / 4) % 4), so each SIMD gets one tile of each
-         * tile column; tile column tc needs k < 16 (tc + 1) only (lprev is
-         * lower triangular). Phase 2, P P^T: the 10 lower tiles on waves
-         * 0..9, at most 3 a SIMD. */
-        const int w = tid >> 6, l = tid & 63, kq = l >> 4;
-        const int tr = w >> 2, tc = ((w & 3) + (w >> 2)) & 3;
-        const int ri = 16 * tr + (l & 15), ci = 16 * tc + (l & 15);
-        const double *trow = A + (long long)(k + min(ri, nb - 1)) * n + k - GP_NB;
-        double ta[16], lb[16];
-        gp_d4 acc = {0.0, 0.0, 0.0, 0.0};
+        const int kq = lane >> 4;
+
+        for (int w = wave; w < 16; w += 4) {
+            const int tr = w >> 2, tc = ((w & 3) + (w >> 2)) & 3;
+            const int ri = 16 * tr + (lane & 15), ci = 16 * tc + (lane & 15);
+            const double *trow = A + (long long)(k + min(ri, nb - 1)) * n + k - GP_NB;
+            double ta[16], lb[16];
+            gp_d4 acc = {0.0, 0.0, 0.0, 0.0};
 
 #pragma unroll
-        for (int kk = 0; kk < 16; kk++)
-            if (kk < 4 * (tc + 1)) {
-                ta[kk] = trow[4 * kk + kq];
-                lb[kk] = lprev[ci * GP_NB + 4 * kk + kq];
-            }
+            for (int kk = 0; kk < 16; kk++)
+                if (kk < 4 * (tc + 1)) {
+                    ta[kk] = trow[4 * kk + kq];
+                    lb[kk] = lprev[ci * GP_NB + 4 * kk + kq];
+                }
 #pragma unroll
-        for (int kk = 0; kk < 16; kk++)
-            if (kk < 4 * (tc + 1))
-                acc = __builtin_amdgcn_mfma_f64_16x16x4f64(ri < nb ? ta[kk] : 0.0, lb[kk], acc, 0,
-                                                          0, 0);
+            for (int kk = 0; kk < 16; kk++)
+                if (kk < 4 * (tc + 1))
+                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(ri < nb ? ta[kk] : 0.0, lb[kk],
+                                                              acc, 0, 0, 0);
 #pragma unroll
-        for (int v = 0; v < 4; v++)
-            f[16 * tr + kq + 4 * v][16 * tc + (l & 15)] = acc[v];
+            for (int v = 0; v < 4; v++)
+                f[16 * tr + kq + 4 * v][16 * tc + (lane & 15)] = acc[v];
+        }
         __syncthreads();
-        if (w < 10) {
-            /* Lower tile w: row tr2 = the largest t with t (t + 1) / 2 <= w. */
+        for (int w = wave; w < 10; w += 4) {
             const int tr2 = w >= 6 ? 3 : w >= 3 ? 2 : w >= 1 ? 1 : 0;
             const int tc2 = w - tr2 * (tr2 + 1) / 2;
-            const int r2 = 16 * tr2 + (l & 15), c2 = 16 * tc2 + (l & 15);
+            const int r2 = 16 * tr2 + (lane & 15), c2 = 16 * tc2 + (lane & 15);
+            gp_d4 acc = {0.0, 0.0, 0.0, 0.0};
 
-            acc = (gp_d4){0.0, 0.0, 0.0, 0.0};
 #pragma unroll
             for (int kk = 0; kk < 16; kk++)
                 acc = __builtin_amdgcn_mfma_f64_16x16x4f64(f[r2][4 * kk + kq], f[c2][4 * kk + kq],
                                                           acc, 0, 0, 0);
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const int r = 16 * tr2 + kq + 4 * v, c = 16 * tc2 + (l & 15);
+                const int r = 16 * tr2 + kq + 4 * v, c = 16 * tc2 + (lane & 15);
 
                 if (r < nb && c <= r)
                     s[r][c] -= acc[v];
@@ -326,89 +319,105 @@ __global__ void __launch_bounds__(1024)
         }
         __syncthreads();
     }
-    /* Two columns per step (j and j1 = j + 1, one barrier): every thread
-     * forms both pivots' roots itself (the second from the first's
-     * update of s[j1][j1]) and the two columns' values it needs, then
-     * applies both rank-one updates to its cells at once. */
-    for (int j = 0; j < nb; j += 2) {
-        const int j1 = j + 1;
-        const bool two = j1 < nb;
-        const double piv0 = s[j][j];
-        const double r0 = rsqrt_nr(piv0);
-        const double l10 = two ? s[j1][j] * r0 : 0.0;
-        const double piv1 = two ? fma(-l10, l10, s[j1][j1]) : 1.0;
-        const double r1 = two ? rsqrt_nr(piv1) : 0.0;
-        /* u, w: column j and j1 values at index x: L below the pivot,
-         * the inverse's rows j and j1 above it. */
-        auto uw = [&](int x, double &u, double &w) {
-            const double sj = s[x][j], sj1 = two ? s[x][j1] : 0.0;
+    if (wave == 0) {
+        /* The factor: lane r holds row r (a[c], c <= r; its upper part
+         * is never read). Column j of L goes to lc[j], the pivot's
+         * reciprocal root to dinv, then the step count to prog. Above
+         * the pivot L[r][j] = 0 is written too, so lc holds the factor
+         * transposed with zeros above its diagonal. */
+        double a[GP_NB];
 
-            u = x == j ? piv0 * r0 : sj * r0;
-            w = !two ? 0.0 : x == j1 ? piv1 * r1 : x == j ? -l10 * r0 * r1 : (sj1 - u * l10) * r1;
-        };
-        double ur[2], wr[2], uc[2], wc[2], v[2][2];
+#pragma unroll
+        for (int c = 0; c < GP_NB; c++)
+            a[c] = s[lane][c];
+#pragma unroll
+        for (int j = 0; j < GP_NB; j++) {
+            if (j >= nb)
+                continue;
+            /* Column j - 1 and its root were written a step ago: counted
+             * now, the release's wait for them costs nothing. */
+            if (j > 0 && lane == 0)
+                __hip_atomic_store(&prog, j, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            const unsigned long long pj = __builtin_bit_cast(unsigned long long, a[j]);
+            const double piv = __builtin_bit_cast(
+                double,
+                ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(pj >> 32), j)
+                 << 32) |
+                    (unsigned)__builtin_amdgcn_readlane((int)pj, j));
+            const double rj = rsqrt_nr(piv);
+            const double lr = lane > j ? a[j] * rj : lane == j ? piv * rj : 0.0;
 
-        if (tid == 0 && bad == 0 && (!(piv0 > 0.0) || (two && !(piv1 > 0.0))))
-            bad = k + (piv0 > 0.0 ? j1 : j) + 1;
-#pragma unroll
-        for (int a2 = 0; a2 < 2; a2++) {
-            uw(ty + 32 * a2, ur[a2], wr[a2]);
-            uw(tx + 32 * a2, uc[a2], wc[a2]);
-        }
-#pragma unroll
-        for (int a2 = 0; a2 < 2; a2++)
-#pragma unroll
-            for (int b2 = 0; b2 < 2; b2++)
-                v[a2][b2] = s[ty + 32 * a2][tx + 32 * b2];
-        /* The finished columns (f holds L and the inverse transposed, the
-         * same layout as s). */
-        if (tx == (j & 31)) {
-#pragma unroll
-            for (int a2 = 0; a2 < 2; a2++)
-                f[ty + 32 * a2][j] = ur[a2];
-            if (ty == 0)
-                dinv[j] = r0;
-        }
-        if (two && tx == (j1 & 31)) {
-#pragma unroll
-            for (int a2 = 0; a2 < 2; a2++)
-                f[ty + 32 * a2][j1] = wr[a2];
-            if (ty == 0)
-                dinv[j1] = r1;
-        }
-        const int jl = two ? j1 : j; /* the last column of the step */
-#pragma unroll
-        for (int a2 = 0; a2 < 2; a2++)
-#pragma unroll
-            for (int b2 = 0; b2 < 2; b2++) {
-                const int r = ty + 32 * a2, c = tx + 32 * b2;
-                /* lower: factor update by both columns; upper (r < c):
-                 * inverse cell (c, r) for r <= jl < c, by the inverse's
-                 * rows j (p, zero at r = j1) and j1 (q). */
-                const bool low = r < nb && c > jl && c <= r;
-                const bool inv = c < nb && r <= jl && jl < c;
-                const double p = r == j ? r0 : r < j ? ur[a2] : 0.0;
-                const double q = r == j1 ? r1 : wr[a2];
-                double x = v[a2][b2];
+            if (lane == 0 && bad == 0 && !(piv > 0.0))
+                bad = k + j + 1;
+            a[j] = lr;
+            lc[j][lane] = lr;
+            if (lane == 0)
+                dinv[j] = rj;
+            /* LDS operations of one wave complete in issue order: these
+             * reads see the column just written. The column is read in
+             * full before the updates, so that the loads overlap. */
+            double col[GP_NB];
 
-                if (low)
-                    x = fma(-ur[a2], uc[b2], fma(-wr[a2], wc[b2], x));
-                else if (inv)
-                    x = fma(-uc[b2], p, fma(-wc[b2], q, x));
-                s[r][c] = x;
-            }
-        __syncthreads();
+#pragma unroll
+            for (int c = j + 1; c < GP_NB; c++)
+                col[c] = lc[j][c];
+            __builtin_amdgcn_sched_group_barrier(0x100, 32, 0); /* LDS reads first */
+#pragma unroll
+            for (int c = j + 1; c < GP_NB; c++)
+                a[c] = fma(-lr, col[c], a[c]);
+        }
+        if (lane == 0)
+            __hip_atomic_store(&prog, nb, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
+    else if (wave == 1) {
+        /* The inverse, one step behind: lane k holds column k of T (the
+         * identity at first), T[j][k] /= L[j][j], then T[c][k] -= L[c][j]
+         * T[j][k] below, with column j of L from lc once wave 0 has
+         * counted it. The wait is on wave 0 of the same block, which
+         * always counts every column; it is capped all the same. */
+        double t[GP_NB];
+
+#pragma unroll
+        for (int c = 0; c < GP_NB; c++)
+            t[c] = c == lane ? 1.0 : 0.0;
+#pragma unroll
+        for (int j = 0; j < GP_NB; j++) {
+            if (j >= nb)
+                continue;
+            int it = 0;
+
+            while (__hip_atomic_load(&prog, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <=
+                       j &&
+                   ++it < (1 << 24))
+                __builtin_amdgcn_s_sleep(1);
+            const double tj = t[j] * dinv[j];
+            double col[GP_NB];
+
+            t[j] = tj;
+#pragma unroll
+            for (int c = j + 1; c < GP_NB; c++)
+                col[c] = lc[j][c];
+            __builtin_amdgcn_sched_group_barrier(0x100, 32, 0);
+#pragma unroll
+            for (int c = j + 1; c < GP_NB; c++)
+                t[c] = fma(-col[c], tj, t[c]);
+        }
+        /* Lane k writes column k, one row of the inverse per store. */
+        if (lane < nb)
+#pragma unroll
+            for (int m = 0; m < GP_NB; m++)
+                if (m < nb)
+                    Linv[m * GP_NB + lane] = m >= lane ? t[m] : 0.0;
+    }
+    __syncthreads();
     if (tid == 0 && bad && *info == 0)
         *info = bad;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int e = tid + 1024 * i, r = e >> 6, c = e & 63;
+    for (int i = 0; i < 16; i++) {
+        const int e = tid + 256 * i, r = e >> 6, c = e & 63;
 
-        if (r < nb && c < nb) {
-            L[(long long)(k + r) * n + k + c] = c <= r ? f[r][c] : 0.0;
-            Linv[r * GP_NB + c] = r == c ? dinv[c] : r > c ? f[c][r] : 0.0;
-        }
+        if (r < nb && c < nb)
+            L[(long long)(k + r) * n + k + c] = lc[c][r];
     }
 }
 
@@ -574,7 +583,7 @@ static void gp_solve_run(struct ops *o, cl_mem K, int n, float noise, cl_mem F, 
                 if (b >= 2)
                     hip_check(hipStreamWaitEvent(s, aux_event(o->ocl, 2 * (b - 2) + 1), 0),
                               "hipStreamWaitEvent");
-                hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(1024), 0, s, A,
+                hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(256), 0, s, A,
                                    L, Lk, n, k, nb, lprev, (const int *)nullptr, spin_max,
                                    info_p);
                 hip_check(hipEventRecord(done_b, s), "hipEventRecord");
@@ -588,7 +597,7 @@ static void gp_solve_run(struct ops *o, cl_mem K, int n, float noise, cl_mem F, 
                                 (void *)&lprev, (void *)&ready, (void *)&spin_max,
                                 (void *)&info_p};
 
-                hip_check(hipExtLaunchKernel((const void *)chol_diag_kernel, dim3(1), dim3(1024),
+                hip_check(hipExtLaunchKernel((const void *)chol_diag_kernel, dim3(1), dim3(256),
                                              args, 0, s, nullptr, done_b, 0),
                           "hipExtLaunchKernel");
             }
