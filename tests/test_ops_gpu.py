@@ -189,6 +189,49 @@ def test_conv_shapes(shape, dev, ic, orc):
     assert err <= 1e-5, f"{shape}: {err:.2e}"
 
 
+# Same-size 3 x 3 convolutions at the edges of the Winograd kernel's
+# blocking: ELoFTR's 80 x 80 layers, outputs that end inside a block of
+# 8 x 16 pixels, a partial last block of output channels, maps smaller
+# than one 2 x 2 tile, channel counts below the kernel's minimum (which
+# take the direct path).
+WINO_SHAPES = [
+    # (nb, C, H, W, K, act)
+    (2, 256, 20, 20, 256, 2),
+    (2, 64, 40, 48, 64, 2),
+    (1, 64, 37, 45, 36, 1),
+    (2, 8, 17, 70, 32, 0),
+    (1, 128, 3, 2, 64, 3),
+    (1, 40, 50, 33, 96, 2),
+    (1, 32, 1, 1, 32, 0),
+]
+
+
+@pytest.mark.parametrize("shape", WINO_SHAPES, ids=[str(s) for s in WINO_SHAPES])
+def test_conv_winograd_edges(shape, dev, ic, orc):
+    """ops_conv2d_batch on 3 x 3 same-size convolutions (the Winograd
+    F(2 x 2, 3 x 3) kernel wherever it applies) against the oracle's direct
+    convolution."""
+    import ctypes as C
+    from oracle_lib import fp
+    nb, Cc, H, W, K, act = shape
+    print(f"[conv] winograd edges {shape}", flush=True)
+    rng = np.random.default_rng(300 + Cc + K)
+    x = rng.uniform(-1, 1, nb * Cc * H * W).astype(np.float32)
+    w = (rng.uniform(-1, 1, K * Cc * 9) / np.sqrt(Cc * 9)).astype(np.float32)
+    b = rng.uniform(-1, 1, K).astype(np.float32)
+    ref = np.zeros(nb * K * H * W, np.float32)
+    for i in range(nb):
+        orc.orc_conv2d(fp(x[i * Cc * H * W:]), Cc, H, W, fp(w), fp(b), K, 3, 3, 1, 1, 1, 1, 1,
+                       1, 1, None, None, None, act, 0.1, fp(ref[i * K * H * W:]))
+    X, Wt, B = dev.upload(x), dev.upload(w), dev.upload(b)
+    Y = dev.zeros(nb * K * H * W)
+    g = ic.geom(3, 3, 1, 1, 1, 1, 1, 1, 1)
+    dev.api.ops_conv2d_batch(dev.po, nb, X.mem, Cc * H * W, Cc, H, W, Wt.mem, B.mem, K,
+                             C.byref(g), None, None, None, act, 0.1, Y.mem, K * H * W)
+    err = opcases.rel_err(dev.read(Y, nb * K * H * W), ref)
+    assert err <= 1e-5, f"{shape}: {err:.2e}"
+
+
 LN_SHAPES = [
     # (rows, C, affine): the RoMa ViT rows (1024) and the float4 variants'
     # lane tails (C / 4 not a multiple of 64), the scalar form (C % 4 != 0).
