@@ -877,6 +877,66 @@ def cpu_baseline_refiners(side=288, H=864):
                       f"{H}x{H}; {thr} OpenMP threads, {nproc} CPUs visible"}
 
 
+def bench_host_loop(ic, dev, net, pairs, steps):
+    """ELoFTR over host-resident pairs, PCIe included: eloftr_match (a
+    blocking upload from pageable memory, the device stage, the match
+    read) against the overlapped loop that ocl_write_async allows (pair
+    t + 1 copied into page-locked memory and uploaded into the other
+    device slot while pair t computes, eloftr_match_enqueue / collect)."""
+    import ctypes as C
+    a = dev.api
+    H, W = pairs[0][0].shape
+    n = H * W
+    seq = [pairs[t % len(pairs)] for t in range(steps)]
+    for g0, g1 in seq[:2]:
+        a.eloftr_match(net.m, g0.ctypes.data, g1.ctypes.data, None, 1)
+    dev.finish()
+    t0 = time.perf_counter()
+    for g0, g1 in seq:
+        a.eloftr_match(net.m, g0.ctypes.data, g1.ctypes.data, None, 1)
+    blocking = (time.perf_counter() - t0) * 1e3 / steps
+
+    ptr = [a.ocl_host_alloc(dev.pb, 8 * n) for _ in range(2)]
+    view = [np.ctypeslib.as_array((C.c_float * (2 * n)).from_address(p)) for p in ptr]
+    slots = [(dev.alloc(4 * n), dev.alloc(4 * n)) for _ in range(2)]
+    tickets = [None, None]
+
+    def upload(t):
+        s = t % 2
+        if tickets[s] is not None:
+            a.ocl_write_wait(dev.pb, tickets[s][1])
+        view[s][:n] = seq[t][0].ravel()
+        view[s][n:] = seq[t][1].ravel()
+        tickets[s] = (a.ocl_write_async(dev.pb, slots[s][0].mem, 0, ptr[s], 4 * n),
+                      a.ocl_write_async(dev.pb, slots[s][1].mem, 0, ptr[s] + 4 * n, 4 * n))
+
+    def loop(k):
+        upload(0)
+        for t in range(k):
+            s = t % 2
+            a.ocl_write_join(dev.pb, tickets[s][0])
+            a.ocl_write_join(dev.pb, tickets[s][1])
+            a.eloftr_match_enqueue(net.m, slots[s][0].mem, slots[s][1].mem)
+            if t + 1 < k:
+                upload(t + 1)
+            a.eloftr_match_collect(net.m)
+
+    try:
+        loop(2)
+        dev.finish()
+        t0 = time.perf_counter()
+        loop(steps)
+        overlapped = (time.perf_counter() - t0) * 1e3 / steps
+    finally:
+        for p in ptr:
+            a.ocl_host_free(p)
+    return {"workload": f"ELoFTR {H}x{W} grey pairs in host memory, {steps} in a row, "
+                        "upload + device stage + match read (host wall clock)",
+            "blocking_pairs_per_s": round(1000.0 / blocking, 3),
+            "overlapped_pairs_per_s": round(1000.0 / overlapped, 3),
+            "ms_per_pair": {"blocking": round(blocking, 4), "overlapped": round(overlapped, 4)}}
+
+
 def copy_calibration(dev, mib):
     """One device-to-device copy of mib MiB: the known-size reference that
     scales the HBM byte counters of a rocprofv3 --pmc run."""
@@ -1141,6 +1201,7 @@ def main():
                     "with B = A shifted by (8, 16) px",
         "coarse_matches": nm_m, "pairs_per_s": round(1000.0 / ms_m, 3),
         "ms_per_pair": round(ms_m, 4)}
+    host_loop = bench_host_loop(ic, dev, net, [(g0, g1), (m0, m1)], args.steps)
 
     net.close()
     roma = None
@@ -1186,7 +1247,8 @@ def main():
     # reference case) go to a file and to stderr; the JSON line on stdout
     # keeps the figures, so that the whole line fits a log's tail.
     detail = {"eloftr640": {"kernels": kernels, "with_matches": with_matches,
-                            "graph": graph_leg, "fine_ms_at_max_matches": round(fine_nmax_ms, 4)},
+                            "graph": graph_leg, "host_loop": host_loop,
+                            "fine_ms_at_max_matches": round(fine_nmax_ms, 4)},
               "roma560": roma, "cpu_baseline": cpu, **extra}
     write_detail(detail)
     rf = {"kernel": "conv_wino (3x3 stride-1 conv, Winograd F(2x2,3x3) on fp32 MFMA)",
@@ -1221,6 +1283,8 @@ def main():
         "eloftr_with_matches": {"coarse_matches": nm_m, "pairs_per_s": with_matches["pairs_per_s"],
                                 "ms_per_pair": with_matches["ms_per_pair"]},
         "eloftr_graph_pairs_per_s": graph_leg["pairs_per_s"],
+        "eloftr_host_pairs_per_s": {"blocking": host_loop["blocking_pairs_per_s"],
+                                    "overlapped": host_loop["overlapped_pairs_per_s"]},
         "pipeline_tflops": round(fl["total"] / (ms * 1e-3) / 1e12, 2),
         "roma560": _short_roma(roma),
         **_short_extra(extra),

@@ -49,6 +49,9 @@ class OclBackend(C.Structure):
         ("aux_stream", C.c_void_p),
         ("aux_events", C.c_void_p),
         ("aux_nevents", C.c_int),
+        ("copy_stream", C.c_void_p),
+        ("copy_events", C.c_void_p),
+        ("copy_tickets", C.c_longlong),
     ]
 
 
@@ -90,6 +93,11 @@ SIGNATURES = {
     "ocl_upload": (Mem, [_B, _P, C.c_size_t, _S]),
     "ocl_write": (None, [_B, Mem, C.c_size_t, _P, C.c_size_t]),
     "ocl_read": (None, [_B, Mem, C.c_size_t, _P, C.c_size_t]),
+    "ocl_host_alloc": (C.c_void_p, [_B, C.c_size_t]),
+    "ocl_host_free": (None, [C.c_void_p]),
+    "ocl_write_async": (C.c_longlong, [_B, Mem, C.c_size_t, _P, C.c_size_t]),
+    "ocl_write_join": (None, [_B, C.c_longlong]),
+    "ocl_write_wait": (None, [_B, C.c_longlong]),
     "ocl_release": (None, [C.POINTER(Mem)]),
     "ocl_copy": (None, [_B, Mem, C.c_size_t, Mem, C.c_size_t, C.c_size_t]),
     "ocl_copy_rect": (None, [_B, Mem, C.c_size_t, C.c_size_t, Mem, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t]),

@@ -346,6 +346,13 @@ extern "C" void ocl_free(struct ocl_backend *ocl)
         free(ocl->aux_events);
         if (ocl->aux_stream)
             (void)hipStreamDestroy((hipStream_t)ocl->aux_stream);
+        if (ocl->copy_stream) {
+            (void)hipStreamSynchronize((hipStream_t)ocl->copy_stream);
+            for (int k = 0; k < OCL_COPY_TICKETS; k++)
+                (void)hipEventDestroy(((hipEvent_t *)ocl->copy_events)[k]);
+            free(ocl->copy_events);
+            (void)hipStreamDestroy((hipStream_t)ocl->copy_stream);
+        }
         (void)hipStreamDestroy((hipStream_t)ocl->stream);
     }
     memset(ocl, 0, sizeof(*ocl));
@@ -405,6 +412,102 @@ extern "C" void ocl_write(struct ocl_backend *ocl, cl_mem dst, size_t off,
                       "hipMemcpyAsync (write)");
     icoreg::hip_check(hipStreamSynchronize(icoreg::stream_of(ocl)),
                       "hipStreamSynchronize (write)");
+    ICOREG_API_END
+}
+
+/* ---- copies beside the stream ----------------------------------------- */
+
+namespace {
+
+/* Fatal while the library's stream is being recorded into a graph: a
+ * copy on another stream would not be part of it. */
+void not_capturing(struct ocl_backend *ocl, const char *what)
+{
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+
+    icoreg::hip_check(hipStreamIsCapturing(icoreg::stream_of(ocl), &st), "hipStreamIsCapturing");
+    if (st != hipStreamCaptureStatusNone)
+        icoreg_fatal("%s: not allowed while a graph is being recorded", what);
+}
+
+hipEvent_t copy_event(struct ocl_backend *ocl, long long ticket, const char *what)
+{
+    if (ticket < 0 || ticket >= ocl->copy_tickets ||
+        ticket < ocl->copy_tickets - OCL_COPY_TICKETS)
+        icoreg_fatal("%s: ticket %lld is not one of the last %d copies (%lld queued)", what,
+                     ticket, OCL_COPY_TICKETS, ocl->copy_tickets);
+    return ((hipEvent_t *)ocl->copy_events)[ticket % OCL_COPY_TICKETS];
+}
+
+} // namespace
+
+extern "C" void *ocl_host_alloc(struct ocl_backend *ocl, size_t n)
+{
+    void *p = nullptr;
+    ICOREG_API_BEGIN
+    icoreg::hip_check(hipSetDevice(ocl->device), "hipSetDevice");
+    icoreg::hip_check(hipHostMalloc(&p, n ? n : 4, hipHostMallocDefault), "hipHostMalloc");
+    ICOREG_API_END_RET(p)
+}
+
+extern "C" void ocl_host_free(void *p)
+{
+    if (p)
+        (void)hipHostFree(p);
+}
+
+extern "C" long long ocl_write_async(struct ocl_backend *ocl, cl_mem dst, size_t off,
+                                     const void *src, size_t n)
+{
+    long long t = -1;
+    ICOREG_API_BEGIN
+    not_capturing(ocl, "ocl_write_async");
+    icoreg::need_bytes(dst, (long long)off, (long long)n, "ocl_write_async", "destination");
+    if (!ocl->copy_stream) {
+        hipStream_t cs;
+        hipEvent_t *ev = (hipEvent_t *)calloc(OCL_COPY_TICKETS, sizeof(hipEvent_t));
+
+        if (!ev)
+            icoreg_fatal("ocl_write_async: out of host memory");
+        icoreg::hip_check(hipSetDevice(ocl->device), "hipSetDevice");
+        for (int k = 0; k < OCL_COPY_TICKETS; k++)
+            icoreg::hip_check(hipEventCreateWithFlags(&ev[k], hipEventDisableTiming),
+                              "hipEventCreate (copy)");
+        icoreg::hip_check(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking),
+                          "hipStreamCreate (copy)");
+        ocl->copy_events = ev;
+        ocl->copy_stream = (void *)cs;
+    }
+    {
+        hipStream_t cs = (hipStream_t)ocl->copy_stream;
+        hipEvent_t ev = ((hipEvent_t *)ocl->copy_events)[ocl->copy_tickets % OCL_COPY_TICKETS];
+
+        if (n)
+            icoreg::hip_check(hipMemcpyAsync((char *)dst->ptr + off, src, n,
+                                             hipMemcpyHostToDevice, cs),
+                              "hipMemcpyAsync (write_async)");
+        icoreg::hip_check(hipEventRecord(ev, cs), "hipEventRecord (write_async)");
+        t = ocl->copy_tickets++;
+    }
+    ICOREG_API_END_RET(t)
+}
+
+extern "C" void ocl_write_join(struct ocl_backend *ocl, long long ticket)
+{
+    ICOREG_API_BEGIN
+    not_capturing(ocl, "ocl_write_join");
+    icoreg::hip_check(hipStreamWaitEvent(icoreg::stream_of(ocl),
+                                         copy_event(ocl, ticket, "ocl_write_join"), 0),
+                      "hipStreamWaitEvent (write_join)");
+    ICOREG_API_END
+}
+
+extern "C" void ocl_write_wait(struct ocl_backend *ocl, long long ticket)
+{
+    ICOREG_API_BEGIN
+    not_capturing(ocl, "ocl_write_wait");
+    icoreg::hip_check(hipEventSynchronize(copy_event(ocl, ticket, "ocl_write_wait")),
+                      "hipEventSynchronize (write_wait)");
     ICOREG_API_END
 }
 

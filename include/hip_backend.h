@@ -1,8 +1,9 @@
 /* SPDX-License-Identifier: Unlicense */
 
 /* Device backend of the matcher tensor path on one AMD Instinct MI355X
- * (gfx950) through the HIP runtime: one device, one in-order stream,
- * hipMalloc-resident buffers, blocking host transfers.
+ * (gfx950) through the HIP runtime: one device, one in-order stream for
+ * every launch, hipMalloc-resident buffers, blocking host transfers (and,
+ * beside them, optional uploads on a copy stream: ocl_write_async).
  *
  * Drop-in for the OpenCL backend of i.coregistration.opencl
  * (ocl_backend.h:15-61): the identifiers its callers use are kept
@@ -62,6 +63,12 @@ struct ocl_backend {
     void *aux_stream;
     void *aux_events;
     int aux_nevents;
+    /* The copy stream of ocl_write_async (default priority), its ring of
+     * OCL_COPY_TICKETS events and the number of copies queued on it, made
+     * on first use; released by ocl_free. */
+    void *copy_stream;
+    void *copy_events;
+    long long copy_tickets;
 };
 
 /* Select the device and create the stream. device_opt: "auto", "gpu"
@@ -109,6 +116,40 @@ void ocl_write(struct ocl_backend *ocl, cl_mem dst, size_t off, const void *src,
                size_t n);
 void ocl_read(struct ocl_backend *ocl, cl_mem src, size_t off, void *dst,
               size_t n);
+
+/* No counterpart in the reference, whose tile loop writes each tile with
+ * a blocking transfer and then computes it (main.c:796-809 through
+ * matcher.run, ocl_backend.c:304-311): host-to-device copies that run
+ * beside the library's stream, so that a caller can upload the next tile
+ * while the current one computes (see eloftr_match_enqueue,
+ * roma_coarse_device).
+ *
+ * ocl_host_alloc: n bytes of page-locked host memory (hipHostMalloc), the
+ * kind of source a copy needs to overlap anything; ocl_host_free frees it.
+ *
+ * ocl_write_async: queue n bytes from src to dst at byte offset off on the
+ * backend's copy stream and return the copy's ticket (>= 0). The copy
+ * does not wait for launches already queued on the library's stream, so
+ * dst's range must not be one they still read (upload into a second
+ * buffer).
+ *
+ * ocl_write_join: launches queued on the library's stream after this call
+ * see the copy's data (the stream waits on the device; the host does not
+ * block).
+ *
+ * ocl_write_wait: the host blocks until the copy is done; src may then be
+ * rewritten.
+ *
+ * A ticket stays valid while fewer than OCL_COPY_TICKETS later copies have
+ * been queued; an older one is an error. All three are errors while a
+ * graph is being recorded (ocl_graph_begin). */
+#define OCL_COPY_TICKETS 64
+void *ocl_host_alloc(struct ocl_backend *ocl, size_t n);
+void ocl_host_free(void *p);
+long long ocl_write_async(struct ocl_backend *ocl, cl_mem dst, size_t off, const void *src,
+                          size_t n);
+void ocl_write_join(struct ocl_backend *ocl, long long ticket);
+void ocl_write_wait(struct ocl_backend *ocl, long long ticket);
 
 /* Free a buffer and NULL the handle. ocl_backend.h:61. */
 void ocl_release(cl_mem *m);

@@ -132,13 +132,17 @@ def test_warp_sample(dev, ic, orc, C, H, W, smooth):
                                             (512, 35, 37, 3, True), (100, 23, 30, 2, True),
                                             (7, 13, 9, 1, True), (64, 21, 19, 7, True),
                                             (512, 108, 108, 3, True), (256, 216, 216, 2, True),
-                                            (37, 20, 22, 3, False), (192, 64, 64, 3, False)])
+                                            (37, 20, 22, 3, False), (192, 64, 64, 3, False),
+                                            (40, 36, 44, 4, True), (64, 33, 46, 3, True),
+                                            (16, 8, 12, 1, False), (512, 108, 108, 3, False),
+                                            (36, 17, 28, 2, True), (128, 216, 216, 2, False)])
 def test_local_corr(dev, ic, orc, C, H, W, r, smooth):
     """Random warps (most 4 x 4 patches scatter: the per-cell path) and
     smooth ones (the matrix-core path over the patch's window box, with a
     few broken cells), up to the refiner config's 1/8 and 1/4 shapes at
-    864 x 864; channel counts that are multiples of 4 (the cell-major
-    form, maps transposed first) and others (channel-major reads)."""
+    864 x 864, radius 1 to 7; channel counts that are multiples of 4 (the
+    cell-major form, maps transposed first) and others (channel-major
+    reads)."""
     print(f"[roma] local_corr C={C} {H}x{W} r={r} smooth={smooth}", flush=True)
     rng = np.random.default_rng(C + r)
     f0 = rng.standard_normal((C, H, W)).astype(np.float32)
