@@ -230,10 +230,12 @@ __global__ void __launch_bounds__(256)
  * one L2.
  *
  * Two forms:
- *  - cell-major (C % 4 == 0, local_corr_cm_kernel): both maps are first
+ *  - cell-major (C % 4 == 0, local_corr_cm_kernel): f2 is first
  *    transposed to (n x C), so that a box cell's channels are one
- *    contiguous row: every operand load is 16 bytes of a lane's own
- *    4 channels, and a 16-channel chunk of a cell is one 64-byte piece.
+ *    contiguous row: every box operand load is 16 bytes of a lane's own
+ *    4 channels, and a 16-channel chunk of a cell is one 64-byte piece;
+ *    f1 (16 cells a patch, each read once) stays channel-major, four
+ *    4-byte loads for a lane's 4 channels.
  *    Each of the 4 waves takes all box tiles over a quarter of the
  *    channels (so a patch or box row is loaded once per block), and the
  *    quarters' products meet in LDS. The per-cell path puts 16
@@ -519,24 +521,44 @@ __device__ __forceinline__ lc_f4 lc_load4(__amdgpu_buffer_rsrc_t r, unsigned off
     return __builtin_bit_cast(lc_f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
+/* Four channels of one cell of a channel-major map: floats at byte
+ * offsets off, off + ps, off + 2 ps, off + 3 ps (ps: a channel plane's
+ * bytes); LC_OOB gives zeros. */
+__device__ __forceinline__ lc_f4 lc_load_planes4(__amdgpu_buffer_rsrc_t r, unsigned off,
+                                                 unsigned ps)
+{
+    lc_f4 v;
+
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+        v[s] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)(off == LC_OOB ? LC_OOB
+                                                                             : off + s * ps),
+                                                        0, 0));
+    return v;
+}
+
 /* NQ box tiles of the cell-major tiled path for one wave: the 16-channel
- * chunks kw, kw + 4, ... (nch chunks in all) into acc[t]. ra, rb: windows
- * over the two cell-major maps; ao / bo[t]: byte offset of the lane's
- * patch cell / box cell row of tile t (LC_OOB: none), plus 16 (4 kq)
- * for its channels. A chunk past C or a missing cell loads zeros from
- * past the window's end, so that the loop has no branches and two
- * chunks load while two multiply. */
+ * chunks kw, kw + 4, ... (nch chunks in all) into acc[t]. ra: window
+ * over f1 (channel-major), ao: byte offset of the lane's patch cell in
+ * its first channel's plane (channel 4 kq; LC_OOB: none), ps: a plane's
+ * bytes; rb: window over the cell-major f2, bo[t]: byte offset of the
+ * lane's box cell row of tile t (LC_OOB: none) plus 16 (4 kq) for its
+ * channels. A chunk past C or a missing cell loads zeros from past the
+ * window's end, so that the loop has no branches and two chunks load
+ * while two multiply. */
 template <int NQ>
 __device__ __forceinline__ void lc_cm_tiles(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
-                                            unsigned ao, const unsigned (&bo)[9], int kw, int nch,
-                                            int C, int kq, float rc, lc_f4 (&acc)[9])
+                                            unsigned ao, unsigned ps, const unsigned (&bo)[9],
+                                            int kw, int nch, int C, int kq, float rc,
+                                            lc_f4 (&acc)[9])
 {
     auto load = [&](int q, lc_f4 &a, lc_f4 (&b)[NQ]) {
         const int c = q * 16 + 4 * kq;
         const bool cok = q < nch && c < C;
         const unsigned cb = 64u * q;
 
-        a = lc_load4(ra, cok && ao != LC_OOB ? ao + cb : LC_OOB) * rc;
+        a = lc_load_planes4(ra, cok && ao != LC_OOB ? ao + 16u * q * ps : LC_OOB, ps) * rc;
 #pragma unroll
         for (int t = 0; t < NQ; t++)
             b[t] = lc_load4(rb, cok && bo[t] != LC_OOB ? bo[t] + cb : LC_OOB);
@@ -569,10 +591,13 @@ __device__ __forceinline__ void lc_cm_tiles(__amdgpu_buffer_rsrc_t ra, __amdgpu_
     }
 }
 
-/* Cell-major form: t1, t2 are f1, f2 as (n x C) with rows ld floats
- * apart (C % 4 == 0, ld % 4 == 0, the maps 16-byte aligned). */
+/* Cell-major form: f1 (C x n) as it is, t2 is f2 as (n x C) with rows
+ * ld floats apart (C % 4 == 0, ld % 4 == 0, t2 16-byte aligned, C n 4 and
+ * n ld 4 below 2^31). The patch's own cells are 16 of n, read a channel
+ * plane at a time; the box cells, read (2 r + 2)^2-fold over the
+ * patches, are the ones worth a contiguous channel row. */
 __global__ void __launch_bounds__(256)
-    local_corr_cm_kernel(const float *__restrict__ t1, const float *__restrict__ t2, int C,
+    local_corr_cm_kernel(const float *__restrict__ f1, const float *__restrict__ t2, int C,
                          int ld, int H, int W, int r, const float *__restrict__ flow,
                          float *__restrict__ out, int coff)
 {
@@ -610,9 +635,10 @@ __global__ void __launch_bounds__(256)
          * outputs add the two planes. */
         const int nt = (nb + 15) >> 4, nch = (C + 15) >> 4;
         const int acell = pt.cid[m];
-        const unsigned bytes = (unsigned)n * (unsigned)ld * 4u;
-        const __amdgpu_buffer_rsrc_t ra = lc_rsrc(t1, bytes), rb = lc_rsrc(t2, bytes);
-        const unsigned ao = acell >= 0 ? ((unsigned)acell * ld + 4 * kq) * 4u : LC_OOB;
+        const unsigned pb = (unsigned)n * 4u; /* bytes of a channel plane */
+        const __amdgpu_buffer_rsrc_t ra = lc_rsrc(f1, (unsigned)C * pb);
+        const __amdgpu_buffer_rsrc_t rb = lc_rsrc(t2, (unsigned)n * (unsigned)ld * 4u);
+        const unsigned ao = acell >= 0 ? (4u * kq * (unsigned)n + (unsigned)acell) * 4u : LC_OOB;
         const bool four = nt <= 9;
         const int gp = four ? LC_PG : LC_GS, gsz = four ? 9 : 8;
         float *Gw = G + (four ? wv : (wv & 1)) * LC_T * gp;
@@ -633,31 +659,31 @@ __global__ void __launch_bounds__(256)
             }
             switch (nq) {
             case 1:
-                lc_cm_tiles<1>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                lc_cm_tiles<1>(ra, rb, ao, pb, bo, wv, nch, C, kq, rc, acc);
                 break;
             case 2:
-                lc_cm_tiles<2>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                lc_cm_tiles<2>(ra, rb, ao, pb, bo, wv, nch, C, kq, rc, acc);
                 break;
             case 3:
-                lc_cm_tiles<3>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                lc_cm_tiles<3>(ra, rb, ao, pb, bo, wv, nch, C, kq, rc, acc);
                 break;
             case 4:
-                lc_cm_tiles<4>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                lc_cm_tiles<4>(ra, rb, ao, pb, bo, wv, nch, C, kq, rc, acc);
                 break;
             case 5:
-                lc_cm_tiles<5>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                lc_cm_tiles<5>(ra, rb, ao, pb, bo, wv, nch, C, kq, rc, acc);
                 break;
             case 6:
-                lc_cm_tiles<6>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                lc_cm_tiles<6>(ra, rb, ao, pb, bo, wv, nch, C, kq, rc, acc);
                 break;
             case 7:
-                lc_cm_tiles<7>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                lc_cm_tiles<7>(ra, rb, ao, pb, bo, wv, nch, C, kq, rc, acc);
                 break;
             case 8:
-                lc_cm_tiles<8>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                lc_cm_tiles<8>(ra, rb, ao, pb, bo, wv, nch, C, kq, rc, acc);
                 break;
             default:
-                lc_cm_tiles<9>(ra, rb, ao, bo, wv, nch, C, kq, rc, acc);
+                lc_cm_tiles<9>(ra, rb, ao, pb, bo, wv, nch, C, kq, rc, acc);
             }
             /* Lane l holds rows 4 (l / 16) + v of the tile's 16 x 16 block,
              * column l % 16. */
@@ -687,15 +713,16 @@ __global__ void __launch_bounds__(256)
          * of a row then added by DPP; S of cell mm over its window goes to
          * row mm of G. */
         const int np2 = ps * ps;
-        const unsigned bytes = (unsigned)n * (unsigned)ld * 4u;
-        const __amdgpu_buffer_rsrc_t ra = lc_rsrc(t1, bytes), rb = lc_rsrc(t2, bytes);
+        const unsigned pb = (unsigned)n * 4u;
+        const __amdgpu_buffer_rsrc_t ra = lc_rsrc(f1, (unsigned)C * pb);
+        const __amdgpu_buffer_rsrc_t rb = lc_rsrc(t2, (unsigned)n * (unsigned)ld * 4u);
 
         for (int mm = wv; mm < LC_T; mm += 4) {
             const int i = pt.cid[mm];
 
             if (i < 0 || !pt.okc[mm])
                 continue;
-            const unsigned ao = (unsigned)i * ld * 4u;
+            const unsigned ao = (unsigned)i * 4u;
 
             for (int e0 = 0; e0 < np2; e0 += 16) {
                 unsigned bo[4];
@@ -711,7 +738,7 @@ __global__ void __launch_bounds__(256)
                     sum[u] = 0.0f;
                 }
                 for (int c = 4 * m; c < C; c += 64) {
-                    const lc_f4 a = lc_load4(ra, ao + 4u * c) * rc;
+                    const lc_f4 a = lc_load_planes4(ra, ao + (unsigned)c * pb, pb) * rc;
 
 #pragma unroll
                     for (int u = 0; u < 4; u++) {
@@ -987,23 +1014,19 @@ extern "C" void roma_warp_sample(struct ops *o, cl_mem in, int C, int H, int W,
     ICOREG_API_END
 }
 
-/* (C x n) to (n x C) for both maps, output rows ld floats apart: one
- * 64-cell x 64-channel tile per block through LDS, blocks 0 .. T - 1 on
- * f1, T .. 2 T - 1 on f2. VEC (n % 4 == 0, C % 4 == 0, ld % 4 == 0, both
- * inputs 16-byte aligned): 16-byte loads along the cells and 16-byte
- * stores along the channels. */
+/* (C x n) to (n x C), output rows ld floats apart: one 64-cell x
+ * 64-channel tile per block through LDS. VEC (n % 4 == 0, C % 4 == 0,
+ * ld % 4 == 0, the input 16-byte aligned): 16-byte loads along the cells
+ * and 16-byte stores along the channels. */
 template <bool VEC>
 __global__ void __launch_bounds__(256)
-    lc_transpose_kernel(const float *__restrict__ f1, const float *__restrict__ f2,
-                        float *__restrict__ o1, float *__restrict__ o2, int C, int ld, int n)
+    lc_transpose_kernel(const float *__restrict__ in, float *__restrict__ out, int C, int ld,
+                        int n)
 {
     __shared__ float t[64][65];
     const int tid = threadIdx.x;
-    const int tiles_i = (n + 63) / 64, tiles = tiles_i * ((C + 63) / 64);
-    const int z = (int)blockIdx.x >= tiles, v = blockIdx.x - z * tiles;
+    const int tiles_i = (n + 63) / 64, v = blockIdx.x;
     const int i0 = (v % tiles_i) * 64, c0 = (v / tiles_i) * 64;
-    const float *in = z ? f2 : f1;
-    float *out = z ? o2 : o1;
 
     if (VEC) {
         const int j4 = (tid & 15) * 4, row = tid >> 4;
@@ -1091,26 +1114,25 @@ extern "C" void roma_local_corr(struct ops *o, cl_mem f1, cl_mem f2, int C,
                 ld += 64;
         }
         if (C % 4 == 0 && ld * n * 4 < (1LL << 31)) {
-            /* Both maps cell-major into the scratch buffer (its start is
-             * 256-byte aligned, and ld % 4 == 0 keeps every row 16-byte
-             * aligned), then the cell-major kernel (its buffer windows
-             * take byte offsets below 2^31). */
+            /* f2 cell-major into the scratch buffer (its start is 256-byte
+             * aligned, and ld % 4 == 0 keeps every row 16-byte aligned),
+             * then the cell-major kernel (its buffer windows take byte
+             * offsets below 2^31; C n 4 <= ld n 4). */
             const size_t cn = (size_t)ld * n;
-            cl_mem sc = scratch_get(o, 2 * cn * sizeof(float));
-            float *t1 = (float *)sc->ptr, *t2 = t1 + cn;
-            const long long ttiles = 2LL * ((n + 63) / 64) * ((C + 63) / 64);
-            const bool vec = n % 4 == 0 && ((uintptr_t)cfptr(f1) & 15) == 0 &&
-                             ((uintptr_t)cfptr(f2) & 15) == 0;
+            cl_mem sc = scratch_get(o, cn * sizeof(float));
+            float *t2 = (float *)sc->ptr;
+            const long long ttiles = ((n + 63) / 64) * ((C + 63) / 64);
+            const bool vec = n % 4 == 0 && ((uintptr_t)cfptr(f2) & 15) == 0;
 
             if (ttiles >= (1LL << 31))
                 icoreg_fatal("%s: transpose grid too large", op);
             if (vec)
                 hipLaunchKernelGGL(lc_transpose_kernel<true>, dim3((unsigned)ttiles), dim3(256),
-                                   0, st, cfptr(f1), cfptr(f2), t1, t2, C, (int)ld, (int)n);
+                                   0, st, cfptr(f2), t2, C, (int)ld, (int)n);
             else
                 hipLaunchKernelGGL(lc_transpose_kernel<false>, dim3((unsigned)ttiles), dim3(256),
-                                   0, st, cfptr(f1), cfptr(f2), t1, t2, C, (int)ld, (int)n);
-            hipLaunchKernelGGL(local_corr_cm_kernel, grid, dim3(256), 0, st, (const float *)t1,
+                                   0, st, cfptr(f2), t2, C, (int)ld, (int)n);
+            hipLaunchKernelGGL(local_corr_cm_kernel, grid, dim3(256), 0, st, cfptr(f1),
                                (const float *)t2, C, (int)ld, H, W, r, cfptr(flow), fptr(out),
                                coff);
         }
