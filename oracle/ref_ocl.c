@@ -37,7 +37,18 @@
  *                                OUT: n D floats
  *         cls:n:ld:C:res:L:OUT   roma_cls_to_flow as roma.c:898-919 on
  *                                L (n ld floats); OUT: flow (2 n floats),
- *                                cert (n floats) */
+ *                                cert (n floats)
+ *         gemmx:M:N:K:transb:act:A:B:BIAS:OUT   ops_gemm, C = act(A B +
+ *                                bias), A M x K, B K x N (N x K when
+ *                                transb); OUT: M N floats
+ *         lnx:rows:C:eps:X:G:BETA:OUT           ops_layernorm
+ *         smx:rows:L:scale:S:OUT                ops_softmax_rows
+ *         attnx:Nq:Nk:nh:d:scale:Q:K:V:OUT      ops_attention, rows of
+ *                                nh d floats, no key mask
+ *         lcx:C:h:w:r:F1:F2:FLOW:OUT            roma_local_corr
+ *         warpx:C:h:w:IN:FLOW:OUT               roma_warp_sample
+ *         gridx:C:H:W:n:align:IN:GRID:OUT       ops_grid_sample
+ *         dwx:C:H:W:IN:WT:BIAS:OUT              roma_dwconv5 */
 
 #define CL_TARGET_OPENCL_VERSION 120
 #include <CL/cl.h>
@@ -845,6 +856,228 @@ static void exec_cls(const char *spec, int n, int ld, int C, int res, const char
     free(out);
 }
 
+/* A file of n floats into a new buffer. */
+static cl_mem file_buf(const char *path, size_t n, float **host)
+{
+    float *h = read_file(path, n * 4);
+    cl_mem m = buf(n * 4, h);
+
+    if (host)
+        *host = h;
+    else
+        free(h);
+    return m;
+}
+
+/* A buffer of n floats to a file. */
+static void buf_file(cl_mem m, size_t n, const char *path)
+{
+    float *h = malloc(n * 4);
+
+    readb(m, n * 4, h);
+    write_file(path, h, n * 4);
+    free(h);
+}
+
+/* gemmx: C = act(A B + bias), ops_gemm's dispatch (ops.c:148-188). */
+static void exec_gemm(const char *spec, int M, int N, int K, int transb, int act, const char *fa,
+                      const char *fb, const char *fbias, const char *fo)
+{
+    cl_mem ba = file_buf(fa, (size_t)M * K, NULL), bb = file_buf(fb, (size_t)K * N, NULL);
+    cl_mem bi = file_buf(fbias, (size_t)N, NULL), bc = buf((size_t)M * N * 4, NULL);
+    const double ms = gemm(M, N, K, mat(ba, 0, K, 0), mat(bb, 0, transb ? K : N, 0), transb,
+                           mat(bc, 0, N, 0), 1, 1, bi, 0, NULL, 0, 1.0f, act);
+
+    buf_file(bc, (size_t)M * N, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"%s\", \"ms\": %.5f}\n", spec, last_gemm, ms);
+    clReleaseMemObject(ba);
+    clReleaseMemObject(bb);
+    clReleaseMemObject(bi);
+    clReleaseMemObject(bc);
+}
+
+/* lnx: layernorm over rows of C, ops_layernorm's dispatch (ops.c:412-429). */
+static void exec_layernorm(const char *spec, int rows, int C, float eps, const char *fx,
+                           const char *fg, const char *fbeta, const char *fo)
+{
+    cl_mem bx = file_buf(fx, (size_t)rows * C, NULL), bg = file_buf(fg, (size_t)C, NULL);
+    cl_mem bb = file_buf(fbeta, (size_t)C, NULL), by = buf((size_t)rows * C * 4, NULL);
+    size_t ls = row_group(C), gs = (size_t)rows * ls;
+
+    SET(k_layernorm, 0, bx);
+    SET(k_layernorm, 1, by);
+    SET(k_layernorm, 2, bg);
+    SET(k_layernorm, 3, bb);
+    SET(k_layernorm, 4, (cl_int)C);
+    SET(k_layernorm, 5, (cl_float)eps);
+    SET(k_layernorm, 6, (cl_int)0);
+    SET(k_layernorm, 7, (cl_float)0.0f);
+    launch(k_layernorm, 1, &gs, &ls);
+    buf_file(by, (size_t)rows * C, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"layernorm\"}\n", spec);
+    clReleaseMemObject(bx);
+    clReleaseMemObject(bg);
+    clReleaseMemObject(bb);
+    clReleaseMemObject(by);
+}
+
+/* smx: softmax over rows of L in place, ops_softmax_rows' dispatch
+ * (ops.c:432-442). */
+static void exec_softmax(const char *spec, int rows, int L, float scale, const char *fs,
+                         const char *fo)
+{
+    cl_mem bs = file_buf(fs, (size_t)rows * L, NULL);
+    size_t ls = row_group(L), gs = (size_t)rows * ls;
+
+    SET(k_softmax, 0, bs);
+    SET(k_softmax, 1, (cl_int)L);
+    SET(k_softmax, 2, (cl_float)scale);
+    launch(k_softmax, 1, &gs, &ls);
+    buf_file(bs, (size_t)rows * L, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"softmax_rows\"}\n", spec);
+    clReleaseMemObject(bs);
+}
+
+/* attnx: heads of d columns in rows of nh d floats, no key mask,
+ * ops_attention's dispatch (ops.c:443-474). */
+static void exec_attention(const char *spec, int Nq, int Nk, int nh, int d, float scale,
+                           const char *fq, const char *fk, const char *fv, const char *fo)
+{
+    const int ld = nh * d;
+    const cl_long zero = 0;
+    const cl_mem none = NULL;
+    cl_mem bq = file_buf(fq, (size_t)Nq * ld, NULL), bk = file_buf(fk, (size_t)Nk * ld, NULL);
+    cl_mem bv = file_buf(fv, (size_t)Nk * ld, NULL), bo = buf((size_t)Nq * ld * 4, NULL);
+    size_t gs[3] = {16, (size_t)(Nq + 15) / 16 * 16, (size_t)nh}, ls[3] = {16, 16, 1};
+
+    SET(k_attention, 0, bq);
+    SET(k_attention, 1, zero);
+    SET(k_attention, 2, (cl_int)ld);
+    SET(k_attention, 3, bk);
+    SET(k_attention, 4, zero);
+    SET(k_attention, 5, (cl_int)ld);
+    SET(k_attention, 6, bv);
+    SET(k_attention, 7, zero);
+    SET(k_attention, 8, (cl_int)ld);
+    SET(k_attention, 9, bo);
+    SET(k_attention, 10, zero);
+    SET(k_attention, 11, (cl_int)ld);
+    SET(k_attention, 12, (cl_int)Nq);
+    SET(k_attention, 13, (cl_int)Nk);
+    SET(k_attention, 14, (cl_int)d);
+    SET(k_attention, 15, (cl_float)scale);
+    SET(k_attention, 16, none);
+    launch(k_attention, 3, gs, ls);
+    buf_file(bo, (size_t)Nq * ld, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"attention\"}\n", spec);
+    clReleaseMemObject(bq);
+    clReleaseMemObject(bk);
+    clReleaseMemObject(bv);
+    clReleaseMemObject(bo);
+}
+
+/* lcx: roma_local_corr as roma.c:956-968 (output channels from 0). */
+static void exec_localcorr(const char *spec, int C, int h, int w, int r, const char *f1,
+                           const char *f2, const char *ffl, const char *fo)
+{
+    const size_t n = (size_t)h * w, side = 2 * (size_t)r + 1;
+    cl_mem b1 = file_buf(f1, (size_t)C * n, NULL), b2 = file_buf(f2, (size_t)C * n, NULL);
+    cl_mem bf = file_buf(ffl, 2 * n, NULL), bo = buf(side * side * n * 4, NULL);
+    size_t gc = n * 64, lc = 64;
+
+    SET(k_corr, 0, b1);
+    SET(k_corr, 1, b2);
+    SET(k_corr, 2, (cl_int)C);
+    SET(k_corr, 3, (cl_int)h);
+    SET(k_corr, 4, (cl_int)w);
+    SET(k_corr, 5, (cl_int)r);
+    SET(k_corr, 6, bf);
+    SET(k_corr, 7, bo);
+    SET(k_corr, 8, (cl_int)0);
+    launch(k_corr, 1, &gc, &lc);
+    buf_file(bo, side * side * n, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"roma_local_corr\"}\n", spec);
+    clReleaseMemObject(b1);
+    clReleaseMemObject(b2);
+    clReleaseMemObject(bf);
+    clReleaseMemObject(bo);
+}
+
+/* warpx: roma_warp_sample as roma.c:936-945 (output channels from 0). */
+static void exec_warpsample(const char *spec, int C, int h, int w, const char *fi,
+                            const char *ffl, const char *fo)
+{
+    const size_t n = (size_t)h * w;
+    cl_mem bi = file_buf(fi, (size_t)C * n, NULL), bf = file_buf(ffl, 2 * n, NULL);
+    cl_mem bo = buf((size_t)C * n * 4, NULL);
+    size_t g2[2] = {n, (size_t)C};
+
+    SET(k_warp, 0, bi);
+    SET(k_warp, 1, (cl_int)C);
+    SET(k_warp, 2, (cl_int)h);
+    SET(k_warp, 3, (cl_int)w);
+    SET(k_warp, 4, bf);
+    SET(k_warp, 5, bo);
+    SET(k_warp, 6, (cl_int)0);
+    launch(k_warp, 2, g2, NULL);
+    buf_file(bo, (size_t)C * n, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"roma_warp_sample\"}\n", spec);
+    clReleaseMemObject(bi);
+    clReleaseMemObject(bf);
+    clReleaseMemObject(bo);
+}
+
+/* gridx: grid_sample, ops_grid_sample's dispatch (ops.c:520-534). */
+static void exec_gridsample(const char *spec, int C, int H, int W, int n, int align,
+                            const char *fi, const char *fg, const char *fo)
+{
+    cl_mem bi = file_buf(fi, (size_t)C * H * W, NULL), bg = file_buf(fg, 2 * (size_t)n, NULL);
+    cl_mem bo = buf((size_t)C * n * 4, NULL);
+    size_t g[2] = {(size_t)(n + 63) / 64 * 64, (size_t)C}, l[2] = {64, 1};
+
+    SET(k_grid, 0, bi);
+    SET(k_grid, 1, (cl_int)C);
+    SET(k_grid, 2, (cl_int)H);
+    SET(k_grid, 3, (cl_int)W);
+    SET(k_grid, 4, bg);
+    SET(k_grid, 5, (cl_int)n);
+    SET(k_grid, 6, (cl_int)align);
+    SET(k_grid, 7, bo);
+    launch(k_grid, 2, g, l);
+    buf_file(bo, (size_t)C * n, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"grid_sample\"}\n", spec);
+    clReleaseMemObject(bi);
+    clReleaseMemObject(bg);
+    clReleaseMemObject(bo);
+}
+
+/* dwx: roma_dwconv5 (depthwise 5 x 5, bias, ReLU) as roma.c:970-981. */
+static void exec_dwconv(const char *spec, int C, int H, int W, const char *fi, const char *fw,
+                        const char *fb, const char *fo)
+{
+    cl_kernel k = kern(prog_roma, "roma_dwconv5");
+    const size_t n = (size_t)H * W;
+    cl_mem bi = file_buf(fi, (size_t)C * n, NULL), bw = file_buf(fw, (size_t)C * 25, NULL);
+    cl_mem bb = file_buf(fb, (size_t)C, NULL), bo = buf((size_t)C * n * 4, NULL);
+    size_t g[3] = {(size_t)(W + 15) / 16 * 16, (size_t)(H + 15) / 16 * 16, (size_t)C},
+           l[3] = {16, 16, 1};
+
+    SET(k, 0, bi);
+    SET(k, 1, (cl_int)H);
+    SET(k, 2, (cl_int)W);
+    SET(k, 3, bw);
+    SET(k, 4, bb);
+    SET(k, 5, bo);
+    launch(k, 3, g, l);
+    buf_file(bo, (size_t)C * n, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"roma_dwconv5\"}\n", spec);
+    clReleaseMemObject(bi);
+    clReleaseMemObject(bw);
+    clReleaseMemObject(bb);
+    clReleaseMemObject(bo);
+    clReleaseKernel(k);
+}
+
 /* A code object of DIR when it was built, else NULL. */
 static cl_program load_optional(const char *dir, const char *name)
 {
@@ -895,10 +1128,10 @@ int main(int argc, char **argv)
     prog_disk = load_optional(argv[1], "disk_kernels");
     fprintf(stderr, "ref_ocl: device %s\n", name);
     for (int i = 2; i < argc; i++) {
-        int a = 0, b = 0, c = 0, d = 0;
+        int a = 0, b = 0, c = 0, d = 0, e5 = 0;
         long lo = 0;
         float fl = 0.0f;
-        char f1[1024], f2[1024], f3[1024];
+        char f1[1024], f2[1024], f3[1024], f4[1024];
 
         if (sscanf(argv[i], "coarse:%d:%d:%1023[^:]:%1023s", &a, &b, f1, f2) == 4)
             exec_coarse(argv[i], a, b, f1, f2);
@@ -910,6 +1143,29 @@ int main(int argc, char **argv)
             exec_gather(argv[i], a, b, c, d, f1, f2, f3);
         else if (sscanf(argv[i], "cls:%d:%d:%d:%d:%1023[^:]:%1023s", &a, &b, &c, &d, f1, f2) == 6)
             exec_cls(argv[i], a, b, c, d, f1, f2);
+        else if (sscanf(argv[i], "gemmx:%d:%d:%d:%d:%d:%1023[^:]:%1023[^:]:%1023[^:]:%1023s",
+                        &a, &b, &c, &d, &e5, f1, f2, f3, f4) == 9)
+            exec_gemm(argv[i], a, b, c, d, e5, f1, f2, f3, f4);
+        else if (sscanf(argv[i], "lnx:%d:%d:%f:%1023[^:]:%1023[^:]:%1023[^:]:%1023s", &a, &b,
+                        &fl, f1, f2, f3, f4) == 7)
+            exec_layernorm(argv[i], a, b, fl, f1, f2, f3, f4);
+        else if (sscanf(argv[i], "smx:%d:%d:%f:%1023[^:]:%1023s", &a, &b, &fl, f1, f2) == 5)
+            exec_softmax(argv[i], a, b, fl, f1, f2);
+        else if (sscanf(argv[i], "attnx:%d:%d:%d:%d:%f:%1023[^:]:%1023[^:]:%1023[^:]:%1023s",
+                        &a, &b, &c, &d, &fl, f1, f2, f3, f4) == 9)
+            exec_attention(argv[i], a, b, c, d, fl, f1, f2, f3, f4);
+        else if (sscanf(argv[i], "lcx:%d:%d:%d:%d:%1023[^:]:%1023[^:]:%1023[^:]:%1023s", &a,
+                        &b, &c, &d, f1, f2, f3, f4) == 8)
+            exec_localcorr(argv[i], a, b, c, d, f1, f2, f3, f4);
+        else if (sscanf(argv[i], "warpx:%d:%d:%d:%1023[^:]:%1023[^:]:%1023s", &a, &b, &c, f1,
+                        f2, f3) == 6)
+            exec_warpsample(argv[i], a, b, c, f1, f2, f3);
+        else if (sscanf(argv[i], "gridx:%d:%d:%d:%d:%d:%1023[^:]:%1023[^:]:%1023s", &a, &b, &c,
+                        &d, &e5, f1, f2, f3) == 8)
+            exec_gridsample(argv[i], a, b, c, d, e5, f1, f2, f3);
+        else if (sscanf(argv[i], "dwx:%d:%d:%d:%1023[^:]:%1023[^:]:%1023[^:]:%1023s", &a, &b,
+                        &c, f1, f2, f3, f4) == 7)
+            exec_dwconv(argv[i], a, b, c, f1, f2, f3, f4);
         else if (sscanf(argv[i], "gemm:%d:%d:%d:%d", &a, &b, &c, &d) == 4)
             case_gemm(argv[i], a, b, c, d);
         else if (sscanf(argv[i], "vitblock:%d", &a) == 1)

@@ -18,6 +18,14 @@ to files; the HIP kernels run here on the same arrays.
     plateaus included); gather_desc within 1e-6.
   * RoMa's cls_to_flow: the same anchor (warp within 1e-5) wherever the
     logit margin exceeds 1e-3, the certainty logit copied exactly.
+  * ops.cl's gemm / gemm_big, attention, layernorm, softmax_rows and
+    grid_sample with ops.c's dispatch, roma_kernels.cl's local
+    correlation, warp sampling and depthwise 5 x 5 with roma.c's, at the
+    pipelines' shapes (the ViT's qkv and attention of a 560² image, the
+    refiners' 1/8 and 1/4 maps of 864²) and ragged ones: contractions
+    within 1e-3 of the reference kernel's outputs, element-wise kernels
+    within 1e-4, the depthwise convolution (same taps, same order)
+    within 1e-6.
 
 Skipped with the reason when the reference's kernels were not built (the
 reference is needed at build time) or no OpenCL GPU device is present."""
@@ -213,3 +221,177 @@ def test_cls_to_flow_vs_reference_kernel(dev, ic, tmp_path):
     assert sure.mean() > 0.9
     assert np.abs(g_flow[:, sure] - r_flow[:, sure]).max() < 1e-5
     assert np.array_equal(g_cert, r_cert)
+
+
+def smooth_warp(rng, h, w, amp=3.0):
+    """The refiners' kind of warp (normalised coordinates): the identity
+    plus a slowly varying displacement of a few cells."""
+    gy = -1 + (2 * np.arange(h) + 1) / h
+    gx = -1 + (2 * np.arange(w) + 1) / w
+    gy, gx = np.meshgrid(gy, gx, indexing="ij")
+    ph = rng.uniform(0, 2 * np.pi, 4)
+    dx = amp / w * (np.sin(2.1 * gy + ph[0]) + np.cos(1.7 * gx + ph[1]))
+    dy = amp / h * (np.sin(1.3 * gx + ph[2]) + np.cos(2.5 * gy + ph[3]))
+    return np.ascontiguousarray(np.stack([gx + dx, gy + dy]).astype(np.float32))
+
+
+def files(tmp_path, **arrays):
+    """Write each array to tmp_path/<name>.f32; the paths by name."""
+    out = {}
+    for k, v in arrays.items():
+        p = tmp_path / f"{k}.f32"
+        np.ascontiguousarray(v, np.float32).tofile(p)
+        out[k] = str(p)
+    return out
+
+
+@pytest.mark.parametrize("M,N,K,transb,act", [(1601, 3072, 1024, 1, 0), (1000, 130, 77, 0, 2),
+                                              (64, 4097, 1024, 1, 0), (400, 256, 512, 0, 1)])
+def test_gemm_vs_reference_kernel(dev, ic, tmp_path, M, N, K, transb, act):
+    """ops_gemm: the ViT's qkv product of one 560² image (B given N x K),
+    ragged shapes with ReLU, RoMa's anchor-logit width, ELoFTR's MLP with
+    GELU: within the contraction bar (1e-3 relative)."""
+    rng = np.random.default_rng(M + N + K)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = (rng.uniform(-1, 1, (N, K) if transb else (K, N)) / np.sqrt(K)).astype(np.float32)
+    bias = rng.uniform(-1, 1, N).astype(np.float32)
+    f = files(tmp_path, A=A, B=B, bias=bias)
+    of = tmp_path / "out.f32"
+    run_reference(f"gemmx:{M}:{N}:{K}:{transb}:{act}:{f['A']}:{f['B']}:{f['bias']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bA, bB, bb, bC = dev.upload(A), dev.upload(B), dev.upload(bias), dev.zeros(M * N)
+    dev.api.ops_gemm(dev.po, M, N, K, ic.mat(bA, 0, K), ic.mat(bB, 0, K if transb else N),
+                     transb, ic.mat(bC, 0, N), 1, 1, bb.mem, 0, None, 0, 1.0, act, 0.0)
+    assert rel(dev.read(bC, M * N), ref) <= TOL
+
+
+@pytest.mark.parametrize("rows,C", [(3202, 1024), (33, 260), (7, 2050)])
+def test_layernorm_vs_reference_kernel(dev, ic, tmp_path, rows, C):
+    """ops_layernorm on the ViT's rows (both images) and ragged widths:
+    within the element-wise bar (1e-4)."""
+    rng = np.random.default_rng(rows + C)
+    x = (rng.standard_normal((rows, C)) * 2 + 0.5).astype(np.float32)
+    g, b = rng.uniform(0.5, 1.5, C).astype(np.float32), rng.uniform(-1, 1, C).astype(np.float32)
+    f = files(tmp_path, x=x, g=g, b=b)
+    of = tmp_path / "out.f32"
+    run_reference(f"lnx:{rows}:{C}:1e-06:{f['x']}:{f['g']}:{f['b']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bx, bg, bb, by = dev.upload(x), dev.upload(g), dev.upload(b), dev.zeros(rows * C)
+    dev.api.ops_layernorm(dev.po, rows, C, bx.mem, by.mem, bg.mem, bb.mem, 1e-6, 0, 0.0)
+    assert rel(dev.read(by, rows * C), ref) <= 1e-4
+
+
+@pytest.mark.parametrize("rows,L,scale", [(1601, 1601, 0.125), (100, 37, 1.0), (3, 5000, 0.5)])
+def test_softmax_vs_reference_kernel(dev, ic, tmp_path, rows, L, scale):
+    """ops_softmax_rows: a ViT head's score rows and ragged rows, within
+    the element-wise bar (1e-4)."""
+    rng = np.random.default_rng(rows + L)
+    s = (rng.standard_normal((rows, L)) * 4).astype(np.float32)
+    f = files(tmp_path, s=s)
+    of = tmp_path / "out.f32"
+    run_reference(f"smx:{rows}:{L}:{scale}:{f['s']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bs = dev.upload(s)
+    dev.api.ops_softmax_rows(dev.po, bs.mem, rows, L, scale)
+    assert rel(dev.read(bs, rows * L), ref) <= 1e-4
+
+
+@pytest.mark.parametrize("Nq,Nk,nh,d", [(1601, 1601, 16, 64), (400, 400, 8, 32), (37, 1000, 2, 128)])
+def test_attention_vs_reference_kernel(dev, ic, tmp_path, Nq, Nk, nh, d):
+    """ops_attention: a ViT layer of one image (16 heads of 64), an
+    ELoFTR aggregated-attention shape, and few queries over many keys
+    with d = 128: outputs within the contraction bar (1e-3)."""
+    rng = np.random.default_rng(Nq + Nk + d)
+    E = nh * d
+    Q = rng.standard_normal((Nq, E)).astype(np.float32)
+    K = rng.standard_normal((Nk, E)).astype(np.float32)
+    V = rng.standard_normal((Nk, E)).astype(np.float32)
+    scale = 1.0 / np.sqrt(d)
+    f = files(tmp_path, q=Q, k=K, v=V)
+    of = tmp_path / "out.f32"
+    run_reference(f"attnx:{Nq}:{Nk}:{nh}:{d}:{scale}:{f['q']}:{f['k']}:{f['v']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bq, bk, bv, bo = dev.upload(Q), dev.upload(K), dev.upload(V), dev.zeros(Nq * E)
+    dev.api.ops_attention(dev.po, ic.mat(bq, 0, E), ic.mat(bk, 0, E), ic.mat(bv, 0, E),
+                          ic.mat(bo, 0, E), Nq, Nk, nh, d, scale, None)
+    assert rel(dev.read(bo, Nq * E), ref) <= TOL
+
+
+@pytest.mark.parametrize("C,h,w,r,smooth", [(512, 108, 108, 3, True), (256, 216, 216, 2, True),
+                                            (64, 37, 50, 3, False), (40, 20, 24, 1, True)])
+def test_local_corr_vs_reference_kernel(dev, ic, tmp_path, C, h, w, r, smooth):
+    """roma_local_corr at the refiner config's 1/8 and 1/4 shapes of 864²
+    on smooth warps, a random warp (the per-cell path) and a channel count
+    that is not a multiple of 16: within the contraction bar (1e-3)."""
+    rng = np.random.default_rng(C + h + r)
+    n = h * w
+    f1 = rng.standard_normal((C, n)).astype(np.float32)
+    f2 = rng.standard_normal((C, n)).astype(np.float32)
+    fl = smooth_warp(rng, h, w) if smooth else rng.uniform(-1.1, 1.1, (2, h, w)).astype(np.float32)
+    f = files(tmp_path, f1=f1, f2=f2, fl=fl)
+    of = tmp_path / "out.f32"
+    run_reference(f"lcx:{C}:{h}:{w}:{r}:{f['f1']}:{f['f2']}:{f['fl']}:{of}")
+    K = (2 * r + 1) ** 2
+    ref = np.fromfile(of, np.float32)
+    b1, b2, bf, bo = dev.upload(f1), dev.upload(f2), dev.upload(fl), dev.zeros(K * n)
+    dev.api.roma_local_corr(dev.po, b1.mem, b2.mem, C, h, w, r, bf.mem, bo.mem, 0)
+    assert rel(dev.read(bo, K * n), ref) <= TOL
+
+
+@pytest.mark.parametrize("C,h,w,smooth", [(512, 108, 108, True), (9, 200, 160, True),
+                                          (33, 40, 50, False)])
+def test_warp_sample_vs_reference_kernel(dev, ic, tmp_path, C, h, w, smooth):
+    """roma_warp_sample on the 1/8 shape of 864², RoMa's 9-channel 1/1
+    form and a random warp with samples outside: within the element-wise
+    bar (1e-4; the sample coordinate is one multiply-add whose fusing may
+    differ between the compilers)."""
+    rng = np.random.default_rng(C + h)
+    n = h * w
+    x = rng.standard_normal((C, n)).astype(np.float32)
+    fl = smooth_warp(rng, h, w) if smooth else rng.uniform(-1.2, 1.2, (2, h, w)).astype(np.float32)
+    f = files(tmp_path, x=x, fl=fl)
+    of = tmp_path / "out.f32"
+    run_reference(f"warpx:{C}:{h}:{w}:{f['x']}:{f['fl']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bx, bf, bo = dev.upload(x), dev.upload(fl), dev.zeros(C * n)
+    dev.api.roma_warp_sample(dev.po, bx.mem, C, h, w, bf.mem, bo.mem, 0)
+    assert rel(dev.read(bo, C * n), ref) <= 1e-4
+
+
+@pytest.mark.parametrize("C,H,W,n,align,smooth", [(512, 108, 108, 11664, 0, True),
+                                                  (64, 50, 70, 5000, 1, False),
+                                                  (3, 33, 17, 999, 0, False)])
+def test_grid_sample_vs_reference_kernel(dev, ic, tmp_path, C, H, W, n, align, smooth):
+    """ops_grid_sample on a smooth warp of the 1/8 grid of 864² and on
+    uniform points past the borders, both corner conventions: within the
+    element-wise bar (1e-4)."""
+    rng = np.random.default_rng(C + n)
+    x = rng.standard_normal((C, H, W)).astype(np.float32)
+    if smooth:
+        g = np.ascontiguousarray(smooth_warp(rng, H, W).reshape(2, -1).T)
+    else:
+        g = rng.uniform(-1.1, 1.1, (n, 2)).astype(np.float32)
+    f = files(tmp_path, x=x, g=g)
+    of = tmp_path / "out.f32"
+    run_reference(f"gridx:{C}:{H}:{W}:{n}:{align}:{f['x']}:{f['g']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bx, bg, bo = dev.upload(x), dev.upload(g), dev.zeros(C * n)
+    dev.api.ops_grid_sample(dev.po, bx.mem, C, H, W, bg.mem, n, align, bo.mem)
+    assert rel(dev.read(bo, C * n), ref) <= 1e-4
+
+
+@pytest.mark.parametrize("C,H,W", [(64, 108, 108), (24, 216, 216), (5, 17, 40)])
+def test_dwconv5_vs_reference_kernel(dev, ic, tmp_path, C, H, W):
+    """roma_dwconv5 (depthwise 5 x 5, bias, ReLU): the same taps in the
+    same order, so within 1e-6."""
+    rng = np.random.default_rng(C + H)
+    x = rng.standard_normal((C, H, W)).astype(np.float32)
+    wt = (rng.standard_normal((C, 25)) / 5).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, C).astype(np.float32)
+    f = files(tmp_path, x=x, w=wt, b=b)
+    of = tmp_path / "out.f32"
+    run_reference(f"dwx:{C}:{H}:{W}:{f['x']}:{f['w']}:{f['b']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bx, bw, bb, bo = dev.upload(x), dev.upload(wt), dev.upload(b), dev.zeros(C * H * W)
+    dev.api.roma_dwconv5(dev.po, bx.mem, C, H, W, bw.mem, bb.mem, bo.mem)
+    assert rel(dev.read(bo, C * H * W), ref) <= 1e-6
