@@ -48,7 +48,13 @@
  *         lcx:C:h:w:r:F1:F2:FLOW:OUT            roma_local_corr
  *         warpx:C:h:w:IN:FLOW:OUT               roma_warp_sample
  *         gridx:C:H:W:n:align:IN:GRID:OUT       ops_grid_sample
- *         dwx:C:H:W:IN:WT:BIAS:OUT              roma_dwconv5 */
+ *         dwx:C:H:W:IN:WT:BIAS:OUT              roma_dwconv5
+ *         c5x:C:H:W:K:norm:IN:WT:BIAS:MEAN:RSTD:ALPHA:OUT   conv5x5
+ *         convx:C:H:W:K:kh:kw:sy:sx:py:px:groups:act:IN:WT:BIAS:OUT conv2d
+ *         statx:C:HW:eps:X:OUT                  chan_stats (mean, rstd)
+ *         resx:C:h:w:H:W:align:scale:IN:OUT     resize_bilinear
+ *         poolx:C:H:W:ks:s:p:max:IN:OUT         pool2d
+ *         ropex:rows:ld:nh:d:npos:interleaved:X:CS:OUT   rope */
 
 #define CL_TARGET_OPENCL_VERSION 120
 #include <CL/cl.h>
@@ -1078,6 +1084,200 @@ static void exec_dwconv(const char *spec, int C, int H, int W, const char *fi, c
     clReleaseKernel(k);
 }
 
+/* c5x: conv5x5 (stride 1, padding 2, bias, no activation), with the
+ * input normalised and gated (instance norm + PReLU) when norm is set,
+ * ops_conv2d's first branch (ops.c:285-305). MEAN, RSTD, ALPHA: C floats
+ * each (read only with norm). */
+static void exec_conv5(const char *spec, int C, int H, int W, int K, int norm, const char *fi,
+                       const char *fw, const char *fb, const char *fm, const char *fr,
+                       const char *fa, const char *fo)
+{
+    cl_kernel k = kern(prog_ops, "conv5x5");
+    cl_mem bi = file_buf(fi, (size_t)C * H * W, NULL), bw = file_buf(fw, (size_t)K * C * 25, NULL);
+    cl_mem bb = file_buf(fb, (size_t)K, NULL), bm = file_buf(fm, (size_t)C, NULL);
+    cl_mem br = file_buf(fr, (size_t)C, NULL), ba = file_buf(fa, (size_t)C, NULL);
+    cl_mem bo = buf((size_t)K * H * W * 4, NULL);
+    size_t gs[3] = {(size_t)(W + 15) / 16 * 16, (size_t)(H + 15) / 16 * 16, (size_t)(K + 7) / 8};
+    size_t ls[3] = {16, 16, 1};
+
+    SET(k, 0, bi);
+    SET(k, 1, (cl_int)C);
+    SET(k, 2, (cl_int)H);
+    SET(k, 3, (cl_int)W);
+    SET(k, 4, bw);
+    SET(k, 5, bb);
+    SET(k, 6, (cl_int)K);
+    SET(k, 7, norm ? bm : bw);
+    SET(k, 8, norm ? br : bw);
+    SET(k, 9, norm ? ba : bw);
+    SET(k, 10, (cl_int)norm);
+    SET(k, 11, bo);
+    launch(k, 3, gs, ls);
+    buf_file(bo, (size_t)K * H * W, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"conv5x5\"}\n", spec);
+    clReleaseMemObject(bi);
+    clReleaseMemObject(bw);
+    clReleaseMemObject(bb);
+    clReleaseMemObject(bm);
+    clReleaseMemObject(br);
+    clReleaseMemObject(ba);
+    clReleaseMemObject(bo);
+    clReleaseKernel(k);
+}
+
+/* convx: the general conv2d kernel (ops.c:307-334) with geometry kh kw
+ * sy sx py px (dilation 1), groups, bias and activation, no input
+ * normalisation. */
+static void exec_conv(const char *spec, const int *gm, int act, const char *fi, const char *fw,
+                      const char *fb, const char *fo)
+{
+    const int C = gm[0], H = gm[1], W = gm[2], K = gm[3], kh = gm[4], kw = gm[5], sy = gm[6],
+              sx = gm[7], py = gm[8], px = gm[9], groups = gm[10];
+    const int Ho = (H + 2 * py - kh) / sy + 1, Wo = (W + 2 * px - kw) / sx + 1;
+    cl_kernel k = kern(prog_ops, "conv2d");
+    const cl_mem none = NULL;
+    cl_mem bi = file_buf(fi, (size_t)C * H * W, NULL);
+    cl_mem bw = file_buf(fw, (size_t)K * (C / groups) * kh * kw, NULL);
+    cl_mem bb = file_buf(fb, (size_t)K, NULL), bo = buf((size_t)K * Ho * Wo * 4, NULL);
+    const cl_int v[11] = {Ho, Wo, kh, kw, sy, sx, py, px, 1, 1, groups};
+    size_t gs[3] = {(size_t)(Wo + 15) / 16 * 16, (size_t)(Ho + 3) / 4 * 4, (size_t)K};
+    size_t ls[3] = {16, 4, 1};
+
+    SET(k, 0, bi);
+    SET(k, 1, (cl_int)C);
+    SET(k, 2, (cl_int)H);
+    SET(k, 3, (cl_int)W);
+    SET(k, 4, bw);
+    SET(k, 5, bb);
+    SET(k, 6, (cl_int)K);
+    for (int i = 0; i < 11; i++)
+        SET(k, 7 + i, v[i]);
+    SET(k, 18, none);
+    SET(k, 19, none);
+    SET(k, 20, none);
+    SET(k, 21, (cl_int)act);
+    SET(k, 22, (cl_float)0.1f);
+    SET(k, 23, bo);
+    launch(k, 3, gs, ls);
+    buf_file(bo, (size_t)K * Ho * Wo, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"conv2d\"}\n", spec);
+    clReleaseMemObject(bi);
+    clReleaseMemObject(bw);
+    clReleaseMemObject(bb);
+    clReleaseMemObject(bo);
+    clReleaseKernel(k);
+}
+
+/* statx: chan_stats (ops.c:338-352); OUT: mean then rstd, C floats each. */
+static void exec_stats(const char *spec, int C, int HW, float eps, const char *fx,
+                       const char *fo)
+{
+    cl_kernel k = kern(prog_ops, "chan_stats");
+    cl_mem bx = file_buf(fx, (size_t)C * HW, NULL), bo = buf((size_t)2 * C * 4, NULL);
+    cl_mem bm = buf((size_t)C * 4, NULL), br = buf((size_t)C * 4, NULL);
+    size_t g = (size_t)C * 256, l = 256;
+    float *h = malloc((size_t)2 * C * 4);
+
+    SET(k, 0, bx);
+    SET(k, 1, (cl_int)HW);
+    SET(k, 2, (cl_float)eps);
+    SET(k, 3, bm);
+    SET(k, 4, br);
+    launch(k, 1, &g, &l);
+    readb(bm, (size_t)C * 4, h);
+    readb(br, (size_t)C * 4, h + C);
+    write_file(fo, h, (size_t)2 * C * 4);
+    printf("{\"case\": \"%s\", \"kernel\": \"chan_stats\"}\n", spec);
+    free(h);
+    clReleaseMemObject(bx);
+    clReleaseMemObject(bo);
+    clReleaseMemObject(bm);
+    clReleaseMemObject(br);
+    clReleaseKernel(k);
+}
+
+/* resx: resize_bilinear (ops.c:496-516), output channels from 0. */
+static void exec_resize(const char *spec, int C, int h, int w, int H, int W, int align,
+                        float scale, const char *fi, const char *fo)
+{
+    cl_kernel k = kern(prog_ops, "resize_bilinear");
+    cl_mem bi = file_buf(fi, (size_t)C * h * w, NULL), bo = buf((size_t)C * H * W * 4, NULL);
+    const cl_float sy = scale > 0 ? 1.0f / scale : (float)h / H;
+    const cl_float sx = scale > 0 ? 1.0f / scale : (float)w / W;
+    size_t g[3] = {(size_t)W, (size_t)H, (size_t)C};
+
+    SET(k, 0, bi);
+    SET(k, 1, (cl_int)h);
+    SET(k, 2, (cl_int)w);
+    SET(k, 3, bo);
+    SET(k, 4, (cl_int)H);
+    SET(k, 5, (cl_int)W);
+    SET(k, 6, (cl_int)0);
+    SET(k, 7, (cl_int)align);
+    SET(k, 8, sy);
+    SET(k, 9, sx);
+    launch(k, 3, g, NULL);
+    buf_file(bo, (size_t)C * H * W, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"resize_bilinear\"}\n", spec);
+    clReleaseMemObject(bi);
+    clReleaseMemObject(bo);
+    clReleaseKernel(k);
+}
+
+/* poolx: pool2d (ops.c:559-578), max or average. */
+static void exec_pool(const char *spec, int C, int H, int W, int ks, int s, int p, int max,
+                      const char *fi, const char *fo)
+{
+    cl_kernel k = kern(prog_ops, "pool2d");
+    const int Ho = (H + 2 * p - ks) / s + 1, Wo = (W + 2 * p - ks) / s + 1;
+    cl_mem bi = file_buf(fi, (size_t)C * H * W, NULL), bo = buf((size_t)C * Ho * Wo * 4, NULL);
+    size_t g[3] = {(size_t)Wo, (size_t)Ho, (size_t)C};
+
+    SET(k, 0, bi);
+    SET(k, 1, (cl_int)H);
+    SET(k, 2, (cl_int)W);
+    SET(k, 3, (cl_int)Ho);
+    SET(k, 4, (cl_int)Wo);
+    SET(k, 5, (cl_int)ks);
+    SET(k, 6, (cl_int)s);
+    SET(k, 7, (cl_int)p);
+    SET(k, 8, (cl_int)max);
+    SET(k, 9, bo);
+    launch(k, 3, g, NULL);
+    buf_file(bo, (size_t)C * Ho * Wo, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"pool2d\"}\n", spec);
+    clReleaseMemObject(bi);
+    clReleaseMemObject(bo);
+    clReleaseKernel(k);
+}
+
+/* ropex: rope in place on rows of ld floats from offset 0 (ops.c:476-494);
+ * CS: npos x d / 2 (cos, sin) pairs. */
+static void exec_rope(const char *spec, int rows, int ld, int nh, int d, int npos,
+                      int interleaved, const char *fx, const char *fcs, const char *fo)
+{
+    cl_kernel k = kern(prog_ops, "rope");
+    cl_mem bx = file_buf(fx, (size_t)rows * ld, NULL), bc = file_buf(fcs, (size_t)npos * d, NULL);
+    const cl_int n = rows * nh * (d / 2);
+    size_t l = 256, g = ((size_t)n + l - 1) / l * l;
+
+    SET(k, 0, bx);
+    SET(k, 1, (cl_long)0);
+    SET(k, 2, (cl_int)ld);
+    SET(k, 3, (cl_int)nh);
+    SET(k, 4, (cl_int)d);
+    SET(k, 5, (cl_int)npos);
+    SET(k, 6, bc);
+    SET(k, 7, (cl_int)interleaved);
+    SET(k, 8, n);
+    launch(k, 1, &g, &l);
+    buf_file(bx, (size_t)rows * ld, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"rope\"}\n", spec);
+    clReleaseMemObject(bx);
+    clReleaseMemObject(bc);
+    clReleaseKernel(k);
+}
+
 /* A code object of DIR when it was built, else NULL. */
 static cl_program load_optional(const char *dir, const char *name)
 {
@@ -1131,7 +1331,8 @@ int main(int argc, char **argv)
         int a = 0, b = 0, c = 0, d = 0, e5 = 0;
         long lo = 0;
         float fl = 0.0f;
-        char f1[1024], f2[1024], f3[1024], f4[1024];
+        int gm[11] = {0};
+        char f1[1024], f2[1024], f3[1024], f4[1024], f5[1024], f6[1024], f7[1024];
 
         if (sscanf(argv[i], "coarse:%d:%d:%1023[^:]:%1023s", &a, &b, f1, f2) == 4)
             exec_coarse(argv[i], a, b, f1, f2);
@@ -1166,6 +1367,25 @@ int main(int argc, char **argv)
         else if (sscanf(argv[i], "dwx:%d:%d:%d:%1023[^:]:%1023[^:]:%1023[^:]:%1023s", &a, &b,
                         &c, f1, f2, f3, f4) == 7)
             exec_dwconv(argv[i], a, b, c, f1, f2, f3, f4);
+        else if (sscanf(argv[i], "c5x:%d:%d:%d:%d:%d:%1023[^:]:%1023[^:]:%1023[^:]:%1023[^:]:"
+                        "%1023[^:]:%1023[^:]:%1023s", &a, &b, &c, &d, &e5, f1, f2, f3, f4, f5,
+                        f6, f7) == 12)
+            exec_conv5(argv[i], a, b, c, d, e5, f1, f2, f3, f4, f5, f6, f7);
+        else if (sscanf(argv[i], "convx:%d:%d:%d:%d:%d:%d:%d:%d:%d:%d:%d:%d:%1023[^:]:%1023[^:]:"
+                        "%1023[^:]:%1023s", &gm[0], &gm[1], &gm[2], &gm[3], &gm[4], &gm[5],
+                        &gm[6], &gm[7], &gm[8], &gm[9], &gm[10], &e5, f1, f2, f3, f4) == 16)
+            exec_conv(argv[i], gm, e5, f1, f2, f3, f4);
+        else if (sscanf(argv[i], "statx:%d:%d:%f:%1023[^:]:%1023s", &a, &b, &fl, f1, f2) == 5)
+            exec_stats(argv[i], a, b, fl, f1, f2);
+        else if (sscanf(argv[i], "resx:%d:%d:%d:%d:%d:%d:%f:%1023[^:]:%1023s", &a, &b, &c, &d,
+                        &gm[0], &e5, &fl, f1, f2) == 9)
+            exec_resize(argv[i], a, b, c, d, gm[0], e5, fl, f1, f2);
+        else if (sscanf(argv[i], "poolx:%d:%d:%d:%d:%d:%d:%d:%1023[^:]:%1023s", &a, &b, &c,
+                        &gm[0], &gm[1], &gm[2], &e5, f1, f2) == 9)
+            exec_pool(argv[i], a, b, c, gm[0], gm[1], gm[2], e5, f1, f2);
+        else if (sscanf(argv[i], "ropex:%d:%d:%d:%d:%d:%d:%1023[^:]:%1023[^:]:%1023s", &a, &b,
+                        &c, &d, &gm[0], &e5, f1, f2, f3) == 9)
+            exec_rope(argv[i], a, b, c, d, gm[0], e5, f1, f2, f3);
         else if (sscanf(argv[i], "gemm:%d:%d:%d:%d", &a, &b, &c, &d) == 4)
             case_gemm(argv[i], a, b, c, d);
         else if (sscanf(argv[i], "vitblock:%d", &a) == 1)

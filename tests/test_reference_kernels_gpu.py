@@ -18,18 +18,21 @@ to files; the HIP kernels run here on the same arrays.
     plateaus included); gather_desc within 1e-6.
   * RoMa's cls_to_flow: the same anchor (warp within 1e-5) wherever the
     logit margin exceeds 1e-3, the certainty logit copied exactly.
-  * ops.cl's gemm / gemm_big, attention, layernorm, softmax_rows and
-    grid_sample with ops.c's dispatch, roma_kernels.cl's local
+  * ops.cl's gemm / gemm_big, attention, layernorm, softmax_rows,
+    grid_sample, conv5x5 (with the fused instance norm and PReLU),
+    conv2d, chan_stats, resize_bilinear, pool2d and rope with ops.c's
+    dispatch, roma_kernels.cl's local
     correlation, warp sampling and depthwise 5 x 5 with roma.c's, at the
     pipelines' shapes (the ViT's qkv and attention of a 560² image, the
     refiners' 1/8 and 1/4 maps of 864²) and ragged ones: contractions
     within 1e-3 of the reference kernel's outputs, element-wise kernels
-    within 1e-4, the depthwise convolution (same taps, same order)
-    within 1e-6.
+    within 1e-4, the depthwise convolution, rotations and average pools
+    within 1e-6, max pools bit-exact.
 
 Skipped with the reason when the reference's kernels were not built (the
 reference is needed at build time) or no OpenCL GPU device is present."""
 
+import ctypes
 import subprocess
 import sys
 from pathlib import Path
@@ -395,3 +398,141 @@ def test_dwconv5_vs_reference_kernel(dev, ic, tmp_path, C, H, W):
     bx, bw, bb, bo = dev.upload(x), dev.upload(wt), dev.upload(b), dev.zeros(C * H * W)
     dev.api.roma_dwconv5(dev.po, bx.mem, C, H, W, bw.mem, bb.mem, bo.mem)
     assert rel(dev.read(bo, C * H * W), ref) <= 1e-6
+
+
+@pytest.mark.parametrize("C,H,W,K,norm", [(64, 128, 128, 64, True), (3, 96, 80, 16, False),
+                                          (80, 64, 64, 129, True), (12, 37, 45, 10, True)])
+def test_conv5x5_vs_reference_kernel(dev, ic, tmp_path, C, H, W, K, norm):
+    """DISK's 5 x 5 convolutions (ops.cl's conv5x5: stride 1, padding 2,
+    bias), with the input instance-normalised and PReLU-gated as the
+    U-Net feeds it, the first layer on the RGB image, the 129-channel
+    head, a ragged map: within the contraction bar (1e-3)."""
+    rng = np.random.default_rng(C + K + H)
+    x = rng.standard_normal((C, H, W)).astype(np.float32) * 2 + 0.3
+    w = (rng.standard_normal((K, C, 25)) / np.sqrt(25 * C)).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, K).astype(np.float32)
+    mean = x.reshape(C, -1).mean(1).astype(np.float32)
+    rstd = (1 / np.sqrt(x.reshape(C, -1).var(1) + 1e-5)).astype(np.float32)
+    alpha = rng.uniform(0.05, 0.3, C).astype(np.float32)
+    f = files(tmp_path, x=x, w=w, b=b, m=mean, r=rstd, a=alpha)
+    of = tmp_path / "out.f32"
+    run_reference(f"c5x:{C}:{H}:{W}:{K}:{int(norm)}:{f['x']}:{f['w']}:{f['b']}:{f['m']}:"
+                  f"{f['r']}:{f['a']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bx, bw, bb, bo = dev.upload(x), dev.upload(w), dev.upload(b), dev.zeros(K * H * W)
+    bm, br, ba = dev.upload(mean), dev.upload(rstd), dev.upload(alpha)
+    g = ic.geom(5, 5, 1, 1, 2, 2, 1, 1, 1)
+    dev.api.ops_conv2d(dev.po, bx.mem, C, H, W, bw.mem, bb.mem, K, ctypes.byref(g),
+                       bm.mem if norm else None, br.mem if norm else None,
+                       ba.mem if norm else None, 0, 0.0, bo.mem)
+    assert rel(dev.read(bo, K * H * W), ref) <= TOL
+
+
+CONV_GEOMS = [
+    # (C, H, W, K, kh, kw, sy, sx, py, px, groups, act): ELoFTR's stride-2
+    # layers, a grouped and a depthwise case, a 1 x 1 with LeakyReLU.
+    (1, 160, 160, 32, 3, 3, 2, 2, 1, 1, 1, 2),
+    (64, 80, 96, 128, 3, 3, 2, 2, 1, 1, 1, 0),
+    (32, 33, 41, 48, 3, 3, 1, 1, 1, 1, 4, 2),
+    (16, 40, 40, 16, 4, 4, 4, 4, 0, 0, 16, 0),
+    (24, 21, 19, 8, 1, 1, 1, 1, 0, 0, 1, 3),
+]
+
+
+@pytest.mark.parametrize("gm", CONV_GEOMS, ids=[str(g) for g in CONV_GEOMS])
+def test_conv2d_vs_reference_kernel(dev, ic, tmp_path, gm):
+    """ops_conv2d against ops.cl's general conv2d kernel (whatever kernel
+    this library picks for the geometry): within 1e-3."""
+    C, H, W, K, kh, kw, sy, sx, py, px, groups, act = gm
+    Ho, Wo = (H + 2 * py - kh) // sy + 1, (W + 2 * px - kw) // sx + 1
+    rng = np.random.default_rng(sum(gm))
+    x = rng.standard_normal((C, H, W)).astype(np.float32)
+    w = (rng.standard_normal((K, C // groups, kh, kw)) /
+         np.sqrt(C // groups * kh * kw)).astype(np.float32)
+    b = rng.uniform(-0.5, 0.5, K).astype(np.float32)
+    f = files(tmp_path, x=x, w=w, b=b)
+    of = tmp_path / "out.f32"
+    spec = ":".join(str(v) for v in gm)
+    run_reference(f"convx:{spec}:{f['x']}:{f['w']}:{f['b']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bx, bw, bb, bo = dev.upload(x), dev.upload(w), dev.upload(b), dev.zeros(K * Ho * Wo)
+    g = ic.geom(kh, kw, sy, sx, py, px, 1, 1, groups)
+    dev.api.ops_conv2d(dev.po, bx.mem, C, H, W, bw.mem, bb.mem, K, ctypes.byref(g), None, None,
+                       None, act, 0.1, bo.mem)
+    assert rel(dev.read(bo, K * Ho * Wo), ref) <= TOL
+
+
+@pytest.mark.parametrize("C,HW", [(64, 512 * 512), (129, 4096), (7, 33)])
+def test_chan_stats_vs_reference_kernel(dev, ic, tmp_path, C, HW):
+    """ops_chan_stats (instance-norm mean and 1 / std) on DISK's 512²
+    layer, its head and a ragged plane: within 1e-4."""
+    rng = np.random.default_rng(C + HW)
+    x = (rng.standard_normal((C, HW)) * 3 + rng.uniform(-2, 2, (C, 1))).astype(np.float32)
+    f = files(tmp_path, x=x)
+    of = tmp_path / "out.f32"
+    run_reference(f"statx:{C}:{HW}:1e-05:{f['x']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bx, bm, br = dev.upload(x), dev.zeros(C), dev.zeros(C)
+    dev.api.ops_chan_stats(dev.po, bx.mem, C, HW, 1e-5, bm.mem, br.mem)
+    assert rel(dev.read(bm, C), ref[:C]) <= 1e-4
+    assert rel(dev.read(br, C), ref[C:]) <= 1e-4
+
+
+@pytest.mark.parametrize("C,h,w,H,W,align,scale", [(256, 80, 80, 160, 160, 0, 2.0),
+                                                   (64, 160, 160, 320, 320, 1, 0.0),
+                                                   (3, 37, 45, 20, 23, 0, 0.0)])
+def test_resize_vs_reference_kernel(dev, ic, tmp_path, C, h, w, H, W, align, scale):
+    """ops_resize (ELoFTR's FPN upsampling by a scale factor, a size with
+    aligned corners, a downsampling): within 1e-4."""
+    rng = np.random.default_rng(C + H)
+    x = rng.standard_normal((C, h, w)).astype(np.float32)
+    f = files(tmp_path, x=x)
+    of = tmp_path / "out.f32"
+    run_reference(f"resx:{C}:{h}:{w}:{H}:{W}:{align}:{scale}:{f['x']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bx, bo = dev.upload(x), dev.zeros(C * H * W)
+    dev.api.ops_resize(dev.po, bx.mem, C, h, w, bo.mem, H, W, 0, align, scale)
+    assert rel(dev.read(bo, C * H * W), ref) <= 1e-4
+
+
+@pytest.mark.parametrize("C,H,W,ks,s,p,mx", [(64, 864, 864, 2, 2, 0, 1), (256, 80, 80, 4, 4, 0, 1),
+                                             (16, 33, 35, 3, 2, 1, 0), (8, 17, 9, 2, 2, 0, 0)])
+def test_pool_vs_reference_kernel(dev, ic, tmp_path, C, H, W, ks, s, p, mx):
+    """ops_pool2d: VGG's 2 x 2 max pool at 864², ELoFTR's 4 x 4 key
+    pooling, padded and ragged average pools: max pools bit-exact,
+    average pools within 1e-6."""
+    Ho, Wo = (H + 2 * p - ks) // s + 1, (W + 2 * p - ks) // s + 1
+    rng = np.random.default_rng(C + H + ks)
+    x = rng.standard_normal((C, H, W)).astype(np.float32)
+    f = files(tmp_path, x=x)
+    of = tmp_path / "out.f32"
+    run_reference(f"poolx:{C}:{H}:{W}:{ks}:{s}:{p}:{mx}:{f['x']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bx, bo = dev.upload(x), dev.zeros(C * Ho * Wo)
+    dev.api.ops_pool2d(dev.po, bx.mem, C, H, W, ks, s, p, mx, bo.mem)
+    got = dev.read(bo, C * Ho * Wo)
+    if mx:
+        assert np.array_equal(got, ref)
+    else:
+        assert rel(got, ref) <= 1e-6
+
+
+@pytest.mark.parametrize("rows,nh,d,npos,inter", [(6400, 8, 32, 6400, 0), (1601, 16, 64, 1601, 1),
+                                                  (37, 3, 8, 5, 1)])
+def test_rope_vs_reference_kernel(dev, ic, tmp_path, rows, nh, d, npos, inter):
+    """ops_rope in place: ELoFTR's 80 x 80 tokens (half form), an
+    interleaved form, positions cycling: within 1e-6 (a rotation of each
+    pair, the same two products)."""
+    rng = np.random.default_rng(rows + d)
+    ld = nh * d + 4
+    x = rng.uniform(-1, 1, (rows, ld)).astype(np.float32)
+    ang = rng.uniform(-3.2, 3.2, (npos, d // 2))
+    cs = np.empty((npos, d // 2, 2), np.float32)
+    cs[..., 0], cs[..., 1] = np.cos(ang), np.sin(ang)
+    f = files(tmp_path, x=x, cs=cs)
+    of = tmp_path / "out.f32"
+    run_reference(f"ropex:{rows}:{ld}:{nh}:{d}:{npos}:{inter}:{f['x']}:{f['cs']}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bx, bc = dev.upload(x), dev.upload(cs)
+    dev.api.ops_rope(dev.po, bx.mem, 0, ld, rows, nh, d, npos, bc.mem, inter)
+    assert rel(dev.read(bx, rows * ld), ref) <= 1e-6
