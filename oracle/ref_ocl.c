@@ -54,7 +54,8 @@
  *         statx:C:HW:eps:X:OUT                  chan_stats (mean, rstd)
  *         resx:C:h:w:H:W:align:scale:IN:OUT     resize_bilinear
  *         poolx:C:H:W:ks:s:p:max:IN:OUT         pool2d
- *         ropex:rows:ld:nh:d:npos:interleaved:X:CS:OUT   rope */
+ *         ropex:rows:ld:nh:d:npos:interleaved:X:CS:OUT   rope
+ *         finex:H:W:M:T:F0:F1:CELLS:OUT          eloftr_fine */
 
 #define CL_TARGET_OPENCL_VERSION 120
 #include <CL/cl.h>
@@ -1278,6 +1279,38 @@ static void exec_rope(const char *spec, int rows, int ld, int nh, int d, int npo
     clReleaseKernel(k);
 }
 
+/* finex: eloftr_fine for M coarse matches, eloftr.c:606-634; CELLS: M
+ * int4 (x0, y0, x1, y1); OUT: M float4 keypoints. */
+static void exec_fine(const char *spec, int H, int W, int M, float T, const char *ff0,
+                      const char *ff1, const char *fc, const char *fo)
+{
+    cl_program pe = need_program(prog_eloftr, "eloftr_kernels");
+    cl_kernel k = kern(pe, "eloftr_fine");
+    const size_t n = (size_t)64 * H * W;
+    int *cells = read_file(fc, (size_t)M * 16);
+    cl_mem b0 = file_buf(ff0, n, NULL), b1 = file_buf(ff1, n, NULL);
+    cl_mem bc = buf((size_t)M * 16, cells), bo = buf((size_t)M * 16, NULL);
+    size_t g = (size_t)M * 256, l = 256;
+
+    SET(k, 0, b0);
+    SET(k, 1, b1);
+    SET(k, 2, (cl_int)H);
+    SET(k, 3, (cl_int)W);
+    SET(k, 4, bc);
+    SET(k, 5, (cl_int)M);
+    SET(k, 6, (cl_float)T);
+    SET(k, 7, bo);
+    launch(k, 1, &g, &l);
+    buf_file(bo, (size_t)M * 4, fo);
+    printf("{\"case\": \"%s\", \"kernel\": \"eloftr_fine\"}\n", spec);
+    free(cells);
+    clReleaseMemObject(b0);
+    clReleaseMemObject(b1);
+    clReleaseMemObject(bc);
+    clReleaseMemObject(bo);
+    clReleaseKernel(k);
+}
+
 /* A code object of DIR when it was built, else NULL. */
 static cl_program load_optional(const char *dir, const char *name)
 {
@@ -1386,6 +1419,9 @@ int main(int argc, char **argv)
         else if (sscanf(argv[i], "ropex:%d:%d:%d:%d:%d:%d:%1023[^:]:%1023[^:]:%1023s", &a, &b,
                         &c, &d, &gm[0], &e5, f1, f2, f3) == 9)
             exec_rope(argv[i], a, b, c, d, gm[0], e5, f1, f2, f3);
+        else if (sscanf(argv[i], "finex:%d:%d:%d:%f:%1023[^:]:%1023[^:]:%1023[^:]:%1023s", &a,
+                        &b, &c, &fl, f1, f2, f3, f4) == 8)
+            exec_fine(argv[i], a, b, c, fl, f1, f2, f3, f4);
         else if (sscanf(argv[i], "gemm:%d:%d:%d:%d", &a, &b, &c, &d) == 4)
             case_gemm(argv[i], a, b, c, d);
         else if (sscanf(argv[i], "vitblock:%d", &a) == 1)

@@ -21,7 +21,9 @@ to files; the HIP kernels run here on the same arrays.
   * ops.cl's gemm / gemm_big, attention, layernorm, softmax_rows,
     grid_sample, conv5x5 (with the fused instance norm and PReLU),
     conv2d, chan_stats, resize_bilinear, pool2d and rope with ops.c's
-    dispatch, roma_kernels.cl's local
+    dispatch, eloftr_kernels.cl's fine matching (the same positions and
+    keypoints within 1e-3 px wherever the first stage's float64 top-2
+    margin exceeds 1e-3), roma_kernels.cl's local
     correlation, warp sampling and depthwise 5 x 5 with roma.c's, at the
     pipelines' shapes (the ViT's qkv and attention of a 560² image, the
     refiners' 1/8 and 1/4 maps of 864²) and ragged ones: contractions
@@ -536,3 +538,33 @@ def test_rope_vs_reference_kernel(dev, ic, tmp_path, rows, nh, d, npos, inter):
     bx, bc = dev.upload(x), dev.upload(cs)
     dev.api.ops_rope(dev.po, bx.mem, 0, ld, rows, nh, d, npos, bc.mem, inter)
     assert rel(dev.read(bx, rows * ld), ref) <= 1e-6
+
+
+@pytest.mark.parametrize("H,W,Mn", [(48, 64, 500), (160, 160, 1000)])
+def test_fine_vs_reference_kernel(dev, ic, tmp_path, H, W, Mn):
+    """ELoFTR's fine matching (eloftr_kernels.cl's eloftr_fine, one
+    work-group per coarse match) against eloftr_fine on the same windows,
+    the border cells included: wherever the float64 first-stage top-2
+    margin exceeds 1e-3 the same integer positions and sub-pixel
+    keypoints within 1e-3 px."""
+    rng = np.random.default_rng(H + Mn)
+    h, w = H // 8, W // 8
+    f0 = rng.standard_normal((64, H, W)).astype(np.float32)
+    f1 = rng.standard_normal((64, H, W)).astype(np.float32)
+    cells = np.stack([rng.integers(0, w, Mn), rng.integers(0, h, Mn),
+                      rng.integers(0, w, Mn), rng.integers(0, h, Mn)], 1).astype(np.int32)
+    cells[:3] = [[0, 0, 0, 0], [w - 1, h - 1, w - 1, h - 1], [0, h - 1, w - 1, 0]]
+    cells = np.ascontiguousarray(cells)
+    f = files(tmp_path, f0=f0, f1=f1)
+    cf, of = tmp_path / "cells.i32", tmp_path / "out.f32"
+    cells.tofile(cf)
+    run_reference(f"finex:{H}:{W}:{Mn}:10.0:{f['f0']}:{f['f1']}:{cf}:{of}")
+    ref = np.fromfile(of, np.float32).reshape(-1, 4)
+    b0, b1, bc, bo = dev.upload(f0), dev.upload(f1), dev.upload(cells), dev.zeros(4 * Mn)
+    dev.api.eloftr_fine(dev.po, b0.mem, b1.mem, H, W, bc.mem, Mn, 10.0, bo.mem)
+    got = dev.read(bo, 4 * Mn).reshape(-1, 4)
+    _, margin = elo_ref.fine_bruteforce(f0, f1, cells)
+    sure = margin > MARGIN
+    assert sure.mean() > 0.9
+    assert np.array_equal(np.floor(got[sure, :2]), np.floor(ref[sure, :2]))
+    assert np.abs(got[sure] - ref[sure]).max() <= 1e-3
