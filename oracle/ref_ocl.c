@@ -55,7 +55,9 @@
  *         resx:C:h:w:H:W:align:scale:IN:OUT     resize_bilinear
  *         poolx:C:H:W:ks:s:p:max:IN:OUT         pool2d
  *         ropex:rows:ld:nh:d:npos:interleaved:X:CS:OUT   rope
- *         finex:H:W:M:T:F0:F1:CELLS:OUT          eloftr_fine */
+ *         finex:H:W:M:T:F0:F1:CELLS:OUT          eloftr_fine
+ *         smallx:KIND:a:b:c:x:y:F1:F2:F3:F4:F5:OUT   the small
+ *                                element-wise kernels (exec_small) */
 
 #define CL_TARGET_OPENCL_VERSION 120
 #include <CL/cl.h>
@@ -1311,6 +1313,231 @@ static void exec_fine(const char *spec, int H, int W, int M, float T, const char
     clReleaseKernel(k);
 }
 
+/* Launch kernel name on a 1-D range of n items (local size 256, as
+ * ops.c's run1d, or the runtime's choice when l0 is 0, as roma.c's run). */
+static void launch1d(cl_kernel k, size_t n, int l0)
+{
+    size_t l = 256, g = (n + l - 1) / l * l;
+
+    if (l0)
+        launch(k, 1, &g, &l);
+    else
+        launch(k, 1, &n, NULL);
+}
+
+/* smallx:KIND:a:b:c:x:y:F1:F2:F3:F4:F5:OUT — the small element-wise
+ * kernels with their reference dispatch; a, b, c integers, x, y floats,
+ * F1..F5 input files ("-" unused), OUT the output buffer(s) in order:
+ *   affine   chan_affine (ops.c:354-373): C=a HW=b act=c slope=x;
+ *            X MEAN RSTD G B; OUT Y
+ *   prelu    prelu (ops.c:375-386): C=a HW=b; X ALPHA; OUT Y
+ *   act      act_map (ops.c:388-400): n=a act=c slope=x; X; OUT Y
+ *   unfold   unfold (ops.c:218-234), 3 x 3 stride b padding c over
+ *            C=a channels of an 16 x 20 map; IN; OUT
+ *   avgpool2 avgpool2 (ops.c:546-557): C=a H=b W=c; IN; OUT
+ *   transpose transpose2d (ops.c:580-593): B=a R=b C=c; IN; OUT
+ *   axpby    axpby (ops.c:595-610): n=a bmod=b alpha=x beta=y; A B; OUT
+ *   rownorm  roma_row_norm (roma.c:858-868): rows=a C=b; X; OUT
+ *   cosexp   roma_cos_exp (roma.c:838-856): N=a M=b T=x eps=y; S NX NY;
+ *            OUT S
+ *   disp     roma_disp (roma.c:940-952): H=a W=b fx=x fy=y; FLOW; OUT
+ *   update   roma_update (roma.c:987-995): n=a scale=x Wf=y Hf=c;
+ *            FLOW CERT D; OUT FLOW then CERT
+ *   update2  roma2_update (roma.c:1095-1103): n=a W=x H=y; FLOW CONF D;
+ *            OUT FLOW then CONF */
+static void exec_small(const char *spec, const char *kind, int a, int b, int c, float x,
+                       float y, char f[5][1024], const char *fo)
+{
+    cl_mem in[5] = {NULL, NULL, NULL, NULL, NULL}, o1 = NULL, o2 = NULL;
+    size_t no1 = 0, no2 = 0, sz[5] = {0, 0, 0, 0, 0};
+    cl_kernel k;
+    int i;
+
+    if (!strcmp(kind, "affine")) {
+        const size_t n = (size_t)a * b;
+
+        sz[0] = n, sz[1] = sz[2] = sz[3] = sz[4] = (size_t)a;
+        for (i = 0; i < 5; i++)
+            in[i] = file_buf(f[i], sz[i], NULL);
+        o1 = buf(n * 4, NULL), no1 = n;
+        k = kern(prog_ops, "chan_affine");
+        SET(k, 0, in[0]);
+        SET(k, 1, o1);
+        SET(k, 2, (cl_int)b);
+        SET(k, 3, (cl_int)n);
+        SET(k, 4, in[1]);
+        SET(k, 5, in[2]);
+        SET(k, 6, in[3]);
+        SET(k, 7, in[4]);
+        SET(k, 8, (cl_int)c);
+        SET(k, 9, (cl_float)x);
+        launch1d(k, n, 1);
+    }
+    else if (!strcmp(kind, "prelu")) {
+        const size_t n = (size_t)a * b;
+
+        in[0] = file_buf(f[0], n, NULL), in[1] = file_buf(f[1], (size_t)a, NULL);
+        o1 = buf(n * 4, NULL), no1 = n;
+        k = kern(prog_ops, "prelu");
+        SET(k, 0, in[0]);
+        SET(k, 1, o1);
+        SET(k, 2, (cl_int)b);
+        SET(k, 3, (cl_int)n);
+        SET(k, 4, in[1]);
+        launch1d(k, n, 1);
+    }
+    else if (!strcmp(kind, "act")) {
+        in[0] = file_buf(f[0], (size_t)a, NULL);
+        o1 = buf((size_t)a * 4, NULL), no1 = (size_t)a;
+        k = kern(prog_ops, "act_map");
+        SET(k, 0, in[0]);
+        SET(k, 1, o1);
+        SET(k, 2, (cl_int)a);
+        SET(k, 3, (cl_int)c);
+        SET(k, 4, (cl_float)x);
+        launch1d(k, (size_t)a, 1);
+    }
+    else if (!strcmp(kind, "unfold")) {
+        const int H = 16, W = 20, Ho = (H + 2 * c - 3) / b + 1, Wo = (W + 2 * c - 3) / b + 1;
+        const cl_int v[13] = {a, H, W, 3, 3, b, b, c, c, Ho, Wo, 0, Ho * Wo};
+        size_t gs[2] = {(size_t)(Ho * Wo + 63) / 64 * 64, (size_t)a * 9}, ls[2] = {64, 1};
+
+        in[0] = file_buf(f[0], (size_t)a * H * W, NULL);
+        no1 = (size_t)a * 9 * Ho * Wo, o1 = buf(no1 * 4, NULL);
+        k = kern(prog_ops, "unfold");
+        SET(k, 0, in[0]);
+        for (i = 0; i < 13; i++)
+            SET(k, 1 + i, v[i]);
+        SET(k, 14, o1);
+        launch(k, 2, gs, ls);
+    }
+    else if (!strcmp(kind, "avgpool2")) {
+        size_t g[3] = {(size_t)c / 2, (size_t)b / 2, (size_t)a};
+
+        in[0] = file_buf(f[0], (size_t)a * b * c, NULL);
+        no1 = (size_t)a * (b / 2) * (c / 2), o1 = buf(no1 * 4, NULL);
+        k = kern(prog_ops, "avgpool2");
+        SET(k, 0, in[0]);
+        SET(k, 1, (cl_int)b);
+        SET(k, 2, (cl_int)c);
+        SET(k, 3, o1);
+        launch(k, 3, g, NULL);
+    }
+    else if (!strcmp(kind, "transpose")) {
+        size_t g[3] = {(size_t)(c + 15) / 16 * 16, (size_t)(b + 15) / 16 * 16, (size_t)a};
+        size_t l[3] = {16, 16, 1};
+
+        in[0] = file_buf(f[0], (size_t)a * b * c, NULL);
+        no1 = (size_t)a * b * c, o1 = buf(no1 * 4, NULL);
+        k = kern(prog_ops, "transpose2d");
+        SET(k, 0, in[0]);
+        SET(k, 1, o1);
+        SET(k, 2, (cl_int)b);
+        SET(k, 3, (cl_int)c);
+        launch(k, 3, g, l);
+    }
+    else if (!strcmp(kind, "axpby")) {
+        in[0] = file_buf(f[0], (size_t)a, NULL), in[1] = file_buf(f[1], (size_t)b, NULL);
+        o1 = buf((size_t)a * 4, NULL), no1 = (size_t)a;
+        k = kern(prog_ops, "axpby");
+        SET(k, 0, o1);
+        SET(k, 1, in[0]);
+        SET(k, 2, (cl_float)x);
+        SET(k, 3, in[1]);
+        SET(k, 4, (cl_float)y);
+        SET(k, 5, (cl_int)a);
+        SET(k, 6, (cl_int)b);
+        launch1d(k, (size_t)a, 1);
+    }
+    else if (!strcmp(kind, "rownorm")) {
+        in[0] = file_buf(f[0], (size_t)a * b, NULL);
+        o1 = buf((size_t)a * 4, NULL), no1 = (size_t)a;
+        k = kern(prog_roma, "roma_row_norm");
+        SET(k, 0, in[0]);
+        SET(k, 1, (cl_int)a);
+        SET(k, 2, (cl_int)b);
+        SET(k, 3, o1);
+        launch1d(k, (size_t)a, 0);
+    }
+    else if (!strcmp(kind, "cosexp")) {
+        size_t g[2] = {(size_t)b, (size_t)a};
+
+        o1 = file_buf(f[0], (size_t)a * b, NULL), no1 = (size_t)a * b;
+        in[1] = file_buf(f[1], (size_t)a, NULL), in[2] = file_buf(f[2], (size_t)b, NULL);
+        k = kern(prog_roma, "roma_cos_exp");
+        SET(k, 0, o1);
+        SET(k, 1, in[1]);
+        SET(k, 2, in[2]);
+        SET(k, 3, (cl_int)a);
+        SET(k, 4, (cl_int)b);
+        SET(k, 5, (cl_float)x);
+        SET(k, 6, (cl_float)y);
+        launch(k, 2, g, NULL);
+    }
+    else if (!strcmp(kind, "disp")) {
+        const size_t n = (size_t)a * b;
+
+        in[0] = file_buf(f[0], 2 * n, NULL);
+        o1 = buf(2 * n * 4, NULL), no1 = 2 * n;
+        k = kern(prog_roma, "roma_disp");
+        SET(k, 0, in[0]);
+        SET(k, 1, (cl_int)a);
+        SET(k, 2, (cl_int)b);
+        SET(k, 3, (cl_float)x);
+        SET(k, 4, (cl_float)y);
+        SET(k, 5, o1);
+        launch1d(k, n, 0);
+    }
+    else if (!strcmp(kind, "update")) {
+        o1 = file_buf(f[0], 2 * (size_t)a, NULL), no1 = 2 * (size_t)a;
+        o2 = file_buf(f[1], (size_t)a, NULL), no2 = (size_t)a;
+        in[2] = file_buf(f[2], 3 * (size_t)a, NULL);
+        k = kern(prog_roma, "roma_update");
+        SET(k, 0, o1);
+        SET(k, 1, o2);
+        SET(k, 2, in[2]);
+        SET(k, 3, (cl_int)a);
+        SET(k, 4, (cl_float)x);
+        SET(k, 5, (cl_float)y);
+        SET(k, 6, (cl_float)c);
+        launch1d(k, (size_t)a, 0);
+    }
+    else if (!strcmp(kind, "update2")) {
+        o1 = file_buf(f[0], 2 * (size_t)a, NULL), no1 = 2 * (size_t)a;
+        o2 = file_buf(f[1], 4 * (size_t)a, NULL), no2 = 4 * (size_t)a;
+        in[2] = file_buf(f[2], 6 * (size_t)a, NULL);
+        k = kern(prog_roma, "roma2_update");
+        SET(k, 0, o1);
+        SET(k, 1, o2);
+        SET(k, 2, in[2]);
+        SET(k, 3, (cl_int)a);
+        SET(k, 4, (cl_float)x);
+        SET(k, 5, (cl_float)y);
+        launch1d(k, (size_t)a, 0);
+    }
+    else {
+        fprintf(stderr, "ref_ocl: unknown small kernel %s\n", kind);
+        exit(2);
+    }
+    {
+        float *h = malloc((no1 + no2) * 4);
+
+        readb(o1, no1 * 4, h);
+        if (o2)
+            readb(o2, no2 * 4, h + no1);
+        write_file(fo, h, (no1 + no2) * 4);
+        free(h);
+    }
+    printf("{\"case\": \"%s\", \"kernel\": \"%s\"}\n", spec, kind);
+    for (i = 0; i < 5; i++)
+        if (in[i] && in[i] != o1)
+            clReleaseMemObject(in[i]);
+    clReleaseMemObject(o1);
+    if (o2)
+        clReleaseMemObject(o2);
+    clReleaseKernel(k);
+}
+
 /* A code object of DIR when it was built, else NULL. */
 static cl_program load_optional(const char *dir, const char *name)
 {
@@ -1365,6 +1592,8 @@ int main(int argc, char **argv)
         long lo = 0;
         float fl = 0.0f;
         int gm[11] = {0};
+        float fl2 = 0.0f;
+        char kind[32], ff[5][1024];
         char f1[1024], f2[1024], f3[1024], f4[1024], f5[1024], f6[1024], f7[1024];
 
         if (sscanf(argv[i], "coarse:%d:%d:%1023[^:]:%1023s", &a, &b, f1, f2) == 4)
@@ -1422,6 +1651,10 @@ int main(int argc, char **argv)
         else if (sscanf(argv[i], "finex:%d:%d:%d:%f:%1023[^:]:%1023[^:]:%1023[^:]:%1023s", &a,
                         &b, &c, &fl, f1, f2, f3, f4) == 8)
             exec_fine(argv[i], a, b, c, fl, f1, f2, f3, f4);
+        else if (sscanf(argv[i], "smallx:%31[^:]:%d:%d:%d:%f:%f:%1023[^:]:%1023[^:]:%1023[^:]:"
+                        "%1023[^:]:%1023[^:]:%1023s", kind, &a, &b, &c, &fl, &fl2, ff[0], ff[1],
+                        ff[2], ff[3], ff[4], f1) == 12)
+            exec_small(argv[i], kind, a, b, c, fl, fl2, ff, f1);
         else if (sscanf(argv[i], "gemm:%d:%d:%d:%d", &a, &b, &c, &d) == 4)
             case_gemm(argv[i], a, b, c, d);
         else if (sscanf(argv[i], "vitblock:%d", &a) == 1)

@@ -30,6 +30,9 @@ to files; the HIP kernels run here on the same arrays.
     within 1e-3 of the reference kernel's outputs, element-wise kernels
     within 1e-4, the depthwise convolution, rotations and average pools
     within 1e-6, max pools bit-exact.
+  * the small element-wise kernels of ops.cl and roma_kernels.cl
+    (chan_affine, prelu, act_map, unfold, avgpool2, transpose2d, axpby,
+    roma_row_norm, roma_cos_exp, roma_disp, roma_update, roma2_update).
 
 Skipped with the reason when the reference's kernels were not built (the
 reference is needed at build time) or no OpenCL GPU device is present."""
@@ -568,3 +571,121 @@ def test_fine_vs_reference_kernel(dev, ic, tmp_path, H, W, Mn):
     assert sure.mean() > 0.9
     assert np.array_equal(np.floor(got[sure, :2]), np.floor(ref[sure, :2]))
     assert np.abs(got[sure] - ref[sure]).max() <= 1e-3
+
+
+def _small_case(kind, rng):
+    """Inputs, the reference spec fields and this library's call for one
+    small element-wise kernel: (a, b, c, x, y, inputs, ours, tol)."""
+    U = lambda *s: rng.uniform(-2, 2, s).astype(np.float32)  # noqa: E731
+    if kind == "affine":
+        C, HW, act = 24, 999, 3
+        X, mu, rs = U(C, HW), U(C), rng.uniform(0.2, 2, C).astype(np.float32)
+        g, b = U(C), U(C)
+        return (C, HW, act, 0.1, 0.0, [X, mu, rs, g, b],
+                lambda d, m, o: d.api.ops_chan_affine(d.po, m[0], o, C, HW, m[1], m[2], m[3],
+                                                      m[4], act, 0.1), C * HW, 1e-6)
+    if kind == "prelu":
+        C, HW = 16, 1234
+        X, al = U(C, HW), rng.uniform(0, 0.5, C).astype(np.float32)
+        return (C, HW, 0, 0.0, 0.0, [X, al],
+                lambda d, m, o: d.api.ops_prelu(d.po, m[0], o, C, HW, m[1]), C * HW, 1e-6)
+    if kind == "act":
+        n, act = 100003, 1
+        X = U(n)
+        return (n, 0, act, 0.0, 0.0, [X],
+                lambda d, m, o: d.api.ops_act(d.po, m[0], o, n, act, 0.0), n, 1e-4)
+    if kind == "unfold":
+        C, s, p = 5, 2, 1
+        Ho, Wo = (16 + 2 * p - 3) // s + 1, (20 + 2 * p - 3) // s + 1
+        X = U(C, 16, 20)
+
+        def ours(d, m, o):
+            g = ic_geom(3, 3, s, s, p, p)
+            d.api.ops_unfold(d.po, m[0], C, 16, 20, ctypes.byref(g), o)
+        return (C, s, p, 0.0, 0.0, [X], ours, C * 9 * Ho * Wo, 0.0)
+    if kind == "avgpool2":
+        C, H, W = 7, 30, 42
+        X = U(C, H, W)
+        return (C, H, W, 0.0, 0.0, [X],
+                lambda d, m, o: d.api.ops_avgpool2(d.po, m[0], C, H, W, o),
+                C * (H // 2) * (W // 2), 1e-6)
+    if kind == "transpose":
+        B, R, Cc = 3, 37, 129
+        X = U(B, R, Cc)
+        return (B, R, Cc, 0.0, 0.0, [X],
+                lambda d, m, o: d.api.ops_transpose(d.po, m[0], o, B, R, Cc), B * R * Cc, 0.0)
+    if kind == "axpby":
+        n, bmod = 10000, 77
+        A, Bv = U(n), U(bmod)
+        return (n, bmod, 0, 0.7, -1.3, [A, Bv],
+                lambda d, m, o: d.api.ops_axpby(d.po, o, m[0], 0.7, m[1], -1.3, n, bmod), n,
+                1e-6)
+    if kind == "rownorm":
+        rows, C = 1600, 512
+        X = U(rows, C)
+        return (rows, C, 0, 0.0, 0.0, [X],
+                lambda d, m, o: d.api.roma_row_norm(d.po, m[0], rows, C, o), rows, 1e-5)
+    if kind == "cosexp":
+        N, M = 300, 411
+        S = U(N, M) * 10
+        nx, ny = rng.uniform(3, 6, N).astype(np.float32), rng.uniform(3, 6, M).astype(np.float32)
+        return (N, M, 0, 0.2, 1e-6, [S, nx, ny], None, N * M, 1e-4)
+    if kind == "disp":
+        H, W = 108, 96
+        fl = U(2, H * W) / 2
+        return (H, W, 0, 3.5, 2.5, [fl],
+                lambda d, m, o: d.api.roma_disp(d.po, m[0], H, W, 3.5, 2.5, o), 2 * H * W,
+                1e-6)
+    if kind == "update":
+        n = 11664
+        return (n, 0, 108, 8.0, 108.0, [U(2, n), U(n), U(3, n)], None, 3 * n, 1e-6)
+    if kind == "update2":
+        n = 16384
+        return (n, 0, 0, 128.0, 128.0, [U(2, n), U(4, n), U(6, n) * 12], None, 6 * n, 1e-5)
+    raise ValueError(kind)
+
+
+def ic_geom(kh, kw, sy, sx, py, px):
+    from conftest import load_package
+    return load_package().geom(kh, kw, sy, sx, py, px, 1, 1, 1)
+
+
+SMALL = ["affine", "prelu", "act", "unfold", "avgpool2", "transpose", "axpby", "rownorm",
+         "cosexp", "disp", "update", "update2"]
+
+
+@pytest.mark.parametrize("kind", SMALL)
+def test_small_kernels_vs_reference(dev, ic, tmp_path, kind):
+    """The small element-wise kernels of ops.cl (chan_affine, prelu,
+    act_map, unfold, avgpool2, transpose2d, axpby) and roma_kernels.cl
+    (row_norm, cos_exp, disp, update, roma2_update) against this
+    library's on the same inputs: copies bit-exact, arithmetic within
+    1e-6, transcendental ones within 1e-5 to 1e-4."""
+    rng = np.random.default_rng(len(kind) * 7 + 1)
+    a, b, c, x, y, ins, ours, nout, tol = _small_case(kind, rng)
+    paths = [str(tmp_path / f"in{i}.f32") for i in range(len(ins))]
+    for p, v in zip(paths, ins):
+        np.ascontiguousarray(v, np.float32).tofile(p)
+    paths += ["-"] * (5 - len(paths))
+    of = tmp_path / "out.f32"
+    run_reference(f"smallx:{kind}:{a}:{b}:{c}:{x!r}:{y!r}:{':'.join(paths)}:{of}")
+    ref = np.fromfile(of, np.float32)
+    bufs = [dev.upload(v) for v in ins]
+    if kind == "cosexp":
+        dev.api.roma_cos_exp(dev.po, bufs[0].mem, bufs[1].mem, bufs[2].mem, a, b, x, y)
+        got = dev.read(bufs[0], nout)
+    elif kind == "update":
+        dev.api.roma_update(dev.po, bufs[0].mem, bufs[1].mem, bufs[2].mem, a, x, y, float(c))
+        got = np.concatenate([dev.read(bufs[0], 2 * a), dev.read(bufs[1], a)])
+    elif kind == "update2":
+        dev.api.roma2_update(dev.po, bufs[0].mem, bufs[1].mem, bufs[2].mem, a, x, y)
+        got = np.concatenate([dev.read(bufs[0], 2 * a), dev.read(bufs[1], 4 * a)])
+    else:
+        out = dev.zeros(nout)
+        ours(dev, [m.mem for m in bufs], out.mem)
+        got = dev.read(out, nout)
+    assert got.shape == ref.shape
+    if tol == 0.0:
+        assert np.array_equal(got, ref)
+    else:
+        assert rel(got, ref) <= tol
