@@ -1,15 +1,17 @@
 /* SPDX-License-Identifier: Unlicense */
 
-/* ORACLE — measurement infrastructure only (bench.py's baseline leg):
- * the reference's own OpenCL kernels on the MI355X. oracle/Makefile
- * compiles ops.cl and roma_kernels.cl of i.coregistration.opencl, where
- * they lie, to gfx950 code objects in oracle/_ref/ (clang, the options of
- * ocl_backend.c:166-187); this program loads them through the ROCm
- * OpenCL runtime, launches kernels with the argument conventions and
- * work sizes of the reference's host dispatch (ops.c, roma.c), times
- * each case with OpenCL profiling events, checks a sample of outputs
- * against a double-precision recomputation (so that a mis-set argument
- * cannot pass as a timing), and prints one JSON line per case.
+/* ORACLE — test and measurement infrastructure only (bench.py's
+ * baseline leg, tests/test_reference_kernels_gpu.py): the reference's own
+ * OpenCL kernels on the MI355X. oracle/Makefile compiles ops.cl,
+ * roma_kernels.cl, eloftr_kernels.cl and disk_kernels.cl of
+ * i.coregistration.opencl, where they lie, to gfx950 code objects in
+ * oracle/_ref/ (clang, the options of ocl_backend.c:166-187); this
+ * program loads them through the ROCm OpenCL runtime and launches
+ * kernels with the argument conventions and work sizes of the
+ * reference's host dispatch (ops.c, roma.c, eloftr.c, disk.c). Timing
+ * cases time each case with OpenCL profiling events, check a sample of
+ * outputs against a double-precision recomputation (so that a mis-set
+ * argument cannot pass as a timing), and print one JSON line per case.
  *
  *   ref_ocl DIR CASE...
  *   CASE: gemm:M:N:K:transb      ops_gemm (ops.c:148-188), one product
