@@ -141,7 +141,7 @@ def test_local_corr(dev, ic, orc, C, H, W, r, smooth):
     smooth ones (the matrix-core path over the patch's window box, with a
     few broken cells), up to the refiner config's 1/8 and 1/4 shapes at
     864 x 864, radius 1 to 7; channel counts that are multiples of 4 (the
-    cell-major form, maps transposed first) and others (channel-major
+    cell-major form, f2 transposed first) and others (channel-major
     reads)."""
     print(f"[roma] local_corr C={C} {H}x{W} r={r} smooth={smooth}", flush=True)
     rng = np.random.default_rng(C + r)
