@@ -102,19 +102,32 @@ def eloftr_conv_layers(H, W):
 
 
 def eloftr_wino_layers(H, W):
-    """The stride-1 layers, which run as Winograd F(2 x 2, 3 x 3)
-    (conv_wino, 22 launches per pair); the 3 stride-2 layers run direct."""
+    """The stride-1 layers, which run as Winograd convolutions (22 launches
+    per pair); the 3 stride-2 layers run direct."""
     return [l for l in eloftr_conv_layers(H, W) if l[4] == 1]
 
 
-def eloftr_wino_flops(H, W):
+def eloftr_wino_forms(dev, H, W):
+    """The Winograd form the library gives each stride-1 layer of a pair on
+    this device (icoreg_conv_wino_choice): 4 for F(4 x 4, 3 x 3), 2 for
+    F(2 x 2, 3 x 3)."""
+    lib = load_package().lib()
+    return [lib.icoreg_conv_wino_choice(dev.po, 2, ci, h, w, co)
+            for ci, co, h, w, _ in eloftr_wino_layers(H, W)]
+
+
+def eloftr_wino_flops(H, W, forms):
     """Algorithmic matrix FLOPs of the Winograd launches of one pair: per
-    image, 2 x 16 x K x C per 2 x 2 output tile (the 16 transform-domain
-    products), ceil(Ho / 2) ceil(Wo / 2) tiles. The input and output
-    transforms (additions on the vector ALUs) are not counted."""
+    image, 2 x 16 x K x C per 2 x 2 output tile for F(2 x 2) (the 16
+    transform-domain products; ceil(Ho / 2) ceil(Wo / 2) tiles), 2 x 36 x
+    K x C per 4 x 4 tile for F(4 x 4). The input and output transforms
+    (vector-ALU work) are not counted."""
     f = 0.0
-    for ci, co, h, w, _ in eloftr_wino_layers(H, W):
-        f += 2 * 2.0 * 16 * co * ci * ((h + 1) // 2) * ((w + 1) // 2)
+    for (ci, co, h, w, _), form in zip(eloftr_wino_layers(H, W), forms):
+        if form == 4:
+            f += 2 * 2.0 * 36 * co * ci * ((h + 3) // 4) * ((w + 3) // 4)
+        else:
+            f += 2 * 2.0 * 16 * co * ci * ((h + 1) // 2) * ((w + 1) // 2)
     return f
 
 
@@ -124,13 +137,13 @@ def eloftr_wino_direct_flops(H, W):
     return sum(2 * 2.0 * co * h * w * ci * 9 for ci, co, h, w, _ in eloftr_wino_layers(H, W))
 
 
-def eloftr_wino_bytes(H, W):
+def eloftr_wino_bytes(H, W, forms):
     """Algorithmic HBM bytes of the Winograd launches of one pair: both
     images' input and output read / written once, the transformed filters
-    (16 K C) and bias once per launch."""
+    (16 K C for F(2 x 2), 36 K C for F(4 x 4)) and bias once per launch."""
     b = 0
-    for ci, co, h, w, _ in eloftr_wino_layers(H, W):
-        b += 4 * (2 * (ci * h * w + co * h * w) + 16 * co * ci + co)
+    for (ci, co, h, w, _), form in zip(eloftr_wino_layers(H, W), forms):
+        b += 4 * (2 * (ci * h * w + co * h * w) + (36 if form == 4 else 16) * co * ci + co)
     return b
 
 
@@ -887,12 +900,13 @@ def bench_host_loop(ic, dev, net, pairs, steps):
     a = dev.api
     H, W = pairs[0][0].shape
     n = H * W
-    seq = [pairs[t % len(pairs)] for t in range(steps)]
+    # At least two pairs: the warm-up loops below run two.
+    seq = [pairs[t % len(pairs)] for t in range(max(steps, 2))]
     for g0, g1 in seq[:2]:
         a.eloftr_match(net.m, g0.ctypes.data, g1.ctypes.data, None, 1)
     dev.finish()
     t0 = time.perf_counter()
-    for g0, g1 in seq:
+    for g0, g1 in seq[:steps]:
         a.eloftr_match(net.m, g0.ctypes.data, g1.ctypes.data, None, 1)
     blocking = (time.perf_counter() - t0) * 1e3 / steps
 
@@ -1150,9 +1164,12 @@ def main():
     dev.set_profile(0)
     ps = args.profile_steps
     fl = eloftr_flops(H, W, nm)
-    wino_ms = table.get("conv_wino", (0.0, 0))[0] / ps
-    wino_calls = table.get("conv_wino", (0.0, 0))[1] / ps
-    wino_fl = eloftr_wino_flops(H, W)
+    # The Winograd convolutions, both forms: F(4 x 4) (conv_wino4) where the
+    # launch fills the GPU, F(2 x 2) (conv_wino) on the others.
+    forms = eloftr_wino_forms(dev, H, W)
+    wino_ms = (table.get("conv_wino", (0.0, 0))[0] + table.get("conv_wino4", (0.0, 0))[0]) / ps
+    wino_calls = (table.get("conv_wino", (0.0, 0))[1] + table.get("conv_wino4", (0.0, 0))[1]) / ps
+    wino_fl = eloftr_wino_flops(H, W, forms)
     achieved = wino_fl / (wino_ms * 1e-3) / 1e12 if wino_ms > 0 else 0.0
     direct_eq = eloftr_wino_direct_flops(H, W) / (wino_ms * 1e-3) / 1e12 if wino_ms > 0 else 0.0
     kernels = {k: {"ms_per_step": round(v[0] / ps, 4), "launches_per_step": v[1] / ps}
@@ -1251,11 +1268,14 @@ def main():
                             "fine_ms_at_max_matches": round(fine_nmax_ms, 4)},
               "roma560": roma, "cpu_baseline": cpu, **extra}
     write_detail(detail)
-    rf = {"kernel": "conv_wino (3x3 stride-1 conv, Winograd F(2x2,3x3) on fp32 MFMA)",
+    n4 = sum(1 for f in forms if f == 4)
+    rf = {"kernel": f"3x3 stride-1 conv on fp32 MFMA: Winograd F(4x4,3x3) (conv_wino4, {n4} "
+                    f"launches) where the launch fills the GPU, F(2x2,3x3) (conv_wino, "
+                    f"{len(forms) - n4}) on the others",
           "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA,
           "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
           "traffic": conv_traffic() if H == W == 640 else None,
-          "algorithmic_bytes_per_launch": round(eloftr_wino_bytes(H, W) / 22),
+          "algorithmic_bytes_per_launch": round(eloftr_wino_bytes(H, W, forms) / len(forms)),
           "launches_per_step": wino_calls, "gflop_per_step": round(wino_fl / 1e9, 2),
           "direct_equivalent_tflops": round(direct_eq, 2)}
     cc = conv_counters() if H == W == 640 else None

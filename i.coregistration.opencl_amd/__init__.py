@@ -239,6 +239,8 @@ SIGNATURES = {
     "icoreg_roma_last": (_I, [_P]),
     "icoreg_roma_set_imagenet": (None, [_P, _I]),
     "icoreg_gp_test_wait": (None, [_I, _I]),
+    "icoreg_conv_wino_form": (None, [_I]),
+    "icoreg_conv_wino_choice": (_I, [_P, _I, _I, _I, _I, _I]),
     "icoreg_roma_gp_retries": (_I, [_P]),
 }
 
@@ -254,7 +256,8 @@ _NO_CHECK = {"ocl_graph_free", "icoreg_set_fatal_mode", "icoreg_last_error", "ic
              "icoreg_roma_new", "icoreg_roma_result", "icoreg_roma_buffer",
              "icoreg_roma_set_imagenet", "icoreg_disk_new", "icoreg_disk_buffer",
              "icoreg_roma_last", "disk_topn_work_bytes", "adalam_nearest_work_bytes",
-             "icoreg_gp_test_wait", "icoreg_roma_gp_retries"}
+             "icoreg_gp_test_wait", "icoreg_roma_gp_retries", "icoreg_conv_wino_form",
+             "icoreg_conv_wino_choice"}
 
 _lib = None
 

@@ -83,9 +83,22 @@ size_t conv_wino_part_floats(const conv_args &a, int nb, const wino_split &sp);
 void conv_wino_launch(const conv_args &a, const float *U, int nb, const wino_split &sp,
                       hipStream_t s);
 
+/* Winograd F(4 x 4, 3 x 3) path (conv_wino4.hip): the F(2 x 2) path's
+ * shapes with C % 4 == 0, K >= 16 and no input normalisation. Filters in
+ * the kernel's operand order, conv_wino4_weight_floats(K, C) floats. */
+bool conv_wino4_ok(int C, int K, bool norm);
+size_t conv_wino4_weight_floats(int K, int C);
+void conv_wino4_weights(const float *w, int K, int C, float *U, hipStream_t s);
+/* Blocks of a launch: 32 output channels x 32 tiles of 4 x 4 pixels. */
+long long conv_wino4_units(int K, int Ho, int Wo, int nb);
+void conv_wino4_launch(const conv_args &a, const float *U, int nb, hipStream_t s);
+
 /* Filters of a 3 x 3 convolution without input normalisation transformed
- * once (a new buffer), for callers that run the same weights many times. */
+ * once (a new buffer), for callers that run the same weights many times:
+ * the F(2 x 2) form, followed, where conv_wino4_ok, by the F(4 x 4) form
+ * at float offset conv_wino4_offset(K, C). */
 cl_mem conv_wino_prepare(struct ops *o, cl_mem w, int K, int C);
+size_t conv_wino4_offset(int K, int C);
 /* ops_conv2d_batch for 3 x 3, stride 1, padding 1, one group, with U
  * from conv_wino_prepare (w is used only when the Winograd path does not
  * take the shape). */

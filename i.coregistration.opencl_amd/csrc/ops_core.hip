@@ -382,6 +382,58 @@ __global__ void __launch_bounds__(256)
     out[idx] = icoreg_act(acc, act, slope);
 }
 
+/* Which Winograd form a convolution takes (icoreg_conv_wino_form): 0 the
+ * shape's choice, 2 or 4 the F(2 x 2) or F(4 x 4) form wherever it
+ * applies. Process-wide; for tests and measurements. */
+static int g_wino_form = 0;
+
+extern "C" void icoreg_conv_wino_form(int form)
+{
+    g_wino_form = form == 2 || form == 4 ? form : 0;
+}
+
+/* F(4 x 4) where its kernel applies: channels in slices of 4, rows of
+ * 16-byte aligned 4-float chunks (the input patch arrives by 16-byte LDS
+ * DMA), byte offsets within an image below 2^31. */
+static bool wino4_applies(const conv_args &a)
+{
+    return conv_wino4_ok(a.C, a.K, a.mean != nullptr) && a.W % 4 == 0 &&
+           a.in_stride % 4 == 0 && ((unsigned long long)(size_t)a.in & 15) == 0 &&
+           (long long)a.C * a.H * a.W * 4 < (1LL << 31);
+}
+
+/* The shape's choice: F(4 x 4) where its launch gives every CU a block
+ * (32 output channels x 32 tiles of 4 x 4); with fewer blocks than CUs
+ * (ELoFTR's 80 x 80 layers: 240 blocks) a CU runs one wave a SIMD and
+ * F(2 x 2), whose smaller blocks fill the GPU, was faster. */
+static bool wino4_chosen(const conv_args &a, int nb, int cus)
+{
+    if (g_wino_form == 2 || !wino4_applies(a))
+        return false;
+    if (g_wino_form == 4)
+        return true;
+    return conv_wino4_units(a.K, a.Ho, a.Wo, nb) >= cus;
+}
+
+/* The Winograd form conv_impl gives a 3 x 3, stride 1, padding 1
+ * convolution of nb images of C x H x W (contiguous, 16-byte aligned) to
+ * K channels without input normalisation on this device: 4, 2, or 0 (not
+ * a Winograd shape). */
+extern "C" int icoreg_conv_wino_choice(struct ops *o, int nb, int C, int H, int W, int K)
+{
+    conv_args a = {};
+
+    if (!o || nb < 1 || !conv_wino_supported(3, 3, 1, 1, 1, 1, 1, 1, 1, C, K, H, W))
+        return 0;
+    a.in = reinterpret_cast<const float *>(static_cast<uintptr_t>(256));
+    a.in_stride = (long long)C * H * W;
+    a.C = C;
+    a.H = a.Ho = H;
+    a.W = a.Wo = W;
+    a.K = K;
+    return wino4_chosen(a, nb, o->ocl->cu_count) ? 4 : 2;
+}
+
 /* ops_conv2d over nb images (in_stride / out_stride floats apart). */
 /* U: the filters already in Winograd form (conv_wino_prepare) or NULL. */
 static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
@@ -452,6 +504,28 @@ static void conv_impl(struct ops *o, int nb, cl_mem in, long long in_stride,
         a.slope = slope;
         a.split = 1;
         a.part = nullptr;
+        if (wino4_chosen(a, nb, o->ocl->cu_count) &&
+            (!U || U->bytes >= (conv_wino4_offset(K, C) + conv_wino4_weight_floats(K, C)) *
+                                   sizeof(float))) {
+            /* F(4 x 4, 3 x 3): the prepared filters' second form, or the
+             * filters transformed into scratch. */
+            const float *U4;
+
+            if (U)
+                U4 = cfptr(U) + conv_wino4_offset(K, C);
+            else {
+                cl_mem sc = scratch_get(o, conv_wino4_weight_floats(K, C) * sizeof(float));
+
+                prof_scope ps(o->ocl, "conv_wino_weights");
+                conv_wino4_weights(cfptr(w), K, C, fptr(sc), stream_of(o->ocl));
+                launch_check("conv_wino_weights");
+                U4 = cfptr(sc);
+            }
+            prof_scope ps(o->ocl, "conv_wino4");
+            conv_wino4_launch(a, U4, nb, stream_of(o->ocl));
+            launch_check("conv_wino4");
+            return;
+        }
         wino_split sp = conv_wino_plan(a, nb, o->ocl->cu_count);
         const size_t pb = conv_wino_part_floats(a, nb, sp) * sizeof(float);
         const float *Uf;
@@ -609,14 +683,25 @@ extern "C" void ops_conv2d_batch(struct ops *o, int nb, cl_mem in,
     ICOREG_API_END
 }
 
+size_t conv_wino4_offset(int K, int C)
+{
+    return (conv_wino_weight_floats(K, C, false) + 63) & ~(size_t)63;
+}
+
 cl_mem conv_wino_prepare(struct ops *o, cl_mem w, int K, int C)
 {
+    const bool f4 = conv_wino4_ok(C, K, false);
+    size_t n = conv_wino_weight_floats(K, C, false);
     cl_mem U;
 
     need_floats(w, 0, (long long)K * C * 9, "conv_wino_prepare", "weights");
-    U = ocl_alloc(o->ocl, conv_wino_weight_floats(K, C, false) * sizeof(float),
-                  "Winograd filters");
+    if (f4)
+        n = conv_wino4_offset(K, C) + conv_wino4_weight_floats(K, C);
+    U = ocl_alloc(o->ocl, n * sizeof(float), "Winograd filters");
     conv_wino_weights(cfptr(w), K, C, false, fptr(U), stream_of(o->ocl));
+    if (f4)
+        conv_wino4_weights(cfptr(w), K, C, fptr(U) + conv_wino4_offset(K, C),
+                           stream_of(o->ocl));
     launch_check("conv_wino_weights");
     return U;
 }

@@ -77,6 +77,14 @@ void icoreg_roma_set_imagenet(struct roma_model *m, int on);
  * spin_max polls and reports info = -1). Process-wide; for tests of the
  * give-up path and of roma_match's recovery. */
 void icoreg_gp_test_wait(int spin_max, int set_flags);
+/* Which Winograd form the same-size 3 x 3 convolutions take: 0 each
+ * shape's own choice (the default), 2 F(2 x 2, 3 x 3) or 4 F(4 x 4, 3 x 3)
+ * wherever that form applies. Process-wide; for tests and measurements. */
+void icoreg_conv_wino_form(int form);
+/* The form (4 or 2; 0: not a Winograd shape) the library gives a 3 x 3,
+ * stride 1, padding 1 convolution of nb contiguous C x H x W images to K
+ * channels on o's device, under the current icoreg_conv_wino_form. */
+int icoreg_conv_wino_choice(struct ops *o, int nb, int C, int H, int W, int K);
 /* How many times roma_match has re-run a GP solve through
  * roma_gp_solve_events after the in-kernel wait gave up. */
 int icoreg_roma_gp_retries(const struct roma_model *m);

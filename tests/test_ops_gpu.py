@@ -232,6 +232,61 @@ def test_conv_winograd_edges(shape, dev, ic, orc):
     assert err <= 1e-5, f"{shape}: {err:.2e}"
 
 
+# Shapes for the Winograd F(4 x 4) kernel (forced): 80 x 80-like and
+# VGG-like layers, outputs that end inside a block and inside a 4 x 4
+# tile, a partial block of 16 output channels, 8 x 8-tile blocks (narrow
+# maps) and 4 x 16-tile blocks (maps 192 pixels wide or more), an odd
+# number of 4-channel slices.
+WINO4_SHAPES = [
+    # (nb, C, H, W, K, act)
+    (2, 256, 20, 20, 256, 2),
+    (2, 64, 40, 48, 64, 2),
+    (1, 64, 37, 44, 36, 1),
+    (2, 32, 17, 72, 32, 0),
+    (1, 128, 3, 4, 64, 3),
+    (1, 40, 50, 32, 96, 2),
+    (2, 32, 26, 200, 48, 0),
+    (1, 36, 9, 196, 32, 2),
+    (1, 4, 12, 16, 32, 1),
+    (1, 8, 12, 64, 40, 4),
+]
+
+
+@pytest.mark.parametrize("shape", WINO4_SHAPES, ids=[str(s) for s in WINO4_SHAPES])
+def test_conv_winograd_f4(shape, dev, ic, orc):
+    """ops_conv2d_batch with the Winograd F(4 x 4, 3 x 3) kernel forced
+    (icoreg_conv_wino_form(4)), with the filters transformed by the call,
+    against the oracle's direct convolution: within 1e-5. One to nine
+    input-channel slices cover the DMA ring's start and end; every
+    activation; K not a multiple of 32; maps 8 and 16 tiles wide."""
+    import ctypes as C
+    from oracle_lib import fp
+    nb, Cc, H, W, K, act = shape
+    form = 4
+    print(f"[conv] winograd F(4x4) {shape}", flush=True)
+    rng = np.random.default_rng(500 + Cc + K + W)
+    x = rng.uniform(-1, 1, nb * Cc * H * W).astype(np.float32)
+    w = (rng.uniform(-1, 1, K * Cc * 9) / np.sqrt(Cc * 9)).astype(np.float32)
+    b = rng.uniform(-1, 1, K).astype(np.float32)
+    ref = np.zeros(nb * K * H * W, np.float32)
+    for i in range(nb):
+        orc.orc_conv2d(fp(x[i * Cc * H * W:]), Cc, H, W, fp(w), fp(b), K, 3, 3, 1, 1, 1, 1, 1,
+                       1, 1, None, None, None, act, 0.1, fp(ref[i * K * H * W:]))
+    X, Wt, B = dev.upload(x), dev.upload(w), dev.upload(b)
+    Y = dev.zeros(nb * K * H * W)
+    g = ic.geom(3, 3, 1, 1, 1, 1, 1, 1, 1)
+    lib = ic.lib()
+    lib.icoreg_conv_wino_form(form)
+    try:
+        dev.api.ops_conv2d_batch(dev.po, nb, X.mem, Cc * H * W, Cc, H, W, Wt.mem, B.mem, K,
+                                 C.byref(g), None, None, None, act, 0.1, Y.mem, K * H * W)
+        got = dev.read(Y, nb * K * H * W)
+    finally:
+        lib.icoreg_conv_wino_form(0)
+    err = opcases.rel_err(got, ref)
+    assert err <= 1e-5, f"{shape}: {err:.2e}"
+
+
 LN_SHAPES = [
     # (rows, C, affine): the RoMa ViT rows (1024) and the float4 variants'
     # lane tails (C / 4 not a multiple of 64), the scalar form (C % 4 != 0).
