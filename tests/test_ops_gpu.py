@@ -249,6 +249,9 @@ WINO4_SHAPES = [
     (1, 36, 9, 196, 32, 2),
     (1, 4, 12, 16, 32, 1),
     (1, 8, 12, 64, 40, 4),
+    # Grids of at least as many blocks as CUs (two blocks a CU resident).
+    (2, 32, 256, 256, 32, 2),
+    (2, 16, 208, 208, 48, 3),
 ]
 
 
@@ -258,7 +261,8 @@ def test_conv_winograd_f4(shape, dev, ic, orc):
     (icoreg_conv_wino_form(4)), with the filters transformed by the call,
     against the oracle's direct convolution: within 1e-5. One to nine
     input-channel slices cover the DMA ring's start and end; every
-    activation; K not a multiple of 32; maps 8 and 16 tiles wide."""
+    activation; K not a multiple of 32; maps 8 and 16 tiles wide; grids
+    below and above one block a CU."""
     import ctypes as C
     from oracle_lib import fp
     nb, Cc, H, W, K, act = shape
