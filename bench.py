@@ -218,8 +218,15 @@ def bench_roma(ic, dev, synth, wdir, steps, warmup, profile_steps):
     dev.finish()
     wall = time.perf_counter() - t0
     ms = max(dev.elapsed_ms(e0, e1), wall * 1e3) / steps
-    if net.gp_info() != 0:
+    info = net.gp_info()
+    if info > 0:
         raise RuntimeError("RoMa GP kernel not positive definite")
+    if info < 0:
+        # The solve's in-kernel wait for its second stream gave up: only
+        # where kernels are serialized (a counter-collecting profiler);
+        # roma_match would rerun the solve with event waits.
+        print("[bench] RoMa GP: in-kernel wait gave up (serialized kernels); "
+              "the timed passes include it", file=sys.stderr, flush=True)
     # The same pass replayed from one HIP graph.
     graph = None
     try:
@@ -247,7 +254,8 @@ def bench_roma(ic, dev, synth, wdir, steps, warmup, profile_steps):
         replayed = outs()
         net.coarse_device(pair)
         dev.finish()
-        if not all(np.array_equal(a, b) for a, b in zip(replayed, outs())):
+        # (An eager pass whose GP wait gave up has no result to compare.)
+        if info == 0 and not all(np.array_equal(a, b) for a, b in zip(replayed, outs())):
             raise RuntimeError("RoMa graph replay differs from the eager pass")
     finally:
         if graph:

@@ -48,7 +48,10 @@
  * block walks the input channels 4 at a time (a slice): the input patch
  * of a slice (from 16-byte aligned columns, the range check of the buffer
  * window giving the zero padding) arrives by LDS DMA (buffer_load ...
- * lds) two slices ahead into a ring of three buffers. The filters (the A
+ * lds) three slices ahead into a ring of four buffers, and a wave reads
+ * the next slice's window into the registers its window has just freed
+ * (after the column transform), beside this slice's products. The
+ * filters (the A
  * operands: 32 channels x 4 input channels x 36 positions a slice, stored
  * in the operand's lane order) go from L2 straight into registers: a wave
  * holds one slice's 36 operands and reloads the 12 of a transform row for
@@ -181,7 +184,7 @@ __global__ void __launch_bounds__(256, 2)
     constexpr int PSZ = PR * PP;
     constexpr int NPC = W4_CS * PR * PCH;
     static_assert(NPC <= W4_PSLOTS, "patch past its DMA slots");
-    static_assert(3 * W4_PBUF <= W4_LDS, "patch buffers past the LDS");
+    static_assert(4 * W4_PBUF <= W4_LDS, "patch ring past the LDS");
     __shared__ __align__(16) float lds[W4_LDS];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -235,13 +238,10 @@ __global__ void __launch_bounds__(256, 2)
     const float *ug = Uf + (long long)bx * nsl * (72 * 64) + 9 * 256 * hf + lane * 4;
     floatx4 ur[9];
 
-    auto compute = [&](int sl, const float *buf) {
-        /* The next slice's operands (the last slice reloads its own). */
-        const float *un = ug + (long long)(sl + 1 < nsl ? sl + 1 : sl) * (72 * 64);
-        /* Window rows hf .. hf + 4 (of 0 .. 5), columns 4 tc + 3 .. + 8,
-         * of channel kq. */
+    /* Window rows hf .. hf + 4 (of 0 .. 5), columns 4 tc + 3 .. + 8, of
+     * channel kq, from a patch buffer. */
+    auto read_window = [&](const float *buf, float (&d)[5][6]) {
         const float *p = buf + kq * PSZ + (4 * tr + hf) * PP + 4 * tc + 3;
-        float d[5][6], r[3][6];
 
 #pragma unroll
         for (int i = 0; i < 5; i++) {
@@ -255,6 +255,15 @@ __global__ void __launch_bounds__(256, 2)
             d[i][4] = v[3];
             d[i][5] = row[5];
         }
+    };
+    /* Slice sl from its window d; once d is spent (the column transform),
+     * d takes the next slice's window from nbuf, so that those LDS reads
+     * run beside this slice's products. */
+    auto compute = [&](int sl, float (&d)[5][6], const float *nbuf) {
+        /* The next slice's operands (the last slice reloads its own). */
+        const float *un = ug + (long long)(sl + 1 < nsl ? sl + 1 : sl) * (72 * 64);
+        float r[3][6];
+
         /* Rows 3 hf .. 3 hf + 2 of B^T d, from window rows hf .. hf + 4. */
         if (hf == 0) {
 #pragma unroll
@@ -278,13 +287,14 @@ __global__ void __launch_bounds__(256, 2)
                 r[2][j] = __builtin_fmaf(4.0f, d[0][j], __builtin_fmaf(-5.0f, d[2][j], d[4][j]));
             }
         }
+        read_window(nbuf, d);
 #pragma unroll
         for (int xl = 0; xl < 3; xl++) {
             w4_bt(r[xl]);
             /* Row xl's operands (loaded during the last slice) have
              * landed once at most 9 loads are outstanding: after them came
-             * the later rows' 6 loads of this slice's operands, the patch
-             * two slices ahead (3) and the next slice's reloads of rows <
+             * the later rows' 6 loads of this slice's operands, this
+             * slice's patch DMA (3) and the next slice's reloads of rows <
              * xl (3 xl): 9 + 3 xl, of which the wait lets 9 be pending. */
             __builtin_amdgcn_s_waitcnt(W4_WAIT_VM9);
 #pragma unroll
@@ -306,38 +316,41 @@ __global__ void __launch_bounds__(256, 2)
         }
     };
 
-    /* Patch of slice s in patch buffer s % 3. In slice s the patch of s +
-     * 2 (3 loads a thread) is issued first, then the 9 operand loads of s
+    /* Patch of slice s in patch buffer s % 4. In slice s the patch of s +
+     * 3 (3 loads a thread) is issued first, then the 9 operand loads of s
      * + 1; vector-memory loads complete in order, so a wait down to those
-     * 12 at the slice's end has the patch of s + 1 (issued a slice
-     * earlier) in LDS. Every slice issues these 12 (empty or repeated ones
-     * at the end), so the counts hold throughout. */
+     * 12 at the slice's end has the patch of s + 2 (issued a slice
+     * earlier) in LDS for the next slice to read the window after. Every
+     * slice issues these 12 (empty or repeated ones at the end), so the
+     * counts hold throughout. */
     float *const pb = lds;
+    float d[5][6];
 
 #pragma unroll
     for (int j = 0; j < 9; j++)
         ur[j] = *(const floatx4 *)(ug + 256 * j);
-    load_patch(0, pb);
-    if (nsl > 1)
-        load_patch(1, pb + W4_PBUF);
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+        load_patch(i, pb + i * W4_PBUF);
     __builtin_amdgcn_s_waitcnt(W4_WAIT_VM0);
     __syncthreads();
+    read_window(pb, d);
     {
-        int p3 = 0;
+        int p4 = 0;
 
         for (int sl = 0; sl < nsl; sl++) {
-            const int p3n = p3 >= 1 ? p3 - 1 : 2;
+            const int p4n = (p4 + 1) & 3, p4f = (p4 + 3) & 3;
 
-            load_patch(sl + 2, pb + p3n * W4_PBUF);
-            compute(sl, pb + p3 * W4_PBUF);
+            load_patch(sl + 3, pb + p4f * W4_PBUF);
+            compute(sl, d, pb + p4n * W4_PBUF);
             /* A bare barrier (an asm statement that also keeps the compiler
              * from moving memory accesses across it): __syncthreads' fence
-             * would wait for every outstanding load, the patch two slices
-             * ahead included. This slice's LDS reads are consumed by now
+             * would wait for every outstanding load, the patch DMA ahead
+             * included. This slice's LDS reads are consumed by now
              * (lgkmcnt 0). */
             __builtin_amdgcn_s_waitcnt(W4_WAIT_VM12_LGKM0);
             asm volatile("s_barrier" ::: "memory");
-            p3 = p3 == 2 ? 0 : p3 + 1;
+            p4 = p4n;
         }
     }
     __builtin_amdgcn_s_waitcnt(W4_WAIT_VM0);
