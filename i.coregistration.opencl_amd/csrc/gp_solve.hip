@@ -180,15 +180,27 @@ __global__ void __launch_bounds__(256) dgemm_kernel(dg_set pr)
 
 /* ---- the diagonal block ------------------------------------------------------------ */
 
-/* 1 / sqrt(x) from the hardware estimate and two Newton steps (each
- * doubles the correct bits). */
+/* 1 / sqrt(x) from the hardware estimate (within 2^29 ulp: about 2^-23
+ * relative) and one Newton step, which squares that error (about 2^-46:
+ * some 100 ulp of a double, far below what the float result can show).
+ * -0.5 x does not depend on the estimate, so the step adds three
+ * dependent operations to the pivot's chain. */
 __device__ __forceinline__ double rsqrt_nr(double x)
 {
-    double r = __builtin_amdgcn_rsq(x);
+    const double h = -0.5 * x;
+    const double r = __builtin_amdgcn_rsq(x);
 
-    r = r * fma(-0.5 * x * r, r, 1.5);
-    r = r * fma(-0.5 * x * r, r, 1.5);
-    return r;
+    return r * fma(h * r, r, 1.5);
+}
+
+/* Lane l's value of v, in every lane. */
+__device__ __forceinline__ double readlane_d(double v, int l)
+{
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+
+    return __builtin_bit_cast(
+        double, ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(b >> 32), l) << 32) |
+                    (unsigned)__builtin_amdgcn_readlane((int)b, l));
 }
 
 typedef double gp_d4 __attribute__((ext_vector_type(4)));
@@ -212,14 +224,24 @@ typedef double gp_d4 __attribute__((ext_vector_type(4)));
  *    triangle, in 16 x 16 tiles on v_mfma_f64_16x16x4f64 (lane l gives
  *    A(l % 16, l / 16) and B(l / 16, l % 16) and holds D(l / 16 + 4 v,
  *    l % 16); the fp32 16 x 16 x 4 form holds rows 4 (l / 16) + v
- *    instead). The 16 P tiles and the 10 lower P P^T tiles are dealt to
- *    the 4 waves in turn; P goes through f.
- *  - Wave 0 then sweeps the columns: lane r holds row r of the block
- *    (a[c], c <= r; its upper part is never read). At step j every lane
- *    forms the pivot's reciprocal root from lane j's a[j] (a cross-lane
- *    read) and L[r][j] = a[j] / sqrt(pivot) on and below the pivot, 0
- *    above; the column goes to LDS (lc) and each lane applies
- *        a[c] -= L[r][j] L[c][j]      (the trailing block, c > j).
+ *    instead). Its operands (the block row of A, lprev) arrive in LDS in
+ *    the same round trip as the block itself; the 16 P tiles (4 a wave,
+ *    held in registers until every wave has read lprev) and the 10
+ *    lower P P^T tiles are dealt to the 4 waves in turn; P goes through
+ *    f.
+ *  - Wave 0 then sweeps the columns two at a time: lane r holds row r
+ *    of the block (a[c], c <= r; its upper part is never read). At step
+ *    j every lane reads the 2 x 2 pivot block [p q; q s] of columns j,
+ *    j + 1 from lanes j and j + 1 (cross-lane reads), forms 1 / sqrt(p),
+ *    l21 = q / sqrt(p) and 1 / sqrt(s - l21^2), then
+ *        L[r][j] = a[j] / sqrt(p),
+ *        L[r][j + 1] = (a[j + 1] - L[r][j] l21) / sqrt(s - l21^2)
+ *    on and below the pivots (0 above); both columns go to LDS (lc)
+ *    and each lane applies the rank-2 update
+ *        a[c] -= L[r][j] L[c][j] + L[r][j + 1] L[c][j + 1]   (c > j + 1).
+ *    The step's dependent chain (cross-lane reads, two roots, one LDS
+ *    round trip, the update of the next pivots) thus serves two
+ *    columns.
  *  - Wave 1, beside it and a step behind, runs the forward substitution
  *    of L X = I column by column: lane k holds column k of T (the
  *    identity at first),
@@ -232,7 +254,8 @@ typedef double gp_d4 __attribute__((ext_vector_type(4)));
  *    from wave 1's registers (lane k: column k, so each store
  *    instruction writes one row of it).
  * Against the earlier form (1024 threads holding the block in LDS, one
- * barrier per two columns): 59.7 -> 41 us a block at n = 1600. */
+ * barrier per two columns): 59.7 -> 41 us a block at n = 1600 with one
+ * column a step. */
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
     chol_diag_kernel(const double *__restrict__ A, double *__restrict__ L,
                       double *__restrict__ Linv, int n, int k, int nb,
@@ -241,8 +264,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 {
     __shared__ double s[GP_NB][GP_NB + 1], f[GP_NB][GP_NB + 1];
     /* lc[j][r] = L[r][j]: each column contiguous, read with wide LDS
-     * loads (every lane the same address). */
-    __shared__ __align__(16) double lc[GP_NB][GP_NB];
+     * loads (every lane the same address). Before the column sweep the
+     * same memory holds ar, the look-ahead's block row of A. */
+    __shared__ __align__(16) union {
+        double lc[GP_NB][GP_NB];
+        double ar[GP_NB][GP_NB + 1];
+    } u;
+    double (*const lc)[GP_NB] = u.lc;
     __shared__ double dinv[GP_NB];
     __shared__ int prog;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -262,12 +290,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     /* The block's lower triangle; rows and columns past nb are zero with
-     * a unit diagonal (their pivots stay 1 and they touch no real row). */
+     * a unit diagonal (their pivots stay 1 and they touch no real row).
+     * With a look-ahead, its operands come in the same round trip: the
+     * block row A[k.., k - 64..] (rows past nb zero) into ar and the
+     * previous panel's inverse factor into f. */
 #pragma unroll
     for (int i = 0; i < 16; i++) {
         const int e = tid + 256 * i, r = e >> 6, c = e & 63;
-        const double v = A[(long long)(k + min(r, nb - 1)) * n + k + min(c, nb - 1)];
+        const long long row = (long long)(k + min(r, nb - 1)) * n;
+        const double v = A[row + k + min(c, nb - 1)];
 
+        if (lprev) {
+            const double va = A[row + k - GP_NB + c], vl = lprev[e];
+
+            u.ar[r][c] = r < nb ? va : 0.0;
+            f[r][c] = vl;
+        }
         s[r][c] = r < nb && c <= r ? v : r == c ? 1.0 : 0.0;
     }
     if (tid == 0)
@@ -275,28 +313,30 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     __syncthreads();
     if (lprev) {
         const int kq = lane >> 4;
+        gp_d4 pacc[4];
 
-        for (int w = wave; w < 16; w += 4) {
-            const int tr = w >> 2, tc = ((w & 3) + (w >> 2)) & 3;
-            const int ri = 16 * tr + (lane & 15), ci = 16 * tc + (lane & 15);
-            const double *trow = A + (long long)(k + min(ri, nb - 1)) * n + k - GP_NB;
-            double ta[16], lb[16];
-            gp_d4 acc = {0.0, 0.0, 0.0, 0.0};
-
+        /* P tiles (i, (wave + i) % 4) of this wave, from LDS; lprev is
+         * lower triangular, so tile column tc needs k < 16 (tc + 1). */
 #pragma unroll
-            for (int kk = 0; kk < 16; kk++)
-                if (kk < 4 * (tc + 1)) {
-                    ta[kk] = trow[4 * kk + kq];
-                    lb[kk] = lprev[ci * GP_NB + 4 * kk + kq];
-                }
+        for (int i = 0; i < 4; i++) {
+            const int tc = (wave + i) & 3;
+            const int ri = 16 * i + (lane & 15), ci = 16 * tc + (lane & 15);
+
+            pacc[i] = (gp_d4){0.0, 0.0, 0.0, 0.0};
 #pragma unroll
             for (int kk = 0; kk < 16; kk++)
                 if (kk < 4 * (tc + 1))
-                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(ri < nb ? ta[kk] : 0.0, lb[kk],
-                                                              acc, 0, 0, 0);
+                    pacc[i] = __builtin_amdgcn_mfma_f64_16x16x4f64(
+                        u.ar[ri][4 * kk + kq], f[ci][4 * kk + kq], pacc[i], 0, 0, 0);
+        }
+        __syncthreads(); /* every wave is done reading f */
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int tc = (wave + i) & 3;
+
 #pragma unroll
             for (int v = 0; v < 4; v++)
-                f[16 * tr + kq + 4 * v][16 * tc + (lane & 15)] = acc[v];
+                f[16 * i + kq + 4 * v][16 * tc + (lane & 15)] = pacc[i][v];
         }
         __syncthreads();
         for (int w = wave; w < 10; w += 4) {
@@ -331,76 +371,104 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
         for (int c = 0; c < GP_NB; c++)
             a[c] = s[lane][c];
 #pragma unroll
-        for (int j = 0; j < GP_NB; j++) {
+        for (int j = 0; j < GP_NB; j += 2) {
             if (j >= nb)
                 continue;
-            /* Column j - 1 and its root were written a step ago: counted
-             * now, the release's wait for them costs nothing. */
+            /* Columns below j and their roots were written a step ago:
+             * counted now, the release's wait for them costs nothing. */
             if (j > 0 && lane == 0)
                 __hip_atomic_store(&prog, j, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-            const unsigned long long pj = __builtin_bit_cast(unsigned long long, a[j]);
-            const double piv = __builtin_bit_cast(
-                double,
-                ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)(pj >> 32), j)
-                 << 32) |
-                    (unsigned)__builtin_amdgcn_readlane((int)pj, j));
-            const double rj = rsqrt_nr(piv);
-            const double lr = lane > j ? a[j] * rj : lane == j ? piv * rj : 0.0;
+            /* Pair j, j + 1: the 2 x 2 pivot block [p q; q s] from lanes j
+             * and j + 1, p's root, then the second pivot s - l21^2 and its
+             * root. Column j + 1 of a lane is its entry less its column-j
+             * value times l21, so one LDS round trip and one rank-2 update
+             * serve both columns. When nb is odd the last step's second
+             * column is a padding column (unit pivot, zero elsewhere),
+             * which leaves the real ones unchanged. */
+            const double p = readlane_d(a[j], j), q = readlane_d(a[j], j + 1);
+            const double sq = readlane_d(a[j + 1], j + 1);
+            const double rp = rsqrt_nr(p);
+            const double l21 = q * rp;
+            const double s2 = fma(-l21, l21, sq);
+            const double rs = rsqrt_nr(s2);
+            const double l0 = lane > j ? a[j] * rp : lane == j ? p * rp : 0.0;
+            const double l1 = lane > j + 1   ? fma(-l0, l21, a[j + 1]) * rs
+                              : lane == j + 1 ? s2 * rs
+                                              : 0.0;
 
-            if (lane == 0 && bad == 0 && !(piv > 0.0))
-                bad = k + j + 1;
-            a[j] = lr;
-            lc[j][lane] = lr;
-            if (lane == 0)
-                dinv[j] = rj;
+            if (lane == 0 && bad == 0) {
+                if (!(p > 0.0))
+                    bad = k + j + 1;
+                else if (!(s2 > 0.0))
+                    bad = k + j + 2;
+            }
+            lc[j][lane] = l0;
+            lc[j + 1][lane] = l1;
+            if (lane == 0) {
+                dinv[j] = rp;
+                dinv[j + 1] = rs;
+            }
             /* LDS operations of one wave complete in issue order: these
-             * reads see the column just written. The column is read in
+             * reads see the columns just written. Both columns are read in
              * full before the updates, so that the loads overlap. */
-            double col[GP_NB];
+            double c0[GP_NB], c1[GP_NB];
 
 #pragma unroll
-            for (int c = j + 1; c < GP_NB; c++)
-                col[c] = lc[j][c];
-            __builtin_amdgcn_sched_group_barrier(0x100, 32, 0); /* LDS reads first */
+            for (int c = j + 2; c < GP_NB; c++) {
+                c0[c] = lc[j][c];
+                c1[c] = lc[j + 1][c];
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 64, 0); /* LDS reads first */
 #pragma unroll
-            for (int c = j + 1; c < GP_NB; c++)
-                a[c] = fma(-lr, col[c], a[c]);
+            for (int c = j + 2; c < GP_NB; c++)
+                a[c] = fma(-l1, c1[c], fma(-l0, c0[c], a[c]));
         }
         if (lane == 0)
             __hip_atomic_store(&prog, nb, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
     else if (wave == 1) {
-        /* The inverse, one step behind: lane k holds column k of T (the
-         * identity at first), T[j][k] /= L[j][j], then T[c][k] -= L[c][j]
-         * T[j][k] below, with column j of L from lc once wave 0 has
-         * counted it. The wait is on wave 0 of the same block, which
-         * always counts every column; it is capped all the same. */
+        /* The inverse, a step behind, two columns at a time as wave 0
+         * makes them: lane k holds column k of T (the identity at first),
+         *     T[j][k] /= L[j][j],
+         *     T[j + 1][k] = (T[j + 1][k] - L[j + 1][j] T[j][k]) / L[j + 1][j + 1],
+         * then T[c][k] -= L[c][j] T[j][k] + L[c][j + 1] T[j + 1][k] below,
+         * with columns j, j + 1 of L from lc once wave 0 has counted them
+         * (or all nb columns, when j + 1 is a padding column). The wait is
+         * on wave 0 of the same block, which always counts every column;
+         * it is capped all the same. */
         double t[GP_NB];
 
 #pragma unroll
         for (int c = 0; c < GP_NB; c++)
             t[c] = c == lane ? 1.0 : 0.0;
 #pragma unroll
-        for (int j = 0; j < GP_NB; j++) {
+        for (int j = 0; j < GP_NB; j += 2) {
             if (j >= nb)
                 continue;
+            const int need = j + 2 < nb ? j + 2 : nb;
             int it = 0;
 
-            while (__hip_atomic_load(&prog, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <=
-                       j &&
+            while (__hip_atomic_load(&prog, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) <
+                       need &&
                    ++it < (1 << 24))
                 __builtin_amdgcn_s_sleep(1);
+            double c0[GP_NB], c1[GP_NB];
+
+#pragma unroll
+            for (int c = j + 1; c < GP_NB; c++)
+                c0[c] = lc[j][c];
+#pragma unroll
+            for (int c = j + 2; c < GP_NB; c++)
+                c1[c] = lc[j + 1][c];
+            __builtin_amdgcn_sched_group_barrier(0x100, 64, 0);
             const double tj = t[j] * dinv[j];
-            double col[GP_NB];
+            const double tj1 = fma(-c0[j + 1], tj, t[j + 1]) * dinv[j + 1];
 
             t[j] = tj;
+            t[j + 1] = tj1;
 #pragma unroll
-            for (int c = j + 1; c < GP_NB; c++)
-                col[c] = lc[j][c];
-            __builtin_amdgcn_sched_group_barrier(0x100, 32, 0);
-#pragma unroll
-            for (int c = j + 1; c < GP_NB; c++)
-                t[c] = fma(-col[c], tj, t[c]);
+            for (int c = j + 2; c < GP_NB; c++)
+                t[c] = fma(-c1[c], tj1, fma(-c0[c], tj, t[c]));
         }
         /* Lane k writes column k, one row of the inverse per store. */
         if (lane < nb)
