@@ -591,6 +591,64 @@ __device__ __forceinline__ void lc_cm_tiles(__amdgpu_buffer_rsrc_t ra, __amdgpu_
     }
 }
 
+/* LDS of a cell-major block: the staging ring's two buffers, or
+ * afterwards the product planes. A ring buffer holds one 32-channel
+ * chunk: 20 rows of 8 box cells (128 bytes a cell, its eight 4-channel
+ * groups in slots swizzled by the cell: slot p holds group p ^ ((cell /
+ * 2) % 8), so that the 16 cells an operand read takes spread over the
+ * banks), then the patch's 16 cells x 32 channels (channel c of cell m at
+ * 16 (8 (c % 4) + c / 4) + m, so that the four channels one MFMA step
+ * reads fall into different banks). */
+#define LC_RBOX 5120
+#define LC_RBUF (LC_RBOX + 512)
+#define LC_SM (2 * LC_RBUF)
+
+/* The staged path of the cell-major kernel for one wave's NTW box tiles
+ * (tw, tw + 2, ...) over its half h of every chunk's channels. Chunk q
+ * (channels 32 q ..) is loaded into registers two chunks ahead (load: 6
+ * 16-byte loads a lane), written to ring buffer q % 2 a chunk ahead
+ * (store), one barrier a chunk; the wave's products accumulate into acc.
+ * In MFMA step s a lane's k index kq stands for channel 16 h + 4 kq + s
+ * of the chunk in both operands; the box operand is one 16-byte LDS read
+ * of the lane's cell (its group 4 h + kq), the patch operand one 4-byte
+ * read a step, times rc = 1 / sqrt(C) as the reference scales f1. */
+template <int NTW, typename Load, typename Store>
+__device__ __forceinline__ void lc_ring_tiles(float *sm, int nq, int h, int tw, int lane, float rc,
+                                              Load &&load, Store &&store, lc_f4 (&acc)[5])
+{
+    const int m = lane & 15, kq = lane >> 4;
+    const int ao = LC_RBOX + 16 * (4 * h + kq) + m;
+    const int bo = 32 * m + 4 * ((4 * h + kq) ^ (m >> 1)) + 512 * tw;
+    lc_f4 st[6];
+
+    load(0, st);
+    store(st, sm);
+    load(1, st);
+    for (int q = 0; q < nq; q++) {
+        const float *buf = sm + (q & 1) * LC_RBUF;
+
+        /* Buffer q % 2 is written; the other one is read by no wave. */
+        __syncthreads();
+        store(st, sm + ((q + 1) & 1) * LC_RBUF);
+        load(q + 2, st);
+        float a[4];
+        lc_f4 b[NTW > 0 ? NTW : 1];
+
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+            a[s] = buf[ao + 128 * s] * rc;
+#pragma unroll
+        for (int i = 0; i < NTW; i++)
+            b[i] = *(const lc_f4 *)(buf + bo + 1024 * i);
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int i = 0; i < NTW; i++)
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[i][s], acc[i], 0, 0, 0);
+    }
+    __syncthreads();
+}
+
 /* Cell-major form: f1 (C x n) as it is, t2 is f2 as (n x C) with rows
  * ld floats apart (C % 4 == 0, ld % 4 == 0, t2 16-byte aligned, C n 4 and
  * n ld 4 below 2^31). The patch's own cells are 16 of n, read a channel
@@ -599,12 +657,14 @@ __device__ __forceinline__ void lc_cm_tiles(__amdgpu_buffer_rsrc_t ra, __amdgpu_
 __global__ void __launch_bounds__(256)
     local_corr_cm_kernel(const float *__restrict__ f1, const float *__restrict__ t2, int C,
                          int ld, int H, int W, int r, const float *__restrict__ flow,
-                         float *__restrict__ out, int coff)
+                         float *__restrict__ out, int coff, int ring)
 {
-    /* Products of the patch's cells: four planes LC_T x LC_PG (tiled path,
-     * at most 144 box cells), two planes LC_T x LC_GS (tiled path, more),
-     * or LC_T rows LC_GS apart (per-cell path's windows). */
-    __shared__ float G[4 * LC_T * LC_PG];
+    /* The staging ring (ring path), then the products of the patch's
+     * cells: two planes LC_T x LC_PG (ring path), four planes LC_T x LC_PG
+     * (tiled path, at most 144 box cells), two planes LC_T x LC_GS (tiled
+     * path, more), or LC_T rows LC_GS apart (per-cell path's windows). */
+    __shared__ __align__(16) float sm[LC_SM];
+    float *const G = sm;
     __shared__ lc_patch pt;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -620,6 +680,103 @@ __global__ void __launch_bounds__(256)
     const int nb = bw * bh;
     const bool tiled = nb <= LC_NB;
 
+    if (ring && nb > 0 && nb <= 144) {
+        /* Boxes of up to 9 tiles with C % 32 == 0 and W % 4 == 0: both
+         * operands staged through LDS a 32-channel chunk at a time (box
+         * rows 128 bytes a cell from the cell-major map, the patch's rows
+         * of 4 cells from the channel planes, each loaded once per block),
+         * the next chunk's loads in flight during this chunk's products.
+         * Wave wv takes the tiles wv / 2, wv / 2 + 2, ... over half wv % 2
+         * of the channels; the halves meet in two planes. */
+        const int nt = (nb + 15) >> 4, h = wv & 1, tw = wv >> 1;
+        const int ntw = nt > tw ? (nt - tw + 1) >> 1 : 0;
+        const int nq = C >> 5;
+        const unsigned pbytes = (unsigned)n * 4u;
+        const __amdgpu_buffer_rsrc_t ra = lc_rsrc(f1, (unsigned)C * pbytes);
+        const __amdgpu_buffer_rsrc_t rb = lc_rsrc(t2, (unsigned)n * (unsigned)ld * 4u);
+        const int px0 = (tile_id % tiles_x) * 4, py0 = (tile_id / tiles_x) * 4;
+        /* Box rows wv + 4 j: lane l loads cell 8 (wv + 4 j) + l / 8,
+         * channel group (l % 8) ^ ((cell / 2) % 8); past the box, zeros. */
+        unsigned boff[5];
+
+#pragma unroll
+        for (int j = 0; j < 5; j++) {
+            const int e = 8 * (wv + 4 * j) + (lane >> 3);
+            const int g = (lane & 7) ^ ((e >> 1) & 7);
+
+            boff[j] = e < nb ? ((unsigned)((by0 + e / bw) * W + bx0 + e % bw) * (unsigned)ld +
+                                4u * (unsigned)g) *
+                                   4u
+                             : LC_OOB;
+        }
+        /* Patch row wv % 2 (waves 2, 3 repeat the rows of 0, 1): lane l
+         * loads slot 64 (wv % 2) + l, 4 cells of row y = l % 4 of channel
+         * 4 (c' % 8) + c' / 8, c' = slot / 4. */
+        const int fsl = 64 * (wv & 1) + lane, fcp = fsl >> 2, fy = fsl & 3;
+        const int fc = 4 * (fcp & 7) + (fcp >> 3);
+        const unsigned foff =
+            py0 + fy < H ? ((unsigned)fc * (unsigned)n + (unsigned)((py0 + fy) * W + px0)) * 4u
+                         : LC_OOB;
+        /* Chunk q's 6 loads of this lane (past C: zeros), and their LDS
+         * slots: box row wv + 4 j at 256 (wv + 4 j) + 4 l floats, patch
+         * row wv % 2 at LC_RBOX + 256 (wv % 2) + 4 l (waves 2, 3 write
+         * the same values as 0, 1). */
+        auto load = [&](int q, lc_f4 (&st)[6]) {
+            const bool in = q < nq;
+            const unsigned cb = 128u * (unsigned)q, fb = 32u * (unsigned)q * pbytes;
+
+#pragma unroll
+            for (int j = 0; j < 5; j++)
+                st[j] = lc_load4(rb, in && boff[j] != LC_OOB ? boff[j] + cb : LC_OOB);
+            st[5] = lc_load4(ra, in && foff != LC_OOB ? foff + fb : LC_OOB);
+        };
+        auto store = [&](const lc_f4 (&st)[6], float *buf) {
+#pragma unroll
+            for (int j = 0; j < 5; j++)
+                *(lc_f4 *)(buf + 256 * (wv + 4 * j) + 4 * lane) = st[j];
+            *(lc_f4 *)(buf + LC_RBOX + 256 * (wv & 1) + 4 * lane) = st[5];
+        };
+        lc_f4 acc[5];
+
+#pragma unroll
+        for (int i = 0; i < 5; i++)
+            acc[i] = (lc_f4){0.0f, 0.0f, 0.0f, 0.0f};
+        switch (ntw) {
+        case 0:
+            lc_ring_tiles<0>(sm, nq, h, tw, lane, rc, load, store, acc);
+            break;
+        case 1:
+            lc_ring_tiles<1>(sm, nq, h, tw, lane, rc, load, store, acc);
+            break;
+        case 2:
+            lc_ring_tiles<2>(sm, nq, h, tw, lane, rc, load, store, acc);
+            break;
+        case 3:
+            lc_ring_tiles<3>(sm, nq, h, tw, lane, rc, load, store, acc);
+            break;
+        case 4:
+            lc_ring_tiles<4>(sm, nq, h, tw, lane, rc, load, store, acc);
+            break;
+        default:
+            lc_ring_tiles<5>(sm, nq, h, tw, lane, rc, load, store, acc);
+        }
+        /* Lane l holds rows 4 (l / 16) + v of each tile's 16 x 16 block,
+         * column l % 16; plane h. */
+        {
+            const int m = lane & 15, kq = lane >> 4;
+            float *Gh = G + h * LC_T * LC_PG;
+
+#pragma unroll
+            for (int i = 0; i < 5; i++)
+                if (i < ntw)
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        Gh[(4 * kq + v) * LC_PG + (tw + 2 * i) * 16 + m] = acc[i][v];
+        }
+        __syncthreads();
+        lc_outputs(pt, G, 2, LC_T * LC_PG, LC_PG, true, r, n, out, coff, tid);
+        return;
+    }
     if (tiled) {
         /* Wave wv takes the 16-channel chunks wv, wv + 4, ... of all box
          * tiles (up to nine at a time), so that each patch and box row is loaded
@@ -1132,9 +1289,13 @@ extern "C" void roma_local_corr(struct ops *o, cl_mem f1, cl_mem f2, int C,
             else
                 hipLaunchKernelGGL(lc_transpose_kernel<false>, dim3((unsigned)ttiles), dim3(256),
                                    0, st, cfptr(f2), t2, C, (int)ld, (int)n);
+            /* The staging ring takes whole 32-channel chunks and rows of
+             * 4 patch cells that are wholly inside or outside the map. */
+            const int ring = C % 32 == 0 && W % 4 == 0;
+
             hipLaunchKernelGGL(local_corr_cm_kernel, grid, dim3(256), 0, st, cfptr(f1),
                                (const float *)t2, C, (int)ld, H, W, r, cfptr(flow), fptr(out),
-                               coff);
+                               coff, ring);
         }
         else
             hipLaunchKernelGGL(local_corr_kernel, grid, dim3(256), 0, st, cfptr(f1),

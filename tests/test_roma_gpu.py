@@ -135,14 +135,18 @@ def test_warp_sample(dev, ic, orc, C, H, W, smooth):
                                             (37, 20, 22, 3, False), (192, 64, 64, 3, False),
                                             (40, 36, 44, 4, True), (64, 33, 46, 3, True),
                                             (16, 8, 12, 1, False), (512, 108, 108, 3, False),
-                                            (36, 17, 28, 2, True), (128, 216, 216, 2, False)])
+                                            (36, 17, 28, 2, True), (128, 216, 216, 2, False),
+                                            (64, 38, 44, 3, True), (96, 30, 40, 2, True),
+                                            (32, 26, 28, 1, True), (1024, 24, 24, 3, True)])
 def test_local_corr(dev, ic, orc, C, H, W, r, smooth):
     """Random warps (most 4 x 4 patches scatter: the per-cell path) and
     smooth ones (the matrix-core path over the patch's window box, with a
     few broken cells), up to the refiner config's 1/8 and 1/4 shapes at
     864 x 864, radius 1 to 7; channel counts that are multiples of 4 (the
     cell-major form, f2 transposed first) and others (channel-major
-    reads)."""
+    reads). Multiples of 32 channels on maps whose width is a multiple of
+    4 take the staged form for boxes of up to 144 cells (the 1/8 and 1/4
+    shapes, a map whose last patch row is cut, radius 1, 1024 channels)."""
     print(f"[roma] local_corr C={C} {H}x{W} r={r} smooth={smooth}", flush=True)
     rng = np.random.default_rng(C + r)
     f0 = rng.standard_normal((C, H, W)).astype(np.float32)
