@@ -156,8 +156,11 @@ __device__ __forceinline__ bil bilinear_setup(float x, float y, int H, int W,
  * (the map is written once and read by the next kernel). A block takes
  * 256 cells of one channel group, so that a few thousand cells still fill
  * the GPU (11 664 cells x 512 channels at 1/8 of 864 x 864: 2944 blocks
- * instead of 46). CG is 8, or 4 when that leaves fewer idle channel slots
- * (9 channels: 3 of 12 instead of 7 of 16). */
+ * instead of 46). CG is 8, or 4 when that leaves fewer idle channel slots;
+ * maps of up to 16 channels (the 1/1 refiner's 9) take one thread per
+ * cell (CG 16), so that the flow and taps of a cell are read and formed
+ * once. Slots past C issue no loads (the test is the same for the whole
+ * block). */
 template <int CG>
 __global__ void __launch_bounds__(256)
     warp_sample_kernel(const float *__restrict__ in, int C, int H, int W,
@@ -191,7 +194,9 @@ __global__ void __launch_bounds__(256)
     o11 = in11 ? (b.y0 + 1) * W + b.x0 + 1 : 0;
 #pragma unroll
     for (int k = 0; k < CG; k++) {
-        const float *p = in + (long long)min(c0 + k, C - 1) * n;
+        if (c0 + k >= C)
+            break;
+        const float *p = in + (long long)(c0 + k) * n;
 
         v[k][0] = in00 ? p[o00] : 0.0f;
         v[k][1] = in01 ? p[o01] : 0.0f;
@@ -1154,11 +1159,15 @@ extern "C" void roma_warp_sample(struct ops *o, cl_mem in, int C, int H, int W,
     need_floats(out, (long long)coff * n, (long long)C * n, op, "out");
     prof_scope ps(o->ocl, op);
     {
-        const int cg = sample_cg(C);
+        const int cg = C <= 16 ? 16 : sample_cg(C);
 
         if ((long long)nblk(n, 256) * nblk(C, cg) >= (1LL << 31))
             icoreg_fatal("%s: grid too large", op);
-        if (cg == 4)
+        if (cg == 16)
+            hipLaunchKernelGGL(warp_sample_kernel<16>, dim3(nblk(n, 256)), dim3(256), 0,
+                               stream_of(o->ocl), cfptr(in), C, H, W, cfptr(flow), fptr(out),
+                               coff);
+        else if (cg == 4)
             hipLaunchKernelGGL(warp_sample_kernel<4>, dim3(nblk(n, 256) * nblk(C, 4)), dim3(256),
                                0, stream_of(o->ocl), cfptr(in), C, H, W, cfptr(flow), fptr(out),
                                coff);
