@@ -106,7 +106,8 @@ def test_cls_to_flow(dev, ic, orc, res, n):
 
 @pytest.mark.parametrize("C,H,W,smooth", [(3, 37, 45, False), (64, 70, 70, False),
                                           (13, 31, 17, True), (512, 108, 108, True),
-                                          (9, 432, 432, True)])
+                                          (9, 432, 432, True), (1, 29, 33, True),
+                                          (16, 40, 52, False), (17, 23, 31, True)])
 def test_warp_sample(dev, ic, orc, C, H, W, smooth):
     print(f"[roma] warp_sample C={C} {H}x{W}", flush=True)
     rng = np.random.default_rng(C)
