@@ -26,18 +26,20 @@
  *    (lower tiles but the next diagonal block), Z_rest -= L21 Y_b and
  *    X[0 : k + nb] += Minv_b^T Y_F,b (fp64 GEMM tiles, up to three
  *    problems per launch).
- * Synchronisation: the second stream waits for diagonal block b through
- * the completion event of that kernel's own launch, and the diagonal
- * kernel of block b waits, inside the kernel, for a flag that a one-wave
- * kernel sets on the second stream after panel b - 2's trailing update.
- * The main stream thus holds the diagonal kernels alone: a stream wait
- * or an event record between them costs 5-7 us of command-processor time
- * each, on the solve's critical path. Under stream capture (a graph has
- * no order between branches that an in-kernel wait could rely on), the
- * diagonal kernels wait through stream events instead.
+ * Synchronisation, inside the kernels: the diagonal kernel of block b
+ * sets a flag once its factor and inverse are stored, which panel b's
+ * first products on the second stream poll before reading them; and it
+ * waits itself for a flag that a one-wave kernel sets on the second
+ * stream after panel b - 2's trailing update. Neither stream then holds
+ * a stream wait or an event record between its kernels (each costs 5-7
+ * us of command-processor time, on the solve's critical path). Every
+ * wait is bounded; one that gives up sets info = -1 and its kernel ends
+ * (the caller then runs the solve again with event waits). Under stream
+ * capture (a graph has no order between branches that an in-kernel wait
+ * could rely on), the two streams wait through stream events instead.
  * Working matrices: A (n x n, the trailing updates), L (n x n, the
- * factor), Linv per panel, Z and Y (n x (d + n)), X (n x d), one flag per
- * panel. No launch reads what another running beside it writes. */
+ * factor), Linv per panel, Z and Y (n x (d + n)), X (n x d), two flags
+ * per panel. No launch reads what another running beside it writes. */
 
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
@@ -71,10 +73,17 @@ struct dg_args {
     int skip00;
 };
 
-/* Up to three independent problems per launch: blockIdx.z picks one. */
+/* Up to three independent problems per launch: blockIdx.z picks one.
+ * wait (when given): a flag the launch's blocks poll (one thread each,
+ * device-coherent loads, at most spin_max polls, then an acquire) before
+ * they read their operands; a wait that gives up sets *info = -1 and
+ * goes on, so that the launch still ends. */
 #define DG_MAXP 3
 struct dg_set {
     dg_args p[DG_MAXP];
+    const int *wait;
+    int spin_max;
+    int *info;
 };
 
 __global__ void __launch_bounds__(256) dgemm_kernel(dg_set pr)
@@ -88,6 +97,19 @@ __global__ void __launch_bounds__(256) dgemm_kernel(dg_set pr)
     if (i0 >= a.M || j0 >= a.N || (a.lower && j0 > i0 + DG_T - 1) ||
         (a.skip00 && i0 == 0 && j0 == 0))
         return;
+    if (pr.wait) {
+        if (tid == 0) {
+            int it = 0;
+
+            while (__hip_atomic_load(pr.wait, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 &&
+                   ++it < pr.spin_max)
+                __builtin_amdgcn_s_sleep(1);
+            if (it >= pr.spin_max)
+                __hip_atomic_store(pr.info, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
     /* The accumulated C is read at the start, so that its latency
      * overlaps the products. */
 #pragma unroll
@@ -218,6 +240,8 @@ typedef double gp_d4 __attribute__((ext_vector_type(4)));
  *  - ready (when given): set once the trailing update this block needs
  *    has finished on the other stream; polled with device-coherent loads,
  *    then an acquire, so the block's reads see that update.
+ *  - done (when given): set to 1 after every store of the block, behind
+ *    a release, for the panel's products on the other stream.
  *  - Look-ahead (lprev: the previous panel's Linv; its trailing update of
  *    this block is left to this kernel): P = A[k.., k - 64..] lprev^T,
  *    the block's row of that panel's L21, then s -= P P^T on the lower
@@ -260,7 +284,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     chol_diag_kernel(const double *__restrict__ A, double *__restrict__ L,
                       double *__restrict__ Linv, int n, int k, int nb,
                       const double *__restrict__ lprev, const int *ready, int spin_max,
-                      int *__restrict__ info)
+                      int *__restrict__ info, int *done)
 {
     __shared__ double s[GP_NB][GP_NB + 1], f[GP_NB][GP_NB + 1];
     /* lc[j][r] = L[r][j]: each column contiguous, read with wide LDS
@@ -487,22 +511,32 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
         if (r < nb && c < nb)
             L[(long long)(k + r) * n + k + c] = lc[c][r];
     }
+    if (done) {
+        /* Every store of the block has reached L2 (the barrier waits for
+         * them); the release writes them back for the other XCDs, then
+         * the flag. */
+        __syncthreads();
+        if (tid == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            __hip_atomic_store(done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 /* A = K + noise I (double), Z = [F | I] (double, rows d + n wide), X = 0
- * (n x d), info and the nblk panel flags cleared. */
+ * (n x d), info and the nflags panel flags cleared. */
 __global__ void __launch_bounds__(256)
     gp_init_kernel(const float *__restrict__ K, int n, double noise,
                    double *__restrict__ A, const float *__restrict__ F, int d,
                    double *__restrict__ Z, double *__restrict__ X, int *__restrict__ info,
-                   int *__restrict__ flags, int nblk)
+                   int *__restrict__ flags, int nflags)
 {
     const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
     const long long nn = (long long)n * n, w = (long long)d + n, nz = n * w;
 
     if (idx == 0)
         *info = 0;
-    if (idx < nblk)
+    if (idx < nflags)
         flags[idx] = 0;
     if (idx < nn) {
         const int r = (int)(idx / n), c = (int)(idx % n);
@@ -544,11 +578,17 @@ static dg_args dg(int M, int N, int K, const double *A, long long a_ri, long lon
     return a;
 }
 
-/* One launch for the problems given (those with no output are skipped). */
-static void dgemm(hipStream_t s, std::initializer_list<const dg_args *> ps)
+/* One launch for the problems given (those with no output are skipped);
+ * wait, spin_max, info as in dg_set. */
+static void dgemm(hipStream_t s, std::initializer_list<const dg_args *> ps,
+                  const int *wait = nullptr, int spin_max = 0, int *info = nullptr)
 {
     dg_set pr;
     int np = 0, tx = 0, ty = 0;
+
+    pr.wait = wait;
+    pr.spin_max = spin_max;
+    pr.info = info;
 
     for (const dg_args *a : ps)
         if (a && a->M > 0 && a->N > 0) {
@@ -570,14 +610,15 @@ extern "C" size_t roma_gp_work_bytes(int n, int d)
 
     return sizeof(double) * (2 * (size_t)n * n + nblk * GP_NB * GP_NB + 2 * (size_t)n * w +
                              (size_t)n * d) +
-           sizeof(int) * nblk;
+           sizeof(int) * 2 * nblk;
 }
 
-/* Test hooks (icoreg_gp_test_wait): the in-kernel wait's poll limit and
- * whether the second stream sets the panel flags at all. With the flags
- * never set and a short limit, every waiting diagonal kernel gives up at
- * once (info = -1) and still exits, so the give-up path and the caller's
- * recovery can be exercised without a stalled stream. */
+/* Test hooks (icoreg_gp_test_wait): the in-kernel waits' poll limit and
+ * whether the panel flags are set at all (by the second stream's flag
+ * kernel and by the diagonal kernels). With the flags never set and a
+ * short limit, every waiting kernel gives up at once (info = -1) and
+ * still exits, so the give-up path and the caller's recovery can be
+ * exercised without a stalled stream. */
 static int g_spin_max = GP_SPIN_MAX;
 static int g_set_flags = 1;
 
@@ -626,15 +667,18 @@ static void gp_solve_run(struct ops *o, cl_mem K, int n, float noise, cl_mem F, 
 
         hipLaunchKernelGGL(gp_init_kernel, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s,
                            cfptr(K), n, (double)noise, A, cfptr(F), d, Z, X, (int *)info->ptr,
-                           flags, nblk);
+                           flags, 2 * nblk);
         /* The diagonal blocks on the main stream s, everything else of a
          * panel on the second stream s2: diagonal block b waits for the
          * trailing update of panel b - 2 (which has the whole of block
          * b - 1's factorisation to finish) and applies panel b - 1's
          * update to its own block itself; panel b's products wait for
          * block b. Y = L^-1 [F | I] alongside, over the columns that are
-         * not yet zero (F and the identity blocks up to this panel's). */
+         * not yet zero (F and the identity blocks up to this panel's).
+         * flags[b]: panel b's trailing update done (set on s2);
+         * dflags[b]: block b factored (set by its diagonal kernel). */
         hipStream_t s2 = aux_stream_of(o->ocl);
+        int *const dflags = flags + nblk;
 
         hip_check(hipEventRecord(aux_event(o->ocl, 2 * nblk), s), "hipEventRecord");
         hip_check(hipStreamWaitEvent(s2, aux_event(o->ocl, 2 * nblk), 0), "hipStreamWaitEvent");
@@ -653,29 +697,26 @@ static void gp_solve_run(struct ops *o, cl_mem K, int n, float noise, cl_mem F, 
                               "hipStreamWaitEvent");
                 hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(256), 0, s, A,
                                    L, Lk, n, k, nb, lprev, (const int *)nullptr, spin_max,
-                                   info_p);
+                                   info_p, (int *)nullptr);
                 hip_check(hipEventRecord(done_b, s), "hipEventRecord");
+                hip_check(hipStreamWaitEvent(s2, done_b, 0), "hipStreamWaitEvent");
             }
-            else {
-                /* The launch's completion signals done_b itself: no
-                 * separate record on s. */
-                const int *ready = b >= 2 ? flags + b - 2 : nullptr;
-                void *args[] = {(void *)&A,  (void *)&L,     (void *)&Lk,
-                                (void *)&n,  (void *)&k,     (void *)&nb,
-                                (void *)&lprev, (void *)&ready, (void *)&spin_max,
-                                (void *)&info_p};
-
-                hip_check(hipExtLaunchKernel((const void *)chol_diag_kernel, dim3(1), dim3(256),
-                                             args, 0, s, nullptr, done_b, 0),
-                          "hipExtLaunchKernel");
-            }
-            hip_check(hipStreamWaitEvent(s2, done_b, 0), "hipStreamWaitEvent");
+            else
+                /* Panel b's first products wait for dflags[b] inside their
+                 * kernel: no stream wait (5-6 us of command-processor
+                 * time a panel on s2) and no completion event. */
+                hipLaunchKernelGGL(chol_diag_kernel, dim3(1), dim3(256), 0, s, A, L, Lk, n, k,
+                                   nb, lprev, b >= 2 ? (const int *)flags + b - 2 : nullptr,
+                                   spin_max, info_p, g_set_flags ? dflags + b : nullptr);
             /* L21 = A21 Linv^T and Y_b = Linv_b Z_b. */
             const dg_args panel = dg(rest, nb, nb, A + (long long)(k + nb) * n + k, n, 1,
                                      Lk, 1, GP_NB, L21, n, 1.0, 0, 0);
             const dg_args yb = dg(nb, wb, nb, Lk, GP_NB, 1, Z + k * w, w, 1, Y + k * w, w,
                                   1.0, 0, 0);
-            dgemm(s2, {&yb, &panel});
+            if (capture)
+                dgemm(s2, {&yb, &panel});
+            else
+                dgemm(s2, {&yb, &panel}, dflags + b, spin_max, info_p);
             /* X[0 : k + nb] += Minv_b^T Y_F,b: this panel's block row of
              * Minv = L^-1 (Y[k.., d..], zero right of its own identity
              * block) is final once Y_b is. */

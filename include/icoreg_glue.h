@@ -71,11 +71,12 @@ int icoreg_roma_last(const struct roma_model *m);
 
 void icoreg_roma_set_imagenet(struct roma_model *m, int on);
 
-/* Test hooks of the GP solve's in-kernel wait (roma_gp_solve): its poll
- * limit (0: the default, about 0.1 s) and whether the panel flags are set
- * at all (0: never, so every waiting diagonal kernel gives up after
- * spin_max polls and reports info = -1). Process-wide; for tests of the
- * give-up path and of roma_match's recovery. */
+/* Test hooks of the GP solve's in-kernel waits (roma_gp_solve): their
+ * poll limit (0: the default, about 0.1 s) and whether the panel flags
+ * are set at all (0: never, so every waiting diagonal kernel and every
+ * panel's first products give up after spin_max polls and report info =
+ * -1). Process-wide; for tests of the give-up path and of roma_match's
+ * recovery. */
 void icoreg_gp_test_wait(int spin_max, int set_flags);
 /* Which Winograd form the same-size 3 x 3 convolutions take: 0 each
  * shape's own choice (the default), 2 F(2 x 2, 3 x 3) or 4 F(4 x 4, 3 x 3)

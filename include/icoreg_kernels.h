@@ -214,9 +214,10 @@ void disk_gather_desc_count(struct ops *o, cl_mem feat, int H, int W, int D,
  * the caller to check once the stream has run. The call runs on the
  * library's stream and on its second stream (joined back before it
  * returns to the stream). Each diagonal block waits inside its kernel for
- * the other stream's trailing update; that wait is bounded (about 0.1 s),
- * and info = -1 reports that it gave up, which can happen only if the
- * other stream's work could not run meanwhile (both streams of two
+ * the other stream's trailing update, and each panel's first products
+ * inside theirs for the diagonal block; those waits are bounded (about
+ * 0.1 s), and info = -1 reports that one gave up, which can happen only
+ * if the other stream's work could not run meanwhile (both streams of two
  * concurrent solves mapped onto shared hardware queues, or a GPU
  * time-sliced away for that long). The result is then not valid: F has
  * been overwritten, so the caller restores it and calls
@@ -224,7 +225,7 @@ void disk_gather_desc_count(struct ops *o, cl_mem feat, int H, int W, int D,
 size_t roma_gp_work_bytes(int n, int d);
 void roma_gp_solve(struct ops *o, cl_mem K, int n, float noise, cl_mem F,
                    int d, cl_mem work, cl_mem info);
-/* The same solve with the diagonal blocks waiting through stream events
+/* The same solve with the two streams waiting through stream events
  * (no in-kernel wait, so info is never -1): the form used under stream
  * capture, and the fallback after info = -1. Same arithmetic and results;
  * about 0.1 ms slower at n = 1600 (the command processor's event waits on

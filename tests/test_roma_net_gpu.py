@@ -72,9 +72,10 @@ def test_gp_solve_reports_indefinite(dev, ic):
 
 
 def test_gp_solve_wait_gives_up_and_events_form(dev, ic):
-    """The diagonal kernels' bounded in-kernel wait forced to give up from
-    the host (icoreg_gp_test_wait: the panel flags never set, 64 polls):
-    every launch still exits, info is -1; roma_gp_solve_events (stream
+    """The solve's bounded in-kernel waits (the diagonal kernels' and the
+    panels' first products') forced to give up from the host
+    (icoreg_gp_test_wait: the panel flags never set, 64 polls): every
+    launch still exits, info is -1; roma_gp_solve_events (stream
     event waits) on the same inputs gives the solution, and with the
     default hooks both forms give the same bits."""
     print("[roma] gp_solve forced give-up, n=300 d=64", flush=True)
