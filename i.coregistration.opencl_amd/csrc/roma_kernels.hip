@@ -224,7 +224,8 @@ __global__ void __launch_bounds__(256)
  * A block takes a 4 x 4 patch of cells. Neighbouring cells of a smooth
  * warp have overlapping windows, so the union of the patch's windows
  * (clipped to the image) is a box of about (4 + 2 r + 1)^2 cells instead
- * of 16 (2 r + 2)^2 reads. When the box holds at most LC_NB cells, the
+ * of 16 (2 r + 2)^2 reads. When the box holds at most LC_NB cells
+ * (LC_NB2 in the cell-major kernel), the
  * block forms every patch-cell x box-cell product on the matrix cores
  * (v_mfma_f32_16x16x4f32: 16 cells x 16 box cells x 4 channels), each
  * wave streaming its operands from memory straight into registers with
@@ -256,6 +257,12 @@ __global__ void __launch_bounds__(256)
 #define LC_NB 256      /* box cells on the matrix-core path */
 #define LC_GS 260      /* LDS row pitch of the products */
 #define LC_PG 148      /* LDS row pitch of a channel-quarter plane (<= 144 box cells) */
+/* The cell-major kernel's limits: boxes of up to 25 tiles stay on the
+ * matrix cores (radius 7 on a smooth warp: 19 x 19 = 361 cells), rows of
+ * its products LC_GS2 floats apart (4 LC_GS2 = 16 mod 64 banks, as for
+ * LC_GS). */
+#define LC_NB2 400
+#define LC_GS2 404
 
 typedef float lc_f4 __attribute__((ext_vector_type(4)));
 
@@ -332,7 +339,7 @@ __device__ __forceinline__ void lc_setup(lc_patch &p, const float *__restrict__ 
 /* The outputs of the patch: out[coff + k, i] for its cells i and the
  * (2 r + 1)^2 offsets k, the bilinear combination of the cell's window
  * products. Tiled: np partial planes G + j pstride (rows gs apart, row m
- * x box cell) added in order j = 0 .. np - 1; else G row m (LC_GS
+ * x box cell) added in order j = 0 .. np - 1; else G row m (gs
  * apart) holds cell m's (2 r + 2)^2 window. Consecutive threads take
  * consecutive cells of one offset. */
 __device__ __forceinline__ void lc_outputs(const lc_patch &p, const float *G, int np, int pstride,
@@ -373,7 +380,7 @@ __device__ __forceinline__ void lc_outputs(const lc_patch &p, const float *G, in
                     s[q] = v2;
                 }
                 else
-                    s[q] = G[m * LC_GS + (ky + (q >> 1)) * ps + kx + (q & 1)];
+                    s[q] = G[m * gs + (ky + (q >> 1)) * ps + kx + (q & 1)];
             }
             v = (1.0f - fy) * ((1.0f - fx) * s[0] + fx * s[1]) +
                 fy * ((1.0f - fx) * s[2] + fx * s[3]);
@@ -606,7 +613,7 @@ __device__ __forceinline__ void lc_cm_tiles(__amdgpu_buffer_rsrc_t ra, __amdgpu_
  * reads fall into different banks). */
 #define LC_RBOX 5120
 #define LC_RBUF (LC_RBOX + 512)
-#define LC_SM (2 * LC_RBUF)
+#define LC_SM (2 * LC_RBUF > 2 * LC_T * LC_GS2 ? 2 * LC_RBUF : 2 * LC_T * LC_GS2)
 
 /* The staged path of the cell-major kernel for one wave's NTW box tiles
  * (tw, tw + 2, ...) over its half h of every chunk's channels. Chunk q
@@ -666,8 +673,8 @@ __global__ void __launch_bounds__(256)
 {
     /* The staging ring (ring path), then the products of the patch's
      * cells: two planes LC_T x LC_PG (ring path), four planes LC_T x LC_PG
-     * (tiled path, at most 144 box cells), two planes LC_T x LC_GS (tiled
-     * path, more), or LC_T rows LC_GS apart (per-cell path's windows). */
+     * (tiled path, at most 144 box cells), two planes LC_T x LC_GS2 (tiled
+     * path, more), or LC_T rows LC_GS2 apart (per-cell path's windows). */
     __shared__ __align__(16) float sm[LC_SM];
     float *const G = sm;
     __shared__ lc_patch pt;
@@ -683,7 +690,7 @@ __global__ void __launch_bounds__(256)
     __syncthreads();
     const int bx0 = pt.box[0], by0 = pt.box[1], bw = pt.box[2], bh = pt.box[3];
     const int nb = bw * bh;
-    const bool tiled = nb <= LC_NB;
+    const bool tiled = nb <= LC_NB2;
 
     if (ring && nb > 0 && nb <= 144) {
         /* Boxes of up to 9 tiles with C % 32 == 0 and W % 4 == 0: both
@@ -793,7 +800,7 @@ __global__ void __launch_bounds__(256)
          * LDS in a fixed order: with at most 9 tiles each wave stores into
          * its own plane (LC_PG pitch) and the outputs add the four planes;
          * with more, per 8 tiles waves 2 and 3 store into two planes
-         * (LC_GS pitch), waves 0 and 1 add theirs after a barrier, and the
+         * (LC_GS2 pitch), waves 0 and 1 add theirs after a barrier, and the
          * outputs add the two planes. */
         const int nt = (nb + 15) >> 4, nch = (C + 15) >> 4;
         const int acell = pt.cid[m];
@@ -802,7 +809,7 @@ __global__ void __launch_bounds__(256)
         const __amdgpu_buffer_rsrc_t rb = lc_rsrc(t2, (unsigned)n * (unsigned)ld * 4u);
         const unsigned ao = acell >= 0 ? (4u * kq * (unsigned)n + (unsigned)acell) * 4u : LC_OOB;
         const bool four = nt <= 9;
-        const int gp = four ? LC_PG : LC_GS, gsz = four ? 9 : 8;
+        const int gp = four ? LC_PG : LC_GS2, gsz = four ? 9 : 8;
         float *Gw = G + (four ? wv : (wv & 1)) * LC_T * gp;
 
         for (int u0 = 0; u0 < nt; u0 += gsz) {
@@ -918,7 +925,7 @@ __global__ void __launch_bounds__(256)
                     const float v = lc_row_sum(sum[u]);
 
                     if (m == 0 && e < np2)
-                        G[mm * LC_GS + e] = v;
+                        G[mm * LC_GS2 + e] = v;
                 }
             }
         }
@@ -927,7 +934,7 @@ __global__ void __launch_bounds__(256)
     {
         const bool four = ((nb + 15) >> 4) <= 9;
 
-        lc_outputs(pt, G, four ? 4 : 2, LC_T * (four ? LC_PG : LC_GS), four ? LC_PG : LC_GS,
+        lc_outputs(pt, G, four ? 4 : 2, LC_T * (four ? LC_PG : LC_GS2), four ? LC_PG : LC_GS2,
                    tiled, r, n, out, coff, tid);
     }
 }
