@@ -139,7 +139,8 @@ def test_warp_sample(dev, ic, orc, C, H, W, smooth):
                                             (36, 17, 28, 2, True), (128, 216, 216, 2, False),
                                             (64, 38, 44, 3, True), (96, 30, 40, 2, True),
                                             (32, 26, 28, 1, True), (1024, 24, 24, 3, True),
-                                            (512, 64, 64, 7, True), (48, 128, 128, 1, True)])
+                                            (512, 64, 64, 7, True), (48, 128, 128, 1, True),
+                                            (64, 40, 52, 2, False), (61, 31, 45, 2, True)])
 def test_local_corr(dev, ic, orc, C, H, W, r, smooth):
     """Random warps (most 4 x 4 patches scatter: the per-cell path) and
     smooth ones (the matrix-core path over the patch's window box, with a
@@ -150,7 +151,9 @@ def test_local_corr(dev, ic, orc, C, H, W, r, smooth):
     4 take the staged form for boxes of up to 144 cells (the 1/8 and 1/4
     shapes, a map whose last patch row is cut, radius 1, 1024 channels).
     Radius 7 on a smooth warp at 64 x 64 (roma_v2ref's 1/16 refiner) gives
-    boxes of 19 x 19 cells: the matrix-core path's 25-tile limit."""
+    boxes of 19 x 19 cells: the matrix-core path's 25-tile limit. 48
+    channels at radius 1 (roma_v2ref's 1/2 refiner), and 64 and 61 channels
+    at radius 2 on random and smooth warps."""
     print(f"[roma] local_corr C={C} {H}x{W} r={r} smooth={smooth}", flush=True)
     rng = np.random.default_rng(C + r)
     f0 = rng.standard_normal((C, H, W)).astype(np.float32)
