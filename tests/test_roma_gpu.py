@@ -150,8 +150,9 @@ def test_local_corr(dev, ic, orc, C, H, W, r, smooth):
     reads). Multiples of 32 channels on maps whose width is a multiple of
     4 take the staged form for boxes of up to 144 cells (the 1/8 and 1/4
     shapes, a map whose last patch row is cut, radius 1, 1024 channels).
-    Radius 7 on a smooth warp at 64 x 64 (roma_v2ref's 1/16 refiner) gives
-    boxes of 19 x 19 cells: the matrix-core path's 25-tile limit. 48
+    Radius 7 on a smooth warp at 64 x 64 (the first refiner's radius and
+    channels, on the coarse grid) gives boxes of 19 x 19 cells: the
+    matrix-core path's 25-tile limit. 48
     channels at radius 1 (roma_v2ref's 1/2 refiner), and 64 and 61 channels
     at radius 2 on random and smooth warps."""
     print(f"[roma] local_corr C={C} {H}x{W} r={r} smooth={smooth}", flush=True)
