@@ -381,6 +381,36 @@ def time_launches(dev, fn, reps=20):
     return dev.elapsed_ms(e0, e1) / reps
 
 
+def bench_local_corr_shapes(dev):
+    """roma_local_corr (cell-major copy of f2 plus correlation) alone at the
+    refiners' shapes, on seeded features and a smooth warp, each timed over
+    20 launches: the v1 refiners at 1/8 and 1/4 of 864 x 864, the first
+    refiner's radius 7 and 512 channels on 64 x 64 and 40 x 40 cells (the
+    coarse grid), roma_v2ref's refiners at 1/4 and 1/2 of 1024 x 1024.
+    frac_hbm: compulsory bytes / time / 8 TB/s."""
+    out = []
+    rng = np.random.default_rng(7)
+    api, po = dev.api, dev.po
+    for C, h, r in ((512, 108, 3), (256, 216, 2), (512, 64, 7), (512, 40, 7), (192, 256, 3),
+                    (48, 512, 1)):
+        n = h * h
+        f1 = dev.upload(rng.standard_normal((C, n), np.float32))
+        f2 = dev.upload(rng.standard_normal((C, n), np.float32))
+        gx = (2 * (np.arange(h) + 0.5) / h - 1)[None, :] + 0 * np.arange(h)[:, None]
+        gy = (2 * (np.arange(h) + 0.5) / h - 1)[:, None] + 0 * np.arange(h)[None, :]
+        fl = np.stack([gx + 0.03 * np.sin(gy * 3), gy + 0.03 * np.cos(gx * 2)]).astype(np.float32)
+        flow = dev.upload(fl)
+        d = dev.zeros((2 * r + 1) ** 2 * n)
+        ms = time_launches(dev, lambda: api.roma_local_corr(po, f1.mem, f2.mem, C, h, h, r,
+                                                            flow.mem, d.mem, 0))
+        b = hbm_kernel_bytes("local_corr", C, n, r)
+        out.append({"C": C, "cells": f"{h}x{h}", "r": r, "us": round(ms * 1e3, 2),
+                    "GBps": round(b / ms / 1e6, 1), "frac_hbm": round(b / ms / 1e6 / PEAK_HBM, 4)})
+        for t in (f1, f2, flow, d):
+            t.release()
+    return out
+
+
 def bench_hbm_kernels(ic, dev, H=864, W=864):
     """The memory-bound kernels alone at their config shapes: the refiner
     stack's (864 x 864: s8, s4, s2, s1) warp sample, local correlation
@@ -1064,7 +1094,8 @@ def main():
     ap.add_argument("--roma-only", action="store_true",
                     help="run only the RoMa leg and print its JSON object (for profiling)")
     ap.add_argument("--roma-steps", type=int, default=10)
-    ap.add_argument("--leg", choices=["refiners864", "v2ref1024", "disk512", "adalam_nn2048"],
+    ap.add_argument("--leg", choices=["refiners864", "v2ref1024", "disk512", "adalam_nn2048",
+                                      "localcorr"],
                     help="run only this extra leg and print its JSON (for profiling)")
     ap.add_argument("--hbm-only", action="store_true",
                     help="run only the memory-bound kernels' leg (and --copy-calib) and "
@@ -1094,7 +1125,8 @@ def main():
         fn = {"refiners864": lambda: bench_refiners(ic, dev, synth, wd, 10, 2, 2),
               "v2ref1024": lambda: bench_v2ref(ic, dev, synth, wd, 3, 1),
               "disk512": lambda: bench_disk(ic, dev, synth, wd, 20, 3),
-              "adalam_nn2048": lambda: bench_adalam(ic, dev)}[args.leg]
+              "adalam_nn2048": lambda: bench_adalam(ic, dev),
+              "localcorr": lambda: bench_local_corr_shapes(dev)}[args.leg]
         print(json.dumps({args.leg: fn()}), flush=True)
         dev.close()
         return
